@@ -1,0 +1,33 @@
+// Fused rel-pos attention launch interface.
+#pragma once
+#include <stdint.h>
+
+struct fa_ctx;
+
+namespace fa {
+
+// Per-launch window table, passed by value in the kernel arguments so no
+// device-side table (and no host->device copy ordering) is involved.
+constexpr int kMaxWin = 64;
+struct WinTable {
+  int n = 0;
+  int off[kMaxWin];
+  int len[kMaxWin];
+};
+
+struct AttnArgs {
+  const void *q = nullptr, *k = nullptr, *v = nullptr;  // [rows, ld*] (head h at columns h*HD ..)
+  int ldq = 0, ldk = 0, ldv = 0;
+  const void *pos = nullptr;  // projected positional table [prows, ldp]
+  int ldp = 0, prows = 0;
+  int pcenter = 0;            // table row of relative position 0
+  const float *pbu = nullptr, *pbv = nullptr;  // [H*HD], 1/sqrt(HD) folded
+  void *out = nullptr;        // [rows, ldo]
+  int ldo = 0;
+  WinTable win;               // window row offsets / lengths (by value: no device table)
+  int H = 0, HD = 0;
+};
+
+int relpos_attention(fa_ctx *ctx, const AttnArgs &a, int in_f32, int out_f32, int Tmax, const char *label);
+
+}  // namespace fa

@@ -1,0 +1,196 @@
+// Fused relative-position multi-head attention (one kernel per layer).
+//
+// Replaces the reference's bmmQK -> relShiftB -> add -> softmax -> bmmPV chain
+// (src/engines/asr-parakeet/raw-encoder.js:337-344; attention.js:14-138,268-287)
+// with one pass that never materialises the [W·H·T, T] score matrix:
+//
+//   S[i,j] = (q_i + u)·k_j + (q_i + v)·P[c - (i - j)]      (rel_shift closed form:
+//            relshift(X)[i,j] = X[i, T-1-i+j], so row T-1-i+j of a [2T-1]-row
+//            table; with a table built for Tmax >= T the centre row c = Tmax-1
+//            serves every window length, since pe rows depend only on i - j)
+//   O_i    = Σ_j softmax_j(S[i,·]) v_j        over keys j < T_w of window w
+//
+// 1/sqrt(HD) is pre-folded into q, u, v (raw-encoder.js:124-125,133).  Keys past
+// a window's length are excluded (key-padding mask), so a window packed with
+// others gives the same result as the window alone.
+//
+// Work decomposition: block = (64-query tile, head, window), 4 waves x 16 query
+// rows.  Per 64-key block each wave runs 16 MFMAs for (q+u)kᵀ, 20 for the
+// 16x80 band of (q+v)Pᵀ it needs, then an online-softmax update and 16 MFMAs
+// for P·V.  The band is turned into the diagonal-shifted score tile through a
+// per-wave LDS strip; V is staged transposed in LDS so the P·V B-operand reads
+// are 16-byte vectors.
+#include "fa_internal.h"
+#include "fa_device.h"
+#include "attention.h"
+
+namespace fa {
+
+template <typename T>
+__device__ __forceinline__ h8 ld8(const T *p) {
+  if constexpr (sizeof(T) == 2) {
+    return *reinterpret_cast<const h8 *>(p);
+  } else {
+    const float4 a = reinterpret_cast<const float4 *>(p)[0], b = reinterpret_cast<const float4 *>(p)[1];
+    h8 r;
+    r[0] = (_Float16)a.x; r[1] = (_Float16)a.y; r[2] = (_Float16)a.z; r[3] = (_Float16)a.w;
+    r[4] = (_Float16)b.x; r[5] = (_Float16)b.y; r[6] = (_Float16)b.z; r[7] = (_Float16)b.w;
+    return r;
+  }
+}
+
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void relpos_attn_kernel(AttnArgs a) {
+  constexpr int HD = 128, QB = 64, KB = 64, SW = 80 + 4, PBS = KB + 8, VTS = KB + 8;
+  __shared__ __attribute__((aligned(16))) _Float16 sVt[HD * VTS];
+  __shared__ float sStrip[4][16 * SW];
+  __shared__ __attribute__((aligned(16))) _Float16 sP[4][16 * PBS];
+
+  const int w = blockIdx.z, h = blockIdx.y, qb = blockIdx.x;
+  const int T = a.win.len[w], off = a.win.off[w];
+  if (qb * QB >= T) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int i0 = qb * QB + wave * 16;  // this wave's first query (window-local)
+  const TI *Q = reinterpret_cast<const TI *>(a.q) + (size_t)off * a.ldq + h * HD;
+  const TI *Kp = reinterpret_cast<const TI *>(a.k) + (size_t)off * a.ldk + h * HD;
+  const TI *Vp = reinterpret_cast<const TI *>(a.v) + (size_t)off * a.ldv + h * HD;
+  const TI *Pp = reinterpret_cast<const TI *>(a.pos) + h * HD;
+
+  // A operands: (q+u) and (q+v) for row i0 + c16, d = s*32 + g*8 .. +8
+  h8 qu[4], qv[4];
+  {
+    const int qi = min(i0 + c16, T - 1);
+    const TI *qr = Q + (size_t)qi * a.ldq;
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      const int d = s * 32 + g * 8;
+      h8 x = ld8(qr + d);
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float xv = (float)x[e];
+        qu[s][e] = (_Float16)(xv + a.pbu[h * HD + d + e]);
+        qv[s][e] = (_Float16)(xv + a.pbv[h * HD + d + e]);
+      }
+    }
+  }
+
+  f4 o[8];
+#pragma unroll
+  for (int t = 0; t < 8; t++) o[t] = f4{0.f, 0.f, 0.f, 0.f};
+  float mrow[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY}, lrow[4] = {0.f, 0.f, 0.f, 0.f};
+  float *strip = sStrip[wave];
+  _Float16 *pb = sP[wave];
+
+  for (int j0 = 0; j0 < T; j0 += KB) {
+    // stage V[j0 .. j0+64) transposed: sVt[d][key]
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const int idx = tid + c * 256, key = idx >> 4, dc = (idx & 15) * 8;
+      const int kj = min(j0 + key, T - 1);
+      h8 x = ld8(Vp + (size_t)kj * a.ldv + dc);
+#pragma unroll
+      for (int e = 0; e < 8; e++) sVt[(dc + e) * VTS + key] = x[e];
+    }
+
+    // content scores (q+u)·kᵀ : 4 tiles of 16 keys
+    f4 sc[4];
+#pragma unroll
+    for (int jt = 0; jt < 4; jt++) {
+      sc[jt] = f4{0.f, 0.f, 0.f, 0.f};
+      const int kj = min(j0 + jt * 16 + c16, T - 1);
+      const TI *kr = Kp + (size_t)kj * a.ldk;
+#pragma unroll
+      for (int s = 0; s < 4; s++) sc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qu[s], ld8(kr + s * 32 + g * 8), sc[jt], 0, 0, 0);
+    }
+    // positional band (q+v)·Pᵀ over table rows pr0 .. pr0+79
+    const int pr0 = a.pcenter - (i0 + 15) + j0;
+#pragma unroll
+    for (int ct = 0; ct < 5; ct++) {
+      f4 bd = f4{0.f, 0.f, 0.f, 0.f};
+      const int pr = min(max(pr0 + ct * 16 + c16, 0), a.prows - 1);
+      const TI *prow = Pp + (size_t)pr * a.ldp;
+#pragma unroll
+      for (int s = 0; s < 4; s++) bd = __builtin_amdgcn_mfma_f32_16x16x32_f16(qv[s], ld8(prow + s * 32 + g * 8), bd, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; r++) strip[(g * 4 + r) * SW + ct * 16 + c16] = bd[r];
+    }
+    __syncthreads();  // strip visible to the wave's lanes; sVt complete
+    // S = ac + band[i][j - j0 + 15 - (i - i0)], mask keys >= T, online softmax
+    float mnew[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int ri = g * 4 + r;
+      float mx = mrow[r];
+#pragma unroll
+      for (int jt = 0; jt < 4; jt++) {
+        const int jj = jt * 16 + c16;
+        float v = sc[jt][r] + strip[ri * SW + jj + 15 - ri];
+        v = (j0 + jj < T) ? v : -INFINITY;
+        sc[jt][r] = v;
+        mx = fmaxf(mx, v);
+      }
+#pragma unroll
+      for (int o2 = 1; o2 < 16; o2 <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o2, 64));
+      mnew[r] = mx;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const float corr = __expf(mrow[r] - mnew[r]);
+      float ls = 0.f;
+#pragma unroll
+      for (int jt = 0; jt < 4; jt++) {
+        const float pv = __expf(sc[jt][r] - mnew[r]);
+        ls += pv;
+        pb[(g * 4 + r) * PBS + jt * 16 + c16] = (_Float16)pv;
+      }
+#pragma unroll
+      for (int o2 = 1; o2 < 16; o2 <<= 1) ls += __shfl_xor(ls, o2, 64);
+      lrow[r] = lrow[r] * corr + ls;
+      mrow[r] = mnew[r];
+#pragma unroll
+      for (int t = 0; t < 8; t++) o[t][r] *= corr;
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    // O += P·V
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++) {
+      const h8 pa = *reinterpret_cast<const h8 *>(&pb[c16 * PBS + kk * 32 + g * 8]);
+#pragma unroll
+      for (int t = 0; t < 8; t++) {
+        const h8 vb = *reinterpret_cast<const h8 *>(&sVt[(t * 16 + c16) * VTS + kk * 32 + g * 8]);
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[t], 0, 0, 0);
+      }
+    }
+  }
+
+  TO *O = reinterpret_cast<TO *>(a.out) + (size_t)off * a.ldo + h * HD;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int i = i0 + g * 4 + r;
+    if (i >= T) continue;
+    const float inv = 1.f / lrow[r];
+#pragma unroll
+    for (int t = 0; t < 8; t++) O[(size_t)i * a.ldo + t * 16 + c16] = (TO)(o[t][r] * inv);
+  }
+}
+
+int relpos_attention(fa_ctx *ctx, const AttnArgs &a, int in_f32, int out_f32, int Tmax, const char *label) {
+  const int W = a.win.n;
+  if (a.HD != 128) return set_err(ctx, FA_E_UNSUPPORTED, "%s: head dim %d (kernel is specialised for 128)", label, a.HD);
+  if (Tmax <= 0 || W <= 0) return FA_OK;
+  if (W > kMaxWin) return set_err(ctx, FA_E_INVALID, "%s: %d windows in one launch (max %d)", label, W, kMaxWin);
+  dim3 grid(cdiv(Tmax, 64), a.H, W);
+  ProfScope ps(ctx, label);
+  if (!in_f32 && !out_f32)
+    hipLaunchKernelGGL((relpos_attn_kernel<_Float16, _Float16>), grid, dim3(256), 0, ctx->stream, a);
+  else if (in_f32 && out_f32)
+    hipLaunchKernelGGL((relpos_attn_kernel<float, float>), grid, dim3(256), 0, ctx->stream, a);
+  else
+    return set_err(ctx, FA_E_UNSUPPORTED, "%s: mixed attention I/O types", label);
+  return check_launch(ctx, label);
+}
+
+}  // namespace fa

@@ -1,0 +1,792 @@
+// Fused Parakeet FastConformer encoder: loadParakeetEncoder + parakeetEncodeBatch
+// (src/engines/asr-parakeet/raw-encoder.js:39-161, 177-222, 235-386) as one
+// native forward over a batch of variable-length windows.
+//
+// HBM layout (rows = frames of all windows, packed back to back or padded to
+// the batch's longest window; one row table per stage, see WinStage):
+//   mel      [R0, melBins]     f32   time-major (the reference transposes on the host)
+//   s1       [R1, 64, Csub]    f16   c0 output, channels-last (t, f, c)
+//   s2, s2p  [R2, 32, Csub]    f16   dw c1 output, pw c2 output
+//   s3, s3p  [R3, 16, Csub]    f16   dw c3 output, pw c4 output
+//   x        [R3, D]           f32   residual stream (the returned frames)
+//   h        [R3, D]           f16   LayerNorm outputs (GEMM A operands)
+//   u        [R3, max(DFF,3D)] f16   FF hidden / fused q|k|v
+//   a, g     [R3, D]           f16   attention output, GLU output, dwconv output
+// Channels-last front-end tensors make the 1x1 convs plain GEMMs over (t, f)
+// rows and make the flatten to [T, Csub*Fsub] free: the linear's weight rows
+// are permuted at load from the reference's c*F+f order to f*Csub+c.
+//
+// Per layer (M = R3 rows):  LN -> FF1 (W1+SiLU, W2·½ + x) -> LN -> QKV (one
+// GEMM, N = 3D) -> fused rel-pos attention -> out-proj + x -> LN -> pw1 with
+// the GLU in the GEMM epilogue -> depthwise k=9 + bias + SiLU (per window) ->
+// pw2 + x -> LN -> FF2 -> LN.  Residual adds ride the GEMM epilogues (as the
+// reference's `add` option, raw-encoder.js:282-284).
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "fa_internal.h"
+#include "fa_device.h"
+#include "gemm.h"
+#include "attention.h"
+#include "ops.h"
+
+namespace fa {
+
+// One stage's window table: rows [off[w], off[w]+len[w]) belong to window w.
+typedef WinTable WinStage;
+
+// ── subsampling kernels (channels-last f16) ──────────────────────────────
+// c0: conv2d 1 -> C, 3x3, stride 2, pad 1, bias + ReLU (raw-encoder.js:188).
+// Thread = 8 channels of one (t1, f1) output; the 9 input taps are shared.
+__global__ __launch_bounds__(256) void sub_c0_kernel(const float *__restrict__ mel, int MB, WinStage in, WinStage out, int F1,
+                                                     const float *__restrict__ w, const float *__restrict__ b, _Float16 *__restrict__ y, int C) {
+  const int cg = C / 8, ppb = 256 / cg;
+  const int win = blockIdx.y;
+  const int pidx = blockIdx.x * ppb + threadIdx.x / cg, c0 = (threadIdx.x % cg) * 8;
+  const int T1 = out.len[win];
+  const int t1 = pidx / F1, f1 = pidx % F1;
+  if (t1 >= T1) return;
+  const int T0 = in.len[win];
+  const float *m = mel + (size_t)in.off[win] * MB;
+  float x[9];
+#pragma unroll
+  for (int a = 0; a < 3; a++)
+#pragma unroll
+    for (int bb = 0; bb < 3; bb++) {
+      const int ti = 2 * t1 - 1 + a, fi = 2 * f1 - 1 + bb;
+      x[a * 3 + bb] = (ti >= 0 && ti < T0 && fi >= 0 && fi < MB) ? m[(size_t)ti * MB + fi] : 0.f;
+    }
+  h8 o;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const float *wc = w + (c0 + e) * 9;
+    float acc = b[c0 + e];
+#pragma unroll
+    for (int k = 0; k < 9; k++) acc += x[k] * wc[k];
+    o[e] = (_Float16)fmaxf(acc, 0.f);
+  }
+  *reinterpret_cast<h8 *>(y + (((size_t)(out.off[win] + t1) * F1 + f1) * C + c0)) = o;
+}
+
+// depthwise conv2d 3x3, stride 2, pad 1, + bias, no act (raw-encoder.js:189,191).
+// wt is [9][C] (tap-major) so 8 channels' weights are two float4 loads.
+__global__ __launch_bounds__(256) void sub_dw_kernel(const _Float16 *__restrict__ x, WinStage in, int Fin, WinStage out, int Fout,
+                                                     const float *__restrict__ wt, const float *__restrict__ b, _Float16 *__restrict__ y, int C) {
+  const int cg = C / 8, ppb = 256 / cg;
+  const int win = blockIdx.y;
+  const int pidx = blockIdx.x * ppb + threadIdx.x / cg, c0 = (threadIdx.x % cg) * 8;
+  const int To = out.len[win];
+  const int to = pidx / Fout, fo = pidx % Fout;
+  if (to >= To) return;
+  const int Ti = in.len[win];
+  const _Float16 *xb = x + (size_t)in.off[win] * Fin * C;
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) acc[e] = b[c0 + e];
+#pragma unroll
+  for (int a = 0; a < 3; a++) {
+    const int ti = 2 * to - 1 + a;
+    if (ti < 0 || ti >= Ti) continue;
+#pragma unroll
+    for (int bb = 0; bb < 3; bb++) {
+      const int fi = 2 * fo - 1 + bb;
+      if (fi < 0 || fi >= Fin) continue;
+      const h8 v = *reinterpret_cast<const h8 *>(xb + ((size_t)ti * Fin + fi) * C + c0);
+      const float *wk = wt + (a * 3 + bb) * C + c0;
+#pragma unroll
+      for (int e = 0; e < 8; e++) acc[e] += (float)v[e] * wk[e];
+    }
+  }
+  h8 o;
+#pragma unroll
+  for (int e = 0; e < 8; e++) o[e] = (_Float16)acc[e];
+  *reinterpret_cast<h8 *>(y + (((size_t)(out.off[win] + to) * Fout + fo) * C + c0)) = o;
+}
+
+// Conv module depthwise conv over time, k taps, symmetric pad (k-1)/2,
+// + bias (BatchNorm folded) + SiLU (raw-encoder.js:365-367), per window.
+// Thread = 8 channels x TT consecutive frames; the TT+k-1 input rows are
+// loaded once into registers.
+template <int KT, int TT>
+__global__ __launch_bounds__(128) void dwconv_silu_kernel(const _Float16 *__restrict__ x, _Float16 *__restrict__ y, const float *__restrict__ wt,
+                                                          const float *__restrict__ b, int D, WinStage st) {
+  const int win = blockIdx.y;
+  const int T = st.len[win];
+  const int t0 = blockIdx.x * TT;
+  if (t0 >= T) return;
+  const int c0 = (blockIdx.z * blockDim.x + threadIdx.x) * 8;
+  if (c0 >= D) return;
+  constexpr int PAD = (KT - 1) / 2;
+  const _Float16 *xb = x + (size_t)st.off[win] * D + c0;
+  _Float16 *yb = y + (size_t)st.off[win] * D + c0;
+  h8 in[TT + KT - 1];
+#pragma unroll
+  for (int r = 0; r < TT + KT - 1; r++) {
+    const int t = t0 - PAD + r;
+    if (t >= 0 && t < T)
+      in[r] = *reinterpret_cast<const h8 *>(xb + (size_t)t * D);
+    else
+      in[r] = h8{0, 0, 0, 0, 0, 0, 0, 0};
+  }
+  float wk[KT][8];
+#pragma unroll
+  for (int k = 0; k < KT; k++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) wk[k][e] = wt[k * D + c0 + e];
+  float bb[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) bb[e] = b[c0 + e];
+#pragma unroll
+  for (int t = 0; t < TT; t++) {
+    if (t0 + t >= T) break;
+    h8 o;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < KT; k++) acc += (float)in[t + k][e] * wk[k][e];
+      o[e] = (_Float16)silu_f(acc + bb[e]);
+    }
+    *reinterpret_cast<h8 *>(yb + (size_t)(t0 + t) * D) = o;
+  }
+}
+
+// Zero rows of a padded batch past each window's length (output contract).
+__global__ void zero_pad_rows_kernel(float *x, int D, WinStage st, int Tpad) {
+  const int win = blockIdx.y;
+  const int r = blockIdx.x;
+  if (r < st.len[win] || r >= Tpad) return;
+  float *row = x + (size_t)(st.off[win] + r) * D;
+  for (int j = threadIdx.x; j < D; j += blockDim.x) row[j] = 0.f;
+}
+
+// f32 -> f16 conversion (load-time positional table)
+__global__ void f32_to_f16_kernel(const float *x, _Float16 *y, long n) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) y[i] = (_Float16)x[i];
+}
+
+// ── host-side weight preparation ─────────────────────────────────────────
+static uint16_t h_f32_to_f16(float f) { return __half_as_ushort(__float2half_rn(f)); }
+static float h_f16_to_f32(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+
+// A linear's device weights in one of the three storage formats.
+struct Lin {
+  void *w = nullptr;          // f16 [N][K] | int8 [N][K] | int4 [N][K/32][16 B]
+  void *scales = nullptr;     // int4: f16 bits [N][K/32]
+  float *colscale = nullptr;  // int8: s[n]·fold[n]; int4: fold[n] (null when all 1)
+  float *bias = nullptr;      // [N] (folded), or null
+  int bkind = B_F16;
+  int N = 0, K = 0;
+};
+
+}  // namespace fa
+
+struct fa_encoder {
+  fa_ctx *ctx = nullptr;
+  fa_encoder_cfg cfg{};
+  int format = FA_W_F16;
+  int maxT = 0;
+  std::vector<void *> allocs;
+  // front end
+  float *c0w = nullptr, *c0b = nullptr, *c1w = nullptr, *c1b = nullptr, *c3w = nullptr, *c3b = nullptr;
+  fa::Lin c2, c4, lin;
+  struct Layer {
+    float *ln[5][2];
+    fa::Lin ff1w1, ff1w2, qkv, out, pw1, pw2, ff2w1, ff2w2;
+    float *pbu = nullptr, *pbv = nullptr, *dww = nullptr, *dwb = nullptr;
+    _Float16 *P = nullptr;  // [2*maxT-1, D]
+  };
+  std::vector<Layer> L;
+  // workspace (grow-only)
+  void *s1 = nullptr, *s2 = nullptr, *s2p = nullptr, *s3 = nullptr, *s3p = nullptr, *h = nullptr, *u = nullptr, *a = nullptr, *g = nullptr;
+  size_t cap_s1 = 0, cap_s2 = 0, cap_s2p = 0, cap_s3 = 0, cap_s3p = 0, cap_m = 0, cap_u = 0;
+};
+
+namespace fa {
+
+template <typename T>
+static T *dupload(fa_encoder *e, const T *host, size_t n) {
+  T *d = (T *)dev_alloc(e->ctx, n * sizeof(T) + 16);
+  if (!d) return nullptr;
+  e->allocs.push_back(d);
+  if (hipMemcpy(d, host, n * sizeof(T), hipMemcpyHostToDevice) != hipSuccess) return nullptr;
+  return d;
+}
+
+// Build a linear from Bt [N][K] raw f32 values (column n of the reference's
+// [K, N] matrix is row n here), a per-column fold factor, optional bias.
+static int build_lin(fa_encoder *e, Lin &L, const std::vector<float> &bt, int N, int K, const std::vector<float> &fold, const std::vector<float> *bias,
+                     const char *name) {
+  fa_ctx *ctx = e->ctx;
+  L.N = N;
+  L.K = K;
+  bool unit = true;
+  for (float f : fold) unit &= (f == 1.f);
+  if (bias) {
+    std::vector<float> bb(N);
+    for (int n = 0; n < N; n++) bb[n] = (float)((double)(*bias)[n] * fold[n]);
+    if (!(L.bias = dupload(e, bb.data(), N))) return set_err(ctx, FA_E_OOM, "encoder load: %s bias", name);
+  }
+  if (e->format == FA_W_F16) {
+    std::vector<uint16_t> h((size_t)N * K);
+    for (int n = 0; n < N; n++)
+      for (int k = 0; k < K; k++) h[(size_t)n * K + k] = h_f32_to_f16((float)((double)bt[(size_t)n * K + k] * fold[n]));
+    if (!(L.w = dupload(e, h.data(), h.size()))) return set_err(ctx, FA_E_OOM, "encoder load: %s", name);
+    L.bkind = B_F16;
+    return FA_OK;
+  }
+  if (e->format == FA_W_INT8) {
+    // per-output-column symmetric (quantize-parakeet-encoder.py:31-36)
+    std::vector<int8_t> q((size_t)N * K);
+    std::vector<float> cs(N);
+    for (int n = 0; n < N; n++) {
+      float mx = 0.f;
+      for (int k = 0; k < K; k++) mx = std::fmax(mx, std::fabs(bt[(size_t)n * K + k]));
+      float s = mx / 127.0f;
+      if (s == 0.f) s = 1.f;
+      for (int k = 0; k < K; k++) {
+        float r = std::rint(bt[(size_t)n * K + k] / s);
+        r = r < -127.f ? -127.f : (r > 127.f ? 127.f : r);
+        q[(size_t)n * K + k] = (int8_t)r;
+      }
+      cs[n] = (float)((double)s * fold[n]);
+    }
+    if (!(L.w = dupload(e, q.data(), q.size())) || !(L.colscale = dupload(e, cs.data(), N))) return set_err(ctx, FA_E_OOM, "encoder load: %s", name);
+    L.bkind = B_I8;
+    return FA_OK;
+  }
+  // int4 symmetric group-32, f16 scales, MatMulNBits nibble order (low = even k)
+  if (K % 32) return set_err(ctx, FA_E_UNSUPPORTED, "encoder load: %s K=%d not a multiple of 32 for int4", name, K);
+  const int nblk = K / 32;
+  std::vector<uint8_t> q((size_t)N * nblk * 16, 0x88);
+  std::vector<uint16_t> sc((size_t)N * nblk);
+  for (int n = 0; n < N; n++)
+    for (int b = 0; b < nblk; b++) {
+      float mx = 0.f;
+      for (int t = 0; t < 32; t++) mx = std::fmax(mx, std::fabs(bt[(size_t)n * K + b * 32 + t]));
+      uint16_t sh = h_f32_to_f16(mx / 7.0f);
+      float s = h_f16_to_f32(sh);
+      if (s == 0.f) {
+        sh = 0x3c00;
+        s = 1.f;
+      }
+      sc[(size_t)n * nblk + b] = sh;
+      uint8_t *blk = &q[((size_t)n * nblk + b) * 16];
+      for (int t = 0; t < 32; t++) {
+        float r = std::rint(bt[(size_t)n * K + b * 32 + t] / s);
+        r = r < -8.f ? -8.f : (r > 7.f ? 7.f : r);
+        const uint8_t nib = (uint8_t)((int)r + 8);
+        blk[t / 2] = (t & 1) ? (uint8_t)((blk[t / 2] & 0x0f) | (nib << 4)) : (uint8_t)((blk[t / 2] & 0xf0) | nib);
+      }
+    }
+  if (!(L.w = dupload(e, q.data(), q.size())) || !(L.scales = dupload(e, sc.data(), sc.size()))) return set_err(ctx, FA_E_OOM, "encoder load: %s", name);
+  if (!unit && !(L.colscale = dupload(e, fold.data(), N))) return set_err(ctx, FA_E_OOM, "encoder load: %s", name);
+  L.bkind = B_I4;
+  return FA_OK;
+}
+
+// Quantise-dequantise raw Bt values the way the chosen format stores them
+// (used for the pos weights, which only enter through the load-time table).
+static void roundtrip_format(int format, std::vector<float> &bt, int N, int K) {
+  if (format == FA_W_INT8) {
+    for (int n = 0; n < N; n++) {
+      float mx = 0.f;
+      for (int k = 0; k < K; k++) mx = std::fmax(mx, std::fabs(bt[(size_t)n * K + k]));
+      float s = mx / 127.0f;
+      if (s == 0.f) s = 1.f;
+      for (int k = 0; k < K; k++) {
+        float r = std::rint(bt[(size_t)n * K + k] / s);
+        r = r < -127.f ? -127.f : (r > 127.f ? 127.f : r);
+        bt[(size_t)n * K + k] = r * s;
+      }
+    }
+  } else if (format == FA_W_INT4) {
+    for (int n = 0; n < N; n++)
+      for (int b = 0; b < K / 32; b++) {
+        float mx = 0.f;
+        for (int t = 0; t < 32; t++) mx = std::fmax(mx, std::fabs(bt[(size_t)n * K + b * 32 + t]));
+        float s = h_f16_to_f32(h_f32_to_f16(mx / 7.0f));
+        if (s == 0.f) s = 1.f;
+        for (int t = 0; t < 32; t++) {
+          float r = std::rint(bt[(size_t)n * K + b * 32 + t] / s);
+          r = r < -8.f ? -8.f : (r > 7.f ? 7.f : r);
+          bt[(size_t)n * K + b * 32 + t] = r * s;
+        }
+      }
+  }
+}
+
+static void set_gemm_b(GemmArgs &p, const Lin &L) {
+  p.B = L.w;
+  p.bkind = L.bkind;
+  p.bscale = L.scales;
+  p.bscale_f32 = 0;
+  p.colscale = L.colscale;
+  p.bias = L.bias;
+  p.N = L.N;
+  p.K = L.K;
+}
+
+static int grow(fa_encoder *e, void **buf, size_t *cap, size_t need) {
+  if (need <= *cap) return FA_OK;
+  if (*buf) {
+    (void)hipStreamSynchronize(e->ctx->stream);
+    (void)hipFree(*buf);
+    *buf = nullptr;
+    *cap = 0;
+  }
+  *buf = dev_alloc(e->ctx, need);
+  if (!*buf) return FA_E_OOM;
+  *cap = need;
+  return FA_OK;
+}
+
+static inline int stride2_len(int T) { return T <= 0 ? 0 : (T - 1) / 2 + 1; }
+
+}  // namespace fa
+
+using namespace fa;
+
+extern "C" {
+
+int fa_encoder_tsub(int T) { return stride2_len(stride2_len(stride2_len(T))); }
+
+void fa_encoder_destroy(fa_encoder *enc) {
+  if (!enc) return;
+  (void)hipStreamSynchronize(enc->ctx->stream);
+  for (void *p : enc->allocs) (void)hipFree(p);
+  for (void *p : {enc->s1, enc->s2, enc->s2p, enc->s3, enc->s3p, enc->h, enc->u, enc->a, enc->g})
+    if (p) (void)hipFree(p);
+  delete enc;
+}
+
+int fa_encoder_load(fa_ctx *ctx, const fa_encoder_cfg *cfg, int n, const char *const *names, const float *const *data, const int64_t *counts,
+                    int format, int max_T, fa_encoder **out) {
+  if (!ctx || !cfg || !out) return FA_E_INVALID;
+  *out = nullptr;
+  const fa_encoder_cfg c = *cfg;
+  if (c.HD != 128 || c.H * c.HD != c.D) return set_err(ctx, FA_E_UNSUPPORTED, "encoder: needs HD=128 and H*HD=D (got H=%d HD=%d D=%d)", c.H, c.HD, c.D);
+  if (c.D % 64 || c.DFF % 64 || c.Csub % 64 || c.melBins != 8 * c.Fsub || (c.Csub * c.Fsub) % 64)
+    return set_err(ctx, FA_E_UNSUPPORTED, "encoder: D, DFF, Csub must be multiples of 64 and melBins = 8*Fsub");
+  if (c.Csub / 8 > 256 || 256 % (c.Csub / 8)) return set_err(ctx, FA_E_UNSUPPORTED, "encoder: Csub/8 must divide 256");
+  if (c.dwK != 9) return set_err(ctx, FA_E_UNSUPPORTED, "encoder: depthwise kernel %d (9 supported)", c.dwK);
+  if (max_T <= 0 || max_T > 1024) return set_err(ctx, FA_E_INVALID, "encoder: max_T %d outside 1..1024", max_T);
+  if (format < FA_W_F16 || format > FA_W_INT4) return set_err(ctx, FA_E_INVALID, "encoder: weight format %d", format);
+  std::unordered_map<std::string, std::pair<const float *, int64_t>> man;
+  for (int i = 0; i < n; i++) man[names[i]] = {data[i], counts[i]};
+  auto get = [&](const std::string &k, int64_t cnt, bool optional, const float **p) -> int {
+    auto it = man.find(k);
+    if (it == man.end()) {
+      if (optional) {
+        *p = nullptr;
+        return FA_OK;
+      }
+      return set_err(ctx, FA_E_INVALID, "encoder load: missing tensor %s", k.c_str());
+    }
+    if (it->second.second != cnt) return set_err(ctx, FA_E_INVALID, "encoder load: %s has %lld values, expected %lld", k.c_str(), (long long)it->second.second, (long long)cnt);
+    *p = it->second.first;
+    return FA_OK;
+  };
+  fa_encoder *e = new fa_encoder();
+  e->ctx = ctx;
+  e->cfg = c;
+  e->format = format;
+  e->maxT = max_T;
+  auto fail = [&](int st) {
+    fa_encoder_destroy(e);
+    return st;
+  };
+  const int D = c.D, DFF = c.DFF, C = c.Csub, F = c.Fsub;
+  const double INV = 1.0 / std::sqrt((double)c.HD);
+  // ── front end ──
+  const float *p;
+  int st;
+  if ((st = get("c0w", (int64_t)C * 9, false, &p))) return fail(st);
+  e->c0w = dupload(e, p, (size_t)C * 9);
+  if ((st = get("c0b", C, false, &p))) return fail(st);
+  e->c0b = dupload(e, p, C);
+  for (int i : {1, 3}) {
+    const float *w, *b;
+    if ((st = get("c" + std::to_string(i) + "w", (int64_t)C * 9, false, &w))) return fail(st);
+    if ((st = get("c" + std::to_string(i) + "b", C, false, &b))) return fail(st);
+    std::vector<float> wt((size_t)9 * C);
+    for (int ch = 0; ch < C; ch++)
+      for (int k = 0; k < 9; k++) wt[(size_t)k * C + ch] = w[ch * 9 + k];
+    float *dw = dupload(e, wt.data(), wt.size()), *db = dupload(e, b, C);
+    if (i == 1) {
+      e->c1w = dw;
+      e->c1b = db;
+    } else {
+      e->c3w = dw;
+      e->c3b = db;
+    }
+  }
+  {
+    // pointwise convs and the linear stay f16 in every format (the quantised
+    // formats cover the conformer layers' linears)
+    const int saved = e->format;
+    e->format = FA_W_F16;
+    for (int i : {2, 4}) {
+      const float *w, *b;
+      if ((st = get("c" + std::to_string(i) + "w", (int64_t)C * C, false, &w))) return fail(st);
+      if ((st = get("c" + std::to_string(i) + "b", C, false, &b))) return fail(st);
+      std::vector<float> bt(w, w + (size_t)C * C), bias(b, b + C), fold(C, 1.f);  // [cout][cin] is already Bt
+      if ((st = build_lin(e, i == 2 ? e->c2 : e->c4, bt, C, C, fold, &bias, "pw conv"))) return fail(st);
+    }
+    const float *w, *b;
+    if ((st = get("linw", (int64_t)C * F * D, false, &w))) return fail(st);
+    if ((st = get("linb", D, false, &b))) return fail(st);
+    std::vector<float> bt((size_t)D * C * F);
+    for (int nn = 0; nn < D; nn++)
+      for (int f = 0; f < F; f++)
+        for (int ch = 0; ch < C; ch++) bt[(size_t)nn * C * F + f * C + ch] = w[(size_t)(ch * F + f) * D + nn];
+    std::vector<float> bias(b, b + D), fold(D, 1.f);
+    if ((st = build_lin(e, e->lin, bt, D, C * F, fold, &bias, "linw"))) return fail(st);
+    e->format = saved;
+  }
+  // positional table pe(maxT) (raw-encoder.js:163-174), f32 on the device
+  const int PR = 2 * max_T - 1;
+  std::vector<float> pe((size_t)PR * D);
+  {
+    const double lg = std::log(10000.0) / D;
+    for (int pi = 0; pi < PR; pi++) {
+      const double pos = max_T - 1 - pi;
+      for (int i = 0; i < D; i += 2) {
+        const double dv = std::exp(i * -lg);
+        pe[(size_t)pi * D + i] = (float)std::sin(pos * dv);
+        pe[(size_t)pi * D + i + 1] = (float)std::cos(pos * dv);
+      }
+    }
+  }
+  float *pe_d = (float *)dev_alloc(ctx, pe.size() * 4);
+  if (!pe_d) return fail(FA_E_OOM);
+  (void)hipMemcpy(pe_d, pe.data(), pe.size() * 4, hipMemcpyHostToDevice);
+  float *ptmp = (float *)dev_alloc(ctx, pe.size() * 4);
+  if (!ptmp) {
+    (void)hipFree(pe_d);
+    return fail(FA_E_OOM);
+  }
+  // ── layers ──
+  e->L.resize(c.layers);
+  static const char *lnk[5] = {"lnff1", "lnatt", "lnconv", "lnff2", "lnout"};
+  for (int li = 0; li < c.layers; li++) {
+    auto g = [&](const char *s) { return "L" + std::to_string(li) + "_" + s; };
+    auto &Ly = e->L[li];
+    for (int j = 0; j < 5; j++) {
+      const float *gw, *gb;
+      if ((st = get(g(lnk[j]) + "_w", D, false, &gw)) || (st = get(g(lnk[j]) + "_b", D, false, &gb))) return fail(st);
+      Ly.ln[j][0] = dupload(e, gw, D);
+      Ly.ln[j][1] = dupload(e, gb, D);
+    }
+    auto kn_to_bt = [](const float *w, int K, int N) {
+      std::vector<float> bt((size_t)N * K);
+      for (int k = 0; k < K; k++)
+        for (int nn = 0; nn < N; nn++) bt[(size_t)nn * K + k] = w[(size_t)k * N + nn];
+      return bt;
+    };
+    auto optvec = [&](const char *k, int cnt, std::vector<float> &dst) -> int {
+      const float *b;
+      int s = get(g(k), cnt, true, &b);
+      if (s) return s;
+      if (b) dst.assign(b, b + cnt);
+      return FA_OK;
+    };
+    // feed-forwards (W2 and b2 carry the macaron 0.5, raw-encoder.js:129-131)
+    for (int ffi = 0; ffi < 2; ffi++) {
+      const char *w1n = ffi ? "ff2w1" : "ff1w1", *w2n = ffi ? "ff2w2" : "ff1w2", *b1n = ffi ? "ff2b1" : "ff1b1", *b2n = ffi ? "ff2b2" : "ff1b2";
+      const float *w1, *w2;
+      if ((st = get(g(w1n), (int64_t)D * DFF, false, &w1)) || (st = get(g(w2n), (int64_t)DFF * D, false, &w2))) return fail(st);
+      std::vector<float> b1, b2;
+      if ((st = optvec(b1n, DFF, b1)) || (st = optvec(b2n, D, b2))) return fail(st);
+      Lin &L1 = ffi ? Ly.ff2w1 : Ly.ff1w1, &L2 = ffi ? Ly.ff2w2 : Ly.ff1w2;
+      if ((st = build_lin(e, L1, kn_to_bt(w1, D, DFF), DFF, D, std::vector<float>(DFF, 1.f), b1.empty() ? nullptr : &b1, w1n))) return fail(st);
+      if ((st = build_lin(e, L2, kn_to_bt(w2, DFF, D), D, DFF, std::vector<float>(D, 0.5f), b2.empty() ? nullptr : &b2, w2n))) return fail(st);
+    }
+    // fused q|k|v, q (and its bias) carrying 1/sqrt(HD) (raw-encoder.js:133,138)
+    {
+      const float *wq, *wk, *wv;
+      if ((st = get(g("q"), (int64_t)D * D, false, &wq)) || (st = get(g("k"), (int64_t)D * D, false, &wk)) || (st = get(g("v"), (int64_t)D * D, false, &wv)))
+        return fail(st);
+      std::vector<float> bt((size_t)3 * D * D), fold(3 * D, 1.f);
+      const float *ws[3] = {wq, wk, wv};
+      for (int part = 0; part < 3; part++)
+        for (int k = 0; k < D; k++)
+          for (int nn = 0; nn < D; nn++) bt[(size_t)(part * D + nn) * D + k] = ws[part][(size_t)k * D + nn];
+      for (int nn = 0; nn < D; nn++) fold[nn] = (float)INV;
+      std::vector<float> bq, bk, bv;
+      if ((st = optvec("qb", D, bq)) || (st = optvec("kb", D, bk)) || (st = optvec("vb", D, bv))) return fail(st);
+      std::vector<float> bias;
+      if (!bq.empty() || !bk.empty() || !bv.empty()) {
+        bias.assign(3 * D, 0.f);
+        for (int nn = 0; nn < D; nn++) {
+          if (!bq.empty()) bias[nn] = bq[nn];
+          if (!bk.empty()) bias[D + nn] = bk[nn];
+          if (!bv.empty()) bias[2 * D + nn] = bv[nn];
+        }
+      }
+      if ((st = build_lin(e, Ly.qkv, bt, 3 * D, D, fold, bias.empty() ? nullptr : &bias, "qkv"))) return fail(st);
+    }
+    {
+      const float *wo;
+      if ((st = get(g("out"), (int64_t)D * D, false, &wo))) return fail(st);
+      std::vector<float> bo;
+      if ((st = optvec("outb", D, bo))) return fail(st);
+      if ((st = build_lin(e, Ly.out, kn_to_bt(wo, D, D), D, D, std::vector<float>(D, 1.f), bo.empty() ? nullptr : &bo, "out"))) return fail(st);
+    }
+    // pos_bias_u/v · 1/sqrt(HD) (raw-encoder.js:124-125)
+    {
+      const float *pu, *pv;
+      if ((st = get(g("pbu"), D, false, &pu)) || (st = get(g("pbv"), D, false, &pv))) return fail(st);
+      std::vector<float> a(D), b(D);
+      for (int i = 0; i < D; i++) {
+        a[i] = (float)((double)pu[i] * INV);
+        b[i] = (float)((double)pv[i] * INV);
+      }
+      Ly.pbu = dupload(e, a.data(), D);
+      Ly.pbv = dupload(e, b.data(), D);
+    }
+    // conv module: pw1 columns permuted for the GLU epilogue (value c at
+    // 16(c/8)+c%8, gate c+D at 16(c/8)+8+c%8)
+    {
+      const float *w1, *w2, *dw, *dwb;
+      if ((st = get(g("pw1"), (int64_t)2 * D * D, false, &w1)) || (st = get(g("pw2"), (int64_t)D * D, false, &w2)) ||
+          (st = get(g("dw"), (int64_t)D * 9, false, &dw)) || (st = get(g("dwb"), D, false, &dwb)))
+        return fail(st);
+      std::vector<float> b1, b2;
+      if ((st = optvec("pw1b", 2 * D, b1)) || (st = optvec("pw2b", D, b2))) return fail(st);
+      std::vector<float> bt((size_t)2 * D * D), bp;
+      if (!b1.empty()) bp.assign(2 * D, 0.f);
+      for (int ch = 0; ch < D; ch++) {
+        const int jv = 16 * (ch / 8) + ch % 8, jg = jv + 8;
+        std::memcpy(&bt[(size_t)jv * D], w1 + (size_t)ch * D, D * 4);
+        std::memcpy(&bt[(size_t)jg * D], w1 + (size_t)(ch + D) * D, D * 4);
+        if (!b1.empty()) {
+          bp[jv] = b1[ch];
+          bp[jg] = b1[ch + D];
+        }
+      }
+      if ((st = build_lin(e, Ly.pw1, bt, 2 * D, D, std::vector<float>(2 * D, 1.f), bp.empty() ? nullptr : &bp, "pw1"))) return fail(st);
+      std::vector<float> bt2(w2, w2 + (size_t)D * D);
+      if ((st = build_lin(e, Ly.pw2, bt2, D, D, std::vector<float>(D, 1.f), b2.empty() ? nullptr : &b2, "pw2"))) return fail(st);
+      std::vector<float> wt((size_t)9 * D);
+      for (int ch = 0; ch < D; ch++)
+        for (int k = 0; k < 9; k++) wt[(size_t)k * D + ch] = dw[ch * 9 + k];
+      Ly.dww = dupload(e, wt.data(), wt.size());
+      Ly.dwb = dupload(e, dwb, D);
+    }
+    // projected positional table P = pe · Wpos, cached for every T <= maxT
+    // (the reference caches it per (layer, Tsub), raw-encoder.js:305-321)
+    {
+      const float *wp;
+      if ((st = get(g("pos"), (int64_t)D * D, false, &wp))) return fail(st);
+      std::vector<float> bt = kn_to_bt(wp, D, D);
+      roundtrip_format(format, bt, D, D);
+      std::vector<uint16_t> h((size_t)D * D);
+      for (size_t i = 0; i < h.size(); i++) h[i] = h_f32_to_f16(bt[i]);
+      void *wpd = dev_alloc(ctx, h.size() * 2);
+      if (!wpd) return fail(FA_E_OOM);
+      (void)hipMemcpy(wpd, h.data(), h.size() * 2, hipMemcpyHostToDevice);
+      Ly.P = (_Float16 *)dev_alloc(ctx, (size_t)PR * D * 2);
+      if (!Ly.P) return fail(FA_E_OOM);
+      e->allocs.push_back(Ly.P);
+      GemmArgs pa;
+      pa.A = pe_d; pa.lda = D; pa.akind = A_F32;
+      pa.B = wpd; pa.bkind = B_F16;
+      pa.C = ptmp; pa.ldc = D;
+      pa.M = PR; pa.N = D; pa.K = D;
+      st = gemm_mfma(ctx, pa, "pos_table");
+      if (!st) {
+        hipLaunchKernelGGL(f32_to_f16_kernel, dim3(1024), dim3(256), 0, ctx->stream, ptmp, Ly.P, (long)PR * D);
+        st = check_launch(ctx, "pos_table_f16");
+      }
+      (void)hipStreamSynchronize(ctx->stream);
+      (void)hipFree(wpd);
+      if (st) {
+        (void)hipFree(pe_d);
+        (void)hipFree(ptmp);
+        return fail(st);
+      }
+    }
+    for (auto &ln : Ly.ln)
+      if (!ln[0] || !ln[1]) return fail(set_err(ctx, FA_E_OOM, "encoder load: layer %d", li));
+  }
+  (void)hipFree(pe_d);
+  (void)hipFree(ptmp);
+  if (!e->c0w || !e->c0b || !e->c1w || !e->c1b || !e->c3w || !e->c3b) return fail(set_err(ctx, FA_E_OOM, "encoder load: front end"));
+  *out = e;
+  return FA_OK;
+}
+
+int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t *lens, int n, int layout, int layers_run, fa_tensor *out) {
+  if (!e || e->ctx != ctx) return set_err(ctx, FA_E_INVALID, "encoderForward: encoder belongs to another context");
+  if (n <= 0) return set_err(ctx, FA_E_INVALID, "encoderForward: no windows");
+  if (n > kMaxWin) return set_err(ctx, FA_E_UNSUPPORTED, "encoderForward: %d windows in one batch (max %d)", n, kMaxWin);
+  if (layout != 0 && layout != 1) return set_err(ctx, FA_E_INVALID, "encoderForward: layout %d", layout);
+  const fa_encoder_cfg &c = e->cfg;
+  const int D = c.D, C = c.Csub, MB = c.melBins;
+  const int F1 = stride2_len(MB), F2 = stride2_len(F1), F3 = stride2_len(F2);
+  if (F3 != c.Fsub) return set_err(ctx, FA_E_INVALID, "encoderForward: melBins %d gives %d freq bins, manifest has %d", MB, F3, c.Fsub);
+  TensorRec *rm;
+  FA_TRY(need(ctx, mel, &rm, "encoderForward mel"));
+  if (rm->kind != S_F32 || rm->cols != MB) return set_err(ctx, FA_E_INVALID, "encoderForward: mel must be f32 [rows, %d]", MB);
+  // per-stage window tables
+  WinStage s0{}, s1{}, s2{}, s3{};
+  s0.n = s1.n = s2.n = s3.n = n;
+  int mx[4] = {0, 0, 0, 0};
+  for (int i = 0; i < n; i++) {
+    if (lens[i] <= 0) return set_err(ctx, FA_E_INVALID, "encoderForward: window %d has length %d", i, lens[i]);
+    s0.len[i] = lens[i];
+    s1.len[i] = stride2_len(lens[i]);
+    s2.len[i] = stride2_len(s1.len[i]);
+    s3.len[i] = stride2_len(s2.len[i]);
+    if (s3.len[i] > e->maxT) return set_err(ctx, FA_E_INVALID, "encoderForward: window %d subsamples to %d frames > max_T %d", i, s3.len[i], e->maxT);
+    mx[0] = std::max(mx[0], s0.len[i]);
+    mx[1] = std::max(mx[1], s1.len[i]);
+    mx[2] = std::max(mx[2], s2.len[i]);
+    mx[3] = std::max(mx[3], s3.len[i]);
+  }
+  WinStage *ss[4] = {&s0, &s1, &s2, &s3};
+  int R[4];
+  for (int s = 0; s < 4; s++) {
+    int acc = 0;
+    for (int i = 0; i < n; i++) {
+      ss[s]->off[i] = layout == 0 ? acc : i * mx[s];
+      acc += layout == 0 ? ss[s]->len[i] : mx[s];
+    }
+    R[s] = acc;
+  }
+  if (rm->rows < R[0]) return set_err(ctx, FA_E_INVALID, "encoderForward: mel has %d rows, windows need %d", rm->rows, R[0]);
+  const int M = R[3];
+  const int layers = layers_run < 0 ? c.layers : std::min(layers_run, c.layers);
+  // workspace
+  FA_TRY(grow(e, &e->s1, &e->cap_s1, (size_t)R[1] * F1 * C * 2));
+  FA_TRY(grow(e, &e->s2, &e->cap_s2, (size_t)R[2] * F2 * C * 2));
+  FA_TRY(grow(e, &e->s2p, &e->cap_s2p, (size_t)R[2] * F2 * C * 2));
+  FA_TRY(grow(e, &e->s3, &e->cap_s3, (size_t)R[3] * F3 * C * 2));
+  FA_TRY(grow(e, &e->s3p, &e->cap_s3p, (size_t)R[3] * F3 * C * 2));
+  const size_t need_m = (size_t)M * D * 2, need_u = (size_t)M * std::max(c.DFF, 3 * D) * 2;
+  if (need_m > e->cap_m) {
+    size_t c1 = 0, c2 = 0, c3 = 0;
+    if (e->h) { (void)hipStreamSynchronize(ctx->stream); (void)hipFree(e->h); (void)hipFree(e->a); (void)hipFree(e->g); e->h = e->a = e->g = nullptr; }
+    FA_TRY(grow(e, &e->h, &c1, need_m));
+    FA_TRY(grow(e, &e->a, &c2, need_m));
+    FA_TRY(grow(e, &e->g, &c3, need_m));
+    e->cap_m = need_m;
+  }
+  FA_TRY(grow(e, &e->u, &e->cap_u, need_u));
+  fa_tensor ox;
+  TensorRec *rx;
+  FA_TRY(new_tensor(ctx, M, D, S_F32, (size_t)M * D * 4, &ox, &rx));
+  rm = get(ctx, mel);
+  float *x = (float *)rx->ptr;
+  _Float16 *h = (_Float16 *)e->h, *u = (_Float16 *)e->u, *a = (_Float16 *)e->a, *gg = (_Float16 *)e->g;
+  const int cg = C / 8, ppb = 256 / cg;
+
+  // ── subsampling ──
+  {
+    ProfScope ps(ctx, "sub_c0");
+    hipLaunchKernelGGL(sub_c0_kernel, dim3(cdiv((long)mx[1] * F1, ppb), n), dim3(256), 0, ctx->stream, (const float *)rm->ptr, MB, s0, s1, F1,
+                       e->c0w, e->c0b, (_Float16 *)e->s1, C);
+    FA_TRY(check_launch(ctx, "sub_c0"));
+  }
+  {
+    ProfScope ps(ctx, "sub_dw1");
+    hipLaunchKernelGGL(sub_dw_kernel, dim3(cdiv((long)mx[2] * F2, ppb), n), dim3(256), 0, ctx->stream, (const _Float16 *)e->s1, s1, F1, s2, F2,
+                       e->c1w, e->c1b, (_Float16 *)e->s2, C);
+    FA_TRY(check_launch(ctx, "sub_dw1"));
+  }
+  {
+    GemmArgs p;
+    p.A = e->s2; p.lda = C; p.akind = A_F16;
+    set_gemm_b(p, e->c2);
+    p.C = e->s2p; p.ldc = C; p.out_f16 = 1; p.act = FA_ACT_RELU;
+    p.M = R[2] * F2;
+    FA_TRY(gemm_mfma(ctx, p, "sub_pw2"));
+  }
+  {
+    ProfScope ps(ctx, "sub_dw3");
+    hipLaunchKernelGGL(sub_dw_kernel, dim3(cdiv((long)mx[3] * F3, ppb), n), dim3(256), 0, ctx->stream, (const _Float16 *)e->s2p, s2, F2, s3, F3,
+                       e->c3w, e->c3b, (_Float16 *)e->s3, C);
+    FA_TRY(check_launch(ctx, "sub_dw3"));
+  }
+  {
+    GemmArgs p;
+    p.A = e->s3; p.lda = C; p.akind = A_F16;
+    set_gemm_b(p, e->c4);
+    p.C = e->s3p; p.ldc = C; p.out_f16 = 1; p.act = FA_ACT_RELU;
+    p.M = R[3] * F3;
+    FA_TRY(gemm_mfma(ctx, p, "sub_pw4"));
+  }
+  {
+    GemmArgs p;
+    p.A = e->s3p; p.lda = C * F3; p.akind = A_F16;
+    set_gemm_b(p, e->lin);
+    p.C = x; p.ldc = D;
+    p.M = M;
+    FA_TRY(gemm_mfma(ctx, p, "sub_linear"));
+  }
+
+  // ── conformer layers ──
+  auto gemm = [&](const void *A, int lda, const Lin &L, void *Cp, int ldc, int out_f16, int act, const float *add, int glu, const char *label) {
+    GemmArgs p;
+    p.A = A; p.lda = lda; p.akind = A_F16;
+    set_gemm_b(p, L);
+    p.C = Cp; p.ldc = ldc; p.out_f16 = out_f16; p.act = act;
+    p.add = add; p.ldadd = ldc; p.glu = glu;
+    p.M = M;
+    return gemm_mfma(ctx, p, label);
+  };
+  AttnArgs at;
+  at.q = u; at.k = u + D; at.v = u + 2 * D;
+  at.ldq = at.ldk = at.ldv = 3 * D;
+  at.ldp = D; at.prows = 2 * e->maxT - 1; at.pcenter = e->maxT - 1;
+  at.out = a; at.ldo = D;
+  at.H = c.H; at.HD = c.HD;
+  at.win.n = n;
+  for (int i = 0; i < n; i++) {
+    at.win.off[i] = s3.off[i];
+    at.win.len[i] = s3.len[i];
+  }
+  for (int li = 0; li < layers; li++) {
+    auto &Ly = e->L[li];
+    // FF1
+    FA_TRY(layernorm_launch(ctx, x, Ly.ln[0][0], Ly.ln[0][1], h, 1, M, D, D, D, 1e-5f, "ln_ff1"));
+    FA_TRY(gemm(h, D, Ly.ff1w1, u, c.DFF, 1, FA_ACT_SILU, nullptr, 0, "ff1_w1"));
+    FA_TRY(gemm(u, c.DFF, Ly.ff1w2, x, D, 0, FA_ACT_NONE, x, 0, "ff1_w2"));
+    // attention
+    FA_TRY(layernorm_launch(ctx, x, Ly.ln[1][0], Ly.ln[1][1], h, 1, M, D, D, D, 1e-5f, "ln_att"));
+    FA_TRY(gemm(h, D, Ly.qkv, u, 3 * D, 1, FA_ACT_NONE, nullptr, 0, "qkv"));
+    at.pos = Ly.P;
+    at.pbu = Ly.pbu;
+    at.pbv = Ly.pbv;
+    FA_TRY(relpos_attention(ctx, at, 0, 0, mx[3], "attention"));
+    FA_TRY(gemm(a, D, Ly.out, x, D, 0, FA_ACT_NONE, x, 0, "attn_out"));
+    // conv module
+    FA_TRY(layernorm_launch(ctx, x, Ly.ln[2][0], Ly.ln[2][1], h, 1, M, D, D, D, 1e-5f, "ln_conv"));
+    FA_TRY(gemm(h, D, Ly.pw1, gg, D, 1, FA_ACT_NONE, nullptr, 1, "pw1_glu"));
+    {
+      ProfScope ps(ctx, "dwconv");
+      const int thr = std::min(128, D / 8);
+      hipLaunchKernelGGL((dwconv_silu_kernel<9, 16>), dim3(cdiv(mx[3], 16), n, cdiv(D / 8, thr)), dim3(thr), 0, ctx->stream, gg, a, Ly.dww, Ly.dwb, D, s3);
+      FA_TRY(check_launch(ctx, "dwconv"));
+    }
+    FA_TRY(gemm(a, D, Ly.pw2, x, D, 0, FA_ACT_NONE, x, 0, "pw2"));
+    // FF2 + norm_out
+    FA_TRY(layernorm_launch(ctx, x, Ly.ln[3][0], Ly.ln[3][1], h, 1, M, D, D, D, 1e-5f, "ln_ff2"));
+    FA_TRY(gemm(h, D, Ly.ff2w1, u, c.DFF, 1, FA_ACT_SILU, nullptr, 0, "ff2_w1"));
+    FA_TRY(gemm(u, c.DFF, Ly.ff2w2, x, D, 0, FA_ACT_NONE, x, 0, "ff2_w2"));
+    FA_TRY(layernorm_launch(ctx, x, Ly.ln[4][0], Ly.ln[4][1], x, 0, M, D, D, D, 1e-5f, "ln_out"));
+  }
+  if (layout == 1) {
+    ProfScope ps(ctx, "zero_pad");
+    hipLaunchKernelGGL(zero_pad_rows_kernel, dim3(mx[3], n), dim3(256), 0, ctx->stream, x, D, s3, mx[3]);
+    FA_TRY(check_launch(ctx, "zero_pad"));
+  }
+  *out = ox;
+  return FA_OK;
+}
+
+}  // extern "C"

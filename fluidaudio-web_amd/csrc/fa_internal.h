@@ -1,0 +1,115 @@
+// Internal declarations shared by the runtime and the kernel translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/fa_hip.h"
+
+namespace fa {
+
+enum StoreKind : int {
+  S_F32 = 0,   // row-major f32 [rows, cols]
+  S_F16KM = 1, // f16 weight, stored K-major: element (k, n) of a [K=rows, N=cols] matrix at n*K + k
+  S_BYTES = 2, // raw bytes (int8/int4 payloads), `bytes` long
+  S_F16RM = 3, // f16 row-major activations [rows, cols] (allocF16)
+};
+
+struct TensorRec {
+  void *ptr = nullptr;
+  size_t bytes = 0;  // allocation size (pool key)
+  int rows = 0, cols = 0;
+  int kind = S_F32;
+  uint32_t gen = 1;
+  bool live = false;
+  bool view = false;       // rowsView alias: never pooled
+  bool pooled = false;     // storage returns to the pool on free/arena pop
+  uint64_t arena = 0;      // owning arena id (0 = persistent / none)
+  void *aux = nullptr;     // derived cache (e.g. repacked int8 weights), freed with the tensor
+  size_t aux_bytes = 0;
+};
+
+struct Arena {
+  uint64_t id;
+  std::vector<uint32_t> slots;
+};
+
+struct ProfRec {
+  char label[48];
+  hipEvent_t a, b;
+};
+
+struct Staged {
+  void *host = nullptr;  // pinned
+  size_t bytes = 0;
+  int kind = S_F32;
+  int rows = 0, cols = 0;
+  hipEvent_t ev = nullptr;
+  bool consumed = false;
+};
+
+}  // namespace fa
+
+struct fa_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string err;
+  std::vector<fa::TensorRec> recs;
+  std::vector<uint32_t> free_slots;
+  std::unordered_map<size_t, std::vector<void *>> pool;
+  size_t pooled_bytes = 0;
+  uint64_t created = 0, created_bytes = 0, reused = 0;
+  std::vector<fa::Arena> arenas;
+  uint64_t next_arena = 1;
+  bool batch_open = false;
+  // profiler
+  bool prof_on = false;
+  int prof_max = 0;
+  std::vector<fa::ProfRec> prof;
+  std::vector<hipEvent_t> prof_free_events;
+  // staged reads
+  std::vector<fa::Staged> staged;
+  std::vector<uint32_t> staged_gen;
+  int num_cu = 256;
+};
+
+namespace fa {
+
+// ── status helpers ────────────────────────────────────────────────────────
+int set_err(fa_ctx *ctx, int code, const char *fmt, ...);
+#define FA_TRY(expr)                  \
+  do {                                \
+    int _st = (expr);                 \
+    if (_st != FA_OK) return _st;     \
+  } while (0)
+#define FA_HIP(ctx, expr)                                                                                   \
+  do {                                                                                                      \
+    hipError_t _e = (expr);                                                                                 \
+    if (_e != hipSuccess) return ::fa::set_err((ctx), FA_E_DEVICE, "%s: %s", #expr, hipGetErrorString(_e)); \
+  } while (0)
+
+// ── tensor access ─────────────────────────────────────────────────────────
+TensorRec *get(fa_ctx *ctx, fa_tensor t);  // nullptr (error set) when stale
+int need(fa_ctx *ctx, fa_tensor t, TensorRec **out, const char *what);
+int opt(fa_ctx *ctx, fa_tensor t, TensorRec **out, const char *what);  // t == 0 -> *out = nullptr
+int new_tensor(fa_ctx *ctx, int rows, int cols, int kind, size_t bytes, fa_tensor *out, TensorRec **rec = nullptr);
+int new_persistent(fa_ctx *ctx, int rows, int cols, int kind, size_t bytes, fa_tensor *out, TensorRec **rec = nullptr);
+void *dev_alloc(fa_ctx *ctx, size_t bytes);  // raw hipMalloc, nullptr on failure (error set)
+
+// ── launch bracketing for the profiler ────────────────────────────────────
+struct ProfScope {
+  fa_ctx *ctx;
+  int idx;
+  ProfScope(fa_ctx *c, const char *label);
+  ~ProfScope();
+};
+int check_launch(fa_ctx *ctx, const char *what);
+
+inline unsigned cdiv(long a, long b) { return (unsigned)((a + b - 1) / b); }
+
+}  // namespace fa

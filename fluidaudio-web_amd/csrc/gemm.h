@@ -1,0 +1,40 @@
+// GEMM launch interface shared by the C-ABI ops and the fused encoder.
+#pragma once
+#include <stdint.h>
+
+struct fa_ctx;
+
+namespace fa {
+
+enum AKind : int { A_F16 = 0, A_F32 = 1 };
+enum BKind : int { B_F16 = 0, B_I8 = 1, B_I4 = 2 };
+
+struct GemmArgs {
+  const void *A = nullptr;  // [M, lda] row-major, f16 or f32
+  int lda = 0;
+  int akind = A_F16;
+  const void *B = nullptr;  // K-major: f16 [N][K] | int8 [N][K] | int4 [N][K/32][16 B]
+  int bkind = B_F16;
+  const void *bscale = nullptr;  // int4 scales [N][K/32]: f16 bits, or f32 when bscale_f32
+  int bscale_f32 = 0;
+  const uint8_t *bzp = nullptr;  // int4 zero points, packed [N][zpb] (null: 8)
+  int zpb = 0;
+  void *C = nullptr;  // [M, ldc], f32 or f16 (out_f16)
+  int ldc = 0;
+  int out_f16 = 0;
+  const float *colscale = nullptr;  // int8 per-output-column scale
+  const float *bias = nullptr;      // [N]
+  const float *add = nullptr;       // f32 residual [M, ldadd]; may alias C
+  int ldadd = 0;
+  int act = 0;
+  int glu = 0;  // GLU-pair epilogue (see gemm.hip), out [M, N/2] f16
+  int M = 0, N = 0, K = 0;
+};
+
+int gemm_mfma(fa_ctx *ctx, const GemmArgs &p, const char *label);
+int gemm_f32(fa_ctx *ctx, const float *A, const float *B, float *C, const float *bias, const float *add, int M, int N, int K, int act,
+             const char *label);
+int gemm_naive_f16(fa_ctx *ctx, const float *A, const void *Bkm, float *C, const float *bias, const float *add, int M, int N, int K, int act,
+                   const char *label);
+
+}  // namespace fa

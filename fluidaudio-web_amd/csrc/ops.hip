@@ -1,0 +1,792 @@
+// ComputeContext ops (src/gpu/compute.d.ts:155-228) on fp32 tensors: the
+// encoder's op subset, each a gfx950 kernel.  Bandwidth kernels use one wave
+// per row with wave-shuffle reductions (the reference uses a 64-lane
+// workgroup-memory tree, normalization.js:29-58, and one thread per softmax
+// row, normalization.js:61-77).
+#include <cstring>
+#include <vector>
+
+#include "fa_internal.h"
+#include "fa_device.h"
+#include "gemm.h"
+#include "attention.h"
+#include "ops.h"
+
+namespace fa {
+
+// ── row layernorm: f32 in, f32 or f16 out; one wave per row ───────────────
+template <typename TO>
+__global__ __launch_bounds__(256) void layernorm_kernel(const float *x, const float *__restrict__ gamma, const float *__restrict__ beta,
+                                                        TO *y, int rows, int cols, int ldx, int ldy,
+                                                        float eps) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const float *xr = x + (size_t)row * ldx;
+  TO *yr = y + (size_t)row * ldy;
+  if (cols == 1024) {  // the encoder width: 16 values per lane held in registers
+    float4 v[4];
+    float s = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      v[t] = reinterpret_cast<const float4 *>(xr)[lane + 64 * t];
+      s += v[t].x + v[t].y + v[t].z + v[t].w;
+    }
+    const float mean = wave_sum(s) * (1.f / 1024.f);
+    float q = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      float a = v[t].x - mean, b = v[t].y - mean, c = v[t].z - mean, d = v[t].w - mean;
+      q += a * a + b * b + c * c + d * d;
+    }
+    const float inv = rsqrtf(wave_sum(q) * (1.f / 1024.f) + eps);
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const int c0 = (lane + 64 * t) * 4;
+      const float4 gm = reinterpret_cast<const float4 *>(gamma)[lane + 64 * t];
+      const float4 bt = reinterpret_cast<const float4 *>(beta)[lane + 64 * t];
+      yr[c0 + 0] = (TO)((v[t].x - mean) * inv * gm.x + bt.x);
+      yr[c0 + 1] = (TO)((v[t].y - mean) * inv * gm.y + bt.y);
+      yr[c0 + 2] = (TO)((v[t].z - mean) * inv * gm.z + bt.z);
+      yr[c0 + 3] = (TO)((v[t].w - mean) * inv * gm.w + bt.w);
+    }
+    return;
+  }
+  float s = 0.f;
+  for (int j = lane; j < cols; j += 64) s += xr[j];
+  const float mean = wave_sum(s) / cols;
+  float q = 0.f;
+  for (int j = lane; j < cols; j += 64) {
+    const float d = xr[j] - mean;
+    q += d * d;
+  }
+  const float inv = rsqrtf(wave_sum(q) / cols + eps);
+  for (int j = lane; j < cols; j += 64) yr[j] = (TO)((xr[j] - mean) * inv * gamma[j] + beta[j]);
+}
+
+int layernorm_launch(fa_ctx *ctx, const float *x, const float *g, const float *b, void *y, int out_f16, int rows, int cols, int ldx, int ldy,
+                     float eps, const char *label) {
+  if (rows <= 0) return FA_OK;
+  ProfScope ps(ctx, label);
+  if (out_f16)
+    hipLaunchKernelGGL(layernorm_kernel<_Float16>, dim3(cdiv(rows, 4)), dim3(256), 0, ctx->stream, x, g, b, (_Float16 *)y, rows, cols, ldx, ldy, eps);
+  else
+    hipLaunchKernelGGL(layernorm_kernel<float>, dim3(cdiv(rows, 4)), dim3(256), 0, ctx->stream, x, g, b, (float *)y, rows, cols, ldx, ldy, eps);
+  return check_launch(ctx, label);
+}
+
+// ── softmax: one wave per row ─────────────────────────────────────────────
+__global__ __launch_bounds__(256) void softmax_kernel(const float *__restrict__ x, float *__restrict__ y, int rows, int cols) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const float *xr = x + (size_t)row * cols;
+  float *yr = y + (size_t)row * cols;
+  float mx = -INFINITY;
+  for (int j = lane; j < cols; j += 64) mx = fmaxf(mx, xr[j]);
+  mx = wave_max(mx);
+  float s = 0.f;
+  for (int j = lane; j < cols; j += 64) s += __expf(xr[j] - mx);
+  const float inv = 1.f / wave_sum(s);
+  for (int j = lane; j < cols; j += 64) yr[j] = __expf(xr[j] - mx) * inv;
+}
+
+// ── elementwise ───────────────────────────────────────────────────────────
+__global__ void ewise_kernel(const float *a, const float *b, float *c, long n, int cols, int bcast, int op) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    const float bv = bcast ? b[i % cols] : b[i];
+    c[i] = op ? a[i] * bv : a[i] + bv;
+  }
+}
+__global__ void unary_kernel(const float *x, float *y, long n, int kind, float s) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    const float v = x[i];
+    y[i] = kind == 0 ? v * s : (kind == 1 ? silu_f(v) : fmaxf(v, 0.f));
+  }
+}
+__global__ void glu_kernel(const float *x, float *y, int C, int T) {
+  const long n = (long)C * T;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    const long c = i / T, t = i % T;
+    const float a = x[c * T + t], b = x[(c + C) * T + t];
+    y[i] = a * (1.f / (1.f + __expf(-fminf(fmaxf(b, -30.f), 30.f))));
+  }
+}
+__global__ void transpose_kernel(const float *x, float *y, int R, int C) {
+  __shared__ float tile[32][33];
+  const int bx = blockIdx.x * 32, by = blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 256 threads: 32 x 8
+  for (int k = ty; k < 32; k += 8) {
+    const int r = by + k, c = bx + tx;
+    if (r < R && c < C) tile[k][tx] = x[(size_t)r * C + c];
+  }
+  __syncthreads();
+  for (int k = ty; k < 32; k += 8) {
+    const int c = bx + k, r = by + tx;
+    if (r < R && c < C) y[(size_t)c * R + r] = tile[tx][k];
+  }
+}
+__global__ void slice_cols_kernel(const float *x, float *y, int rows, int C, int col0, int W) {
+  const long n = (long)rows * W;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    const long r = i / W, j = i % W;
+    y[i] = x[r * C + col0 + j];
+  }
+}
+__global__ void set_cols_kernel(const float *src, float *dst, int rows, int C, int col0, int W) {
+  const long n = (long)rows * W;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    const long r = i / W, j = i % W;
+    dst[r * C + col0 + j] = src[i];
+  }
+}
+__global__ void sub_reshape_kernel(const float *x, float *y, int C, int Tsub, int F) {
+  const long CF = (long)C * F, n = (long)Tsub * CF;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    const long ho = i / CF, rem = i % CF, c = rem / F, wo = rem % F;
+    y[i] = x[c * ((long)Tsub * F) + ho * F + wo];
+  }
+}
+__global__ void row_bias_act_kernel(const float *x, const float *b, float *y, int rows, int cols, int act) {
+  const long n = (long)rows * cols;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) y[i] = act_apply(x[i] + b[i / cols], act);
+}
+
+// ── convolutions (direct; the encoder's fused path has its own kernels) ────
+__global__ void conv1d_kernel(const float *x, const float *w, const float *bias, float *y, int cout, int cin, int L, int Lout, int K, int stride,
+                              int padl, int dil, int groups, int act) {
+  const long n = (long)cout * Lout;
+  for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += (long)gridDim.x * blockDim.x) {
+    const int co = (int)(idx / Lout), lo = (int)(idx % Lout);
+    const int cinG = cin / groups, coutG = cout / groups, g = co / coutG;
+    float acc = 0.f;
+    for (int ci = 0; ci < cinG; ci++) {
+      const float *xr = x + (size_t)(g * cinG + ci) * L;
+      const float *wr = w + ((size_t)co * cinG + ci) * K;
+      for (int k = 0; k < K; k++) {
+        const int li = lo * stride + k * dil - padl;
+        if (li >= 0 && li < L) acc += xr[li] * wr[k];
+      }
+    }
+    if (bias) acc += bias[co];
+    y[idx] = act_apply(acc, act);
+  }
+}
+__global__ void conv2d_kernel(const float *x, const float *w, const float *bias, float *y, int cout, int cin, int H, int Wd, int Ho, int Wo, int kh,
+                              int kw, int sh, int sw, int pt, int pl, int groups, int act) {
+  const long n = (long)cout * Ho * Wo;
+  for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += (long)gridDim.x * blockDim.x) {
+    const int co = (int)(idx / ((long)Ho * Wo));
+    const int rem = (int)(idx % ((long)Ho * Wo)), ho = rem / Wo, wo = rem % Wo;
+    const int cinG = cin / groups, coutG = cout / groups, g = co / coutG;
+    float acc = bias ? bias[co] : 0.f;
+    for (int ci = 0; ci < cinG; ci++) {
+      const float *xc = x + (size_t)(g * cinG + ci) * H * Wd;
+      const float *wc = w + ((size_t)co * cinG + ci) * kh * kw;
+      for (int a = 0; a < kh; a++) {
+        const int hi = ho * sh + a - pt;
+        if (hi < 0 || hi >= H) continue;
+        for (int b = 0; b < kw; b++) {
+          const int wi = wo * sw + b - pl;
+          if (wi < 0 || wi >= Wd) continue;
+          acc += xc[(size_t)hi * Wd + wi] * wc[a * kw + b];
+        }
+      }
+    }
+    y[idx] = act_apply(acc, act);
+  }
+}
+
+// ── attention building blocks (fp32; the fused kernel is attention.hip) ────
+__global__ void bmm_qk_kernel(const float *q, const float *b, const float *qb, float *out, int T, int Tb, int H, int HD, int W, int bShared) {
+  const long n = (long)W * H * T * Tb;
+  const int stride = H * HD;
+  for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += (long)gridDim.x * blockDim.x) {
+    const int j = (int)(idx % Tb);
+    const long r = idx / Tb;
+    const int i = (int)(r % T), wh = (int)(r / T), h = wh % H, w = wh / H;
+    const float *qr = q + ((size_t)w * T + i) * stride + h * HD;
+    const float *br = b + (size_t)(bShared ? j : w * Tb + j) * stride + h * HD;
+    float acc = 0.f;
+    for (int d = 0; d < HD; d++) acc += (qr[d] + (qb ? qb[h * HD + d] : 0.f)) * br[d];
+    out[idx] = acc;
+  }
+}
+__global__ void bmm_pv_kernel(const float *p, const float *v, float *out, int Tq, int Tk, int H, int HD, int W) {
+  const int stride = H * HD;
+  const long n = (long)W * Tq * stride;
+  for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += (long)gridDim.x * blockDim.x) {
+    const int c = (int)(idx % stride);
+    const long r = idx / stride;
+    const int i = (int)(r % Tq), w = (int)(r / Tq), h = c / HD;
+    const float *pr = p + (((size_t)w * H + h) * Tq + i) * Tk;
+    float acc = 0.f;
+    for (int j = 0; j < Tk; j++) acc += pr[j] * v[((size_t)w * Tk + j) * stride + c];
+    out[idx] = acc;
+  }
+}
+// NeMo rel_shift closed form (attention.js:283-286): y[i,j] = xp[f], f = t + i(2t-1) + j
+// over the left-padded [t, 2t] view (column 0 = 0).
+__global__ void relshift_kernel(const float *x, float *y, int t, int H) {
+  const long n = (long)H * t * t;
+  const long p = 2L * t - 1, twoT = 2L * t;
+  for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += (long)gridDim.x * blockDim.x) {
+    const long j = idx % t, hi = idx / t, i = hi % t, h = hi / t;
+    const long f = t + i * p + j, col = f % twoT;
+    y[idx] = col == 0 ? 0.f : x[(h * t + f / twoT) * p + (col - 1)];
+  }
+}
+
+// ── quantised-weight helpers ──────────────────────────────────────────────
+__global__ void repack_i8_kernel(const int8_t *src, int8_t *dst, int K, int N) {  // [K][N] -> [N][K]
+  __shared__ int8_t tile[64][65];
+  const int bk = blockIdx.y * 64, bn = blockIdx.x * 64;
+  for (int e = threadIdx.x; e < 64 * 64; e += blockDim.x) {
+    const int r = e / 64, c = e % 64;
+    if (bk + r < K && bn + c < N) tile[r][c] = src[(size_t)(bk + r) * N + bn + c];
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < 64 * 64; e += blockDim.x) {
+    const int r = e / 64, c = e % 64;  // r: n, c: k
+    if (bn + r < N && bk + c < K) dst[(size_t)(bn + r) * K + bk + c] = tile[c][r];
+  }
+}
+__global__ void dequant_i8_kernel(const int8_t *q, const float *s, float *w, int K, int N) {
+  const long n = (long)K * N;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) w[i] = (float)q[i] * s[i % N];
+}
+__global__ void dequant_i4_kernel(const uint8_t *bq, const _Float16 *s, float *w, int K, int N) {
+  const long n = (long)K * N;
+  const int nblk = (K + 31) / 32;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    const int k = (int)(i / N), c = (int)(i % N);
+    const int b = k >> 5, t = k & 31;
+    const uint8_t byte = bq[((size_t)c * nblk + b) * 16 + (t >> 1)];
+    const int nib = (t & 1) ? (byte >> 4) : (byte & 0xf);
+    w[i] = (float)(nib - 8) * (float)s[(size_t)c * nblk + b];
+  }
+}
+
+static inline unsigned gs(long n) {
+  long b = (n + 255) / 256;
+  return (unsigned)(b < 1 ? 1 : (b > 65535 * 4 ? 65535 * 4 : b));
+}
+
+}  // namespace fa
+
+using namespace fa;
+
+// ── C ABI ──────────────────────────────────────────────────────────────────
+#define F32(r) reinterpret_cast<float *>((r)->ptr)
+#define CF32(r) reinterpret_cast<const float *>((r) ? (r)->ptr : nullptr)
+
+static int need_f32(fa_ctx *ctx, TensorRec *r, const char *what) {
+  if (r && r->kind != S_F32) return set_err(ctx, FA_E_INVALID, "%s: expected an f32 tensor", what);
+  return FA_OK;
+}
+
+extern "C" {
+
+int fa_matmul(fa_ctx *ctx, fa_tensor a, fa_tensor b, fa_tensor bias, int act, fa_tensor add, fa_tensor *out) {
+  TensorRec *ra, *rb, *rbias, *radd;
+  FA_TRY(need(ctx, a, &ra, "matmul"));
+  FA_TRY(need(ctx, b, &rb, "matmul"));
+  FA_TRY(opt(ctx, bias, &rbias, "matmul bias"));
+  FA_TRY(opt(ctx, add, &radd, "matmul add"));
+  FA_TRY(need_f32(ctx, ra, "matmul A"));
+  const int M = ra->rows, K = ra->cols, N = rb->cols;
+  if (rb->rows != K) return set_err(ctx, FA_E_INVALID, "matmul: A [%d,%d] @ B [%d,%d]", M, K, rb->rows, rb->cols);
+  if (rbias && rbias->rows * rbias->cols != N) return set_err(ctx, FA_E_INVALID, "matmul: bias has %d elements, N=%d", rbias->rows * rbias->cols, N);
+  if (radd && (radd->rows != M || radd->cols != N)) return set_err(ctx, FA_E_INVALID, "matmul: add [%d,%d] != [%d,%d]", radd->rows, radd->cols, M, N);
+  if (act < 0 || act > 5) return set_err(ctx, FA_E_INVALID, "matmul: act code %d", act);
+  fa_tensor o;
+  TensorRec *ro;
+  FA_TRY(new_tensor(ctx, M, N, S_F32, (size_t)M * N * 4, &o, &ro));
+  ra = get(ctx, a); rb = get(ctx, b); rbias = bias ? get(ctx, bias) : nullptr; radd = add ? get(ctx, add) : nullptr;  // recs may move
+  if (rb->kind == S_F16KM) {
+    if (K % 64 == 0) {
+      GemmArgs p;
+      p.A = ra->ptr; p.lda = K; p.akind = A_F32;
+      p.B = rb->ptr; p.bkind = B_F16;
+      p.C = ro->ptr; p.ldc = N;
+      p.bias = CF32(rbias); p.add = CF32(radd); p.ldadd = N; p.act = act;
+      p.M = M; p.N = N; p.K = K;
+      FA_TRY(gemm_mfma(ctx, p, "matmul_f16"));
+    } else {
+      FA_TRY(gemm_naive_f16(ctx, F32(ra), rb->ptr, F32(ro), CF32(rbias), CF32(radd), M, N, K, act, "matmul_f16_naive"));
+    }
+  } else if (rb->kind == S_F32) {
+    FA_TRY(gemm_f32(ctx, F32(ra), F32(rb), F32(ro), CF32(rbias), CF32(radd), M, N, K, act, "matmul_f32"));
+  } else {
+    return set_err(ctx, FA_E_INVALID, "matmul: B must be an f32 or f16 tensor");
+  }
+  *out = o;
+  return FA_OK;
+}
+
+int fa_matmul_int8(fa_ctx *ctx, fa_tensor a, fa_tensor wq, fa_tensor scale, int N, int K, fa_tensor bias, int act, fa_tensor *out) {
+  TensorRec *ra, *rw, *rs, *rbias;
+  FA_TRY(need(ctx, a, &ra, "matmulInt8"));
+  FA_TRY(need(ctx, wq, &rw, "matmulInt8 wq"));
+  FA_TRY(need(ctx, scale, &rs, "matmulInt8 scale"));
+  FA_TRY(opt(ctx, bias, &rbias, "matmulInt8 bias"));
+  FA_TRY(need_f32(ctx, ra, "matmulInt8 A"));
+  if (ra->cols != K) return set_err(ctx, FA_E_INVALID, "matmulInt8: A has %d cols, K=%d", ra->cols, K);
+  if (rw->kind != S_BYTES || rw->bytes < (size_t)K * N) return set_err(ctx, FA_E_INVALID, "matmulInt8: wq must hold K*N int8 bytes");
+  const int M = ra->rows;
+  // Repack once into the K-major layout the GEMM streams (cached on the tensor).
+  if (!rw->aux) {
+    void *p = dev_alloc(ctx, (size_t)K * N);
+    if (!p) return FA_E_OOM;
+    rw = get(ctx, wq);
+    rw->aux = p;
+    rw->aux_bytes = (size_t)K * N;
+    ProfScope ps(ctx, "repack_i8");
+    hipLaunchKernelGGL(repack_i8_kernel, dim3(cdiv(N, 64), cdiv(K, 64)), dim3(256), 0, ctx->stream, (const int8_t *)rw->ptr, (int8_t *)p, K, N);
+    FA_TRY(check_launch(ctx, "repack_i8"));
+  }
+  fa_tensor o;
+  TensorRec *ro;
+  FA_TRY(new_tensor(ctx, M, N, S_F32, (size_t)M * N * 4, &o, &ro));
+  ra = get(ctx, a); rw = get(ctx, wq); rs = get(ctx, scale); rbias = bias ? get(ctx, bias) : nullptr;
+  if (M <= 64 || K % 64 != 0) {
+    FA_TRY(gemv_quant_launch(ctx, F32(ra), rw->aux, F32(rs), 1, M, N, K, F32(ro), CF32(rbias), act, "matmulInt8_gemv"));
+  } else {
+    GemmArgs p;
+    p.A = ra->ptr; p.lda = K; p.akind = A_F32;
+    p.B = rw->aux; p.bkind = B_I8;
+    p.colscale = F32(rs);
+    p.C = ro->ptr; p.ldc = N;
+    p.bias = CF32(rbias); p.act = act;
+    p.M = M; p.N = N; p.K = K;
+    FA_TRY(gemm_mfma(ctx, p, "matmulInt8"));
+  }
+  *out = o;
+  return FA_OK;
+}
+
+int fa_matmul_nbits(fa_ctx *ctx, fa_tensor a, fa_tensor bq, fa_tensor scales, fa_tensor zp, int N, int block_size, fa_tensor *out) {
+  TensorRec *ra, *rq, *rs, *rz;
+  FA_TRY(need(ctx, a, &ra, "matmulNBits"));
+  FA_TRY(need(ctx, bq, &rq, "matmulNBits bq"));
+  FA_TRY(need(ctx, scales, &rs, "matmulNBits scales"));
+  FA_TRY(need(ctx, zp, &rz, "matmulNBits zp"));
+  FA_TRY(need_f32(ctx, ra, "matmulNBits A"));
+  if (block_size != 32) return set_err(ctx, FA_E_UNSUPPORTED, "matmulNBits: block_size %d (32 supported)", block_size);
+  const int M = ra->rows, K = ra->cols;
+  const int nblk = (K + 31) / 32, zpb = (nblk + 1) / 2;
+  if (rq->bytes < (size_t)N * nblk * 16) return set_err(ctx, FA_E_INVALID, "matmulNBits: bq too small");
+  fa_tensor o;
+  TensorRec *ro;
+  FA_TRY(new_tensor(ctx, M, N, S_F32, (size_t)M * N * 4, &o, &ro));
+  ra = get(ctx, a); rq = get(ctx, bq); rs = get(ctx, scales); rz = get(ctx, zp);
+  if (M <= 64 || K % 64 != 0) {
+    FA_TRY(gemv_nbits_launch(ctx, F32(ra), (const uint8_t *)rq->ptr, F32(rs), (const uint8_t *)rz->ptr, zpb, M, N, K, F32(ro), "matmulNBits_gemv"));
+  } else {
+    GemmArgs p;
+    p.A = ra->ptr; p.lda = K; p.akind = A_F32;
+    p.B = rq->ptr; p.bkind = B_I4;
+    p.bscale = rs->ptr; p.bscale_f32 = 1;
+    p.bzp = (const uint8_t *)rz->ptr; p.zpb = zpb;
+    p.C = ro->ptr; p.ldc = N;
+    p.M = M; p.N = N; p.K = K;
+    FA_TRY(gemm_mfma(ctx, p, "matmulNBits"));
+  }
+  *out = o;
+  return FA_OK;
+}
+
+int fa_layernorm(fa_ctx *ctx, fa_tensor x, fa_tensor gamma, fa_tensor beta, float eps, fa_tensor *out) {
+  TensorRec *rx, *rg, *rb;
+  FA_TRY(need(ctx, x, &rx, "layernorm"));
+  FA_TRY(need(ctx, gamma, &rg, "layernorm gamma"));
+  FA_TRY(need(ctx, beta, &rb, "layernorm beta"));
+  FA_TRY(need_f32(ctx, rx, "layernorm x"));
+  const int R = rx->rows, Cc = rx->cols;
+  if (rg->rows * rg->cols < Cc || rb->rows * rb->cols < Cc) return set_err(ctx, FA_E_INVALID, "layernorm: gamma/beta shorter than %d", Cc);
+  fa_tensor o;
+  TensorRec *ro;
+  FA_TRY(new_tensor(ctx, R, Cc, S_F32, (size_t)R * Cc * 4, &o, &ro));
+  rx = get(ctx, x); rg = get(ctx, gamma); rb = get(ctx, beta);
+  FA_TRY(layernorm_launch(ctx, F32(rx), F32(rg), F32(rb), ro->ptr, 0, R, Cc, Cc, Cc, eps, "layernorm"));
+  *out = o;
+  return FA_OK;
+}
+
+int fa_softmax(fa_ctx *ctx, fa_tensor x, fa_tensor *out) {
+  TensorRec *rx;
+  FA_TRY(need(ctx, x, &rx, "softmax"));
+  FA_TRY(need_f32(ctx, rx, "softmax"));
+  const int R = rx->rows, Cc = rx->cols;
+  fa_tensor o;
+  TensorRec *ro;
+  FA_TRY(new_tensor(ctx, R, Cc, S_F32, (size_t)R * Cc * 4, &o, &ro));
+  rx = get(ctx, x);
+  ProfScope ps(ctx, "softmax");
+  if (R) hipLaunchKernelGGL(softmax_kernel, dim3(cdiv(R, 4)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), R, Cc);
+  FA_TRY(check_launch(ctx, "softmax"));
+  *out = o;
+  return FA_OK;
+}
+
+static int unary(fa_ctx *ctx, fa_tensor x, int kind, float s, fa_tensor *out, const char *name) {
+  TensorRec *rx;
+  FA_TRY(need(ctx, x, &rx, name));
+  FA_TRY(need_f32(ctx, rx, name));
+  fa_tensor o;
+  TensorRec *ro;
+  const long n = (long)rx->rows * rx->cols;
+  FA_TRY(new_tensor(ctx, rx->rows, rx->cols, S_F32, (size_t)n * 4, &o, &ro));
+  rx = get(ctx, x);
+  ProfScope ps(ctx, name);
+  if (n) hipLaunchKernelGGL(unary_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), n, kind, s);
+  FA_TRY(check_launch(ctx, name));
+  *out = o;
+  return FA_OK;
+}
+int fa_scale(fa_ctx *ctx, fa_tensor x, float s, fa_tensor *out) { return unary(ctx, x, 0, s, out, "scale"); }
+int fa_silu(fa_ctx *ctx, fa_tensor x, fa_tensor *out) { return unary(ctx, x, 1, 0.f, out, "silu"); }
+int fa_relu(fa_ctx *ctx, fa_tensor x, fa_tensor *out) { return unary(ctx, x, 2, 0.f, out, "relu"); }
+
+int fa_ewise(fa_ctx *ctx, fa_tensor a, fa_tensor b, int op, fa_tensor *out) {
+  TensorRec *ra, *rb;
+  FA_TRY(need(ctx, a, &ra, "ewise"));
+  FA_TRY(need(ctx, b, &rb, "ewise"));
+  FA_TRY(need_f32(ctx, ra, "ewise a"));
+  FA_TRY(need_f32(ctx, rb, "ewise b"));
+  const int bcast = rb->rows == 1;
+  if (!bcast && (rb->rows != ra->rows || rb->cols != ra->cols)) return set_err(ctx, FA_E_INVALID, "ewise: shapes [%d,%d] vs [%d,%d]", ra->rows, ra->cols, rb->rows, rb->cols);
+  if (bcast && rb->cols != ra->cols) return set_err(ctx, FA_E_INVALID, "ewise: broadcast row has %d cols, need %d", rb->cols, ra->cols);
+  const long n = (long)ra->rows * ra->cols;
+  fa_tensor o;
+  TensorRec *ro;
+  FA_TRY(new_tensor(ctx, ra->rows, ra->cols, S_F32, (size_t)n * 4, &o, &ro));
+  ra = get(ctx, a); rb = get(ctx, b);
+  ProfScope ps(ctx, "ewise");
+  if (n) hipLaunchKernelGGL(ewise_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, F32(ra), F32(rb), F32(ro), n, ra->cols, bcast, op ? 1 : 0);
+  FA_TRY(check_launch(ctx, "ewise"));
+  *out = o;
+  return FA_OK;
+}
+
+int fa_glu(fa_ctx *ctx, fa_tensor x, fa_tensor *out) {
+  TensorRec *rx;
+  FA_TRY(need(ctx, x, &rx, "glu"));
+  FA_TRY(need_f32(ctx, rx, "glu"));
+  if (rx->rows % 2) return set_err(ctx, FA_E_INVALID, "glu: odd channel count %d", rx->rows);
+  const int C = rx->rows / 2, T = rx->cols;
+  fa_tensor o;
+  TensorRec *ro;
+  FA_TRY(new_tensor(ctx, C, T, S_F32, (size_t)C * T * 4, &o, &ro));
+  rx = get(ctx, x);
+  ProfScope ps(ctx, "glu");
+  if ((long)C * T) hipLaunchKernelGGL(glu_kernel, dim3(gs((long)C * T)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), C, T);
+  FA_TRY(check_launch(ctx, "glu"));
+  *out = o;
+  return FA_OK;
+}
+
+int fa_transpose(fa_ctx *ctx, fa_tensor x, fa_tensor *out) {
+  TensorRec *rx;
+  FA_TRY(need(ctx, x, &rx, "transpose"));
+  FA_TRY(need_f32(ctx, rx, "transpose"));
+  const int R = rx->rows, Cc = rx->cols;
+  fa_tensor o;
+  TensorRec *ro;
+  FA_TRY(new_tensor(ctx, Cc, R, S_F32, (size_t)R * Cc * 4, &o, &ro));
+  rx = get(ctx, x);
+  ProfScope ps(ctx, "transpose");
+  if ((long)R * Cc) hipLaunchKernelGGL(transpose_kernel, dim3(cdiv(Cc, 32), cdiv(R, 32)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), R, Cc);
+  FA_TRY(check_launch(ctx, "transpose"));
+  *out = o;
+  return FA_OK;
+}
+
+int fa_slice_cols(fa_ctx *ctx, fa_tensor x, int col0, int width, fa_tensor *out) {
+  TensorRec *rx;
+  FA_TRY(need(ctx, x, &rx, "sliceCols"));
+  FA_TRY(need_f32(ctx, rx, "sliceCols"));
+  if (col0 < 0 || width < 0 || col0 + width > rx->cols) return set_err(ctx, FA_E_INVALID, "sliceCols: [%d,%d) of %d cols", col0, col0 + width, rx->cols);
+  fa_tensor o;
+  TensorRec *ro;
+  FA_TRY(new_tensor(ctx, rx->rows, width, S_F32, (size_t)rx->rows * width * 4, &o, &ro));
+  rx = get(ctx, x);
+  const long n = (long)rx->rows * width;
+  ProfScope ps(ctx, "sliceCols");
+  if (n) hipLaunchKernelGGL(slice_cols_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), rx->rows, rx->cols, col0, width);
+  FA_TRY(check_launch(ctx, "sliceCols"));
+  *out = o;
+  return FA_OK;
+}
+
+int fa_set_cols(fa_ctx *ctx, fa_tensor dst, fa_tensor src, int col0) {
+  TensorRec *rd, *rs;
+  FA_TRY(need(ctx, dst, &rd, "setCols"));
+  FA_TRY(need(ctx, src, &rs, "setCols"));
+  FA_TRY(need_f32(ctx, rd, "setCols"));
+  FA_TRY(need_f32(ctx, rs, "setCols"));
+  if (rs->rows != rd->rows || col0 < 0 || col0 + rs->cols > rd->cols) return set_err(ctx, FA_E_INVALID, "setCols: src [%d,%d] at col %d of [%d,%d]", rs->rows, rs->cols, col0, rd->rows, rd->cols);
+  const long n = (long)rs->rows * rs->cols;
+  ProfScope ps(ctx, "setCols");
+  if (n) hipLaunchKernelGGL(set_cols_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, F32(rs), F32(rd), rs->rows, rd->cols, col0, rs->cols);
+  return check_launch(ctx, "setCols");
+}
+
+int fa_slice_rows(fa_ctx *ctx, fa_tensor x, int row0, int count, fa_tensor *out) {
+  TensorRec *rx;
+  FA_TRY(need(ctx, x, &rx, "sliceRows"));
+  FA_TRY(need_f32(ctx, rx, "sliceRows"));
+  if (row0 < 0 || count < 0 || row0 + count > rx->rows) return set_err(ctx, FA_E_INVALID, "sliceRows: [%d,%d) of %d rows", row0, row0 + count, rx->rows);
+  fa_tensor o;
+  TensorRec *ro;
+  FA_TRY(new_tensor(ctx, count, rx->cols, S_F32, (size_t)count * rx->cols * 4, &o, &ro));
+  rx = get(ctx, x);
+  if (count) FA_HIP(ctx, hipMemcpyAsync(ro->ptr, F32(rx) + (size_t)row0 * rx->cols, (size_t)count * rx->cols * 4, hipMemcpyDeviceToDevice, ctx->stream));
+  *out = o;
+  return FA_OK;
+}
+
+int fa_copy_rows(fa_ctx *ctx, fa_tensor dst, fa_tensor src, int row_offset) {
+  TensorRec *rd, *rs;
+  FA_TRY(need(ctx, dst, &rd, "copyRows"));
+  FA_TRY(need(ctx, src, &rs, "copyRows"));
+  if (rs->cols != rd->cols || row_offset < 0 || row_offset + rs->rows > rd->rows) return set_err(ctx, FA_E_INVALID, "copyRows: out of range");
+  const size_t nb = (size_t)rs->rows * rs->cols * 4;
+  if (nb) FA_HIP(ctx, hipMemcpyAsync(F32(rd) + (size_t)row_offset * rd->cols, rs->ptr, nb, hipMemcpyDeviceToDevice, ctx->stream));
+  return FA_OK;
+}
+
+int fa_concat_rows(fa_ctx *ctx, const fa_tensor *ts, int n, fa_tensor *out) {
+  if (n <= 0) return set_err(ctx, FA_E_INVALID, "concatRows: no tensors");
+  int rows = 0, cols = -1;
+  for (int i = 0; i < n; i++) {
+    TensorRec *r;
+    FA_TRY(need(ctx, ts[i], &r, "concatRows"));
+    FA_TRY(need_f32(ctx, r, "concatRows"));
+    if (cols >= 0 && r->cols != cols) return set_err(ctx, FA_E_INVALID, "concatRows: column mismatch");
+    cols = r->cols;
+    rows += r->rows;
+  }
+  fa_tensor o;
+  TensorRec *ro;
+  FA_TRY(new_tensor(ctx, rows, cols, S_F32, (size_t)rows * cols * 4, &o, &ro));
+  size_t off = 0;
+  for (int i = 0; i < n; i++) {
+    TensorRec *r = get(ctx, ts[i]);
+    ro = get(ctx, o);
+    const size_t nb = (size_t)r->rows * r->cols * 4;
+    if (nb) FA_HIP(ctx, hipMemcpyAsync((char *)ro->ptr + off, r->ptr, nb, hipMemcpyDeviceToDevice, ctx->stream));
+    off += nb;
+  }
+  *out = o;
+  return FA_OK;
+}
+
+int fa_sub_reshape(fa_ctx *ctx, fa_tensor x, int C, int Tsub, int F, fa_tensor *out) {
+  TensorRec *rx;
+  FA_TRY(need(ctx, x, &rx, "subReshape"));
+  FA_TRY(need_f32(ctx, rx, "subReshape"));
+  if ((long)rx->rows * rx->cols != (long)C * Tsub * F) return set_err(ctx, FA_E_INVALID, "subReshape: %d elements != C*Tsub*F", rx->rows * rx->cols);
+  fa_tensor o;
+  TensorRec *ro;
+  FA_TRY(new_tensor(ctx, Tsub, C * F, S_F32, (size_t)Tsub * C * F * 4, &o, &ro));
+  rx = get(ctx, x);
+  const long n = (long)Tsub * C * F;
+  ProfScope ps(ctx, "subReshape");
+  if (n) hipLaunchKernelGGL(sub_reshape_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), C, Tsub, F);
+  FA_TRY(check_launch(ctx, "subReshape"));
+  *out = o;
+  return FA_OK;
+}
+
+int fa_row_bias_act(fa_ctx *ctx, fa_tensor x, fa_tensor bias, int act, fa_tensor *out) {
+  TensorRec *rx, *rb;
+  FA_TRY(need(ctx, x, &rx, "rowBiasAct"));
+  FA_TRY(need(ctx, bias, &rb, "rowBiasAct bias"));
+  if (rb->rows * rb->cols < rx->rows) return set_err(ctx, FA_E_INVALID, "rowBiasAct: bias shorter than rows");
+  fa_tensor o;
+  TensorRec *ro;
+  const long n = (long)rx->rows * rx->cols;
+  FA_TRY(new_tensor(ctx, rx->rows, rx->cols, S_F32, (size_t)n * 4, &o, &ro));
+  rx = get(ctx, x); rb = get(ctx, bias);
+  ProfScope ps(ctx, "rowBiasAct");
+  if (n) hipLaunchKernelGGL(row_bias_act_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, F32(rx), F32(rb), F32(ro), rx->rows, rx->cols, act);
+  FA_TRY(check_launch(ctx, "rowBiasAct"));
+  *out = o;
+  return FA_OK;
+}
+
+int fa_conv1d(fa_ctx *ctx, fa_tensor x, fa_tensor w, int cout, int k, fa_tensor bias, int stride, int pad_left, int pad_right, int dilation,
+              int groups, int act, fa_tensor *out) {
+  TensorRec *rx, *rw, *rb;
+  FA_TRY(need(ctx, x, &rx, "conv1d"));
+  FA_TRY(need(ctx, w, &rw, "conv1d w"));
+  FA_TRY(opt(ctx, bias, &rb, "conv1d bias"));
+  FA_TRY(need_f32(ctx, rx, "conv1d x"));
+  FA_TRY(need_f32(ctx, rw, "conv1d w"));
+  const int Cin = rx->rows, L = rx->cols;
+  if (groups <= 0 || Cin % groups || cout % groups || stride <= 0 || dilation <= 0 || k <= 0)
+    return set_err(ctx, FA_E_INVALID, "conv1d: bad geometry (cin %d, cout %d, groups %d)", Cin, cout, groups);
+  if ((long)rw->rows * rw->cols < (long)cout * (Cin / groups) * k) return set_err(ctx, FA_E_INVALID, "conv1d: weight too small");
+  const int Lout = (L + pad_left + pad_right - dilation * (k - 1) - 1) / stride + 1;
+  if (Lout <= 0) return set_err(ctx, FA_E_INVALID, "conv1d: empty output");
+  fa_tensor o;
+  TensorRec *ro;
+  FA_TRY(new_tensor(ctx, cout, Lout, S_F32, (size_t)cout * Lout * 4, &o, &ro));
+  rx = get(ctx, x); rw = get(ctx, w); rb = bias ? get(ctx, bias) : nullptr;
+  ProfScope ps(ctx, "conv1d");
+  hipLaunchKernelGGL(conv1d_kernel, dim3(gs((long)cout * Lout)), dim3(256), 0, ctx->stream, F32(rx), F32(rw), CF32(rb), F32(ro), cout, Cin, L, Lout,
+                     k, stride, pad_left, dilation, groups, act);
+  FA_TRY(check_launch(ctx, "conv1d"));
+  *out = o;
+  return FA_OK;
+}
+
+int fa_conv2d(fa_ctx *ctx, fa_tensor x, fa_tensor w, int cout, int cin, int h, int wd, int kh, int kw, fa_tensor bias, int sh, int sw, int pt,
+              int pb, int pl, int pr, int groups, int act, fa_tensor *out) {
+  TensorRec *rx, *rw, *rb;
+  FA_TRY(need(ctx, x, &rx, "conv2d"));
+  FA_TRY(need(ctx, w, &rw, "conv2d w"));
+  FA_TRY(opt(ctx, bias, &rb, "conv2d bias"));
+  FA_TRY(need_f32(ctx, rx, "conv2d x"));
+  if ((long)rx->rows * rx->cols != (long)cin * h * wd) return set_err(ctx, FA_E_INVALID, "conv2d: x has %ld elements, cin*h*w=%ld", (long)rx->rows * rx->cols, (long)cin * h * wd);
+  if (groups <= 0 || cin % groups || cout % groups) return set_err(ctx, FA_E_INVALID, "conv2d: bad groups");
+  const int Ho = (h + pt + pb - kh) / sh + 1, Wo = (wd + pl + pr - kw) / sw + 1;
+  if (Ho <= 0 || Wo <= 0) return set_err(ctx, FA_E_INVALID, "conv2d: empty output");
+  fa_tensor o;
+  TensorRec *ro;
+  FA_TRY(new_tensor(ctx, cout, Ho * Wo, S_F32, (size_t)cout * Ho * Wo * 4, &o, &ro));
+  rx = get(ctx, x); rw = get(ctx, w); rb = bias ? get(ctx, bias) : nullptr;
+  ProfScope ps(ctx, "conv2d");
+  hipLaunchKernelGGL(conv2d_kernel, dim3(gs((long)cout * Ho * Wo)), dim3(256), 0, ctx->stream, F32(rx), F32(rw), CF32(rb), F32(ro), cout, cin, h, wd,
+                     Ho, Wo, kh, kw, sh, sw, pt, pl, groups, act);
+  FA_TRY(check_launch(ctx, "conv2d"));
+  *out = o;
+  return FA_OK;
+}
+
+int fa_bmm_qk(fa_ctx *ctx, fa_tensor q, fa_tensor b, fa_tensor qb, int H, int HD, int W, int b_shared, fa_tensor *out) {
+  TensorRec *rq, *rb, *rqb;
+  FA_TRY(need(ctx, q, &rq, "bmmQK"));
+  FA_TRY(need(ctx, b, &rb, "bmmQK b"));
+  FA_TRY(opt(ctx, qb, &rqb, "bmmQK qb"));
+  if (W <= 0 || rq->rows % W || (!b_shared && rb->rows % W) || rq->cols != H * HD || rb->cols != H * HD)
+    return set_err(ctx, FA_E_INVALID, "bmmQK: shapes");
+  const int T = rq->rows / W, Tb = b_shared ? rb->rows : rb->rows / W;
+  fa_tensor o;
+  TensorRec *ro;
+  FA_TRY(new_tensor(ctx, W * H * T, Tb, S_F32, (size_t)W * H * T * Tb * 4, &o, &ro));
+  rq = get(ctx, q); rb = get(ctx, b); rqb = qb ? get(ctx, qb) : nullptr;
+  ProfScope ps(ctx, "bmmQK");
+  hipLaunchKernelGGL(bmm_qk_kernel, dim3(gs((long)W * H * T * Tb)), dim3(256), 0, ctx->stream, F32(rq), F32(rb), CF32(rqb), F32(ro), T, Tb, H, HD, W,
+                     b_shared);
+  FA_TRY(check_launch(ctx, "bmmQK"));
+  *out = o;
+  return FA_OK;
+}
+
+int fa_bmm_pv(fa_ctx *ctx, fa_tensor p, fa_tensor v, int H, int HD, int W, fa_tensor *out) {
+  TensorRec *rp, *rv;
+  FA_TRY(need(ctx, p, &rp, "bmmPV"));
+  FA_TRY(need(ctx, v, &rv, "bmmPV v"));
+  if (W <= 0 || rv->rows % W || rp->rows % (W * H) || rv->cols != H * HD) return set_err(ctx, FA_E_INVALID, "bmmPV: shapes");
+  const int Tk = rv->rows / W, Tq = rp->rows / (W * H);
+  if (rp->cols != Tk) return set_err(ctx, FA_E_INVALID, "bmmPV: probs have %d cols, Tk=%d", rp->cols, Tk);
+  fa_tensor o;
+  TensorRec *ro;
+  FA_TRY(new_tensor(ctx, W * Tq, H * HD, S_F32, (size_t)W * Tq * H * HD * 4, &o, &ro));
+  rp = get(ctx, p); rv = get(ctx, v);
+  ProfScope ps(ctx, "bmmPV");
+  hipLaunchKernelGGL(bmm_pv_kernel, dim3(gs((long)W * Tq * H * HD)), dim3(256), 0, ctx->stream, F32(rp), F32(rv), F32(ro), Tq, Tk, H, HD, W);
+  FA_TRY(check_launch(ctx, "bmmPV"));
+  *out = o;
+  return FA_OK;
+}
+
+int fa_rel_shift_b(fa_ctx *ctx, fa_tensor x, int H, fa_tensor *out) {
+  TensorRec *rx;
+  FA_TRY(need(ctx, x, &rx, "relShiftB"));
+  if (H <= 0 || rx->rows % H) return set_err(ctx, FA_E_INVALID, "relShiftB: rows %d not divisible by H=%d", rx->rows, H);
+  const int t = rx->rows / H;
+  if (rx->cols != 2 * t - 1) return set_err(ctx, FA_E_INVALID, "relShiftB: expected %d cols, got %d", 2 * t - 1, rx->cols);
+  fa_tensor o;
+  TensorRec *ro;
+  FA_TRY(new_tensor(ctx, H * t, t, S_F32, (size_t)H * t * t * 4, &o, &ro));
+  rx = get(ctx, x);
+  ProfScope ps(ctx, "relShiftB");
+  if ((long)H * t * t) hipLaunchKernelGGL(relshift_kernel, dim3(gs((long)H * t * t)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), t, H);
+  FA_TRY(check_launch(ctx, "relShiftB"));
+  *out = o;
+  return FA_OK;
+}
+
+int fa_rel_shift(fa_ctx *ctx, fa_tensor x, fa_tensor *out) { return fa_rel_shift_b(ctx, x, 1, out); }
+
+int fa_attn_fused(fa_ctx *ctx, fa_tensor q, fa_tensor k, fa_tensor v, fa_tensor pos, fa_tensor pbu, fa_tensor pbv, int H, int HD, int W, fa_tensor *out) {
+  TensorRec *rq, *rk, *rv, *rp, *ru, *rw;
+  FA_TRY(need(ctx, q, &rq, "attnFused q"));
+  FA_TRY(need(ctx, k, &rk, "attnFused k"));
+  FA_TRY(need(ctx, v, &rv, "attnFused v"));
+  FA_TRY(need(ctx, pos, &rp, "attnFused pos"));
+  FA_TRY(need(ctx, pbu, &ru, "attnFused pbu"));
+  FA_TRY(need(ctx, pbv, &rw, "attnFused pbv"));
+  if (W <= 0 || rq->rows % W || rq->cols != H * HD || rk->rows != rq->rows || rv->rows != rq->rows) return set_err(ctx, FA_E_INVALID, "attnFused: shapes");
+  const int T = rq->rows / W;
+  if (rp->rows != 2 * T - 1 || rp->cols != H * HD) return set_err(ctx, FA_E_INVALID, "attnFused: pos must be [2T-1, H*HD]");
+  if (HD != 128) return set_err(ctx, FA_E_UNSUPPORTED, "attnFused: HD %d", HD);
+  if (T > 1024) return set_err(ctx, FA_E_UNSUPPORTED, "attnFused: T %d > 1024", T);
+  fa_tensor o;
+  TensorRec *ro;
+  FA_TRY(new_tensor(ctx, rq->rows, H * HD, S_F32, (size_t)rq->rows * H * HD * 4, &o, &ro));
+  rq = get(ctx, q); rk = get(ctx, k); rv = get(ctx, v); rp = get(ctx, pos); ru = get(ctx, pbu); rw = get(ctx, pbv);
+  AttnArgs a;
+  a.q = rq->ptr; a.k = rk->ptr; a.v = rv->ptr;
+  a.ldq = a.ldk = a.ldv = H * HD;
+  a.pos = rp->ptr; a.ldp = H * HD; a.prows = 2 * T - 1; a.pcenter = T - 1;
+  a.pbu = F32(ru); a.pbv = F32(rw);
+  a.out = ro->ptr; a.ldo = H * HD;
+  a.H = H; a.HD = HD;
+  for (int w0 = 0; w0 < W; w0 += kMaxWin) {  // windows in launches of at most kMaxWin
+    a.win.n = W - w0 < kMaxWin ? W - w0 : kMaxWin;
+    for (int i = 0; i < a.win.n; i++) {
+      a.win.off[i] = (w0 + i) * T;
+      a.win.len[i] = T;
+    }
+    FA_TRY(relpos_attention(ctx, a, 1, 1, T, "attnFused"));
+  }
+  *out = o;
+  return FA_OK;
+}
+
+int fa_dequant_int8(fa_ctx *ctx, fa_tensor wq, fa_tensor scale, int K, int N, fa_tensor *out) {
+  TensorRec *rw, *rs;
+  FA_TRY(need(ctx, wq, &rw, "dequantInt8"));
+  FA_TRY(need(ctx, scale, &rs, "dequantInt8 scale"));
+  if (rw->bytes < (size_t)K * N || (long)rs->rows * rs->cols < N) return set_err(ctx, FA_E_INVALID, "dequantInt8: sizes");
+  fa_tensor o;
+  TensorRec *ro;
+  FA_TRY(new_tensor(ctx, K, N, S_F32, (size_t)K * N * 4, &o, &ro));
+  rw = get(ctx, wq); rs = get(ctx, scale);
+  ProfScope ps(ctx, "dequantInt8");
+  hipLaunchKernelGGL(dequant_i8_kernel, dim3(gs((long)K * N)), dim3(256), 0, ctx->stream, (const int8_t *)rw->ptr, F32(rs), F32(ro), K, N);
+  FA_TRY(check_launch(ctx, "dequantInt8"));
+  *out = o;
+  return FA_OK;
+}
+
+int fa_dequant_int4(fa_ctx *ctx, fa_tensor bq, fa_tensor scales_f16, int K, int N, fa_tensor *out) {
+  TensorRec *rq, *rs;
+  FA_TRY(need(ctx, bq, &rq, "dequantInt4"));
+  FA_TRY(need(ctx, scales_f16, &rs, "dequantInt4 scales"));
+  const int nblk = (K + 31) / 32;
+  if (rq->bytes < (size_t)N * nblk * 16 || rs->bytes < (size_t)N * nblk * 2) return set_err(ctx, FA_E_INVALID, "dequantInt4: sizes");
+  fa_tensor o;
+  TensorRec *ro;
+  FA_TRY(new_tensor(ctx, K, N, S_F32, (size_t)K * N * 4, &o, &ro));
+  rq = get(ctx, bq); rs = get(ctx, scales_f16);
+  ProfScope ps(ctx, "dequantInt4");
+  hipLaunchKernelGGL(dequant_i4_kernel, dim3(gs((long)K * N)), dim3(256), 0, ctx->stream, (const uint8_t *)rq->ptr, (const _Float16 *)rs->ptr, F32(ro), K, N);
+  FA_TRY(check_launch(ctx, "dequantInt4"));
+  *out = o;
+  return FA_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,242 @@
+"""Parakeet FastConformer encoder on a HipContext.
+
+Two forms with the same result contract:
+
+* ``loadParakeetEncoder`` / ``parakeetEncodeBatch`` restate the reference's
+  op-by-op encoder (src/engines/asr-parakeet/raw-encoder.js:39-161, 177-222,
+  235-386) against the ComputeContext methods, so the sequence of backend
+  calls is the reference's.  With ``weights="f32"`` every matmul runs the
+  fp32 MFMA kernels: this is the GPU fp32 path used as the reference for the
+  fused f16 encoder at full size.
+* ``FusedEncoder`` is the production path: one native call per batch
+  (fa_encoder_forward) over packed or padded variable-length windows, with
+  f16 / int8 / int4 weight storage.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+
+import numpy as np
+
+from . import _lib as L
+from ._lib import check, lib
+from .compute import HipContext, HipTensor
+
+
+def inferConfig(man: dict) -> dict:
+    """raw-encoder.js:28-35 on a {name: array} manifest."""
+    layers = sum(1 for k in man if k.startswith("L") and k.endswith("_lnff1_w"))
+    D, DFF = man["L0_ff1w1"].shape
+    H, HD = man["L0_pbu"].shape
+    Csub = man["c0w"].shape[0]
+    Fsub = man["linw"].shape[0] // Csub
+    return dict(D=D, DFF=DFF, H=H, HD=HD, layers=layers, dwK=man["L0_dw"].shape[2], Csub=Csub, Fsub=Fsub, melBins=Fsub * 8)
+
+
+def _f32(a):
+    return np.ascontiguousarray(np.asarray(a, np.float32))
+
+
+# ── op-by-op restatement ────────────────────────────────────────────────────
+def loadParakeetEncoder(ctx: HipContext, man: dict, weights: str = "f16", layers: int | None = None) -> dict:
+    """Upload weights with the reference's load-time folds (raw-encoder.js:
+    124-156): q·1/√HD, pos_bias·1/√HD, FF linear2·0.5; pointwise convs as
+    transposed [cin, cout] matrices.  weights: "f16" (uploadF16) or "f32"."""
+    cfg = inferConfig(man)
+    if layers is not None:
+        cfg["layers"] = layers
+    INV = 1.0 / math.sqrt(cfg["HD"])
+    up_mat = ctx.uploadF16 if weights == "f16" else ctx.upload
+
+    def mat(k, s=1.0):
+        a = _f32(man[k]).astype(np.float64) * s if s != 1.0 else _f32(man[k])
+        a = _f32(a)
+        return up_mat(a, a.shape[0], a.shape[1])
+
+    def vec(k, s=1.0):
+        a = _f32(_f32(man[k]).astype(np.float64) * s) if s != 1.0 else _f32(man[k])
+        return ctx.upload(a.reshape(-1), 1, a.size)
+
+    def vec_opt(k, s=1.0):
+        return vec(k, s) if k in man else None
+
+    def pwT(k, cout, cin):
+        w = _f32(man[k]).reshape(cout, cin)
+        t = np.ascontiguousarray(w.T)
+        return up_mat(t, cin, cout)
+
+    D = cfg["D"]
+    sub = {"conv": [{"w": vec(f"c{i}w"), "b": vec(f"c{i}b")} for i in range(5)], "linw": mat("linw"), "linb": vec("linb")}
+    Ls = []
+    for Li in range(cfg["layers"]):
+        g = lambda s: f"L{Li}_{s}"
+        Ls.append({
+            "lnff1": [vec(g("lnff1_w")), vec(g("lnff1_b"))],
+            "ff1w1": mat(g("ff1w1")), "ff1w2": mat(g("ff1w2"), 0.5),
+            "ff1b1": vec_opt(g("ff1b1")), "ff1b2": vec_opt(g("ff1b2"), 0.5),
+            "lnatt": [vec(g("lnatt_w")), vec(g("lnatt_b"))],
+            "q": mat(g("q"), INV), "k": mat(g("k")), "v": mat(g("v")), "pos": mat(g("pos")), "out": mat(g("out")),
+            "qb": vec_opt(g("qb"), INV), "kb": vec_opt(g("kb")), "vb": vec_opt(g("vb")), "outb": vec_opt(g("outb")),
+            "pbuAll": vec(g("pbu"), INV), "pbvAll": vec(g("pbv"), INV),
+            "lnconv": [vec(g("lnconv_w")), vec(g("lnconv_b"))],
+            "pw1T": pwT(g("pw1"), 2 * D, D), "dw": vec(g("dw")), "dwb": vec(g("dwb")), "pw2T": pwT(g("pw2"), D, D),
+            "pw1b": vec_opt(g("pw1b")), "pw2b": vec_opt(g("pw2b")),
+            "lnff2": [vec(g("lnff2_w")), vec(g("lnff2_b"))],
+            "ff2w1": mat(g("ff2w1")), "ff2w2": mat(g("ff2w2"), 0.5),
+            "ff2b1": vec_opt(g("ff2b1")), "ff2b2": vec_opt(g("ff2b2"), 0.5),
+            "lnout": [vec(g("lnout_w")), vec(g("lnout_b"))],
+        })
+    return {"sub": sub, "layers": Ls, "cfg": cfg}
+
+
+def posEncoding(Tsub: int, D: int) -> np.ndarray:
+    """raw-encoder.js:163-174."""
+    pos = (Tsub - 1 - np.arange(2 * Tsub - 1, dtype=np.float64))[:, None]
+    dv = np.exp(np.arange(0, D, 2, dtype=np.float64) * -(math.log(10000.0) / D))
+    pe = np.empty((2 * Tsub - 1, D), np.float32)
+    pe[:, 0::2] = np.sin(pos * dv)
+    pe[:, 1::2] = np.cos(pos * dv)
+    return pe
+
+
+def _pre_encode(ctx, enc, mel):
+    """raw-encoder.js:177-222 for one window; mel [melBins, T] channel-major."""
+    cfg = enc["cfg"]
+    Csub, mb = cfg["Csub"], cfg["melBins"]
+    T = mel.shape[1]
+    s = ctx.upload(np.ascontiguousarray(_f32(mel).T), 1, T * mb)
+    Hh, Wd = T, mb
+    conv = [(Csub, 1, 3, 2, 1, "relu", True), (Csub, Csub, 3, 2, Csub, "none", True), (Csub, Csub, 1, 1, 1, "relu", False),
+            (Csub, Csub, 3, 2, Csub, "none", True), (Csub, Csub, 1, 1, 1, "relu", False)]
+    for i, (cout, cin, k, st, gr, act, s2) in enumerate(conv):
+        p = 1 if s2 else 0
+        s = ctx.conv2d(s, enc["sub"]["conv"][i]["w"], cout, cin, Hh, Wd, k, k, bias=enc["sub"]["conv"][i]["b"], strideH=st, strideW=st,
+                       padTop=p, padBottom=p, padLeft=p, padRight=p, groups=gr, act=act)
+        Hh = (Hh + 2 * p - k) // st + 1
+        Wd = (Wd + 2 * p - k) // st + 1
+    flat = ctx.subReshape(s, Csub, Hh, Wd)
+    return ctx.matmul(flat, enc["sub"]["linw"], bias=enc["sub"]["linb"]), Hh
+
+
+def parakeetEncodeBatch(ctx: HipContext, enc: dict, mels: list) -> tuple:
+    """raw-encoder.js:235-386 (no chunk mask, Parakeet BN-folded conv module).
+    Returns (frames [W*Tsub, D] tensor, Tsub)."""
+    cfg = enc["cfg"]
+    D, H, HD, K = cfg["D"], cfg["H"], cfg["HD"], cfg["dwK"]
+    W = len(mels)
+    pre = [_pre_encode(ctx, enc, m) for m in mels]
+    Tsub = pre[0][1]
+    if any(p[1] != Tsub for p in pre):
+        raise ValueError("parakeetEncodeBatch: windows must have equal Tsub")
+    x = pre[0][0] if W == 1 else ctx.concatRows([p[0] for p in pre])
+    peT = ctx.upload(posEncoding(Tsub, D), 2 * Tsub - 1, D)
+    ln = lambda t, lp: ctx.layernorm(t, lp[0], lp[1])
+    ff = lambda t, lp, w1, w2, b1, b2: ctx.matmul(ctx.matmul(ln(t, lp), w1, bias=b1, act="silu"), w2, bias=b2, add=t)
+    pad = (K - 1) >> 1
+
+    def run():
+        nonlocal x
+        for w in enc["layers"]:
+            arena = ctx.pushArena()
+            x = ff(x, w["lnff1"], w["ff1w1"], w["ff1w2"], w["ff1b1"], w["ff1b2"])
+            xln = ln(x, w["lnatt"])
+            q = ctx.matmul(xln, w["q"], bias=w["qb"])
+            k = ctx.matmul(xln, w["k"], bias=w["kb"])
+            v = ctx.matmul(xln, w["v"], bias=w["vb"])
+            p = ctx.matmul(peT, w["pos"])
+            ac = ctx.bmmQK(q, k, w["pbuAll"], H, HD, W)
+            bd = ctx.relShiftB(ctx.bmmQK(q, p, w["pbvAll"], H, HD, W, True), W * H)
+            probs = ctx.softmax(ctx.add(ac, bd))
+            outc = ctx.bmmPV(probs, v, H, HD, W)
+            x = ctx.matmul(outc, w["out"], bias=w["outb"], add=x)
+            pre1 = ctx.matmul(ln(x, w["lnconv"]), w["pw1T"], bias=w["pw1b"])
+            glu = ctx.glu(ctx.transpose(pre1))
+            if W == 1:
+                dwo = ctx.conv1d(glu, w["dw"], D, K, groups=D, padLeft=pad, padRight=pad, bias=w["dwb"], act="silu")
+            else:
+                dwo = ctx.alloc(D, W * Tsub)
+                for wi in range(W):
+                    ctx.setCols(dwo, ctx.conv1d(ctx.sliceCols(glu, wi * Tsub, Tsub), w["dw"], D, K, groups=D, padLeft=pad, padRight=pad,
+                                                bias=w["dwb"], act="silu"), wi * Tsub)
+            x = ctx.matmul(ctx.transpose(dwo), w["pw2T"], bias=w["pw2b"], add=x)
+            x = ff(x, w["lnff2"], w["ff2w1"], w["ff2w2"], w["ff2b1"], w["ff2b2"])
+            x = ln(x, w["lnout"])
+            ctx.pin(x, True)
+            ctx.popArena(arena)
+        return x
+
+    out = ctx.withBatchSync(run)
+    return out, Tsub
+
+
+# ── fused production path ───────────────────────────────────────────────────
+FORMATS = {"f16": L.W_F16, "int8": L.W_INT8, "int4": L.W_INT4}
+
+
+def tsub(T: int) -> int:
+    """Subsampled length of T mel frames (raw-encoder.js:217-218)."""
+    return int(lib().fa_encoder_tsub(int(T)))
+
+
+class FusedEncoder:
+    """Native whole-encoder forward (fa_encoder_load / fa_encoder_forward)."""
+
+    def __init__(self, ctx: HipContext, man: dict, fmt: str = "f16", max_T: int = 512, layers: int | None = None):
+        cfg = inferConfig(man)
+        if layers is not None:
+            cfg["layers"] = min(layers, cfg["layers"])
+        self.ctx, self.cfg, self.fmt, self.max_T = ctx, cfg, fmt, max_T
+        keep = {k: _f32(v).reshape(-1) for k, v in man.items()
+                if not (k.startswith("L") and int(k[1:k.index("_")]) >= cfg["layers"])}
+        names = list(keep)
+        arr_names = (C.c_char_p * len(names))(*[n.encode() for n in names])
+        arr_data = (L.F32P * len(names))(*[keep[n].ctypes.data_as(L.F32P) for n in names])
+        arr_cnt = (C.c_int64 * len(names))(*[keep[n].size for n in names])
+        c = L.EncoderCfg(*(cfg[k] for k in ("D", "DFF", "H", "HD", "layers", "dwK", "Csub", "Fsub", "melBins")))
+        p = L.P()
+        check(ctx._p, lib().fa_encoder_load(ctx._p, C.byref(c), len(names), arr_names, arr_data, arr_cnt, FORMATS[fmt], max_T, C.byref(p)))
+        self._p = p
+
+    def close(self):
+        if getattr(self, "_p", None):
+            lib().fa_encoder_destroy(self._p)
+            self._p = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def forward(self, mel: HipTensor, lens, layout: str = "packed", layers: int = -1) -> HipTensor:
+        """mel: packed/padded time-major [rows, melBins] tensor (packWindows);
+        returns [Σ Tsub, D] (packed) or [n*TsubMax, D] (padded) frames."""
+        l = np.ascontiguousarray(lens, np.int32)
+        o = L.T()
+        check(self.ctx._p, lib().fa_encoder_forward(self.ctx._p, self._p, mel.h, l.ctypes.data_as(L.I32P), len(l),
+                                                    0 if layout == "packed" else 1, layers, C.byref(o)))
+        return self.ctx._t(o.value)
+
+    def encode(self, mels: list, layout: str = "packed", layers: int = -1) -> np.ndarray:
+        """Convenience: list of [melBins, T_i] windows -> list of [Tsub_i, D] arrays."""
+        lens = [m.shape[1] for m in mels]
+        stream = np.concatenate([_f32(m) for m in mels], axis=1)
+        starts = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int32)
+        feats = self.ctx.upload(stream, stream.shape[0], stream.shape[1])
+        arena = self.ctx.pushArena()
+        try:
+            packed = self.ctx.packWindows(feats, starts, lens, layout)
+            y = self.forward(packed, lens, layout, layers)
+            out = self.ctx.download(y).reshape(y.rows, y.cols)
+        finally:
+            self.ctx.popArena(arena)
+            self.ctx.freeTensor(feats)
+        ts = [tsub(t) for t in lens]
+        res, off = [], 0
+        tmax = max(ts)
+        for i, t in enumerate(ts):
+            base = off if layout == "packed" else i * tmax
+            res.append(out[base:base + t].copy())
+            off += t
+        return res

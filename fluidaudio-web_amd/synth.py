@@ -1,0 +1,79 @@
+"""Synthetic encoder weights and features in the reference's manifest naming.
+
+There is no network and no checkpoint, so every benchmark and parity test
+runs on random-init weights of the real architecture.  Key names and shapes
+are the manifest's (src/engines/asr-parakeet/raw-encoder.js:28-35,101-158):
+  c{0..4}w / c{0..4}b      subsampling convs, [Cout, Cin/groups, kh, kw] flat
+  linw [Csub*Fsub, D], linb [D]
+  L{L}_{name}              per conformer layer; matrices are [in, out],
+                           pw1 [2D, D, 1], pw2 [D, D, 1], dw [D, 1, K]
+Parakeet has no linear biases (the optional *b keys are absent) and its
+BatchNorm is folded into dw/dwb.
+
+Distribution choices (documented build choices, seeded):
+  - layer matrices ~ N(0, 0.02) rounded to f16-representable values, so the
+    fp32 reference path and the f16-storage GPU path see identical weights;
+  - LayerNorm gamma = 1 + N(0, 0.02), beta = N(0, 0.02); pos_bias_u/v, dw bias
+    ~ N(0, 0.02);
+  - depthwise k=9 weights ~ N(0, 1/3) (a unit-gain conv, like a folded BN);
+  - subsampling convs use He-style std sqrt(2 / fan_in) so activations stay
+    O(1) through the front end instead of decaying into f16 subnormals.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+PARAKEET_CFG = dict(D=1024, DFF=4096, H=8, HD=128, layers=24, dwK=9, Csub=256, Fsub=16, melBins=128)
+
+
+def tiny_cfg(layers=2):
+    """Small config for CPU cross-checks (same structure, reduced dims)."""
+    return dict(D=64, DFF=256, H=2, HD=32, layers=layers, dwK=9, Csub=8, Fsub=4, melBins=32)
+
+
+def _f16r(a: np.ndarray) -> np.ndarray:
+    return a.astype(np.float16).astype(np.float32)
+
+
+def make_weights(cfg: dict, seed: int = 1, layers: int | None = None, biases: bool = False) -> dict:
+    """Random weights for `layers` layers (default cfg['layers']).  biases=True
+    adds the optional linear biases (Sortformer-style), exercising those
+    epilogue paths."""
+    rng = np.random.default_rng(seed)
+    D, DFF, H, HD, K, C, Fs = cfg["D"], cfg["DFF"], cfg["H"], cfg["HD"], cfg["dwK"], cfg["Csub"], cfg["Fsub"]
+    layers = cfg["layers"] if layers is None else layers
+    n = lambda shape, std: (rng.standard_normal(shape) * std).astype(np.float32)
+    m = {}
+    m["c0w"], m["c0b"] = _f16r(n((C, 1, 3, 3), np.sqrt(2 / 9))), n(C, 0.02)
+    m["c1w"], m["c1b"] = _f16r(n((C, 1, 3, 3), np.sqrt(2 / 9))), n(C, 0.02)
+    m["c2w"], m["c2b"] = _f16r(n((C, C, 1, 1), np.sqrt(2 / C))), n(C, 0.02)
+    m["c3w"], m["c3b"] = _f16r(n((C, 1, 3, 3), np.sqrt(2 / 9))), n(C, 0.02)
+    m["c4w"], m["c4b"] = _f16r(n((C, C, 1, 1), np.sqrt(2 / C))), n(C, 0.02)
+    m["linw"], m["linb"] = _f16r(n((C * Fs, D), 0.02)), n(D, 0.02)
+    for L in range(layers):
+        g = lambda s: f"L{L}_{s}"
+        for ln in ("lnff1", "lnatt", "lnconv", "lnff2", "lnout"):
+            m[g(ln + "_w")] = (1 + n(D, 0.02)).astype(np.float32)
+            m[g(ln + "_b")] = n(D, 0.02)
+        m[g("ff1w1")], m[g("ff1w2")] = _f16r(n((D, DFF), 0.02)), _f16r(n((DFF, D), 0.02))
+        m[g("ff2w1")], m[g("ff2w2")] = _f16r(n((D, DFF), 0.02)), _f16r(n((DFF, D), 0.02))
+        for k in ("q", "k", "v", "pos", "out"):
+            m[g(k)] = _f16r(n((D, D), 0.02))
+        m[g("pbu")], m[g("pbv")] = n((H, HD), 0.02), n((H, HD), 0.02)
+        m[g("pw1")] = _f16r(n((2 * D, D, 1), 0.02))
+        m[g("pw2")] = _f16r(n((D, D, 1), 0.02))
+        m[g("dw")] = _f16r(n((D, 1, K), np.sqrt(1 / 3)))
+        m[g("dwb")] = n(D, 0.02)
+        if biases:
+            for k in ("ff1b1", "ff2b1", "pw1b"):
+                m[g(k)] = n(DFF if k != "pw1b" else 2 * D, 0.02)
+            for k in ("ff1b2", "ff2b2", "qb", "kb", "vb", "outb", "pw2b"):
+                m[g(k)] = n(D, 0.02)
+    return m
+
+
+def make_features(melBins: int, T: int, seed: int = 1, W: int = 1) -> list:
+    """W synthetic log-mel windows [melBins, T] ~ N(0, 1), channel-major like the
+    reference's mel output (raw-encoder.js:224)."""
+    rng = np.random.default_rng(seed)
+    return [rng.standard_normal((melBins, T)).astype(np.float32) for _ in range(W)]

@@ -1,0 +1,215 @@
+/*
+ * fa_hip.h — C ABI of the MI355X (gfx950) backend for fluidaudio-web's
+ * Parakeet FastConformer encoder path.
+ *
+ * The ABI mirrors the reference's backend contract, `ComputeContext`
+ * (src/gpu/compute.d.ts:106-255), restricted to the members the encoder uses,
+ * plus one fused whole-encoder entry that replaces the op-by-op
+ * `parakeetEncodeBatch` (src/engines/asr-parakeet/raw-encoder.js:235-386).
+ * A host binds it through FFI (N-API addon, ctypes); nothing here exposes a
+ * C++ or torch type.  Each declaration cites the reference member it replaces.
+ *
+ * Conventions
+ *  - Every call returns FA_OK (0) or an error code; fa_last_error(ctx) then
+ *    holds the message (the reference throws an Error with that text).
+ *  - Tensors are opaque 64-bit handles (0 = none).  A tensor is a 2-D
+ *    row-major matrix {rows, cols}; storage is device memory owned by the
+ *    context.  Using a handle after its arena closed or after fa_free_tensor
+ *    fails with FA_E_INVALID ("stale tensor handle") instead of touching
+ *    recycled memory.
+ *  - All work is ordered on the context's single HIP stream, so a later op
+ *    always sees the results of earlier ones; only download/staged reads wait.
+ *  - Calls are not thread-safe: one host thread drives one context, as one JS
+ *    thread drives a GpuContext.
+ */
+#ifndef FA_HIP_H
+#define FA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct fa_ctx fa_ctx;
+typedef struct fa_encoder fa_encoder;
+typedef uint64_t fa_tensor; /* 0 = null */
+typedef uint64_t fa_arena;  /* 0 = "the newest open arena" */
+typedef uint64_t fa_staged;
+
+enum fa_status {
+  FA_OK = 0,
+  FA_E_INVALID = 1,     /* bad argument, shape mismatch, stale handle */
+  FA_E_STATE = 2,       /* misuse: nested batch, second staged read, ... */
+  FA_E_DEVICE = 3,      /* HIP runtime error */
+  FA_E_OOM = 4,         /* device allocation failed */
+  FA_E_UNSUPPORTED = 5  /* shape/format the kernels do not cover */
+};
+
+/* Activation codes: src/gpu/kernels/actf.js:24 (ACT). */
+enum fa_act { FA_ACT_NONE = 0, FA_ACT_GELU = 1, FA_ACT_TANH = 2, FA_ACT_RELU = 3, FA_ACT_SILU = 4, FA_ACT_GELU_ERF = 5 };
+
+/* Tensor storage kinds reported by fa_tensor_info. */
+enum fa_dtype { FA_F32 = 0, FA_F16 = 1, FA_BYTES = 2 };
+
+/* ── lifecycle ───────────────────────────────────────────────────────────────
+ * Replaces createContext / new GpuContext(device) (src/gpu/context.js:23-37,
+ * src/gpu/compute.js:78) and destroy() (compute.d.ts:133). */
+int fa_ctx_create(int device, fa_ctx **out);
+void fa_ctx_destroy(fa_ctx *ctx);
+const char *fa_last_error(const fa_ctx *ctx);
+/* Library version string, e.g. "fa_hip 0.1 gfx950". */
+const char *fa_version(void);
+/* Wait for all queued work (no reference counterpart; hosts use it before timing). */
+int fa_sync(fa_ctx *ctx);
+
+/* ── tensors & memory: compute.d.ts:110-133 ─────────────────────────────────── */
+int fa_upload(fa_ctx *ctx, const float *data, int rows, int cols, fa_tensor *out);     /* upload */
+int fa_upload_f16(fa_ctx *ctx, const float *data, int rows, int cols, fa_tensor *out); /* uploadF16: f16 storage (RNE) */
+int fa_alloc(fa_ctx *ctx, int rows, int cols, fa_tensor *out);                         /* alloc (uninitialised) */
+int fa_alloc_f16(fa_ctx *ctx, int rows, int cols, fa_tensor *out);                     /* allocF16 */
+int fa_upload_bytes(fa_ctx *ctx, const void *data, size_t nbytes, fa_tensor *out);     /* uploadBytes (int8/int4 payloads) */
+int fa_free_tensor(fa_ctx *ctx, fa_tensor t);                                          /* freeTensor (f16/views ignored) */
+int fa_pin(fa_ctx *ctx, fa_tensor t, int to_parent);                                   /* pin */
+int fa_push_arena(fa_ctx *ctx, fa_arena *out);                                         /* pushArena */
+int fa_pop_arena(fa_ctx *ctx, fa_arena handle);                                        /* popArena (0 = newest) */
+int fa_trim_pool(fa_ctx *ctx, size_t budget_bytes);                                    /* trimPool */
+int fa_tensor_info(fa_ctx *ctx, fa_tensor t, int *rows, int *cols, int *dtype);
+/* Pool telemetry (poolInfo/memStats, compute.d.ts:252-254). */
+int fa_pool_info(fa_ctx *ctx, size_t *pooled_bytes, uint64_t *created, uint64_t *created_bytes, uint64_t *reused);
+
+/* ── readback: compute.d.ts:136-145 ─────────────────────────────────────────── */
+int fa_download(fa_ctx *ctx, fa_tensor t, float *out);          /* download (rows*cols floats) */
+int fa_stage_download(fa_ctx *ctx, fa_tensor t, fa_staged *out); /* stageDownload */
+int fa_staged_read(fa_ctx *ctx, fa_staged s, float *out);        /* StagedRead.read (single-use) */
+int fa_rows_view(fa_ctx *ctx, fa_tensor t, int rows, fa_tensor *out); /* rowsView */
+
+/* ── batching: compute.d.ts:148-151 ─────────────────────────────────────────── */
+int fa_begin_batch(fa_ctx *ctx); /* beginBatch (nesting is FA_E_STATE) */
+int fa_end_batch(fa_ctx *ctx);   /* endBatch */
+int fa_batch_open(fa_ctx *ctx);  /* 1 when a batch is open */
+
+/* ── linear algebra: compute.d.ts:155-168 ───────────────────────────────────── */
+/* matmul: C = act(A[M,K] @ B[K,N] + bias[1,N]) (+ add[M,N]).  B may be f32
+ * (fp32 MFMA path) or f16 (A rounded to f16, f16 MFMA, f32 accumulate — the
+ * reference's f16-compute route, compute.js:413-416). */
+int fa_matmul(fa_ctx *ctx, fa_tensor a, fa_tensor b, fa_tensor bias, int act, fa_tensor add, fa_tensor *out);
+/* matmulInt8: wq = int8 [K,N] row-major bytes (4 per u32, gemm.js:679-708),
+ * scale [1,N] per output column; out = act(scale[n]·Σ a·q + bias). */
+int fa_matmul_int8(fa_ctx *ctx, fa_tensor a, fa_tensor wq, fa_tensor scale, int N, int K, fa_tensor bias, int act, fa_tensor *out);
+/* matmulNBits: ONNX MatMulNBits (bits=4): bq [N][nblk][16 B], scales f32
+ * [N*nblk], zp packed int4 [N][ceil(nblk/2)] (gemm.js:893-919). */
+int fa_matmul_nbits(fa_ctx *ctx, fa_tensor a, fa_tensor bq, fa_tensor scales, fa_tensor zp, int N, int block_size, fa_tensor *out);
+int fa_layernorm(fa_ctx *ctx, fa_tensor x, fa_tensor gamma, fa_tensor beta, float eps, fa_tensor *out); /* layernorm */
+int fa_softmax(fa_ctx *ctx, fa_tensor x, fa_tensor *out);                                               /* softmax */
+
+/* ── convolution: compute.d.ts:172-179 ──────────────────────────────────────── */
+/* conv1d: x [Cin, L], w = Cout*(Cin/groups)*K, out [Cout, Lout]. */
+int fa_conv1d(fa_ctx *ctx, fa_tensor x, fa_tensor w, int cout, int k, fa_tensor bias, int stride, int pad_left, int pad_right, int dilation,
+              int groups, int act, fa_tensor *out);
+/* conv2d (batch 1): x [Cin, H*W], w [Cout, Cin/groups, kh, kw] flat, out [Cout, Ho*Wo]. */
+int fa_conv2d(fa_ctx *ctx, fa_tensor x, fa_tensor w, int cout, int cin, int h, int wd, int kh, int kw, fa_tensor bias, int stride_h, int stride_w,
+              int pad_top, int pad_bottom, int pad_left, int pad_right, int groups, int act, fa_tensor *out);
+
+/* ── attention: compute.d.ts:191-197 ────────────────────────────────────────── */
+int fa_bmm_qk(fa_ctx *ctx, fa_tensor q, fa_tensor b, fa_tensor qb, int H, int HD, int W, int b_shared, fa_tensor *out); /* bmmQK */
+int fa_bmm_pv(fa_ctx *ctx, fa_tensor p, fa_tensor v, int H, int HD, int W, fa_tensor *out);                          /* bmmPV */
+int fa_rel_shift(fa_ctx *ctx, fa_tensor x, fa_tensor *out);                                                           /* relShift */
+int fa_rel_shift_b(fa_ctx *ctx, fa_tensor x, int H, fa_tensor *out);                                                  /* relShiftB */
+/* attnFused (compute.d.ts:248): fused rel-pos attention over W windows of T
+ * rows; q/k/v [W*T, H*HD], pos [2T-1, H*HD], pbu/pbv [1, H*HD].  Unlike the
+ * reference (T <= 256, compute.js:680) any T up to 1024 is accepted. */
+int fa_attn_fused(fa_ctx *ctx, fa_tensor q, fa_tensor k, fa_tensor v, fa_tensor pos, fa_tensor pbu, fa_tensor pbv, int H, int HD, int W,
+                  fa_tensor *out);
+
+/* ── elementwise & data movement: compute.d.ts:202-228 ──────────────────────── */
+int fa_ewise(fa_ctx *ctx, fa_tensor a, fa_tensor b, int op /*0 add, 1 mul*/, fa_tensor *out); /* ewise/add/mul (b [1,cols] broadcasts) */
+int fa_scale(fa_ctx *ctx, fa_tensor x, float s, fa_tensor *out);
+int fa_silu(fa_ctx *ctx, fa_tensor x, fa_tensor *out);
+int fa_relu(fa_ctx *ctx, fa_tensor x, fa_tensor *out);
+int fa_glu(fa_ctx *ctx, fa_tensor x, fa_tensor *out); /* [2C,T] -> [C,T], gate clamped to ±30 (tensor-ops.js:5-19) */
+int fa_transpose(fa_ctx *ctx, fa_tensor x, fa_tensor *out);
+int fa_slice_cols(fa_ctx *ctx, fa_tensor x, int col0, int width, fa_tensor *out);
+int fa_set_cols(fa_ctx *ctx, fa_tensor dst, fa_tensor src, int col0);
+int fa_slice_rows(fa_ctx *ctx, fa_tensor x, int row0, int count, fa_tensor *out);
+int fa_copy_rows(fa_ctx *ctx, fa_tensor dst, fa_tensor src, int row_offset);
+int fa_concat_rows(fa_ctx *ctx, const fa_tensor *ts, int n, fa_tensor *out);
+int fa_sub_reshape(fa_ctx *ctx, fa_tensor x, int C, int Tsub, int F, fa_tensor *out); /* subReshape */
+int fa_row_bias_act(fa_ctx *ctx, fa_tensor x, fa_tensor bias, int act, fa_tensor *out); /* rowBiasAct (compute.d.ts:249) */
+
+/* ── profiling: startProfile/endProfile (compute.d.ts:250-251) ──────────────────
+ * While a profile is open every kernel launch is bracketed by HIP events on
+ * the context stream.  fa_profile_end waits, then returns up to `cap` records
+ * (label, milliseconds) and the number recorded in *count. */
+int fa_profile_start(fa_ctx *ctx, int max_ops);
+int fa_profile_end(fa_ctx *ctx, int cap, char (*labels)[48], float *ms, int *count);
+
+/* ── weight-only quantised formats (no single reference function: the
+ * quantiser is scripts/quantize-parakeet-encoder.py:31-36, the dequant
+ * raw-encoder.js:64-75; int4 follows MatMulNBits, lib.rs:164-203) ─────────── */
+/* Dequantise int8 per-column [K,N] (q·scale[n], exact in f32) into out [K,N] f32. */
+int fa_dequant_int8(fa_ctx *ctx, fa_tensor wq, fa_tensor scale, int K, int N, fa_tensor *out);
+/* Dequantise symmetric int4 group-32 (bq [N][K/32][16 B], f16 scale bits
+ * [N][K/32] as bytes) into out [K,N] f32: (nibble-8)·scale. */
+int fa_dequant_int4(fa_ctx *ctx, fa_tensor bq, fa_tensor scales_f16, int K, int N, fa_tensor *out);
+
+/* Skinny weight-only GEMV (M <= 64): y [M,N] f32 = a[M,K] (f32) @ W, W int8
+ * per-column (scale f32 [N]) or int4 group-32 (f16 scale bits).  format: 1 =
+ * int8 ([N][K] K-major bytes), 2 = int4 (bq [N][K/32][16 B]).  The weight
+ * layouts are the ones the fused encoder stores (see fa_encoder_load). */
+int fa_gemv_quant(fa_ctx *ctx, fa_tensor a, fa_tensor w, fa_tensor scales, int format, int N, int K, fa_tensor *out);
+
+/* ── ragged window packing (the new batched-window path) ──────────────────────
+ * Cuts n windows [start_i, start_i+len_i) out of a channel-major feature
+ * stream feats [melBins, Ttotal] (the reference's mel layout,
+ * raw-encoder.js:181-182 transposes it per window on the host) and packs
+ * them time-major into out.
+ *   layout 0 (packed):  out [Σ len_i, melBins], window i at row Σ_{j<i} len_j;
+ *   layout 1 (padded):  out [n*Tmax, melBins], window i at row i*Tmax, rows
+ *                       past len_i zero-filled; Tmax = max len_i.
+ * Windows may overlap in the stream.  starts/lens are host arrays. */
+int fa_pack_windows(fa_ctx *ctx, fa_tensor feats, const int32_t *starts, const int32_t *lens, int n, int layout, fa_tensor *out);
+/* Row -> window index map of a batch (the index map every window-aware kernel
+ * uses), computed on the device and copied to host_map: entry r is the window
+ * owning row r, or -1 for a padding row.  stage 0 = mel frames, 1..3 = after
+ * each stride-2 subsampling conv (3 = encoder frames).  Call with host_map ==
+ * NULL to get the row count in *rows first. */
+int fa_window_row_map(fa_ctx *ctx, const int32_t *lens, int n, int layout, int stage, int32_t *host_map, int *rows);
+
+/* ── fused encoder: loadParakeetEncoder + parakeetEncodeBatch
+ * (raw-encoder.js:39-161, 235-386) ────────────────────────────────────────── */
+typedef struct fa_encoder_cfg {
+  int D, DFF, H, HD, layers, dwK, Csub, Fsub, melBins;
+} fa_encoder_cfg;
+
+/* Weight storage formats for the encoder's linears. */
+enum fa_weight_format { FA_W_F16 = 0, FA_W_INT8 = 1, FA_W_INT4 = 2 };
+
+/* Load weights given as manifest entries (name, f32 data, element count); the
+ * names are the reference manifest's ("c0w", "linw", "L3_ff1w1", ...).  The
+ * load-time folds of raw-encoder.js:124-156 (q·1/√HD, pos_bias·1/√HD, FF
+ * linear2·0.5) are applied here.  `format` picks the storage of the layer
+ * linears: f16, int8 per-output-channel (quantize-parakeet-encoder.py:31-36)
+ * or int4 symmetric group-32 with f16 scales; dequant is fused into the GEMM
+ * loads.  max_T bounds the subsampled window length (frames per window after
+ * the 8x front end) the encoder will accept (<= 1024). */
+int fa_encoder_load(fa_ctx *ctx, const fa_encoder_cfg *cfg, int n, const char *const *names, const float *const *data, const int64_t *counts,
+                    int format, int max_T, fa_encoder **out);
+void fa_encoder_destroy(fa_encoder *enc);
+
+/* Encode a batch of windows.  mel: [Σ len_i, melBins] (layout 0) or
+ * [n*Tmax, melBins] (layout 1) time-major f32 rows as fa_pack_windows makes
+ * them; lens: host mel-frame lengths.  out receives [Σ Tsub_i, D] (layout 0)
+ * or [n*TsubMax, D] (layout 1, rows past a window's Tsub are zero) f32
+ * frames.  Each window's frames equal its standalone encode: attention keys,
+ * the depthwise conv and the subsampling convs never cross window bounds.
+ * layers_run < 0 runs all layers. */
+int fa_encoder_forward(fa_ctx *ctx, fa_encoder *enc, fa_tensor mel, const int32_t *lens, int n, int layout, int layers_run, fa_tensor *out);
+/* Subsampled length of a window of T mel frames (raw-encoder.js:217-218). */
+int fa_encoder_tsub(int T);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FA_HIP_H */

@@ -1,0 +1,72 @@
+"""Fused encoder (fa_encoder_forward) parity against the CPU oracle's
+restatement of parakeetEncodeBatch, on reduced dims the oracle finishes in
+seconds.  Bar: rel-L2 <= 1e-2 vs the fp32 path, and
+frame-wise argmax of a fixed random projection R [D, 64] ~ N(0,1) (seed 2)
+identical on >= 99.9% of frames."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(D=256, DFF=1024, H=2, HD=128, layers=2, dwK=9, Csub=64, Fsub=16, melBins=128)
+
+
+def rel_l2(a, b):
+    return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+
+
+def argmax_agree(a, b, D, seed=2):
+    R = np.random.default_rng(seed).standard_normal((D, 64)).astype(np.float32)
+    return float(np.mean(np.argmax(a @ R, 1) == np.argmax(b @ R, 1)))
+
+
+@pytest.fixture(scope="module")
+def small(fa):
+    return fa.synth.make_weights(SMALL, seed=1)
+
+
+def test_fused_single_window(ctx, fa, orc, small):
+    mel = fa.synth.make_features(128, 300, seed=4)
+    enc = fa.FusedEncoder(ctx, small, "f16", max_T=128)
+    got = enc.encode(mel)[0]
+    ref = orc.encode_batch(SMALL, small, mel)
+    assert got.shape == ref.shape
+    assert rel_l2(got, ref) <= 1e-2
+    enc.close()
+
+
+def test_fused_batch_equals_oracle_batch(ctx, fa, orc, small):
+    mels = fa.synth.make_features(128, 200, seed=5, W=3)
+    enc = fa.FusedEncoder(ctx, small, "f16", max_T=128)
+    got = np.concatenate(enc.encode(mels))
+    ref = orc.encode_batch(SMALL, small, mels)
+    assert rel_l2(got, ref) <= 1e-2
+    assert argmax_agree(got, ref, SMALL["D"]) >= 0.999
+    enc.close()
+
+
+@pytest.mark.parametrize("layout", ["packed", "padded"])
+def test_ragged_windows_equal_standalone(ctx, fa, small, layout):
+    """Each window of a ragged batch equals its standalone encode (the
+    W-vs-1 equivalence of scripts/parakeet-profile.mjs:67-79, maxΔ < 1e-4 there)."""
+    lens = [333, 80, 257, 401, 9]
+    mels = [fa.synth.make_features(128, t, seed=10 + i)[0] for i, t in enumerate(lens)]
+    enc = fa.FusedEncoder(ctx, small, "f16", max_T=128)
+    batch = enc.encode(mels, layout=layout)
+    for m, g in zip(mels, batch):
+        alone = enc.encode([m])[0]
+        assert g.shape == alone.shape == (fa.tsub(m.shape[1]), SMALL["D"])
+        assert np.abs(g - alone).max() < 1e-4
+    enc.close()
+
+
+@pytest.mark.parametrize("fmt,tol", [("int8", 2e-2), ("int4", 1e-1)])
+def test_quantized_encoder_tracks_f16(ctx, fa, small, fmt, tol):
+    mels = fa.synth.make_features(128, 240, seed=6, W=2)
+    e16 = fa.FusedEncoder(ctx, small, "f16", max_T=128)
+    eq = fa.FusedEncoder(ctx, small, fmt, max_T=128)
+    a = np.concatenate(e16.encode(mels))
+    b = np.concatenate(eq.encode(mels))
+    assert rel_l2(b, a) <= tol
+    e16.close()
+    eq.close()
