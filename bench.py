@@ -1,0 +1,275 @@
+"""Benchmark: the fused Parakeet FastConformer encoder on one MI355X.
+
+Default workload: the full 24-layer encoder with
+the dw-striding 8x front end over 16 windows of 15 s (1500 log-mel frames,
+128 bins, ~N(0,1), seed 1), random-init f16 weights (seed 1).  One step =
+pack the 16 windows out of the resident feature stream + the whole encoder
+forward.  value = audio-s / wall-s over the K timed steps (inputs resident in
+HBM, output left on the device).
+
+The JSON line also carries
+  roofline      the dominant kernel (by total time in the timed region),
+                timed live with HIP events on the encoder's stream, against
+                the MI355X dense f16 MFMA peak (or HBM peak for bandwidth
+                kernels); flops/bytes are algorithmic (valid rows only);
+  kernels       the same for every kernel class, and the GEMM aggregate;
+  cpu_baseline  the CPU oracle (a restatement of the reference's WASM path:
+                SSE f32 GEMM without FMA, JS-double LN/softmax/conv) on one
+                core, on a bounded sample: preEncode of one window plus one
+                conformer layer at full dims, scaled to 24 layers.
+
+Other workloads (--workload): layer, ragged,
+gemv (configs[4] GEMV), quant (configs[4] encoder).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+import __graft_entry__ as ge  # noqa: E402
+
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16
+HBM_PEAK_GBS = 8000.0
+FULL = dict(D=1024, DFF=4096, H=8, HD=128, layers=24, dwK=9, Csub=256, Fsub=16, melBins=128)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ── algorithmic work per kernel launch (valid rows only) ────────────────────
+def kernel_work(cfg, lens, layout):
+    """label -> (kind, amount per launch); kind 'flop' (MFMA) or 'byte' (HBM)."""
+    enc = ge.load_package()
+    D, DFF, C, F, MB = cfg["D"], cfg["DFF"], cfg["Csub"], cfg["Fsub"], cfg["melBins"]
+    s2 = lambda t: (t - 1) // 2 + 1
+    T1 = [s2(t) for t in lens]
+    T2 = [s2(t) for t in T1]
+    T3 = [s2(t) for t in T2]
+    R0, R1, R2, M = sum(lens), sum(T1), sum(T2), sum(T3)
+    att = sum(2 * t * t * D * 3 for t in T3)  # (q+u)kᵀ, bd (t x t band entries used), P·V
+    return {
+        "pack_windows": ("byte", R0 * MB * 8),
+        "sub_c0": ("byte", R0 * MB * 4 + R1 * (MB // 2) * C * 2),
+        "sub_dw1": ("byte", R1 * (MB // 2) * C * 2 + R2 * (MB // 4) * C * 2),
+        "sub_pw2": ("flop", 2 * R2 * (MB // 4) * C * C),
+        "sub_dw3": ("byte", R2 * (MB // 4) * C * 2 + M * F * C * 2),
+        "sub_pw4": ("flop", 2 * M * F * C * C),
+        "sub_linear": ("flop", 2 * M * F * C * D),
+        "ln_ff1": ("byte", M * D * 6), "ln_att": ("byte", M * D * 6), "ln_conv": ("byte", M * D * 6), "ln_ff2": ("byte", M * D * 6),
+        "ln_out": ("byte", M * D * 8),
+        "ff1_w1": ("flop", 2 * M * D * DFF), "ff1_w2": ("flop", 2 * M * D * DFF),
+        "ff2_w1": ("flop", 2 * M * D * DFF), "ff2_w2": ("flop", 2 * M * D * DFF),
+        "qkv": ("flop", 2 * M * D * 3 * D), "attn_out": ("flop", 2 * M * D * D),
+        "pw1_glu": ("flop", 2 * M * D * 2 * D), "pw2": ("flop", 2 * M * D * D),
+        "attention": ("flop", att),
+        "dwconv": ("byte", M * D * 4),
+        "zero_pad": ("byte", 0),
+    }
+
+
+def summarize(prof, work, steps):
+    agg = {}
+    for r in prof:
+        a = agg.setdefault(r["label"], [0, 0.0])
+        a[0] += 1
+        a[1] += r["ms"]
+    out = {}
+    for lab, (n, ms) in agg.items():
+        kind, amt = work.get(lab, ("byte", 0))
+        avg = ms / n
+        rec = {"launches": n, "avg_us": round(avg * 1e3, 2), "total_ms_per_step": round(ms / steps, 3)}
+        if amt:
+            if kind == "flop":
+                tf = amt / (avg * 1e-3) / 1e12
+                rec.update(tflops=round(tf, 1), frac=round(tf / MFMA_F16_PEAK_TFLOPS, 4), bound="mfma")
+            else:
+                gbs = amt / (avg * 1e-3) / 1e9
+                rec.update(gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4), bound="hbm")
+        out[lab] = rec
+    return out
+
+
+def cpu_baseline(seconds_budget=30.0):
+    """Oracle on 1 core: preEncode of one 15 s window + one full-size layer,
+    scaled to the 24-layer encoder.  Returns the cpu_baseline object."""
+    fa = ge.load_package()
+    orc = ge.load_oracle()
+    orc.set_threads(1)
+    cfg = dict(FULL)
+    man = fa.synth.make_weights(cfg, seed=1, layers=1)
+    mel = fa.synth.make_features(128, 1500, seed=1)
+    t0 = time.perf_counter()
+    orc.encode_batch(cfg, man, mel, layers=0)
+    t_pre = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    orc.encode_batch(cfg, man, mel, layers=1)
+    t_layer = time.perf_counter() - t0 - t_pre
+    per_window = t_pre + 24 * t_layer
+    return {"value": round(15.0 / per_window, 3), "unit": "audio-s/wall-s", "cores": 1, "kind": "port",
+            "sample": f"1 window x 15 s: preEncode {t_pre:.2f} s + 1 of 24 layers {t_layer:.2f} s, scaled to 24 layers "
+                      f"(oracle/fa_oracle.c, single thread; {os.cpu_count()} host cores visible)"}
+
+
+def run_encoder(args, fa, ctx, cfg, lens, layout, fmt="f16", seed=1):
+    man = fa.synth.make_weights(cfg, seed=seed)
+    log(f"[bench] weights generated ({sum(v.size for v in man.values()) / 1e6:.0f} M values); loading {fmt}")
+    enc = fa.FusedEncoder(ctx, man, fmt, max_T=max(fa.tsub(int(t)) for t in lens))
+    del man
+    rng = np.random.default_rng(seed)
+    total = int(sum(lens))
+    stream = rng.standard_normal((cfg["melBins"], total), dtype=np.float32)
+    feats = ctx.upload(stream, cfg["melBins"], total)
+    starts = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int32)
+    lens = np.asarray(lens, np.int32)
+
+    def step():
+        a = ctx.pushArena()
+        mel = ctx.packWindows(feats, starts, lens, layout)
+        enc.forward(mel, lens, layout)
+        ctx.popArena(a)
+
+    for _ in range(args.warmup):
+        step()
+    ctx.sync()
+    # discovery pass: every launch bracketed, to rank kernels and fill `kernels`
+    ctx.startProfile(200000)
+    for _ in range(2):
+        step()
+    prof_all = ctx.endProfile()
+    totals = {}
+    for r in prof_all:
+        totals[r["label"]] = totals.get(r["label"], 0.0) + r["ms"]
+    dom = max(totals, key=totals.get)
+    # timed region: K steps, only the dominant kernel's launches bracketed by
+    # HIP events on the encoder stream (few events: the timeline is unperturbed)
+    ctx.sync()
+    ctx.startProfile(200000, only=dom)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    prof_dom = [r for r in ctx.endProfile() if r["label"] == dom]
+    enc.close()
+    ctx.freeTensor(feats)
+    return wall, prof_all, dom, prof_dom
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", default="encoder", choices=["encoder", "layer", "ragged", "quant", "gemv"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); multi-GPU runs are not part of it", file=sys.stderr)
+        sys.exit(2)
+    fa = ge.load_package()
+    ctx = fa.createContext("hip")
+    if args.workload == "gemv":
+        return bench_gemv(args, fa, ctx)
+    cfg = dict(FULL)
+    layout = "packed"
+    if args.workload in ("encoder", "quant"):
+        lens = [1500] * 16
+        workload = ("configs[2]: 24-layer FastConformer encoder + dw-striding 8x subsampling, 16 windows x 15 s "
+                    "(1500 mel frames), packed on-GPU")
+    elif args.workload == "layer":
+        cfg["layers"] = 1
+        lens = [1500] * 8
+        workload = "configs[1]-shaped: one FastConformer layer (plus front end), 8 windows x 188 frames"
+    else:
+        from importlib import import_module  # noqa: F401
+
+        starts, lens = fa.windowing.planRaggedWindows(360000, 200, 3000, 100, seed=1)
+        lens = list(lens[:32])
+        workload = "configs[3] batch: 32 ragged windows (2-30 s) cut from the 3600 s stream, packed"
+    fmt = "int8" if args.workload == "quant" else "f16"
+    wall, prof_all, dom, prof_dom = run_encoder(args, fa, ctx, cfg, lens, layout, fmt)
+    audio_s = sum(lens) * 0.01 * args.steps
+    work = kernel_work(cfg, lens, layout)
+    kern = summarize(prof_all, work, 2)
+    gemm_labels = [k for k, v in kern.items() if v.get("bound") == "mfma" and k != "attention"]
+    gemm_ms = sum(kern[k]["total_ms_per_step"] for k in gemm_labels)
+    gemm_flop = sum(work[k][1] * kern[k]["launches"] / 2 for k in gemm_labels)
+    gemm_tf = gemm_flop / (gemm_ms * 1e-3) / 1e12 if gemm_ms else 0.0
+    dom_us = sum(r["ms"] for r in prof_dom) / len(prof_dom) * 1e3
+    kind, amt = work.get(dom, ("byte", 0))
+    if kind == "flop":
+        ach = amt / (dom_us * 1e-6) / 1e12
+        roof = {"bound": "mfma", "achieved": round(ach, 1), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK_TFLOPS, 4)}
+    else:
+        ach = amt / (dom_us * 1e-6) / 1e9
+        roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4)}
+    roof.update(kernel=dom, traffic=None, avg_us=round(dom_us, 2), launches_timed=len(prof_dom))
+    res = {
+        "metric": "encoder audio-s/wall-s at 1 GPU", "value": round(audio_s / wall, 1), "unit": "audio-s/wall-s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f16" if fmt == "f16" else f"{fmt}-weights/f16",
+        "data": "synthetic log-mel ~N(0,1) (seed 1), random-init weights (seed 1)",
+        "config": {"workload": workload, "windows": len(lens), "mel_frames": int(sum(lens)), "layers": cfg["layers"], "weights": fmt,
+                   "parallelism": "single GPU"},
+        "roofline": roof,
+        "gemm_aggregate": {"tflops": round(gemm_tf, 1), "frac": round(gemm_tf / MFMA_F16_PEAK_TFLOPS, 4), "ms_per_step": round(gemm_ms, 3)},
+        "kernels": kern,  # discovery pass (every launch event-bracketed: inflated by the events)
+    }
+    if not args.no_cpu and args.workload == "encoder":
+        log("[bench] CPU baseline (oracle, 1 core, bounded sample)")
+        res["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(res), flush=True)
+
+
+def bench_gemv(args, fa, ctx):
+    """configs[4] GEMV: M in {1,4,16} x K=1024 x N=4096, int8 / int4 weights,
+    distinct weight buffers rotated (> 256 MB total) so the MALL cannot serve them."""
+    K, N = 1024, 4096
+    rng = np.random.default_rng(1)
+    out = {}
+    for fmt, code, wbytes in (("int8", 1, K * N), ("int4", 2, K * N // 2)):
+        nbuf = max(2, (320 << 20) // wbytes + 1)
+        sbytes = N * 4 if code == 1 else N * (K // 32) * 2
+        ws = [ctx.uploadBytes(rng.integers(0, 256, wbytes, dtype=np.uint8)) for _ in range(nbuf)]
+        if code == 1:
+            ss = [ctx.upload(rng.random(N, dtype=np.float32) * 0.01, 1, N) for _ in range(nbuf)]
+        else:
+            ss = [ctx.uploadBytes((rng.random(N * K // 32, dtype=np.float32) * 0.01).astype(np.float16)) for _ in range(nbuf)]
+        for M in (1, 4, 16):
+            a = ctx.upload(rng.standard_normal((M, K), dtype=np.float32), M, K)
+            def call(i):
+                ar = ctx.pushArena()
+                ctx.gemvQuant(a, ws[i], ss[i], code, N, K)
+                ctx.popArena(ar)
+
+            for i in range(nbuf):
+                call(i)
+            ctx.sync()
+            ctx.startProfile(100000)
+            t0 = time.perf_counter()
+            reps = 4
+            for _ in range(reps):
+                for i in range(nbuf):
+                    call(i)
+            ctx.sync()
+            wall = time.perf_counter() - t0
+            prof = ctx.endProfile()
+            ms = [r["ms"] for r in prof if r["label"].startswith("gemv")]
+            avg = sum(ms) / len(ms)
+            by = wbytes + sbytes + M * K * 4 + M * N * 4
+            out[f"{fmt}_M{M}"] = {"avg_us": round(avg * 1e3, 2), "gbs": round(by / (avg * 1e-3) / 1e9, 1),
+                                  "frac": round(by / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                  "wall_us_per_call": round(wall / (reps * nbuf) * 1e6, 2), "buffers": nbuf}
+    print(json.dumps({"metric": "weight-only quantised GEMV HBM GB/s", "workload": "configs[4] GEMV K=1024 N=4096", "results": out}), flush=True)
+
+
+if __name__ == "__main__":
+    main()

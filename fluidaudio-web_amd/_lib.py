@@ -88,6 +88,7 @@ SIGNATURES = [
     ("fa_row_bias_act", I, [P, T, T, I, C.POINTER(T)]),
     ("fa_profile_start", I, [P, I]),
     ("fa_profile_end", I, [P, I, C.c_void_p, F32P, C.POINTER(I)]),
+    ("fa_profile_only", I, [P, C.c_char_p]),
     ("fa_dequant_int8", I, [P, T, T, I, I, C.POINTER(T)]),
     ("fa_dequant_int4", I, [P, T, T, I, I, C.POINTER(T)]),
     ("fa_gemv_quant", I, [P, T, T, T, I, I, I, C.POINTER(T)]),

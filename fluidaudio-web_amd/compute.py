@@ -368,8 +368,10 @@ class HipContext:
         return HipTensor(self, o.value, x.rows, x.cols)
 
     # ── profiling (compute.d.ts:250-251) ──────────────────────────────────
-    def startProfile(self, maxOps=4096):
+    def startProfile(self, maxOps=4096, only=None):
+        """Bracket launches with HIP events; `only` restricts it to labels with that prefix."""
         self._prof_cap = maxOps
+        check(self._p, lib().fa_profile_only(self._p, (only or "").encode()))
         check(self._p, lib().fa_profile_start(self._p, maxOps))
 
     def endProfile(self):

@@ -185,9 +185,9 @@ int relpos_attention(fa_ctx *ctx, const AttnArgs &a, int in_f32, int out_f32, in
   dim3 grid(cdiv(Tmax, 64), a.H, W);
   ProfScope ps(ctx, label);
   if (!in_f32 && !out_f32)
-    hipLaunchKernelGGL((relpos_attn_kernel<_Float16, _Float16>), grid, dim3(256), 0, ctx->stream, a);
+    FA_LAUNCH(ps, (relpos_attn_kernel<_Float16, _Float16>), grid, dim3(256), 0, ctx->stream, a);
   else if (in_f32 && out_f32)
-    hipLaunchKernelGGL((relpos_attn_kernel<float, float>), grid, dim3(256), 0, ctx->stream, a);
+    FA_LAUNCH(ps, (relpos_attn_kernel<float, float>), grid, dim3(256), 0, ctx->stream, a);
   else
     return set_err(ctx, FA_E_UNSUPPORTED, "%s: mixed attention I/O types", label);
   return check_launch(ctx, label);

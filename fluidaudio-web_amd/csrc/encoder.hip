@@ -688,13 +688,13 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
   // ── subsampling ──
   {
     ProfScope ps(ctx, "sub_c0");
-    hipLaunchKernelGGL(sub_c0_kernel, dim3(cdiv((long)mx[1] * F1, ppb), n), dim3(256), 0, ctx->stream, (const float *)rm->ptr, MB, s0, s1, F1,
+    FA_LAUNCH(ps, sub_c0_kernel, dim3(cdiv((long)mx[1] * F1, ppb), n), dim3(256), 0, ctx->stream, (const float *)rm->ptr, MB, s0, s1, F1,
                        e->c0w, e->c0b, (_Float16 *)e->s1, C);
     FA_TRY(check_launch(ctx, "sub_c0"));
   }
   {
     ProfScope ps(ctx, "sub_dw1");
-    hipLaunchKernelGGL(sub_dw_kernel, dim3(cdiv((long)mx[2] * F2, ppb), n), dim3(256), 0, ctx->stream, (const _Float16 *)e->s1, s1, F1, s2, F2,
+    FA_LAUNCH(ps, sub_dw_kernel, dim3(cdiv((long)mx[2] * F2, ppb), n), dim3(256), 0, ctx->stream, (const _Float16 *)e->s1, s1, F1, s2, F2,
                        e->c1w, e->c1b, (_Float16 *)e->s2, C);
     FA_TRY(check_launch(ctx, "sub_dw1"));
   }
@@ -708,7 +708,7 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
   }
   {
     ProfScope ps(ctx, "sub_dw3");
-    hipLaunchKernelGGL(sub_dw_kernel, dim3(cdiv((long)mx[3] * F3, ppb), n), dim3(256), 0, ctx->stream, (const _Float16 *)e->s2p, s2, F2, s3, F3,
+    FA_LAUNCH(ps, sub_dw_kernel, dim3(cdiv((long)mx[3] * F3, ppb), n), dim3(256), 0, ctx->stream, (const _Float16 *)e->s2p, s2, F2, s3, F3,
                        e->c3w, e->c3b, (_Float16 *)e->s3, C);
     FA_TRY(check_launch(ctx, "sub_dw3"));
   }
@@ -770,7 +770,7 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
     {
       ProfScope ps(ctx, "dwconv");
       const int thr = std::min(128, D / 8);
-      hipLaunchKernelGGL((dwconv_silu_kernel<9, 16>), dim3(cdiv(mx[3], 16), n, cdiv(D / 8, thr)), dim3(thr), 0, ctx->stream, gg, a, Ly.dww, Ly.dwb, D, s3);
+      FA_LAUNCH(ps, (dwconv_silu_kernel<9, 16>), dim3(cdiv(mx[3], 16), n, cdiv(D / 8, thr)), dim3(thr), 0, ctx->stream, gg, a, Ly.dww, Ly.dwb, D, s3);
       FA_TRY(check_launch(ctx, "dwconv"));
     }
     FA_TRY(gemm(a, D, Ly.pw2, x, D, 0, FA_ACT_NONE, x, 0, "pw2"));
@@ -782,7 +782,7 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
   }
   if (layout == 1) {
     ProfScope ps(ctx, "zero_pad");
-    hipLaunchKernelGGL(zero_pad_rows_kernel, dim3(mx[3], n), dim3(256), 0, ctx->stream, x, D, s3, mx[3]);
+    FA_LAUNCH(ps, zero_pad_rows_kernel, dim3(mx[3], n), dim3(256), 0, ctx->stream, x, D, s3, mx[3]);
     FA_TRY(check_launch(ctx, "zero_pad"));
   }
   *out = ox;

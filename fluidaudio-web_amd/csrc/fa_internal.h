@@ -2,6 +2,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
+#include <hip/hip_ext.h>
 
 #include <cstdint>
 #include <cstdio>
@@ -72,6 +73,7 @@ struct fa_ctx {
   int prof_max = 0;
   std::vector<fa::ProfRec> prof;
   std::vector<hipEvent_t> prof_free_events;
+  std::string prof_filter;  // label prefix; empty = all launches
   // staged reads
   std::vector<fa::Staged> staged;
   std::vector<uint32_t> staged_gen;
@@ -102,12 +104,26 @@ int new_persistent(fa_ctx *ctx, int rows, int cols, int kind, size_t bytes, fa_t
 void *dev_alloc(fa_ctx *ctx, size_t bytes);  // raw hipMalloc, nullptr on failure (error set)
 
 // ── launch bracketing for the profiler ────────────────────────────────────
+// A ProfScope opened around a launch claims a (start, stop) event pair when a
+// profile is open for its label.  FA_LAUNCH hands the pair to
+// hipExtLaunchKernelGGL, which stamps them at the kernel's own start and end
+// (no marker packets between dispatches); a scope that covers several
+// launches or copies (ext = false) records the events on the stream instead.
 struct ProfScope {
   fa_ctx *ctx;
   int idx;
-  ProfScope(fa_ctx *c, const char *label);
+  bool ext;
+  hipEvent_t a = nullptr, b = nullptr;
+  ProfScope(fa_ctx *c, const char *label, bool ext_launch = true);
   ~ProfScope();
 };
+#define FA_LAUNCH(ps, kernel, grid, block, shm, stream, ...)                                           \
+  do {                                                                                                 \
+    if ((ps).a)                                                                                        \
+      hipExtLaunchKernelGGL(kernel, grid, block, shm, stream, (ps).a, (ps).b, 0, __VA_ARGS__);         \
+    else                                                                                               \
+      hipLaunchKernelGGL(kernel, grid, block, shm, stream, __VA_ARGS__);                               \
+  } while (0)
 int check_launch(fa_ctx *ctx, const char *what);
 
 inline unsigned cdiv(long a, long b) { return (unsigned)((a + b - 1) / b); }

@@ -18,6 +18,9 @@
 #include "fa_device.h"
 #include "gemm.h"
 
+#include <cstdio>
+#include <cstdlib>
+
 namespace fa {
 
 // ── MFMA f16 GEMM ───────────────────────────────────────────────────────────
@@ -69,7 +72,14 @@ __device__ __forceinline__ h8 load_b8(const GemmArgs &p, int n, int k) {
   }
 }
 
-template <int BM, int BN, int WM, int WN, int AK, int BKND>
+// Epilogue variants, fixed at compile time so the per-element code is short and
+// the accumulators stay in registers (a runtime activation switch per element
+// pushed large tiles' accumulators to scratch).
+enum Epi : int { EPI_F32 = 0, EPI_F16 = 1, EPI_F16_SILU = 2, EPI_F16_RELU = 3, EPI_GLU = 4, EPI_GENERIC = 5 };
+
+__device__ __forceinline__ float sigmoid_mul(float v, float g) { return __fdividef(v, 1.f + __expf(-fminf(fmaxf(g, -30.f), 30.f))); }
+
+template <int BM, int BN, int WM, int WN, int AK, int BKND, int EPI>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_kernel(GemmArgs p) {
   constexpr int NT = 64 * WM * WN;
   constexpr int BK = 64, LS = BK + 8;  // LDS row stride in halfs (+8 breaks bank conflicts)
@@ -128,57 +138,138 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_kernel(GemmArgs p) {
   for (int kt = 0; kt < nk; kt++) {
     const int buf = kt & 1;
     if (kt + 1 < nk) gload((kt + 1) * BK);
+    h8 af[2][TI], bf[2][TJ];
 #pragma unroll
-    for (int s = 0; s < 2; s++) {
-      h8 af[TI], bf[TJ];
+    for (int i = 0; i < TI; i++) af[0][i] = *reinterpret_cast<const h8 *>(&sA[buf][(arow + i * 16) * LS + kq]);
 #pragma unroll
-      for (int i = 0; i < TI; i++) af[i] = *reinterpret_cast<const h8 *>(&sA[buf][(arow + i * 16) * LS + s * 32 + kq]);
+    for (int j = 0; j < TJ; j++) bf[0][j] = *reinterpret_cast<const h8 *>(&sB[buf][(brow + j * 16) * LS + kq]);
 #pragma unroll
-      for (int j = 0; j < TJ; j++) bf[j] = *reinterpret_cast<const h8 *>(&sB[buf][(brow + j * 16) * LS + s * 32 + kq]);
+    for (int i = 0; i < TI; i++) af[1][i] = *reinterpret_cast<const h8 *>(&sA[buf][(arow + i * 16) * LS + 32 + kq]);
+#pragma unroll
+    for (int j = 0; j < TJ; j++) bf[1][j] = *reinterpret_cast<const h8 *>(&sB[buf][(brow + j * 16) * LS + 32 + kq]);
+#pragma unroll
+    for (int s = 0; s < 2; s++)
 #pragma unroll
       for (int i = 0; i < TI; i++)
 #pragma unroll
-        for (int j = 0; j < TJ; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
+        for (int j = 0; j < TJ; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s][i], bf[s][j], acc[i][j], 0, 0, 0);
     if (kt + 1 < nk) lstore(buf ^ 1);
     __syncthreads();
   }
 
-  // epilogue
-  const int rbase = m0 + wm * WTM + (lane >> 4) * 4;
-  const int cbase = n0 + wn * WTN;
+  // Epilogue, staged through LDS (free after the main loop): each wave writes
+  // 16-row strips of its accumulators, then reads them back row-contiguous so
+  // every global access is a 16-byte vector and each row segment is written
+  // by consecutive lanes (the MFMA layout itself gives 2-4 byte scattered stores).
+  constexpr int SS = WTN + 4;  // strip row stride (floats)
+  static_assert(4 * 16 * SS * 4 <= 2 * (BM + BN) * LS * 2, "epilogue strip does not fit in LDS");
+  float *strip = reinterpret_cast<float *>(&sA[0][0]) + wave * 16 * SS;
+  const int r0 = m0 + wm * WTM, c0 = n0 + wn * WTN;
+  constexpr int OCOLS = EPI == EPI_GLU ? WTN / 2 : WTN;  // output columns of this wave's strip
+  constexpr int LPR = OCOLS / 4;                         // lanes per output row (4 values each)
+  constexpr int RPP = 64 / LPR;                          // rows per pass
+  static_assert(LPR >= 1 && LPR <= 64, "epilogue lane mapping");
+  const int lc = (lane % LPR) * 4, lr = lane / LPR;
+  // per-lane column constants (fixed across strips)
+  float cs[4] = {1.f, 1.f, 1.f, 1.f}, bv[4] = {0.f, 0.f, 0.f, 0.f}, gcs[4] = {1.f, 1.f, 1.f, 1.f}, gbv[4] = {0.f, 0.f, 0.f, 0.f};
+  int vcol[4], gcol[4];
 #pragma unroll
-  for (int j = 0; j < TJ; j++) {
-    const int col = cbase + j * 16 + (lane & 15);
-    const bool cok = col < p.N;
-    const float cs = (p.colscale && cok) ? p.colscale[col] : 1.f;
-    const float bv = (p.bias && cok) ? p.bias[col] : 0.f;
+  for (int e = 0; e < 4; e++) {
+    if constexpr (EPI == EPI_GLU) {
+      const int ch = lc + e;  // output channel within the strip
+      vcol[e] = (ch >> 3) * 16 + (ch & 7);
+      gcol[e] = vcol[e] + 8;
+    } else {
+      vcol[e] = lc + e;
+      gcol[e] = vcol[e];
+    }
+    const int gv = c0 + vcol[e], gg = c0 + gcol[e];
+    if (p.colscale) {
+      cs[e] = gv < p.N ? p.colscale[gv] : 1.f;
+      gcs[e] = gg < p.N ? p.colscale[gg] : 1.f;
+    }
+    if (p.bias) {
+      bv[e] = gv < p.N ? p.bias[gv] : 0.f;
+      gbv[e] = gg < p.N ? p.bias[gg] : 0.f;
+    }
+  }
 #pragma unroll
-    for (int i = 0; i < TI; i++) {
+  for (int i = 0; i < TI; i++) {
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int row = rbase + i * 16 + r;
-        float v = acc[i][j][r];
-        if (p.colscale) v *= cs;
-        v += bv;
-        if (p.glu) {
-          const float g = __shfl_xor(v, 8, 64);
-          if ((lane & 8) == 0 && row < p.M && cok) {
-            const int ch = ((cbase + j * 16) >> 1) + (lane & 7);
-            const float o = v / (1.f + __expf(-fminf(fmaxf(g, -30.f), 30.f)));
-            reinterpret_cast<_Float16 *>(p.C)[(size_t)row * p.ldc + ch] = (_Float16)o;
+    for (int j = 0; j < TJ; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) strip[((lane >> 4) * 4 + r) * SS + j * 16 + (lane & 15)] = acc[i][j][r];
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int pr = 0; pr < 16; pr += RPP) {
+      const int rr = pr + lr;
+      const int row = r0 + i * 16 + rr;
+      if (lr < RPP && rr < 16 && row < p.M) {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] = strip[rr * SS + vcol[e]] * cs[e] + bv[e];
+        if constexpr (EPI == EPI_GLU) {
+          const int ocol = (c0 >> 1) + lc;
+          if (ocol + 3 < (p.N >> 1)) {
+            h4 o;
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = (_Float16)sigmoid_mul(v[e], strip[rr * SS + gcol[e]] * gcs[e] + gbv[e]);
+            *reinterpret_cast<h4 *>(reinterpret_cast<_Float16 *>(p.C) + (size_t)row * p.ldc + ocol) = o;
           }
-          continue;
+        } else {
+          const int col = c0 + lc;
+          if (col + 3 < p.N) {
+            if constexpr (EPI == EPI_F32) {
+              float4 o = make_float4(v[0], v[1], v[2], v[3]);
+              if (p.add) {
+                const float4 ad = *reinterpret_cast<const float4 *>(p.add + (size_t)row * p.ldadd + col);
+                o.x += ad.x; o.y += ad.y; o.z += ad.z; o.w += ad.w;
+              }
+              *reinterpret_cast<float4 *>(reinterpret_cast<float *>(p.C) + (size_t)row * p.ldc + col) = o;
+            } else if constexpr (EPI == EPI_GENERIC) {
+#pragma unroll
+              for (int e = 0; e < 4; e++) {
+                float o = act_apply(v[e], p.act);
+                if (p.add) o += p.add[(size_t)row * p.ldadd + col + e];
+                if (p.out_f16)
+                  reinterpret_cast<_Float16 *>(p.C)[(size_t)row * p.ldc + col + e] = (_Float16)o;
+                else
+                  reinterpret_cast<float *>(p.C)[(size_t)row * p.ldc + col + e] = o;
+              }
+            } else {
+              h4 o;
+#pragma unroll
+              for (int e = 0; e < 4; e++) {
+                float t = v[e];
+                if constexpr (EPI == EPI_F16_SILU) t = sigmoid_mul(t, t);
+                if constexpr (EPI == EPI_F16_RELU) t = fmaxf(t, 0.f);
+                o[e] = (_Float16)t;
+              }
+              *reinterpret_cast<h4 *>(reinterpret_cast<_Float16 *>(p.C) + (size_t)row * p.ldc + col) = o;
+            }
+          } else {
+            // ragged right edge (N not a multiple of 4 within this tile)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+              if (col + e >= p.N) break;
+              float o = v[e];
+              if constexpr (EPI == EPI_GENERIC) o = act_apply(o, p.act);
+              if constexpr (EPI == EPI_F16_SILU) o = sigmoid_mul(o, o);
+              if constexpr (EPI == EPI_F16_RELU) o = fmaxf(o, 0.f);
+              if constexpr (EPI == EPI_F32 || EPI == EPI_GENERIC)
+                if (p.add) o += p.add[(size_t)row * p.ldadd + col + e];
+              if (EPI == EPI_F32 || (EPI == EPI_GENERIC && !p.out_f16))
+                reinterpret_cast<float *>(p.C)[(size_t)row * p.ldc + col + e] = o;
+              else
+                reinterpret_cast<_Float16 *>(p.C)[(size_t)row * p.ldc + col + e] = (_Float16)o;
+            }
+          }
         }
-        if (row >= p.M || !cok) continue;
-        v = act_apply(v, p.act);
-        if (p.add) v += p.add[(size_t)row * p.ldadd + col];
-        if (p.out_f16)
-          reinterpret_cast<_Float16 *>(p.C)[(size_t)row * p.ldc + col] = (_Float16)v;
-        else
-          reinterpret_cast<float *>(p.C)[(size_t)row * p.ldc + col] = v;
       }
     }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
@@ -260,20 +351,99 @@ __global__ void gemm_naive_kernel(const float *A, const void *B, int b_kind, flo
 }
 
 // ── host dispatch ───────────────────────────────────────────────────────────
-template <int BM, int BN, int WM, int WN, int AK, int BKND>
+template <int BM, int BN, int WM, int WN, int AK, int BKND, int EPI>
 static int launch_cfg(fa_ctx *ctx, const GemmArgs &p, const char *label) {
   const unsigned tiles = cdiv(p.M, BM) * cdiv(p.N, BN);
   ProfScope ps(ctx, label);
-  hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, WM, WN, AK, BKND>), dim3(tiles), dim3(64 * WM * WN), 0, ctx->stream, p);
+  FA_LAUNCH(ps, (gemm_mfma_kernel<BM, BN, WM, WN, AK, BKND, EPI>), dim3(tiles), dim3(64 * WM * WN), 0, ctx->stream, p);
   return check_launch(ctx, label);
+}
+
+static int epi_of(const GemmArgs &p) {
+  if (p.glu) return EPI_GLU;
+  if (!p.out_f16) return (p.act == 0) ? EPI_F32 : EPI_GENERIC;
+  if (p.add) return EPI_GENERIC;
+  if (p.act == 0) return EPI_F16;
+  if (p.act == 4) return EPI_F16_SILU;
+  if (p.act == 3) return EPI_F16_RELU;
+  return EPI_GENERIC;
+}
+
+// Tile configurations (BM x BN, 2x2 waves of (BM/2)x(BN/2)).  `slots` is how
+// many workgroups fit on a CU (LDS-limited); rate1/rate2 are measured
+// per-CU throughputs on MI355X (tile-area·K per µs, K=1024, f16) with one
+// workgroup per CU and with every slot busy.  Bigger wave tiles read less
+// LDS per MFMA; smaller tiles quantise better over 256 CUs.
+struct TileCfg {
+  int bm, bn, slots;
+  float rate1, rate2;
+};
+static const TileCfg kTiles[] = {
+    {256, 256, 1, 1285.f, 1285.f}, {192, 256, 1, 1199.f, 1199.f}, {256, 192, 1, 1228.f, 1228.f}, {192, 192, 1, 1072.f, 1072.f},
+    {256, 128, 1, 1062.f, 1062.f}, {128, 256, 1, 1137.f, 1137.f}, {192, 128, 1, 1007.f, 1007.f}, {128, 128, 2, 1170.f, 1638.f},
+    {192, 64, 2, 962.f, 1117.f},   {64, 128, 2, 700.f, 1024.f}};
+
+static int pick_tile(fa_ctx *ctx, int M, int N) {
+  // FA_GEMM_TILE=BMxBN pins one configuration (tuning sweeps).
+  if (const char *e = getenv("FA_GEMM_TILE")) {
+    int bm = 0, bn = 0;
+    if (sscanf(e, "%dx%d", &bm, &bn) == 2)
+      for (int i = 0; i < (int)(sizeof kTiles / sizeof kTiles[0]); i++)
+        if (kTiles[i].bm == bm && kTiles[i].bn == bn) return i;
+  }
+  int best = 0;
+  double bestc = 1e300;
+  for (int i = 0; i < (int)(sizeof kTiles / sizeof kTiles[0]); i++) {
+    const TileCfg &t = kTiles[i];
+    const long tiles = (long)cdiv(M, t.bm) * cdiv(N, t.bn);
+    const double area = (double)t.bm * t.bn;
+    double c;
+    if (tiles <= ctx->num_cu) {
+      c = area / t.rate1;
+    } else {
+      const long rounds = (tiles + (long)t.slots * ctx->num_cu - 1) / ((long)t.slots * ctx->num_cu);
+      c = rounds * area * t.slots / t.rate2;
+    }
+    if (c < bestc * 0.999) {
+      bestc = c;
+      best = i;
+    }
+  }
+  return best;
+}
+
+template <int AK, int BKND, int EPI>
+static int launch_tile(fa_ctx *ctx, const GemmArgs &p, const char *label) {
+  if constexpr (AK == A_F32 || EPI == EPI_GENERIC) {  // ComputeContext path: mid-size tiles
+    const long t128 = (long)cdiv(p.M, 128) * cdiv(p.N, 128);
+    if (t128 >= ctx->num_cu) return launch_cfg<128, 128, 2, 2, AK, BKND, EPI>(ctx, p, label);
+    return launch_cfg<64, 128, 2, 2, AK, BKND, EPI>(ctx, p, label);
+  } else {
+    switch (pick_tile(ctx, p.M, p.N)) {
+      case 0: return launch_cfg<256, 256, 2, 2, AK, BKND, EPI>(ctx, p, label);
+      case 1: return launch_cfg<192, 256, 2, 2, AK, BKND, EPI>(ctx, p, label);
+      case 2: return launch_cfg<256, 192, 2, 2, AK, BKND, EPI>(ctx, p, label);
+      case 3: return launch_cfg<192, 192, 2, 2, AK, BKND, EPI>(ctx, p, label);
+      case 4: return launch_cfg<256, 128, 2, 2, AK, BKND, EPI>(ctx, p, label);
+      case 5: return launch_cfg<128, 256, 2, 2, AK, BKND, EPI>(ctx, p, label);
+      case 6: return launch_cfg<192, 128, 2, 2, AK, BKND, EPI>(ctx, p, label);
+      case 7: return launch_cfg<128, 128, 2, 2, AK, BKND, EPI>(ctx, p, label);
+      case 8: return launch_cfg<192, 64, 2, 2, AK, BKND, EPI>(ctx, p, label);
+      default: return launch_cfg<64, 128, 2, 2, AK, BKND, EPI>(ctx, p, label);
+    }
+  }
 }
 
 template <int AK, int BKND>
 static int launch_kind(fa_ctx *ctx, const GemmArgs &p, const char *label) {
-  // Tile choice: keep >= ~1 tile per CU; wide tiles for big N.
-  const long t128 = (long)cdiv(p.M, 128) * cdiv(p.N, 128);
-  if (t128 >= ctx->num_cu) return launch_cfg<128, 128, 2, 2, AK, BKND>(ctx, p, label);
-  return launch_cfg<64, 128, 2, 2, AK, BKND>(ctx, p, label);
+  switch (epi_of(p)) {
+    case EPI_F32: return launch_tile<AK, BKND, EPI_F32>(ctx, p, label);
+    case EPI_F16: return launch_tile<AK, BKND, EPI_F16>(ctx, p, label);
+    case EPI_F16_SILU: return launch_tile<AK, BKND, EPI_F16_SILU>(ctx, p, label);
+    case EPI_F16_RELU: return launch_tile<AK, BKND, EPI_F16_RELU>(ctx, p, label);
+    case EPI_GLU: return launch_tile<AK, BKND, EPI_GLU>(ctx, p, label);
+    default: return launch_tile<AK, BKND, EPI_GENERIC>(ctx, p, label);
+  }
 }
 
 int gemm_mfma(fa_ctx *ctx, const GemmArgs &p, const char *label) {
@@ -295,9 +465,9 @@ int gemm_f32(fa_ctx *ctx, const float *A, const float *B, float *C, const float 
   if (M <= 0 || N <= 0) return FA_OK;
   ProfScope ps(ctx, label);
   if (K % 16 == 0 && N % 4 == 0) {
-    hipLaunchKernelGGL(gemm_f32_kernel, dim3(cdiv(M, 64) * cdiv(N, 64)), dim3(256), 0, ctx->stream, A, B, C, bias, add, M, N, K, act);
+    FA_LAUNCH(ps, gemm_f32_kernel, dim3(cdiv(M, 64) * cdiv(N, 64)), dim3(256), 0, ctx->stream, A, B, C, bias, add, M, N, K, act);
   } else {
-    hipLaunchKernelGGL(gemm_naive_kernel, dim3(cdiv((long)M * N, 256)), dim3(256), 0, ctx->stream, A, (const void *)B, 0, C, bias, add, M, N,
+    FA_LAUNCH(ps, gemm_naive_kernel, dim3(cdiv((long)M * N, 256)), dim3(256), 0, ctx->stream, A, (const void *)B, 0, C, bias, add, M, N,
                        K, act);
   }
   return check_launch(ctx, label);
@@ -307,7 +477,7 @@ int gemm_naive_f16(fa_ctx *ctx, const float *A, const void *Bkm, float *C, const
                    const char *label) {
   if (M <= 0 || N <= 0) return FA_OK;
   ProfScope ps(ctx, label);
-  hipLaunchKernelGGL(gemm_naive_kernel, dim3(cdiv((long)M * N, 256)), dim3(256), 0, ctx->stream, A, Bkm, 1, C, bias, add, M, N, K, act);
+  FA_LAUNCH(ps, gemm_naive_kernel, dim3(cdiv((long)M * N, 256)), dim3(256), 0, ctx->stream, A, Bkm, 1, C, bias, add, M, N, K, act);
   return check_launch(ctx, label);
 }
 

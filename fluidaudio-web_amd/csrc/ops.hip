@@ -68,9 +68,9 @@ int layernorm_launch(fa_ctx *ctx, const float *x, const float *g, const float *b
   if (rows <= 0) return FA_OK;
   ProfScope ps(ctx, label);
   if (out_f16)
-    hipLaunchKernelGGL(layernorm_kernel<_Float16>, dim3(cdiv(rows, 4)), dim3(256), 0, ctx->stream, x, g, b, (_Float16 *)y, rows, cols, ldx, ldy, eps);
+    FA_LAUNCH(ps, layernorm_kernel<_Float16>, dim3(cdiv(rows, 4)), dim3(256), 0, ctx->stream, x, g, b, (_Float16 *)y, rows, cols, ldx, ldy, eps);
   else
-    hipLaunchKernelGGL(layernorm_kernel<float>, dim3(cdiv(rows, 4)), dim3(256), 0, ctx->stream, x, g, b, (float *)y, rows, cols, ldx, ldy, eps);
+    FA_LAUNCH(ps, layernorm_kernel<float>, dim3(cdiv(rows, 4)), dim3(256), 0, ctx->stream, x, g, b, (float *)y, rows, cols, ldx, ldy, eps);
   return check_launch(ctx, label);
 }
 
@@ -291,7 +291,7 @@ int fa_matmul(fa_ctx *ctx, fa_tensor a, fa_tensor b, fa_tensor bias, int act, fa
   FA_TRY(need(ctx, b, &rb, "matmul"));
   FA_TRY(opt(ctx, bias, &rbias, "matmul bias"));
   FA_TRY(opt(ctx, add, &radd, "matmul add"));
-  FA_TRY(need_f32(ctx, ra, "matmul A"));
+  if (ra->kind != S_F32 && ra->kind != S_F16RM) return set_err(ctx, FA_E_INVALID, "matmul: A must be an f32 or row-major f16 tensor");
   const int M = ra->rows, K = ra->cols, N = rb->cols;
   if (rb->rows != K) return set_err(ctx, FA_E_INVALID, "matmul: A [%d,%d] @ B [%d,%d]", M, K, rb->rows, rb->cols);
   if (rbias && rbias->rows * rbias->cols != N) return set_err(ctx, FA_E_INVALID, "matmul: bias has %d elements, N=%d", rbias->rows * rbias->cols, N);
@@ -301,10 +301,11 @@ int fa_matmul(fa_ctx *ctx, fa_tensor a, fa_tensor b, fa_tensor bias, int act, fa
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, M, N, S_F32, (size_t)M * N * 4, &o, &ro));
   ra = get(ctx, a); rb = get(ctx, b); rbias = bias ? get(ctx, bias) : nullptr; radd = add ? get(ctx, add) : nullptr;  // recs may move
+  if (ra->kind == S_F16RM && (rb->kind != S_F16KM || K % 64)) return set_err(ctx, FA_E_UNSUPPORTED, "matmul: f16 A needs an f16 B and K %% 64 == 0");
   if (rb->kind == S_F16KM) {
     if (K % 64 == 0) {
       GemmArgs p;
-      p.A = ra->ptr; p.lda = K; p.akind = A_F32;
+      p.A = ra->ptr; p.lda = K; p.akind = ra->kind == S_F16RM ? A_F16 : A_F32;
       p.B = rb->ptr; p.bkind = B_F16;
       p.C = ro->ptr; p.ldc = N;
       p.bias = CF32(rbias); p.add = CF32(radd); p.ldadd = N; p.act = act;
@@ -340,7 +341,7 @@ int fa_matmul_int8(fa_ctx *ctx, fa_tensor a, fa_tensor wq, fa_tensor scale, int 
     rw->aux = p;
     rw->aux_bytes = (size_t)K * N;
     ProfScope ps(ctx, "repack_i8");
-    hipLaunchKernelGGL(repack_i8_kernel, dim3(cdiv(N, 64), cdiv(K, 64)), dim3(256), 0, ctx->stream, (const int8_t *)rw->ptr, (int8_t *)p, K, N);
+    FA_LAUNCH(ps, repack_i8_kernel, dim3(cdiv(N, 64), cdiv(K, 64)), dim3(256), 0, ctx->stream, (const int8_t *)rw->ptr, (int8_t *)p, K, N);
     FA_TRY(check_launch(ctx, "repack_i8"));
   }
   fa_tensor o;
@@ -421,7 +422,7 @@ int fa_softmax(fa_ctx *ctx, fa_tensor x, fa_tensor *out) {
   FA_TRY(new_tensor(ctx, R, Cc, S_F32, (size_t)R * Cc * 4, &o, &ro));
   rx = get(ctx, x);
   ProfScope ps(ctx, "softmax");
-  if (R) hipLaunchKernelGGL(softmax_kernel, dim3(cdiv(R, 4)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), R, Cc);
+  if (R) FA_LAUNCH(ps, softmax_kernel, dim3(cdiv(R, 4)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), R, Cc);
   FA_TRY(check_launch(ctx, "softmax"));
   *out = o;
   return FA_OK;
@@ -437,7 +438,7 @@ static int unary(fa_ctx *ctx, fa_tensor x, int kind, float s, fa_tensor *out, co
   FA_TRY(new_tensor(ctx, rx->rows, rx->cols, S_F32, (size_t)n * 4, &o, &ro));
   rx = get(ctx, x);
   ProfScope ps(ctx, name);
-  if (n) hipLaunchKernelGGL(unary_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), n, kind, s);
+  if (n) FA_LAUNCH(ps, unary_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), n, kind, s);
   FA_TRY(check_launch(ctx, name));
   *out = o;
   return FA_OK;
@@ -461,7 +462,7 @@ int fa_ewise(fa_ctx *ctx, fa_tensor a, fa_tensor b, int op, fa_tensor *out) {
   FA_TRY(new_tensor(ctx, ra->rows, ra->cols, S_F32, (size_t)n * 4, &o, &ro));
   ra = get(ctx, a); rb = get(ctx, b);
   ProfScope ps(ctx, "ewise");
-  if (n) hipLaunchKernelGGL(ewise_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, F32(ra), F32(rb), F32(ro), n, ra->cols, bcast, op ? 1 : 0);
+  if (n) FA_LAUNCH(ps, ewise_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, F32(ra), F32(rb), F32(ro), n, ra->cols, bcast, op ? 1 : 0);
   FA_TRY(check_launch(ctx, "ewise"));
   *out = o;
   return FA_OK;
@@ -478,7 +479,7 @@ int fa_glu(fa_ctx *ctx, fa_tensor x, fa_tensor *out) {
   FA_TRY(new_tensor(ctx, C, T, S_F32, (size_t)C * T * 4, &o, &ro));
   rx = get(ctx, x);
   ProfScope ps(ctx, "glu");
-  if ((long)C * T) hipLaunchKernelGGL(glu_kernel, dim3(gs((long)C * T)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), C, T);
+  if ((long)C * T) FA_LAUNCH(ps, glu_kernel, dim3(gs((long)C * T)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), C, T);
   FA_TRY(check_launch(ctx, "glu"));
   *out = o;
   return FA_OK;
@@ -494,7 +495,7 @@ int fa_transpose(fa_ctx *ctx, fa_tensor x, fa_tensor *out) {
   FA_TRY(new_tensor(ctx, Cc, R, S_F32, (size_t)R * Cc * 4, &o, &ro));
   rx = get(ctx, x);
   ProfScope ps(ctx, "transpose");
-  if ((long)R * Cc) hipLaunchKernelGGL(transpose_kernel, dim3(cdiv(Cc, 32), cdiv(R, 32)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), R, Cc);
+  if ((long)R * Cc) FA_LAUNCH(ps, transpose_kernel, dim3(cdiv(Cc, 32), cdiv(R, 32)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), R, Cc);
   FA_TRY(check_launch(ctx, "transpose"));
   *out = o;
   return FA_OK;
@@ -511,7 +512,7 @@ int fa_slice_cols(fa_ctx *ctx, fa_tensor x, int col0, int width, fa_tensor *out)
   rx = get(ctx, x);
   const long n = (long)rx->rows * width;
   ProfScope ps(ctx, "sliceCols");
-  if (n) hipLaunchKernelGGL(slice_cols_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), rx->rows, rx->cols, col0, width);
+  if (n) FA_LAUNCH(ps, slice_cols_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), rx->rows, rx->cols, col0, width);
   FA_TRY(check_launch(ctx, "sliceCols"));
   *out = o;
   return FA_OK;
@@ -526,7 +527,7 @@ int fa_set_cols(fa_ctx *ctx, fa_tensor dst, fa_tensor src, int col0) {
   if (rs->rows != rd->rows || col0 < 0 || col0 + rs->cols > rd->cols) return set_err(ctx, FA_E_INVALID, "setCols: src [%d,%d] at col %d of [%d,%d]", rs->rows, rs->cols, col0, rd->rows, rd->cols);
   const long n = (long)rs->rows * rs->cols;
   ProfScope ps(ctx, "setCols");
-  if (n) hipLaunchKernelGGL(set_cols_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, F32(rs), F32(rd), rs->rows, rd->cols, col0, rs->cols);
+  if (n) FA_LAUNCH(ps, set_cols_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, F32(rs), F32(rd), rs->rows, rd->cols, col0, rs->cols);
   return check_launch(ctx, "setCols");
 }
 
@@ -591,7 +592,7 @@ int fa_sub_reshape(fa_ctx *ctx, fa_tensor x, int C, int Tsub, int F, fa_tensor *
   rx = get(ctx, x);
   const long n = (long)Tsub * C * F;
   ProfScope ps(ctx, "subReshape");
-  if (n) hipLaunchKernelGGL(sub_reshape_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), C, Tsub, F);
+  if (n) FA_LAUNCH(ps, sub_reshape_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), C, Tsub, F);
   FA_TRY(check_launch(ctx, "subReshape"));
   *out = o;
   return FA_OK;
@@ -608,7 +609,7 @@ int fa_row_bias_act(fa_ctx *ctx, fa_tensor x, fa_tensor bias, int act, fa_tensor
   FA_TRY(new_tensor(ctx, rx->rows, rx->cols, S_F32, (size_t)n * 4, &o, &ro));
   rx = get(ctx, x); rb = get(ctx, bias);
   ProfScope ps(ctx, "rowBiasAct");
-  if (n) hipLaunchKernelGGL(row_bias_act_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, F32(rx), F32(rb), F32(ro), rx->rows, rx->cols, act);
+  if (n) FA_LAUNCH(ps, row_bias_act_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, F32(rx), F32(rb), F32(ro), rx->rows, rx->cols, act);
   FA_TRY(check_launch(ctx, "rowBiasAct"));
   *out = o;
   return FA_OK;
@@ -633,7 +634,7 @@ int fa_conv1d(fa_ctx *ctx, fa_tensor x, fa_tensor w, int cout, int k, fa_tensor 
   FA_TRY(new_tensor(ctx, cout, Lout, S_F32, (size_t)cout * Lout * 4, &o, &ro));
   rx = get(ctx, x); rw = get(ctx, w); rb = bias ? get(ctx, bias) : nullptr;
   ProfScope ps(ctx, "conv1d");
-  hipLaunchKernelGGL(conv1d_kernel, dim3(gs((long)cout * Lout)), dim3(256), 0, ctx->stream, F32(rx), F32(rw), CF32(rb), F32(ro), cout, Cin, L, Lout,
+  FA_LAUNCH(ps, conv1d_kernel, dim3(gs((long)cout * Lout)), dim3(256), 0, ctx->stream, F32(rx), F32(rw), CF32(rb), F32(ro), cout, Cin, L, Lout,
                      k, stride, pad_left, dilation, groups, act);
   FA_TRY(check_launch(ctx, "conv1d"));
   *out = o;
@@ -656,7 +657,7 @@ int fa_conv2d(fa_ctx *ctx, fa_tensor x, fa_tensor w, int cout, int cin, int h, i
   FA_TRY(new_tensor(ctx, cout, Ho * Wo, S_F32, (size_t)cout * Ho * Wo * 4, &o, &ro));
   rx = get(ctx, x); rw = get(ctx, w); rb = bias ? get(ctx, bias) : nullptr;
   ProfScope ps(ctx, "conv2d");
-  hipLaunchKernelGGL(conv2d_kernel, dim3(gs((long)cout * Ho * Wo)), dim3(256), 0, ctx->stream, F32(rx), F32(rw), CF32(rb), F32(ro), cout, cin, h, wd,
+  FA_LAUNCH(ps, conv2d_kernel, dim3(gs((long)cout * Ho * Wo)), dim3(256), 0, ctx->stream, F32(rx), F32(rw), CF32(rb), F32(ro), cout, cin, h, wd,
                      Ho, Wo, kh, kw, sh, sw, pt, pl, groups, act);
   FA_TRY(check_launch(ctx, "conv2d"));
   *out = o;
@@ -676,7 +677,7 @@ int fa_bmm_qk(fa_ctx *ctx, fa_tensor q, fa_tensor b, fa_tensor qb, int H, int HD
   FA_TRY(new_tensor(ctx, W * H * T, Tb, S_F32, (size_t)W * H * T * Tb * 4, &o, &ro));
   rq = get(ctx, q); rb = get(ctx, b); rqb = qb ? get(ctx, qb) : nullptr;
   ProfScope ps(ctx, "bmmQK");
-  hipLaunchKernelGGL(bmm_qk_kernel, dim3(gs((long)W * H * T * Tb)), dim3(256), 0, ctx->stream, F32(rq), F32(rb), CF32(rqb), F32(ro), T, Tb, H, HD, W,
+  FA_LAUNCH(ps, bmm_qk_kernel, dim3(gs((long)W * H * T * Tb)), dim3(256), 0, ctx->stream, F32(rq), F32(rb), CF32(rqb), F32(ro), T, Tb, H, HD, W,
                      b_shared);
   FA_TRY(check_launch(ctx, "bmmQK"));
   *out = o;
@@ -695,7 +696,7 @@ int fa_bmm_pv(fa_ctx *ctx, fa_tensor p, fa_tensor v, int H, int HD, int W, fa_te
   FA_TRY(new_tensor(ctx, W * Tq, H * HD, S_F32, (size_t)W * Tq * H * HD * 4, &o, &ro));
   rp = get(ctx, p); rv = get(ctx, v);
   ProfScope ps(ctx, "bmmPV");
-  hipLaunchKernelGGL(bmm_pv_kernel, dim3(gs((long)W * Tq * H * HD)), dim3(256), 0, ctx->stream, F32(rp), F32(rv), F32(ro), Tq, Tk, H, HD, W);
+  FA_LAUNCH(ps, bmm_pv_kernel, dim3(gs((long)W * Tq * H * HD)), dim3(256), 0, ctx->stream, F32(rp), F32(rv), F32(ro), Tq, Tk, H, HD, W);
   FA_TRY(check_launch(ctx, "bmmPV"));
   *out = o;
   return FA_OK;
@@ -712,7 +713,7 @@ int fa_rel_shift_b(fa_ctx *ctx, fa_tensor x, int H, fa_tensor *out) {
   FA_TRY(new_tensor(ctx, H * t, t, S_F32, (size_t)H * t * t * 4, &o, &ro));
   rx = get(ctx, x);
   ProfScope ps(ctx, "relShiftB");
-  if ((long)H * t * t) hipLaunchKernelGGL(relshift_kernel, dim3(gs((long)H * t * t)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), t, H);
+  if ((long)H * t * t) FA_LAUNCH(ps, relshift_kernel, dim3(gs((long)H * t * t)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), t, H);
   FA_TRY(check_launch(ctx, "relShiftB"));
   *out = o;
   return FA_OK;
@@ -766,7 +767,7 @@ int fa_dequant_int8(fa_ctx *ctx, fa_tensor wq, fa_tensor scale, int K, int N, fa
   FA_TRY(new_tensor(ctx, K, N, S_F32, (size_t)K * N * 4, &o, &ro));
   rw = get(ctx, wq); rs = get(ctx, scale);
   ProfScope ps(ctx, "dequantInt8");
-  hipLaunchKernelGGL(dequant_i8_kernel, dim3(gs((long)K * N)), dim3(256), 0, ctx->stream, (const int8_t *)rw->ptr, F32(rs), F32(ro), K, N);
+  FA_LAUNCH(ps, dequant_i8_kernel, dim3(gs((long)K * N)), dim3(256), 0, ctx->stream, (const int8_t *)rw->ptr, F32(rs), F32(ro), K, N);
   FA_TRY(check_launch(ctx, "dequantInt8"));
   *out = o;
   return FA_OK;
@@ -783,7 +784,7 @@ int fa_dequant_int4(fa_ctx *ctx, fa_tensor bq, fa_tensor scales_f16, int K, int 
   FA_TRY(new_tensor(ctx, K, N, S_F32, (size_t)K * N * 4, &o, &ro));
   rq = get(ctx, bq); rs = get(ctx, scales_f16);
   ProfScope ps(ctx, "dequantInt4");
-  hipLaunchKernelGGL(dequant_i4_kernel, dim3(gs((long)K * N)), dim3(256), 0, ctx->stream, (const uint8_t *)rq->ptr, (const _Float16 *)rs->ptr, F32(ro), K, N);
+  FA_LAUNCH(ps, dequant_i4_kernel, dim3(gs((long)K * N)), dim3(256), 0, ctx->stream, (const uint8_t *)rq->ptr, (const _Float16 *)rs->ptr, F32(ro), K, N);
   FA_TRY(check_launch(ctx, "dequantInt4"));
   *out = o;
   return FA_OK;

@@ -83,7 +83,7 @@ int fa_pack_windows(fa_ctx *ctx, fa_tensor feats, const int32_t *starts, const i
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, (int)rows, MB, S_F32, (size_t)rows * MB * 4, &o, &ro));
   rf = get(ctx, feats);
-  ProfScope ps(ctx, "pack_windows");
+  ProfScope ps(ctx, "pack_windows", n <= kMaxWin);
   for (int w0 = 0; w0 < n; w0 += kMaxWin) {
     WinTable dst{}, src{};
     dst.n = src.n = std::min(kMaxWin, n - w0);
@@ -97,7 +97,7 @@ int fa_pack_windows(fa_ctx *ctx, fa_tensor feats, const int32_t *starts, const i
       src.len[i] = lens[wi];
       acc += lens[wi];
     }
-    hipLaunchKernelGGL(pack_windows_kernel, dim3(cdiv(mx, 64), dst.n), dim3(256), 0, ctx->stream, (const float *)rf->ptr, Ttot, MB, dst, src,
+    FA_LAUNCH(ps, pack_windows_kernel, dim3(cdiv(mx, 64), dst.n), dim3(256), 0, ctx->stream, (const float *)rf->ptr, Ttot, MB, dst, src,
                        layout == 1 ? mx : 0, (float *)ro->ptr);
     FA_TRY(check_launch(ctx, "pack_windows"));
   }

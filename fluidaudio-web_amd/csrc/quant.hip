@@ -143,16 +143,17 @@ __global__ void gemv_naive_kernel(GemvArgs p, int fmt) {
 
 static int gemv_launch(fa_ctx *ctx, const GemvArgs &p, int fmt, const char *label) {
   if (p.M <= 0 || p.N <= 0) return FA_OK;
-  ProfScope ps(ctx, label);
+  const bool single = !(p.M > 16 && p.M <= 64 && p.K % 64 == 0 && (size_t)16 * (p.K + 8) * 2 <= 64 * 1024);
+  ProfScope ps(ctx, label, single);
   if (p.M <= 16 && p.K % 64 == 0 && (size_t)16 * (p.K + 8) * 2 <= 64 * 1024) {
     const size_t shm = (size_t)16 * (p.K + 8) * 2;
     const dim3 grid(cdiv(p.N, 16));
     if (fmt == 1)
-      hipLaunchKernelGGL(gemv_mfma_kernel<1>, grid, dim3(256), shm, ctx->stream, p);
+      FA_LAUNCH(ps, gemv_mfma_kernel<1>, grid, dim3(256), shm, ctx->stream, p);
     else if (fmt == 2)
-      hipLaunchKernelGGL(gemv_mfma_kernel<2>, grid, dim3(256), shm, ctx->stream, p);
+      FA_LAUNCH(ps, gemv_mfma_kernel<2>, grid, dim3(256), shm, ctx->stream, p);
     else
-      hipLaunchKernelGGL(gemv_mfma_kernel<3>, grid, dim3(256), shm, ctx->stream, p);
+      FA_LAUNCH(ps, gemv_mfma_kernel<3>, grid, dim3(256), shm, ctx->stream, p);
   } else if (p.M <= 64 && p.K % 64 == 0 && (size_t)16 * (p.K + 8) * 2 <= 64 * 1024) {
     // M in (16, 64]: run 16-row slabs
     for (int m0 = 0; m0 < p.M; m0 += 16) {
@@ -169,7 +170,7 @@ static int gemv_launch(fa_ctx *ctx, const GemvArgs &p, int fmt, const char *labe
         hipLaunchKernelGGL(gemv_mfma_kernel<3>, dim3(cdiv(p.N, 16)), dim3(256), shm, ctx->stream, q);
     }
   } else {
-    hipLaunchKernelGGL(gemv_naive_kernel, dim3(cdiv((long)p.M * p.N, 256)), dim3(256), 0, ctx->stream, p, fmt);
+    FA_LAUNCH(ps, gemv_naive_kernel, dim3(cdiv((long)p.M * p.N, 256)), dim3(256), 0, ctx->stream, p, fmt);
   }
   return check_launch(ctx, label);
 }

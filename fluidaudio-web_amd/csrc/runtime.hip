@@ -174,19 +174,24 @@ static hipEvent_t take_event(fa_ctx *ctx) {
   return e;
 }
 
-ProfScope::ProfScope(fa_ctx *c, const char *label) : ctx(c), idx(-1) {
+ProfScope::ProfScope(fa_ctx *c, const char *label, bool ext_launch) : ctx(c), idx(-1), ext(ext_launch) {
   if (!ctx->prof_on || (int)ctx->prof.size() >= ctx->prof_max) return;
+  if (!ctx->prof_filter.empty() && std::strncmp(label, ctx->prof_filter.c_str(), ctx->prof_filter.size()) != 0) return;
   ProfRec r;
   std::snprintf(r.label, sizeof r.label, "%s", label);
   r.a = take_event(ctx);
   r.b = take_event(ctx);
   if (!r.a || !r.b) return;
-  (void)hipEventRecord(r.a, ctx->stream);
+  if (!ext) (void)hipEventRecord(r.a, ctx->stream);
   ctx->prof.push_back(r);
   idx = (int)ctx->prof.size() - 1;
+  if (ext) {
+    a = r.a;
+    b = r.b;
+  }
 }
 ProfScope::~ProfScope() {
-  if (idx >= 0) (void)hipEventRecord(ctx->prof[idx].b, ctx->stream);
+  if (idx >= 0 && !ext) (void)hipEventRecord(ctx->prof[idx].b, ctx->stream);
 }
 
 int check_launch(fa_ctx *ctx, const char *what) {
@@ -533,6 +538,11 @@ int fa_profile_start(fa_ctx *ctx, int max_ops) {
   ctx->prof_max = max_ops > 0 ? max_ops : 4096;
   ctx->prof.reserve(ctx->prof_max);
   ctx->prof_on = true;
+  return FA_OK;
+}
+
+int fa_profile_only(fa_ctx *ctx, const char *prefix) {
+  ctx->prof_filter = prefix ? prefix : "";
   return FA_OK;
 }
 
