@@ -91,6 +91,7 @@ SIGNATURES = [
     ("fa_profile_only", I, [P, C.c_char_p]),
     ("fa_dequant_int8", I, [P, T, T, I, I, C.POINTER(T)]),
     ("fa_dequant_int4", I, [P, T, T, I, I, C.POINTER(T)]),
+    ("fa_quantize_weights", I, [I, F32P, I, I, C.c_void_p, C.c_void_p]),
     ("fa_gemv_quant", I, [P, T, T, T, I, I, I, C.POINTER(T)]),
     ("fa_pack_windows", I, [P, T, I32P, I32P, I, I, C.POINTER(T)]),
     ("fa_window_row_map", I, [P, I32P, I, I, I, I32P, C.POINTER(I)]),

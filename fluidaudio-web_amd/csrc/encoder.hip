@@ -216,6 +216,50 @@ static T *dupload(fa_encoder *e, const T *host, size_t n) {
   return d;
 }
 
+// Per-output-column symmetric int8 of Bt [N][K] (row n = output column n):
+// s = f32(max|w|)/127 (0 -> 1), q = clip(rint(w/s), -127, 127)
+// (quantize-parakeet-encoder.py:31-36, computed in f32 as numpy does).
+static void quantize_int8_km(const float *bt, int N, int K, int8_t *q, float *scale) {
+  for (int n = 0; n < N; n++) {
+    float mx = 0.f;
+    for (int k = 0; k < K; k++) mx = std::fmax(mx, std::fabs(bt[(size_t)n * K + k]));
+    float s = mx / 127.0f;
+    if (s == 0.f) s = 1.f;
+    for (int k = 0; k < K; k++) {
+      float r = std::rint(bt[(size_t)n * K + k] / s);
+      r = r < -127.f ? -127.f : (r > 127.f ? 127.f : r);
+      q[(size_t)n * K + k] = (int8_t)r;
+    }
+    scale[n] = s;
+  }
+}
+
+// Symmetric int4 group-32 of Bt [N][K] into [N][ceil(K/32)][16 B] (low nibble
+// = even k, nibble = q + 8) with f16 scales f16(max|w|/7) (0 -> 1.0).
+static void quantize_int4_km(const float *bt, int N, int K, uint8_t *q, uint16_t *sc) {
+  const int nblk = (K + 31) / 32;
+  for (int n = 0; n < N; n++)
+    for (int b = 0; b < nblk; b++) {
+      float mx = 0.f;
+      for (int t = 0; t < 32 && b * 32 + t < K; t++) mx = std::fmax(mx, std::fabs(bt[(size_t)n * K + b * 32 + t]));
+      uint16_t sh = h_f32_to_f16(mx / 7.0f);
+      float s = h_f16_to_f32(sh);
+      if (s == 0.f) {
+        sh = 0x3c00;
+        s = 1.f;
+      }
+      sc[(size_t)n * nblk + b] = sh;
+      uint8_t *blk = &q[((size_t)n * nblk + b) * 16];
+      std::memset(blk, 0x88, 16);
+      for (int t = 0; t < 32 && b * 32 + t < K; t++) {
+        float r = std::rint(bt[(size_t)n * K + b * 32 + t] / s);
+        r = r < -8.f ? -8.f : (r > 7.f ? 7.f : r);
+        const uint8_t nib = (uint8_t)((int)r + 8);
+        blk[t / 2] = (t & 1) ? (uint8_t)((blk[t / 2] & 0x0f) | (nib << 4)) : (uint8_t)((blk[t / 2] & 0xf0) | nib);
+      }
+    }
+}
+
 // Build a linear from Bt [N][K] raw f32 values (column n of the reference's
 // [K, N] matrix is row n here), a per-column fold factor, optional bias.
 static int build_lin(fa_encoder *e, Lin &L, const std::vector<float> &bt, int N, int K, const std::vector<float> &fold, const std::vector<float> *bias,
@@ -239,49 +283,19 @@ static int build_lin(fa_encoder *e, Lin &L, const std::vector<float> &bt, int N,
     return FA_OK;
   }
   if (e->format == FA_W_INT8) {
-    // per-output-column symmetric (quantize-parakeet-encoder.py:31-36)
     std::vector<int8_t> q((size_t)N * K);
     std::vector<float> cs(N);
-    for (int n = 0; n < N; n++) {
-      float mx = 0.f;
-      for (int k = 0; k < K; k++) mx = std::fmax(mx, std::fabs(bt[(size_t)n * K + k]));
-      float s = mx / 127.0f;
-      if (s == 0.f) s = 1.f;
-      for (int k = 0; k < K; k++) {
-        float r = std::rint(bt[(size_t)n * K + k] / s);
-        r = r < -127.f ? -127.f : (r > 127.f ? 127.f : r);
-        q[(size_t)n * K + k] = (int8_t)r;
-      }
-      cs[n] = (float)((double)s * fold[n]);
-    }
+    quantize_int8_km(bt.data(), N, K, q.data(), cs.data());
+    for (int n = 0; n < N; n++) cs[n] = (float)((double)cs[n] * fold[n]);
     if (!(L.w = dupload(e, q.data(), q.size())) || !(L.colscale = dupload(e, cs.data(), N))) return set_err(ctx, FA_E_OOM, "encoder load: %s", name);
     L.bkind = B_I8;
     return FA_OK;
   }
-  // int4 symmetric group-32, f16 scales, MatMulNBits nibble order (low = even k)
   if (K % 32) return set_err(ctx, FA_E_UNSUPPORTED, "encoder load: %s K=%d not a multiple of 32 for int4", name, K);
   const int nblk = K / 32;
-  std::vector<uint8_t> q((size_t)N * nblk * 16, 0x88);
+  std::vector<uint8_t> q((size_t)N * nblk * 16);
   std::vector<uint16_t> sc((size_t)N * nblk);
-  for (int n = 0; n < N; n++)
-    for (int b = 0; b < nblk; b++) {
-      float mx = 0.f;
-      for (int t = 0; t < 32; t++) mx = std::fmax(mx, std::fabs(bt[(size_t)n * K + b * 32 + t]));
-      uint16_t sh = h_f32_to_f16(mx / 7.0f);
-      float s = h_f16_to_f32(sh);
-      if (s == 0.f) {
-        sh = 0x3c00;
-        s = 1.f;
-      }
-      sc[(size_t)n * nblk + b] = sh;
-      uint8_t *blk = &q[((size_t)n * nblk + b) * 16];
-      for (int t = 0; t < 32; t++) {
-        float r = std::rint(bt[(size_t)n * K + b * 32 + t] / s);
-        r = r < -8.f ? -8.f : (r > 7.f ? 7.f : r);
-        const uint8_t nib = (uint8_t)((int)r + 8);
-        blk[t / 2] = (t & 1) ? (uint8_t)((blk[t / 2] & 0x0f) | (nib << 4)) : (uint8_t)((blk[t / 2] & 0xf0) | nib);
-      }
-    }
+  quantize_int4_km(bt.data(), N, K, q.data(), sc.data());
   if (!(L.w = dupload(e, q.data(), q.size())) || !(L.scales = dupload(e, sc.data(), sc.size()))) return set_err(ctx, FA_E_OOM, "encoder load: %s", name);
   if (!unit && !(L.colscale = dupload(e, fold.data(), N))) return set_err(ctx, FA_E_OOM, "encoder load: %s", name);
   L.bkind = B_I4;
@@ -292,29 +306,21 @@ static int build_lin(fa_encoder *e, Lin &L, const std::vector<float> &bt, int N,
 // (used for the pos weights, which only enter through the load-time table).
 static void roundtrip_format(int format, std::vector<float> &bt, int N, int K) {
   if (format == FA_W_INT8) {
-    for (int n = 0; n < N; n++) {
-      float mx = 0.f;
-      for (int k = 0; k < K; k++) mx = std::fmax(mx, std::fabs(bt[(size_t)n * K + k]));
-      float s = mx / 127.0f;
-      if (s == 0.f) s = 1.f;
-      for (int k = 0; k < K; k++) {
-        float r = std::rint(bt[(size_t)n * K + k] / s);
-        r = r < -127.f ? -127.f : (r > 127.f ? 127.f : r);
-        bt[(size_t)n * K + k] = r * s;
-      }
-    }
-  } else if (format == FA_W_INT4) {
+    std::vector<int8_t> q((size_t)N * K);
+    std::vector<float> s(N);
+    quantize_int8_km(bt.data(), N, K, q.data(), s.data());
     for (int n = 0; n < N; n++)
-      for (int b = 0; b < K / 32; b++) {
-        float mx = 0.f;
-        for (int t = 0; t < 32; t++) mx = std::fmax(mx, std::fabs(bt[(size_t)n * K + b * 32 + t]));
-        float s = h_f16_to_f32(h_f32_to_f16(mx / 7.0f));
-        if (s == 0.f) s = 1.f;
-        for (int t = 0; t < 32; t++) {
-          float r = std::rint(bt[(size_t)n * K + b * 32 + t] / s);
-          r = r < -8.f ? -8.f : (r > 7.f ? 7.f : r);
-          bt[(size_t)n * K + b * 32 + t] = r * s;
-        }
+      for (int k = 0; k < K; k++) bt[(size_t)n * K + k] = (float)q[(size_t)n * K + k] * s[n];
+  } else if (format == FA_W_INT4) {
+    const int nblk = (K + 31) / 32;
+    std::vector<uint8_t> q((size_t)N * nblk * 16);
+    std::vector<uint16_t> sc((size_t)N * nblk);
+    quantize_int4_km(bt.data(), N, K, q.data(), sc.data());
+    for (int n = 0; n < N; n++)
+      for (int k = 0; k < K; k++) {
+        const uint8_t byte = q[((size_t)n * nblk + k / 32) * 16 + (k % 32) / 2];
+        const int nib = (k & 1) ? (byte >> 4) : (byte & 0xf);
+        bt[(size_t)n * K + k] = (float)(nib - 8) * h_f16_to_f32(sc[(size_t)n * nblk + k / 32]);
       }
   }
 }
@@ -353,6 +359,22 @@ using namespace fa;
 extern "C" {
 
 int fa_encoder_tsub(int T) { return stride2_len(stride2_len(stride2_len(T))); }
+
+int fa_quantize_weights(int format, const float *w, int K, int N, void *q_out, void *scales_out) {
+  if (!w || !q_out || !scales_out || K <= 0 || N <= 0) return FA_E_INVALID;
+  std::vector<float> bt((size_t)N * K);
+  for (int k = 0; k < K; k++)
+    for (int n = 0; n < N; n++) bt[(size_t)n * K + k] = w[(size_t)k * N + n];
+  if (format == 1) {
+    quantize_int8_km(bt.data(), N, K, (int8_t *)q_out, (float *)scales_out);
+    return FA_OK;
+  }
+  if (format == 2) {
+    quantize_int4_km(bt.data(), N, K, (uint8_t *)q_out, (uint16_t *)scales_out);
+    return FA_OK;
+  }
+  return FA_E_INVALID;
+}
 
 void fa_encoder_destroy(fa_encoder *enc) {
   if (!enc) return;

@@ -159,6 +159,19 @@ int fa_dequant_int8(fa_ctx *ctx, fa_tensor wq, fa_tensor scale, int K, int N, fa
  * [N][K/32] as bytes) into out [K,N] f32: (nibble-8)·scale. */
 int fa_dequant_int4(fa_ctx *ctx, fa_tensor bq, fa_tensor scales_f16, int K, int N, fa_tensor *out);
 
+/* Host-side quantiser used by fa_encoder_load (no device work, callable
+ * without a GPU).  w is the reference's [K, N] ([in, out]) f32 matrix.
+ *   format 1 (int8, quantize-parakeet-encoder.py:31-36): q_out int8 K-major
+ *     [N][K]; scales_out f32 [N] = f32(max_k|w|)/127 (0 -> 1); q =
+ *     clip(rint(w/s), -127, 127).
+ *   format 2 (int4 symmetric group-32): q_out [N][ceil(K/32)][16 B], nibble =
+ *     q + 8, low nibble = even k (MatMulNBits order, lib.rs:164-203);
+ *     scales_out f16 bits [N][ceil(K/32)] = f16(max|w|/7) (0 -> 1.0);
+ *     q = clip(rint(w/s), -8, 7); padding nibbles of a partial block encode 0.
+ * No reference counterpart for format 2: the reference's int4 path is
+ * asymmetric MatMulNBits with f32 scales. */
+int fa_quantize_weights(int format, const float *w, int K, int N, void *q_out, void *scales_out);
+
 /* Skinny weight-only GEMV (M <= 64): y [M,N] f32 = a[M,K] (f32) @ W, W int8
  * per-column (scale f32 [N]) or int4 group-32 (f16 scale bits).  format: 1 =
  * int8 ([N][K] K-major bytes), 2 = int4 (bq [N][K/32][16 B]).  The weight
