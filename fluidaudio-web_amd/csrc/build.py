@@ -43,7 +43,26 @@ def build(jobs: int = 8) -> str:
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
     os.replace(tmp, OUT)
+    build_node_addon()
     return OUT
+
+
+NODE_INC = "/usr/include/node"
+
+
+def build_node_addon() -> str | None:
+    """The N-API addon (fluidaudio-web_amd/node/fa_hip.node) over libfa_hip.so,
+    when Node's headers are installed (gcc only: N-API is a C interface)."""
+    if not os.path.exists(os.path.join(NODE_INC, "node_api.h")):
+        return None
+    ndir = os.path.join(PKG, "node")
+    out = os.path.join(ndir, "fa_hip.node")
+    cmd = ["gcc", "-O2", "-Wall", "-shared", "-fPIC", f"-I{NODE_INC}", os.path.join(ndir, "fa_napi.c"), "-o", out,
+           f"-L{PKG}", "-l:libfa_hip.so", "-Wl,-rpath,$ORIGIN/.."]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("N-API addon build failed:\n" + r.stdout + r.stderr)
+    return out
 
 
 if __name__ == "__main__":

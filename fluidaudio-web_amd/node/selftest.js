@@ -1,0 +1,107 @@
+// Node self-test of the N-API addon + HipContext on a GPU: each op against an
+// inline JS reference (the way scripts/gpu-verify.mjs checks WGSL kernels),
+// then the fused encoder's packed-vs-standalone equality.  Exit code 0 = pass.
+"use strict";
+const { HipContext, version, encoderTsub } = require("./hip-context.js");
+
+let seed = 0x5eed; // mulberry32, as scripts/backend-conformance.mjs:46-54
+const rand = () => {
+  seed |= 0;
+  seed = (seed + 0x6d2b79f5) | 0;
+  let t = Math.imul(seed ^ (seed >>> 15), 1 | seed);
+  t = (t + Math.imul(t ^ (t >>> 7), 61 | t)) ^ t;
+  return ((t ^ (t >>> 14)) >>> 0) / 4294967296;
+};
+const mk = (n, s = 1) => Float32Array.from({ length: n }, () => (rand() - 0.5) * s);
+const maxdiff = (a, b) => a.reduce((m, v, i) => Math.max(m, Math.abs(v - b[i])), 0);
+let failed = 0;
+const check = (name, d, tol) => {
+  const ok = d <= tol;
+  if (!ok) failed++;
+  console.log(`${ok ? "ok  " : "FAIL"} ${name}: maxΔ ${d.toExponential(2)} (tol ${tol})`);
+};
+
+(async () => {
+  console.log("addon", version());
+  const ctx = new HipContext(0);
+  // matmul f32 B + bias + silu + add
+  const M = 37, K = 64, N = 41;
+  const a = mk(M * K), b = mk(K * N), bias = mk(N), add = mk(M * N);
+  const ref = new Float32Array(M * N);
+  for (let i = 0; i < M; i++)
+    for (let j = 0; j < N; j++) {
+      let s = 0;
+      for (let k = 0; k < K; k++) s += a[i * K + k] * b[k * N + j];
+      const v = s + bias[j];
+      ref[i * N + j] = v / (1 + Math.exp(-Math.max(-30, Math.min(30, v)))) + add[i * N + j];
+    }
+  const y = ctx.matmul(ctx.upload(a, M, K), ctx.upload(b, K, N), { bias: ctx.upload(bias, 1, N), act: "silu", add: ctx.upload(add, M, N) });
+  check("matmul f32 bias+silu+add", maxdiff(await ctx.download(y), ref), 1e-4);
+  const y16 = ctx.matmul(ctx.upload(a, M, K), ctx.uploadF16(b, K, N), { bias: ctx.upload(bias, 1, N), act: "silu", add: ctx.upload(add, M, N) });
+  check("matmul f16 weights", maxdiff(await ctx.download(y16), ref), 2e-2);
+  // layernorm
+  const R = 5, C = 1024, x = mk(R * C, 6), g = mk(C), be = mk(C);
+  const lref = new Float32Array(R * C);
+  for (let r = 0; r < R; r++) {
+    let m = 0;
+    for (let j = 0; j < C; j++) m += x[r * C + j];
+    m /= C;
+    let v = 0;
+    for (let j = 0; j < C; j++) v += (x[r * C + j] - m) ** 2;
+    const inv = 1 / Math.sqrt(v / C + 1e-5);
+    for (let j = 0; j < C; j++) lref[r * C + j] = (x[r * C + j] - m) * inv * g[j] + be[j];
+  }
+  check("layernorm", maxdiff(await ctx.download(ctx.layernorm(ctx.upload(x, R, C), ctx.upload(g, 1, C), ctx.upload(be, 1, C))), lref), 1e-4);
+  // relShiftB closed form
+  const H = 2, t = 7, xs = mk(H * t * (2 * t - 1));
+  const rs = new Float32Array(H * t * t);
+  for (let hh = 0; hh < H; hh++) for (let i = 0; i < t; i++) for (let j = 0; j < t; j++) rs[(hh * t + i) * t + j] = xs[(hh * t + i) * (2 * t - 1) + t - 1 - i + j];
+  check("relShiftB", maxdiff(await ctx.download(ctx.relShiftB(ctx.upload(xs, H * t, 2 * t - 1), H)), rs), 0);
+  // staged read is single-use
+  const st = ctx.stageDownload(y);
+  await st.read();
+  let threw = false;
+  try {
+    await st.read();
+  } catch (e) {
+    threw = /single-use/.test(e.message);
+  }
+  check("stageDownload single-use throws", threw ? 0 : 1, 0);
+  // fused encoder: packed batch == standalone
+  const cfg = { D: 256, DFF: 1024, H: 2, HD: 128, layers: 1, dwK: 9, Csub: 64, Fsub: 16, melBins: 128 };
+  const man = {};
+  const add_ = (k, n, s) => (man[k] = { data: mk(n, s) });
+  for (let i = 0; i < 5; i++) {
+    add_(`c${i}w`, i === 2 || i === 4 ? 64 * 64 : 64 * 9, 0.5);
+    add_(`c${i}b`, 64, 0.05);
+  }
+  add_("linw", 64 * 16 * 256, 0.05);
+  add_("linb", 256, 0.05);
+  for (const ln of ["lnff1", "lnatt", "lnconv", "lnff2", "lnout"]) {
+    man[`L0_${ln}_w`] = { data: Float32Array.from({ length: 256 }, () => 1 + (rand() - 0.5) * 0.04) };
+    add_(`L0_${ln}_b`, 256, 0.04);
+  }
+  for (const k of ["ff1w1", "ff2w1"]) add_(`L0_${k}`, 256 * 1024, 0.04);
+  for (const k of ["ff1w2", "ff2w2"]) add_(`L0_${k}`, 1024 * 256, 0.04);
+  for (const k of ["q", "k", "v", "pos", "out"]) add_(`L0_${k}`, 256 * 256, 0.04);
+  add_("L0_pbu", 256, 0.04);
+  add_("L0_pbv", 256, 0.04);
+  add_("L0_pw1", 512 * 256, 0.04);
+  add_("L0_pw2", 256 * 256, 0.04);
+  add_("L0_dw", 256 * 9, 1);
+  add_("L0_dwb", 256, 0.04);
+  const fused = ctx.loadFusedEncoder(man, cfg, { maxT: 64 });
+  const mels = [mk(128 * 300, 2), mk(128 * 97, 2)];
+  const batch = await ctx.download(ctx.encodeFused(fused, mels));
+  const t0 = encoderTsub(300);
+  const alone0 = await ctx.download(ctx.encodeFused(fused, [mels[0]]));
+  const alone1 = await ctx.download(ctx.encodeFused(fused, [mels[1]]));
+  check("fused encoder window 0 packed == alone", maxdiff(batch.subarray(0, t0 * 256), alone0), 1e-4);
+  check("fused encoder window 1 packed == alone", maxdiff(batch.subarray(t0 * 256), alone1), 1e-4);
+  ctx.destroyFusedEncoder(fused);
+  ctx.destroy();
+  process.exit(failed ? 1 : 0);
+})().catch((e) => {
+  console.error(e);
+  process.exit(2);
+});
