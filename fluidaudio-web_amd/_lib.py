@@ -46,6 +46,7 @@ SIGNATURES = [
     ("fa_upload_f16", I, [P, F32P, I, I, C.POINTER(T)]),
     ("fa_alloc", I, [P, I, I, C.POINTER(T)]),
     ("fa_alloc_f16", I, [P, I, I, C.POINTER(T)]),
+    ("fa_upload_f16_rows", I, [P, F32P, I, I, C.POINTER(T)]),
     ("fa_upload_bytes", I, [P, C.c_void_p, C.c_size_t, C.POINTER(T)]),
     ("fa_free_tensor", I, [P, T]),
     ("fa_pin", I, [P, T, I]),

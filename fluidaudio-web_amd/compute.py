@@ -128,6 +128,15 @@ class HipContext:
         check(self._p, lib().fa_upload_f16(self._p, d.ctypes.data_as(L.F32P), rows, cols, C.byref(o)))
         return HipTensor(self, o.value, rows, cols, f16=True)
 
+    def _uploadF16Rows(self, data, rows, cols):
+        """Row-major f16 activations (no ComputeContext counterpart; feeds matmul's f16 x f16 route)."""
+        d = _f32(data).reshape(-1)
+        if d.size != rows * cols:
+            raise FaError(L.FA_E_INVALID, f"_uploadF16Rows: {d.size} values for [{rows},{cols}]")
+        o = self._out()
+        check(self._p, lib().fa_upload_f16_rows(self._p, d.ctypes.data_as(L.F32P), rows, cols, C.byref(o)))
+        return HipTensor(self, o.value, rows, cols, f16=True)
+
     def alloc(self, rows, cols):
         o = self._out()
         check(self._p, lib().fa_alloc(self._p, rows, cols, C.byref(o)))

@@ -79,92 +79,15 @@ enum Epi : int { EPI_F32 = 0, EPI_F16 = 1, EPI_F16_SILU = 2, EPI_F16_RELU = 3, E
 
 __device__ __forceinline__ float sigmoid_mul(float v, float g) { return __fdividef(v, 1.f + __expf(-fminf(fmaxf(g, -30.f), 30.f))); }
 
-template <int BM, int BN, int WM, int WN, int AK, int BKND, int EPI>
-__global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_kernel(GemmArgs p) {
-  constexpr int NT = 64 * WM * WN;
-  constexpr int BK = 64, LS = BK + 8;  // LDS row stride in halfs (+8 breaks bank conflicts)
-  constexpr int WTM = BM / WM, WTN = BN / WN;
-  constexpr int TI = WTM / 16, TJ = WTN / 16;
-  constexpr int CA = BM * 8 / NT, CB = BN * 8 / NT;
-  static_assert(CA >= 1 && CB >= 1 && BM * 8 % NT == 0 && BN * 8 % NT == 0, "tile/thread mismatch");
-  __shared__ __attribute__((aligned(16))) _Float16 sA[2][BM * LS];
-  __shared__ __attribute__((aligned(16))) _Float16 sB[2][BN * LS];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
-  const int nTN = (p.N + BN - 1) / BN, nTM = (p.M + BM - 1) / BM;
-  const int tile = xcd_remap(blockIdx.x, nTM * nTN);
-  const int m0 = (tile / nTN) * BM, n0 = (tile % nTN) * BN;
-
-  f4 acc[TI][TJ];
-#pragma unroll
-  for (int i = 0; i < TI; i++)
-#pragma unroll
-    for (int j = 0; j < TJ; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
-
-  h8 ra[CA], rb[CB];
-  auto gload = [&](int k0) {
-#pragma unroll
-    for (int c = 0; c < CA; c++) {
-      const int idx = tid + c * NT, row = idx >> 3, kc = idx & 7;
-      const int gr = min(m0 + row, p.M - 1);
-      ra[c] = load_a8<AK>(p, gr, k0 + kc * 8);
-    }
-#pragma unroll
-    for (int c = 0; c < CB; c++) {
-      const int idx = tid + c * NT, row = idx >> 3, kc = idx & 7;
-      const int gn = min(n0 + row, p.N - 1);
-      rb[c] = load_b8<BKND>(p, gn, k0 + kc * 8);
-    }
-  };
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int c = 0; c < CA; c++) {
-      const int idx = tid + c * NT, row = idx >> 3, kc = idx & 7;
-      *reinterpret_cast<h8 *>(&sA[buf][row * LS + kc * 8]) = ra[c];
-    }
-#pragma unroll
-    for (int c = 0; c < CB; c++) {
-      const int idx = tid + c * NT, row = idx >> 3, kc = idx & 7;
-      *reinterpret_cast<h8 *>(&sB[buf][row * LS + kc * 8]) = rb[c];
-    }
-  };
-
-  const int nk = p.K / BK;
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  const int arow = wm * WTM + (lane & 15), brow = wn * WTN + (lane & 15), kq = (lane >> 4) * 8;
-  for (int kt = 0; kt < nk; kt++) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) gload((kt + 1) * BK);
-    h8 af[2][TI], bf[2][TJ];
-#pragma unroll
-    for (int i = 0; i < TI; i++) af[0][i] = *reinterpret_cast<const h8 *>(&sA[buf][(arow + i * 16) * LS + kq]);
-#pragma unroll
-    for (int j = 0; j < TJ; j++) bf[0][j] = *reinterpret_cast<const h8 *>(&sB[buf][(brow + j * 16) * LS + kq]);
-#pragma unroll
-    for (int i = 0; i < TI; i++) af[1][i] = *reinterpret_cast<const h8 *>(&sA[buf][(arow + i * 16) * LS + 32 + kq]);
-#pragma unroll
-    for (int j = 0; j < TJ; j++) bf[1][j] = *reinterpret_cast<const h8 *>(&sB[buf][(brow + j * 16) * LS + 32 + kq]);
-#pragma unroll
-    for (int s = 0; s < 2; s++)
-#pragma unroll
-      for (int i = 0; i < TI; i++)
-#pragma unroll
-        for (int j = 0; j < TJ; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s][i], bf[s][j], acc[i][j], 0, 0, 0);
-    if (kt + 1 < nk) lstore(buf ^ 1);
-    __syncthreads();
-  }
-
-  // Epilogue, staged through LDS (free after the main loop): each wave writes
-  // 16-row strips of its accumulators, then reads them back row-contiguous so
-  // every global access is a 16-byte vector and each row segment is written
-  // by consecutive lanes (the MFMA layout itself gives 2-4 byte scattered stores).
+// Epilogue, staged through LDS (free after the main loop): each wave writes
+// 16-row strips of its accumulators, then reads them back row-contiguous so
+// every global access is a 16-byte vector and each row segment is written
+// by consecutive lanes (the MFMA layout itself gives 2-4 byte scattered stores).
+// `lds` holds 16 * (WTN + 4) floats per wave; (r0, c0) is the wave tile's origin.
+template <int WTM, int WTN, int TI, int TJ, int EPI>
+__device__ __forceinline__ void epilogue(const GemmArgs &p, f4 (&acc)[TI][TJ], float *lds, int r0, int c0, int wave, int lane) {
   constexpr int SS = WTN + 4;  // strip row stride (floats)
-  static_assert(4 * 16 * SS * 4 <= 2 * (BM + BN) * LS * 2, "epilogue strip does not fit in LDS");
-  float *strip = reinterpret_cast<float *>(&sA[0][0]) + wave * 16 * SS;
-  const int r0 = m0 + wm * WTM, c0 = n0 + wn * WTN;
+  float *strip = lds + wave * 16 * SS;
   constexpr int OCOLS = EPI == EPI_GLU ? WTN / 2 : WTN;  // output columns of this wave's strip
   constexpr int LPR = OCOLS / 4;                         // lanes per output row (4 values each)
   constexpr int RPP = 64 / LPR;                          // rows per pass
@@ -271,6 +194,223 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_kernel(GemmArgs p) {
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_wave_barrier();
   }
+}
+
+template <int BM, int BN, int WM, int WN, int AK, int BKND, int EPI>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_kernel(GemmArgs p) {
+  constexpr int NT = 64 * WM * WN;
+  constexpr int BK = 64, LS = BK + 8;  // LDS row stride in halfs (+8 breaks bank conflicts)
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TI = WTM / 16, TJ = WTN / 16;
+  constexpr int CA = BM * 8 / NT, CB = BN * 8 / NT;
+  static_assert(CA >= 1 && CB >= 1 && BM * 8 % NT == 0 && BN * 8 % NT == 0, "tile/thread mismatch");
+  __shared__ __attribute__((aligned(16))) _Float16 sA[2][BM * LS];
+  __shared__ __attribute__((aligned(16))) _Float16 sB[2][BN * LS];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int nTN = (p.N + BN - 1) / BN, nTM = (p.M + BM - 1) / BM;
+  const int tile = xcd_remap(blockIdx.x, nTM * nTN);
+  const int m0 = (tile / nTN) * BM, n0 = (tile % nTN) * BN;
+
+  f4 acc[TI][TJ];
+#pragma unroll
+  for (int i = 0; i < TI; i++)
+#pragma unroll
+    for (int j = 0; j < TJ; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+  h8 ra[CA], rb[CB];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int c = 0; c < CA; c++) {
+      const int idx = tid + c * NT, row = idx >> 3, kc = idx & 7;
+      const int gr = min(m0 + row, p.M - 1);
+      ra[c] = load_a8<AK>(p, gr, k0 + kc * 8);
+    }
+#pragma unroll
+    for (int c = 0; c < CB; c++) {
+      const int idx = tid + c * NT, row = idx >> 3, kc = idx & 7;
+      const int gn = min(n0 + row, p.N - 1);
+      rb[c] = load_b8<BKND>(p, gn, k0 + kc * 8);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int c = 0; c < CA; c++) {
+      const int idx = tid + c * NT, row = idx >> 3, kc = idx & 7;
+      *reinterpret_cast<h8 *>(&sA[buf][row * LS + kc * 8]) = ra[c];
+    }
+#pragma unroll
+    for (int c = 0; c < CB; c++) {
+      const int idx = tid + c * NT, row = idx >> 3, kc = idx & 7;
+      *reinterpret_cast<h8 *>(&sB[buf][row * LS + kc * 8]) = rb[c];
+    }
+  };
+
+  const int nk = p.K / BK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  const int arow = wm * WTM + (lane & 15), brow = wn * WTN + (lane & 15), kq = (lane >> 4) * 8;
+  for (int kt = 0; kt < nk; kt++) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) gload((kt + 1) * BK);
+    h8 af[2][TI], bf[2][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; i++) af[0][i] = *reinterpret_cast<const h8 *>(&sA[buf][(arow + i * 16) * LS + kq]);
+#pragma unroll
+    for (int j = 0; j < TJ; j++) bf[0][j] = *reinterpret_cast<const h8 *>(&sB[buf][(brow + j * 16) * LS + kq]);
+#pragma unroll
+    for (int i = 0; i < TI; i++) af[1][i] = *reinterpret_cast<const h8 *>(&sA[buf][(arow + i * 16) * LS + 32 + kq]);
+#pragma unroll
+    for (int j = 0; j < TJ; j++) bf[1][j] = *reinterpret_cast<const h8 *>(&sB[buf][(brow + j * 16) * LS + 32 + kq]);
+#pragma unroll
+    for (int s = 0; s < 2; s++)
+#pragma unroll
+      for (int i = 0; i < TI; i++)
+#pragma unroll
+        for (int j = 0; j < TJ; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s][i], bf[s][j], acc[i][j], 0, 0, 0);
+    if (kt + 1 < nk) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  epilogue<WTM, WTN, TI, TJ, EPI>(p, acc, reinterpret_cast<float *>(&sA[0][0]), m0 + wm * WTM, n0 + wn * WTN, wave, lane);
+}
+
+// ── direct-to-LDS multi-stage f16 GEMM (A f16, B f16 K-major) ──────────────
+// The encoder's hot path.  Each K tile (64 halfs = 128 B per row) of the
+// stacked A|B panel is copied global->LDS by global_load_lds_dwordx4 (no VGPR
+// staging), S tiles in flight, one LDS array per stage.  Within a 128-byte
+// row the 16-byte chunk c of row r lives in slot c ^ (r & 7), so the eight
+// rows one ds_read_b128 phase touches hit distinct banks and each 8-lane group
+// of a copy still reads one contiguous 128-byte row segment.  8-wave
+// configurations run two waves per SIMD so one wave's MFMAs cover the other's
+// LDS reads and barrier waits.
+//
+// The copies are issued from inline asm and their completion is tracked with
+// explicit vmcnt waits: the compiler cannot tell the stages apart and would
+// otherwise wait for every copy in flight before each LDS read.
+// M0 is never a register-allocation candidate; the compiler only writes it
+// immediately before its own M0-reading instructions, so setting it inside the
+// asm statement is safe (clang still warns about clobbering a reserved register).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void *g, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_addr) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {  // gfx9 s_waitcnt: vmcnt [3:0]+[15:14], expcnt 7, lgkmcnt 15 = no wait
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+template <int BYTES>
+struct LdsStage {
+  char d[BYTES];
+};
+
+template <int BM, int BN, int WM, int WN, int S, int EPI>
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4))) void gemm_dma_kernel(GemmArgs p) {
+  constexpr int NW = WM * WN, BK = 64, RB = 128;
+  constexpr int WTM = BM / WM, WTN = BN / WN, TI = WTM / 16, TJ = WTN / 16;
+  constexpr int SA = BM * RB, STG = (BM + BN) * RB;
+  constexpr int IT = (BM + BN) / 8;                   // 1 KB copies per stage (8 rows each)
+  constexpr int IW = (IT + NW - 1) / NW, IMIN = IT / NW;  // per wave: at most / at least
+  static_assert(BM % 16 == 0 && BN % 16 == 0 && NW % 4 == 0, "tile shape");
+  static_assert(S >= 2 && S <= 4 && S * STG <= 160 * 1024, "LDS stages");
+  static_assert(NW * 16 * (WTN + 4) * 4 <= STG, "epilogue strips must fit in stage 0");
+  __shared__ __attribute__((aligned(1024))) LdsStage<STG> st0, st1, st2, st3;
+  char *const stg[4] = {st0.d, st1.d, st2.d, st3.d};
+  uint32_t sadr[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) sadr[i] = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)stg[i]);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int nTN = p.N / BN, nTM = (p.M + BM - 1) / BM;
+  const int tile = xcd_remap(blockIdx.x, nTM * nTN);
+  const int m0 = (tile / nTN) * BM, n0 = (tile % nTN) * BN;
+  const _Float16 *A = reinterpret_cast<const _Float16 *>(p.A), *B = reinterpret_cast<const _Float16 *>(p.B);
+
+  // copy i of this wave moves rows [ins*8, ins*8+8) of the stacked A|B tile
+  const _Float16 *src[IW];
+  const int lr = lane >> 3, lch = lane & 7;
+#pragma unroll
+  for (int i = 0; i < IW; i++) {
+    const int r = (wave + i * NW) * 8 + lr;
+    const int ch = lch ^ (r & 7);
+    if (r < BM)
+      src[i] = A + (size_t)min(m0 + r, p.M - 1) * p.lda + ch * 8;  // rows past M repeat the last row; never stored
+    else
+      src[i] = B + (size_t)(n0 + r - BM) * p.K + ch * 8;
+  }
+  auto issue = [&](int sidx, int k0) {
+#pragma unroll
+    for (int i = 0; i < IW; i++) {
+      const int ins = wave + i * NW;
+      if (IT % NW == 0 || ins < IT) dma16(src[i] + k0, sadr[sidx] + ins * 1024);
+    }
+  };
+
+  f4 acc[TI][TJ];
+#pragma unroll
+  for (int i = 0; i < TI; i++)
+#pragma unroll
+    for (int j = 0; j < TJ; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = p.K / BK;
+#pragma unroll
+  for (int s = 0; s < S - 1; s++)
+    if (s < nk) issue(s, s * BK);
+
+  const int q = lane >> 4, sw = lane & 7;  // fragment rows are 16-aligned + (lane & 15)
+  const int abase = (wm * WTM + (lane & 15)) * RB, bbase = SA + (wn * WTN + (lane & 15)) * RB;
+  h8 af[2][TI], bf[2][TJ];
+  auto rdfrag = [&](int sidx, int ks, int slot) {
+    const char *base = stg[sidx];
+    const int so = ((ks * 4 + q) ^ sw) * 16;
+#pragma unroll
+    for (int i = 0; i < TI; i++) af[slot][i] = *reinterpret_cast<const h8 *>(base + abase + i * 16 * RB + so);
+#pragma unroll
+    for (int j = 0; j < TJ; j++) bf[slot][j] = *reinterpret_cast<const h8 *>(base + bbase + j * 16 * RB + so);
+  };
+  auto mma = [&](int slot) {
+#pragma unroll
+    for (int i = 0; i < TI; i++)
+#pragma unroll
+      for (int j = 0; j < TJ; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[slot][i], bf[slot][j], acc[i][j], 0, 0, 0);
+  };
+  // K tile kt is in LDS once at most (S-2) later tiles are still in flight
+  // (copies complete in issue order), for every wave: then barrier.
+  auto ready = [&](int kt) {
+    if (kt + S - 2 < nk)
+      wait_vmcnt<(S - 2) * IMIN>();
+    else
+      wait_vmcnt<0>();
+    __syncthreads();
+  };
+
+  ready(0);
+  rdfrag(0, 0, 0);
+  for (int kt0 = 0; kt0 < nk; kt0 += S) {
+#pragma unroll
+    for (int u = 0; u < S; u++) {
+      const int kt = kt0 + u;
+      if (kt < nk) {
+        // refill the stage every wave finished reading before the last barrier
+        if (kt + S - 1 < nk) issue((u + S - 1) % S, (kt + S - 1) * BK);
+        rdfrag(u, 1, 1);
+        mma(0);
+        mma(1);  // placed before the wait so its MFMAs overlap the barrier
+        if (kt + 1 < nk) {
+          ready(kt + 1);
+          rdfrag((u + 1) % S, 0, 0);
+        }
+      }
+    }
+  }
+  __syncthreads();  // every wave is done with the stages before strips reuse stage 0
+  epilogue<WTM, WTN, TI, TJ, EPI>(p, acc, reinterpret_cast<float *>(st0.d), m0 + wm * WTM, n0 + wn * WTN, wave, lane);
 }
 
 // ── fp32 MFMA GEMM: B f32 row-major [K,N] ───────────────────────────────────
@@ -412,8 +552,56 @@ static int pick_tile(fa_ctx *ctx, int M, int N) {
   return best;
 }
 
+// Direct-to-LDS configurations for f16 x f16: BM x BN, waves, stages, and the
+// measured time of one full round (every CU busy with one tile, K = 1024) on
+// MI355X at M = 3008; a launch costs ceil(tiles / CUs) rounds, scaled by K.
+struct DmaCfg {
+  int bm, bn;
+  float us_round;
+};
+static const DmaCfg kDma[] = {{192, 256, 30.0f}, {192, 128, 18.3f}, {128, 128, 12.6f}, {96, 128, 11.7f}};
+
+static int pick_dma(fa_ctx *ctx, const GemmArgs &p) {
+  if (p.K % 64 || p.lda % 8 || ((uintptr_t)p.A & 15) || ((uintptr_t)p.B & 15)) return -1;
+  // FA_GEMM_DMA=0 turns the route off; 1..4 pins configuration 0..3 when N fits it.
+  if (const char *e = getenv("FA_GEMM_DMA")) {
+    const int f = atoi(e);
+    if (f == 0) return -1;
+    if (f >= 1 && f <= (int)(sizeof kDma / sizeof kDma[0]) && p.N % kDma[f - 1].bn == 0) return f - 1;
+  }
+  int best = -1;
+  double bestc = 1e300;
+  for (int i = 0; i < (int)(sizeof kDma / sizeof kDma[0]); i++) {
+    if (p.N % kDma[i].bn) continue;
+    const long tiles = (long)cdiv(p.M, kDma[i].bm) * (p.N / kDma[i].bn);
+    const double c = (double)cdiv(tiles, ctx->num_cu) * kDma[i].us_round;
+    if (c < bestc * 0.999) {
+      bestc = c;
+      best = i;
+    }
+  }
+  return best;
+}
+
+template <int BM, int BN, int WM, int WN, int S, int EPI>
+static int launch_dma(fa_ctx *ctx, const GemmArgs &p, const char *label) {
+  const unsigned tiles = cdiv(p.M, BM) * (p.N / BN);
+  ProfScope ps(ctx, label);
+  FA_LAUNCH(ps, (gemm_dma_kernel<BM, BN, WM, WN, S, EPI>), dim3(tiles), dim3(64 * WM * WN), 0, ctx->stream, p);
+  return check_launch(ctx, label);
+}
+
 template <int AK, int BKND, int EPI>
 static int launch_tile(fa_ctx *ctx, const GemmArgs &p, const char *label) {
+  if constexpr (AK == A_F16 && BKND == B_F16 && EPI != EPI_GENERIC) {
+    switch (pick_dma(ctx, p)) {
+      case 0: return launch_dma<192, 256, 2, 4, 2, EPI>(ctx, p, label);
+      case 1: return launch_dma<192, 128, 4, 2, 3, EPI>(ctx, p, label);
+      case 2: return launch_dma<128, 128, 2, 4, 4, EPI>(ctx, p, label);
+      case 3: return launch_dma<96, 128, 2, 4, 4, EPI>(ctx, p, label);
+      default: break;
+    }
+  }
   if constexpr (AK == A_F32 || EPI == EPI_GENERIC) {  // ComputeContext path: mid-size tiles
     const long t128 = (long)cdiv(p.M, 128) * cdiv(p.N, 128);
     if (t128 >= ctx->num_cu) return launch_cfg<128, 128, 2, 2, AK, BKND, EPI>(ctx, p, label);

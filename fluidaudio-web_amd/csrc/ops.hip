@@ -549,6 +549,8 @@ int fa_copy_rows(fa_ctx *ctx, fa_tensor dst, fa_tensor src, int row_offset) {
   TensorRec *rd, *rs;
   FA_TRY(need(ctx, dst, &rd, "copyRows"));
   FA_TRY(need(ctx, src, &rs, "copyRows"));
+  FA_TRY(need_f32(ctx, rd, "copyRows dst"));
+  FA_TRY(need_f32(ctx, rs, "copyRows src"));
   if (rs->cols != rd->cols || row_offset < 0 || row_offset + rs->rows > rd->rows) return set_err(ctx, FA_E_INVALID, "copyRows: out of range");
   const size_t nb = (size_t)rs->rows * rs->cols * 4;
   if (nb) FA_HIP(ctx, hipMemcpyAsync(F32(rd) + (size_t)row_offset * rd->cols, rs->ptr, nb, hipMemcpyDeviceToDevice, ctx->stream));

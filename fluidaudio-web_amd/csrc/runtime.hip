@@ -288,6 +288,17 @@ int fa_upload_f16(fa_ctx *ctx, const float *data, int rows, int cols, fa_tensor 
   return FA_OK;
 }
 
+int fa_upload_f16_rows(fa_ctx *ctx, const float *data, int rows, int cols, fa_tensor *out) {
+  const size_t n = (size_t)rows * cols;
+  std::vector<__half> h(n);
+  for (size_t i = 0; i < n; i++) h[i] = __float2half_rn(data[i]);
+  TensorRec *r;
+  FA_TRY(new_tensor(ctx, rows, cols, S_F16RM, n * 2, out, &r));
+  if (n) FA_HIP(ctx, hipMemcpyAsync(r->ptr, h.data(), n * 2, hipMemcpyHostToDevice, ctx->stream));
+  FA_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return FA_OK;
+}
+
 int fa_alloc(fa_ctx *ctx, int rows, int cols, fa_tensor *out) {
   return new_tensor(ctx, rows, cols, S_F32, (size_t)rows * cols * 4, out);
 }

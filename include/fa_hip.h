@@ -69,6 +69,10 @@ int fa_upload(fa_ctx *ctx, const float *data, int rows, int cols, fa_tensor *out
 int fa_upload_f16(fa_ctx *ctx, const float *data, int rows, int cols, fa_tensor *out); /* uploadF16: f16 storage (RNE) */
 int fa_alloc(fa_ctx *ctx, int rows, int cols, fa_tensor *out);                         /* alloc (uninitialised) */
 int fa_alloc_f16(fa_ctx *ctx, int rows, int cols, fa_tensor *out);                     /* allocF16 */
+/* Row-major f16 activations [rows, cols] (RNE), pool-owned like alloc.  No
+ * counterpart in compute.d.ts: a host that keeps activations in f16 feeds them
+ * to matmul's f16 x f16 route (A f16, B from uploadF16) with this. */
+int fa_upload_f16_rows(fa_ctx *ctx, const float *data, int rows, int cols, fa_tensor *out);
 int fa_upload_bytes(fa_ctx *ctx, const void *data, size_t nbytes, fa_tensor *out);     /* uploadBytes (int8/int4 payloads) */
 int fa_free_tensor(fa_ctx *ctx, fa_tensor t);                                          /* freeTensor (f16/views ignored) */
 int fa_pin(fa_ctx *ctx, fa_tensor t, int to_parent);                                   /* pin */

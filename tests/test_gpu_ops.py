@@ -49,6 +49,23 @@ def test_matmul_f16_weights(ctx, orc, shape):
     assert err < 2e-2, err
 
 
+@pytest.mark.parametrize("cfg", ["auto", "1", "2", "3", "4", "0"])
+@pytest.mark.parametrize("shape", [(3008, 1024, 4096), (3008, 4096, 1024), (1504, 1024, 2048), (203, 256, 256), (1, 64, 128)])
+def test_matmul_f16_activations(ctx, orc, monkeypatch, cfg, shape):
+    """f16 A x f16 B (the encoder's GEMM route: direct-to-LDS kernels, each
+    configuration pinned in turn, M tails included) vs float64 dot products of
+    the same f16-rounded operands; bias + residual epilogue."""
+    M, K, N = shape
+    if cfg != "auto":
+        monkeypatch.setenv("FA_GEMM_DMA", cfg)
+    a, b, bias, d = rnd(M, K) * 4, rnd(K, N) * 0.1, rnd(1, N), rnd(M, N)
+    a16, b16 = a.astype(np.float16), b.astype(np.float16)
+    got = dl(ctx, ctx.matmul(ctx._uploadF16Rows(a, M, K), ctx.uploadF16(b, K, N), bias=ctx.upload(bias, 1, N), add=ctx.upload(d, M, N)))
+    ref = a16.astype(np.float64) @ b16.astype(np.float64) + bias.astype(np.float64) + d
+    err = np.abs(got - ref).max() / np.abs(ref).max()
+    assert err < 1e-5, (cfg, shape, err)
+
+
 def test_layernorm(ctx, orc):
     for R, Cc in [(5, 1024), (33, 77)]:
         x, g, b = rnd(R, Cc) * 3 + 1, rnd(1, Cc) + 1, rnd(1, Cc)
