@@ -5,9 +5,9 @@
 // HBM layout (rows = frames of all windows, packed back to back or padded to
 // the batch's longest window; one row table per stage, see WinStage):
 //   mel      [R0, melBins]     f32   time-major (the reference transposes on the host)
-//   s1       [R1, 64, Csub]    f16   c0 output, channels-last (t, f, c)
-//   s2, s2p  [R2, 32, Csub]    f16   dw c1 output, pw c2 output
-//   s3, s3p  [R3, 16, Csub]    f16   dw c3 output, pw c4 output
+//   s2       [R2, 32, 2*Csub]  f16   c0+c1 output (c0 fused, never stored), hi/lo pairs
+//   s2p      [R2, 32, Csub]    f32   pw c2 output before its ReLU
+//   s3, s3p  [R3, 16, 2*Csub]  f16   dw c3 output, pw c4 output, hi/lo pairs
 //   x        [R3, D]           f32   residual stream (the returned frames)
 //   h        [R3, D]           f16   LayerNorm outputs (GEMM A operands)
 //   u        [R3, max(DFF,3D)] f16   FF hidden / fused q|k|v
@@ -38,73 +38,192 @@ namespace fa {
 // One stage's window table: rows [off[w], off[w]+len[w]) belong to window w.
 typedef WinTable WinStage;
 
-// ── subsampling kernels (channels-last f16) ──────────────────────────────
-// c0: conv2d 1 -> C, 3x3, stride 2, pad 1, bias + ReLU (raw-encoder.js:188).
-// Thread = 8 channels of one (t1, f1) output; the 9 input taps are shared.
-__global__ __launch_bounds__(256) void sub_c0_kernel(const float *__restrict__ mel, int MB, WinStage in, WinStage out, int F1,
-                                                     const float *__restrict__ w, const float *__restrict__ b, _Float16 *__restrict__ y, int C) {
-  const int cg = C / 8, ppb = 256 / cg;
-  const int win = blockIdx.y;
-  const int pidx = blockIdx.x * ppb + threadIdx.x / cg, c0 = (threadIdx.x % cg) * 8;
-  const int T1 = out.len[win];
-  const int t1 = pidx / F1, f1 = pidx % F1;
-  if (t1 >= T1) return;
-  const int T0 = in.len[win];
-  const float *m = mel + (size_t)in.off[win] * MB;
-  float x[9];
+// ── subsampling kernels (channels-last) ──────────────────────────────────
+// One wavefront per output row (window, t) sweeping the frequency axis; lane l
+// owns channels [CPL*l, CPL*l + CPL), so each lane's weights stay in registers
+// for the whole sweep, inputs every lane shares (mel taps) are wave-uniform,
+// and a row position's channels are one contiguous store.
+//
+// The activations that feed the pointwise-conv GEMMs are stored as exact f16
+// pairs (hi = f16(v), lo = f16(v - hi), interleaved per channel) and those
+// GEMMs read K = 2*Csub against duplicated weight rows: the front end then
+// carries f32-accurate activations through f16 matrix cores.
+
+template <int CPL>
+__device__ __forceinline__ void store_hilo(_Float16 *dst, const float (&v)[CPL]) {
+  _Float16 o[2 * CPL];
 #pragma unroll
-  for (int a = 0; a < 3; a++)
-#pragma unroll
-    for (int bb = 0; bb < 3; bb++) {
-      const int ti = 2 * t1 - 1 + a, fi = 2 * f1 - 1 + bb;
-      x[a * 3 + bb] = (ti >= 0 && ti < T0 && fi >= 0 && fi < MB) ? m[(size_t)ti * MB + fi] : 0.f;
-    }
-  h8 o;
-#pragma unroll
-  for (int e = 0; e < 8; e++) {
-    const float *wc = w + (c0 + e) * 9;
-    float acc = b[c0 + e];
-#pragma unroll
-    for (int k = 0; k < 9; k++) acc += x[k] * wc[k];
-    o[e] = (_Float16)fmaxf(acc, 0.f);
+  for (int e = 0; e < CPL; e++) {
+    const _Float16 hi = (_Float16)v[e];
+    o[2 * e] = hi;
+    o[2 * e + 1] = (_Float16)(v[e] - (float)hi);
   }
-  *reinterpret_cast<h8 *>(y + (((size_t)(out.off[win] + t1) * F1 + f1) * C + c0)) = o;
+  if constexpr (CPL == 1) {
+    *reinterpret_cast<h2 *>(dst) = h2{o[0], o[1]};
+  } else if constexpr (CPL == 2) {
+    *reinterpret_cast<h4 *>(dst) = h4{o[0], o[1], o[2], o[3]};
+  } else {
+#pragma unroll
+    for (int e = 0; e < 2 * CPL; e += 8) *reinterpret_cast<h8 *>(dst + e) = h8{o[e], o[e + 1], o[e + 2], o[e + 3], o[e + 4], o[e + 5], o[e + 6], o[e + 7]};
+  }
 }
 
-// depthwise conv2d 3x3, stride 2, pad 1, + bias, no act (raw-encoder.js:189,191).
-// wt is [9][C] (tap-major) so 8 channels' weights are two float4 loads.
-__global__ __launch_bounds__(256) void sub_dw_kernel(const _Float16 *__restrict__ x, WinStage in, int Fin, WinStage out, int Fout,
-                                                     const float *__restrict__ wt, const float *__restrict__ b, _Float16 *__restrict__ y, int C) {
-  const int cg = C / 8, ppb = 256 / cg;
-  const int win = blockIdx.y;
-  const int pidx = blockIdx.x * ppb + threadIdx.x / cg, c0 = (threadIdx.x % cg) * 8;
-  const int To = out.len[win];
-  const int to = pidx / Fout, fo = pidx % Fout;
-  if (to >= To) return;
-  const int Ti = in.len[win];
-  const _Float16 *xb = x + (size_t)in.off[win] * Fin * C;
-  float acc[8];
+// c0 (conv2d 1 -> C, 3x3, stride 2, pad 1, + bias, ReLU; raw-encoder.js:188)
+// fused into c1 (depthwise 3x3, stride 2, pad 1, + bias; raw-encoder.js:189):
+// the c0 map never reaches memory.  c0 outputs outside [0,T1) x [0,F1) are
+// c1's zero padding.  w0 [C][9], b0 [C]; w1 [9][C] (tap-major), b1 [C].
+// Output: [rows of stage 2][F2][C] as hi/lo pairs (2C halfs per position).
+template <int CPL>
+__global__ __launch_bounds__(256) void sub_c01_kernel(const float *__restrict__ mel, int MB, WinStage s0, WinStage s1, int F1, WinStage s2, int F2,
+                                                      const float *__restrict__ w0, const float *__restrict__ b0, const float *__restrict__ w1,
+                                                      const float *__restrict__ b1, _Float16 *__restrict__ y) {
+  constexpr int C = 64 * CPL;
+  const int lane = threadIdx.x & 63, win = blockIdx.y;
+  const int t2 = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (t2 >= s2.len[win]) return;
+  float k0[CPL][9], c0b[CPL], k1[9][CPL], c1b[CPL];
 #pragma unroll
-  for (int e = 0; e < 8; e++) acc[e] = b[c0 + e];
+  for (int e = 0; e < CPL; e++) {
+    const int ch = CPL * lane + e;
+    c0b[e] = b0[ch];
+    c1b[e] = b1[ch];
 #pragma unroll
-  for (int a = 0; a < 3; a++) {
-    const int ti = 2 * to - 1 + a;
-    if (ti < 0 || ti >= Ti) continue;
-#pragma unroll
-    for (int bb = 0; bb < 3; bb++) {
-      const int fi = 2 * fo - 1 + bb;
-      if (fi < 0 || fi >= Fin) continue;
-      const h8 v = *reinterpret_cast<const h8 *>(xb + ((size_t)ti * Fin + fi) * C + c0);
-      const float *wk = wt + (a * 3 + bb) * C + c0;
-#pragma unroll
-      for (int e = 0; e < 8; e++) acc[e] += (float)v[e] * wk[e];
+    for (int k = 0; k < 9; k++) {
+      k0[e][k] = w0[ch * 9 + k];
+      k1[k][e] = w1[k * C + ch];
     }
   }
-  h8 o;
+  const int T0 = s0.len[win], T1 = s1.len[win];
+  const float *m = mel + (size_t)s0.off[win] * MB;
+  // c0 output (t1, f1) for this lane's channels; zero outside the c0 map
+  auto c0 = [&](int t1, int f1, float (&o)[CPL]) {
+    if (t1 < 0 || t1 >= T1 || f1 < 0 || f1 >= F1) {
 #pragma unroll
-  for (int e = 0; e < 8; e++) o[e] = (_Float16)acc[e];
-  *reinterpret_cast<h8 *>(y + (((size_t)(out.off[win] + to) * Fout + fo) * C + c0)) = o;
+      for (int e = 0; e < CPL; e++) o[e] = 0.f;
+      return;
+    }
+    float x[9];
+#pragma unroll
+    for (int a = 0; a < 3; a++) {
+      const int ti = 2 * t1 - 1 + a;
+#pragma unroll
+      for (int bb = 0; bb < 3; bb++) {
+        const int fi = 2 * f1 - 1 + bb;
+        x[a * 3 + bb] = (ti >= 0 && ti < T0 && fi >= 0 && fi < MB) ? m[(size_t)ti * MB + fi] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < CPL; e++) {
+      float acc = c0b[e];
+#pragma unroll
+      for (int k = 0; k < 9; k++) acc += x[k] * k0[e][k];
+      o[e] = fmaxf(acc, 0.f);
+    }
+  };
+  float left[3][CPL];  // c0 column 2*f2-1 of rows 2*t2-1 .. 2*t2+1 (the previous step's right column)
+#pragma unroll
+  for (int a = 0; a < 3; a++) c0(2 * t2 - 1 + a, -1, left[a]);
+  _Float16 *yr = y + (size_t)(s2.off[win] + t2) * F2 * 2 * C + 2 * CPL * lane;
+  for (int f2 = 0; f2 < F2; f2++) {
+    float o[CPL];
+#pragma unroll
+    for (int e = 0; e < CPL; e++) o[e] = c1b[e];
+#pragma unroll
+    for (int a = 0; a < 3; a++) {
+      float mid[CPL], right[CPL];
+      c0(2 * t2 - 1 + a, 2 * f2, mid);
+      c0(2 * t2 - 1 + a, 2 * f2 + 1, right);
+#pragma unroll
+      for (int e = 0; e < CPL; e++) {
+        o[e] += left[a][e] * k1[a * 3][e];
+        o[e] += mid[e] * k1[a * 3 + 1][e];
+        o[e] += right[e] * k1[a * 3 + 2][e];
+        left[a][e] = right[e];
+      }
+    }
+    store_hilo<CPL>(yr + (size_t)f2 * 2 * C, o);
+  }
 }
+
+// c3: depthwise conv2d 3x3, stride 2, pad 1, + bias (raw-encoder.js:191) over
+// the c2 GEMM's f32 pre-activation output, applying c2's ReLU on load.
+// wt [9][C] (tap-major).  Output hi/lo pairs like sub_c01_kernel.
+template <int CPL>
+__global__ __launch_bounds__(256) void sub_dw_kernel(const float *__restrict__ x, WinStage in, int Fin, WinStage out, int Fout,
+                                                     const float *__restrict__ wt, const float *__restrict__ b, _Float16 *__restrict__ y) {
+  constexpr int C = 64 * CPL;
+  const int lane = threadIdx.x & 63, win = blockIdx.y;
+  const int to = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (to >= out.len[win]) return;
+  float wr[9][CPL], br[CPL];
+#pragma unroll
+  for (int e = 0; e < CPL; e++) {
+    br[e] = b[CPL * lane + e];
+#pragma unroll
+    for (int k = 0; k < 9; k++) wr[k][e] = wt[k * C + CPL * lane + e];
+  }
+  const int Ti = in.len[win];
+  const float *xb = x + (size_t)in.off[win] * Fin * C + CPL * lane;
+  auto ld = [&](int ti, int fi, float (&v)[CPL]) {
+    if (ti >= 0 && ti < Ti && fi >= 0 && fi < Fin) {
+      const float *src = xb + ((size_t)ti * Fin + fi) * C;
+#pragma unroll
+      for (int e = 0; e < CPL; e++) v[e] = fmaxf(src[e], 0.f);
+    } else {
+#pragma unroll
+      for (int e = 0; e < CPL; e++) v[e] = 0.f;
+    }
+  };
+  float left[3][CPL];  // input column 2*fo-1 of rows 2*to-1 .. 2*to+1
+#pragma unroll
+  for (int a = 0; a < 3; a++) ld(2 * to - 1 + a, -1, left[a]);
+  _Float16 *yr = y + (size_t)(out.off[win] + to) * Fout * 2 * C + 2 * CPL * lane;
+  for (int fo = 0; fo < Fout; fo++) {
+    float o[CPL];
+#pragma unroll
+    for (int e = 0; e < CPL; e++) o[e] = br[e];
+#pragma unroll
+    for (int a = 0; a < 3; a++) {
+      const int ti = 2 * to - 1 + a;
+      float mid[CPL], right[CPL];
+      ld(ti, 2 * fo, mid);
+      ld(ti, 2 * fo + 1, right);
+#pragma unroll
+      for (int e = 0; e < CPL; e++) {
+        o[e] += left[a][e] * wr[a * 3][e];
+        o[e] += mid[e] * wr[a * 3 + 1][e];
+        o[e] += right[e] * wr[a * 3 + 2][e];
+        left[a][e] = right[e];
+      }
+    }
+    store_hilo<CPL>(yr + (size_t)fo * 2 * C, o);
+  }
+}
+
+// Front-end launches: C = 64 * CPL channels, grid (rows / 4, windows).
+#define FA_CPL_SWITCH(C, CALL)                                        \
+  switch ((C) / 64) {                                                 \
+    case 1: CALL(1); break;                                           \
+    case 2: CALL(2); break;                                           \
+    case 4: CALL(4); break;                                           \
+    case 8: CALL(8); break;                                           \
+    default: return set_err(ctx, FA_E_UNSUPPORTED, "Csub=%d", (C)); \
+  }
+static int launch_c01(fa_ctx *ctx, ProfScope &ps, dim3 grid, const float *mel, int MB, WinStage s0, WinStage s1, int F1, WinStage s2, int F2,
+                      const float *w0, const float *b0, const float *w1, const float *b1, _Float16 *y, int C) {
+#define FA_C01(K) FA_LAUNCH(ps, sub_c01_kernel<K>, grid, dim3(256), 0, ctx->stream, mel, MB, s0, s1, F1, s2, F2, w0, b0, w1, b1, y)
+  FA_CPL_SWITCH(C, FA_C01)
+#undef FA_C01
+  return FA_OK;
+}
+static int launch_dw(fa_ctx *ctx, ProfScope &ps, dim3 grid, const float *x, WinStage in, int Fin, WinStage out, int Fout, const float *wt,
+                     const float *b, _Float16 *y, int C) {
+#define FA_DW(K) FA_LAUNCH(ps, sub_dw_kernel<K>, grid, dim3(256), 0, ctx->stream, x, in, Fin, out, Fout, wt, b, y)
+  FA_CPL_SWITCH(C, FA_DW)
+#undef FA_DW
+  return FA_OK;
+}
+#undef FA_CPL_SWITCH
 
 // Conv module depthwise conv over time, k taps, symmetric pad (k-1)/2,
 // + bias (BatchNorm folded) + SiLU (raw-encoder.js:365-367), per window.
@@ -201,8 +320,8 @@ struct fa_encoder {
   };
   std::vector<Layer> L;
   // workspace (grow-only)
-  void *s1 = nullptr, *s2 = nullptr, *s2p = nullptr, *s3 = nullptr, *s3p = nullptr, *h = nullptr, *u = nullptr, *a = nullptr, *g = nullptr;
-  size_t cap_s1 = 0, cap_s2 = 0, cap_s2p = 0, cap_s3 = 0, cap_s3p = 0, cap_m = 0, cap_u = 0;
+  void *s2 = nullptr, *s2p = nullptr, *s3 = nullptr, *s3p = nullptr, *h = nullptr, *u = nullptr, *a = nullptr, *g = nullptr;
+  size_t cap_s2 = 0, cap_s2p = 0, cap_s3 = 0, cap_s3p = 0, cap_m = 0, cap_u = 0;
 };
 
 namespace fa {
@@ -380,7 +499,7 @@ void fa_encoder_destroy(fa_encoder *enc) {
   if (!enc) return;
   (void)hipStreamSynchronize(enc->ctx->stream);
   for (void *p : enc->allocs) (void)hipFree(p);
-  for (void *p : {enc->s1, enc->s2, enc->s2p, enc->s3, enc->s3p, enc->h, enc->u, enc->a, enc->g})
+  for (void *p : {enc->s2, enc->s2p, enc->s3, enc->s3p, enc->h, enc->u, enc->a, enc->g})
     if (p) (void)hipFree(p);
   delete enc;
 }
@@ -393,7 +512,7 @@ int fa_encoder_load(fa_ctx *ctx, const fa_encoder_cfg *cfg, int n, const char *c
   if (c.HD != 128 || c.H * c.HD != c.D) return set_err(ctx, FA_E_UNSUPPORTED, "encoder: needs HD=128 and H*HD=D (got H=%d HD=%d D=%d)", c.H, c.HD, c.D);
   if (c.D % 64 || c.DFF % 64 || c.Csub % 64 || c.melBins != 8 * c.Fsub || (c.Csub * c.Fsub) % 64)
     return set_err(ctx, FA_E_UNSUPPORTED, "encoder: D, DFF, Csub must be multiples of 64 and melBins = 8*Fsub");
-  if (c.Csub / 8 > 256 || 256 % (c.Csub / 8)) return set_err(ctx, FA_E_UNSUPPORTED, "encoder: Csub/8 must divide 256");
+  if (c.Csub != 64 && c.Csub != 128 && c.Csub != 256 && c.Csub != 512) return set_err(ctx, FA_E_UNSUPPORTED, "encoder: Csub must be 64, 128, 256 or 512");
   if (c.dwK != 9) return set_err(ctx, FA_E_UNSUPPORTED, "encoder: depthwise kernel %d (9 supported)", c.dwK);
   if (max_T <= 0 || max_T > 1024) return set_err(ctx, FA_E_INVALID, "encoder: max_T %d outside 1..1024", max_T);
   if (format < FA_W_F16 || format > FA_W_INT4) return set_err(ctx, FA_E_INVALID, "encoder: weight format %d", format);
@@ -455,18 +574,27 @@ int fa_encoder_load(fa_ctx *ctx, const fa_encoder_cfg *cfg, int n, const char *c
       const float *w, *b;
       if ((st = get("c" + std::to_string(i) + "w", (int64_t)C * C, false, &w))) return fail(st);
       if ((st = get("c" + std::to_string(i) + "b", C, false, &b))) return fail(st);
-      std::vector<float> bt(w, w + (size_t)C * C), bias(b, b + C), fold(C, 1.f);  // [cout][cin] is already Bt
-      if ((st = build_lin(e, i == 2 ? e->c2 : e->c4, bt, C, C, fold, &bias, "pw conv"))) return fail(st);
+      // [cout][cin] is already Bt; each input channel's row appears twice
+      // (hi and lo halves of the activation pairs)
+      std::vector<float> bt((size_t)C * 2 * C), bias(b, b + C), fold(C, 1.f);
+      for (int co = 0; co < C; co++)
+        for (int ci = 0; ci < C; ci++) bt[(size_t)co * 2 * C + 2 * ci] = bt[(size_t)co * 2 * C + 2 * ci + 1] = w[(size_t)co * C + ci];
+      if ((st = build_lin(e, i == 2 ? e->c2 : e->c4, bt, C, 2 * C, fold, &bias, "pw conv"))) return fail(st);
     }
     const float *w, *b;
     if ((st = get("linw", (int64_t)C * F * D, false, &w))) return fail(st);
     if ((st = get("linb", D, false, &b))) return fail(st);
-    std::vector<float> bt((size_t)D * C * F);
+    // rows permuted from the reference's c*F+f to the channels-last f*C+c,
+    // each duplicated for the hi/lo activation pairs: k' = 2*(f*C+c) + {0,1}
+    std::vector<float> bt((size_t)D * 2 * C * F);
     for (int nn = 0; nn < D; nn++)
       for (int f = 0; f < F; f++)
-        for (int ch = 0; ch < C; ch++) bt[(size_t)nn * C * F + f * C + ch] = w[(size_t)(ch * F + f) * D + nn];
+        for (int ch = 0; ch < C; ch++) {
+          const size_t k = (size_t)nn * 2 * C * F + 2 * (f * C + ch);
+          bt[k] = bt[k + 1] = w[(size_t)(ch * F + f) * D + nn];
+        }
     std::vector<float> bias(b, b + D), fold(D, 1.f);
-    if ((st = build_lin(e, e->lin, bt, D, C * F, fold, &bias, "linw"))) return fail(st);
+    if ((st = build_lin(e, e->lin, bt, D, 2 * C * F, fold, &bias, "linw"))) return fail(st);
     e->format = saved;
   }
   // positional table pe(maxT) (raw-encoder.js:163-174), f32 on the device
@@ -684,11 +812,10 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
   const int M = R[3];
   const int layers = layers_run < 0 ? c.layers : std::min(layers_run, c.layers);
   // workspace
-  FA_TRY(grow(e, &e->s1, &e->cap_s1, (size_t)R[1] * F1 * C * 2));
-  FA_TRY(grow(e, &e->s2, &e->cap_s2, (size_t)R[2] * F2 * C * 2));
-  FA_TRY(grow(e, &e->s2p, &e->cap_s2p, (size_t)R[2] * F2 * C * 2));
-  FA_TRY(grow(e, &e->s3, &e->cap_s3, (size_t)R[3] * F3 * C * 2));
-  FA_TRY(grow(e, &e->s3p, &e->cap_s3p, (size_t)R[3] * F3 * C * 2));
+  FA_TRY(grow(e, &e->s2, &e->cap_s2, (size_t)R[2] * F2 * 2 * C * 2));  // hi/lo f16
+  FA_TRY(grow(e, &e->s2p, &e->cap_s2p, (size_t)R[2] * F2 * C * 4));    // f32 pre-ReLU
+  FA_TRY(grow(e, &e->s3, &e->cap_s3, (size_t)R[3] * F3 * 2 * C * 2));  // hi/lo f16
+  FA_TRY(grow(e, &e->s3p, &e->cap_s3p, (size_t)R[3] * F3 * 2 * C * 2));  // hi/lo f16
   const size_t need_m = (size_t)M * D * 2, need_u = (size_t)M * std::max(c.DFF, 3 * D) * 2;
   if (need_m > e->cap_m) {
     size_t c1 = 0, c2 = 0, c3 = 0;
@@ -705,46 +832,38 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
   rm = get(ctx, mel);
   float *x = (float *)rx->ptr;
   _Float16 *h = (_Float16 *)e->h, *u = (_Float16 *)e->u, *a = (_Float16 *)e->a, *gg = (_Float16 *)e->g;
-  const int cg = C / 8, ppb = 256 / cg;
 
   // ── subsampling ──
   {
-    ProfScope ps(ctx, "sub_c0");
-    FA_LAUNCH(ps, sub_c0_kernel, dim3(cdiv((long)mx[1] * F1, ppb), n), dim3(256), 0, ctx->stream, (const float *)rm->ptr, MB, s0, s1, F1,
-                       e->c0w, e->c0b, (_Float16 *)e->s1, C);
-    FA_TRY(check_launch(ctx, "sub_c0"));
+    ProfScope ps(ctx, "sub_c01");
+    FA_TRY(launch_c01(ctx, ps, dim3(cdiv(mx[2], 4), n), (const float *)rm->ptr, MB, s0, s1, F1, s2, F2, e->c0w, e->c0b, e->c1w, e->c1b,
+                      (_Float16 *)e->s2, C));
+    FA_TRY(check_launch(ctx, "sub_c01"));
   }
   {
-    ProfScope ps(ctx, "sub_dw1");
-    FA_LAUNCH(ps, sub_dw_kernel, dim3(cdiv((long)mx[2] * F2, ppb), n), dim3(256), 0, ctx->stream, (const _Float16 *)e->s1, s1, F1, s2, F2,
-                       e->c1w, e->c1b, (_Float16 *)e->s2, C);
-    FA_TRY(check_launch(ctx, "sub_dw1"));
-  }
-  {
-    GemmArgs p;
-    p.A = e->s2; p.lda = C; p.akind = A_F16;
+    GemmArgs p;  // c2 (1x1) + bias; its ReLU is applied by the c3 kernel's loads
+    p.A = e->s2; p.lda = 2 * C; p.akind = A_F16;
     set_gemm_b(p, e->c2);
-    p.C = e->s2p; p.ldc = C; p.out_f16 = 1; p.act = FA_ACT_RELU;
+    p.C = e->s2p; p.ldc = C;
     p.M = R[2] * F2;
     FA_TRY(gemm_mfma(ctx, p, "sub_pw2"));
   }
   {
     ProfScope ps(ctx, "sub_dw3");
-    FA_LAUNCH(ps, sub_dw_kernel, dim3(cdiv((long)mx[3] * F3, ppb), n), dim3(256), 0, ctx->stream, (const _Float16 *)e->s2p, s2, F2, s3, F3,
-                       e->c3w, e->c3b, (_Float16 *)e->s3, C);
+    FA_TRY(launch_dw(ctx, ps, dim3(cdiv(mx[3], 4), n), (const float *)e->s2p, s2, F2, s3, F3, e->c3w, e->c3b, (_Float16 *)e->s3, C));
     FA_TRY(check_launch(ctx, "sub_dw3"));
   }
   {
-    GemmArgs p;
-    p.A = e->s3; p.lda = C; p.akind = A_F16;
+    GemmArgs p;  // c4 (1x1) + bias + ReLU, written as hi/lo pairs for the linear
+    p.A = e->s3; p.lda = 2 * C; p.akind = A_F16;
     set_gemm_b(p, e->c4);
-    p.C = e->s3p; p.ldc = C; p.out_f16 = 1; p.act = FA_ACT_RELU;
+    p.C = e->s3p; p.ldc = 2 * C; p.out_f16 = 1; p.hilo = 1;
     p.M = R[3] * F3;
     FA_TRY(gemm_mfma(ctx, p, "sub_pw4"));
   }
   {
     GemmArgs p;
-    p.A = e->s3p; p.lda = C * F3; p.akind = A_F16;
+    p.A = e->s3p; p.lda = 2 * C * F3; p.akind = A_F16;
     set_gemm_b(p, e->lin);
     p.C = x; p.ldc = D;
     p.M = M;

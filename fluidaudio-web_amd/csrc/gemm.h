@@ -27,7 +27,8 @@ struct GemmArgs {
   const float *add = nullptr;       // f32 residual [M, ldadd]; may alias C
   int ldadd = 0;
   int act = 0;
-  int glu = 0;  // GLU-pair epilogue (see gemm.hip), out [M, N/2] f16
+  int glu = 0;   // GLU-pair epilogue (see gemm.hip), out [M, N/2] f16
+  int hilo = 0;  // ReLU then an exact f16 pair per value: out [M, 2N] f16, (hi, lo) at columns 2n, 2n+1
   int M = 0, N = 0, K = 0;
 };
 

@@ -75,7 +75,7 @@ __device__ __forceinline__ h8 load_b8(const GemmArgs &p, int n, int k) {
 // Epilogue variants, fixed at compile time so the per-element code is short and
 // the accumulators stay in registers (a runtime activation switch per element
 // pushed large tiles' accumulators to scratch).
-enum Epi : int { EPI_F32 = 0, EPI_F16 = 1, EPI_F16_SILU = 2, EPI_F16_RELU = 3, EPI_GLU = 4, EPI_GENERIC = 5 };
+enum Epi : int { EPI_F32 = 0, EPI_F16 = 1, EPI_F16_SILU = 2, EPI_F16_RELU = 3, EPI_GLU = 4, EPI_GENERIC = 5, EPI_HILO_RELU = 6 };
 
 __device__ __forceinline__ float sigmoid_mul(float v, float g) { return __fdividef(v, 1.f + __expf(-fminf(fmaxf(g, -30.f), 30.f))); }
 
@@ -150,6 +150,18 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f4 (&acc)[TI][TJ], f
                 o.x += ad.x; o.y += ad.y; o.z += ad.z; o.w += ad.w;
               }
               *reinterpret_cast<float4 *>(reinterpret_cast<float *>(p.C) + (size_t)row * p.ldc + col) = o;
+            } else if constexpr (EPI == EPI_HILO_RELU) {
+              // v = hi + lo exactly (hi = f16(v), lo = f16(v - hi)) for a consumer
+              // GEMM that reads both halves against duplicated weight rows
+              h8 o;
+#pragma unroll
+              for (int e = 0; e < 4; e++) {
+                const float t = fmaxf(v[e], 0.f);
+                const _Float16 hi = (_Float16)t;
+                o[2 * e] = hi;
+                o[2 * e + 1] = (_Float16)(t - (float)hi);
+              }
+              *reinterpret_cast<h8 *>(reinterpret_cast<_Float16 *>(p.C) + (size_t)row * p.ldc + 2 * col) = o;
             } else if constexpr (EPI == EPI_GENERIC) {
 #pragma unroll
               for (int e = 0; e < 4; e++) {
@@ -182,7 +194,12 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f4 (&acc)[TI][TJ], f
               if constexpr (EPI == EPI_F16_RELU) o = fmaxf(o, 0.f);
               if constexpr (EPI == EPI_F32 || EPI == EPI_GENERIC)
                 if (p.add) o += p.add[(size_t)row * p.ldadd + col + e];
-              if (EPI == EPI_F32 || (EPI == EPI_GENERIC && !p.out_f16))
+              if constexpr (EPI == EPI_HILO_RELU) {
+                o = fmaxf(o, 0.f);
+                const _Float16 hi = (_Float16)o;
+                reinterpret_cast<_Float16 *>(p.C)[(size_t)row * p.ldc + 2 * (col + e)] = hi;
+                reinterpret_cast<_Float16 *>(p.C)[(size_t)row * p.ldc + 2 * (col + e) + 1] = (_Float16)(o - (float)hi);
+              } else if (EPI == EPI_F32 || (EPI == EPI_GENERIC && !p.out_f16))
                 reinterpret_cast<float *>(p.C)[(size_t)row * p.ldc + col + e] = o;
               else
                 reinterpret_cast<_Float16 *>(p.C)[(size_t)row * p.ldc + col + e] = (_Float16)o;
@@ -501,6 +518,7 @@ static int launch_cfg(fa_ctx *ctx, const GemmArgs &p, const char *label) {
 
 static int epi_of(const GemmArgs &p) {
   if (p.glu) return EPI_GLU;
+  if (p.hilo) return EPI_HILO_RELU;
   if (!p.out_f16) return (p.act == 0) ? EPI_F32 : EPI_GENERIC;
   if (p.add) return EPI_GENERIC;
   if (p.act == 0) return EPI_F16;
@@ -630,6 +648,7 @@ static int launch_kind(fa_ctx *ctx, const GemmArgs &p, const char *label) {
     case EPI_F16_SILU: return launch_tile<AK, BKND, EPI_F16_SILU>(ctx, p, label);
     case EPI_F16_RELU: return launch_tile<AK, BKND, EPI_F16_RELU>(ctx, p, label);
     case EPI_GLU: return launch_tile<AK, BKND, EPI_GLU>(ctx, p, label);
+    case EPI_HILO_RELU: return launch_tile<AK, BKND, EPI_HILO_RELU>(ctx, p, label);
     default: return launch_tile<AK, BKND, EPI_GENERIC>(ctx, p, label);
   }
 }
@@ -638,6 +657,8 @@ int gemm_mfma(fa_ctx *ctx, const GemmArgs &p, const char *label) {
   if (p.M <= 0 || p.N <= 0) return FA_OK;
   if (p.K % 64 != 0) return set_err(ctx, FA_E_UNSUPPORTED, "%s: K=%d must be a multiple of 64", label, p.K);
   if (p.glu && (p.N % 16 != 0 || !p.out_f16)) return set_err(ctx, FA_E_UNSUPPORTED, "%s: GLU epilogue needs N%%16==0 and f16 out", label);
+  if (p.hilo && (p.glu || p.act != 0 || p.add || p.akind != A_F16 || p.bkind != B_F16))
+    return set_err(ctx, FA_E_UNSUPPORTED, "%s: hi/lo epilogue is the f16 x f16 route's ReLU output only", label);
   if (p.akind == A_F16) {
     if (p.bkind == B_F16) return launch_kind<A_F16, B_F16>(ctx, p, label);
     if (p.bkind == B_I8) return launch_kind<A_F16, B_I8>(ctx, p, label);
