@@ -177,6 +177,241 @@ __global__ __launch_bounds__(256) void relpos_attn_kernel(AttnArgs a) {
   }
 }
 
+// ── f16 encoder attention: LDS-staged, direct-to-LDS copies ────────────────
+// Same math as relpos_attn_kernel, for the fused encoder's f16 q|k|v buffer.
+// Per 64-key block the workgroup copies its K tile [64][128], the
+// transposed V tile [128 d][64 keys] (from v_transpose_kernel's buffer) and
+// the union of its four waves' positional bands [128 rows][128] into LDS with
+// global_load_lds_dwordx4, two blocks in flight; every MFMA operand is then a
+// 16-byte LDS read.  Rows are XOR-swizzled in 16-byte chunks (chunk ^ (row & 7))
+// so the 8 rows one ds_read_b128 phase touches hit distinct banks.
+
+// Vt[w][h][d][Tp] = V[off_w + t][h*HD + d] for t < T_w, 0 for T_w <= t < Tp.
+__global__ __launch_bounds__(256) void v_transpose_kernel(const _Float16 *__restrict__ v, int ldv, WinTable win, int H, int Tp,
+                                                          _Float16 *__restrict__ vt) {
+  constexpr int HD = 128, TS = 64;
+  __shared__ _Float16 tile[TS][HD + 8];
+  const int t0 = blockIdx.x * TS, h = blockIdx.y, w = blockIdx.z, tid = threadIdx.x;
+  if (t0 >= Tp) return;
+  const int T = win.len[w];
+  const _Float16 *src = v + (size_t)win.off[w] * ldv + h * HD;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {  // 64 rows x 16 chunks of 8 halfs
+    const int idx = tid + c * 256, r = idx >> 4, ch = idx & 15;
+    h8 x = h8{0, 0, 0, 0, 0, 0, 0, 0};
+    if (t0 + r < T) x = *reinterpret_cast<const h8 *>(src + (size_t)(t0 + r) * ldv + ch * 8);
+    *reinterpret_cast<h8 *>(&tile[r][ch * 8]) = x;
+  }
+  __syncthreads();
+  _Float16 *dst = vt + ((size_t)(w * H + h) * HD) * Tp + t0;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {  // 128 d rows x 8 chunks of 8 keys
+    const int idx = tid + c * 256, d = idx >> 3, ch = idx & 7;
+    h8 x;
+#pragma unroll
+    for (int e = 0; e < 8; e++) x[e] = tile[ch * 8 + e][d];
+    *reinterpret_cast<h8 *>(dst + (size_t)d * Tp + ch * 8) = x;
+  }
+}
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// global -> LDS, 16 B per lane (lane i lands at lds_addr + 16 i); M0 carries the
+// wave-uniform LDS address.  Completion is tracked with explicit vmcnt waits.
+__device__ __forceinline__ void attn_dma16(const void *g, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_addr) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__global__ __launch_bounds__(256) void relpos_attn_lds_kernel(AttnArgs a, const _Float16 *__restrict__ vt, int Tp) {
+  constexpr int HD = 128, QB = 64, KB = 64, SW = 80 + 4, PBS = KB + 8;
+  constexpr int KBYTES = KB * 256, VBYTES = HD * 128, PROWS = 128, PBYTES = PROWS * 256;
+  constexpr int STG = KBYTES + VBYTES + PBYTES;  // 64 KB
+  __shared__ __attribute__((aligned(1024))) char st0[STG];
+  __shared__ __attribute__((aligned(1024))) char st1[STG];
+  __shared__ float sStrip[4][16 * SW];
+  __shared__ __attribute__((aligned(16))) _Float16 sP[4][16 * PBS];
+
+  const int w = blockIdx.z, h = blockIdx.y, q0 = blockIdx.x * QB;
+  const int T = a.win.len[w], off = a.win.off[w];
+  if (q0 >= T) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, c16 = lane & 15;
+  const int i0 = q0 + wave * 16;
+  const _Float16 *Q = reinterpret_cast<const _Float16 *>(a.q) + (size_t)off * a.ldq + h * HD;
+  const _Float16 *Kp = reinterpret_cast<const _Float16 *>(a.k) + (size_t)off * a.ldk + h * HD;
+  const _Float16 *Pp = reinterpret_cast<const _Float16 *>(a.pos) + h * HD;
+  const _Float16 *Vt = vt + ((size_t)(w * a.H + h) * HD) * Tp;
+  const uint32_t sadr[2] = {(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)st0),
+                            (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)st1)};
+  const int pbase0 = a.pcenter - (q0 + QB - 1);  // band table row of local row 0 for key block 0
+
+  // 64 copies per key block, 16 per wave: K (16: 4 rows of 256 B each),
+  // Vt (16: 8 rows of 128 B), band (32: 4 rows of 256 B).
+  auto issue = [&](int sidx, int j0) {
+    const uint32_t base = sadr[sidx];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const int ins = wave + i * 4;  // 0..63
+      const void *src;
+      if (ins < 16) {
+        const int r = ins * 4 + (lane >> 4), ch = (lane & 15) ^ (r & 7);
+        src = Kp + (size_t)min(j0 + r, T - 1) * a.ldk + ch * 8;
+      } else if (ins < 32) {
+        const int r = (ins - 16) * 8 + (lane >> 3), ch = (lane & 7) ^ (r & 7);
+        src = Vt + (size_t)r * Tp + j0 + ch * 8;
+      } else {
+        const int r = (ins - 32) * 4 + (lane >> 4), ch = (lane & 15) ^ (r & 7);
+        const int pr = min(max(pbase0 + j0 + r, 0), a.prows - 1);
+        src = Pp + (size_t)pr * a.ldp + ch * 8;
+      }
+      attn_dma16(src, base + ins * 1024);
+    }
+  };
+
+  // A operands: (q+u) and (q+v) for row i0 + c16, d = s*32 + g*8 .. +8
+  h8 qu[4], qv[4];
+  {
+    const int qi = min(i0 + c16, T - 1);
+    const _Float16 *qr = Q + (size_t)qi * a.ldq;
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      const int d = s * 32 + g * 8;
+      const h8 x = *reinterpret_cast<const h8 *>(qr + d);
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float xv = (float)x[e];
+        qu[s][e] = (_Float16)(xv + a.pbu[h * HD + d + e]);
+        qv[s][e] = (_Float16)(xv + a.pbv[h * HD + d + e]);
+      }
+    }
+  }
+  issue(0, 0);
+
+  f4 o[8];
+#pragma unroll
+  for (int t = 0; t < 8; t++) o[t] = f4{0.f, 0.f, 0.f, 0.f};
+  float mrow[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY}, lrow[4] = {0.f, 0.f, 0.f, 0.f};
+  float *strip = sStrip[wave];
+  _Float16 *pb = sP[wave];
+  const int lb = QB - 16 - wave * 16;  // first band row of this wave within the block's band
+
+  const int nkb = (T + KB - 1) / KB;
+  for (int kb = 0; kb < nkb; kb++) {
+    const int j0 = kb * KB, cur = kb & 1;
+    __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8));  // vmcnt(0): this block's copies landed
+    __syncthreads();                                               // ... for every wave; previous block's reads done
+    if (kb + 1 < nkb) issue(cur ^ 1, j0 + KB);
+    const char *Ks = cur ? st1 : st0, *Vs = Ks + KBYTES, *Ps = Ks + KBYTES + VBYTES;
+
+    // content scores (q+u)·kᵀ : 4 tiles of 16 keys
+    f4 sc[4];
+#pragma unroll
+    for (int jt = 0; jt < 4; jt++) {
+      sc[jt] = f4{0.f, 0.f, 0.f, 0.f};
+      const int r = jt * 16 + c16;
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        const h8 kf = *reinterpret_cast<const h8 *>(Ks + r * 256 + (((s * 4 + g) ^ (r & 7)) * 16));
+        sc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qu[s], kf, sc[jt], 0, 0, 0);
+      }
+    }
+    // positional band (q+v)·Pᵀ over this wave's 80 band rows
+#pragma unroll
+    for (int ct = 0; ct < 5; ct++) {
+      f4 bd = f4{0.f, 0.f, 0.f, 0.f};
+      const int r = lb + ct * 16 + c16;
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        const h8 pf = *reinterpret_cast<const h8 *>(Ps + r * 256 + (((s * 4 + g) ^ (r & 7)) * 16));
+        bd = __builtin_amdgcn_mfma_f32_16x16x32_f16(qv[s], pf, bd, 0, 0, 0);
+      }
+#pragma unroll
+      for (int rr = 0; rr < 4; rr++) strip[(g * 4 + rr) * SW + ct * 16 + c16] = bd[rr];
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): strip writes done (wave-private strip)
+    __builtin_amdgcn_wave_barrier();
+    // S = ac + band[i][j - j0 + 15 - (i - i0)], mask keys >= T, online softmax
+    float mnew[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int ri = g * 4 + r;
+      float mx = mrow[r];
+#pragma unroll
+      for (int jt = 0; jt < 4; jt++) {
+        const int jj = jt * 16 + c16;
+        float v = sc[jt][r] + strip[ri * SW + jj + 15 - ri];
+        v = (j0 + jj < T) ? v : -INFINITY;
+        sc[jt][r] = v;
+        mx = fmaxf(mx, v);
+      }
+#pragma unroll
+      for (int o2 = 1; o2 < 16; o2 <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o2, 64));
+      mnew[r] = mx;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const float corr = __expf(mrow[r] - mnew[r]);
+      float ls = 0.f;
+#pragma unroll
+      for (int jt = 0; jt < 4; jt++) {
+        const float pv = __expf(sc[jt][r] - mnew[r]);
+        ls += pv;
+        pb[(g * 4 + r) * PBS + jt * 16 + c16] = (_Float16)pv;
+      }
+#pragma unroll
+      for (int o2 = 1; o2 < 16; o2 <<= 1) ls += __shfl_xor(ls, o2, 64);
+      lrow[r] = lrow[r] * corr + ls;
+      mrow[r] = mnew[r];
+#pragma unroll
+      for (int t = 0; t < 8; t++) o[t][r] *= corr;
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    // O += P·V  (B operand: Vt rows d, keys kk*32 + g*8 .. +8)
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++) {
+      const h8 pa = *reinterpret_cast<const h8 *>(&pb[c16 * PBS + kk * 32 + g * 8]);
+#pragma unroll
+      for (int t = 0; t < 8; t++) {
+        const int d = t * 16 + c16;
+        const h8 vb = *reinterpret_cast<const h8 *>(Vs + d * 128 + (((kk * 4 + g) ^ (d & 7)) * 16));
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[t], 0, 0, 0);
+      }
+    }
+  }
+
+  _Float16 *O = reinterpret_cast<_Float16 *>(a.out) + (size_t)off * a.ldo + h * HD;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int i = i0 + g * 4 + r;
+    if (i >= T) continue;
+    const float inv = 1.f / lrow[r];
+#pragma unroll
+    for (int t = 0; t < 8; t++) O[(size_t)i * a.ldo + t * 16 + c16] = (_Float16)(o[t][r] * inv);
+  }
+}
+
+int relpos_attention_f16(fa_ctx *ctx, const AttnArgs &a, int Tmax, _Float16 *vt, const char *label) {
+  const int W = a.win.n;
+  if (a.HD != 128) return set_err(ctx, FA_E_UNSUPPORTED, "%s: head dim %d (kernel is specialised for 128)", label, a.HD);
+  if (Tmax <= 0 || W <= 0) return FA_OK;
+  if (W > kMaxWin) return set_err(ctx, FA_E_INVALID, "%s: %d windows in one launch (max %d)", label, W, kMaxWin);
+  for (int i = 0; i < W; i++)
+    if (a.win.len[i] > Tmax || a.pcenter - (a.win.len[i] - 1) < 0 || a.pcenter + a.win.len[i] - 1 >= a.prows)
+      return set_err(ctx, FA_E_INVALID, "%s: window %d length %d outside the positional table", label, i, a.win.len[i]);
+  const int Tp = (Tmax + 63) / 64 * 64;
+  {
+    ProfScope ps(ctx, "v_transpose");
+    FA_LAUNCH(ps, v_transpose_kernel, dim3(Tp / 64, a.H, W), dim3(256), 0, ctx->stream, reinterpret_cast<const _Float16 *>(a.v), a.ldv, a.win, a.H,
+              Tp, vt);
+    FA_TRY(check_launch(ctx, "v_transpose"));
+  }
+  ProfScope ps(ctx, label);
+  FA_LAUNCH(ps, relpos_attn_lds_kernel, dim3(cdiv(Tmax, 64), a.H, W), dim3(256), 0, ctx->stream, a, (const _Float16 *)vt, Tp);
+  return check_launch(ctx, label);
+}
+
 int relpos_attention(fa_ctx *ctx, const AttnArgs &a, int in_f32, int out_f32, int Tmax, const char *label) {
   const int W = a.win.n;
   if (a.HD != 128) return set_err(ctx, FA_E_UNSUPPORTED, "%s: head dim %d (kernel is specialised for 128)", label, a.HD);

@@ -320,8 +320,8 @@ struct fa_encoder {
   };
   std::vector<Layer> L;
   // workspace (grow-only)
-  void *s2 = nullptr, *s2p = nullptr, *s3 = nullptr, *s3p = nullptr, *h = nullptr, *u = nullptr, *a = nullptr, *g = nullptr;
-  size_t cap_s2 = 0, cap_s2p = 0, cap_s3 = 0, cap_s3p = 0, cap_m = 0, cap_u = 0;
+  void *vt = nullptr, *s2 = nullptr, *s2p = nullptr, *s3 = nullptr, *s3p = nullptr, *h = nullptr, *u = nullptr, *a = nullptr, *g = nullptr;
+  size_t cap_vt = 0, cap_s2 = 0, cap_s2p = 0, cap_s3 = 0, cap_s3p = 0, cap_m = 0, cap_u = 0;
 };
 
 namespace fa {
@@ -499,7 +499,7 @@ void fa_encoder_destroy(fa_encoder *enc) {
   if (!enc) return;
   (void)hipStreamSynchronize(enc->ctx->stream);
   for (void *p : enc->allocs) (void)hipFree(p);
-  for (void *p : {enc->s2, enc->s2p, enc->s3, enc->s3p, enc->h, enc->u, enc->a, enc->g})
+  for (void *p : {enc->vt, enc->s2, enc->s2p, enc->s3, enc->s3p, enc->h, enc->u, enc->a, enc->g})
     if (p) (void)hipFree(p);
   delete enc;
 }
@@ -826,6 +826,7 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
     e->cap_m = need_m;
   }
   FA_TRY(grow(e, &e->u, &e->cap_u, need_u));
+  FA_TRY(grow(e, &e->vt, &e->cap_vt, (size_t)n * c.H * c.HD * ((mx[3] + 63) / 64 * 64) * 2));  // transposed V per (window, head)
   fa_tensor ox;
   TensorRec *rx;
   FA_TRY(new_tensor(ctx, M, D, S_F32, (size_t)M * D * 4, &ox, &rx));
@@ -903,7 +904,7 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
     at.pos = Ly.P;
     at.pbu = Ly.pbu;
     at.pbv = Ly.pbv;
-    FA_TRY(relpos_attention(ctx, at, 0, 0, mx[3], "attention"));
+    FA_TRY(relpos_attention_f16(ctx, at, mx[3], (_Float16 *)e->vt, "attention"));
     FA_TRY(gemm(a, D, Ly.out, x, D, 0, FA_ACT_NONE, x, 0, "attn_out"));
     // conv module
     FA_TRY(layernorm_launch(ctx, x, Ly.ln[2][0], Ly.ln[2][1], h, 1, M, D, D, D, 1e-5f, "ln_conv"));
