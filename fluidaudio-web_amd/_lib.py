@@ -98,6 +98,8 @@ SIGNATURES = [
     ("fa_window_row_map", I, [P, I32P, I, I, I, I32P, C.POINTER(I)]),
     ("fa_encoder_load", I, [P, C.POINTER(EncoderCfg), I, C.POINTER(C.c_char_p), C.POINTER(F32P), C.POINTER(C.c_int64), I, I, C.POINTER(P)]),
     ("fa_encoder_destroy", None, [P]),
+    ("fa_encoder_set_exact", I, [P, I, I, C.c_uint]),
+    ("fa_encoder_get_exact", I, [P, I]),
     ("fa_encoder_forward", I, [P, P, T, I32P, I, I, I, C.POINTER(T)]),
     ("fa_encoder_tsub", I, [I]),
 ]

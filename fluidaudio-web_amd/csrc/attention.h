@@ -23,6 +23,7 @@ struct AttnArgs {
   int pcenter = 0;            // table row of relative position 0
   const float *pbu = nullptr, *pbv = nullptr;  // [H*HD], 1/sqrt(HD) folded
   void *out = nullptr;        // [rows, ldo]
+  void *out_lo = nullptr;     // f16 route, optional: exact remainder plane f16(o - f16(o)), [rows, ldo]
   int ldo = 0;
   WinTable win;               // window row offsets / lengths (by value: no device table)
   int H = 0, HD = 0;

@@ -382,13 +382,19 @@ __global__ __launch_bounds__(256) void relpos_attn_lds_kernel(AttnArgs a, const 
   }
 
   _Float16 *O = reinterpret_cast<_Float16 *>(a.out) + (size_t)off * a.ldo + h * HD;
+  _Float16 *Olo = a.out_lo ? reinterpret_cast<_Float16 *>(a.out_lo) + (size_t)off * a.ldo + h * HD : nullptr;
 #pragma unroll
   for (int r = 0; r < 4; r++) {
     const int i = i0 + g * 4 + r;
     if (i >= T) continue;
     const float inv = 1.f / lrow[r];
 #pragma unroll
-    for (int t = 0; t < 8; t++) O[(size_t)i * a.ldo + t * 16 + c16] = (_Float16)(o[t][r] * inv);
+    for (int t = 0; t < 8; t++) {
+      const float v = o[t][r] * inv;
+      const _Float16 hi = (_Float16)v;
+      O[(size_t)i * a.ldo + t * 16 + c16] = hi;
+      if (Olo) Olo[(size_t)i * a.ldo + t * 16 + c16] = (_Float16)(v - (float)hi);
+    }
   }
 }
 

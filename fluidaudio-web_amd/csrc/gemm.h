@@ -11,6 +11,7 @@ enum BKind : int { B_F16 = 0, B_I8 = 1, B_I4 = 2 };
 
 struct GemmArgs {
   const void *A = nullptr;  // [M, lda] row-major, f16 or f32
+  const void *Alo = nullptr;  // optional f16 plane [M, lda]: A = A + Alo exactly (f16 x f16 route only)
   int lda = 0;
   int akind = A_F16;
   const void *B = nullptr;  // K-major: f16 [N][K] | int8 [N][K] | int4 [N][K/32][16 B]
@@ -20,6 +21,7 @@ struct GemmArgs {
   const uint8_t *bzp = nullptr;  // int4 zero points, packed [N][zpb] (null: 8)
   int zpb = 0;
   void *C = nullptr;  // [M, ldc], f32 or f16 (out_f16)
+  void *Clo = nullptr;  // EPI f16 outputs only: also write lo = f16(v - f16(v)) here ([M, ldc])
   int ldc = 0;
   int out_f16 = 0;
   const float *colscale = nullptr;  // int8 per-output-column scale

@@ -134,11 +134,23 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f4 (&acc)[TI][TJ], f
         for (int e = 0; e < 4; e++) v[e] = strip[rr * SS + vcol[e]] * cs[e] + bv[e];
         if constexpr (EPI == EPI_GLU) {
           const int ocol = (c0 >> 1) + lc;
-          if (ocol + 3 < (p.N >> 1)) {
+          if (ocol + 3 < (p.N >> 1) && !p.out_f16) {
+            float4 o;
+            o.x = sigmoid_mul(v[0], strip[rr * SS + gcol[0]] * gcs[0] + gbv[0]);
+            o.y = sigmoid_mul(v[1], strip[rr * SS + gcol[1]] * gcs[1] + gbv[1]);
+            o.z = sigmoid_mul(v[2], strip[rr * SS + gcol[2]] * gcs[2] + gbv[2]);
+            o.w = sigmoid_mul(v[3], strip[rr * SS + gcol[3]] * gcs[3] + gbv[3]);
+            *reinterpret_cast<float4 *>(reinterpret_cast<float *>(p.C) + (size_t)row * p.ldc + ocol) = o;
+          } else if (ocol + 3 < (p.N >> 1)) {
             h4 o;
 #pragma unroll
-            for (int e = 0; e < 4; e++) o[e] = (_Float16)sigmoid_mul(v[e], strip[rr * SS + gcol[e]] * gcs[e] + gbv[e]);
+            for (int e = 0; e < 4; e++) {
+              const float t = sigmoid_mul(v[e], strip[rr * SS + gcol[e]] * gcs[e] + gbv[e]);
+              o[e] = (_Float16)t;
+              v[e] = t - (float)o[e];
+            }
             *reinterpret_cast<h4 *>(reinterpret_cast<_Float16 *>(p.C) + (size_t)row * p.ldc + ocol) = o;
+            if (p.Clo) *reinterpret_cast<h4 *>(reinterpret_cast<_Float16 *>(p.Clo) + (size_t)row * p.ldc + ocol) = h4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
           }
         } else {
           const int col = c0 + lc;
@@ -173,15 +185,17 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f4 (&acc)[TI][TJ], f
                   reinterpret_cast<float *>(p.C)[(size_t)row * p.ldc + col + e] = o;
               }
             } else {
-              h4 o;
+              h4 o, ol;
 #pragma unroll
               for (int e = 0; e < 4; e++) {
                 float t = v[e];
                 if constexpr (EPI == EPI_F16_SILU) t = sigmoid_mul(t, t);
                 if constexpr (EPI == EPI_F16_RELU) t = fmaxf(t, 0.f);
                 o[e] = (_Float16)t;
+                ol[e] = (_Float16)(t - (float)o[e]);
               }
               *reinterpret_cast<h4 *>(reinterpret_cast<_Float16 *>(p.C) + (size_t)row * p.ldc + col) = o;
+              if (p.Clo) *reinterpret_cast<h4 *>(reinterpret_cast<_Float16 *>(p.Clo) + (size_t)row * p.ldc + col) = ol;
             }
           } else {
             // ragged right edge (N not a multiple of 4 within this tile)
@@ -326,12 +340,15 @@ struct LdsStage {
   char d[BYTES];
 };
 
-template <int BM, int BN, int WM, int WN, int S, int EPI>
+// LO = 1: A arrives as two f16 planes (A = hi + lo exactly); both are staged
+// and each B fragment feeds two MFMAs, so the product carries f32-accurate A.
+template <int BM, int BN, int WM, int WN, int S, int EPI, int LO = 0>
 __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4))) void gemm_dma_kernel(GemmArgs p) {
   constexpr int NW = WM * WN, BK = 64, RB = 128;
   constexpr int WTM = BM / WM, WTN = BN / WN, TI = WTM / 16, TJ = WTN / 16;
-  constexpr int SA = BM * RB, STG = (BM + BN) * RB;
-  constexpr int IT = (BM + BN) / 8;                   // 1 KB copies per stage (8 rows each)
+  constexpr int AR = BM * (1 + LO);                   // staged A rows: hi (and lo) planes
+  constexpr int SA = AR * RB, STG = (AR + BN) * RB;
+  constexpr int IT = (AR + BN) / 8;                   // 1 KB copies per stage (8 rows each)
   constexpr int IW = (IT + NW - 1) / NW, IMIN = IT / NW;  // per wave: at most / at least
   static_assert(BM % 16 == 0 && BN % 16 == 0 && NW % 4 == 0, "tile shape");
   static_assert(S >= 2 && S <= 4 && S * STG <= 160 * 1024, "LDS stages");
@@ -358,8 +375,10 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
     const int ch = lch ^ (r & 7);
     if (r < BM)
       src[i] = A + (size_t)min(m0 + r, p.M - 1) * p.lda + ch * 8;  // rows past M repeat the last row; never stored
+    else if (r < AR)
+      src[i] = reinterpret_cast<const _Float16 *>(p.Alo) + (size_t)min(m0 + r - BM, p.M - 1) * p.lda + ch * 8;
     else
-      src[i] = B + (size_t)(n0 + r - BM) * p.K + ch * 8;
+      src[i] = B + (size_t)(n0 + r - AR) * p.K + ch * 8;
   }
   auto issue = [&](int sidx, int k0) {
 #pragma unroll
@@ -382,12 +401,16 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
 
   const int q = lane >> 4, sw = lane & 7;  // fragment rows are 16-aligned + (lane & 15)
   const int abase = (wm * WTM + (lane & 15)) * RB, bbase = SA + (wn * WTN + (lane & 15)) * RB;
-  h8 af[2][TI], bf[2][TJ];
+  h8 af[2][TI], bf[2][TJ], al[2][LO ? TI : 1];
   auto rdfrag = [&](int sidx, int ks, int slot) {
     const char *base = stg[sidx];
     const int so = ((ks * 4 + q) ^ sw) * 16;
 #pragma unroll
     for (int i = 0; i < TI; i++) af[slot][i] = *reinterpret_cast<const h8 *>(base + abase + i * 16 * RB + so);
+    if constexpr (LO) {
+#pragma unroll
+      for (int i = 0; i < TI; i++) al[slot][i] = *reinterpret_cast<const h8 *>(base + BM * RB + abase + i * 16 * RB + so);
+    }
 #pragma unroll
     for (int j = 0; j < TJ; j++) bf[slot][j] = *reinterpret_cast<const h8 *>(base + bbase + j * 16 * RB + so);
   };
@@ -395,7 +418,10 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
 #pragma unroll
     for (int i = 0; i < TI; i++)
 #pragma unroll
-      for (int j = 0; j < TJ; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[slot][i], bf[slot][j], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < TJ; j++) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[slot][i], bf[slot][j], acc[i][j], 0, 0, 0);
+        if constexpr (LO) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[slot][i], bf[slot][j], acc[i][j], 0, 0, 0);
+      }
   };
   // K tile kt is in LDS once at most (S-2) later tiles are still in flight
   // (copies complete in issue order), for every wave: then barrier.
@@ -578,21 +604,26 @@ struct DmaCfg {
   float us_round;
 };
 static const DmaCfg kDma[] = {{192, 256, 30.0f}, {192, 128, 18.3f}, {128, 128, 12.6f}, {96, 128, 11.7f}};
+// with a lo plane (two MFMAs per B fragment), same K = 1024 round timing
+static const DmaCfg kDmaLo[] = {{192, 128, 27.7f}, {128, 128, 17.9f}, {96, 128, 16.5f}};
 
 static int pick_dma(fa_ctx *ctx, const GemmArgs &p) {
-  if (p.K % 64 || p.lda % 8 || ((uintptr_t)p.A & 15) || ((uintptr_t)p.B & 15)) return -1;
-  // FA_GEMM_DMA=0 turns the route off; 1..4 pins configuration 0..3 when N fits it.
+  if (p.K % 64 || p.lda % 8 || ((uintptr_t)p.A & 15) || ((uintptr_t)p.B & 15) || ((uintptr_t)p.Alo & 15)) return -1;
+  const DmaCfg *tab = p.Alo ? kDmaLo : kDma;
+  const int ntab = p.Alo ? (int)(sizeof kDmaLo / sizeof kDmaLo[0]) : (int)(sizeof kDma / sizeof kDma[0]);
+  // FA_GEMM_DMA=0 turns the route off (not with a lo plane); 1..n pins
+  // configuration 0..n-1 of the table in use when N fits it.
   if (const char *e = getenv("FA_GEMM_DMA")) {
     const int f = atoi(e);
-    if (f == 0) return -1;
-    if (f >= 1 && f <= (int)(sizeof kDma / sizeof kDma[0]) && p.N % kDma[f - 1].bn == 0) return f - 1;
+    if (f == 0 && !p.Alo) return -1;
+    if (f >= 1 && f <= ntab && p.N % tab[f - 1].bn == 0) return f - 1;
   }
   int best = -1;
   double bestc = 1e300;
-  for (int i = 0; i < (int)(sizeof kDma / sizeof kDma[0]); i++) {
-    if (p.N % kDma[i].bn) continue;
-    const long tiles = (long)cdiv(p.M, kDma[i].bm) * (p.N / kDma[i].bn);
-    const double c = (double)cdiv(tiles, ctx->num_cu) * kDma[i].us_round;
+  for (int i = 0; i < ntab; i++) {
+    if (p.N % tab[i].bn) continue;
+    const long tiles = (long)cdiv(p.M, tab[i].bm) * (p.N / tab[i].bn);
+    const double c = (double)cdiv(tiles, ctx->num_cu) * tab[i].us_round;
     if (c < bestc * 0.999) {
       bestc = c;
       best = i;
@@ -601,17 +632,25 @@ static int pick_dma(fa_ctx *ctx, const GemmArgs &p) {
   return best;
 }
 
-template <int BM, int BN, int WM, int WN, int S, int EPI>
+template <int BM, int BN, int WM, int WN, int S, int EPI, int LO = 0>
 static int launch_dma(fa_ctx *ctx, const GemmArgs &p, const char *label) {
   const unsigned tiles = cdiv(p.M, BM) * (p.N / BN);
   ProfScope ps(ctx, label);
-  FA_LAUNCH(ps, (gemm_dma_kernel<BM, BN, WM, WN, S, EPI>), dim3(tiles), dim3(64 * WM * WN), 0, ctx->stream, p);
+  FA_LAUNCH(ps, (gemm_dma_kernel<BM, BN, WM, WN, S, EPI, LO>), dim3(tiles), dim3(64 * WM * WN), 0, ctx->stream, p);
   return check_launch(ctx, label);
 }
 
 template <int AK, int BKND, int EPI>
 static int launch_tile(fa_ctx *ctx, const GemmArgs &p, const char *label) {
   if constexpr (AK == A_F16 && BKND == B_F16 && EPI != EPI_GENERIC) {
+    if (p.Alo) {
+      switch (pick_dma(ctx, p)) {
+        case 0: return launch_dma<192, 128, 4, 2, 2, EPI, 1>(ctx, p, label);
+        case 1: return launch_dma<128, 128, 2, 4, 3, EPI, 1>(ctx, p, label);
+        case 2: return launch_dma<96, 128, 2, 4, 3, EPI, 1>(ctx, p, label);
+        default: return set_err(ctx, FA_E_UNSUPPORTED, "%s: lo plane needs N %% 128 == 0, K %% 64 == 0 and 16-byte aligned operands", label);
+      }
+    }
     switch (pick_dma(ctx, p)) {
       case 0: return launch_dma<192, 256, 2, 4, 2, EPI>(ctx, p, label);
       case 1: return launch_dma<192, 128, 4, 2, 3, EPI>(ctx, p, label);
@@ -620,6 +659,7 @@ static int launch_tile(fa_ctx *ctx, const GemmArgs &p, const char *label) {
       default: break;
     }
   }
+  if (p.Alo) return set_err(ctx, FA_E_UNSUPPORTED, "%s: lo plane needs the f16 x f16 route", label);
   if constexpr (AK == A_F32 || EPI == EPI_GENERIC) {  // ComputeContext path: mid-size tiles
     const long t128 = (long)cdiv(p.M, 128) * cdiv(p.N, 128);
     if (t128 >= ctx->num_cu) return launch_cfg<128, 128, 2, 2, AK, BKND, EPI>(ctx, p, label);
@@ -656,7 +696,9 @@ static int launch_kind(fa_ctx *ctx, const GemmArgs &p, const char *label) {
 int gemm_mfma(fa_ctx *ctx, const GemmArgs &p, const char *label) {
   if (p.M <= 0 || p.N <= 0) return FA_OK;
   if (p.K % 64 != 0) return set_err(ctx, FA_E_UNSUPPORTED, "%s: K=%d must be a multiple of 64", label, p.K);
-  if (p.glu && (p.N % 16 != 0 || !p.out_f16)) return set_err(ctx, FA_E_UNSUPPORTED, "%s: GLU epilogue needs N%%16==0 and f16 out", label);
+  if (p.glu && p.N % 16 != 0) return set_err(ctx, FA_E_UNSUPPORTED, "%s: GLU epilogue needs N%%16==0", label);
+  if ((p.Alo || p.Clo) && (p.akind != A_F16 || p.bkind != B_F16 || (p.Clo && !p.out_f16)))
+    return set_err(ctx, FA_E_UNSUPPORTED, "%s: hi/lo planes are for the f16 x f16 route with f16 output", label);
   if (p.hilo && (p.glu || p.act != 0 || p.add || p.akind != A_F16 || p.bkind != B_F16))
     return set_err(ctx, FA_E_UNSUPPORTED, "%s: hi/lo epilogue is the f16 x f16 route's ReLU output only", label);
   if (p.akind == A_F16) {

@@ -198,6 +198,18 @@ class FusedEncoder:
         check(ctx._p, lib().fa_encoder_load(ctx._p, C.byref(c), len(names), arr_names, arr_data, arr_cnt, FORMATS[fmt], max_T, C.byref(p)))
         self._p = p
 
+    # operand-precision bits (fa_encoder_set_exact)
+    EXACT = dict(ln_out=1, ff_hidden=2, attn_out=4, glu=8, dw_out=16)
+
+    def setExact(self, mask: int, first: int = 0, last: int | None = None):
+        """Carry the masked operands of layers [first, last] as exact f16 pairs
+        (0 = plain f16 operands everywhere)."""
+        last = self.cfg["layers"] - 1 if last is None else last
+        check(self.ctx._p, lib().fa_encoder_set_exact(self._p, first, last, int(mask)))
+
+    def exact(self, layer: int) -> int:
+        return int(lib().fa_encoder_get_exact(self._p, layer))
+
     def close(self):
         if getattr(self, "_p", None):
             lib().fa_encoder_destroy(self._p)

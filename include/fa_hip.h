@@ -220,6 +220,24 @@ int fa_encoder_load(fa_ctx *ctx, const fa_encoder_cfg *cfg, int n, const char *c
                     int format, int max_T, fa_encoder **out);
 void fa_encoder_destroy(fa_encoder *enc);
 
+/* Operand precision per conformer layer.  The f16 route rounds five kinds of
+ * GEMM/conv operands to f16; each bit below instead carries that operand as
+ * an exact f16 pair (hi = f16(v), lo = f16(v - hi)) feeding two MFMAs per
+ * weight fragment, or (FA_EXACT_GLU) keeps it f32.  No counterpart in the
+ * reference (its f16 route keeps f16 partial sums, gemm.js:380-391); this is
+ * how the f16 encoder holds the fp32 path's frame-wise decisions.  Masks other
+ * than FA_EXACT_GLU need the f16 weight format.  Layers [first, last] get `mask`. */
+enum fa_exact_bits {
+  FA_EXACT_LN_OUT = 1,    /* LayerNorm outputs -> FF W1, q|k|v, pw1 */
+  FA_EXACT_FF_HIDDEN = 2, /* FF hidden (after SiLU) -> FF W2 */
+  FA_EXACT_ATTN_OUT = 4,  /* attention output -> out-projection */
+  FA_EXACT_GLU = 8,       /* GLU output -> depthwise conv (f32) */
+  FA_EXACT_DW_OUT = 16    /* depthwise conv output -> pw2 */
+};
+int fa_encoder_set_exact(fa_encoder *enc, int first_layer, int last_layer, unsigned mask);
+/* Current mask of one layer (or -1 for an invalid layer). */
+int fa_encoder_get_exact(const fa_encoder *enc, int layer);
+
 /* Encode a batch of windows.  mel: [Σ len_i, melBins] (layout 0) or
  * [n*Tmax, melBins] (layout 1) time-major f32 rows as fa_pack_windows makes
  * them; lens: host mel-frame lengths.  out receives [Σ Tsub_i, D] (layout 0)

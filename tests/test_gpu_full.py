@@ -14,23 +14,81 @@ def full_weights(fa):
     return fa.synth.make_weights(FULL, seed=1)
 
 
-def test_config3_fused_f16_vs_fp32_path(ctx, fa, full_weights):
-    mels = fa.synth.make_features(128, 1500, seed=1, W=16)
-    enc = fa.FusedEncoder(ctx, full_weights, "f16", max_T=188)
-    got = np.concatenate(enc.encode(mels))
-    enc.close()
-    ref32 = fa.loadParakeetEncoder(ctx, full_weights, weights="f32")
+def _ref_path(ctx, fa, ref32, mels):
     a = ctx.pushArena()
     y, T = fa.parakeetEncodeBatch(ctx, ref32, mels)
     ref = ctx.download(y).reshape(-1, FULL["D"])
     ctx.popArena(a)
-    assert got.shape == ref.shape == (16 * 188, 1024)
-    rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    return ref
+
+
+def test_config3_fused_f16_vs_fp32_path(ctx, fa, full_weights):
+    """north_star bar at configs[2]: rel-L2 <= 1e-2 per batch, and frame-wise
+    argmax of R [1024, 64] ~ N(0,1) (seed 2) identical on >= 99.9 % of frames.
+    The disagreement rate is a property of the f16 path (~0.07 % with the
+    default operand precision); one batch of 3008 frames would estimate it
+    with +-0.05 % noise, so it is measured over 8 batches (24,064 frames,
+    feature seeds 1..8)."""
+    enc = fa.FusedEncoder(ctx, full_weights, "f16", max_T=188)
+    ref32 = fa.loadParakeetEncoder(ctx, full_weights, weights="f32")
     R = np.random.default_rng(2).standard_normal((1024, 64)).astype(np.float32)
-    agree = np.mean(np.argmax(got @ R, 1) == np.argmax(ref @ R, 1))
-    print(f"configs[2]: rel-L2 {rel:.3e}, projected argmax agreement {agree:.5f}")
-    assert rel <= 1e-2
+    flips = frames = 0
+    for seed in range(1, 9):
+        mels = fa.synth.make_features(128, 1500, seed=seed, W=16)
+        got = np.concatenate(enc.encode(mels))
+        ref = _ref_path(ctx, fa, ref32, mels)
+        assert got.shape == ref.shape == (16 * 188, 1024)
+        rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+        f = int(np.sum(np.argmax(got @ R, 1) != np.argmax(ref @ R, 1)))
+        print(f"configs[2] seed {seed}: rel-L2 {rel:.3e}, argmax disagreements {f}/{len(got)}")
+        assert rel <= 1e-2
+        flips += f
+        frames += len(got)
+    enc.close()
+    agree = 1.0 - flips / frames
+    print(f"configs[2]: projected argmax agreement {agree:.5f} over {frames} frames")
     assert agree >= 0.999
+
+
+def test_exact_operands_track_fp32_path(ctx, fa, full_weights):
+    """Every operand carried as an exact f16 pair (fa_encoder_set_exact with all
+    bits, all layers): the f16 route then differs from the fp32 path only by
+    f32 accumulation order and f16 attention internals -> rel-L2 well under
+    1e-4 at full width (4 layers, 4 windows); plain f16 operands are ~10x
+    further away.  Pins the two-plane GEMM, LayerNorm, attention and
+    depthwise-conv paths against the fp32 reference."""
+    lw = {k: v for k, v in full_weights.items() if not (k.startswith("L") and int(k[1:k.index("_")]) >= 4)}
+    mels = fa.synth.make_features(128, 1500, seed=3, W=4)
+    enc = fa.FusedEncoder(ctx, lw, "f16", max_T=188)
+    ref = _ref_path(ctx, fa, fa.loadParakeetEncoder(ctx, lw, weights="f32"), mels)
+    enc.setExact(31)
+    assert all(enc.exact(l) == 31 for l in range(4))
+    exact = np.concatenate(enc.encode(mels))
+    enc.setExact(0)
+    plain = np.concatenate(enc.encode(mels))
+    enc.close()
+    r_exact = np.linalg.norm(exact - ref) / np.linalg.norm(ref)
+    r_plain = np.linalg.norm(plain - ref) / np.linalg.norm(ref)
+    print(f"4 layers: rel-L2 exact operands {r_exact:.2e}, plain f16 {r_plain:.2e}")
+    assert r_exact < 5e-5
+    assert r_plain > 3 * r_exact
+
+
+def test_set_exact_validation(ctx, fa, full_weights):
+    lw = {k: v for k, v in full_weights.items() if not (k.startswith("L") and int(k[1:k.index("_")]) >= 2)}
+    enc = fa.FusedEncoder(ctx, lw, "f16", max_T=64)
+    assert enc.exact(1) == 31 and enc.exact(5) == -1  # default tail covers both layers of a 2-layer model
+    with pytest.raises(fa.FaError):
+        enc.setExact(64)
+    with pytest.raises(fa.FaError):
+        enc.setExact(1, 1, 5)
+    enc.close()
+    q = fa.FusedEncoder(ctx, lw, "int8", max_T=64)
+    assert q.exact(0) == 0
+    with pytest.raises(fa.FaError):
+        q.setExact(1)
+    q.setExact(8)  # f32 GLU output needs no f16 weights
+    q.close()
 
 
 def test_config4_ragged_batch_equals_standalone(ctx, fa, full_weights):
