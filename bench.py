@@ -55,24 +55,28 @@ def kernel_work(cfg, lens, layout):
     T3 = [s2(t) for t in T2]
     R0, R1, R2, M = sum(lens), sum(T1), sum(T2), sum(T3)
     att = sum(2 * t * t * D * 3 for t in T3)  # (q+u)kᵀ, bd (t x t band entries used), P·V
-    return {
+    gemm = {"ff1_w1": 2 * M * D * DFF, "ff1_w2": 2 * M * D * DFF, "ff2_w1": 2 * M * D * DFF, "ff2_w2": 2 * M * D * DFF,
+            "qkv": 2 * M * D * 3 * D, "attn_out": 2 * M * D * D, "pw1_glu": 2 * M * D * 2 * D, "pw2": 2 * M * D * D}
+    w = {
         "pack_windows": ("byte", R0 * MB * 8),
-        "sub_c0": ("byte", R0 * MB * 4 + R1 * (MB // 2) * C * 2),
-        "sub_dw1": ("byte", R1 * (MB // 2) * C * 2 + R2 * (MB // 4) * C * 2),
+        "sub_c01": ("byte", R0 * MB * 4 + R2 * (MB // 4) * C * 2 * 2),  # mel in, hi/lo pairs out
         "sub_pw2": ("flop", 2 * R2 * (MB // 4) * C * C),
-        "sub_dw3": ("byte", R2 * (MB // 4) * C * 2 + M * F * C * 2),
+        "sub_dw3": ("byte", R2 * (MB // 4) * C * 4 + M * F * C * 2 * 2),  # f32 in, hi/lo pairs out
         "sub_pw4": ("flop", 2 * M * F * C * C),
         "sub_linear": ("flop", 2 * M * F * C * D),
-        "ln_ff1": ("byte", M * D * 6), "ln_att": ("byte", M * D * 6), "ln_conv": ("byte", M * D * 6), "ln_ff2": ("byte", M * D * 6),
         "ln_out": ("byte", M * D * 8),
-        "ff1_w1": ("flop", 2 * M * D * DFF), "ff1_w2": ("flop", 2 * M * D * DFF),
-        "ff2_w1": ("flop", 2 * M * D * DFF), "ff2_w2": ("flop", 2 * M * D * DFF),
-        "qkv": ("flop", 2 * M * D * 3 * D), "attn_out": ("flop", 2 * M * D * D),
-        "pw1_glu": ("flop", 2 * M * D * 2 * D), "pw2": ("flop", 2 * M * D * D),
-        "attention": ("flop", att),
-        "dwconv": ("byte", M * D * 4),
+        "v_transpose": ("byte", M * D * 2 * 2),
+        "attention": ("flop", att), "attention_x": ("flop", att),
+        "dwconv": ("byte", M * D * 4), "dwconv_f32": ("byte", M * D * 6), "dwconv_lo": ("byte", M * D * 6), "dwconv_x": ("byte", M * D * 8),
         "zero_pad": ("byte", 0),
     }
+    for ln in ("ln_ff1", "ln_att", "ln_conv", "ln_ff2"):
+        w[ln] = ("byte", M * D * 6)       # f32 in, f16 out
+        w[ln + "_x"] = ("byte", M * D * 8)  # f32 in, f16 hi + lo planes out
+    for k, f in gemm.items():  # algorithmic flops: a lo plane (_x) or a lo output (_u, _f32) does not add any
+        for suf in ("", "_x", "_u", "_f32"):
+            w[k + suf] = ("flop", f)
+    return w
 
 
 def summarize(prof, work, steps):
@@ -168,7 +172,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="encoder", choices=["encoder", "layer", "ragged", "quant", "gemv"])
+    ap.add_argument("--workload", default="encoder", choices=["encoder", "layer", "ragged", "quant", "gemv", "copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -178,6 +182,8 @@ def main():
     ctx = fa.createContext("hip")
     if args.workload == "gemv":
         return bench_gemv(args, fa, ctx)
+    if args.workload == "copy":
+        return bench_copy(args, fa, ctx)
     cfg = dict(FULL)
     layout = "packed"
     if args.workload in ("encoder", "quant"):
@@ -199,7 +205,7 @@ def main():
     audio_s = sum(lens) * 0.01 * args.steps
     work = kernel_work(cfg, lens, layout)
     kern = summarize(prof_all, work, 2)
-    gemm_labels = [k for k, v in kern.items() if v.get("bound") == "mfma" and k != "attention"]
+    gemm_labels = [k for k, v in kern.items() if v.get("bound") == "mfma" and not k.startswith("attention")]
     gemm_ms = sum(kern[k]["total_ms_per_step"] for k in gemm_labels)
     gemm_flop = sum(work[k][1] * kern[k]["launches"] / 2 for k in gemm_labels)
     gemm_tf = gemm_flop / (gemm_ms * 1e-3) / 1e12 if gemm_ms else 0.0
@@ -227,6 +233,26 @@ def main():
         log("[bench] CPU baseline (oracle, 1 core, bounded sample)")
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res), flush=True)
+
+
+def bench_copy(args, fa, ctx):
+    """Calibration for the rocprofv3 FETCH_SIZE / WRITE_SIZE counters: a plain
+    device-to-device copy of a known 256 MiB (copyRows -> the runtime's copy
+    kernel), so counter KiB per dispatch can be scaled to bytes moved."""
+    rows, cols = 65536, 1024  # 256 MiB of f32
+    src = ctx.upload(np.ones((rows, cols), np.float32), rows, cols)
+    dst = ctx.alloc(rows, cols)
+    for _ in range(args.warmup):
+        ctx.copyRows(dst, src, 0)
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ctx.copyRows(dst, src, 0)
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    nbytes = rows * cols * 4
+    print(json.dumps({"metric": "copy GB/s (counter calibration)", "value": round(2 * nbytes * args.steps / wall / 1e9, 1), "unit": "GB/s",
+                      "bytes_read_per_launch": nbytes, "bytes_written_per_launch": nbytes, "steps": args.steps}), flush=True)
 
 
 def bench_gemv(args, fa, ctx):

@@ -131,9 +131,7 @@ __global__ __launch_bounds__(256) void relpos_attn_kernel(AttnArgs a) {
         sc[jt][r] = v;
         mx = fmaxf(mx, v);
       }
-#pragma unroll
-      for (int o2 = 1; o2 < 16; o2 <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o2, 64));
-      mnew[r] = mx;
+      mnew[r] = row16_max(mx);
     }
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -145,9 +143,7 @@ __global__ __launch_bounds__(256) void relpos_attn_kernel(AttnArgs a) {
         ls += pv;
         pb[(g * 4 + r) * PBS + jt * 16 + c16] = (_Float16)pv;
       }
-#pragma unroll
-      for (int o2 = 1; o2 < 16; o2 <<= 1) ls += __shfl_xor(ls, o2, 64);
-      lrow[r] = lrow[r] * corr + ls;
+      lrow[r] = lrow[r] * corr + row16_sum(ls);
       mrow[r] = mnew[r];
 #pragma unroll
       for (int t = 0; t < 8; t++) o[t][r] *= corr;
@@ -345,9 +341,7 @@ __global__ __launch_bounds__(256) void relpos_attn_lds_kernel(AttnArgs a, const 
         sc[jt][r] = v;
         mx = fmaxf(mx, v);
       }
-#pragma unroll
-      for (int o2 = 1; o2 < 16; o2 <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o2, 64));
-      mnew[r] = mx;
+      mnew[r] = row16_max(mx);
     }
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -359,9 +353,7 @@ __global__ __launch_bounds__(256) void relpos_attn_lds_kernel(AttnArgs a, const 
         ls += pv;
         pb[(g * 4 + r) * PBS + jt * 16 + c16] = (_Float16)pv;
       }
-#pragma unroll
-      for (int o2 = 1; o2 < 16; o2 <<= 1) ls += __shfl_xor(ls, o2, 64);
-      lrow[r] = lrow[r] * corr + ls;
+      lrow[r] = lrow[r] * corr + row16_sum(ls);
       mrow[r] = mnew[r];
 #pragma unroll
       for (int t = 0; t < 8; t++) o[t][r] *= corr;

@@ -269,14 +269,47 @@ __global__ __launch_bounds__(256) void enc_ln_kernel(const float *__restrict__ x
   }
 }
 
+// The layer's closing LayerNorm (norm_out) in place on the f32 residual
+// stream, D = 256 * V (one wavefront per row, float4 loads and stores).
+template <int V>
+__global__ __launch_bounds__(256) void enc_ln_f32_kernel(float *__restrict__ x, const float *__restrict__ gamma, const float *__restrict__ beta, int rows,
+                                                         float eps) {
+  constexpr int D = 256 * V;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  float4 *xr = reinterpret_cast<float4 *>(x + (size_t)row * D);
+  float4 v[V];
+  float s = 0.f;
+#pragma unroll
+  for (int t = 0; t < V; t++) {
+    v[t] = xr[lane + 64 * t];
+    s += v[t].x + v[t].y + v[t].z + v[t].w;
+  }
+  const float mean = wave_sum(s) * (1.f / D);
+  float q = 0.f;
+#pragma unroll
+  for (int t = 0; t < V; t++) {
+    const float a = v[t].x - mean, b = v[t].y - mean, c = v[t].z - mean, d = v[t].w - mean;
+    q += a * a + b * b + c * c + d * d;
+  }
+  const float inv = rsqrtf(wave_sum(q) * (1.f / D) + eps);
+#pragma unroll
+  for (int t = 0; t < V; t++) {
+    const int j = lane + 64 * t;
+    const float4 gm = reinterpret_cast<const float4 *>(gamma)[j], bt = reinterpret_cast<const float4 *>(beta)[j];
+    xr[j] = make_float4((v[t].x - mean) * inv * gm.x + bt.x, (v[t].y - mean) * inv * gm.y + bt.y, (v[t].z - mean) * inv * gm.z + bt.z,
+                        (v[t].w - mean) * inv * gm.w + bt.w);
+  }
+}
+
 // Conv module depthwise conv over time, k taps, symmetric pad (k-1)/2,
 // + bias (BatchNorm folded) + SiLU (raw-encoder.js:365-367), per window.
 // Thread = 8 channels x TT consecutive frames; the TT+k-1 input rows are
-// loaded once into registers.
+// loaded once into registers.  One wavefront covers 512 channels.
 // TI = float: the GLU output arrives in f32; ylo (optional) receives the exact
 // f16 remainder of each output for a two-plane GEMM operand.
 template <int KT, int TT, typename TI>
-__global__ __launch_bounds__(128) void dwconv_silu_kernel(const TI *__restrict__ x, _Float16 *__restrict__ y, _Float16 *__restrict__ ylo,
+__global__ __launch_bounds__(64) void dwconv_silu_kernel(const TI *__restrict__ x, _Float16 *__restrict__ y, _Float16 *__restrict__ ylo,
                                                           const float *__restrict__ wt, const float *__restrict__ b, int D, WinStage st) {
   const int win = blockIdx.y;
   const int T = st.len[win];
@@ -1024,39 +1057,45 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
     const void *hl = (ex & FA_EXACT_LN_OUT) ? hlo : nullptr;
     void *ul = (ex & FA_EXACT_FF_HIDDEN) ? ulo : nullptr;
     // FF1
-    FA_TRY(ln(0, Ly, "ln_ff1"));
-    FA_TRY(gemm(h, hl, D, Ly.ff1w1, u, ul, c.DFF, 1, FA_ACT_SILU, nullptr, 0, "ff1_w1"));
-    FA_TRY(gemm(u, ul, c.DFF, Ly.ff1w2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, "ff1_w2"));
+    FA_TRY(ln(0, Ly, hl ? "ln_ff1_x" : "ln_ff1"));
+    FA_TRY(gemm(h, hl, D, Ly.ff1w1, u, ul, c.DFF, 1, FA_ACT_SILU, nullptr, 0, hl ? "ff1_w1_x" : (ul ? "ff1_w1_u" : "ff1_w1")));
+    FA_TRY(gemm(u, ul, c.DFF, Ly.ff1w2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, ul ? "ff1_w2_x" : "ff1_w2"));
     // attention
-    FA_TRY(ln(1, Ly, "ln_att"));
-    FA_TRY(gemm(h, hl, D, Ly.qkv, u, nullptr, 3 * D, 1, FA_ACT_NONE, nullptr, 0, "qkv"));
+    FA_TRY(ln(1, Ly, hl ? "ln_att_x" : "ln_att"));
+    FA_TRY(gemm(h, hl, D, Ly.qkv, u, nullptr, 3 * D, 1, FA_ACT_NONE, nullptr, 0, hl ? "qkv_x" : "qkv"));
     at.pos = Ly.P;
     at.pbu = Ly.pbu;
     at.pbv = Ly.pbv;
     at.out_lo = (ex & FA_EXACT_ATTN_OUT) ? alo : nullptr;
-    FA_TRY(relpos_attention_f16(ctx, at, mx[3], (_Float16 *)e->vt, "attention"));
-    FA_TRY(gemm(a, at.out_lo, D, Ly.out, x, nullptr, D, 0, FA_ACT_NONE, x, 0, "attn_out"));
+    FA_TRY(relpos_attention_f16(ctx, at, mx[3], (_Float16 *)e->vt, at.out_lo ? "attention_x" : "attention"));
+    FA_TRY(gemm(a, at.out_lo, D, Ly.out, x, nullptr, D, 0, FA_ACT_NONE, x, 0, at.out_lo ? "attn_out_x" : "attn_out"));
     // conv module: pw1 + GLU (f16, or f32 when exact) -> depthwise + SiLU -> pw2
-    FA_TRY(ln(2, Ly, "ln_conv"));
+    FA_TRY(ln(2, Ly, hl ? "ln_conv_x" : "ln_conv"));
     const bool glu32 = ex & FA_EXACT_GLU;
-    FA_TRY(gemm(h, hl, D, Ly.pw1, glu32 ? (void *)g32 : (void *)gg, nullptr, D, glu32 ? 0 : 1, FA_ACT_NONE, nullptr, 1, "pw1_glu"));
+    FA_TRY(gemm(h, hl, D, Ly.pw1, glu32 ? (void *)g32 : (void *)gg, nullptr, D, glu32 ? 0 : 1, FA_ACT_NONE, nullptr, 1, hl ? "pw1_glu_x" : (glu32 ? "pw1_glu_f32" : "pw1_glu")));
     _Float16 *dlo = (ex & FA_EXACT_DW_OUT) ? alo : nullptr;
     {
-      ProfScope ps(ctx, "dwconv");
-      const int thr = std::min(128, D / 8);
-      const dim3 grid(cdiv(mx[3], 16), n, cdiv(D / 8, thr));
+      ProfScope ps(ctx, glu32 ? (dlo ? "dwconv_x" : "dwconv_f32") : (dlo ? "dwconv_lo" : "dwconv"));
+      const int thr = std::min(64, D / 8);
+      const dim3 grid(cdiv(mx[3], 4), n, cdiv(D / 8, thr));
       if (glu32)
-        FA_LAUNCH(ps, (dwconv_silu_kernel<9, 16, float>), grid, dim3(thr), 0, ctx->stream, (const float *)g32, a, dlo, Ly.dww, Ly.dwb, D, s3);
+        FA_LAUNCH(ps, (dwconv_silu_kernel<9, 4, float>), grid, dim3(thr), 0, ctx->stream, (const float *)g32, a, dlo, Ly.dww, Ly.dwb, D, s3);
       else
-        FA_LAUNCH(ps, (dwconv_silu_kernel<9, 16, _Float16>), grid, dim3(thr), 0, ctx->stream, (const _Float16 *)gg, a, dlo, Ly.dww, Ly.dwb, D, s3);
+        FA_LAUNCH(ps, (dwconv_silu_kernel<9, 4, _Float16>), grid, dim3(thr), 0, ctx->stream, (const _Float16 *)gg, a, dlo, Ly.dww, Ly.dwb, D, s3);
       FA_TRY(check_launch(ctx, "dwconv"));
     }
-    FA_TRY(gemm(a, dlo, D, Ly.pw2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, "pw2"));
+    FA_TRY(gemm(a, dlo, D, Ly.pw2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, dlo ? "pw2_x" : "pw2"));
     // FF2 + norm_out
-    FA_TRY(ln(3, Ly, "ln_ff2"));
-    FA_TRY(gemm(h, hl, D, Ly.ff2w1, u, ul, c.DFF, 1, FA_ACT_SILU, nullptr, 0, "ff2_w1"));
-    FA_TRY(gemm(u, ul, c.DFF, Ly.ff2w2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, "ff2_w2"));
-    FA_TRY(layernorm_launch(ctx, x, Ly.ln[4][0], Ly.ln[4][1], x, 0, M, D, D, D, 1e-5f, "ln_out"));
+    FA_TRY(ln(3, Ly, hl ? "ln_ff2_x" : "ln_ff2"));
+    FA_TRY(gemm(h, hl, D, Ly.ff2w1, u, ul, c.DFF, 1, FA_ACT_SILU, nullptr, 0, hl ? "ff2_w1_x" : (ul ? "ff2_w1_u" : "ff2_w1")));
+    FA_TRY(gemm(u, ul, c.DFF, Ly.ff2w2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, ul ? "ff2_w2_x" : "ff2_w2"));
+    if (D == 1024) {
+      ProfScope ps(ctx, "ln_out");
+      FA_LAUNCH(ps, enc_ln_f32_kernel<4>, dim3(cdiv(M, 4)), dim3(256), 0, ctx->stream, x, Ly.ln[4][0], Ly.ln[4][1], M, 1e-5f);
+      FA_TRY(check_launch(ctx, "ln_out"));
+    } else {
+      FA_TRY(layernorm_launch(ctx, x, Ly.ln[4][0], Ly.ln[4][1], x, 0, M, D, D, D, 1e-5f, "ln_out"));
+    }
   }
   if (layout == 1) {
     ProfScope ps(ctx, "zero_pad");
