@@ -63,6 +63,7 @@ SIGNATURES = [
     ("fa_end_batch", I, [P]),
     ("fa_batch_open", I, [P]),
     ("fa_matmul", I, [P, T, T, T, I, T, C.POINTER(T)]),
+    ("fa_matmul_pair", I, [P, T, T, T, T, T, C.POINTER(T)]),
     ("fa_matmul_int8", I, [P, T, T, T, I, I, T, I, C.POINTER(T)]),
     ("fa_matmul_nbits", I, [P, T, T, T, T, I, I, C.POINTER(T)]),
     ("fa_layernorm", I, [P, T, T, T, C.c_float, C.POINTER(T)]),

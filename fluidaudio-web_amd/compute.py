@@ -241,6 +241,12 @@ class HipContext:
 
     matmulV3 = matmulV4 = matmulF16 = matmulV2
 
+    def _matmulPair(self, a_hi, a_lo, b, bias=None, add=None):
+        """(A_hi + A_lo) · B with A as two exact f16 planes (no ComputeContext counterpart)."""
+        o = self._out()
+        check(self._p, lib().fa_matmul_pair(self._p, a_hi.h, a_lo.h, b.h, self._h(bias), self._h(add), C.byref(o)))
+        return HipTensor(self, o.value, a_hi.rows, b.cols)
+
     def matmulInt8(self, a, wq, scale, N, K, bias=None, act="none"):
         o = self._out()
         check(self._p, lib().fa_matmul_int8(self._p, a.h, wq.h, scale.h, N, K, self._h(bias), ACT[act], C.byref(o)))

@@ -351,7 +351,7 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
   constexpr int IT = (AR + BN) / 8;                   // 1 KB copies per stage (8 rows each)
   constexpr int IW = (IT + NW - 1) / NW, IMIN = IT / NW;  // per wave: at most / at least
   static_assert(BM % 16 == 0 && BN % 16 == 0 && NW % 4 == 0, "tile shape");
-  static_assert(S >= 2 && S <= 4 && S * STG <= 160 * 1024, "LDS stages");
+  static_assert(S >= 2 && S <= 4 && S * STG <= 160 * 1024, "LDS stages");  // gfx950: 160 KiB per workgroup
   static_assert(NW * 16 * (WTN + 4) * 4 <= STG, "epilogue strips must fit in stage 0");
   __shared__ __attribute__((aligned(1024))) LdsStage<STG> st0, st1, st2, st3;
   char *const stg[4] = {st0.d, st1.d, st2.d, st3.d};
@@ -605,7 +605,7 @@ struct DmaCfg {
 };
 static const DmaCfg kDma[] = {{192, 256, 30.0f}, {192, 128, 18.3f}, {128, 128, 12.6f}, {96, 128, 11.7f}};
 // with a lo plane (two MFMAs per B fragment), same K = 1024 round timing
-static const DmaCfg kDmaLo[] = {{192, 128, 27.7f}, {128, 128, 17.9f}, {96, 128, 16.5f}};
+static const DmaCfg kDmaLo[] = {{192, 256, 51.0f}, {192, 128, 27.7f}, {96, 256, 27.0f}, {128, 128, 17.9f}, {96, 128, 16.5f}};
 
 static int pick_dma(fa_ctx *ctx, const GemmArgs &p) {
   if (p.K % 64 || p.lda % 8 || ((uintptr_t)p.A & 15) || ((uintptr_t)p.B & 15) || ((uintptr_t)p.Alo & 15)) return -1;
@@ -645,9 +645,11 @@ static int launch_tile(fa_ctx *ctx, const GemmArgs &p, const char *label) {
   if constexpr (AK == A_F16 && BKND == B_F16 && EPI != EPI_GENERIC) {
     if (p.Alo) {
       switch (pick_dma(ctx, p)) {
-        case 0: return launch_dma<192, 128, 4, 2, 2, EPI, 1>(ctx, p, label);
-        case 1: return launch_dma<128, 128, 2, 4, 3, EPI, 1>(ctx, p, label);
-        case 2: return launch_dma<96, 128, 2, 4, 3, EPI, 1>(ctx, p, label);
+        case 0: return launch_dma<192, 256, 2, 4, 2, EPI, 1>(ctx, p, label);
+        case 1: return launch_dma<192, 128, 4, 2, 2, EPI, 1>(ctx, p, label);
+        case 2: return launch_dma<96, 256, 2, 4, 2, EPI, 1>(ctx, p, label);
+        case 3: return launch_dma<128, 128, 2, 4, 3, EPI, 1>(ctx, p, label);
+        case 4: return launch_dma<96, 128, 2, 4, 3, EPI, 1>(ctx, p, label);
         default: return set_err(ctx, FA_E_UNSUPPORTED, "%s: lo plane needs N %% 128 == 0, K %% 64 == 0 and 16-byte aligned operands", label);
       }
     }

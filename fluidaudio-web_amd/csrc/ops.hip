@@ -323,6 +323,35 @@ int fa_matmul(fa_ctx *ctx, fa_tensor a, fa_tensor b, fa_tensor bias, int act, fa
   return FA_OK;
 }
 
+int fa_matmul_pair(fa_ctx *ctx, fa_tensor a_hi, fa_tensor a_lo, fa_tensor b, fa_tensor bias, fa_tensor add, fa_tensor *out) {
+  TensorRec *rh, *rl, *rb, *rbias, *radd;
+  FA_TRY(need(ctx, a_hi, &rh, "matmulPair"));
+  FA_TRY(need(ctx, a_lo, &rl, "matmulPair lo"));
+  FA_TRY(need(ctx, b, &rb, "matmulPair"));
+  FA_TRY(opt(ctx, bias, &rbias, "matmulPair bias"));
+  FA_TRY(opt(ctx, add, &radd, "matmulPair add"));
+  if (rh->kind != S_F16RM || rl->kind != S_F16RM || rh->rows != rl->rows || rh->cols != rl->cols)
+    return set_err(ctx, FA_E_INVALID, "matmulPair: A hi and lo must be row-major f16 tensors of one shape");
+  if (rb->kind != S_F16KM) return set_err(ctx, FA_E_INVALID, "matmulPair: B must be an f16 weight tensor (uploadF16)");
+  const int M = rh->rows, K = rh->cols, N = rb->cols;
+  if (rb->rows != K) return set_err(ctx, FA_E_INVALID, "matmulPair: A [%d,%d] @ B [%d,%d]", M, K, rb->rows, rb->cols);
+  if (rbias && rbias->rows * rbias->cols != N) return set_err(ctx, FA_E_INVALID, "matmulPair: bias has %d elements, N=%d", rbias->rows * rbias->cols, N);
+  if (radd && (radd->rows != M || radd->cols != N)) return set_err(ctx, FA_E_INVALID, "matmulPair: add [%d,%d] != [%d,%d]", radd->rows, radd->cols, M, N);
+  fa_tensor o;
+  TensorRec *ro;
+  FA_TRY(new_tensor(ctx, M, N, S_F32, (size_t)M * N * 4, &o, &ro));
+  rh = get(ctx, a_hi); rl = get(ctx, a_lo); rb = get(ctx, b); rbias = bias ? get(ctx, bias) : nullptr; radd = add ? get(ctx, add) : nullptr;
+  GemmArgs p;
+  p.A = rh->ptr; p.Alo = rl->ptr; p.lda = K; p.akind = A_F16;
+  p.B = rb->ptr; p.bkind = B_F16;
+  p.C = ro->ptr; p.ldc = N;
+  p.bias = CF32(rbias); p.add = CF32(radd); p.ldadd = N;
+  p.M = M; p.N = N; p.K = K;
+  FA_TRY(gemm_mfma(ctx, p, "matmul_pair"));
+  *out = o;
+  return FA_OK;
+}
+
 int fa_matmul_int8(fa_ctx *ctx, fa_tensor a, fa_tensor wq, fa_tensor scale, int N, int K, fa_tensor bias, int act, fa_tensor *out) {
   TensorRec *ra, *rw, *rs, *rbias;
   FA_TRY(need(ctx, a, &ra, "matmulInt8"));

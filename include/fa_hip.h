@@ -101,6 +101,12 @@ int fa_batch_open(fa_ctx *ctx);  /* 1 when a batch is open */
 int fa_matmul(fa_ctx *ctx, fa_tensor a, fa_tensor b, fa_tensor bias, int act, fa_tensor add, fa_tensor *out);
 /* matmulInt8: wq = int8 [K,N] row-major bytes (4 per u32, gemm.js:679-708),
  * scale [1,N] per output column; out = act(scale[n]·Σ a·q + bias). */
+/* C = (A_hi + A_lo) · B (+ bias) (+ add), f32 out: A carried as two exact f16
+ * planes (from fa_upload_f16_rows), B an f16 weight tensor; each B fragment
+ * feeds two MFMAs.  No counterpart in compute.d.ts: the fused encoder's
+ * two-plane operand route, exposed for hosts that need f32-accurate
+ * activations against f16 weights.  Needs N % 128 == 0 and K % 64 == 0. */
+int fa_matmul_pair(fa_ctx *ctx, fa_tensor a_hi, fa_tensor a_lo, fa_tensor b, fa_tensor bias, fa_tensor add, fa_tensor *out);
 int fa_matmul_int8(fa_ctx *ctx, fa_tensor a, fa_tensor wq, fa_tensor scale, int N, int K, fa_tensor bias, int act, fa_tensor *out);
 /* matmulNBits: ONNX MatMulNBits (bits=4): bq [N][nblk][16 B], scales f32
  * [N*nblk], zp packed int4 [N][ceil(nblk/2)] (gemm.js:893-919). */

@@ -66,6 +66,30 @@ def test_matmul_f16_activations(ctx, orc, monkeypatch, cfg, shape):
     assert err < 1e-5, (cfg, shape, err)
 
 
+@pytest.mark.parametrize("cfg", ["auto", "1", "2", "3", "4", "5"])
+@pytest.mark.parametrize("shape", [(3008, 1024, 4096), (3008, 4096, 1024), (1504, 1024, 2048), (203, 128, 256), (1, 64, 128)])
+def test_matmul_two_plane_activations(ctx, orc, monkeypatch, cfg, shape):
+    """A carried as exact f16 hi + lo planes (the encoder's exact-operand route,
+    every two-plane configuration pinned in turn, M tails included) vs float64
+    dot products of hi + lo with the f16 weights: f32-level agreement, far
+    tighter than the one-plane route allows."""
+    M, K, N = shape
+    if cfg != "auto":
+        monkeypatch.setenv("FA_GEMM_DMA", cfg)
+    a, b, bias, d = rnd(M, K) * 4, rnd(K, N) * 0.1, rnd(1, N), rnd(M, N)
+    hi = a.astype(np.float16)
+    lo = (a - hi.astype(np.float32)).astype(np.float16)
+    got = dl(ctx, ctx._matmulPair(ctx._uploadF16Rows(hi.astype(np.float32), M, K), ctx._uploadF16Rows(lo.astype(np.float32), M, K),
+                                  ctx.uploadF16(b, K, N), bias=ctx.upload(bias, 1, N), add=ctx.upload(d, M, N)))
+    b16 = b.astype(np.float16).astype(np.float64)
+    ref = (hi.astype(np.float64) + lo.astype(np.float64)) @ b16 + bias.astype(np.float64) + d
+    one_plane = hi.astype(np.float64) @ b16 + bias.astype(np.float64) + d
+    err = np.abs(got - ref).max() / np.abs(ref).max()
+    assert err < 2e-6, (cfg, shape, err)
+    if M * N > 1000:  # the lo plane is carried: the one-plane product is much further away
+        assert np.abs(one_plane - ref).max() / np.abs(ref).max() > 20 * err
+
+
 def test_layernorm(ctx, orc):
     for R, Cc in [(5, 1024), (33, 77)]:
         x, g, b = rnd(R, Cc) * 3 + 1, rnd(1, Cc) + 1, rnd(1, Cc)
