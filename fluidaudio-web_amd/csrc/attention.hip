@@ -219,45 +219,53 @@ __device__ __forceinline__ void attn_dma16(const void *g, uint32_t lds_addr) {
 }
 #pragma clang diagnostic pop
 
-__global__ __launch_bounds__(256) void relpos_attn_lds_kernel(AttnArgs a, const _Float16 *__restrict__ vt, int Tp) {
-  constexpr int HD = 128, QB = 64, KB = 64, SW = 80 + 4, PBS = KB + 8;
-  constexpr int KBYTES = KB * 256, VBYTES = HD * 128, PROWS = 128, PBYTES = PROWS * 256;
-  constexpr int STG = KBYTES + VBYTES + PBYTES;  // 64 KB
+// Workgroup = 128 queries of one (window, head), 4 waves x 32 queries (two
+// 16-row MFMA tiles per wave, so every K / V / band fragment read from LDS
+// feeds two MFMAs).  Keys advance 32 per stage, two stages in flight:
+//   K   [32 keys][128 d]        (256 B rows, 16-byte chunk c at slot c ^ (row & 7))
+//   Vt  [128 d][32 keys]        (64 B rows,  chunk c at slot c ^ ((row >> 1) & 3))
+//   band [160 rows][128 d]      table rows pbase .. pbase+159, pbase = pc - (q0+127) + j0
+// A query i and key j use band row (j - j0) + (q0 + 127 - i).
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void relpos_attn_lds_kernel(AttnArgs a, const _Float16 *__restrict__ vt, int Tp) {
+  constexpr int HD = 128, QB = 128, KB = 32, BR = 160;
+  constexpr int KBYTES = KB * 256, VBYTES = HD * 64, PBYTES = BR * 256;
+  constexpr int STG = KBYTES + VBYTES + PBYTES;  // 56 KB
+  constexpr int SW = 48 + 4, PBS = KB + 8;         // strip row stride (floats), probability row stride (halfs)
   __shared__ __attribute__((aligned(1024))) char st0[STG];
   __shared__ __attribute__((aligned(1024))) char st1[STG];
-  __shared__ float sStrip[4][16 * SW];
-  __shared__ __attribute__((aligned(16))) _Float16 sP[4][16 * PBS];
+  __shared__ float sStrip[4][2][16 * SW];
+  __shared__ __attribute__((aligned(16))) _Float16 sP[4][2][16 * PBS];
 
   const int w = blockIdx.z, h = blockIdx.y, q0 = blockIdx.x * QB;
   const int T = a.win.len[w], off = a.win.off[w];
   if (q0 >= T) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, c16 = lane & 15;
-  const int i0 = q0 + wave * 16;
+  const int iw = q0 + wave * 32;  // this wave's first query (window-local); row tile rt covers iw + 16 rt ..
   const _Float16 *Q = reinterpret_cast<const _Float16 *>(a.q) + (size_t)off * a.ldq + h * HD;
   const _Float16 *Kp = reinterpret_cast<const _Float16 *>(a.k) + (size_t)off * a.ldk + h * HD;
   const _Float16 *Pp = reinterpret_cast<const _Float16 *>(a.pos) + h * HD;
   const _Float16 *Vt = vt + ((size_t)(w * a.H + h) * HD) * Tp;
   const uint32_t sadr[2] = {(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)st0),
                             (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)st1)};
-  const int pbase0 = a.pcenter - (q0 + QB - 1);  // band table row of local row 0 for key block 0
+  const int pbase0 = a.pcenter - (q0 + QB - 1);
 
-  // 64 copies per key block, 16 per wave: K (16: 4 rows of 256 B each),
-  // Vt (16: 8 rows of 128 B), band (32: 4 rows of 256 B).
+  // 56 copies of 1 KB per stage, 14 per wave: K (8: 4 rows each), Vt (8: 16
+  // rows each), band (40: 4 rows each).
   auto issue = [&](int sidx, int j0) {
     const uint32_t base = sadr[sidx];
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const int ins = wave + i * 4;  // 0..63
+    for (int i = 0; i < 14; i++) {
+      const int ins = wave + i * 4;  // 0..55
       const void *src;
-      if (ins < 16) {
+      if (ins < 8) {
         const int r = ins * 4 + (lane >> 4), ch = (lane & 15) ^ (r & 7);
         src = Kp + (size_t)min(j0 + r, T - 1) * a.ldk + ch * 8;
-      } else if (ins < 32) {
-        const int r = (ins - 16) * 8 + (lane >> 3), ch = (lane & 7) ^ (r & 7);
+      } else if (ins < 16) {
+        const int r = (ins - 8) * 16 + (lane >> 2), ch = (lane & 3) ^ ((r >> 1) & 3);
         src = Vt + (size_t)r * Tp + j0 + ch * 8;
       } else {
-        const int r = (ins - 32) * 4 + (lane >> 4), ch = (lane & 15) ^ (r & 7);
+        const int r = (ins - 16) * 4 + (lane >> 4), ch = (lane & 15) ^ (r & 7);
         const int pr = min(max(pbase0 + j0 + r, 0), a.prows - 1);
         src = Pp + (size_t)pr * a.ldp + ch * 8;
       }
@@ -265,129 +273,183 @@ __global__ __launch_bounds__(256) void relpos_attn_lds_kernel(AttnArgs a, const 
     }
   };
 
-  // A operands: (q+u) and (q+v) for row i0 + c16, d = s*32 + g*8 .. +8
-  h8 qu[4], qv[4];
-  {
-    const int qi = min(i0 + c16, T - 1);
+  // A operands: (q+u) and (q+v) for rows iw + 16 rt + c16, d = s*32 + g*8 .. +8
+  h8 qu[2][4], qv[2][4];
+#pragma unroll
+  for (int rt = 0; rt < 2; rt++) {
+    const int qi = min(iw + rt * 16 + c16, T - 1);
     const _Float16 *qr = Q + (size_t)qi * a.ldq;
 #pragma unroll
     for (int s = 0; s < 4; s++) {
       const int d = s * 32 + g * 8;
       const h8 x = *reinterpret_cast<const h8 *>(qr + d);
+      const float4 *bu = reinterpret_cast<const float4 *>(a.pbu + h * HD + d), *bv = reinterpret_cast<const float4 *>(a.pbv + h * HD + d);
+      const float4 u0 = bu[0], u1 = bu[1], v0 = bv[0], v1 = bv[1];
+      const float ub[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w}, vb[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
       for (int e = 0; e < 8; e++) {
         const float xv = (float)x[e];
-        qu[s][e] = (_Float16)(xv + a.pbu[h * HD + d + e]);
-        qv[s][e] = (_Float16)(xv + a.pbv[h * HD + d + e]);
+        qu[rt][s][e] = (_Float16)(xv + ub[e]);
+        qv[rt][s][e] = (_Float16)(xv + vb[e]);
       }
     }
   }
   issue(0, 0);
 
-  f4 o[8];
+  f4 o[2][8];
 #pragma unroll
-  for (int t = 0; t < 8; t++) o[t] = f4{0.f, 0.f, 0.f, 0.f};
-  float mrow[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY}, lrow[4] = {0.f, 0.f, 0.f, 0.f};
-  float *strip = sStrip[wave];
-  _Float16 *pb = sP[wave];
-  const int lb = QB - 16 - wave * 16;  // first band row of this wave within the block's band
+  for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+    for (int t = 0; t < 8; t++) o[rt][t] = f4{0.f, 0.f, 0.f, 0.f};
+  float mrow[2][4], lrow[2][4];
+#pragma unroll
+  for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      mrow[rt][r] = -INFINITY;
+      lrow[rt][r] = 0.f;
+    }
+  const int lbw = QB - 32 - wave * 32;  // band row of this wave's union tile 0 (= row tile 1's first band row)
 
   const int nkb = (T + KB - 1) / KB;
   for (int kb = 0; kb < nkb; kb++) {
     const int j0 = kb * KB, cur = kb & 1;
-    __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8));  // vmcnt(0): this block's copies landed
-    __syncthreads();                                               // ... for every wave; previous block's reads done
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0): this stage's copies landed
+    __syncthreads();                                    // ... for every wave; the other stage is free
     if (kb + 1 < nkb) issue(cur ^ 1, j0 + KB);
     const char *Ks = cur ? st1 : st0, *Vs = Ks + KBYTES, *Ps = Ks + KBYTES + VBYTES;
 
-    // content scores (q+u)·kᵀ : 4 tiles of 16 keys
-    f4 sc[4];
+    // fragment reads: K (2 key tiles x 4 k-steps), band (4 union tiles x 4)
+    h8 kf[2][4], pf[4][4];
 #pragma unroll
-    for (int jt = 0; jt < 4; jt++) {
-      sc[jt] = f4{0.f, 0.f, 0.f, 0.f};
-      const int r = jt * 16 + c16;
+    for (int kt = 0; kt < 2; kt++) {
+      const int r = kt * 16 + c16;
 #pragma unroll
-      for (int s = 0; s < 4; s++) {
-        const h8 kf = *reinterpret_cast<const h8 *>(Ks + r * 256 + (((s * 4 + g) ^ (r & 7)) * 16));
-        sc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qu[s], kf, sc[jt], 0, 0, 0);
-      }
+      for (int s = 0; s < 4; s++) kf[kt][s] = *reinterpret_cast<const h8 *>(Ks + r * 256 + (((s * 4 + g) ^ (r & 7)) * 16));
     }
-    // positional band (q+v)·Pᵀ over this wave's 80 band rows
 #pragma unroll
-    for (int ct = 0; ct < 5; ct++) {
-      f4 bd = f4{0.f, 0.f, 0.f, 0.f};
-      const int r = lb + ct * 16 + c16;
+    for (int u = 0; u < 4; u++) {
+      const int r = lbw + u * 16 + c16;
 #pragma unroll
-      for (int s = 0; s < 4; s++) {
-        const h8 pf = *reinterpret_cast<const h8 *>(Ps + r * 256 + (((s * 4 + g) ^ (r & 7)) * 16));
-        bd = __builtin_amdgcn_mfma_f32_16x16x32_f16(qv[s], pf, bd, 0, 0, 0);
-      }
-#pragma unroll
-      for (int rr = 0; rr < 4; rr++) strip[(g * 4 + rr) * SW + ct * 16 + c16] = bd[rr];
+      for (int s = 0; s < 4; s++) pf[u][s] = *reinterpret_cast<const h8 *>(Ps + r * 256 + (((s * 4 + g) ^ (r & 7)) * 16));
     }
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): strip writes done (wave-private strip)
+    __builtin_amdgcn_sched_barrier(0);
+    // row tile rt uses band union tiles (1 - rt) .. (3 - rt)
+    f4 sc[2][2], bd[2][3];
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++) {
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++) sc[rt][kt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ct = 0; ct < 3; ct++) bd[rt][ct] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int s = 0; s < 4; s++)
+#pragma unroll
+      for (int rt = 0; rt < 2; rt++) {
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++) sc[rt][kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qu[rt][s], kf[kt][s], sc[rt][kt], 0, 0, 0);
+#pragma unroll
+        for (int ct = 0; ct < 3; ct++) bd[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qv[rt][s], pf[1 - rt + ct][s], bd[rt][ct], 0, 0, 0);
+      }
+    // V fragments (d rows t*16 + c16, keys g*8 .. +8), read now to hide behind the softmax
+    h8 vf[8];
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+      const int d = t * 16 + c16;
+      vf[t] = *reinterpret_cast<const h8 *>(Vs + d * 64 + ((g ^ ((d >> 1) & 3)) * 16));
+    }
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+      for (int ct = 0; ct < 3; ct++)
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) sStrip[wave][rt][(g * 4 + rr) * SW + ct * 16 + c16] = bd[rt][ct][rr];
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): strip writes done (wave-private strips)
     __builtin_amdgcn_wave_barrier();
-    // S = ac + band[i][j - j0 + 15 - (i - i0)], mask keys >= T, online softmax
-    float mnew[4];
+    // S = ac + band[i][jj + 15 - (i - ib)], keys >= T masked, online softmax.
+    // Lazy rescaling: probabilities are taken against a per-row reference
+    // max mref that only moves (rescaling l and O) when some row's running
+    // max exceeds it by more than kLazy nats, decided wave-wide; p <= e^kLazy
+    // stays well inside f16 range with unchanged relative precision.
+    constexpr float kLazy = 8.f;
+    float sv[2][4][2];
+    bool need = false;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int ri = g * 4 + r;
-      float mx = mrow[r];
+    for (int rt = 0; rt < 2; rt++) {
+      const float *strip = sStrip[wave][rt];
 #pragma unroll
-      for (int jt = 0; jt < 4; jt++) {
-        const int jj = jt * 16 + c16;
-        float v = sc[jt][r] + strip[ri * SW + jj + 15 - ri];
-        v = (j0 + jj < T) ? v : -INFINITY;
-        sc[jt][r] = v;
-        mx = fmaxf(mx, v);
+      for (int r = 0; r < 4; r++) {
+        const int ri = g * 4 + r;
+        float v0 = sc[rt][0][r] + strip[ri * SW + c16 + 15 - ri];
+        float v1 = sc[rt][1][r] + strip[ri * SW + 16 + c16 + 15 - ri];
+        v0 = (j0 + c16 < T) ? v0 : -INFINITY;
+        v1 = (j0 + 16 + c16 < T) ? v1 : -INFINITY;
+        sv[rt][r][0] = v0;
+        sv[rt][r][1] = v1;
+        need |= fmaxf(v0, v1) > mrow[rt][r] + kLazy;
       }
-      mnew[r] = row16_max(mx);
+    }
+    if (__builtin_amdgcn_ballot_w64(need)) {
+#pragma unroll
+      for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const float mx = row16_max(fmaxf(sv[rt][r][0], sv[rt][r][1]));
+          if (mx > mrow[rt][r]) {
+            const float corr = __expf(mrow[rt][r] - mx);  // 0 on the first key block (mref = -inf)
+            lrow[rt][r] *= corr;  // per-lane partial sums scale with their row
+#pragma unroll
+            for (int t = 0; t < 8; t++) o[rt][t][r] *= corr;
+            mrow[rt][r] = mx;
+          }
+        }
     }
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const float corr = __expf(mrow[r] - mnew[r]);
-      float ls = 0.f;
+    for (int rt = 0; rt < 2; rt++) {
+      _Float16 *pb = sP[wave][rt];
 #pragma unroll
-      for (int jt = 0; jt < 4; jt++) {
-        const float pv = __expf(sc[jt][r] - mnew[r]);
-        ls += pv;
-        pb[(g * 4 + r) * PBS + jt * 16 + c16] = (_Float16)pv;
+      for (int r = 0; r < 4; r++) {
+        const int ri = g * 4 + r;
+        const float p0 = __expf(sv[rt][r][0] - mrow[rt][r]), p1 = __expf(sv[rt][r][1] - mrow[rt][r]);
+        pb[ri * PBS + c16] = (_Float16)p0;
+        pb[ri * PBS + 16 + c16] = (_Float16)p1;
+        lrow[rt][r] += p0 + p1;  // per-lane partial; rows reduced once after the last key block
       }
-      lrow[r] = lrow[r] * corr + row16_sum(ls);
-      mrow[r] = mnew[r];
-#pragma unroll
-      for (int t = 0; t < 8; t++) o[t][r] *= corr;
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
-    // O += P·V  (B operand: Vt rows d, keys kk*32 + g*8 .. +8)
+    // O += P·V
 #pragma unroll
-    for (int kk = 0; kk < 2; kk++) {
-      const h8 pa = *reinterpret_cast<const h8 *>(&pb[c16 * PBS + kk * 32 + g * 8]);
+    for (int rt = 0; rt < 2; rt++) {
+      const h8 pa = *reinterpret_cast<const h8 *>(&sP[wave][rt][c16 * PBS + g * 8]);
 #pragma unroll
-      for (int t = 0; t < 8; t++) {
-        const int d = t * 16 + c16;
-        const h8 vb = *reinterpret_cast<const h8 *>(Vs + d * 128 + (((kk * 4 + g) ^ (d & 7)) * 16));
-        o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[t], 0, 0, 0);
-      }
+      for (int t = 0; t < 8; t++) o[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vf[t], o[rt][t], 0, 0, 0);
     }
   }
 
   _Float16 *O = reinterpret_cast<_Float16 *>(a.out) + (size_t)off * a.ldo + h * HD;
   _Float16 *Olo = a.out_lo ? reinterpret_cast<_Float16 *>(a.out_lo) + (size_t)off * a.ldo + h * HD : nullptr;
+  float lsum[2][4];  // row sums, reduced with every lane active
 #pragma unroll
-  for (int r = 0; r < 4; r++) {
-    const int i = i0 + g * 4 + r;
-    if (i >= T) continue;
-    const float inv = 1.f / lrow[r];
+  for (int rt = 0; rt < 2; rt++)
 #pragma unroll
-    for (int t = 0; t < 8; t++) {
-      const float v = o[t][r] * inv;
-      const _Float16 hi = (_Float16)v;
-      O[(size_t)i * a.ldo + t * 16 + c16] = hi;
-      if (Olo) Olo[(size_t)i * a.ldo + t * 16 + c16] = (_Float16)(v - (float)hi);
+    for (int r = 0; r < 4; r++) lsum[rt][r] = row16_sum(lrow[rt][r]);
+#pragma unroll
+  for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int i = iw + rt * 16 + g * 4 + r;
+      if (i >= T) continue;
+      const float inv = 1.f / lsum[rt][r];
+#pragma unroll
+      for (int t = 0; t < 8; t++) {
+        const float v = o[rt][t][r] * inv;
+        const _Float16 hi = (_Float16)v;
+        O[(size_t)i * a.ldo + t * 16 + c16] = hi;
+        if (Olo) Olo[(size_t)i * a.ldo + t * 16 + c16] = (_Float16)(v - (float)hi);
+      }
     }
-  }
 }
 
 int relpos_attention_f16(fa_ctx *ctx, const AttnArgs &a, int Tmax, _Float16 *vt, const char *label) {
@@ -398,7 +460,7 @@ int relpos_attention_f16(fa_ctx *ctx, const AttnArgs &a, int Tmax, _Float16 *vt,
   for (int i = 0; i < W; i++)
     if (a.win.len[i] > Tmax || a.pcenter - (a.win.len[i] - 1) < 0 || a.pcenter + a.win.len[i] - 1 >= a.prows)
       return set_err(ctx, FA_E_INVALID, "%s: window %d length %d outside the positional table", label, i, a.win.len[i]);
-  const int Tp = (Tmax + 63) / 64 * 64;
+  const int Tp = (Tmax + 63) / 64 * 64;  // v_transpose_kernel tiles of 64 keys; the attention reads 32 at a time
   {
     ProfScope ps(ctx, "v_transpose");
     FA_LAUNCH(ps, v_transpose_kernel, dim3(Tp / 64, a.H, W), dim3(256), 0, ctx->stream, reinterpret_cast<const _Float16 *>(a.v), a.ldv, a.win, a.H,
@@ -406,7 +468,7 @@ int relpos_attention_f16(fa_ctx *ctx, const AttnArgs &a, int Tmax, _Float16 *vt,
     FA_TRY(check_launch(ctx, "v_transpose"));
   }
   ProfScope ps(ctx, label);
-  FA_LAUNCH(ps, relpos_attn_lds_kernel, dim3(cdiv(Tmax, 64), a.H, W), dim3(256), 0, ctx->stream, a, (const _Float16 *)vt, Tp);
+  FA_LAUNCH(ps, relpos_attn_lds_kernel, dim3(cdiv(Tmax, 128), a.H, W), dim3(256), 0, ctx->stream, a, (const _Float16 *)vt, Tp);
   return check_launch(ctx, label);
 }
 
