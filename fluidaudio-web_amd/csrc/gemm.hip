@@ -362,8 +362,13 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const int nTN = p.N / BN, nTM = (p.M + BM - 1) / BM;
+  // XCD-contiguous tile runs (xcd_remap), ordered in groups of 8 M-rows with N
+  // outer inside a group: one XCD's run covers ~8 A panels x (run/8) B panels,
+  // so its L2 holds both operands instead of streaming every B panel.
   const int tile = xcd_remap(blockIdx.x, nTM * nTN);
-  const int m0 = (tile / nTN) * BM, n0 = (tile % nTN) * BN;
+  constexpr int GM = 8;
+  const int grp = tile / (GM * nTN), gm = min(GM, nTM - grp * GM), gi = tile - grp * GM * nTN;
+  const int m0 = (grp * GM + gi % gm) * BM, n0 = (gi / gm) * BN;
   const _Float16 *A = reinterpret_cast<const _Float16 *>(p.A), *B = reinterpret_cast<const _Float16 *>(p.B);
 
   // copy i of this wave moves rows [ins*8, ins*8+8) of the stacked A|B tile
