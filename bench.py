@@ -46,11 +46,9 @@ def log(*a):
 
 # ── algorithmic work per kernel launch (valid rows only) ────────────────────
 # Labels that launch the same kernel on the same shape, pooled for the
-# roofline (the timed region brackets every label with the class's prefix and
-# keeps the class's launches).
+# roofline (the timed region brackets exactly the class's labels).
 _CLASSES = {"ff1_w1": "ff_w1", "ff2_w1": "ff_w1", "ff1_w2": "ff_w2", "ff2_w2": "ff_w2",
             "ln_ff1": "ln", "ln_att": "ln", "ln_conv": "ln", "ln_ff2": "ln"}
-CLASS_PREFIX = {"ff_w1": "ff", "ff_w2": "ff", "ln": "ln_"}
 
 
 def kernel_class(label):
@@ -186,7 +184,7 @@ def run_encoder(args, fa, ctx, cfg, lens, layout, fmt="f16", seed=1):
     # timed region: K steps, only the dominant kernel's launches bracketed by
     # HIP events on the encoder stream (few events: the timeline is unperturbed)
     ctx.sync()
-    ctx.startProfile(200000, only=CLASS_PREFIX.get(dom, dom))
+    ctx.startProfile(200000, only=",".join(l for l in totals if kernel_class(l) == dom))
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()

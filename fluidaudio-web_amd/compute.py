@@ -384,7 +384,8 @@ class HipContext:
 
     # ── profiling (compute.d.ts:250-251) ──────────────────────────────────
     def startProfile(self, maxOps=4096, only=None):
-        """Bracket launches with HIP events; `only` restricts it to labels with that prefix."""
+        """Bracket launches with HIP events; `only` restricts it to a comma-separated
+        list of exact labels (an entry ending in '*' matches a prefix)."""
         self._prof_cap = maxOps
         check(self._p, lib().fa_profile_only(self._p, (only or "").encode()))
         check(self._p, lib().fa_profile_start(self._p, maxOps))

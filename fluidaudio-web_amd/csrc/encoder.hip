@@ -412,6 +412,16 @@ struct fa_encoder {
     unsigned exact = 0;     // FA_EXACT_* operands carried as exact f16 hi/lo pairs
   };
   std::vector<Layer> L;
+  // captured forwards (hipGraph), keyed by everything baked into the launch
+  // arguments; ws_gen moves whenever a workspace buffer or a precision mask
+  // changes, so stale graphs never match again
+  struct Captured {
+    std::vector<int64_t> key;
+    hipGraphExec_t exec = nullptr;
+    uint64_t used = 0;
+  };
+  std::vector<Captured> graphs;
+  uint64_t ws_gen = 0, graph_clock = 0;
   // workspace (grow-only)
   void *hlo = nullptr, *ulo = nullptr, *alo = nullptr, *g32 = nullptr, *vt = nullptr, *s2 = nullptr, *s2p = nullptr, *s3 = nullptr, *s3p = nullptr, *h = nullptr, *u = nullptr, *a = nullptr, *g = nullptr;
   size_t cap_hlo = 0, cap_ulo = 0, cap_alo = 0, cap_g32 = 0, cap_vt = 0, cap_s2 = 0, cap_s2p = 0, cap_s3 = 0, cap_s3p = 0, cap_m = 0, cap_u = 0;
@@ -550,6 +560,7 @@ static void set_gemm_b(GemmArgs &p, const Lin &L) {
 
 static int grow(fa_encoder *e, void **buf, size_t *cap, size_t need) {
   if (need <= *cap) return FA_OK;
+  e->ws_gen++;
   if (*buf) {
     (void)hipStreamSynchronize(e->ctx->stream);
     (void)hipFree(*buf);
@@ -604,6 +615,8 @@ void fa_encoder_destroy(fa_encoder *enc) {
   if (!enc) return;
   (void)hipStreamSynchronize(enc->ctx->stream);
   for (void *p : enc->allocs) (void)hipFree(p);
+  for (auto &g : enc->graphs)
+    if (g.exec) (void)hipGraphExecDestroy(g.exec);
   for (void *p : {enc->hlo, enc->ulo, enc->alo, enc->g32, enc->vt, enc->s2, enc->s2p, enc->s3, enc->s3p, enc->h, enc->u, enc->a, enc->g})
     if (p) (void)hipFree(p);
   delete enc;
@@ -619,6 +632,7 @@ int fa_encoder_set_exact(fa_encoder *enc, int first_layer, int last_layer, unsig
   if ((mask & FA_EXACT_LN_OUT) && (enc->cfg.D % 256 || enc->cfg.D > 2048))
     return set_err(enc->ctx, FA_E_UNSUPPORTED, "setExact: exact LayerNorm output needs D a multiple of 256 (<= 2048)");
   for (int l = first_layer; l <= last_layer; l++) enc->L[l].exact = mask;
+  enc->ws_gen++;  // captured forwards bake the masks in
   return FA_OK;
 }
 
@@ -950,7 +964,7 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
   const size_t need_m = (size_t)M * D * 2, need_u = (size_t)M * std::max(c.DFF, 3 * D) * 2;
   if (need_m > e->cap_m) {
     size_t c1 = 0, c2 = 0, c3 = 0;
-    if (e->h) { (void)hipStreamSynchronize(ctx->stream); (void)hipFree(e->h); (void)hipFree(e->a); (void)hipFree(e->g); e->h = e->a = e->g = nullptr; }
+    if (e->h) { (void)hipStreamSynchronize(ctx->stream); (void)hipFree(e->h); (void)hipFree(e->a); (void)hipFree(e->g); e->h = e->a = e->g = nullptr; e->ws_gen++; }
     FA_TRY(grow(e, &e->h, &c1, need_m));
     FA_TRY(grow(e, &e->a, &c2, need_m));
     FA_TRY(grow(e, &e->g, &c3, need_m));
@@ -973,135 +987,179 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
   float *x = (float *)rx->ptr;
   _Float16 *h = (_Float16 *)e->h, *u = (_Float16 *)e->u, *a = (_Float16 *)e->a, *gg = (_Float16 *)e->g;
 
+  // The whole forward is a fixed kernel sequence for a given signature: it is
+  // captured once into a hipGraph and replayed (one submission instead of
+  // ~700 launches).  Profiling runs eagerly (its events are per launch).
+  auto launch_all = [&]() -> int {
   // ── subsampling ──
-  {
-    ProfScope ps(ctx, "sub_c01");
-    FA_TRY(launch_c01(ctx, ps, dim3(cdiv(mx[2], 4), n), (const float *)rm->ptr, MB, s0, s1, F1, s2, F2, e->c0w, e->c0b, e->c1w, e->c1b,
-                      (_Float16 *)e->s2, C));
-    FA_TRY(check_launch(ctx, "sub_c01"));
-  }
-  {
-    GemmArgs p;  // c2 (1x1) + bias; its ReLU is applied by the c3 kernel's loads
-    p.A = e->s2; p.lda = 2 * C; p.akind = A_F16;
-    set_gemm_b(p, e->c2);
-    p.C = e->s2p; p.ldc = C;
-    p.M = R[2] * F2;
-    FA_TRY(gemm_mfma(ctx, p, "sub_pw2"));
-  }
-  {
-    ProfScope ps(ctx, "sub_dw3");
-    FA_TRY(launch_dw(ctx, ps, dim3(cdiv(mx[3], 4), n), (const float *)e->s2p, s2, F2, s3, F3, e->c3w, e->c3b, (_Float16 *)e->s3, C));
-    FA_TRY(check_launch(ctx, "sub_dw3"));
-  }
-  {
-    GemmArgs p;  // c4 (1x1) + bias + ReLU, written as hi/lo pairs for the linear
-    p.A = e->s3; p.lda = 2 * C; p.akind = A_F16;
-    set_gemm_b(p, e->c4);
-    p.C = e->s3p; p.ldc = 2 * C; p.out_f16 = 1; p.hilo = 1;
-    p.M = R[3] * F3;
-    FA_TRY(gemm_mfma(ctx, p, "sub_pw4"));
-  }
-  {
-    GemmArgs p;
-    p.A = e->s3p; p.lda = 2 * C * F3; p.akind = A_F16;
-    set_gemm_b(p, e->lin);
-    p.C = x; p.ldc = D;
-    p.M = M;
-    FA_TRY(gemm_mfma(ctx, p, "sub_linear"));
-  }
-
-  // ── conformer layers ──
-  // A operand (with an optional exact lo plane) -> C (with an optional lo plane)
-  auto gemm = [&](const void *A, const void *Alo, int lda, const Lin &L, void *Cp, void *Clo, int ldc, int out_f16, int act, const float *add, int glu,
-                  const char *label) {
-    GemmArgs p;
-    p.A = A; p.Alo = Alo; p.lda = lda; p.akind = A_F16;
-    set_gemm_b(p, L);
-    p.C = Cp; p.Clo = Clo; p.ldc = ldc; p.out_f16 = out_f16; p.act = act;
-    p.add = add; p.ldadd = ldc; p.glu = glu;
-    p.M = M;
-    return gemm_mfma(ctx, p, label);
-  };
-  _Float16 *hlo = (_Float16 *)e->hlo, *ulo = (_Float16 *)e->ulo, *alo = (_Float16 *)e->alo;
-  float *g32 = (float *)e->g32;
-  auto ln = [&](int which, const fa_encoder::Layer &Ly, const char *label) -> int {
-    _Float16 *lo = (Ly.exact & FA_EXACT_LN_OUT) ? hlo : nullptr;
-    if (D % 256 == 0 && D <= 2048) {
-      ProfScope ps(ctx, label);
-      const dim3 grid(cdiv(M, 4));
-      switch (D / 256) {
-        case 1: FA_LAUNCH(ps, enc_ln_kernel<1>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[which][0], Ly.ln[which][1], h, lo, M, 1e-5f); break;
-        case 2: FA_LAUNCH(ps, enc_ln_kernel<2>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[which][0], Ly.ln[which][1], h, lo, M, 1e-5f); break;
-        case 4: FA_LAUNCH(ps, enc_ln_kernel<4>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[which][0], Ly.ln[which][1], h, lo, M, 1e-5f); break;
-        case 8: FA_LAUNCH(ps, enc_ln_kernel<8>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[which][0], Ly.ln[which][1], h, lo, M, 1e-5f); break;
-        default: return layernorm_launch(ctx, x, Ly.ln[which][0], Ly.ln[which][1], h, 1, M, D, D, D, 1e-5f, label);
-      }
-      return check_launch(ctx, label);
-    }
-    return layernorm_launch(ctx, x, Ly.ln[which][0], Ly.ln[which][1], h, 1, M, D, D, D, 1e-5f, label);
-  };
-  AttnArgs at;
-  at.q = u; at.k = u + D; at.v = u + 2 * D;
-  at.ldq = at.ldk = at.ldv = 3 * D;
-  at.ldp = D; at.prows = 2 * e->maxT - 1; at.pcenter = e->maxT - 1;
-  at.out = a; at.ldo = D;
-  at.H = c.H; at.HD = c.HD;
-  at.win.n = n;
-  for (int i = 0; i < n; i++) {
-    at.win.off[i] = s3.off[i];
-    at.win.len[i] = s3.len[i];
-  }
-  for (int li = 0; li < layers; li++) {
-    auto &Ly = e->L[li];
-    const unsigned ex = Ly.exact;
-    const void *hl = (ex & FA_EXACT_LN_OUT) ? hlo : nullptr;
-    void *ul = (ex & FA_EXACT_FF_HIDDEN) ? ulo : nullptr;
-    // FF1
-    FA_TRY(ln(0, Ly, hl ? "ln_ff1_x" : "ln_ff1"));
-    FA_TRY(gemm(h, hl, D, Ly.ff1w1, u, ul, c.DFF, 1, FA_ACT_SILU, nullptr, 0, hl ? "ff1_w1_x" : (ul ? "ff1_w1_u" : "ff1_w1")));
-    FA_TRY(gemm(u, ul, c.DFF, Ly.ff1w2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, ul ? "ff1_w2_x" : "ff1_w2"));
-    // attention
-    FA_TRY(ln(1, Ly, hl ? "ln_att_x" : "ln_att"));
-    FA_TRY(gemm(h, hl, D, Ly.qkv, u, nullptr, 3 * D, 1, FA_ACT_NONE, nullptr, 0, hl ? "qkv_x" : "qkv"));
-    at.pos = Ly.P;
-    at.pbu = Ly.pbu;
-    at.pbv = Ly.pbv;
-    at.out_lo = (ex & FA_EXACT_ATTN_OUT) ? alo : nullptr;
-    FA_TRY(relpos_attention_f16(ctx, at, mx[3], (_Float16 *)e->vt, at.out_lo ? "attention_x" : "attention"));
-    FA_TRY(gemm(a, at.out_lo, D, Ly.out, x, nullptr, D, 0, FA_ACT_NONE, x, 0, at.out_lo ? "attn_out_x" : "attn_out"));
-    // conv module: pw1 + GLU (f16, or f32 when exact) -> depthwise + SiLU -> pw2
-    FA_TRY(ln(2, Ly, hl ? "ln_conv_x" : "ln_conv"));
-    const bool glu32 = ex & FA_EXACT_GLU;
-    FA_TRY(gemm(h, hl, D, Ly.pw1, glu32 ? (void *)g32 : (void *)gg, nullptr, D, glu32 ? 0 : 1, FA_ACT_NONE, nullptr, 1, hl ? "pw1_glu_x" : (glu32 ? "pw1_glu_f32" : "pw1_glu")));
-    _Float16 *dlo = (ex & FA_EXACT_DW_OUT) ? alo : nullptr;
     {
-      ProfScope ps(ctx, glu32 ? (dlo ? "dwconv_x" : "dwconv_f32") : (dlo ? "dwconv_lo" : "dwconv"));
-      const int thr = std::min(64, D / 8);
-      const dim3 grid(cdiv(mx[3], 4), n, cdiv(D / 8, thr));
-      if (glu32)
-        FA_LAUNCH(ps, (dwconv_silu_kernel<9, 4, float>), grid, dim3(thr), 0, ctx->stream, (const float *)g32, a, dlo, Ly.dww, Ly.dwb, D, s3);
-      else
-        FA_LAUNCH(ps, (dwconv_silu_kernel<9, 4, _Float16>), grid, dim3(thr), 0, ctx->stream, (const _Float16 *)gg, a, dlo, Ly.dww, Ly.dwb, D, s3);
-      FA_TRY(check_launch(ctx, "dwconv"));
+      ProfScope ps(ctx, "sub_c01");
+      FA_TRY(launch_c01(ctx, ps, dim3(cdiv(mx[2], 4), n), (const float *)rm->ptr, MB, s0, s1, F1, s2, F2, e->c0w, e->c0b, e->c1w, e->c1b,
+                        (_Float16 *)e->s2, C));
+      FA_TRY(check_launch(ctx, "sub_c01"));
     }
-    FA_TRY(gemm(a, dlo, D, Ly.pw2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, dlo ? "pw2_x" : "pw2"));
-    // FF2 + norm_out
-    FA_TRY(ln(3, Ly, hl ? "ln_ff2_x" : "ln_ff2"));
-    FA_TRY(gemm(h, hl, D, Ly.ff2w1, u, ul, c.DFF, 1, FA_ACT_SILU, nullptr, 0, hl ? "ff2_w1_x" : (ul ? "ff2_w1_u" : "ff2_w1")));
-    FA_TRY(gemm(u, ul, c.DFF, Ly.ff2w2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, ul ? "ff2_w2_x" : "ff2_w2"));
-    if (D == 1024) {
-      ProfScope ps(ctx, "ln_out");
-      FA_LAUNCH(ps, enc_ln_f32_kernel<4>, dim3(cdiv(M, 4)), dim3(256), 0, ctx->stream, x, Ly.ln[4][0], Ly.ln[4][1], M, 1e-5f);
-      FA_TRY(check_launch(ctx, "ln_out"));
-    } else {
-      FA_TRY(layernorm_launch(ctx, x, Ly.ln[4][0], Ly.ln[4][1], x, 0, M, D, D, D, 1e-5f, "ln_out"));
+    {
+      GemmArgs p;  // c2 (1x1) + bias; its ReLU is applied by the c3 kernel's loads
+      p.A = e->s2; p.lda = 2 * C; p.akind = A_F16;
+      set_gemm_b(p, e->c2);
+      p.C = e->s2p; p.ldc = C;
+      p.M = R[2] * F2;
+      FA_TRY(gemm_mfma(ctx, p, "sub_pw2"));
     }
+    {
+      ProfScope ps(ctx, "sub_dw3");
+      FA_TRY(launch_dw(ctx, ps, dim3(cdiv(mx[3], 4), n), (const float *)e->s2p, s2, F2, s3, F3, e->c3w, e->c3b, (_Float16 *)e->s3, C));
+      FA_TRY(check_launch(ctx, "sub_dw3"));
+    }
+    {
+      GemmArgs p;  // c4 (1x1) + bias + ReLU, written as hi/lo pairs for the linear
+      p.A = e->s3; p.lda = 2 * C; p.akind = A_F16;
+      set_gemm_b(p, e->c4);
+      p.C = e->s3p; p.ldc = 2 * C; p.out_f16 = 1; p.hilo = 1;
+      p.M = R[3] * F3;
+      FA_TRY(gemm_mfma(ctx, p, "sub_pw4"));
+    }
+    {
+      GemmArgs p;
+      p.A = e->s3p; p.lda = 2 * C * F3; p.akind = A_F16;
+      set_gemm_b(p, e->lin);
+      p.C = x; p.ldc = D;
+      p.M = M;
+      FA_TRY(gemm_mfma(ctx, p, "sub_linear"));
+    }
+  
+    // ── conformer layers ──
+    // A operand (with an optional exact lo plane) -> C (with an optional lo plane)
+    auto gemm = [&](const void *A, const void *Alo, int lda, const Lin &L, void *Cp, void *Clo, int ldc, int out_f16, int act, const float *add, int glu,
+                    const char *label) {
+      GemmArgs p;
+      p.A = A; p.Alo = Alo; p.lda = lda; p.akind = A_F16;
+      set_gemm_b(p, L);
+      p.C = Cp; p.Clo = Clo; p.ldc = ldc; p.out_f16 = out_f16; p.act = act;
+      p.add = add; p.ldadd = ldc; p.glu = glu;
+      p.M = M;
+      return gemm_mfma(ctx, p, label);
+    };
+    _Float16 *hlo = (_Float16 *)e->hlo, *ulo = (_Float16 *)e->ulo, *alo = (_Float16 *)e->alo;
+    float *g32 = (float *)e->g32;
+    auto ln = [&](int which, const fa_encoder::Layer &Ly, const char *label) -> int {
+      _Float16 *lo = (Ly.exact & FA_EXACT_LN_OUT) ? hlo : nullptr;
+      if (D % 256 == 0 && D <= 2048) {
+        ProfScope ps(ctx, label);
+        const dim3 grid(cdiv(M, 4));
+        switch (D / 256) {
+          case 1: FA_LAUNCH(ps, enc_ln_kernel<1>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[which][0], Ly.ln[which][1], h, lo, M, 1e-5f); break;
+          case 2: FA_LAUNCH(ps, enc_ln_kernel<2>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[which][0], Ly.ln[which][1], h, lo, M, 1e-5f); break;
+          case 4: FA_LAUNCH(ps, enc_ln_kernel<4>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[which][0], Ly.ln[which][1], h, lo, M, 1e-5f); break;
+          case 8: FA_LAUNCH(ps, enc_ln_kernel<8>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[which][0], Ly.ln[which][1], h, lo, M, 1e-5f); break;
+          default: return layernorm_launch(ctx, x, Ly.ln[which][0], Ly.ln[which][1], h, 1, M, D, D, D, 1e-5f, label);
+        }
+        return check_launch(ctx, label);
+      }
+      return layernorm_launch(ctx, x, Ly.ln[which][0], Ly.ln[which][1], h, 1, M, D, D, D, 1e-5f, label);
+    };
+    AttnArgs at;
+    at.q = u; at.k = u + D; at.v = u + 2 * D;
+    at.ldq = at.ldk = at.ldv = 3 * D;
+    at.ldp = D; at.prows = 2 * e->maxT - 1; at.pcenter = e->maxT - 1;
+    at.out = a; at.ldo = D;
+    at.H = c.H; at.HD = c.HD;
+    at.win.n = n;
+    for (int i = 0; i < n; i++) {
+      at.win.off[i] = s3.off[i];
+      at.win.len[i] = s3.len[i];
+    }
+    for (int li = 0; li < layers; li++) {
+      auto &Ly = e->L[li];
+      const unsigned ex = Ly.exact;
+      const void *hl = (ex & FA_EXACT_LN_OUT) ? hlo : nullptr;
+      void *ul = (ex & FA_EXACT_FF_HIDDEN) ? ulo : nullptr;
+      // FF1
+      FA_TRY(ln(0, Ly, hl ? "ln_ff1_x" : "ln_ff1"));
+      FA_TRY(gemm(h, hl, D, Ly.ff1w1, u, ul, c.DFF, 1, FA_ACT_SILU, nullptr, 0, hl ? "ff1_w1_x" : (ul ? "ff1_w1_u" : "ff1_w1")));
+      FA_TRY(gemm(u, ul, c.DFF, Ly.ff1w2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, ul ? "ff1_w2_x" : "ff1_w2"));
+      // attention
+      FA_TRY(ln(1, Ly, hl ? "ln_att_x" : "ln_att"));
+      FA_TRY(gemm(h, hl, D, Ly.qkv, u, nullptr, 3 * D, 1, FA_ACT_NONE, nullptr, 0, hl ? "qkv_x" : "qkv"));
+      at.pos = Ly.P;
+      at.pbu = Ly.pbu;
+      at.pbv = Ly.pbv;
+      at.out_lo = (ex & FA_EXACT_ATTN_OUT) ? alo : nullptr;
+      FA_TRY(relpos_attention_f16(ctx, at, mx[3], (_Float16 *)e->vt, at.out_lo ? "attention_x" : "attention"));
+      FA_TRY(gemm(a, at.out_lo, D, Ly.out, x, nullptr, D, 0, FA_ACT_NONE, x, 0, at.out_lo ? "attn_out_x" : "attn_out"));
+      // conv module: pw1 + GLU (f16, or f32 when exact) -> depthwise + SiLU -> pw2
+      FA_TRY(ln(2, Ly, hl ? "ln_conv_x" : "ln_conv"));
+      const bool glu32 = ex & FA_EXACT_GLU;
+      FA_TRY(gemm(h, hl, D, Ly.pw1, glu32 ? (void *)g32 : (void *)gg, nullptr, D, glu32 ? 0 : 1, FA_ACT_NONE, nullptr, 1, hl ? "pw1_glu_x" : (glu32 ? "pw1_glu_f32" : "pw1_glu")));
+      _Float16 *dlo = (ex & FA_EXACT_DW_OUT) ? alo : nullptr;
+      {
+        ProfScope ps(ctx, glu32 ? (dlo ? "dwconv_x" : "dwconv_f32") : (dlo ? "dwconv_lo" : "dwconv"));
+        const int thr = std::min(64, D / 8);
+        const dim3 grid(cdiv(mx[3], 4), n, cdiv(D / 8, thr));
+        if (glu32)
+          FA_LAUNCH(ps, (dwconv_silu_kernel<9, 4, float>), grid, dim3(thr), 0, ctx->stream, (const float *)g32, a, dlo, Ly.dww, Ly.dwb, D, s3);
+        else
+          FA_LAUNCH(ps, (dwconv_silu_kernel<9, 4, _Float16>), grid, dim3(thr), 0, ctx->stream, (const _Float16 *)gg, a, dlo, Ly.dww, Ly.dwb, D, s3);
+        FA_TRY(check_launch(ctx, "dwconv"));
+      }
+      FA_TRY(gemm(a, dlo, D, Ly.pw2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, dlo ? "pw2_x" : "pw2"));
+      // FF2 + norm_out
+      FA_TRY(ln(3, Ly, hl ? "ln_ff2_x" : "ln_ff2"));
+      FA_TRY(gemm(h, hl, D, Ly.ff2w1, u, ul, c.DFF, 1, FA_ACT_SILU, nullptr, 0, hl ? "ff2_w1_x" : (ul ? "ff2_w1_u" : "ff2_w1")));
+      FA_TRY(gemm(u, ul, c.DFF, Ly.ff2w2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, ul ? "ff2_w2_x" : "ff2_w2"));
+      if (D == 1024) {
+        ProfScope ps(ctx, "ln_out");
+        FA_LAUNCH(ps, enc_ln_f32_kernel<4>, dim3(cdiv(M, 4)), dim3(256), 0, ctx->stream, x, Ly.ln[4][0], Ly.ln[4][1], M, 1e-5f);
+        FA_TRY(check_launch(ctx, "ln_out"));
+      } else {
+        FA_TRY(layernorm_launch(ctx, x, Ly.ln[4][0], Ly.ln[4][1], x, 0, M, D, D, D, 1e-5f, "ln_out"));
+      }
+    }
+    if (layout == 1) {
+      ProfScope ps(ctx, "zero_pad");
+      FA_LAUNCH(ps, zero_pad_rows_kernel, dim3(mx[3], n), dim3(256), 0, ctx->stream, x, D, s3, mx[3]);
+      FA_TRY(check_launch(ctx, "zero_pad"));
+    }
+    return FA_OK;
+  };
+  const char *ge = getenv("FA_GRAPH");
+  if (ctx->prof_on || (ge && ge[0] == '0')) {
+    FA_TRY(launch_all());
+    *out = ox;
+    return FA_OK;
   }
-  if (layout == 1) {
-    ProfScope ps(ctx, "zero_pad");
-    FA_LAUNCH(ps, zero_pad_rows_kernel, dim3(mx[3], n), dim3(256), 0, ctx->stream, x, D, s3, mx[3]);
-    FA_TRY(check_launch(ctx, "zero_pad"));
+  std::vector<int64_t> key = {(int64_t)e->ws_gen, layers, n, layout, (int64_t)(intptr_t)rm->ptr, (int64_t)(intptr_t)x};
+  key.insert(key.end(), lens, lens + n);
+  fa_encoder::Captured *hit = nullptr;
+  for (auto &g : e->graphs)
+    if (g.key == key) hit = &g;
+  if (!hit) {
+    FA_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    const int st = launch_all();
+    hipGraph_t graph = nullptr;
+    const hipError_t ce = hipStreamEndCapture(ctx->stream, &graph);
+    if (st != FA_OK) {
+      if (graph) (void)hipGraphDestroy(graph);
+      return st;
+    }
+    if (ce != hipSuccess) return set_err(ctx, FA_E_DEVICE, "encoderForward: graph capture: %s", hipGetErrorString(ce));
+    hipGraphExec_t exec = nullptr;
+    const hipError_t ie = hipGraphInstantiateWithFlags(&exec, graph, 0);
+    (void)hipGraphDestroy(graph);
+    if (ie != hipSuccess) return set_err(ctx, FA_E_DEVICE, "encoderForward: graph instantiate: %s", hipGetErrorString(ie));
+    constexpr size_t kMaxGraphs = 8;
+    if (e->graphs.size() >= kMaxGraphs) {  // evict the least recently used
+      size_t lru = 0;
+      for (size_t i = 1; i < e->graphs.size(); i++)
+        if (e->graphs[i].used < e->graphs[lru].used) lru = i;
+      (void)hipGraphExecDestroy(e->graphs[lru].exec);
+      e->graphs.erase(e->graphs.begin() + lru);
+    }
+    e->graphs.push_back({key, exec, 0});
+    hit = &e->graphs.back();
   }
+  hit->used = ++e->graph_clock;
+  FA_HIP(ctx, hipGraphLaunch(hit->exec, ctx->stream));
   *out = ox;
   return FA_OK;
 }

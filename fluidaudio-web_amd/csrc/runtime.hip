@@ -174,9 +174,27 @@ static hipEvent_t take_event(fa_ctx *ctx) {
   return e;
 }
 
+// Profile filter: comma-separated entries, each an exact label or, ending in
+// '*', a label prefix.
+static bool prof_match(const std::string &filter, const char *label) {
+  size_t i = 0;
+  while (i <= filter.size()) {
+    size_t j = filter.find(',', i);
+    if (j == std::string::npos) j = filter.size();
+    if (j > i) {
+      const bool prefix = filter[j - 1] == '*';
+      const size_t len = j - i - (prefix ? 1 : 0);
+      if (prefix ? std::strncmp(label, filter.c_str() + i, len) == 0 : (std::strlen(label) == len && std::strncmp(label, filter.c_str() + i, len) == 0))
+        return true;
+    }
+    i = j + 1;
+  }
+  return false;
+}
+
 ProfScope::ProfScope(fa_ctx *c, const char *label, bool ext_launch) : ctx(c), idx(-1), ext(ext_launch) {
   if (!ctx->prof_on || (int)ctx->prof.size() >= ctx->prof_max) return;
-  if (!ctx->prof_filter.empty() && std::strncmp(label, ctx->prof_filter.c_str(), ctx->prof_filter.size()) != 0) return;
+  if (!ctx->prof_filter.empty() && !prof_match(ctx->prof_filter, label)) return;
   ProfRec r;
   std::snprintf(r.label, sizeof r.label, "%s", label);
   r.a = take_event(ctx);

@@ -154,11 +154,12 @@ int fa_row_bias_act(fa_ctx *ctx, fa_tensor x, fa_tensor bias, int act, fa_tensor
  * (label, milliseconds) and the number recorded in *count. */
 int fa_profile_start(fa_ctx *ctx, int max_ops);
 int fa_profile_end(fa_ctx *ctx, int cap, char (*labels)[48], float *ms, int *count);
-/* Restrict the open profile to launches whose label starts with `prefix`
+/* Restrict the open profile to some launches: `filter` is a comma-separated
+ * list of exact labels, an entry ending in '*' matching a label prefix
  * (NULL or "" = every launch).  Fewer bracketing events perturb the stream
  * less; this is how a benchmark times one kernel inside a full forward.  No
  * reference counterpart (an extension of startProfile). */
-int fa_profile_only(fa_ctx *ctx, const char *prefix);
+int fa_profile_only(fa_ctx *ctx, const char *filter);
 
 /* ── weight-only quantised formats (no single reference function: the
  * quantiser is scripts/quantize-parakeet-encoder.py:31-36, the dequant

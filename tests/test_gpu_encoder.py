@@ -70,3 +70,32 @@ def test_quantized_encoder_tracks_f16(ctx, fa, small, fmt, tol):
     assert rel_l2(b, a) <= tol
     e16.close()
     eq.close()
+
+
+def test_graph_replay_equals_eager(ctx, fa, small, monkeypatch):
+    """The captured forward (hipGraph, replayed per signature) must give the
+    eager forward's bits on every replay, with eager library work and
+    synchronisations between replays, for two signatures in turn."""
+    enc = fa.FusedEncoder(ctx, small, "f16", max_T=128)
+    sets = [fa.synth.make_features(128, 300, seed=7, W=3), fa.synth.make_features(128, 177, seed=8, W=2)]
+    monkeypatch.setenv("FA_GRAPH", "0")
+    eager = [enc.encode(m) for m in sets]
+    monkeypatch.setenv("FA_GRAPH", "1")
+    feats = []
+    for m in sets:  # resident inputs so the signature (tensor addresses) repeats
+        lens = [x.shape[1] for x in m]
+        stream = np.concatenate(m, axis=1)
+        f = ctx.upload(stream, stream.shape[0], stream.shape[1])
+        starts = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int32)
+        feats.append((f, starts, np.asarray(lens, np.int32), ctx.packWindows(f, starts, lens, "packed")))
+    a = np.ones((64, 64), np.float32)
+    for rep in range(3):
+        for (f, starts, lens, packed), ref in zip(feats, eager):
+            y = enc.forward(packed, lens, "packed")
+            got = ctx.download(y).reshape(y.rows, y.cols)
+            ctx.freeTensor(y)
+            want = np.concatenate(ref)
+            assert np.array_equal(got, want), f"replay {rep}: max diff {np.abs(got - want).max()}"
+            ctx.download(ctx.matmul(ctx.upload(a, 64, 64), ctx.upload(a, 64, 64)))  # eager work in between
+            ctx.sync()
+    enc.close()
