@@ -5,8 +5,8 @@
 // waves) owns 16 output columns; the K range is split across its waves and
 // each wave streams 64-k chunks of its 16 weight rows (K-major storage: a
 // column's weights are contiguous), dequantises them in registers and feeds a
-// v_mfma_f32_16x16x32_f16 with the activations staged once in LDS as f16
-// (rows >= M are zero).  MFMA keeps the M=16 case off the VALU; for M=1/4 the
+// v_mfma_f32_16x16x32_f16 whose A fragments are the activations read straight
+// from global as f16 (rows >= M are zero).  MFMA keeps the M=16 case off the VALU; for M=1/4 the
 // unused MFMA rows are free next to the memory time.  Partial tiles are
 // summed through LDS, then scale/bias/act are applied.
 //
@@ -38,55 +38,85 @@ struct GemvArgs {
   int act;
 };
 
+// 16 output columns per workgroup; wave w takes the 64-k chunks w, w+4, ...
+// All of a lane's weight loads (16 k of its column per chunk) are issued
+// before any MFMA so the workgroup's whole weight slice is in flight at once;
+// the activations are read straight from global (L1/L2: every workgroup reads
+// the same M x K block) as MFMA A fragments, rows >= M being register zeros.
+template <int FMT>
+__device__ __forceinline__ void gemv_dequant(const GemvArgs &p, int n, int kb, const uint4 &u8, const uint2 &u4, h8 &b0, h8 &b1) {
+  if constexpr (FMT == 1) {
+    const uint32_t w[4] = {u8.x, u8.y, u8.z, u8.w};
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      b0[e] = (_Float16)(float)(int8_t)((w[e >> 2] >> (8 * (e & 3))) & 0xff);
+      b1[e] = (_Float16)(float)(int8_t)((w[2 + (e >> 2)] >> (8 * (e & 3))) & 0xff);
+    }
+  } else {
+    const int blk = kb >> 5, nblk = p.K >> 5;
+    float s, zp = 8.f;
+    if constexpr (FMT == 2) {
+      s = (float)reinterpret_cast<const _Float16 *>(p.scales)[(size_t)n * nblk + blk];
+    } else {
+      s = reinterpret_cast<const float *>(p.scales)[(size_t)n * nblk + blk];
+      const uint8_t zb = p.zp[(size_t)n * p.zpb + (blk >> 1)];
+      zp = (float)((blk & 1) ? (zb >> 4) : (zb & 0xf));
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      b0[e] = (_Float16)(((float)((u4.x >> (4 * e)) & 0xf) - zp) * s);
+      b1[e] = (_Float16)(((float)((u4.y >> (4 * e)) & 0xf) - zp) * s);
+    }
+  }
+}
+
+__device__ __forceinline__ h8 gemv_a8(const float *a) {
+  const float4 x = reinterpret_cast<const float4 *>(a)[0], y = reinterpret_cast<const float4 *>(a)[1];
+  return h8{(_Float16)x.x, (_Float16)x.y, (_Float16)x.z, (_Float16)x.w, (_Float16)y.x, (_Float16)y.y, (_Float16)y.z, (_Float16)y.w};
+}
+
 template <int FMT>
 __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs p) {
-  extern __shared__ __attribute__((aligned(16))) _Float16 sA[];  // [16][K + 8]
+  constexpr int CB = 4;  // chunks per wave held in flight together
   __shared__ f4 sPart[4][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n0 = blockIdx.x * 16;
-  const int LK = p.K + 8;
-  // stage activations as f16, rows >= M zero
-  for (int e = tid; e < 16 * p.K; e += 256) {
-    const int m = e / p.K, k = e % p.K;
-    sA[m * LK + k] = m < p.M ? (_Float16)p.A[(size_t)m * p.K + k] : (_Float16)0.f;
-  }
-  __syncthreads();
   const int c16 = lane & 15, g = lane >> 4;
   const int n = min(n0 + c16, p.N - 1);
+  const bool arow = c16 < p.M;
+  const float *arow_p = p.A + (size_t)min(c16, p.M - 1) * p.K;
   f4 acc = f4{0.f, 0.f, 0.f, 0.f};
   const int nch = p.K / 64;
-  for (int ch = wave; ch < nch; ch += 4) {
-    const int kb = ch * 64 + g * 16;  // this lane's 16 k values (one int4 group half)
-    h8 b0, b1;
-    if constexpr (FMT == 1) {
-      const uint4 u = *reinterpret_cast<const uint4 *>(reinterpret_cast<const int8_t *>(p.W) + (size_t)n * p.K + kb);
-      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+  for (int c0 = wave; c0 < nch; c0 += 4 * CB) {
+    uint4 w8[CB];
+    uint2 w4[CB];
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
-        b0[e] = (_Float16)(float)(int8_t)((w[e >> 2] >> (8 * (e & 3))) & 0xff);
-        b1[e] = (_Float16)(float)(int8_t)((w[2 + (e >> 2)] >> (8 * (e & 3))) & 0xff);
-      }
-    } else {
-      const uint2 u = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint8_t *>(p.W) + (size_t)n * (p.K >> 1) + (kb >> 1));
-      const int blk = kb >> 5, nblk = p.K >> 5;
-      float s, zp = 8.f;
-      if constexpr (FMT == 2) {
-        s = (float)reinterpret_cast<const _Float16 *>(p.scales)[(size_t)n * nblk + blk];
-      } else {
-        s = reinterpret_cast<const float *>(p.scales)[(size_t)n * nblk + blk];
-        const uint8_t zb = p.zp[(size_t)n * p.zpb + (blk >> 1)];
-        zp = (float)((blk & 1) ? (zb >> 4) : (zb & 0xf));
-      }
-#pragma unroll
-      for (int e = 0; e < 8; e++) {
-        b0[e] = (_Float16)(((float)((u.x >> (4 * e)) & 0xf) - zp) * s);
-        b1[e] = (_Float16)(((float)((u.y >> (4 * e)) & 0xf) - zp) * s);
+    for (int i = 0; i < CB; i++) {
+      const int ch = c0 + 4 * i;
+      if (ch < nch) {
+        const int kb = ch * 64 + g * 16;
+        if constexpr (FMT == 1)
+          w8[i] = *reinterpret_cast<const uint4 *>(reinterpret_cast<const int8_t *>(p.W) + (size_t)n * p.K + kb);
+        else
+          w4[i] = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint8_t *>(p.W) + (size_t)n * (p.K >> 1) + (kb >> 1));
       }
     }
-    const h8 a0 = *reinterpret_cast<const h8 *>(&sA[c16 * LK + kb]);
-    const h8 a1 = *reinterpret_cast<const h8 *>(&sA[c16 * LK + kb + 8]);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b0, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b1, acc, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < CB; i++) {
+      const int ch = c0 + 4 * i;
+      if (ch < nch) {
+        const int kb = ch * 64 + g * 16;
+        h8 b0, b1;
+        gemv_dequant<FMT>(p, n, kb, w8[i], w4[i], b0, b1);
+        h8 a0 = h8{0, 0, 0, 0, 0, 0, 0, 0}, a1 = a0;
+        if (arow) {
+          a0 = gemv_a8(arow_p + kb);
+          a1 = gemv_a8(arow_p + kb + 8);
+        }
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b0, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b1, acc, 0, 0, 0);
+      }
+    }
   }
   sPart[wave][lane] = acc;
   __syncthreads();
@@ -143,10 +173,10 @@ __global__ void gemv_naive_kernel(GemvArgs p, int fmt) {
 
 static int gemv_launch(fa_ctx *ctx, const GemvArgs &p, int fmt, const char *label) {
   if (p.M <= 0 || p.N <= 0) return FA_OK;
-  const bool single = !(p.M > 16 && p.M <= 64 && p.K % 64 == 0 && (size_t)16 * (p.K + 8) * 2 <= 64 * 1024);
+  const bool single = !(p.M > 16 && p.M <= 64 && p.K % 64 == 0);
   ProfScope ps(ctx, label, single);
-  if (p.M <= 16 && p.K % 64 == 0 && (size_t)16 * (p.K + 8) * 2 <= 64 * 1024) {
-    const size_t shm = (size_t)16 * (p.K + 8) * 2;
+  if (p.M <= 16 && p.K % 64 == 0) {
+    const size_t shm = 0;
     const dim3 grid(cdiv(p.N, 16));
     if (fmt == 1)
       FA_LAUNCH(ps, gemv_mfma_kernel<1>, grid, dim3(256), shm, ctx->stream, p);
@@ -154,14 +184,14 @@ static int gemv_launch(fa_ctx *ctx, const GemvArgs &p, int fmt, const char *labe
       FA_LAUNCH(ps, gemv_mfma_kernel<2>, grid, dim3(256), shm, ctx->stream, p);
     else
       FA_LAUNCH(ps, gemv_mfma_kernel<3>, grid, dim3(256), shm, ctx->stream, p);
-  } else if (p.M <= 64 && p.K % 64 == 0 && (size_t)16 * (p.K + 8) * 2 <= 64 * 1024) {
+  } else if (p.M <= 64 && p.K % 64 == 0) {
     // M in (16, 64]: run 16-row slabs
     for (int m0 = 0; m0 < p.M; m0 += 16) {
       GemvArgs q = p;
       q.A = p.A + (size_t)m0 * p.K;
       q.Y = p.Y + (size_t)m0 * p.N;
       q.M = p.M - m0 < 16 ? p.M - m0 : 16;
-      const size_t shm = (size_t)16 * (p.K + 8) * 2;
+      const size_t shm = 0;
       if (fmt == 1)
         hipLaunchKernelGGL(gemv_mfma_kernel<1>, dim3(cdiv(p.N, 16)), dim3(256), shm, ctx->stream, q);
       else if (fmt == 2)
