@@ -19,7 +19,8 @@ The JSON line also carries
                 conformer layer at full dims, scaled to 24 layers.
 
 Other workloads (--workload): layer, ragged,
-gemv (configs[4] GEMV), quant (configs[4] encoder).
+gemv (configs[4] GEMV), quant / quant4 (configs[4] encoder, int8 / int4
+weights), copy (counter calibration).
 """
 from __future__ import annotations
 
@@ -201,7 +202,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="encoder", choices=["encoder", "layer", "ragged", "quant", "gemv", "copy"])
+    ap.add_argument("--workload", default="encoder", choices=["encoder", "layer", "ragged", "quant", "quant4", "gemv", "copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -215,7 +216,7 @@ def main():
         return bench_copy(args, fa, ctx)
     cfg = dict(FULL)
     layout = "packed"
-    if args.workload in ("encoder", "quant"):
+    if args.workload in ("encoder", "quant", "quant4"):
         lens = [1500] * 16
         workload = ("configs[2]: 24-layer FastConformer encoder + dw-striding 8x subsampling, 16 windows x 15 s "
                     "(1500 mel frames), packed on-GPU")
@@ -229,7 +230,7 @@ def main():
         starts, lens = fa.windowing.planRaggedWindows(360000, 200, 3000, 100, seed=1)
         lens = list(lens[:32])
         workload = "configs[3] batch: 32 ragged windows (2-30 s) cut from the 3600 s stream, packed"
-    fmt = "int8" if args.workload == "quant" else "f16"
+    fmt = {"quant": "int8", "quant4": "int4"}.get(args.workload, "f16")
     wall, prof_all, dom, prof_dom = run_encoder(args, fa, ctx, cfg, lens, layout, fmt)
     audio_s = sum(lens) * 0.01 * args.steps
     work = kernel_work(cfg, lens, layout)

@@ -340,17 +340,33 @@ struct LdsStage {
   char d[BYTES];
 };
 
+// int8 weights -> f16 pairs, exactly: with x = w ^ 0x80808080 each byte is
+// b + 128, and the f16 with bits 0x64XX is 1024 + XX, so two byte_perms and a
+// packed f16 subtract of 1152 give b for four bytes.
+__device__ __forceinline__ h8 i8x8_to_h8(uint2 w) {
+  const uint32_t x0 = w.x ^ 0x80808080u, x1 = w.y ^ 0x80808080u;
+  const h2 off = h2{(_Float16)1152.f, (_Float16)1152.f};
+  const h2 a = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u)) - off;
+  const h2 b = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, x0, 0x04030402u)) - off;
+  const h2 c = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u)) - off;
+  const h2 d = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u)) - off;
+  return h8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
 // LO = 1: A arrives as two f16 planes (A = hi + lo exactly); both are staged
 // and each B fragment feeds two MFMAs, so the product carries f32-accurate A.
-template <int BM, int BN, int WM, int WN, int S, int EPI, int LO = 0>
+// B8 = 1: B is int8 K-major (per-column scale in the epilogue); its K tile is
+// 64 bytes per row (16-byte chunk c at slot c ^ ((row >> 1) & 3)) and each
+// fragment is widened to f16 exactly after the LDS read.
+template <int BM, int BN, int WM, int WN, int S, int EPI, int LO = 0, int B8 = 0>
 __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4))) void gemm_dma_kernel(GemmArgs p) {
-  constexpr int NW = WM * WN, BK = 64, RB = 128;
+  constexpr int NW = WM * WN, BK = 64, RB = 128, RBB = B8 ? 64 : 128;
   constexpr int WTM = BM / WM, WTN = BN / WN, TI = WTM / 16, TJ = WTN / 16;
   constexpr int AR = BM * (1 + LO);                   // staged A rows: hi (and lo) planes
-  constexpr int SA = AR * RB, STG = (AR + BN) * RB;
-  constexpr int IT = (AR + BN) / 8;                   // 1 KB copies per stage (8 rows each)
+  constexpr int SA = AR * RB, STG = AR * RB + BN * RBB;
+  constexpr int ITA = AR / 8, IT = ITA + BN * RBB / 1024;  // 1 KB copies per stage (A: 8 rows each; B: 8 or 16 rows)
   constexpr int IW = (IT + NW - 1) / NW, IMIN = IT / NW;  // per wave: at most / at least
-  static_assert(BM % 16 == 0 && BN % 16 == 0 && NW % 4 == 0, "tile shape");
+  static_assert(BM % 16 == 0 && BN % 16 == 0 && NW % 4 == 0 && (BN * RBB) % 1024 == 0, "tile shape");
   static_assert(S >= 2 && S <= 4 && S * STG <= 160 * 1024, "LDS stages");  // gfx950: 160 KiB per workgroup
   static_assert(NW * 16 * (WTN + 4) * 4 <= STG, "epilogue strips must fit in stage 0");
   __shared__ __attribute__((aligned(1024))) LdsStage<STG> st0, st1, st2, st3;
@@ -371,25 +387,34 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
   const int m0 = (grp * GM + gi % gm) * BM, n0 = (gi / gm) * BN;
   const _Float16 *A = reinterpret_cast<const _Float16 *>(p.A), *B = reinterpret_cast<const _Float16 *>(p.B);
 
-  // copy i of this wave moves rows [ins*8, ins*8+8) of the stacked A|B tile
-  const _Float16 *src[IW];
-  const int lr = lane >> 3, lch = lane & 7;
+  // copy i of this wave: an A copy moves rows [ins*8, ins*8+8) of the stacked
+  // A (hi | lo) tile, a B copy 8 (f16) or 16 (int8) rows of the B tile
+  const void *src[IW];
 #pragma unroll
   for (int i = 0; i < IW; i++) {
-    const int r = (wave + i * NW) * 8 + lr;
-    const int ch = lch ^ (r & 7);
-    if (r < BM)
-      src[i] = A + (size_t)min(m0 + r, p.M - 1) * p.lda + ch * 8;  // rows past M repeat the last row; never stored
-    else if (r < AR)
-      src[i] = reinterpret_cast<const _Float16 *>(p.Alo) + (size_t)min(m0 + r - BM, p.M - 1) * p.lda + ch * 8;
-    else
-      src[i] = B + (size_t)(n0 + r - AR) * p.K + ch * 8;
+    const int ins = wave + i * NW;
+    if (ins < ITA) {
+      const int r = ins * 8 + (lane >> 3), ch = (lane & 7) ^ (r & 7);
+      if (r < BM)
+        src[i] = A + (size_t)min(m0 + r, p.M - 1) * p.lda + ch * 8;  // rows past M repeat the last row; never stored
+      else
+        src[i] = reinterpret_cast<const _Float16 *>(p.Alo) + (size_t)min(m0 + r - BM, p.M - 1) * p.lda + ch * 8;
+    } else if constexpr (B8) {
+      const int r = (ins - ITA) * 16 + (lane >> 2), ch = (lane & 3) ^ ((r >> 1) & 3);
+      src[i] = reinterpret_cast<const int8_t *>(p.B) + (size_t)(n0 + r) * p.K + ch * 16;
+    } else {
+      const int r = (ins - ITA) * 8 + (lane >> 3), ch = (lane & 7) ^ (r & 7);
+      src[i] = B + (size_t)(n0 + r) * p.K + ch * 8;
+    }
   }
   auto issue = [&](int sidx, int k0) {
 #pragma unroll
     for (int i = 0; i < IW; i++) {
       const int ins = wave + i * NW;
-      if (IT % NW == 0 || ins < IT) dma16(src[i] + k0, sadr[sidx] + ins * 1024);
+      if (IT % NW == 0 || ins < IT) {
+        const size_t koff = (ins < ITA || !B8) ? (size_t)k0 * 2 : (size_t)k0;  // bytes
+        dma16(reinterpret_cast<const char *>(src[i]) + koff, sadr[sidx] + ins * 1024);
+      }
     }
   };
 
@@ -405,7 +430,8 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
     if (s < nk) issue(s, s * BK);
 
   const int q = lane >> 4, sw = lane & 7;  // fragment rows are 16-aligned + (lane & 15)
-  const int abase = (wm * WTM + (lane & 15)) * RB, bbase = SA + (wn * WTN + (lane & 15)) * RB;
+  const int abase = (wm * WTM + (lane & 15)) * RB, bbase = SA + (wn * WTN + (lane & 15)) * RBB;
+  const int sw8 = ((lane & 15) >> 1) & 3;  // int8 B rows: (row >> 1) & 3
   h8 af[2][TI], bf[2][TJ], al[2][LO ? TI : 1];
   auto rdfrag = [&](int sidx, int ks, int slot) {
     const char *base = stg[sidx];
@@ -416,8 +442,15 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
 #pragma unroll
       for (int i = 0; i < TI; i++) al[slot][i] = *reinterpret_cast<const h8 *>(base + BM * RB + abase + i * 16 * RB + so);
     }
+    if constexpr (B8) {
+      // k = ks*32 + q*8: 16-byte chunk 2*ks + q/2, half q & 1
+      const int so8 = ((((ks * 2 + (q >> 1)) ^ sw8) * 16) + (q & 1) * 8);
 #pragma unroll
-    for (int j = 0; j < TJ; j++) bf[slot][j] = *reinterpret_cast<const h8 *>(base + bbase + j * 16 * RB + so);
+      for (int j = 0; j < TJ; j++) bf[slot][j] = i8x8_to_h8(*reinterpret_cast<const uint2 *>(base + bbase + j * 16 * RBB + so8));
+    } else {
+#pragma unroll
+      for (int j = 0; j < TJ; j++) bf[slot][j] = *reinterpret_cast<const h8 *>(base + bbase + j * 16 * RB + so);
+    }
   };
   auto mma = [&](int slot) {
 #pragma unroll
@@ -637,11 +670,11 @@ static int pick_dma(fa_ctx *ctx, const GemmArgs &p) {
   return best;
 }
 
-template <int BM, int BN, int WM, int WN, int S, int EPI, int LO = 0>
+template <int BM, int BN, int WM, int WN, int S, int EPI, int LO = 0, int B8 = 0>
 static int launch_dma(fa_ctx *ctx, const GemmArgs &p, const char *label) {
   const unsigned tiles = cdiv(p.M, BM) * (p.N / BN);
   ProfScope ps(ctx, label);
-  FA_LAUNCH(ps, (gemm_dma_kernel<BM, BN, WM, WN, S, EPI, LO>), dim3(tiles), dim3(64 * WM * WN), 0, ctx->stream, p);
+  FA_LAUNCH(ps, (gemm_dma_kernel<BM, BN, WM, WN, S, EPI, LO, B8>), dim3(tiles), dim3(64 * WM * WN), 0, ctx->stream, p);
   return check_launch(ctx, label);
 }
 
@@ -665,6 +698,15 @@ static int launch_tile(fa_ctx *ctx, const GemmArgs &p, const char *label) {
       case 3: return launch_dma<96, 128, 2, 4, 4, EPI>(ctx, p, label);
       default: break;
     }
+  }
+  if constexpr (AK == A_F16 && BKND == B_I8 && EPI != EPI_GENERIC) {
+    if (!p.Alo) switch (pick_dma(ctx, p)) {  // int8 weights: same tile table, half the B bytes
+        case 0: return launch_dma<192, 256, 2, 4, 2, EPI, 0, 1>(ctx, p, label);
+        case 1: return launch_dma<192, 128, 2, 4, 3, EPI, 0, 1>(ctx, p, label);
+        case 2: return launch_dma<128, 128, 2, 4, 4, EPI, 0, 1>(ctx, p, label);
+        case 3: return launch_dma<96, 128, 2, 4, 4, EPI, 0, 1>(ctx, p, label);
+        default: break;
+      }
   }
   if (p.Alo) return set_err(ctx, FA_E_UNSUPPORTED, "%s: lo plane needs the f16 x f16 route", label);
   if constexpr (AK == A_F32 || EPI == EPI_GENERIC) {  // ComputeContext path: mid-size tiles

@@ -99,3 +99,18 @@ def test_graph_replay_equals_eager(ctx, fa, small, monkeypatch):
             ctx.download(ctx.matmul(ctx.upload(a, 64, 64), ctx.upload(a, 64, 64)))  # eager work in between
             ctx.sync()
     enc.close()
+
+
+def test_int8_direct_to_lds_route_matches_staged_route(ctx, fa, small, monkeypatch):
+    """int8 weights through the direct-to-LDS GEMM (raw int8 tiles, exact
+    int8 -> f16 widening after the LDS read) give the same bits as the
+    register-staged dequant route: both accumulate f16(a) * q over the same
+    K order in f32 and scale the column in the epilogue."""
+    mels = fa.synth.make_features(128, 300, seed=9, W=2)
+    eq = fa.FusedEncoder(ctx, small, "int8", max_T=128)
+    monkeypatch.setenv("FA_GRAPH", "0")
+    fast = np.concatenate(eq.encode(mels))
+    monkeypatch.setenv("FA_GEMM_DMA", "0")
+    staged = np.concatenate(eq.encode(mels))
+    eq.close()
+    assert np.array_equal(fast, staged), float(np.abs(fast - staged).max())
