@@ -308,10 +308,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_kernel(GemmArgs p) {
   epilogue<WTM, WTN, TI, TJ, EPI>(p, acc, reinterpret_cast<float *>(&sA[0][0]), m0 + wm * WTM, n0 + wn * WTN, wave, lane);
 }
 
-// ── direct-to-LDS multi-stage f16 GEMM (A f16, B f16 K-major) ──────────────
+// ── direct-to-LDS multi-stage GEMM (A f16, B f16 / int8 / int4 K-major) ────
 // The encoder's hot path.  Each K tile (64 halfs = 128 B per row) of the
 // stacked A|B panel is copied global->LDS by global_load_lds_dwordx4 (no VGPR
-// staging), S tiles in flight, one LDS array per stage.  Within a 128-byte
+// staging), S tiles in flight in one LDS buffer.  Within a 128-byte
 // row the 16-byte chunk c of row r lives in slot c ^ (r & 7), so the eight
 // rows one ds_read_b128 phase touches hit distinct banks and each 8-lane group
 // of a copy still reads one contiguous 128-byte row segment.  8-wave
@@ -335,10 +335,6 @@ __device__ __forceinline__ void wait_vmcnt() {  // gfx9 s_waitcnt: vmcnt [3:0]+[
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
-template <int BYTES>
-struct LdsStage {
-  char d[BYTES];
-};
 
 // int8 weights -> f16 pairs, exactly: with x = w ^ 0x80808080 each byte is
 // b + 128, and the f16 with bits 0x64XX is 1024 + XX, so two byte_perms and a
@@ -353,28 +349,51 @@ __device__ __forceinline__ h8 i8x8_to_h8(uint2 w) {
   return h8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
+// 8 int4 weights (low nibble = even k) of one group-32 block -> f16
+// (q - 8) * s, rounded once: nibbles are placed under an 0x64 high byte
+// (f16 1024 + q), 1032 is subtracted exactly and the packed f16 multiply by
+// the block scale rounds the exact product -- the value the register-staged
+// route computes in f32 and rounds.
+__device__ __forceinline__ h8 i4x8_to_h8(uint32_t u, _Float16 s) {
+  const uint32_t lo = u & 0x0F0F0F0Fu, hi = (u >> 4) & 0x0F0F0F0Fu;
+  const h2 off = h2{(_Float16)1032.f, (_Float16)1032.f}, sc = h2{s, s};
+  const h2 a = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(hi, lo, 0x0C040C00u) | 0x64006400u) - off) * sc;
+  const h2 b = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(hi, lo, 0x0C050C01u) | 0x64006400u) - off) * sc;
+  const h2 c = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(hi, lo, 0x0C060C02u) | 0x64006400u) - off) * sc;
+  const h2 d = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(hi, lo, 0x0C070C03u) | 0x64006400u) - off) * sc;
+  return h8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
 // LO = 1: A arrives as two f16 planes (A = hi + lo exactly); both are staged
 // and each B fragment feeds two MFMAs, so the product carries f32-accurate A.
-// B8 = 1: B is int8 K-major (per-column scale in the epilogue); its K tile is
+// BQ = 1: B is int8 K-major (per-column scale in the epilogue); its K tile is
 // 64 bytes per row (16-byte chunk c at slot c ^ ((row >> 1) & 3)) and each
 // fragment is widened to f16 exactly after the LDS read.
-template <int BM, int BN, int WM, int WN, int S, int EPI, int LO = 0, int B8 = 0>
+// BQ = 2: B is symmetric int4 group-32 ([N][K/32][16 B], f16 scales [N][K/32]);
+// its K tile is 32 bytes per row (chunk c at slot c ^ ((row >> 2) & 1)), the
+// two block scales of a row's K tile are one 4-byte load made a K tile ahead.
+template <int BM, int BN, int WM, int WN, int S, int EPI, int LO = 0, int BQ = 0>
 __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4))) void gemm_dma_kernel(GemmArgs p) {
-  constexpr int NW = WM * WN, BK = 64, RB = 128, RBB = B8 ? 64 : 128;
+  constexpr int B8 = BQ == 1, B4 = BQ == 2;
+  constexpr int NW = WM * WN, BK = 64, RB = 128, RBB = B8 ? 64 : (B4 ? 32 : 128);
+  static_assert(!B4 || S % 2 == 0, "int4 scale double-buffering follows the stage parity");
   constexpr int WTM = BM / WM, WTN = BN / WN, TI = WTM / 16, TJ = WTN / 16;
   constexpr int AR = BM * (1 + LO);                   // staged A rows: hi (and lo) planes
   constexpr int SA = AR * RB, STG = AR * RB + BN * RBB;
   constexpr int ITA = AR / 8, IT = ITA + BN * RBB / 1024;  // 1 KB copies per stage (A: 8 rows each; B: 8 or 16 rows)
   constexpr int IW = (IT + NW - 1) / NW, IMIN = IT / NW;  // per wave: at most / at least
   static_assert(BM % 16 == 0 && BN % 16 == 0 && NW % 4 == 0 && (BN * RBB) % 1024 == 0, "tile shape");
-  static_assert(S >= 2 && S <= 4 && S * STG <= 160 * 1024, "LDS stages");  // gfx950: 160 KiB per workgroup
-  static_assert(NW * 16 * (WTN + 4) * 4 <= STG, "epilogue strips must fit in stage 0");
-  __shared__ __attribute__((aligned(1024))) LdsStage<STG> st0, st1, st2, st3;
-  char *const stg[4] = {st0.d, st1.d, st2.d, st3.d};
+  static_assert(S >= 2 && S <= 4, "LDS stages");
+  constexpr int STRIPS = NW * 16 * (WTN + 4) * 4;  // epilogue strips reuse the stage buffer
+  constexpr int SMEM = S * STG > STRIPS ? S * STG : STRIPS;
+  static_assert(SMEM <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(1024))) char smem[SMEM];
   uint32_t sadr[4];
+  {
+    const uint32_t s0 = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)smem);
 #pragma unroll
-  for (int i = 0; i < 4; i++) sadr[i] = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)stg[i]);
-
+    for (int i = 0; i < 4; i++) sadr[i] = s0 + i * STG;
+  }
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const int nTN = p.N / BN, nTM = (p.M + BM - 1) / BM;
@@ -402,6 +421,9 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
     } else if constexpr (B8) {
       const int r = (ins - ITA) * 16 + (lane >> 2), ch = (lane & 3) ^ ((r >> 1) & 3);
       src[i] = reinterpret_cast<const int8_t *>(p.B) + (size_t)(n0 + r) * p.K + ch * 16;
+    } else if constexpr (B4) {
+      const int r = (ins - ITA) * 32 + (lane >> 1), ch = (lane & 1) ^ ((r >> 2) & 1);
+      src[i] = reinterpret_cast<const uint8_t *>(p.B) + (size_t)(n0 + r) * (p.K >> 1) + ch * 16;
     } else {
       const int r = (ins - ITA) * 8 + (lane >> 3), ch = (lane & 7) ^ (r & 7);
       src[i] = B + (size_t)(n0 + r) * p.K + ch * 8;
@@ -412,7 +434,7 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
     for (int i = 0; i < IW; i++) {
       const int ins = wave + i * NW;
       if (IT % NW == 0 || ins < IT) {
-        const size_t koff = (ins < ITA || !B8) ? (size_t)k0 * 2 : (size_t)k0;  // bytes
+        const size_t koff = (ins < ITA || !BQ) ? (size_t)k0 * 2 : (B8 ? (size_t)k0 : (size_t)(k0 >> 1));  // bytes
         dma16(reinterpret_cast<const char *>(src[i]) + koff, sadr[sidx] + ins * 1024);
       }
     }
@@ -432,9 +454,21 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
   const int q = lane >> 4, sw = lane & 7;  // fragment rows are 16-aligned + (lane & 15)
   const int abase = (wm * WTM + (lane & 15)) * RB, bbase = SA + (wn * WTN + (lane & 15)) * RBB;
   const int sw8 = ((lane & 15) >> 1) & 3;  // int8 B rows: (row >> 1) & 3
+  const int sw4 = ((lane & 15) >> 2) & 1;  // int4 B rows: (row >> 2) & 1
   h8 af[2][TI], bf[2][TJ], al[2][LO ? TI : 1];
-  auto rdfrag = [&](int sidx, int ks, int slot) {
-    const char *base = stg[sidx];
+  // int4 block scales of the K tile being read, two sets by tile parity
+  uint32_t scs[2][B4 ? TJ : 1];
+  auto ldscale = [&](int set, int kt) {
+    if constexpr (B4) {
+      const int nblk = p.K >> 5;
+#pragma unroll
+      for (int j = 0; j < TJ; j++)
+        scs[set][j] = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const _Float16 *>(p.bscale) +
+                                                          (size_t)(n0 + wn * WTN + j * 16 + (lane & 15)) * nblk + 2 * kt);
+    }
+  };
+  auto rdfrag = [&](int sidx, int ks, int slot, int set) {
+    const char *base = smem + sidx * STG;
     const int so = ((ks * 4 + q) ^ sw) * 16;
 #pragma unroll
     for (int i = 0; i < TI; i++) af[slot][i] = *reinterpret_cast<const h8 *>(base + abase + i * 16 * RB + so);
@@ -447,6 +481,15 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
       const int so8 = ((((ks * 2 + (q >> 1)) ^ sw8) * 16) + (q & 1) * 8);
 #pragma unroll
       for (int j = 0; j < TJ; j++) bf[slot][j] = i8x8_to_h8(*reinterpret_cast<const uint2 *>(base + bbase + j * 16 * RBB + so8));
+    } else if constexpr (B4) {
+      // k = ks*32 + q*8: 16-byte chunk ks (block ks of the tile), 4 bytes at q*4
+      const int so4 = ((ks ^ sw4) * 16) + q * 4;
+#pragma unroll
+      for (int j = 0; j < TJ; j++) {
+        const uint32_t sw2 = scs[set][j];
+        const _Float16 sc = __builtin_bit_cast(_Float16, (uint16_t)(ks ? (sw2 >> 16) : (sw2 & 0xffffu)));
+        bf[slot][j] = i4x8_to_h8(*reinterpret_cast<const uint32_t *>(base + bbase + j * 16 * RBB + so4), sc);
+      }
     } else {
 #pragma unroll
       for (int j = 0; j < TJ; j++) bf[slot][j] = *reinterpret_cast<const h8 *>(base + bbase + j * 16 * RB + so);
@@ -471,8 +514,9 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
     __syncthreads();
   };
 
+  ldscale(0, 0);
   ready(0);
-  rdfrag(0, 0, 0);
+  rdfrag(0, 0, 0, 0);
   for (int kt0 = 0; kt0 < nk; kt0 += S) {
 #pragma unroll
     for (int u = 0; u < S; u++) {
@@ -480,18 +524,19 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
       if (kt < nk) {
         // refill the stage every wave finished reading before the last barrier
         if (kt + S - 1 < nk) issue((u + S - 1) % S, (kt + S - 1) * BK);
-        rdfrag(u, 1, 1);
+        if (kt + 1 < nk) ldscale((u + 1) & 1, kt + 1);  // int4: next tile's scales (S is even)
+        rdfrag(u, 1, 1, u & 1);
         mma(0);
         mma(1);  // placed before the wait so its MFMAs overlap the barrier
         if (kt + 1 < nk) {
           ready(kt + 1);
-          rdfrag((u + 1) % S, 0, 0);
+          rdfrag((u + 1) % S, 0, 0, (u + 1) & 1);
         }
       }
     }
   }
   __syncthreads();  // every wave is done with the stages before strips reuse stage 0
-  epilogue<WTM, WTN, TI, TJ, EPI>(p, acc, reinterpret_cast<float *>(st0.d), m0 + wm * WTM, n0 + wn * WTN, wave, lane);
+  epilogue<WTM, WTN, TI, TJ, EPI>(p, acc, reinterpret_cast<float *>(smem), m0 + wm * WTM, n0 + wn * WTN, wave, lane);
 }
 
 // ── fp32 MFMA GEMM: B f32 row-major [K,N] ───────────────────────────────────
@@ -670,11 +715,11 @@ static int pick_dma(fa_ctx *ctx, const GemmArgs &p) {
   return best;
 }
 
-template <int BM, int BN, int WM, int WN, int S, int EPI, int LO = 0, int B8 = 0>
+template <int BM, int BN, int WM, int WN, int S, int EPI, int LO = 0, int BQ = 0>
 static int launch_dma(fa_ctx *ctx, const GemmArgs &p, const char *label) {
   const unsigned tiles = cdiv(p.M, BM) * (p.N / BN);
   ProfScope ps(ctx, label);
-  FA_LAUNCH(ps, (gemm_dma_kernel<BM, BN, WM, WN, S, EPI, LO, B8>), dim3(tiles), dim3(64 * WM * WN), 0, ctx->stream, p);
+  FA_LAUNCH(ps, (gemm_dma_kernel<BM, BN, WM, WN, S, EPI, LO, BQ>), dim3(tiles), dim3(64 * WM * WN), 0, ctx->stream, p);
   return check_launch(ctx, label);
 }
 
@@ -705,6 +750,17 @@ static int launch_tile(fa_ctx *ctx, const GemmArgs &p, const char *label) {
         case 1: return launch_dma<192, 128, 2, 4, 3, EPI, 0, 1>(ctx, p, label);
         case 2: return launch_dma<128, 128, 2, 4, 4, EPI, 0, 1>(ctx, p, label);
         case 3: return launch_dma<96, 128, 2, 4, 4, EPI, 0, 1>(ctx, p, label);
+        default: break;
+      }
+  }
+  if constexpr (AK == A_F16 && BKND == B_I4 && EPI != EPI_GENERIC) {
+    // symmetric group-32 with f16 scales (the encoder's int4 format): same tile
+    // table, even stage counts (the scale sets alternate with the stages)
+    if (!p.Alo && !p.bzp && !p.bscale_f32) switch (pick_dma(ctx, p)) {
+        case 0: return launch_dma<192, 256, 2, 4, 2, EPI, 0, 2>(ctx, p, label);
+        case 1: return launch_dma<192, 128, 2, 4, 2, EPI, 0, 2>(ctx, p, label);
+        case 2: return launch_dma<128, 128, 2, 4, 4, EPI, 0, 2>(ctx, p, label);
+        case 3: return launch_dma<96, 128, 2, 4, 4, EPI, 0, 2>(ctx, p, label);
         default: break;
       }
   }

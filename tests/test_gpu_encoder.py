@@ -114,3 +114,17 @@ def test_int8_direct_to_lds_route_matches_staged_route(ctx, fa, small, monkeypat
     staged = np.concatenate(eq.encode(mels))
     eq.close()
     assert np.array_equal(fast, staged), float(np.abs(fast - staged).max())
+
+
+def test_int4_direct_to_lds_route_matches_staged_route(ctx, fa, small, monkeypatch):
+    """int4 group-32 weights through the direct-to-LDS GEMM (raw nibble tiles,
+    block scales a K tile ahead, (q - 8) * s rounded once to f16 after the LDS
+    read) give the register-staged dequant route's bits."""
+    mels = fa.synth.make_features(128, 300, seed=10, W=2)
+    eq = fa.FusedEncoder(ctx, small, "int4", max_T=128)
+    monkeypatch.setenv("FA_GRAPH", "0")
+    fast = np.concatenate(eq.encode(mels))
+    monkeypatch.setenv("FA_GEMM_DMA", "0")
+    staged = np.concatenate(eq.encode(mels))
+    eq.close()
+    assert np.array_equal(fast, staged), float(np.abs(fast - staged).max())
