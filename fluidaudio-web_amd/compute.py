@@ -19,6 +19,7 @@ scope and raise NotImplementedError naming the op.
 from __future__ import annotations
 
 import ctypes as C
+import weakref
 from contextlib import contextmanager
 
 import numpy as np
@@ -81,10 +82,13 @@ class HipContext:
             raise FaError(st, f"fa_ctx_create(device={device}) failed with status {st} (no gfx950 GPU visible?)")
         self._p = p
         self._destroyed = False
+        self._children = weakref.WeakSet()  # native objects bound to this context (encoders)
 
     # ── lifecycle ─────────────────────────────────────────────────────────
     def destroy(self):
         if not self._destroyed:
+            for c in list(self._children):  # they free device memory through the context
+                c.close()
             lib().fa_ctx_destroy(self._p)
             self._destroyed = True
 

@@ -836,7 +836,7 @@ int fa_encoder_load(fa_ctx *ctx, const fa_encoder_cfg *cfg, int n, const char *c
       Ly.pbv = dupload(e, b.data(), D);
     }
     // conv module: pw1 columns permuted for the GLU epilogue (value c at
-    // 16(c/8)+c%8, gate c+D at 16(c/8)+8+c%8)
+    // 16(c/8) + 4((c%8)/2) + c%2, gate c+D two columns later)
     {
       const float *w1, *w2, *dw, *dwb;
       if ((st = get(g("pw1"), (int64_t)2 * D * D, false, &w1)) || (st = get(g("pw2"), (int64_t)D * D, false, &w2)) ||
@@ -847,7 +847,7 @@ int fa_encoder_load(fa_ctx *ctx, const fa_encoder_cfg *cfg, int n, const char *c
       std::vector<float> bt((size_t)2 * D * D), bp;
       if (!b1.empty()) bp.assign(2 * D, 0.f);
       for (int ch = 0; ch < D; ch++) {
-        const int jv = 16 * (ch / 8) + ch % 8, jg = jv + 8;
+        const int jv = 16 * (ch / 8) + 4 * ((ch % 8) / 2) + ch % 2, jg = jv + 2;
         std::memcpy(&bt[(size_t)jv * D], w1 + (size_t)ch * D, D * 4);
         std::memcpy(&bt[(size_t)jg * D], w1 + (size_t)(ch + D) * D, D * 4);
         if (!b1.empty()) {

@@ -12,8 +12,8 @@
 //
 // Epilogue order matches the reference kernels: × per-column scale (int8,
 // gemm.js:704-706) → + bias → act → + residual (gemm.js:398-404).  The GLU
-// epilogue pairs column 16g+x (value) with 16g+8+x (gate) and writes channel
-// 8g+x = value·σ(gate) (gate clamped to ±30 as tensor-ops.js:18).
+// epilogue pairs column 4g+x (value) with 4g+2+x (gate), x = 0, 1, and writes
+// channel 2g+x = value·σ(gate) (gate clamped to ±30 as tensor-ops.js:18).
 #include "fa_internal.h"
 #include "fa_device.h"
 #include "gemm.h"
@@ -77,9 +77,19 @@ __device__ __forceinline__ h8 load_b8(const GemmArgs &p, int n, int k) {
 // pushed large tiles' accumulators to scratch).
 enum Epi : int { EPI_F32 = 0, EPI_F16 = 1, EPI_F16_SILU = 2, EPI_F16_RELU = 3, EPI_GLU = 4, EPI_GENERIC = 5, EPI_HILO_RELU = 6 };
 
+// Epilogue results: computed in f32, then rounded to f16.  The empty asm pins
+// the f32 value in a register; without it the compiler may fuse the preceding
+// scale-and-bias fma with the conversion into one f16-rounding v_fma_mix on
+// some code paths and not others, and two kernels of the same math would
+// disagree in the last f16 bit.
+__device__ __forceinline__ _Float16 to_f16(float t) {
+  asm("" : "+v"(t));
+  return (_Float16)t;
+}
+
 __device__ __forceinline__ float sigmoid_mul(float v, float g) { return __fdividef(v, 1.f + __expf(-fminf(fmaxf(g, -30.f), 30.f))); }
 
-// Epilogue, staged through LDS (free after the main loop): each wave writes
+// Epilogue of the register-staged kernel, through LDS (free after the main loop): each wave writes
 // 16-row strips of its accumulators, then reads them back row-contiguous so
 // every global access is a 16-byte vector and each row segment is written
 // by consecutive lanes (the MFMA layout itself gives 2-4 byte scattered stores).
@@ -100,8 +110,8 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f4 (&acc)[TI][TJ], f
   for (int e = 0; e < 4; e++) {
     if constexpr (EPI == EPI_GLU) {
       const int ch = lc + e;  // output channel within the strip
-      vcol[e] = (ch >> 3) * 16 + (ch & 7);
-      gcol[e] = vcol[e] + 8;
+      vcol[e] = (ch >> 3) * 16 + ((ch & 7) >> 1) * 4 + (ch & 1);
+      gcol[e] = vcol[e] + 2;
     } else {
       vcol[e] = lc + e;
       gcol[e] = vcol[e];
@@ -122,7 +132,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f4 (&acc)[TI][TJ], f
     for (int j = 0; j < TJ; j++)
 #pragma unroll
       for (int r = 0; r < 4; r++) strip[((lane >> 4) * 4 + r) * SS + j * 16 + (lane & 15)] = acc[i][j][r];
-    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): strip written (global stores stay in flight)
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int pr = 0; pr < 16; pr += RPP) {
@@ -146,7 +156,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f4 (&acc)[TI][TJ], f
 #pragma unroll
             for (int e = 0; e < 4; e++) {
               const float t = sigmoid_mul(v[e], strip[rr * SS + gcol[e]] * gcs[e] + gbv[e]);
-              o[e] = (_Float16)t;
+              o[e] = to_f16(t);
               v[e] = t - (float)o[e];
             }
             *reinterpret_cast<h4 *>(reinterpret_cast<_Float16 *>(p.C) + (size_t)row * p.ldc + ocol) = o;
@@ -169,7 +179,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f4 (&acc)[TI][TJ], f
 #pragma unroll
               for (int e = 0; e < 4; e++) {
                 const float t = fmaxf(v[e], 0.f);
-                const _Float16 hi = (_Float16)t;
+                const _Float16 hi = to_f16(t);
                 o[2 * e] = hi;
                 o[2 * e + 1] = (_Float16)(t - (float)hi);
               }
@@ -180,7 +190,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f4 (&acc)[TI][TJ], f
                 float o = act_apply(v[e], p.act);
                 if (p.add) o += p.add[(size_t)row * p.ldadd + col + e];
                 if (p.out_f16)
-                  reinterpret_cast<_Float16 *>(p.C)[(size_t)row * p.ldc + col + e] = (_Float16)o;
+                  reinterpret_cast<_Float16 *>(p.C)[(size_t)row * p.ldc + col + e] = to_f16(o);
                 else
                   reinterpret_cast<float *>(p.C)[(size_t)row * p.ldc + col + e] = o;
               }
@@ -191,7 +201,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f4 (&acc)[TI][TJ], f
                 float t = v[e];
                 if constexpr (EPI == EPI_F16_SILU) t = sigmoid_mul(t, t);
                 if constexpr (EPI == EPI_F16_RELU) t = fmaxf(t, 0.f);
-                o[e] = (_Float16)t;
+                o[e] = to_f16(t);
                 ol[e] = (_Float16)(t - (float)o[e]);
               }
               *reinterpret_cast<h4 *>(reinterpret_cast<_Float16 *>(p.C) + (size_t)row * p.ldc + col) = o;
@@ -210,19 +220,19 @@ __device__ __forceinline__ void epilogue(const GemmArgs &p, f4 (&acc)[TI][TJ], f
                 if (p.add) o += p.add[(size_t)row * p.ldadd + col + e];
               if constexpr (EPI == EPI_HILO_RELU) {
                 o = fmaxf(o, 0.f);
-                const _Float16 hi = (_Float16)o;
+                const _Float16 hi = to_f16(o);
                 reinterpret_cast<_Float16 *>(p.C)[(size_t)row * p.ldc + 2 * (col + e)] = hi;
                 reinterpret_cast<_Float16 *>(p.C)[(size_t)row * p.ldc + 2 * (col + e) + 1] = (_Float16)(o - (float)hi);
               } else if (EPI == EPI_F32 || (EPI == EPI_GENERIC && !p.out_f16))
                 reinterpret_cast<float *>(p.C)[(size_t)row * p.ldc + col + e] = o;
               else
-                reinterpret_cast<_Float16 *>(p.C)[(size_t)row * p.ldc + col + e] = (_Float16)o;
+                reinterpret_cast<_Float16 *>(p.C)[(size_t)row * p.ldc + col + e] = to_f16(o);
             }
           }
         }
       }
     }
-    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): strip reads done before the next strip overwrites it
     __builtin_amdgcn_wave_barrier();
   }
 }
@@ -308,6 +318,83 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_kernel(GemmArgs p) {
   epilogue<WTM, WTN, TI, TJ, EPI>(p, acc, reinterpret_cast<float *>(&sA[0][0]), m0 + wm * WTM, n0 + wn * WTN, wave, lane);
 }
 
+// Epilogue of the direct-to-LDS kernel, which runs its MFMAs with the operands
+// swapped (C^T tiles): acc[i][j] holds row r0 + 16i + (lane & 15), columns
+// c0 + 16j + 4(lane >> 4) + {0..3}.  Each lane owns four consecutive columns of
+// one row and stores them straight from registers (16-byte f32 / 8-byte f16
+// vectors): no LDS round trip, and nothing waits for the stores.  GLU weight
+// columns are interleaved so the four columns are (value c, value c+1, gate c,
+// gate c+1) of two consecutive output channels.
+template <int TI, int TJ, int EPI>
+__device__ __forceinline__ void epilogue_direct(const GemmArgs &p, f4 (&acc)[TI][TJ], int r0, int c0, int lane) {
+  const int cl = 4 * (lane >> 4);
+  const bool scaled = p.colscale != nullptr;  // int8 column scales, per-column folds
+  f4 bv[TJ], cs[TJ];
+#pragma unroll
+  for (int j = 0; j < TJ; j++) {
+    const int col = c0 + 16 * j + cl;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      bv[j][e] = p.bias ? p.bias[col + e] : 0.f;
+      cs[j][e] = scaled ? p.colscale[col + e] : 1.f;
+    }
+  }
+  if (scaled) {  // acc * s + b in one rounding, as the register-staged route computes it
+#pragma unroll
+    for (int i = 0; i < TI; i++)
+#pragma unroll
+      for (int j = 0; j < TJ; j++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) acc[i][j][e] = __builtin_fmaf(acc[i][j][e], cs[j][e], bv[j][e]);
+  }
+#pragma unroll
+  for (int i = 0; i < TI; i++) {
+    const int row = r0 + 16 * i + (lane & 15);
+    if (row >= p.M) continue;
+#pragma unroll
+    for (int j = 0; j < TJ; j++) {
+      const int col = c0 + 16 * j + cl;
+      f4 v = scaled ? acc[i][j] : acc[i][j] + bv[j];
+      if constexpr (EPI == EPI_F32) {
+        if (p.add) v += *reinterpret_cast<const f4 *>(p.add + (size_t)row * p.ldadd + col);
+        *reinterpret_cast<f4 *>(reinterpret_cast<float *>(p.C) + (size_t)row * p.ldc + col) = v;
+      } else if constexpr (EPI == EPI_GLU) {
+        const float t0 = sigmoid_mul(v[0], v[2]), t1 = sigmoid_mul(v[1], v[3]);
+        const size_t o = (size_t)row * p.ldc + (col >> 1);
+        if (!p.out_f16) {
+          *reinterpret_cast<float2 *>(reinterpret_cast<float *>(p.C) + o) = make_float2(t0, t1);
+        } else {
+          const h2 h = h2{to_f16(t0), to_f16(t1)};
+          *reinterpret_cast<h2 *>(reinterpret_cast<_Float16 *>(p.C) + o) = h;
+          if (p.Clo) *reinterpret_cast<h2 *>(reinterpret_cast<_Float16 *>(p.Clo) + o) = h2{(_Float16)(t0 - (float)h[0]), (_Float16)(t1 - (float)h[1])};
+        }
+      } else if constexpr (EPI == EPI_HILO_RELU) {
+        h8 o;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float t = fmaxf(v[e], 0.f);
+          const _Float16 hi = to_f16(t);
+          o[2 * e] = hi;
+          o[2 * e + 1] = (_Float16)(t - (float)hi);
+        }
+        *reinterpret_cast<h8 *>(reinterpret_cast<_Float16 *>(p.C) + (size_t)row * p.ldc + 2 * col) = o;
+      } else {
+        h4 o, ol;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          float t = v[e];
+          if constexpr (EPI == EPI_F16_SILU) t = sigmoid_mul(t, t);
+          if constexpr (EPI == EPI_F16_RELU) t = fmaxf(t, 0.f);
+          o[e] = to_f16(t);
+          ol[e] = (_Float16)(t - (float)o[e]);
+        }
+        *reinterpret_cast<h4 *>(reinterpret_cast<_Float16 *>(p.C) + (size_t)row * p.ldc + col) = o;
+        if (p.Clo) *reinterpret_cast<h4 *>(reinterpret_cast<_Float16 *>(p.Clo) + (size_t)row * p.ldc + col) = ol;
+      }
+    }
+  }
+}
+
 // ── direct-to-LDS multi-stage GEMM (A f16, B f16 / int8 / int4 K-major) ────
 // The encoder's hot path.  Each K tile (64 halfs = 128 B per row) of the
 // stacked A|B panel is copied global->LDS by global_load_lds_dwordx4 (no VGPR
@@ -384,8 +471,7 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
   constexpr int IW = (IT + NW - 1) / NW, IMIN = IT / NW;  // per wave: at most / at least
   static_assert(BM % 16 == 0 && BN % 16 == 0 && NW % 4 == 0 && (BN * RBB) % 1024 == 0, "tile shape");
   static_assert(S >= 2 && S <= 4, "LDS stages");
-  constexpr int STRIPS = NW * 16 * (WTN + 4) * 4;  // epilogue strips reuse the stage buffer
-  constexpr int SMEM = S * STG > STRIPS ? S * STG : STRIPS;
+  constexpr int SMEM = S * STG;
   static_assert(SMEM <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
   uint32_t sadr[4];
@@ -500,8 +586,8 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
     for (int i = 0; i < TI; i++)
 #pragma unroll
       for (int j = 0; j < TJ; j++) {
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[slot][i], bf[slot][j], acc[i][j], 0, 0, 0);
-        if constexpr (LO) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[slot][i], bf[slot][j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[slot][j], af[slot][i], acc[i][j], 0, 0, 0);  // C^T tile
+        if constexpr (LO) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[slot][j], al[slot][i], acc[i][j], 0, 0, 0);
       }
   };
   // K tile kt is in LDS once at most (S-2) later tiles are still in flight
@@ -535,8 +621,7 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
       }
     }
   }
-  __syncthreads();  // every wave is done with the stages before strips reuse stage 0
-  epilogue<WTM, WTN, TI, TJ, EPI>(p, acc, reinterpret_cast<float *>(smem), m0 + wm * WTM, n0 + wn * WTN, wave, lane);
+  epilogue_direct<TI, TJ, EPI>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane);
 }
 
 // ── fp32 MFMA GEMM: B f32 row-major [K,N] ───────────────────────────────────
@@ -691,7 +776,9 @@ static const DmaCfg kDma[] = {{192, 256, 30.0f}, {192, 128, 18.3f}, {128, 128, 1
 static const DmaCfg kDmaLo[] = {{192, 256, 51.0f}, {192, 128, 27.7f}, {96, 256, 27.0f}, {128, 128, 17.9f}, {96, 128, 16.5f}};
 
 static int pick_dma(fa_ctx *ctx, const GemmArgs &p) {
+  // 16-byte operand copies; vector epilogue stores (up to 16 bytes at a multiple-of-4 column)
   if (p.K % 64 || p.lda % 8 || ((uintptr_t)p.A & 15) || ((uintptr_t)p.B & 15) || ((uintptr_t)p.Alo & 15)) return -1;
+  if (p.ldc % 8 || p.ldadd % 4 || ((uintptr_t)p.C & 15) || ((uintptr_t)p.Clo & 15) || ((uintptr_t)p.add & 15)) return -1;
   const DmaCfg *tab = p.Alo ? kDmaLo : kDma;
   const int ntab = p.Alo ? (int)(sizeof kDmaLo / sizeof kDmaLo[0]) : (int)(sizeof kDma / sizeof kDma[0]);
   // FA_GEMM_DMA=0 turns the route off (not with a lo plane); 1..n pins

@@ -197,6 +197,7 @@ class FusedEncoder:
         p = L.P()
         check(ctx._p, lib().fa_encoder_load(ctx._p, C.byref(c), len(names), arr_names, arr_data, arr_cnt, FORMATS[fmt], max_T, C.byref(p)))
         self._p = p
+        ctx._children.add(self)
 
     # operand-precision bits (fa_encoder_set_exact)
     EXACT = dict(ln_out=1, ff_hidden=2, attn_out=4, glu=8, dw_out=16)
