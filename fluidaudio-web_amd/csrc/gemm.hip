@@ -771,9 +771,9 @@ struct DmaCfg {
   int bm, bn;
   float us_round;
 };
-static const DmaCfg kDma[] = {{192, 256, 30.0f}, {192, 128, 18.3f}, {128, 128, 12.6f}, {96, 128, 11.7f}};
+static const DmaCfg kDma[] = {{192, 256, 30.0f}, {192, 128, 18.3f}, {128, 128, 12.6f}, {96, 128, 11.7f}, {192, 192, 25.1f}};
 // with a lo plane (two MFMAs per B fragment), same K = 1024 round timing
-static const DmaCfg kDmaLo[] = {{192, 256, 51.0f}, {192, 128, 27.7f}, {96, 256, 27.0f}, {128, 128, 17.9f}, {96, 128, 16.5f}};
+static const DmaCfg kDmaLo[] = {{192, 256, 51.0f}, {192, 128, 27.7f}, {96, 256, 27.0f}, {128, 128, 17.9f}, {96, 128, 16.5f}, {192, 192, 40.7f}};
 
 static int pick_dma(fa_ctx *ctx, const GemmArgs &p) {
   // 16-byte operand copies; vector epilogue stores (up to 16 bytes at a multiple-of-4 column)
@@ -820,6 +820,7 @@ static int launch_tile(fa_ctx *ctx, const GemmArgs &p, const char *label) {
         case 2: return launch_dma<96, 256, 2, 4, 2, EPI, 1>(ctx, p, label);
         case 3: return launch_dma<128, 128, 2, 4, 3, EPI, 1>(ctx, p, label);
         case 4: return launch_dma<96, 128, 2, 4, 3, EPI, 1>(ctx, p, label);
+        case 5: return launch_dma<192, 192, 2, 4, 2, EPI, 1>(ctx, p, label);
         default: return set_err(ctx, FA_E_UNSUPPORTED, "%s: lo plane needs N %% 128 == 0, K %% 64 == 0 and 16-byte aligned operands", label);
       }
     }
@@ -828,6 +829,7 @@ static int launch_tile(fa_ctx *ctx, const GemmArgs &p, const char *label) {
       case 1: return launch_dma<192, 128, 4, 2, 3, EPI>(ctx, p, label);
       case 2: return launch_dma<128, 128, 2, 4, 4, EPI>(ctx, p, label);
       case 3: return launch_dma<96, 128, 2, 4, 4, EPI>(ctx, p, label);
+      case 4: return launch_dma<192, 192, 2, 4, 3, EPI>(ctx, p, label);  // 48 KB stages: three fit
       default: break;
     }
   }
@@ -837,6 +839,7 @@ static int launch_tile(fa_ctx *ctx, const GemmArgs &p, const char *label) {
         case 1: return launch_dma<192, 128, 2, 4, 3, EPI, 0, 1>(ctx, p, label);
         case 2: return launch_dma<128, 128, 2, 4, 4, EPI, 0, 1>(ctx, p, label);
         case 3: return launch_dma<96, 128, 2, 4, 4, EPI, 0, 1>(ctx, p, label);
+        case 4: return launch_dma<192, 192, 2, 4, 3, EPI, 0, 1>(ctx, p, label);
         default: break;
       }
   }
@@ -848,6 +851,7 @@ static int launch_tile(fa_ctx *ctx, const GemmArgs &p, const char *label) {
         case 1: return launch_dma<192, 128, 2, 4, 2, EPI, 0, 2>(ctx, p, label);
         case 2: return launch_dma<128, 128, 2, 4, 4, EPI, 0, 2>(ctx, p, label);
         case 3: return launch_dma<96, 128, 2, 4, 4, EPI, 0, 2>(ctx, p, label);
+        case 4: return launch_dma<192, 192, 2, 4, 4, EPI, 0, 2>(ctx, p, label);
         default: break;
       }
   }

@@ -101,28 +101,21 @@ def test_graph_replay_equals_eager(ctx, fa, small, monkeypatch):
     enc.close()
 
 
-def test_int8_direct_to_lds_route_matches_staged_route(ctx, fa, small, monkeypatch):
-    """int8 weights through the direct-to-LDS GEMM (raw int8 tiles, exact
-    int8 -> f16 widening after the LDS read) give the same bits as the
-    register-staged dequant route: both accumulate f16(a) * q over the same
-    K order in f32 and scale the column in the epilogue."""
-    mels = fa.synth.make_features(128, 300, seed=9, W=2)
-    eq = fa.FusedEncoder(ctx, small, "int8", max_T=128)
+@pytest.mark.parametrize("cfg", ["auto", "1", "2", "3", "4", "5"])
+@pytest.mark.parametrize("fmt", ["int8", "int4"])
+def test_quantized_direct_to_lds_route_matches_staged_route(ctx, fa, small, monkeypatch, fmt, cfg):
+    """Quantised weights through the direct-to-LDS GEMM (each tile
+    configuration pinned in turn; a pin whose tile width does not divide N
+    falls back to the automatic choice) give the register-staged dequant
+    route's bits.  int8: raw int8 tiles widened exactly to f16 after the LDS
+    read, column scale in the epilogue.  int4 group-32: raw nibble tiles,
+    block scales loaded a K tile ahead, (q - 8) * s rounded once to f16.  Both
+    routes accumulate the same f16 products over the same K order in f32."""
+    mels = fa.synth.make_features(128, 300, seed=9 if fmt == "int8" else 10, W=2)
+    eq = fa.FusedEncoder(ctx, small, fmt, max_T=128)
     monkeypatch.setenv("FA_GRAPH", "0")
-    fast = np.concatenate(eq.encode(mels))
-    monkeypatch.setenv("FA_GEMM_DMA", "0")
-    staged = np.concatenate(eq.encode(mels))
-    eq.close()
-    assert np.array_equal(fast, staged), float(np.abs(fast - staged).max())
-
-
-def test_int4_direct_to_lds_route_matches_staged_route(ctx, fa, small, monkeypatch):
-    """int4 group-32 weights through the direct-to-LDS GEMM (raw nibble tiles,
-    block scales a K tile ahead, (q - 8) * s rounded once to f16 after the LDS
-    read) give the register-staged dequant route's bits."""
-    mels = fa.synth.make_features(128, 300, seed=10, W=2)
-    eq = fa.FusedEncoder(ctx, small, "int4", max_T=128)
-    monkeypatch.setenv("FA_GRAPH", "0")
+    if cfg != "auto":
+        monkeypatch.setenv("FA_GEMM_DMA", cfg)
     fast = np.concatenate(eq.encode(mels))
     monkeypatch.setenv("FA_GEMM_DMA", "0")
     staged = np.concatenate(eq.encode(mels))

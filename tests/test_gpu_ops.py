@@ -49,8 +49,8 @@ def test_matmul_f16_weights(ctx, orc, shape):
     assert err < 2e-2, err
 
 
-@pytest.mark.parametrize("cfg", ["auto", "1", "2", "3", "4", "0"])
-@pytest.mark.parametrize("shape", [(3008, 1024, 4096), (3008, 4096, 1024), (1504, 1024, 2048), (203, 256, 256), (1, 64, 128)])
+@pytest.mark.parametrize("cfg", ["auto", "1", "2", "3", "4", "5", "0"])
+@pytest.mark.parametrize("shape", [(3008, 1024, 4096), (3008, 4096, 1024), (1504, 1024, 2048), (515, 512, 576), (203, 256, 256), (1, 64, 128)])
 def test_matmul_f16_activations(ctx, orc, monkeypatch, cfg, shape):
     """f16 A x f16 B (the encoder's GEMM route: direct-to-LDS kernels, each
     configuration pinned in turn, M tails included) vs float64 dot products of
@@ -66,8 +66,8 @@ def test_matmul_f16_activations(ctx, orc, monkeypatch, cfg, shape):
     assert err < 1e-5, (cfg, shape, err)
 
 
-@pytest.mark.parametrize("cfg", ["auto", "1", "2", "3", "4", "5"])
-@pytest.mark.parametrize("shape", [(3008, 1024, 4096), (3008, 4096, 1024), (1504, 1024, 2048), (203, 128, 256), (1, 64, 128)])
+@pytest.mark.parametrize("cfg", ["auto", "1", "2", "3", "4", "5", "6"])
+@pytest.mark.parametrize("shape", [(3008, 1024, 4096), (3008, 4096, 1024), (1504, 1024, 2048), (515, 512, 576), (203, 128, 256), (1, 64, 128)])
 def test_matmul_two_plane_activations(ctx, orc, monkeypatch, cfg, shape):
     """A carried as exact f16 hi + lo planes (the encoder's exact-operand route,
     every two-plane configuration pinned in turn, M tails included) vs float64
