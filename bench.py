@@ -90,6 +90,8 @@ def kernel_work(cfg, lens, layout):
         "sub_pw4": ("flop", 2 * M * F * C * C),
         "sub_linear": ("flop", 2 * M * F * C * D),
         "ln_out": ("byte", M * D * 8),
+        "ln_out_ff1": ("byte", M * D * 10),    # f32 in + out, f16 out
+        "ln_out_ff1_x": ("byte", M * D * 12),  # plus the lo plane
         "v_transpose": ("byte", M * D * 2 * 2),
         "attention": ("flop", att), "attention_x": ("flop", att),
         "dwconv": ("byte", M * D * 4), "dwconv_f32": ("byte", M * D * 6), "dwconv_lo": ("byte", M * D * 6), "dwconv_x": ("byte", M * D * 8),

@@ -302,6 +302,60 @@ __global__ __launch_bounds__(256) void enc_ln_f32_kernel(float *__restrict__ x, 
   }
 }
 
+// A layer's norm_out fused with the next layer's first LayerNorm (norm_ff1):
+// the row is read once, normalised in place on the f32 residual stream, and
+// normalised again from registers into the f16 operand (and its lo plane when
+// the next layer carries it exact).  Same arithmetic as enc_ln_f32_kernel
+// followed by enc_ln_kernel.
+template <int V>
+__global__ __launch_bounds__(256) void enc_ln2_kernel(float *__restrict__ x, const float *__restrict__ g0, const float *__restrict__ b0,
+                                                      const float *__restrict__ g1, const float *__restrict__ b1, _Float16 *__restrict__ y,
+                                                      _Float16 *__restrict__ ylo, int rows, float eps) {
+  constexpr int D = 256 * V;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  float4 *xr = reinterpret_cast<float4 *>(x + (size_t)row * D);
+  float4 v[V];
+#pragma unroll
+  for (int t = 0; t < V; t++) v[t] = xr[lane + 64 * t];
+#pragma unroll
+  for (int pass = 0; pass < 2; pass++) {
+    float s = 0.f;
+#pragma unroll
+    for (int t = 0; t < V; t++) s += v[t].x + v[t].y + v[t].z + v[t].w;
+    const float mean = wave_sum(s) * (1.f / D);
+    float q = 0.f;
+#pragma unroll
+    for (int t = 0; t < V; t++) {
+      const float a = v[t].x - mean, b = v[t].y - mean, c = v[t].z - mean, d = v[t].w - mean;
+      q += a * a + b * b + c * c + d * d;
+    }
+    const float inv = rsqrtf(wave_sum(q) * (1.f / D) + eps);
+    const float *gamma = pass ? g1 : g0, *beta = pass ? b1 : b0;
+#pragma unroll
+    for (int t = 0; t < V; t++) {
+      const int j = lane + 64 * t;
+      const float4 gm = reinterpret_cast<const float4 *>(gamma)[j], bt = reinterpret_cast<const float4 *>(beta)[j];
+      const float4 o = make_float4((v[t].x - mean) * inv * gm.x + bt.x, (v[t].y - mean) * inv * gm.y + bt.y, (v[t].z - mean) * inv * gm.z + bt.z,
+                                   (v[t].w - mean) * inv * gm.w + bt.w);
+      if (pass == 0) {
+        xr[j] = o;
+        v[t] = o;
+      } else {
+        const float oo[4] = {o.x, o.y, o.z, o.w};
+        h4 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          hi[e] = (_Float16)oo[e];
+          lo[e] = (_Float16)(oo[e] - (float)hi[e]);
+        }
+        reinterpret_cast<h4 *>(y + (size_t)row * D)[j] = hi;
+        if (ylo) reinterpret_cast<h4 *>(ylo + (size_t)row * D)[j] = lo;
+      }
+    }
+  }
+}
+
 // Conv module depthwise conv over time, k taps, symmetric pad (k-1)/2,
 // + bias (BatchNorm folded) + SiLU (raw-encoder.js:365-367), per window.
 // Thread = 8 channels x TT consecutive frames; the TT+k-1 input rows are
@@ -1069,13 +1123,14 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
       at.win.off[i] = s3.off[i];
       at.win.len[i] = s3.len[i];
     }
+    const bool fuse_ln = D == 256 || D == 512 || D == 1024 || D == 2048;  // norm_out + the next layer's norm_ff1 in one pass
     for (int li = 0; li < layers; li++) {
       auto &Ly = e->L[li];
       const unsigned ex = Ly.exact;
       const void *hl = (ex & FA_EXACT_LN_OUT) ? hlo : nullptr;
       void *ul = (ex & FA_EXACT_FF_HIDDEN) ? ulo : nullptr;
-      // FF1
-      FA_TRY(ln(0, Ly, hl ? "ln_ff1_x" : "ln_ff1"));
+      // FF1 (its LayerNorm ran with the previous layer's norm_out)
+      if (li == 0 || !fuse_ln) FA_TRY(ln(0, Ly, hl ? "ln_ff1_x" : "ln_ff1"));
       FA_TRY(gemm(h, hl, D, Ly.ff1w1, u, ul, c.DFF, 1, FA_ACT_SILU, nullptr, 0, hl ? "ff1_w1_x" : (ul ? "ff1_w1_u" : "ff1_w1")));
       FA_TRY(gemm(u, ul, c.DFF, Ly.ff1w2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, ul ? "ff1_w2_x" : "ff1_w2"));
       // attention
@@ -1107,7 +1162,21 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
       FA_TRY(ln(3, Ly, hl ? "ln_ff2_x" : "ln_ff2"));
       FA_TRY(gemm(h, hl, D, Ly.ff2w1, u, ul, c.DFF, 1, FA_ACT_SILU, nullptr, 0, hl ? "ff2_w1_x" : (ul ? "ff2_w1_u" : "ff2_w1")));
       FA_TRY(gemm(u, ul, c.DFF, Ly.ff2w2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, ul ? "ff2_w2_x" : "ff2_w2"));
-      if (D == 1024) {
+      if (fuse_ln && li + 1 < layers) {
+        const auto &Ln = e->L[li + 1];
+        _Float16 *nlo = (Ln.exact & FA_EXACT_LN_OUT) ? hlo : nullptr;
+        const char *lab = nlo ? "ln_out_ff1_x" : "ln_out_ff1";
+        ProfScope ps(ctx, lab);
+        const dim3 grid(cdiv(M, 4));
+        switch (D / 256) {
+          case 1: FA_LAUNCH(ps, enc_ln2_kernel<1>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[4][0], Ly.ln[4][1], Ln.ln[0][0], Ln.ln[0][1], h, nlo, M, 1e-5f); break;
+          case 2: FA_LAUNCH(ps, enc_ln2_kernel<2>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[4][0], Ly.ln[4][1], Ln.ln[0][0], Ln.ln[0][1], h, nlo, M, 1e-5f); break;
+          case 4: FA_LAUNCH(ps, enc_ln2_kernel<4>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[4][0], Ly.ln[4][1], Ln.ln[0][0], Ln.ln[0][1], h, nlo, M, 1e-5f); break;
+          case 8: FA_LAUNCH(ps, enc_ln2_kernel<8>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[4][0], Ly.ln[4][1], Ln.ln[0][0], Ln.ln[0][1], h, nlo, M, 1e-5f); break;
+          default: return set_err(ctx, FA_E_UNSUPPORTED, "fused LayerNorm: D = %d", D);
+        }
+        FA_TRY(check_launch(ctx, lab));
+      } else if (D == 1024) {
         ProfScope ps(ctx, "ln_out");
         FA_LAUNCH(ps, enc_ln_f32_kernel<4>, dim3(cdiv(M, 4)), dim3(256), 0, ctx->stream, x, Ly.ln[4][0], Ly.ln[4][1], M, 1e-5f);
         FA_TRY(check_launch(ctx, "ln_out"));
