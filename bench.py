@@ -204,7 +204,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="encoder", choices=["encoder", "layer", "ragged", "quant", "quant4", "gemv", "copy"])
+    ap.add_argument("--workload", default="encoder", choices=["encoder", "layer", "ragged", "quant", "quant4", "gemv", "copy", "mel"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -216,6 +216,8 @@ def main():
         return bench_gemv(args, fa, ctx)
     if args.workload == "copy":
         return bench_copy(args, fa, ctx)
+    if args.workload == "mel":
+        return bench_mel(args, fa, ctx)
     cfg = dict(FULL)
     layout = "packed"
     if args.workload in ("encoder", "quant", "quant4"):
@@ -265,6 +267,73 @@ def main():
         log("[bench] CPU baseline (oracle, 1 core, bounded sample)")
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res), flush=True)
+
+
+def bench_mel(args, fa, ctx):
+    """The log-mel front end (fa_mel_windows) over the configs[2] windows: 16
+    windows of 15 s cut at the pipeline's 13 s hop from one resident 210 s
+    sample stream (synthetic: a gliding harmonic tone plus noise, seed 1).
+    value = audio-s (16 x 15 s per step) / wall-s; the dominant kernel
+    (mel_frames) is timed with event pairs in the timed region."""
+    rng = np.random.default_rng(1)
+    n_win, win, hop = 16, 240000, 208000
+    n = hop * (n_win - 1) + win
+    t = np.arange(n) / 16000
+    pcm_h = (0.3 * np.sin(2 * np.pi * (150 + 50 * np.sin(2 * np.pi * 0.5 * t)) * t) + 0.05 * rng.standard_normal(n)).astype(np.float32)
+    pcm = ctx.upload(pcm_h.reshape(1, -1), 1, n)
+    starts, lens = [i * hop for i in range(n_win)], [win] * n_win
+
+    def step():
+        a = ctx.pushArena()
+        ctx.melWindows(pcm, starts, lens)
+        ctx.popArena(a)
+
+    for _ in range(args.warmup):
+        step()
+    ctx.sync()
+    ctx.startProfile(100000)
+    step()
+    prof_all = ctx.endProfile()
+    ctx.sync()
+    ctx.startProfile(100000, only="mel_frames")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    prof = [r for r in ctx.endProfile() if r["label"] == "mel_frames"]
+    frames = n_win * (win // 160)
+    # algorithmic bytes of mel_frames: each window's samples (with the 200-sample
+    # halo of its frames) read once, the f32 raw log-mel written once
+    fbytes = n_win * (win + 400) * 4 + 128 * frames * 4
+    us = sum(r["ms"] for r in prof) / len(prof) * 1e3
+    kern = {}
+    for r in prof_all:
+        k = kern.setdefault(r["label"], {"launches": 0, "avg_us": 0.0})
+        k["launches"] += 1
+        k["avg_us"] += r["ms"] * 1e3
+    for k in kern.values():
+        k["avg_us"] = round(k["avg_us"] / k["launches"], 2)
+    audio_s = n_win * win / 16000 * args.steps
+    line = {"metric": "log-mel front end audio-s/wall-s at 1 GPU", "value": round(audio_s / wall, 1), "unit": "audio-s/wall-s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 3), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f64", "data": "synthetic PCM: gliding harmonic tone + noise (seed 1)",
+            "config": {"workload": "configs[2] windows: 16 x 15 s cut at a 13 s hop from a 210 s stream, 128 mels, per-feature normalisation",
+                       "windows": n_win, "frames": frames},
+            "roofline": {"bound": "hbm", "achieved": round(fbytes / us * 1e-3, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(fbytes / us * 1e-3 / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "mel_frames", "avg_us": round(us, 2),
+                         "launches_timed": len(prof)},
+            "kernels": kern}
+    if not args.no_cpu:
+        orc = ge.load_oracle()
+        orc.set_threads(1)
+        t0 = time.perf_counter()
+        for i in range(2):
+            orc.mel(pcm_h[starts[i]:starts[i] + win])
+        cw = time.perf_counter() - t0
+        line["cpu_baseline"] = {"value": round(2 * win / 16000 / cw, 1), "unit": "audio-s/wall-s", "cores": 1, "kind": "port",
+                                "sample": "2 of the 16 windows (30 s of audio) through the oracle's restatement of nemotron-mel.js (oracle/fa_oracle.c or_mel, single thread)"}
+    print(json.dumps(line), flush=True)
 
 
 def bench_copy(args, fa, ctx):

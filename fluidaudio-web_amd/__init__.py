@@ -12,7 +12,8 @@ __graft_entry__.load_package) or put its parent on sys.path under an alias.
 from ._lib import ACT, FaError, lib
 from .compute import HipContext, HipTensor, PackedBytes, createContext
 from .encoder import FusedEncoder, inferConfig, loadParakeetEncoder, parakeetEncodeBatch, posEncoding, tsub
+from .mel import JsPreprocessor, ParakeetMel
 from . import synth, windowing
 
 __all__ = ["ACT", "FaError", "lib", "HipContext", "HipTensor", "PackedBytes", "createContext", "FusedEncoder", "inferConfig",
-           "loadParakeetEncoder", "parakeetEncodeBatch", "posEncoding", "tsub", "synth", "windowing"]
+           "loadParakeetEncoder", "parakeetEncodeBatch", "posEncoding", "tsub", "synth", "windowing", "JsPreprocessor", "ParakeetMel"]

@@ -96,6 +96,7 @@ SIGNATURES = [
     ("fa_quantize_weights", I, [I, F32P, I, I, C.c_void_p, C.c_void_p]),
     ("fa_gemv_quant", I, [P, T, T, T, I, I, I, C.POINTER(T)]),
     ("fa_pack_windows", I, [P, T, I32P, I32P, I, I, C.POINTER(T)]),
+    ("fa_mel_windows", I, [P, T, I32P, I32P, I, I, C.c_double, I, C.POINTER(T)]),
     ("fa_window_row_map", I, [P, I32P, I, I, I, I32P, C.POINTER(I)]),
     ("fa_encoder_load", I, [P, C.POINTER(EncoderCfg), I, C.POINTER(C.c_char_p), C.POINTER(F32P), C.POINTER(C.c_int64), I, I, C.POINTER(P)]),
     ("fa_encoder_destroy", None, [P]),

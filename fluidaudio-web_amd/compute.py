@@ -428,6 +428,17 @@ class HipContext:
                                              0 if layout == "packed" else 1, C.byref(o)))
         return self._t(o.value)
 
+    def melWindows(self, pcm, starts, lens, nMels=128, logGuard=2.0 ** -24, normalize=True):
+        """Log-mel features of windows [starts[i], starts[i]+lens[i]) of a
+        resident f32 sample stream -> f32 [nMels, Σ floor(lens[i]/160)]
+        (fa_mel_windows), the layout packWindows reads."""
+        s = np.ascontiguousarray(starts, np.int32)
+        l = np.ascontiguousarray(lens, np.int32)
+        o = self._out()
+        check(self._p, lib().fa_mel_windows(self._p, pcm.h, s.ctypes.data_as(L.I32P), l.ctypes.data_as(L.I32P), len(l), int(nMels),
+                                            float(logGuard), int(bool(normalize)), C.byref(o)))
+        return self._t(o.value)
+
     def windowRowMap(self, lens, layout="packed", stage=0):
         l = np.ascontiguousarray(lens, np.int32)
         lay = 0 if layout == "packed" else 1

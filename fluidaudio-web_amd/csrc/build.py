@@ -16,7 +16,10 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 OUT = os.path.join(PKG, "libfa_hip.so")
-SOURCES = ["runtime.hip", "gemm.hip", "attention.hip", "ops.hip", "quant.hip", "encoder.hip", "pack.hip"]
+SOURCES = ["runtime.hip", "gemm.hip", "attention.hip", "ops.hip", "quant.hip", "encoder.hip", "pack.hip", "mel.hip"]
+# per-source flags: the log-mel kernels restate f64 JS arithmetic, so no
+# multiply-add may be fused there
+EXTRA = {"mel.hip": ["-ffp-contract=off"]}
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
@@ -24,7 +27,7 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-u
 
 def _compile(src: str) -> str:
     obj = os.path.join(HERE, "_build", src.replace(".hip", ".o"))
-    cmd = [HIPCC, *FLAGS, "-c", os.path.join(HERE, src), "-o", obj]
+    cmd = [HIPCC, *FLAGS, *EXTRA.get(src, []), "-c", os.path.join(HERE, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     msgs = [l for l in (r.stdout + r.stderr).splitlines() if "packed-fp32-ops" not in l]
     if r.returncode != 0:

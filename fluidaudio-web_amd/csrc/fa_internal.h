@@ -78,6 +78,12 @@ struct fa_ctx {
   std::vector<fa::Staged> staged;
   std::vector<uint32_t> staged_gen;
   int num_cu = 256;
+  // log-mel front end: constant tables (window, twiddles, filterbank) for
+  // mel_tab_mels bins, and per-(window, bin) statistics scratch
+  void *mel_tab = nullptr;
+  int mel_tab_mels = 0;
+  void *mel_scratch = nullptr;
+  size_t mel_scratch_bytes = 0;
 };
 
 namespace fa {

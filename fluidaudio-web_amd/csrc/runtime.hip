@@ -261,6 +261,8 @@ void fa_ctx_destroy(fa_ctx *ctx) {
   }
   for (auto &kv : ctx->pool)
     for (void *p : kv.second) (void)hipFree(p);
+  if (ctx->mel_tab) (void)hipFree(ctx->mel_tab);
+  if (ctx->mel_scratch) (void)hipFree(ctx->mel_scratch);
   for (auto &p : ctx->prof) {
     (void)hipEventDestroy(p.a);
     (void)hipEventDestroy(p.b);

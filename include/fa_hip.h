@@ -199,6 +199,26 @@ int fa_gemv_quant(fa_ctx *ctx, fa_tensor a, fa_tensor w, fa_tensor scales, int f
  *                       past len_i zero-filled; Tmax = max len_i.
  * Windows may overlap in the stream.  starts/lens are host arrays. */
 int fa_pack_windows(fa_ctx *ctx, fa_tensor feats, const int32_t *starts, const int32_t *lens, int n, int layout, fa_tensor *out);
+
+/* ── log-mel front end (PCM windows -> the feature stream above) ─────────────
+ * Replaces ParakeetMel.process (src/engines/asr-parakeet/parakeet-mel.js:14-22)
+ * applied to each window slice of the sample stream, as the pipeline's mel
+ * scheduler does (src/engines/asr-parakeet/mel-scheduler.js:8-21); the
+ * arithmetic is JsPreprocessor.computeRawMel + normalizeFeatures
+ * (src/engines/asr-nemotron/nemotron-mel.js:451-603): pre-emphasis 0.97,
+ * symmetric 400-point Hann window in a 512-point f64 FFT, hop 160, slaney
+ * filterbank, log(mel + log_guard), then (normalize = 1) per-feature
+ * mean / (std + 1e-5) over the window's frames.
+ *   pcm:   f32 tensor holding the mono 16 kHz sample stream (any shape; read flat);
+ *   window i = samples [starts[i], starts[i] + lens[i]) (may overlap);
+ *   out:   f32 [n_mels, Σ floor(lens[i]/160)], window i's features at column
+ *          Σ_{j<i} floor(lens[j]/160): the channel-major stream fa_pack_windows
+ *          reads.  A window shorter than 160 samples contributes no column (the
+ *          reference returns length 0 and the scheduler drops it).
+ * n_mels 1..128 (Parakeet 128); log_guard 2^-24 (Parakeet) or 1e-10 with
+ * normalize 0 (Nemotron's raw log-mel, its first floor(len/160) frames). */
+int fa_mel_windows(fa_ctx *ctx, fa_tensor pcm, const int32_t *starts, const int32_t *lens, int n, int n_mels, double log_guard, int normalize,
+                   fa_tensor *out);
 /* Row -> window index map of a batch (the index map every window-aware kernel
  * uses), computed on the device and copied to host_map: entry r is the window
  * owning row r, or -1 for a padding row.  stage 0 = mel frames, 1..3 = after

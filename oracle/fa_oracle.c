@@ -669,3 +669,189 @@ int or_tsub(int T) {
   for (int i = 0; i < 3; i++) T = (T + 2 - 3) / 2 + 1;
   return T;
 }
+
+/* ── log-mel front end ──────────────────────────────────────────────────────
+ * JsPreprocessor (src/engines/asr-nemotron/nemotron-mel.js) with Parakeet's
+ * settings (src/engines/asr-parakeet/parakeet-mel.js:8-22: log guard 2^-24,
+ * per-feature normalisation).  JS doubles throughout; the arrays the reference
+ * keeps in Float32Array (pre-emphasised samples, power spectrum, raw log-mel,
+ * features, filterbank) are rounded to f32 where it stores them.  Built with
+ * -ffp-contract=off: every a*b+c is a separate multiply and add, as in JS. */
+#define MEL_NFFT 512
+#define MEL_WIN 400
+#define MEL_HOP 160
+#define MEL_NBINS 257
+
+static double mel_hz_to_mel(double f) { /* nemotron-mel.js:63-65 */
+  const double f_sp = 200.0 / 3, min_log_hz = 1000.0, min_log_mel = min_log_hz / f_sp, log_step = log(6.4) / 27.0;
+  return f >= min_log_hz ? min_log_mel + log(f / min_log_hz) / log_step : f / f_sp;
+}
+static double mel_mel_to_hz(double m) { /* nemotron-mel.js:67-69 */
+  const double f_sp = 200.0 / 3, min_log_hz = 1000.0, min_log_mel = min_log_hz / f_sp, log_step = log(6.4) / 27.0;
+  return m >= min_log_mel ? min_log_hz * exp(log_step * (m - min_log_mel)) : m * f_sp;
+}
+
+/* Slaney-normalised triangular filterbank [nmels][257], f32 (nemotron-mel.js:80-118). */
+void or_mel_filterbank(int nmels, float *fb) {
+  double freqs[MEL_NBINS];
+  for (int i = 0; i < MEL_NBINS; i++) freqs[i] = (8000.0 * i) / (MEL_NBINS - 1);
+  const double mmin = mel_hz_to_mel(0.0), mmax = mel_hz_to_mel(8000.0);
+  const int np = nmels + 2;
+  double *fpts = (double *)malloc(sizeof(double) * np), *fdiff = (double *)malloc(sizeof(double) * (np - 1));
+  for (int i = 0; i < np; i++) fpts[i] = mel_mel_to_hz(mmin + ((mmax - mmin) * i) / (np - 1));
+  for (int i = 0; i < np - 1; i++) fdiff[i] = fpts[i + 1] - fpts[i];
+  for (int m = 0; m < nmels; m++) {
+    const double enorm = 2.0 / (fpts[m + 2] - fpts[m]);
+    for (int k = 0; k < MEL_NBINS; k++) {
+      const double down = (freqs[k] - fpts[m]) / fdiff[m], up = (fpts[m + 2] - freqs[k]) / fdiff[m + 1];
+      const double v = down < up ? down : up;
+      fb[m * MEL_NBINS + k] = (float)((v > 0 ? v : 0) * enorm);
+    }
+  }
+  free(fpts);
+  free(fdiff);
+}
+
+/* Symmetric 400-point Hann window zero-padded to 512 (nemotron-mel.js:141-151). */
+void or_mel_hann(double *w) {
+  for (int i = 0; i < MEL_NFFT; i++) w[i] = 0;
+  for (int n = 0; n < MEL_WIN; n++) w[56 + n] = 0.5 * (1 - cos((2 * M_PI * n) / (MEL_WIN - 1)));
+}
+
+/* cos/sin of -2*pi*i/n, i < n/2 (nemotron-mel.js:163-176). */
+void or_mel_twiddles(int n, double *c, double *s) {
+  for (int i = 0; i < n / 2; i++) {
+    const double a = (-2 * M_PI * i) / n;
+    c[i] = cos(a);
+    s[i] = sin(a);
+  }
+}
+
+/* In-place radix-2 DIT FFT with the reference's stage structure: bit
+ * reversal, explicit stages of length 2, 4 and 8 (constants (1,0), (0,-1),
+ * (+-SQRT1_2, -SQRT1_2)), then table twiddles (nemotron-mel.js:199-330). */
+static void mel_fft(double *re, double *im, int n, const double *tc, const double *ts) {
+  int bits = 0;
+  while ((1 << bits) < n) bits++;
+  for (int i = 0; i < n; i++) {
+    int x = i, r = 0;
+    for (int b = 0; b < bits; b++) {
+      r = (r << 1) | (x & 1);
+      x >>= 1;
+    }
+    if (i < r) {
+      double t = re[i]; re[i] = re[r]; re[r] = t;
+      t = im[i]; im[i] = im[r]; im[r] = t;
+    }
+  }
+#define BFLY(p, q, tr, ti) do { re[q] = re[p] - (tr); im[q] = im[p] - (ti); re[p] += (tr); im[p] += (ti); } while (0)
+  for (int i = 0; i < n; i += 2) { const double tr = re[i + 1], ti = im[i + 1]; BFLY(i, i + 1, tr, ti); }
+  for (int i = 0; i < n; i += 4) {
+    { const double tr = re[i + 2], ti = im[i + 2]; BFLY(i, i + 2, tr, ti); }
+    { const double tr = im[i + 3], ti = -re[i + 3]; BFLY(i + 1, i + 3, tr, ti); }
+  }
+  const double r2 = 0.70710678118654757; /* Math.SQRT1_2 */
+  for (int i = 0; i < n; i += 8) {
+    { const double tr = re[i + 4], ti = im[i + 4]; BFLY(i, i + 4, tr, ti); }
+    { const double wc = r2, ws = -r2; const int q = i + 5;
+      const double tr = re[q] * wc - im[q] * ws, ti = re[q] * ws + im[q] * wc; BFLY(i + 1, q, tr, ti); }
+    { const double tr = im[i + 6], ti = -re[i + 6]; BFLY(i + 2, i + 6, tr, ti); }
+    { const double wc = -r2, ws = -r2; const int q = i + 7;
+      const double tr = re[q] * wc - im[q] * ws, ti = re[q] * ws + im[q] * wc; BFLY(i + 3, q, tr, ti); }
+  }
+  for (int len = 16; len <= n; len <<= 1) {
+    const int half = len >> 1, step = n / len;
+    for (int i = 0; i < n; i += len)
+      for (int k = 0; k < half; k++) {
+        const double wc = tc[k * step], ws = ts[k * step];
+        const int p = i + k, q = p + half;
+        const double tr = re[q] * wc - im[q] * ws, ti = re[q] * ws + im[q] * wc;
+        BFLY(p, q, tr, ti);
+      }
+  }
+#undef BFLY
+}
+
+/* Power spectrum (257 bins, f32) of one windowed 512-sample frame `x` (f64):
+ * one 256-point complex FFT of the even/odd samples, then the real-spectrum
+ * reconstruction (nemotron-mel.js:503-537). */
+void or_mel_power(const double *x, float *power) {
+  double re[256], im[256], c256[128], s256[128], c512[256], s512[256];
+  or_mel_twiddles(256, c256, s256);
+  or_mel_twiddles(512, c512, s512);
+  for (int k = 0; k < 256; k++) {
+    re[k] = x[2 * k];
+    im[k] = x[2 * k + 1];
+  }
+  mel_fft(re, im, 256, c256, s256);
+  const double z0r = re[0], z0i = im[0];
+  power[0] = (float)((z0r + z0i) * (z0r + z0i));
+  power[256] = (float)((z0r - z0i) * (z0r - z0i));
+  for (int k = 1; k < 128; k++) {
+    const double rk = re[k], ik = im[k], rnk = re[256 - k], ink = im[256 - k];
+    const double xer = 0.5 * (rk + rnk), xei = 0.5 * (ik - ink), xor_ = 0.5 * (ik + ink), xoi = -0.5 * (rk - rnk);
+    const double wc = c512[k], ws = s512[k];
+    const double tr = xor_ * wc - xoi * ws, ti = xor_ * ws + xoi * wc;
+    const double xkr = xer + tr, xki = xei + ti, xnr = xer - tr, xni = xei - ti;
+    power[k] = (float)(xkr * xkr + xki * xki);
+    power[256 - k] = (float)(xnr * xnr + xni * xni);
+  }
+  power[128] = (float)(re[128] * re[128] + im[128] * im[128]);
+}
+
+/* Log-mel features of one mono 16 kHz window (computeRawMel
+ * nemotron-mel.js:451-557, then normalizeFeatures :569-603 when `normalize`).
+ * out: [nmels][floor(n/160)] f32.  Returns floor(n/160). */
+int or_mel(const float *audio, long n, int nmels, double log_guard, int normalize, float *out) {
+  const long T = n / MEL_HOP;
+  if (n <= 0 || T == 0) return 0;
+  const long plen = n + MEL_NFFT;
+  double *padded = (double *)calloc(plen, sizeof(double));
+  padded[256] = audio[0];
+  for (long i = 1; i < n; i++) padded[256 + i] = (float)((double)audio[i] - 0.97 * (double)audio[i - 1]);
+  double win[MEL_NFFT], x[MEL_NFFT];
+  or_mel_hann(win);
+  float *fb = (float *)malloc(sizeof(float) * nmels * MEL_NBINS);
+  or_mel_filterbank(nmels, fb);
+  int *lo = (int *)malloc(sizeof(int) * nmels), *hi = (int *)malloc(sizeof(int) * nmels);
+  for (int m = 0; m < nmels; m++) { /* fbBounds, nemotron-mel.js:401-419 */
+    int s = -1, e = -1;
+    for (int k = 0; k < MEL_NBINS; k++)
+      if (fb[m * MEL_NBINS + k] > 0) {
+        if (s < 0) s = k;
+        e = k;
+      }
+    if (s < 0) { s = 0; e = -1; }
+    lo[m] = s;
+    hi[m] = e + 1;
+  }
+  float power[MEL_NBINS];
+  for (long t = 0; t < T; t++) {
+    for (int i = 0; i < MEL_NFFT; i++) x[i] = padded[t * MEL_HOP + i] * win[i];
+    or_mel_power(x, power);
+    for (int m = 0; m < nmels; m++) {
+      double v = 0;
+      for (int k = lo[m]; k < hi[m]; k++) v += (double)power[k] * (double)fb[m * MEL_NBINS + k];
+      out[m * T + t] = (float)log(v + log_guard);
+    }
+  }
+  if (normalize)
+    for (int m = 0; m < nmels; m++) {
+      float *r = out + m * T;
+      double sum = 0;
+      for (long t = 0; t < T; t++) sum += r[t];
+      const double mean = sum / T;
+      double var = 0;
+      for (long t = 0; t < T; t++) {
+        const double d = r[t] - mean;
+        var += d * d;
+      }
+      const double inv = T > 1 ? 1.0 / (sqrt(var / (T - 1)) + 1e-5) : 0;
+      for (long t = 0; t < T; t++) r[t] = (float)((r[t] - mean) * inv);
+    }
+  free(padded);
+  free(fb);
+  free(lo);
+  free(hi);
+  return (int)T;
+}

@@ -89,6 +89,14 @@ def _declare(L):
     L.or_f32_to_f16.argtypes = [C.c_float]
     L.or_f32_to_f16.restype = C.c_uint16
 
+    f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
+    L.or_mel_filterbank.argtypes = [C.c_int, f32p]
+    L.or_mel_hann.argtypes = [f64p]
+    L.or_mel_twiddles.argtypes = [C.c_int, f64p, f64p]
+    L.or_mel_power.argtypes = [f64p, f32p]
+    L.or_mel.argtypes = [f32p, C.c_long, C.c_int, C.c_double, C.c_int, f32p]
+    L.or_mel.restype = C.c_int
+
 
 def _f32(a):
     return np.ascontiguousarray(a, dtype=np.float32)
@@ -324,4 +332,43 @@ def encode_batch(cfg, man, mels, layers=None):
     ts = lib().or_encode_batch(C.byref(cfg_struct(cfg)), flat, off, m, W, T, layers, out)
     if ts < 0:
         raise ValueError("encode_batch: windows must have equal Tsub")
+    return out
+
+
+# ── log-mel front end (nemotron-mel.js JsPreprocessor, Parakeet settings) ──
+MEL_LOG_GUARD = 2.0 ** -24
+
+
+def mel_filterbank(nmels=128):
+    fb = np.empty((nmels, 257), np.float32)
+    lib().or_mel_filterbank(nmels, fb)
+    return fb
+
+
+def mel_hann():
+    w = np.empty(512, np.float64)
+    lib().or_mel_hann(w)
+    return w
+
+
+def mel_twiddles(n):
+    c, s = np.empty(n // 2, np.float64), np.empty(n // 2, np.float64)
+    lib().or_mel_twiddles(n, c, s)
+    return c, s
+
+
+def mel_power(frame):
+    """257-bin f32 power spectrum of one windowed 512-sample f64 frame."""
+    p = np.empty(257, np.float32)
+    lib().or_mel_power(np.ascontiguousarray(frame, np.float64), p)
+    return p
+
+
+def mel(audio, nmels=128, log_guard=MEL_LOG_GUARD, normalize=True):
+    """[nmels, floor(len/160)] f32 log-mel features of one mono 16 kHz window."""
+    a = _f32(audio).reshape(-1)
+    T = len(a) // 160
+    out = np.empty((nmels, max(T, 0)), np.float32)
+    got = lib().or_mel(a, len(a), nmels, float(log_guard), int(bool(normalize)), out) if T > 0 else 0
+    assert got == T
     return out
