@@ -327,6 +327,27 @@ static napi_value js_pack_windows(napi_env env, napi_callback_info info) {
   return st ? throw_status(env, c, st) : mkbig(env, o);
 }
 
+/* melWindows(ctx, pcm, starts: Int32Array, lens: Int32Array, nMels, logGuard, normalize) */
+static napi_value js_mel_windows(napi_env env, napi_callback_info info) {
+  napi_value a[MAXA];
+  if (!args(env, info, 7, a)) return NULL;
+  CTX;
+  size_t nb1 = 0, nb2 = 0;
+  int32_t *starts = typed(env, a[2], &nb1), *lens = typed(env, a[3], &nb2);
+  if (!starts || !lens || nb1 != nb2) {
+    napi_throw_type_error(env, NULL, "melWindows: starts/lens must be Int32Arrays of one length");
+    return NULL;
+  }
+  double guard = 0;
+  if (napi_get_value_double(env, a[5], &guard) != napi_ok) {
+    napi_throw_type_error(env, NULL, "melWindows: logGuard must be a number");
+    return NULL;
+  }
+  fa_tensor o = 0;
+  int st = fa_mel_windows(c, T(1), starts, lens, (int)(nb2 / 4), I(4), guard, I(6), &o);
+  return st ? throw_status(env, c, st) : mkbig(env, o);
+}
+
 static void enc_finalize(napi_env env, void *data, void *hint) {
   (void)env;
   (void)hint;
@@ -410,7 +431,7 @@ static napi_value init(napi_env env, napi_value exports) {
       EXPORT("silu", js_silu), EXPORT("relu", js_relu), EXPORT("glu", js_glu), EXPORT("transpose", js_transpose),
       EXPORT("sliceCols", js_slice_cols), EXPORT("setCols", js_set_cols), EXPORT("sliceRows", js_slice_rows), EXPORT("copyRows", js_copy_rows),
       EXPORT("concatRows", js_concat_rows), EXPORT("subReshape", js_sub_reshape), EXPORT("rowBiasAct", js_row_bias_act),
-      EXPORT("profileStart", js_profile_start), EXPORT("profileEnd", js_profile_end), EXPORT("packWindows", js_pack_windows),
+      EXPORT("profileStart", js_profile_start), EXPORT("profileEnd", js_profile_end), EXPORT("packWindows", js_pack_windows), EXPORT("melWindows", js_mel_windows),
       EXPORT("encoderLoad", js_encoder_load), EXPORT("encoderForward", js_encoder_forward), EXPORT("encoderDestroy", js_encoder_destroy),
       EXPORT("encoderTsub", js_encoder_tsub),
   };

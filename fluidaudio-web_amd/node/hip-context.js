@@ -252,6 +252,13 @@ class HipContext {
     this.freeTensor(feats);
     return out;
   }
+  /** Log-mel features (ParakeetMel.process semantics, parakeet-mel.js:14-22) of
+   * windows [starts[i], starts[i]+lens[i]) of a resident f32 sample tensor ->
+   * f32 tensor [nMels, Σ floor(lens[i]/160)] in the stream layout packWindows
+   * reads.  Nemotron's raw log-mel: logGuard 1e-10, normalize false. */
+  _melWindows(pcm, starts, lens, nMels = 128, logGuard = 2 ** -24, normalize = true) {
+    return this._info(addon.melWindows(this.ctx, pcm.h, Int32Array.from(starts), Int32Array.from(lens), nMels, logGuard, normalize ? 1 : 0));
+  }
   destroyFusedEncoder(fused) {
     addon.encoderDestroy(fused.enc);
   }

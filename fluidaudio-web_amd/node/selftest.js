@@ -99,6 +99,21 @@ const check = (name, d, tol) => {
   check("fused encoder window 0 packed == alone", maxdiff(batch.subarray(0, t0 * 256), alone0), 1e-4);
   check("fused encoder window 1 packed == alone", maxdiff(batch.subarray(t0 * 256), alone1), 1e-4);
   ctx.destroyFusedEncoder(fused);
+  // log-mel front end: windows of one stream == each window alone; silence -> 0
+  const pcmH = mk(16000 * 3, 0.2);
+  const pcm = ctx.upload(pcmH, 1, pcmH.length);
+  const both = await ctx.download(ctx._melWindows(pcm, [0, 16000], [16000, 32000]));
+  const w0 = await ctx.download(ctx._melWindows(pcm, [0], [16000]));
+  const w1 = await ctx.download(ctx._melWindows(pcm, [16000], [32000]));
+  let md = 0;
+  for (let m = 0; m < 128; m++)
+    for (let t = 0; t < 300; t++) {
+      const v = both[m * 300 + t], r = t < 100 ? w0[m * 100 + t] : w1[m * 200 + t - 100];
+      md = Math.max(md, Math.abs(v - r));
+    }
+  check("melWindows stream == windows alone", md, 0);
+  const sil = await ctx.download(ctx._melWindows(ctx.upload(new Float32Array(4800), 1, 4800), [0], [4800]));
+  check("melWindows silence normalises to 0", sil.reduce((a, b) => Math.max(a, Math.abs(b)), 0), 0);
   ctx.destroy();
   process.exit(failed ? 1 : 0);
 })().catch((e) => {
