@@ -219,29 +219,34 @@ __device__ __forceinline__ void attn_dma16(const void *g, uint32_t lds_addr) {
 }
 #pragma clang diagnostic pop
 
-// Workgroup = 128 queries of one (window, head), 4 waves x 32 queries (two
-// 16-row MFMA tiles per wave, so every K / V / band fragment read from LDS
-// feeds two MFMAs).  Keys advance 32 per stage, two stages in flight:
+// Workgroup = QB = 16·RT·NWV queries of one (window, head): NWV waves, each
+// owning RT 16-row MFMA tiles (with RT = 2 every K / V / band fragment read
+// from LDS feeds two MFMAs; with RT = 1 more waves share a CU).  Keys advance
+// 32 per stage, two stages in flight:
 //   K   [32 keys][128 d]        (256 B rows, 16-byte chunk c at slot c ^ (row & 7))
 //   Vt  [128 d][32 keys]        (64 B rows,  chunk c at slot c ^ ((row >> 1) & 3))
-//   band [160 rows][128 d]      table rows pbase .. pbase+159, pbase = pc - (q0+127) + j0
-// A query i and key j use band row (j - j0) + (q0 + 127 - i).
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void relpos_attn_lds_kernel(AttnArgs a, const _Float16 *__restrict__ vt, int Tp) {
-  constexpr int HD = 128, QB = 128, KB = 32, BR = 160;
+//   band [QB+32 rows][128 d]    table rows pbase .. , pbase = pc - (q0 + QB - 1) + j0
+// A query i and key j use band row (j - j0) + (q0 + QB - 1 - i).
+template <int RT, int NWV>
+__global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(NWV > 4 ? 2 : 1, NWV > 4 ? 2 : 1))) void relpos_attn_lds_kernel(
+    AttnArgs a, const _Float16 *__restrict__ vt, int Tp) {
+  constexpr int HD = 128, QB = 16 * RT * NWV, KB = 32, BR = QB + 32, UT = RT + 2;  // UT: band tiles per wave
+  constexpr int IT = 16 + BR / 4, IW = IT / NWV;                                  // 1 KB copies per stage / per wave
+  static_assert(IT % NWV == 0, "copies per wave");
   constexpr int KBYTES = KB * 256, VBYTES = HD * 64, PBYTES = BR * 256;
   constexpr int STG = KBYTES + VBYTES + PBYTES;  // 56 KB
   constexpr int SW = 48 + 4, PBS = KB + 8;         // strip row stride (floats), probability row stride (halfs)
   __shared__ __attribute__((aligned(1024))) char st0[STG];
   __shared__ __attribute__((aligned(1024))) char st1[STG];
-  __shared__ float sStrip[4][2][16 * SW];
-  __shared__ __attribute__((aligned(16))) _Float16 sP[4][2][16 * PBS];
+  __shared__ float sStrip[NWV][RT][16 * SW];
+  __shared__ __attribute__((aligned(16))) _Float16 sP[NWV][RT][16 * PBS];
 
   const int w = blockIdx.z, h = blockIdx.y, q0 = blockIdx.x * QB;
   const int T = a.win.len[w], off = a.win.off[w];
   if (q0 >= T) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, c16 = lane & 15;
-  const int iw = q0 + wave * 32;  // this wave's first query (window-local); row tile rt covers iw + 16 rt ..
+  const int iw = q0 + wave * 16 * RT;  // this wave's first query (window-local); row tile rt covers iw + 16 rt ..
   const _Float16 *Q = reinterpret_cast<const _Float16 *>(a.q) + (size_t)off * a.ldq + h * HD;
   const _Float16 *Kp = reinterpret_cast<const _Float16 *>(a.k) + (size_t)off * a.ldk + h * HD;
   const _Float16 *Pp = reinterpret_cast<const _Float16 *>(a.pos) + h * HD;
@@ -255,8 +260,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   auto issue = [&](int sidx, int j0) {
     const uint32_t base = sadr[sidx];
 #pragma unroll
-    for (int i = 0; i < 14; i++) {
-      const int ins = wave + i * 4;  // 0..55
+    for (int i = 0; i < IW; i++) {
+      const int ins = wave + i * NWV;  // 0..IT-1
       const void *src;
       if (ins < 8) {
         const int r = ins * 4 + (lane >> 4), ch = (lane & 15) ^ (r & 7);
@@ -274,9 +279,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   };
 
   // A operands: (q+u) and (q+v) for rows iw + 16 rt + c16, d = s*32 + g*8 .. +8
-  h8 qu[2][4], qv[2][4];
+  h8 qu[RT][4], qv[RT][4];
 #pragma unroll
-  for (int rt = 0; rt < 2; rt++) {
+  for (int rt = 0; rt < RT; rt++) {
     const int qi = min(iw + rt * 16 + c16, T - 1);
     const _Float16 *qr = Q + (size_t)qi * a.ldq;
 #pragma unroll
@@ -296,20 +301,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
   issue(0, 0);
 
-  f4 o[2][8];
+  f4 o[RT][8];
 #pragma unroll
-  for (int rt = 0; rt < 2; rt++)
+  for (int rt = 0; rt < RT; rt++)
 #pragma unroll
     for (int t = 0; t < 8; t++) o[rt][t] = f4{0.f, 0.f, 0.f, 0.f};
-  float mrow[2][4], lrow[2][4];
+  float mrow[RT][4], lrow[RT][4];
 #pragma unroll
-  for (int rt = 0; rt < 2; rt++)
+  for (int rt = 0; rt < RT; rt++)
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       mrow[rt][r] = -INFINITY;
       lrow[rt][r] = 0.f;
     }
-  const int lbw = QB - 32 - wave * 32;  // band row of this wave's union tile 0 (= row tile 1's first band row)
+  const int lbw = QB - 16 * RT - wave * 16 * RT;  // band row of this wave's union tile 0 (= the last row tile's first band row)
 
   const int nkb = (T + KB - 1) / KB;
   for (int kb = 0; kb < nkb; kb++) {
@@ -320,7 +325,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const char *Ks = cur ? st1 : st0, *Vs = Ks + KBYTES, *Ps = Ks + KBYTES + VBYTES;
 
     // fragment reads: K (2 key tiles x 4 k-steps), band (4 union tiles x 4)
-    h8 kf[2][4], pf[4][4];
+    h8 kf[2][4], pf[UT][4];
 #pragma unroll
     for (int kt = 0; kt < 2; kt++) {
       const int r = kt * 16 + c16;
@@ -328,16 +333,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       for (int s = 0; s < 4; s++) kf[kt][s] = *reinterpret_cast<const h8 *>(Ks + r * 256 + (((s * 4 + g) ^ (r & 7)) * 16));
     }
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
+    for (int u = 0; u < UT; u++) {
       const int r = lbw + u * 16 + c16;
 #pragma unroll
       for (int s = 0; s < 4; s++) pf[u][s] = *reinterpret_cast<const h8 *>(Ps + r * 256 + (((s * 4 + g) ^ (r & 7)) * 16));
     }
     __builtin_amdgcn_sched_barrier(0);
-    // row tile rt uses band union tiles (1 - rt) .. (3 - rt)
-    f4 sc[2][2], bd[2][3];
+    // row tile rt uses band union tiles (RT - 1 - rt) .. (RT + 1 - rt)
+    f4 sc[RT][2], bd[RT][3];
 #pragma unroll
-    for (int rt = 0; rt < 2; rt++) {
+    for (int rt = 0; rt < RT; rt++) {
 #pragma unroll
       for (int kt = 0; kt < 2; kt++) sc[rt][kt] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -346,11 +351,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
     for (int s = 0; s < 4; s++)
 #pragma unroll
-      for (int rt = 0; rt < 2; rt++) {
+      for (int rt = 0; rt < RT; rt++) {
 #pragma unroll
         for (int kt = 0; kt < 2; kt++) sc[rt][kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qu[rt][s], kf[kt][s], sc[rt][kt], 0, 0, 0);
 #pragma unroll
-        for (int ct = 0; ct < 3; ct++) bd[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qv[rt][s], pf[1 - rt + ct][s], bd[rt][ct], 0, 0, 0);
+        for (int ct = 0; ct < 3; ct++) bd[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qv[rt][s], pf[RT - 1 - rt + ct][s], bd[rt][ct], 0, 0, 0);
       }
     // V fragments (d rows t*16 + c16, keys g*8 .. +8), read now to hide behind the softmax
     h8 vf[8];
@@ -360,7 +365,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       vf[t] = *reinterpret_cast<const h8 *>(Vs + d * 64 + ((g ^ ((d >> 1) & 3)) * 16));
     }
 #pragma unroll
-    for (int rt = 0; rt < 2; rt++)
+    for (int rt = 0; rt < RT; rt++)
 #pragma unroll
       for (int ct = 0; ct < 3; ct++)
 #pragma unroll
@@ -373,10 +378,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // max exceeds it by more than kLazy nats, decided wave-wide; p <= e^kLazy
     // stays well inside f16 range with unchanged relative precision.
     constexpr float kLazy = 8.f;
-    float sv[2][4][2];
+    float sv[RT][4][2];
     bool need = false;
 #pragma unroll
-    for (int rt = 0; rt < 2; rt++) {
+    for (int rt = 0; rt < RT; rt++) {
       const float *strip = sStrip[wave][rt];
 #pragma unroll
       for (int r = 0; r < 4; r++) {
@@ -392,7 +397,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
     if (__builtin_amdgcn_ballot_w64(need)) {
 #pragma unroll
-      for (int rt = 0; rt < 2; rt++)
+      for (int rt = 0; rt < RT; rt++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
           const float mx = row16_max(fmaxf(sv[rt][r][0], sv[rt][r][1]));
@@ -406,7 +411,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         }
     }
 #pragma unroll
-    for (int rt = 0; rt < 2; rt++) {
+    for (int rt = 0; rt < RT; rt++) {
       _Float16 *pb = sP[wave][rt];
 #pragma unroll
       for (int r = 0; r < 4; r++) {
@@ -421,7 +426,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     __builtin_amdgcn_wave_barrier();
     // O += P·V
 #pragma unroll
-    for (int rt = 0; rt < 2; rt++) {
+    for (int rt = 0; rt < RT; rt++) {
       const h8 pa = *reinterpret_cast<const h8 *>(&sP[wave][rt][c16 * PBS + g * 8]);
 #pragma unroll
       for (int t = 0; t < 8; t++) o[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vf[t], o[rt][t], 0, 0, 0);
@@ -430,13 +435,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
   _Float16 *O = reinterpret_cast<_Float16 *>(a.out) + (size_t)off * a.ldo + h * HD;
   _Float16 *Olo = a.out_lo ? reinterpret_cast<_Float16 *>(a.out_lo) + (size_t)off * a.ldo + h * HD : nullptr;
-  float lsum[2][4];  // row sums, reduced with every lane active
+  float lsum[RT][4];  // row sums, reduced with every lane active
 #pragma unroll
-  for (int rt = 0; rt < 2; rt++)
+  for (int rt = 0; rt < RT; rt++)
 #pragma unroll
     for (int r = 0; r < 4; r++) lsum[rt][r] = row16_sum(lrow[rt][r]);
 #pragma unroll
-  for (int rt = 0; rt < 2; rt++)
+  for (int rt = 0; rt < RT; rt++)
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const int i = iw + rt * 16 + g * 4 + r;
@@ -468,7 +473,14 @@ int relpos_attention_f16(fa_ctx *ctx, const AttnArgs &a, int Tmax, _Float16 *vt,
     FA_TRY(check_launch(ctx, "v_transpose"));
   }
   ProfScope ps(ctx, label);
-  FA_LAUNCH(ps, relpos_attn_lds_kernel, dim3(cdiv(Tmax, 128), a.H, W), dim3(256), 0, ctx->stream, a, (const _Float16 *)vt, Tp);
+  // FA_ATTN=1: 128-query workgroups (4 waves x 2 row tiles); default: 96-query
+  // workgroups (6 waves x 1 row tile, 1.5 waves per SIMD, and a 188-frame
+  // window splits 96 + 92 instead of 128 + 60)
+  const char *ev = getenv("FA_ATTN");
+  if (ev && ev[0] == '1')
+    FA_LAUNCH(ps, (relpos_attn_lds_kernel<2, 4>), dim3(cdiv(Tmax, 128), a.H, W), dim3(256), 0, ctx->stream, a, (const _Float16 *)vt, Tp);
+  else
+    FA_LAUNCH(ps, (relpos_attn_lds_kernel<1, 6>), dim3(cdiv(Tmax, 96), a.H, W), dim3(384), 0, ctx->stream, a, (const _Float16 *)vt, Tp);
   return check_launch(ctx, label);
 }
 

@@ -121,3 +121,18 @@ def test_quantized_direct_to_lds_route_matches_staged_route(ctx, fa, small, monk
     staged = np.concatenate(eq.encode(mels))
     eq.close()
     assert np.array_equal(fast, staged), float(np.abs(fast - staged).max())
+
+
+def test_attention_workgroup_shapes_agree(ctx, fa, small, monkeypatch):
+    """The two rel-pos attention workgroup shapes (default: 96 queries as 6
+    waves x 1 row tile; FA_ATTN=1: 128 queries as 4 waves x 2 row tiles) give
+    the same encoder output up to f16 rounding (their lazy softmax rescaling
+    points differ), on ragged windows that end mid-tile in both shapes."""
+    mels = [fa.synth.make_features(128, t, seed=40 + i)[0] for i, t in enumerate((1500, 777, 1001))]
+    monkeypatch.setenv("FA_GRAPH", "0")
+    enc = fa.FusedEncoder(ctx, small, "f16", max_T=188)
+    a = np.concatenate(enc.encode(mels))
+    monkeypatch.setenv("FA_ATTN", "1")
+    b = np.concatenate(enc.encode(mels))
+    enc.close()
+    assert rel_l2(a, b) < 2e-3, rel_l2(a, b)
