@@ -77,3 +77,34 @@ def make_features(melBins: int, T: int, seed: int = 1, W: int = 1) -> list:
     reference's mel output (raw-encoder.js:224)."""
     rng = np.random.default_rng(seed)
     return [rng.standard_normal((melBins, T)).astype(np.float32) for _ in range(W)]
+
+
+def make_decoder_weights(seed: int = 1, blank_bias: float = 4.5, hid: int = 640, vocab: int = 8193, ndur: int = 5) -> dict:
+    """Synthetic Parakeet TDT decoder + joint weights in the reference's decoder
+    manifest naming (src/engines/asr-parakeet/gpu-decoder.js:232-242;
+    rust/parakeet-decoder/src/lib.rs:4-7): embed [vocab, hid], l{0,1}_W / _R
+    [4*hid, hid] (gate rows i, o, f, c), l{0,1}_B [8*hid] (W bias, R bias),
+    predW [hid, hid] (k-major), predB, outW [hid, vocab + ndur] (row n = hidden
+    unit), outB.  Random-init weights emit a non-blank token on nearly every
+    step; the blank logit is biased (and the duration logits favour one or two
+    frames) so emission looks like speech: about one token per three frames."""
+    rng = np.random.default_rng(seed)
+    f = lambda *s, sc=1.0: (rng.standard_normal(s) * sc).astype(np.float32)  # noqa: E731
+    w = {"embed": f(vocab, hid, sc=0.5)}
+    for l in (0, 1):
+        w[f"l{l}_W"] = f(4 * hid, hid, sc=1 / np.sqrt(hid))
+        w[f"l{l}_R"] = f(4 * hid, hid, sc=1 / np.sqrt(hid))
+        w[f"l{l}_B"] = f(8 * hid, sc=0.1)
+    w["predW"] = f(hid, hid, sc=1 / np.sqrt(hid))
+    w["predB"] = f(hid, sc=0.1)
+    w["outW"] = f(hid, vocab + ndur, sc=0.06)
+    ob = f(vocab + ndur, sc=0.1)
+    ob[vocab - 1] += blank_bias
+    ob[vocab:vocab + ndur] += np.array([0.0, 1.2, 0.9, 0.3, -0.5], np.float32)[:ndur]
+    w["outB"] = ob
+    return w
+
+
+def make_projected_frames(T: int, seed: int = 1, hid: int = 640) -> np.ndarray:
+    """Encoder frames after the joint's encoder projection, [T, hid] ~ N(0, 1)."""
+    return np.random.default_rng(seed).standard_normal((T, hid)).astype(np.float32)

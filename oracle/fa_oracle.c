@@ -855,3 +855,157 @@ int or_mel(const float *audio, long n, int nmels, double log_guard, int normaliz
   free(hi);
   return (int)T;
 }
+
+/* ── greedy TDT decoder ─────────────────────────────────────────────────────
+ * rust/parakeet-decoder/src/lib.rs `decode_proj` (:285-318) and its helpers,
+ * restated in f32 exactly as the wasm32 code computes them: the decoder's own
+ * polynomial expf (:47-54) with its floorf / ldexpf (:55-62), sigmoid / tanhf
+ * (:44, :63), 4-lane dot products summed lane by lane (:108-121), the ONNX
+ * iofc LSTM step (:124-137), pred projection (:148-162) and the joint over
+ * pre-projected frames (:164-217, :220-223).  Weights:
+ *   embed [8193][640], lw/lr [2][2560][640] (gate rows i, o, f, c), lb [2][5120]
+ *   (W bias then R bias), pred_w [640][640] (k-major), pred_b [640],
+ *   out_w [640][8198] (row n = hidden unit), out_b [8198]. */
+#define TDT_HID 640
+#define TDT_VOCAB 8193
+#define TDT_LOGITS 8198
+#define TDT_BLANK 8192
+#define TDT_MAX_SYMBOLS 10
+
+static float tdt_floorf(float x) {
+  const float i = (float)(int)x;
+  return i > x ? i - 1.0f : i;
+}
+static float tdt_ldexpf(float x, int e) {
+  float r = x;
+  int n = e;
+  while (n > 30) { r *= 1073741824.0f; n -= 30; }
+  while (n < -30) { r *= 9.313225746154785e-10f; n += 30; }
+  union { uint32_t u; float f; } b;
+  b.u = (uint32_t)(127 + n) << 23;
+  return r * b.f;
+}
+float or_tdt_expf(float x) {
+  const float xc = x > 30.0f ? 30.0f : (x < -30.0f ? -30.0f : x);
+  const float t = xc * 1.4426950408889634f;
+  const float fl = tdt_floorf(t);
+  const float frac = t - fl;
+  const float p = 1.0f + frac * (0.6931472f + frac * (0.2402265f + frac * (0.0555041f + frac * 0.0096181f)));
+  return tdt_ldexpf(p, (int)fl);
+}
+static float tdt_sigmoid(float x) { return 1.0f / (1.0f + or_tdt_expf(-x)); }
+static float tdt_tanhf(float x) {
+  const float e = or_tdt_expf(2.0f * x);
+  return (e - 1.0f) / (e + 1.0f);
+}
+static float tdt_dotv(const float *a, const float *b, int n) {
+  float acc[4] = {0, 0, 0, 0};
+  int i = 0;
+  for (; i + 4 <= n; i += 4)
+    for (int l = 0; l < 4; l++) acc[l] = acc[l] + a[i + l] * b[i + l];
+  float s = acc[0] + acc[1] + acc[2] + acc[3];
+  for (; i < n; i++) s += a[i] * b[i];
+  return s;
+}
+
+typedef struct {
+  const float *embed, *lw[2], *lr[2], *lb[2], *pred_w, *pred_b, *out_w, *out_b;
+  float h[2][TDT_HID], c[2][TDT_HID], nh[2][TDT_HID], nc[2][TDT_HID], predproj[TDT_HID], j[TDT_HID], out[TDT_LOGITS];
+} tdt_state;
+
+static void tdt_lstm_step(tdt_state *s, int layer, const float *x) {
+  const float *w = s->lw[layer], *r = s->lr[layer], *b = s->lb[layer];
+  const float *hp = s->h[layer];
+  const int H = TDT_HID;
+  for (int g = 0; g < H; g++) {
+    const int wi = g * H, wo = (H + g) * H, wf = (2 * H + g) * H, wc = (3 * H + g) * H;
+    const float zi = b[g] + b[4 * H + g] + tdt_dotv(w + wi, x, H) + tdt_dotv(r + wi, hp, H);
+    const float zo = b[H + g] + b[5 * H + g] + tdt_dotv(w + wo, x, H) + tdt_dotv(r + wo, hp, H);
+    const float zf = b[2 * H + g] + b[6 * H + g] + tdt_dotv(w + wf, x, H) + tdt_dotv(r + wf, hp, H);
+    const float zc = b[3 * H + g] + b[7 * H + g] + tdt_dotv(w + wc, x, H) + tdt_dotv(r + wc, hp, H);
+    const float cc = tdt_sigmoid(zf) * s->c[layer][g] + tdt_sigmoid(zi) * tdt_tanhf(zc);
+    s->nc[layer][g] = cc;
+    s->nh[layer][g] = tdt_sigmoid(zo) * tdt_tanhf(cc);
+  }
+}
+/* predict(token) (:140-145) + compute_predproj (:148-162) */
+static void tdt_predict(tdt_state *s, int token) {
+  tdt_lstm_step(s, 0, s->embed + (size_t)token * TDT_HID);
+  tdt_lstm_step(s, 1, s->nh[0]);
+  for (int n = 0; n < TDT_HID; n++) s->predproj[n] = s->pred_b[n];
+  for (int k = 0; k < TDT_HID; k++) {
+    const float d = s->nh[1][k];
+    const float *row = s->pred_w + (size_t)k * TDT_HID;
+    for (int n = 0; n < TDT_HID; n++) s->predproj[n] = s->predproj[n] + d * row[n];
+  }
+}
+/* joint_tail over a pre-projected frame (:164-217) */
+static void tdt_joint(tdt_state *s, const float *frame) {
+  for (int n = 0; n < TDT_HID; n++) {
+    const float v = frame[n] + s->predproj[n];
+    s->j[n] = v > 0.0f ? v : 0.0f;
+  }
+  for (int m = 0; m < TDT_LOGITS; m++) s->out[m] = s->out_b[m];
+  for (int n = 0; n < TDT_HID; n++) {
+    const float jn = s->j[n];
+    if (jn == 0.0f) continue;
+    const float *row = s->out_w + (size_t)n * TDT_LOGITS;
+    for (int m = 0; m < TDT_LOGITS; m++) s->out[m] = s->out[m] + jn * row[m];
+  }
+}
+
+/* decode_proj: greedy TDT over T pre-projected frames [T][640]; returns the
+ * token count, writes ids and their frame indices (at most cap). */
+int or_tdt_decode_proj(const float *embed, const float *l0w, const float *l0r, const float *l0b, const float *l1w, const float *l1r,
+                       const float *l1b, const float *pred_w, const float *pred_b, const float *out_w, const float *out_b, const float *frames,
+                       int T, int32_t *ids, int32_t *fr, int cap) {
+  tdt_state *s = (tdt_state *)calloc(1, sizeof(tdt_state));
+  s->embed = embed;
+  s->lw[0] = l0w; s->lr[0] = l0r; s->lb[0] = l0b;
+  s->lw[1] = l1w; s->lr[1] = l1r; s->lb[1] = l1b;
+  s->pred_w = pred_w; s->pred_b = pred_b; s->out_w = out_w; s->out_b = out_b;
+  int n_out = 0, emitted = 0, t = 0;
+  tdt_predict(s, TDT_BLANK);
+  while (t < T) {
+    tdt_joint(s, frames + (size_t)t * TDT_HID);
+    int max_id = 0, step = 0;
+    float max_v = -INFINITY, dv = -INFINITY;
+    for (int i = 0; i < TDT_VOCAB; i++)
+      if (s->out[i] > max_v) { max_v = s->out[i]; max_id = i; }
+    for (int i = TDT_VOCAB; i < TDT_LOGITS; i++)
+      if (s->out[i] > dv) { dv = s->out[i]; step = i - TDT_VOCAB; }
+    if (max_id != TDT_BLANK) {
+      memcpy(s->h, s->nh, sizeof s->h); /* commit_state (:146) */
+      memcpy(s->c, s->nc, sizeof s->c);
+      if (n_out < cap) { ids[n_out] = max_id; fr[n_out] = t; }
+      n_out++;
+      emitted++;
+      tdt_predict(s, max_id);
+    }
+    if (step > 0) { t += step; emitted = 0; }
+    else if (max_id == TDT_BLANK || emitted >= TDT_MAX_SYMBOLS) { t += 1; emitted = 0; }
+  }
+  free(s);
+  return n_out;
+}
+
+/* Pieces for the pins: one LSTM step of `layer` from (h, c) with input x ->
+ * (nh, nc), and the joint logits of one frame with a given pred projection. */
+void or_tdt_lstm(const float *w, const float *r, const float *b, const float *x, const float *h, const float *c, float *nh, float *nc) {
+  tdt_state *s = (tdt_state *)calloc(1, sizeof(tdt_state));
+  s->lw[0] = w; s->lr[0] = r; s->lb[0] = b;
+  memcpy(s->h[0], h, sizeof(float) * TDT_HID);
+  memcpy(s->c[0], c, sizeof(float) * TDT_HID);
+  tdt_lstm_step(s, 0, x);
+  memcpy(nh, s->nh[0], sizeof(float) * TDT_HID);
+  memcpy(nc, s->nc[0], sizeof(float) * TDT_HID);
+  free(s);
+}
+void or_tdt_joint(const float *out_w, const float *out_b, const float *frame, const float *predproj, float *logits) {
+  tdt_state *s = (tdt_state *)calloc(1, sizeof(tdt_state));
+  s->out_w = out_w; s->out_b = out_b;
+  memcpy(s->predproj, predproj, sizeof(float) * TDT_HID);
+  tdt_joint(s, frame);
+  memcpy(logits, s->out, sizeof(float) * TDT_LOGITS);
+  free(s);
+}

@@ -96,6 +96,13 @@ def _declare(L):
     L.or_mel_power.argtypes = [f64p, f32p]
     L.or_mel.argtypes = [f32p, C.c_long, C.c_int, C.c_double, C.c_int, f32p]
     L.or_mel.restype = C.c_int
+    i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+    L.or_tdt_expf.argtypes = [C.c_float]
+    L.or_tdt_expf.restype = C.c_float
+    L.or_tdt_decode_proj.argtypes = [f32p] * 12 + [C.c_int, i32p, i32p, C.c_int]
+    L.or_tdt_decode_proj.restype = C.c_int
+    L.or_tdt_lstm.argtypes = [f32p] * 8
+    L.or_tdt_joint.argtypes = [f32p] * 5
 
 
 def _f32(a):
@@ -372,3 +379,33 @@ def mel(audio, nmels=128, log_guard=MEL_LOG_GUARD, normalize=True):
     got = lib().or_mel(a, len(a), nmels, float(log_guard), int(bool(normalize)), out) if T > 0 else 0
     assert got == T
     return out
+
+
+# ── greedy TDT decoder (rust/parakeet-decoder/src/lib.rs decode_proj) ──────
+TDT_HID, TDT_VOCAB, TDT_LOGITS, TDT_BLANK = 640, 8193, 8198, 8192
+DEC_KEYS = ["embed", "l0_W", "l0_R", "l0_B", "l1_W", "l1_R", "l1_B", "predW", "predB", "outW", "outB"]
+
+
+def tdt_expf(x: float) -> float:
+    return float(lib().or_tdt_expf(float(x)))
+
+
+def tdt_lstm(w, r, b, x, h, c):
+    nh, nc = np.empty(TDT_HID, np.float32), np.empty(TDT_HID, np.float32)
+    lib().or_tdt_lstm(_f32(w), _f32(r), _f32(b), _f32(x), _f32(h), _f32(c), nh, nc)
+    return nh, nc
+
+
+def tdt_joint(out_w, out_b, frame, predproj):
+    o = np.empty(TDT_LOGITS, np.float32)
+    lib().or_tdt_joint(_f32(out_w), _f32(out_b), _f32(frame), _f32(predproj), o)
+    return o
+
+
+def tdt_decode(dec: dict, frames, cap: int = 1 << 16):
+    """Greedy TDT decode of pre-projected frames [T, 640] -> (ids, frame indices)."""
+    f = _f32(frames).reshape(-1, TDT_HID)
+    ids, fr = np.empty(cap, np.int32), np.empty(cap, np.int32)
+    n = lib().or_tdt_decode_proj(*[_f32(dec[k]) for k in DEC_KEYS], f, f.shape[0], ids, fr, cap)
+    n = min(n, cap)
+    return ids[:n].copy(), fr[:n].copy()
