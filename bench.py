@@ -204,7 +204,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="encoder", choices=["encoder", "layer", "ragged", "quant", "quant4", "gemv", "copy", "mel"])
+    ap.add_argument("--workload", default="encoder", choices=["encoder", "layer", "ragged", "quant", "quant4", "gemv", "copy", "mel", "decode"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -218,6 +218,8 @@ def main():
         return bench_copy(args, fa, ctx)
     if args.workload == "mel":
         return bench_mel(args, fa, ctx)
+    if args.workload == "decode":
+        return bench_decode(args, fa, ctx)
     cfg = dict(FULL)
     layout = "packed"
     if args.workload in ("encoder", "quant", "quant4"):
@@ -333,6 +335,60 @@ def bench_mel(args, fa, ctx):
         cw = time.perf_counter() - t0
         line["cpu_baseline"] = {"value": round(2 * win / 16000 / cw, 1), "unit": "audio-s/wall-s", "cores": 1, "kind": "port",
                                 "sample": "2 of the 16 windows (30 s of audio) through the oracle's restatement of nemotron-mel.js (oracle/fa_oracle.c or_mel, single thread)"}
+    print(json.dumps(line), flush=True)
+
+
+def bench_decode(args, fa, ctx):
+    """Greedy TDT decoding (fa_tdt_decode) of the configs[2] encoder output: 16
+    windows x 188 pre-projected frames (synthetic ~N(0,1), seed 1; synthetic
+    decoder weights with a blank bias that gives ~1 token per 3 frames).
+    value = audio-s (16 x 15 s) / wall-s of the whole decode call (steps in
+    lock-step on the GPU, results copied to the host)."""
+    dec_w = fa.synth.make_decoder_weights(1)
+    n_win, T = 16, 188
+    frames_h = np.concatenate([fa.synth.make_projected_frames(T, seed=100 + i) for i in range(n_win)])
+    frames = ctx.upload(frames_h, frames_h.shape[0], 640)
+    dec = fa.TdtDecoder(ctx, dec_w)
+    lens = [T] * n_win
+    for _ in range(args.warmup):
+        dec.decodeBatch(frames, lens)
+    ctx.startProfile(200000)
+    res = dec.decodeBatch(frames, lens)
+    prof = ctx.endProfile()
+    tokens = sum(r["count"] for r in res)
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        dec.decodeBatch(frames, lens)
+    wall = time.perf_counter() - t0
+    kern = {}
+    for r in prof:
+        k = kern.setdefault(r["label"], {"launches": 0, "total_ms": 0.0})
+        k["launches"] += 1
+        k["total_ms"] += r["ms"]
+    for k in kern.values():
+        k["avg_us"] = round(k["total_ms"] / k["launches"] * 1e3, 2)
+        k["total_ms"] = round(k["total_ms"], 3)
+    j = kern.get("tdt_joint", {"avg_us": 0.0, "launches": 0})
+    jbytes = 640 * 8198 * 4  # the joint matrix, read once per step for the batch
+    audio_s = n_win * 15.0 * args.steps
+    line = {"metric": "greedy TDT decode audio-s/wall-s at 1 GPU", "value": round(audio_s / wall, 1), "unit": "audio-s/wall-s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 3), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic projected frames ~N(0,1), synthetic decoder weights (seed 1)",
+            "config": {"workload": "configs[2] encoder output: 16 windows x 188 frames, greedy TDT (durations 0..4, <= 10 symbols/frame)",
+                       "windows": n_win, "frames": n_win * T, "tokens": tokens, "decode_steps": j["launches"]},
+            "roofline": {"bound": "hbm", "achieved": round(jbytes / max(j["avg_us"], 1e-9) * 1e-3, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(jbytes / max(j["avg_us"], 1e-9) * 1e-3 / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "tdt_joint",
+                         "avg_us": j["avg_us"], "launches_timed": j["launches"]},
+            "kernels": kern}
+    if not args.no_cpu:
+        orc = ge.load_oracle()
+        t0 = time.perf_counter()
+        orc.tdt_decode(dec_w, frames_h[:T])
+        cw = time.perf_counter() - t0
+        line["cpu_baseline"] = {"value": round(15.0 / cw, 1), "unit": "audio-s/wall-s", "cores": 1, "kind": "port",
+                                "sample": "1 of the 16 windows through the oracle's restatement of decode_proj (oracle/fa_oracle.c or_tdt_decode_proj, single thread)"}
+    dec.close()
     print(json.dumps(line), flush=True)
 
 

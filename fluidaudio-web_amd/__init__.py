@@ -13,7 +13,8 @@ from ._lib import ACT, FaError, lib
 from .compute import HipContext, HipTensor, PackedBytes, createContext
 from .encoder import FusedEncoder, inferConfig, loadParakeetEncoder, parakeetEncodeBatch, posEncoding, tsub
 from .mel import JsPreprocessor, ParakeetMel
+from .decoder import TdtDecoder
 from . import synth, windowing
 
 __all__ = ["ACT", "FaError", "lib", "HipContext", "HipTensor", "PackedBytes", "createContext", "FusedEncoder", "inferConfig",
-           "loadParakeetEncoder", "parakeetEncodeBatch", "posEncoding", "tsub", "synth", "windowing", "JsPreprocessor", "ParakeetMel"]
+           "loadParakeetEncoder", "parakeetEncodeBatch", "posEncoding", "tsub", "synth", "windowing", "JsPreprocessor", "ParakeetMel", "TdtDecoder"]

@@ -97,6 +97,9 @@ SIGNATURES = [
     ("fa_gemv_quant", I, [P, T, T, T, I, I, I, C.POINTER(T)]),
     ("fa_pack_windows", I, [P, T, I32P, I32P, I, I, C.POINTER(T)]),
     ("fa_mel_windows", I, [P, T, I32P, I32P, I, I, C.c_double, I, C.POINTER(T)]),
+    ("fa_tdt_load", I, [P, C.POINTER(C.POINTER(C.c_float)), C.POINTER(P)]),
+    ("fa_tdt_destroy", None, [P]),
+    ("fa_tdt_decode", I, [P, T, I32P, I, I, I32P, I32P, I32P]),
     ("fa_window_row_map", I, [P, I32P, I, I, I, I32P, C.POINTER(I)]),
     ("fa_encoder_load", I, [P, C.POINTER(EncoderCfg), I, C.POINTER(C.c_char_p), C.POINTER(F32P), C.POINTER(C.c_int64), I, I, C.POINTER(P)]),
     ("fa_encoder_destroy", None, [P]),

@@ -200,6 +200,26 @@ int fa_gemv_quant(fa_ctx *ctx, fa_tensor a, fa_tensor w, fa_tensor scales, int f
  * Windows may overlap in the stream.  starts/lens are host arrays. */
 int fa_pack_windows(fa_ctx *ctx, fa_tensor feats, const int32_t *starts, const int32_t *lens, int n, int layout, fa_tensor *out);
 
+/* ── greedy TDT decoding (joint + prediction network + token loop) ───────────
+ * Replaces the decoder the pipeline runs after each encoder batch:
+ * rust/parakeet-decoder/src/lib.rs decode_proj (:285-318), reached through
+ * src/engines/asr-parakeet/raw-decoder-wasm.js, and its WebGPU port
+ * gpuDecodeBatch (src/engines/asr-parakeet/gpu-decoder.js:248-273).  Same
+ * arithmetic as decode_proj (f32, its polynomial expf, lane-ordered dots), so
+ * token ids and frames equal the reference's.
+ * fa_tdt_load: w = 11 host f32 arrays in the reference's decoder manifest order
+ *   embed [8193*640], l0_W [2560*640], l0_R [2560*640], l0_B [5120], l1_W, l1_R,
+ *   l1_B, predW [640*640] (k-major), predB [640], outW [640*8198], outB [8198].
+ * fa_tdt_decode: frames = f32 [rows, 640] pre-projected encoder frames (the
+ *   joint's encoder projection applied, pipeline.js:57-61), window i = lens[i]
+ *   rows after the previous windows' rows; writes up to cap token ids and their
+ *   frame indices per window (ids / frame_idx are [n][cap]) and each window's
+ *   token count (may exceed cap: the tokens past cap are dropped).  Synchronous. */
+typedef struct fa_tdt fa_tdt;
+int fa_tdt_load(fa_ctx *ctx, const float *const *w, fa_tdt **out);
+void fa_tdt_destroy(fa_tdt *dec);
+int fa_tdt_decode(fa_tdt *dec, fa_tensor frames, const int32_t *lens, int n, int cap, int32_t *ids, int32_t *frame_idx, int32_t *counts);
+
 /* ── log-mel front end (PCM windows -> the feature stream above) ─────────────
  * Replaces ParakeetMel.process (src/engines/asr-parakeet/parakeet-mel.js:14-22)
  * applied to each window slice of the sample stream, as the pipeline's mel
