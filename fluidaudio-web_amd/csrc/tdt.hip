@@ -18,8 +18,8 @@
 //                       per window group); per-block argmax per window
 //   tdt_update_kernel   per window: final argmax, token record, TDT advance,
 //                       emit flag; H, C <- candidate state when a token was emitted
-//   tdt_z_kernel        LSTM gate pre-activations, gate row per thread, the
-//                       layer's weights read once per group of windows
+//   tdt_z_kernel        LSTM gate pre-activations: thread = (gate row, one of
+//                       the dot's four lane sums), a group of windows per block
 //   tdt_gates_kernel    LSTM cell -> candidate state
 //   tdt_proj_kernel     pred projection (emitting windows) and the next joint
 //                       input relu(frame + pred) (every active window)
@@ -42,12 +42,12 @@ constexpr int TNB = (TL + TJB - 1) / TJB;  // joint blocks (129)
 
 struct TdtWin {
   int t, T, emitted, n_out, emit, off, last;
-  int pad;
+  int cur;  // slot of the committed LSTM state; the candidate is in 1 - cur
 };
 
 struct TdtState {
   TdtWin *win;
-  float *h, *c, *nh, *nc;  // [n][2][TH]
+  float *h, *c;            // [n][slot 2][layer 2][TH]: committed (cur) and candidate states
   float *pp, *j;           // [n][TH]
   float *z;                // [n][4 TH]
   float *pv;               // [n][TNB] token partial maxima
@@ -111,56 +111,57 @@ __device__ void block_argmax(float v, int i, float *rv, int *ri, float &ov, int 
 
 // Block = 64 logits, one per thread; every thread keeps the accumulators of
 // a group of windows and sums over hidden units n in order (the reference's
-// axpy order), the weight column loads issued 16 ahead of the adds.
-__global__ __launch_bounds__(64) void tdt_joint_kernel(const float *__restrict__ out_w, const float *__restrict__ out_b, TdtState st, int n) {
-  __shared__ float js[TG][TH];
+// axpy order), the weight column loads issued ahead of the adds.  The joint
+// inputs are wave-uniform (scalar loads).  The reference skips n with
+// j[n] == 0; with finite weights adding 0·w changes no value (at most the sign
+// of an exact zero, which compares equal), so the sum here does not branch.
+__global__ __launch_bounds__(64) void tdt_joint_kernel(const float *__restrict__ out_w, const float *__restrict__ out_b,
+                                                       const float *__restrict__ jin, TdtState st, int n) {
   __shared__ float rv[64];
   __shared__ int ri[64];
   const int tid = threadIdx.x, m = blockIdx.x * TJB + tid;
   const bool valid = m < TL;
-  {
-    const int w0 = blockIdx.y * TG;
-    bool any = false;
-    for (int g = 0; g < TG && w0 + g < n; g++) any |= st.win[w0 + g].t < st.win[w0 + g].T;
-    if (!any) return;  // uniform: every thread reads the same flags
-    for (int e = tid; e < TG * TH; e += 64) {
-      const int g = e / TH, k = e % TH, w = w0 + g;
-      js[g][k] = (w < n && st.win[w].t < st.win[w].T) ? st.j[(size_t)w * TH + k] : 0.f;
+  const int w0 = blockIdx.y * TG;
+  bool act[TG];
+  bool any = false;
+#pragma unroll
+  for (int g = 0; g < TG; g++) {
+    act[g] = w0 + g < n && st.win[w0 + g].t < st.win[w0 + g].T;
+    any |= act[g];
+  }
+  if (!any) return;  // uniform: every thread reads the same flags
+  const float *jw[TG];
+#pragma unroll
+  for (int g = 0; g < TG; g++) jw[g] = jin + (size_t)(act[g] ? w0 + g : w0) * TH;  // inactive: any valid row, never used
+  float acc[TG];
+  const float b = valid ? out_b[m] : 0.f;
+#pragma unroll
+  for (int g = 0; g < TG; g++) acc[g] = b;
+  const float *col = out_w + (valid ? m : 0);
+  for (int k0 = 0; k0 < TH; k0 += 32) {
+    float wv[32];
+#pragma unroll
+    for (int u = 0; u < 32; u++) wv[u] = col[(size_t)(k0 + u) * TL];
+#pragma unroll
+    for (int u = 0; u < 32; u++)
+#pragma unroll
+      for (int g = 0; g < TG; g++) acc[g] = acc[g] + jw[g][k0 + u] * wv[u];
+  }
+  for (int g = 0; g < TG; g++) {
+    const int w = w0 + g;
+    if (!act[g]) continue;  // uniform
+    float bv;
+    int bi;
+    block_argmax((valid && m < TV) ? acc[g] : -INFINITY, (valid && m < TV) ? m : 0x7fffffff, rv, ri, bv, bi);
+    if (tid == 0) {
+      st.pv[w * TNB + blockIdx.x] = bv;
+      st.pi[w * TNB + blockIdx.x] = bi;
     }
-    __syncthreads();
-    float acc[TG];
-    const float b = valid ? out_b[m] : 0.f;
-#pragma unroll
-    for (int g = 0; g < TG; g++) acc[g] = b;
-    const float *col = out_w + (valid ? m : 0);
-    for (int k0 = 0; k0 < TH; k0 += 16) {
-      float wv[16];
-#pragma unroll
-      for (int u = 0; u < 16; u++) wv[u] = col[(size_t)(k0 + u) * TL];
-#pragma unroll
-      for (int u = 0; u < 16; u++)
-#pragma unroll
-        for (int g = 0; g < TG; g++) {
-          const float jn = js[g][k0 + u];
-          if (jn != 0.0f) acc[g] = acc[g] + jn * wv[u];
-        }
-    }
-    for (int g = 0; g < TG; g++) {
-      const int w = w0 + g;
-      if (w >= n || st.win[w].t >= st.win[w].T) continue;  // uniform
-      float bv;
-      int bi;
-      block_argmax((valid && m < TV) ? acc[g] : -INFINITY, (valid && m < TV) ? m : 0x7fffffff, rv, ri, bv, bi);
+    if (blockIdx.x == TNB - 1) {
+      block_argmax((valid && m >= TV) ? acc[g] : -INFINITY, (valid && m >= TV) ? m - TV : 0x7fffffff, rv, ri, bv, bi);
       if (tid == 0) {
-        st.pv[w * TNB + blockIdx.x] = bv;
-        st.pi[w * TNB + blockIdx.x] = bi;
-      }
-      if (blockIdx.x == TNB - 1) {
-        block_argmax((valid && m >= TV) ? acc[g] : -INFINITY, (valid && m >= TV) ? m - TV : 0x7fffffff, rv, ri, bv, bi);
-        if (tid == 0) {
-          st.dv[w] = bv;
-          st.di[w] = bi;
-        }
+        st.dv[w] = bv;
+        st.di[w] = bi;
       }
     }
   }
@@ -173,7 +174,6 @@ __global__ __launch_bounds__(64) void tdt_joint_kernel(const float *__restrict__
 __global__ __launch_bounds__(64) void tdt_update_kernel(TdtState st, int cap) {
   __shared__ float rv[64];
   __shared__ int ri[64];
-  __shared__ int emit;
   const int w = blockIdx.x, tid = threadIdx.x;
   TdtWin s = st.win[w];
   if (s.t >= s.T) {  // uniform
@@ -205,6 +205,7 @@ __global__ __launch_bounds__(64) void tdt_update_kernel(TdtState st, int cap) {
       s.emitted++;
       s.emit = 1;
       s.last = tok;
+      s.cur ^= 1;  // commit_state: the candidate slot becomes the committed one
     }
     if (step > 0) {
       s.t += step;
@@ -215,84 +216,76 @@ __global__ __launch_bounds__(64) void tdt_update_kernel(TdtState st, int cap) {
     }
     st.win[w] = s;
     st.alive[w] = s.t < s.T;
-    emit = s.emit;
   }
-  __syncthreads();
-  if (emit)
-    for (int e = tid; e < 2 * TH; e += 64) {
-      st.h[(size_t)w * 2 * TH + e] = st.nh[(size_t)w * 2 * TH + e];
-      st.c[(size_t)w * 2 * TH + e] = st.nc[(size_t)w * 2 * TH + e];
-    }
 }
 
 // Gate pre-activations of one LSTM layer for the windows that emitted:
 // z[r] = ((b[r] + b[4H + r]) + W[r]·x) + R[r]·h.  The reference's dot keeps
 // four lane sums (k = l mod 4, k ascending) added as ((s0 + s1) + s2) + s3, so
 // each lane sum is one thread here: thread = (gate row r, lane l), 64 rows x
-// 4 lanes per block; W and R are stored k-major (WT[k][r]) so the loads of a
-// k are contiguous across rows.  Layer 0 reads x = embed[last token], layer 1
-// x = the layer-0 candidate hidden state.
+// 4 lanes per block, a group of windows per block (x and h staged in LDS); W
+// and R are stored k-major (WT[k][r]) so the loads of a k are contiguous
+// across rows.  Layer 0 reads x = embed[last token], layer 1 x = the layer-0
+// candidate hidden state.
 __global__ __launch_bounds__(256) void tdt_z_kernel(const float *__restrict__ WT, const float *__restrict__ RT, const float *__restrict__ B,
                                                     const float *__restrict__ embed, int layer, TdtState st, int n) {
-  __shared__ float xs[TG][TH], hs[TG][TH];
+  __shared__ float xs[TG][TH], hsm[TG][TH];
   __shared__ float part[2][TG][64][4];
   const int l = threadIdx.x & 3, rl = threadIdx.x >> 2, r = blockIdx.x * 64 + rl;  // 40 blocks
-  {
-    const int w0 = blockIdx.y * TG;
-    bool any = false;
-    for (int g = 0; g < TG && w0 + g < n; g++) any |= st.win[w0 + g].emit != 0;
-    if (!any) return;
-    for (int e = threadIdx.x; e < TG * TH; e += 256) {
-      const int g = e / TH, k = e % TH, w = w0 + g;
-      float xv = 0.f, hv = 0.f;
-      if (w < n && st.win[w].emit) {
-        xv = layer == 0 ? embed[(size_t)st.win[w].last * TH + k] : st.nh[(size_t)w * 2 * TH + k];
-        hv = st.h[((size_t)w * 2 + layer) * TH + k];
-      }
-      xs[g][k] = xv;
-      hs[g][k] = hv;
+  const int w0 = blockIdx.y * TG;
+  bool any = false;
+  for (int g = 0; g < TG && w0 + g < n; g++) any |= st.win[w0 + g].emit != 0;
+  if (!any) return;
+  for (int e = threadIdx.x; e < TG * TH; e += 256) {
+    const int g = e / TH, k = e % TH, w = w0 + g;
+    float xv = 0.f, hv = 0.f;
+    if (w < n && st.win[w].emit) {
+      const int cur = st.win[w].cur;
+      xv = layer == 0 ? embed[(size_t)st.win[w].last * TH + k] : st.h[(((size_t)w * 2 + (cur ^ 1)) * 2 + 0) * TH + k];
+      hv = st.h[(((size_t)w * 2 + cur) * 2 + layer) * TH + k];
     }
-    __syncthreads();
-    float aw[TG], ar[TG];
+    xs[g][k] = xv;
+    hsm[g][k] = hv;
+  }
+  __syncthreads();
+  float aw[TG], ar[TG];
 #pragma unroll
-    for (int g = 0; g < TG; g++) aw[g] = ar[g] = 0.f;
-    for (int i0 = 0; i0 < TH / 4; i0 += 8) {
-      float wv[8], rv[8];
+  for (int g = 0; g < TG; g++) aw[g] = ar[g] = 0.f;
+  for (int i0 = 0; i0 < TH / 4; i0 += 32) {
+    float wv[32], rv[32];
 #pragma unroll
-      for (int u = 0; u < 8; u++) {
-        const int k = 4 * (i0 + u) + l;
-        wv[u] = WT[(size_t)k * 4 * TH + r];
-        rv[u] = RT[(size_t)k * 4 * TH + r];
-      }
-#pragma unroll
-      for (int u = 0; u < 8; u++) {
-        const int k = 4 * (i0 + u) + l;
-#pragma unroll
-        for (int g = 0; g < TG; g++) {
-          aw[g] = aw[g] + wv[u] * xs[g][k];
-          ar[g] = ar[g] + rv[u] * hs[g][k];
-        }
-      }
+    for (int u = 0; u < 32; u++) {
+      const int k = 4 * (i0 + u) + l;
+      wv[u] = WT[(size_t)k * 4 * TH + r];
+      rv[u] = RT[(size_t)k * 4 * TH + r];
     }
 #pragma unroll
-    for (int g = 0; g < TG; g++) {
-      part[0][g][rl][l] = aw[g];
-      part[1][g][rl][l] = ar[g];
-    }
-    __syncthreads();
-    if (l == 0) {
-      const float b = B[r] + B[4 * TH + r];
+    for (int u = 0; u < 32; u++) {
+      const int k = 4 * (i0 + u) + l;
+#pragma unroll
       for (int g = 0; g < TG; g++) {
-        const int w = w0 + g;
-        if (w < n && st.win[w].emit) {
-          const float *pw = part[0][g][rl], *pr = part[1][g][rl];
-          const float dw = pw[0] + pw[1] + pw[2] + pw[3];
-          const float dr = pr[0] + pr[1] + pr[2] + pr[3];
-          st.z[(size_t)w * 4 * TH + r] = b + dw + dr;
-        }
+        aw[g] = aw[g] + wv[u] * xs[g][k];
+        ar[g] = ar[g] + rv[u] * hsm[g][k];
       }
     }
-    __syncthreads();
+  }
+#pragma unroll
+  for (int g = 0; g < TG; g++) {
+    part[0][g][rl][l] = aw[g];
+    part[1][g][rl][l] = ar[g];
+  }
+  __syncthreads();
+  if (l == 0) {
+    const float b = B[r] + B[4 * TH + r];
+    for (int g = 0; g < TG; g++) {
+      const int w = w0 + g;
+      if (w < n && st.win[w].emit) {
+        const float *pw = part[0][g][rl], *pr = part[1][g][rl];
+        const float dw = pw[0] + pw[1] + pw[2] + pw[3];
+        const float dr = pr[0] + pr[1] + pr[2] + pr[3];
+        st.z[(size_t)w * 4 * TH + r] = b + dw + dr;
+      }
+    }
   }
 }
 
@@ -302,54 +295,36 @@ __global__ __launch_bounds__(256) void tdt_gates_kernel(int layer, TdtState st) 
   if (g >= TH || !st.win[w].emit) return;
   const float *z = st.z + (size_t)w * 4 * TH;
   const float zi = z[g], zo = z[TH + g], zf = z[2 * TH + g], zc = z[3 * TH + g];
-  const size_t o = ((size_t)w * 2 + layer) * TH + g;
+  const int cur = st.win[w].cur;
+  const size_t o = (((size_t)w * 2 + cur) * 2 + layer) * TH + g, on = (((size_t)w * 2 + (cur ^ 1)) * 2 + layer) * TH + g;
   const float cc = tdt_sigmoid(zf) * st.c[o] + tdt_sigmoid(zi) * tdt_tanhf(zc);
-  st.nc[o] = cc;
-  st.nh[o] = tdt_sigmoid(zo) * tdt_tanhf(cc);
+  st.c[on] = cc;
+  st.h[on] = tdt_sigmoid(zo) * tdt_tanhf(cc);
 }
 
-// Pred projection of the windows that emitted (pp[n] = b[n] + Σ_k dec[k] w[k][n],
-// k in order), then the next joint input j = relu(frame[t] + pp) of every
-// active window.  Block = 64 output units (10 blocks); loads issued 16 ahead.
+// Pred projection of one window if it emitted (pp[n] = b[n] + Σ_k dec[k] w[k][n],
+// k in order; dec arrives as scalar loads), then its next joint input
+// j = relu(frame[t] + pp) if it is still active.  Block = 64 output units x one
+// window (10 x n blocks); weight loads issued ahead of the adds.
 __global__ __launch_bounds__(64) void tdt_proj_kernel(const float *__restrict__ pw, const float *__restrict__ pb, const float *__restrict__ frames,
-                                                      TdtState st, int n) {
-  __shared__ float ds[TG][TH];
-  const int u = blockIdx.x * 64 + threadIdx.x;
-  {
-    const int w0 = blockIdx.y * TG;
-    bool any = false;
-    for (int g = 0; g < TG && w0 + g < n; g++) any |= st.win[w0 + g].emit != 0;
-    if (any) {
-      for (int e = threadIdx.x; e < TG * TH; e += 64) {
-        const int g = e / TH, k = e % TH, w = w0 + g;
-        ds[g][k] = (w < n && st.win[w].emit) ? st.nh[((size_t)w * 2 + 1) * TH + k] : 0.f;
-      }
-      __syncthreads();
-      float acc[TG];
-      const float b = pb[u];
+                                                      const float *__restrict__ hs, TdtState st) {
+  const int u = blockIdx.x * 64 + threadIdx.x, w = blockIdx.y;
+  const TdtWin s = st.win[w];
+  if (__builtin_amdgcn_readfirstlane(s.emit)) {  // uniform
+    const float *dec = hs + (((size_t)w * 2 + (__builtin_amdgcn_readfirstlane(s.cur) ^ 1)) * 2 + 1) * TH;
+    float acc = pb[u];
+    for (int k0 = 0; k0 < TH; k0 += 64) {
+      float wv[64];
 #pragma unroll
-      for (int g = 0; g < TG; g++) acc[g] = b;
-      for (int k0 = 0; k0 < TH; k0 += 16) {
-        float wv[16];
+      for (int q = 0; q < 64; q++) wv[q] = pw[(size_t)(k0 + q) * TH + u];
 #pragma unroll
-        for (int q = 0; q < 16; q++) wv[q] = pw[(size_t)(k0 + q) * TH + u];
-#pragma unroll
-        for (int q = 0; q < 16; q++)
-#pragma unroll
-          for (int g = 0; g < TG; g++) acc[g] = acc[g] + ds[g][k0 + q] * wv[q];
-      }
-#pragma unroll
-      for (int g = 0; g < TG; g++)
-        if (w0 + g < n && st.win[w0 + g].emit) st.pp[(size_t)(w0 + g) * TH + u] = acc[g];
-      __syncthreads();
+      for (int q = 0; q < 64; q++) acc = acc + dec[k0 + q] * wv[q];
     }
-    for (int g = 0; g < TG && w0 + g < n; g++) {
-      const TdtWin s = st.win[w0 + g];
-      if (s.t < s.T) {
-        const float v = frames[(size_t)(s.off + s.t) * TH + u] + st.pp[(size_t)(w0 + g) * TH + u];
-        st.j[(size_t)(w0 + g) * TH + u] = v > 0.0f ? v : 0.0f;
-      }
-    }
+    st.pp[(size_t)w * TH + u] = acc;
+  }
+  if (s.t < s.T) {
+    const float v = frames[(size_t)(s.off + s.t) * TH + u] + st.pp[(size_t)w * TH + u];
+    st.j[(size_t)w * TH + u] = v > 0.0f ? v : 0.0f;
   }
 }
 
@@ -422,7 +397,7 @@ int fa_tdt_decode(fa_tdt *d, fa_tensor frames, const int32_t *lens, int n, int c
   int tmax = 0;
   for (int i = 0; i < n; i++) {
     if (lens[i] < 0) return set_err(ctx, FA_E_INVALID, "tdtDecode: window %d length %d", i, lens[i]);
-    win[i] = TdtWin{0, lens[i], 0, 0, lens[i] > 0 ? 1 : 0, (int)off, TBLANK, 0};
+    win[i] = TdtWin{0, lens[i], 0, 0, lens[i] > 0 ? 1 : 0, (int)off, TBLANK, 0};  // committed state in slot 0 (zero)
     off += lens[i];
     tmax = std::max(tmax, lens[i]);
   }
@@ -434,8 +409,7 @@ int fa_tdt_decode(fa_tdt *d, fa_tensor frames, const int32_t *lens, int n, int c
     o += (bytes + 255) & ~(size_t)255;
     return at;
   };
-  const size_t o_win = take(sizeof(TdtWin) * n), o_h = take(4ul * n * 2 * TH), o_c = take(4ul * n * 2 * TH), o_nh = take(4ul * n * 2 * TH),
-               o_nc = take(4ul * n * 2 * TH), o_pp = take(4ul * n * TH), o_j = take(4ul * n * TH), o_z = take(4ul * n * 4 * TH),
+  const size_t o_win = take(sizeof(TdtWin) * n), o_h = take(4ul * n * 4 * TH), o_c = take(4ul * n * 4 * TH), o_pp = take(4ul * n * TH), o_j = take(4ul * n * TH), o_z = take(4ul * n * 4 * TH),
                o_pv = take(4ul * n * TNB), o_pi = take(4ul * n * TNB), o_dv = take(4ul * n), o_di = take(4ul * n), o_ids = take(4ul * n * cap),
                o_frs = take(4ul * n * cap), o_act = take(4ul * n);
   if (d->state_bytes < o) {
@@ -453,8 +427,6 @@ int fa_tdt_decode(fa_tdt *d, fa_tensor frames, const int32_t *lens, int n, int c
   st.win = (TdtWin *)(base + o_win);
   st.h = (float *)(base + o_h);
   st.c = (float *)(base + o_c);
-  st.nh = (float *)(base + o_nh);
-  st.nc = (float *)(base + o_nc);
   st.pp = (float *)(base + o_pp);
   st.j = (float *)(base + o_j);
   st.z = (float *)(base + o_z);
@@ -468,19 +440,20 @@ int fa_tdt_decode(fa_tdt *d, fa_tensor frames, const int32_t *lens, int n, int c
   rf = get(ctx, frames);
   const float *fr = (const float *)rf->ptr;
   const int ng = (n + TG - 1) / TG;  // window groups
-  FA_HIP(ctx, hipMemsetAsync(base + o_h, 0, o_nh - o_h, ctx->stream));  // H, C = 0
+  FA_HIP(ctx, hipMemsetAsync(base + o_h, 0, o_pp - o_h, ctx->stream));  // both state slots = 0
   FA_HIP(ctx, hipMemcpyAsync(st.win, win.data(), sizeof(TdtWin) * n, hipMemcpyHostToDevice, ctx->stream));
   auto predict = [&]() -> int {  // candidate state + pred projection for windows with emit set
     for (int layer = 0; layer < 2; layer++) {
       {
         ProfScope ps(ctx, "tdt_lstm_z");
-        FA_LAUNCH(ps, tdt_z_kernel, dim3(4 * TH / 64, ng), dim3(256), 0, ctx->stream, d->lw[layer], d->lr[layer], d->lb[layer], d->embed, layer, st, n);
+        FA_LAUNCH(ps, tdt_z_kernel, dim3(4 * TH / 64, ng), dim3(256), 0, ctx->stream, d->lw[layer], d->lr[layer], d->lb[layer], d->embed, layer,
+                  st, n);
       }
       ProfScope ps(ctx, "tdt_lstm_cell");
       FA_LAUNCH(ps, tdt_gates_kernel, dim3(cdiv(TH, 256), n), dim3(256), 0, ctx->stream, layer, st);
     }
     ProfScope ps(ctx, "tdt_proj");
-    FA_LAUNCH(ps, tdt_proj_kernel, dim3(TH / 64, ng), dim3(64), 0, ctx->stream, d->pred_w, d->pred_b, fr, st, n);
+    FA_LAUNCH(ps, tdt_proj_kernel, dim3(TH / 64, n), dim3(64), 0, ctx->stream, d->pred_w, d->pred_b, fr, (const float *)st.h, st);
     return check_launch(ctx, "tdt_predict");
   };
   FA_TRY(predict());  // predict(BLANK) from the zero state, then j for t = 0
@@ -494,7 +467,7 @@ int fa_tdt_decode(fa_tdt *d, fa_tensor frames, const int32_t *lens, int n, int c
     for (int k = 0; k < kChunk; k++) {
       {
         ProfScope ps(ctx, "tdt_joint");
-        FA_LAUNCH(ps, tdt_joint_kernel, dim3(TNB, ng), dim3(64), 0, ctx->stream, d->out_w, d->out_b, st, n);
+        FA_LAUNCH(ps, tdt_joint_kernel, dim3(TNB, ng), dim3(64), 0, ctx->stream, d->out_w, d->out_b, (const float *)st.j, st, n);
       }
       {
         ProfScope ps(ctx, "tdt_update");
