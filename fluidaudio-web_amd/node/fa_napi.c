@@ -348,6 +348,53 @@ static napi_value js_mel_windows(napi_env env, napi_callback_info info) {
   return st ? throw_status(env, c, st) : mkbig(env, o);
 }
 
+/* tdtLoad(ctx, [Float32Array x 11] in the decoder manifest order) -> external */
+static napi_value js_tdt_load(napi_env env, napi_callback_info info) {
+  napi_value a[MAXA];
+  if (!args(env, info, 2, a)) return NULL;
+  CTX;
+  const float *w[11];
+  for (uint32_t i = 0; i < 11; i++) {
+    napi_value d;
+    NA(napi_get_element(env, a[1], i, &d));
+    w[i] = typed(env, d, NULL);
+  }
+  fa_tdt *dec = NULL;
+  int st = fa_tdt_load(c, w, &dec);
+  if (st) return throw_status(env, c, st);
+  napi_value r;
+  NA(napi_create_external(env, dec, NULL, NULL, &r));
+  return r;
+}
+
+/* tdtDecode(ctx, dec, frames, Int32Array lens, cap, Int32Array ids, Int32Array frameIdx, Int32Array counts) */
+static napi_value js_tdt_decode(napi_env env, napi_callback_info info) {
+  napi_value a[MAXA];
+  if (!args(env, info, 8, a)) return NULL;
+  CTX;
+  size_t nl = 0, ni = 0, nf = 0, nc = 0;
+  int32_t *lens = typed(env, a[3], &nl), *ids = typed(env, a[5], &ni), *fr = typed(env, a[6], &nf), *cnt = typed(env, a[7], &nc);
+  const int n = (int)(nl / 4), cap = I(4);
+  if (!lens || !ids || !fr || !cnt || cap <= 0 || ni < (size_t)n * cap * 4 || nf < ni || nc < (size_t)n * 4) {
+    napi_throw_type_error(env, NULL, "tdtDecode: lens / ids / frameIdx / counts must be Int32Arrays of n, n*cap, n*cap, n");
+    return NULL;
+  }
+  int st = fa_tdt_decode((fa_tdt *)ext(env, a[1]), T(2), lens, n, cap, ids, fr, cnt);
+  if (st) return throw_status(env, c, st);
+  napi_value u;
+  NA(napi_get_undefined(env, &u));
+  return u;
+}
+
+static napi_value js_tdt_destroy(napi_env env, napi_callback_info info) {
+  napi_value a[MAXA];
+  if (!args(env, info, 1, a)) return NULL;
+  fa_tdt_destroy((fa_tdt *)ext(env, a[0]));
+  napi_value u;
+  NA(napi_get_undefined(env, &u));
+  return u;
+}
+
 static void enc_finalize(napi_env env, void *data, void *hint) {
   (void)env;
   (void)hint;
@@ -433,7 +480,7 @@ static napi_value init(napi_env env, napi_value exports) {
       EXPORT("concatRows", js_concat_rows), EXPORT("subReshape", js_sub_reshape), EXPORT("rowBiasAct", js_row_bias_act),
       EXPORT("profileStart", js_profile_start), EXPORT("profileEnd", js_profile_end), EXPORT("packWindows", js_pack_windows), EXPORT("melWindows", js_mel_windows),
       EXPORT("encoderLoad", js_encoder_load), EXPORT("encoderForward", js_encoder_forward), EXPORT("encoderDestroy", js_encoder_destroy),
-      EXPORT("encoderTsub", js_encoder_tsub),
+      EXPORT("encoderTsub", js_encoder_tsub), EXPORT("tdtLoad", js_tdt_load), EXPORT("tdtDecode", js_tdt_decode), EXPORT("tdtDestroy", js_tdt_destroy),
   };
   napi_define_properties(env, exports, sizeof d / sizeof d[0], d);
   return exports;

@@ -259,6 +259,28 @@ class HipContext {
   _melWindows(pcm, starts, lens, nMels = 128, logGuard = 2 ** -24, normalize = true) {
     return this._info(addon.melWindows(this.ctx, pcm.h, Int32Array.from(starts), Int32Array.from(lens), nMels, logGuard, normalize ? 1 : 0));
   }
+  /** Greedy TDT decoder weights (loadGpuDecoder, gpu-decoder.js:220-246): an
+   * object of Float32Arrays in the decoder manifest naming. */
+  _loadTdtDecoder(w) {
+    const keys = ["embed", "l0_W", "l0_R", "l0_B", "l1_W", "l1_R", "l1_B", "predW", "predB", "outW", "outB"];
+    return { dec: addon.tdtLoad(this.ctx, keys.map((k) => (w[k] instanceof Float32Array ? w[k] : Float32Array.from(w[k])))) };
+  }
+  /** gpuDecodeBatch (gpu-decoder.js:248-273): frames = tensor [Σ lens, 640] of
+   * pre-projected encoder frames -> per window { ids, idFrames }. */
+  _tdtDecodeBatch(d, frames, lens, cap = 4096) {
+    const n = lens.length;
+    const ids = new Int32Array(n * cap), fr = new Int32Array(n * cap), cnt = new Int32Array(n);
+    addon.tdtDecode(this.ctx, d.dec, this.ensureTensor(frames).h, Int32Array.from(lens), cap, ids, fr, cnt);
+    const out = [];
+    for (let w = 0; w < n; w++) {
+      const k = Math.min(cnt[w], cap);
+      out.push({ ids: Array.from(ids.subarray(w * cap, w * cap + k)), idFrames: Array.from(fr.subarray(w * cap, w * cap + k)) });
+    }
+    return out;
+  }
+  _destroyTdtDecoder(d) {
+    addon.tdtDestroy(d.dec);
+  }
   destroyFusedEncoder(fused) {
     addon.encoderDestroy(fused.enc);
   }

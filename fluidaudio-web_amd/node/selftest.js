@@ -114,6 +114,18 @@ const check = (name, d, tol) => {
   check("melWindows stream == windows alone", md, 0);
   const sil = await ctx.download(ctx._melWindows(ctx.upload(new Float32Array(4800), 1, 4800), [0], [4800]));
   check("melWindows silence normalises to 0", sil.reduce((a, b) => Math.max(a, Math.abs(b)), 0), 0);
+  // greedy TDT decode through the binding: constant logits (outW = 0) with
+  // token 5 and duration 0 on top -> 10 symbols per frame (MAX_SYMBOLS)
+  const dz = (n) => new Float32Array(n);
+  const outB = dz(8198);
+  outB[5] = 1;
+  outB[8193] = 1;
+  const tdt = ctx._loadTdtDecoder({ embed: dz(8193 * 640), l0_W: dz(2560 * 640), l0_R: dz(2560 * 640), l0_B: dz(5120), l1_W: dz(2560 * 640),
+    l1_R: dz(2560 * 640), l1_B: dz(5120), predW: dz(640 * 640), predB: dz(640), outW: dz(640 * 8198), outB });
+  const dres = ctx._tdtDecodeBatch(tdt, ctx.upload(dz(7 * 640), 7, 640), [7], 128)[0];
+  const want = [].concat(...Array.from({ length: 7 }, (_, t) => Array(10).fill(t)));
+  check("tdtDecode known answer (10 symbols per frame)", dres.ids.every((v) => v === 5) && dres.idFrames.join() === want.join() ? 0 : 1, 0);
+  ctx._destroyTdtDecoder(tdt);
   ctx.destroy();
   process.exit(failed ? 1 : 0);
 })().catch((e) => {
