@@ -13,15 +13,18 @@
 // frames equal the reference's.
 //
 // The windows advance in lock-step, one decoding step per kernel sequence:
-//   tdt_joint_kernel    logit m per thread, a group of 4 windows' accumulators
-//                       in registers (the joint matrix is read once per step
-//                       per window group); per-block argmax per window
+//   tdt_rowsum_kernel<0>  joint logits: a 32-column slab of the joint matrix
+//                       streamed through LDS once per step for up to 16 live
+//                       windows; per-slab argmax per window
 //   tdt_update_kernel   per window: final argmax, token record, TDT advance,
-//                       emit flag; H, C <- candidate state when a token was emitted
-//   tdt_z_kernel        LSTM gate pre-activations: thread = (gate row, one of
-//                       the dot's four lane sums), a group of windows per block
-//   tdt_gates_kernel    LSTM cell -> candidate state
-//   tdt_proj_kernel     pred projection (emitting windows) and the next joint
+//                       emit flag; the candidate state becomes the committed one
+//                       when a token was emitted
+//   tdt_z_kernel        LSTM gate partial dot products: thread = gate row, block
+//                       = (matrix, one of the dot's four lane sums, a group of
+//                       emitting windows)
+//   tdt_gates_kernel    lane sums -> gate pre-activations -> LSTM cell ->
+//                       candidate state
+//   tdt_rowsum_kernel<1>  pred projection (emitting windows) and the next joint
 //                       input relu(frame + pred) (every active window)
 // The reference's GPU decoder (src/engines/asr-parakeet/gpu-decoder.js) runs one
 // workgroup per window that streams the whole joint matrix per step; batching
@@ -36,9 +39,9 @@
 namespace fa {
 
 constexpr int TH = 640, TV = 8193, TL = 8198, TBLANK = 8192, TMAXSYM = 10;
-constexpr int TG = 4;                      // windows per block (grid.y = window groups)
-constexpr int TJB = 64;                    // joint logits per block
-constexpr int TNB = (TL + TJB - 1) / TJB;  // joint blocks (129)
+constexpr int TJB = 32;                    // joint / projection columns per block
+constexpr int TNB = (TL + TJB - 1) / TJB;  // joint column slabs (257)
+constexpr int TLP = TNB * TJB;             // padded row stride of the joint matrix on the device
 
 struct TdtWin {
   int t, T, emitted, n_out, emit, off, last;
@@ -49,7 +52,7 @@ struct TdtState {
   TdtWin *win;
   float *h, *c;            // [n][slot 2][layer 2][TH]: committed (cur) and candidate states
   float *pp, *j;           // [n][TH]
-  float *z;                // [n][4 TH]
+  float *z;                // [n][matrix 2][lane 4][4 TH] partial dot products
   float *pv;               // [n][TNB] token partial maxima
   int *pi;                 // [n][TNB]
   float *dv;               // [n]
@@ -109,59 +112,236 @@ __device__ void block_argmax(float v, int i, float *rv, int *ri, float &ov, int 
   __syncthreads();
 }
 
-// Block = 64 logits, one per thread; every thread keeps the accumulators of
-// a group of windows and sums over hidden units n in order (the reference's
-// axpy order), the weight column loads issued ahead of the adds.  The joint
-// inputs are wave-uniform (scalar loads).  The reference skips n with
-// j[n] == 0; with finite weights adding 0·w changes no value (at most the sign
-// of an exact zero, which compares equal), so the sum here does not branch.
-__global__ __launch_bounds__(64) void tdt_joint_kernel(const float *__restrict__ out_w, const float *__restrict__ out_b,
-                                                       const float *__restrict__ jin, TdtState st, int n) {
-  __shared__ float rv[64];
-  __shared__ int ri[64];
-  const int tid = threadIdx.x, m = blockIdx.x * TJB + tid;
-  const bool valid = m < TL;
-  const int w0 = blockIdx.y * TG;
-  bool act[TG];
-  bool any = false;
+// Window groups.  A 64-thread block (lane = window, n <= 64) finds the
+// windows of its group among those selected by `pred` (ranks first ..
+// first + G - 1 in window order) and returns how many there are; grid rows
+// past the last group exit at once.  Grouping the selected windows (rather
+// than fixed runs of windows) keeps the number of blocks, and the number of
+// times a weight matrix is read, to what the live windows need.
+__device__ __forceinline__ int tdt_group(bool pred, int first, int G, int *lst) {
+  const unsigned long long m = __ballot(pred);
+  const int lane = threadIdx.x;
+  const int rank = __popcll(m & ((1ull << lane) - 1ull));
+  if (pred && rank >= first && rank < first + G) lst[rank - first] = lane;
+  __syncthreads();
+  const int cnt = __popcll(m) - first;
+  return cnt < 0 ? 0 : (cnt > G ? G : cnt);
+}
+
+// acc[g] = (...((acc[g] + w(0) x(g, 0)) + w(1) x(g, 1)) ... + w(N-1) x(g, N-1)):
+// the in-order sums of the reference, one chain per (thread, g).  Two named
+// register buffers of B loads alternate inside a loop step of 2B, so the
+// loads of one buffer are in flight while the other is summed; the prefetch
+// is unconditional (clamped to the last row) so that no buffer is copied
+// between iterations (a copy would wait for every load in flight).
+template <int N, int B, int G, typename LW, typename XV>
+__device__ __forceinline__ void chain_dot(float (&acc)[G], LW lw, XV xv) {
+  static_assert(N % (2 * B) == 0, "chain length must be a whole number of buffer pairs");
+  float wa[B], wb[B];
 #pragma unroll
-  for (int g = 0; g < TG; g++) {
-    act[g] = w0 + g < n && st.win[w0 + g].t < st.win[w0 + g].T;
-    any |= act[g];
+  for (int u = 0; u < B; u++) wa[u] = lw(u);
+#pragma unroll 1
+  for (int i0 = 0; i0 < N; i0 += 2 * B) {
+#pragma unroll
+    for (int u = 0; u < B; u++) wb[u] = lw(i0 + B + u);
+#pragma unroll
+    for (int u = 0; u < B; u++)
+#pragma unroll
+      for (int g = 0; g < G; g++) acc[g] = acc[g] + wa[u] * xv(g, i0 + u);
+    const int nx = i0 + 2 * B < N ? i0 + 2 * B : N - B;  // last step: a harmless reload
+#pragma unroll
+    for (int u = 0; u < B; u++) wa[u] = lw(nx + u);
+#pragma unroll
+    for (int u = 0; u < B; u++)
+#pragma unroll
+      for (int g = 0; g < G; g++) acc[g] = acc[g] + wb[u] * xv(g, i0 + B + u);
   }
-  if (!any) return;  // uniform: every thread reads the same flags
-  const float *jw[TG];
-#pragma unroll
-  for (int g = 0; g < TG; g++) jw[g] = jin + (size_t)(act[g] ? w0 + g : w0) * TH;  // inactive: any valid row, never used
-  float acc[TG];
-  const float b = valid ? out_b[m] : 0.f;
-#pragma unroll
-  for (int g = 0; g < TG; g++) acc[g] = b;
-  const float *col = out_w + (valid ? m : 0);
-  for (int k0 = 0; k0 < TH; k0 += 32) {
-    float wv[32];
-#pragma unroll
-    for (int u = 0; u < 32; u++) wv[u] = col[(size_t)(k0 + u) * TL];
-#pragma unroll
-    for (int u = 0; u < 32; u++)
-#pragma unroll
-      for (int g = 0; g < TG; g++) acc[g] = acc[g] + jw[g][k0 + u] * wv[u];
-  }
-  for (int g = 0; g < TG; g++) {
-    const int w = w0 + g;
-    if (!act[g]) continue;  // uniform
-    float bv;
-    int bi;
-    block_argmax((valid && m < TV) ? acc[g] : -INFINITY, (valid && m < TV) ? m : 0x7fffffff, rv, ri, bv, bi);
-    if (tid == 0) {
-      st.pv[w * TNB + blockIdx.x] = bv;
-      st.pi[w * TNB + blockIdx.x] = bi;
+}
+
+// Weight loads through a buffer resource: the row offset of a strided column
+// walk is a scalar operand, the lane's column a 32-bit vector offset.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tdt_rsrc(const float *p, size_t n) {
+  return __builtin_amdgcn_make_buffer_rsrc((void *)p, 0, (int)(n * 4), 0x00020000);
+}
+__device__ __forceinline__ float tdt_ld(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+
+
+// ── joint logits and pred projection: in-order sums over 640 hidden units ──
+// out[w][m] = init[m] + Σ_k x[w][k] W[k][m], k ascending (the reference's
+// axpy order), for a column slab of TJB = 32 columns and up to 16 windows per
+// block.  The slab's rows are streamed global->LDS by global_load_lds_dwordx4
+// in chunks of 64 rows, RS_S chunks in flight (no VGPR staging, so the copy
+// depth does not depend on register budget: each wave walking 640 dependent
+// rows on its own is latency-bound); the windows' x vectors are staged in LDS
+// once and read as broadcasts.  Lane = (column c, half h); window slot
+// s = wave + 4 h + 8 q (q < 2) so few windows still spread over all waves.
+// W rows must be 16-byte aligned and the slab must lie inside every row.
+// The reference skips k with x[k] == 0; with finite weights adding 0·w changes
+// no value (at most the sign of an exact zero, which compares equal), so the
+// sum does not branch.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void tdt_dma16(const void *g, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_addr) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+template <int N>
+__device__ __forceinline__ void tdt_wait_vmcnt() {  // gfx9 s_waitcnt: vmcnt [3:0]+[15:14], expcnt 7, lgkmcnt 15 = no wait
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+constexpr int RS_KC = 64, RS_S = 4, RS_SLOTS = 16, RS_WPL = 2;  // rows per chunk, chunks in flight, windows per block / per lane
+
+// EPI 0: joint (selected = windows with frames left; per-slab token maximum,
+// and the duration maximum in the last slab).  EPI 1: pred projection
+// (selected = windows that emitted; pp and the next joint input j =
+// relu(frame[t] + pp)); the last grid row instead refreshes j of the active
+// windows that did not emit.
+template <int EPI>
+__global__ __launch_bounds__(256) void tdt_rowsum_kernel(const float *__restrict__ W, int ldw, int ncols, const float *__restrict__ bias,
+                                                         const float *__restrict__ xsrc, const float *__restrict__ frames, TdtState st, int n) {
+  __shared__ __attribute__((aligned(1024))) float ws[RS_S][RS_KC][TJB];
+  __shared__ __attribute__((aligned(16))) float xs[RS_SLOTS][TH];
+  __shared__ int lst[RS_SLOTS], lcnt;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, h = lane >> 5, slab = blockIdx.x, col = slab * TJB + c;
+  if (EPI == 1 && (int)blockIdx.y == (int)gridDim.y - 1) {
+    for (int w = tid >> 5; w < n; w += 8) {
+      const TdtWin s = st.win[w];
+      if (!s.emit && s.t < s.T) {
+        const float v = frames[(size_t)(s.off + s.t) * TH + col] + st.pp[(size_t)w * TH + col];
+        st.j[(size_t)w * TH + col] = v > 0.0f ? v : 0.0f;
+      }
     }
-    if (blockIdx.x == TNB - 1) {
-      block_argmax((valid && m >= TV) ? acc[g] : -INFINITY, (valid && m >= TV) ? m - TV : 0x7fffffff, rv, ri, bv, bi);
-      if (tid == 0) {
-        st.dv[w] = bv;
-        st.di[w] = bi;
+    return;
+  }
+  if (wave == 0) {
+    const bool sel = lane < n && (EPI == 0 ? st.win[lane].t < st.win[lane].T : st.win[lane].emit != 0);
+    const unsigned long long m = __ballot(sel);
+    const int first = blockIdx.y * RS_SLOTS, rank = __popcll(m & ((1ull << lane) - 1ull));
+    if (sel && rank >= first && rank < first + RS_SLOTS) lst[rank - first] = lane;
+    if (lane == 0) lcnt = min(max(__popcll(m) - first, 0), RS_SLOTS);
+  }
+  __syncthreads();
+  const int cnt = lcnt;
+  if (cnt == 0) return;  // uniform
+  const uint32_t sb = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)&ws[0][0][0]);
+  const float *wsrc = W + (size_t)(lane >> 3) * ldw + slab * TJB + (lane & 7) * 4;
+  auto issue = [&](int ch) {  // 64 rows x 128 B = 8 copies of 1 KB, two per wave
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int ins = wave * 2 + i;
+      tdt_dma16(wsrc + (size_t)(ch * RS_KC + ins * 8) * ldw, sb + (ch % RS_S) * (RS_KC * TJB * 4) + ins * 1024);
+    }
+  };
+  constexpr int NCH = TH / RS_KC;
+#pragma unroll
+  for (int ch = 0; ch < RS_S - 1; ch++) issue(ch);
+  // x vectors of the block's windows
+  for (int e = tid; e < cnt * TH; e += 256) {
+    const int sl = e / TH, k = e - sl * TH, w = lst[sl];
+    const float *src = EPI == 0 ? xsrc + (size_t)w * TH : xsrc + (((size_t)w * 2 + (st.win[w].cur ^ 1)) * 2 + 1) * TH;
+    xs[sl][k] = src[k];
+  }
+  int slot[RS_WPL];
+  bool act[RS_WPL];
+#pragma unroll
+  for (int q = 0; q < RS_WPL; q++) {
+    const int sl = wave + 4 * h + 8 * q;
+    act[q] = sl < cnt;
+    slot[q] = act[q] ? sl : 0;
+  }
+  const bool work = wave < cnt;  // the wave's smallest slot
+  const bool valid = col < ncols;
+  const float b0 = valid ? bias[col] : 0.f;
+  float acc[RS_WPL];
+#pragma unroll
+  for (int q = 0; q < RS_WPL; q++) acc[q] = b0;
+  for (int ch = 0; ch < NCH; ch++) {
+    const int newer = min(RS_S - 2, NCH - 1 - ch);  // copies issued after chunk ch, per wave: 2 each
+    if (newer >= 2) tdt_wait_vmcnt<4>();
+    else if (newer == 1) tdt_wait_vmcnt<2>();
+    else tdt_wait_vmcnt<0>();
+    __syncthreads();  // chunk ch visible to every wave; the stage of chunk ch - 1 is free
+    if (ch + RS_S - 1 < NCH) issue(ch + RS_S - 1);
+    if (work) {
+      // 16-row groups in two register sets: the LDS reads of group g + 1 are
+      // issued before group g is summed (reads issued next to their use would
+      // expose the LDS latency at every row)
+      const float *wr = &ws[ch % RS_S][0][c];
+      const int k0 = ch * RS_KC;
+      float wA[16], wB[16];
+      float4 xA[RS_WPL][4], xB[RS_WPL][4];
+      auto ld = [&](int kk, float(&wv)[16], float4(&xv)[RS_WPL][4]) {
+#pragma unroll
+        for (int u = 0; u < 16; u++) wv[u] = wr[(kk + u) * TJB];
+#pragma unroll
+        for (int q = 0; q < RS_WPL; q++)
+#pragma unroll
+          for (int v = 0; v < 4; v++) xv[q][v] = *reinterpret_cast<const float4 *>(&xs[slot[q]][k0 + kk + 4 * v]);
+      };
+      auto sum = [&](const float(&wv)[16], const float4(&xv)[RS_WPL][4]) {
+#pragma unroll
+        for (int u = 0; u < 16; u++)
+#pragma unroll
+          for (int q = 0; q < RS_WPL; q++) acc[q] = acc[q] + xv[q][u >> 2][u & 3] * wv[u];
+      };
+      ld(0, wA, xA);
+      ld(16, wB, xB);
+      sum(wA, xA);
+      ld(32, wA, xA);
+      sum(wB, xB);
+      ld(48, wB, xB);
+      sum(wA, xA);
+      sum(wB, xB);
+    }
+  }
+  if (!work) return;
+#pragma unroll
+  for (int q = 0; q < RS_WPL; q++) {
+    const int w = lst[slot[q]];
+    if (EPI == 0) {
+      float bv = (valid && col < TV) ? acc[q] : -INFINITY;
+      int bi = (valid && col < TV) ? col : 0x7fffffff;
+#pragma unroll
+      for (int sh = 16; sh > 0; sh >>= 1) {  // within the 32-lane half
+        const float ov = __shfl_xor(bv, sh);
+        const int oi = __shfl_xor(bi, sh);
+        if (better(ov, oi, bv, bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      if (act[q] && c == 0) {
+        st.pv[w * TNB + slab] = bv;
+        st.pi[w * TNB + slab] = bi;
+      }
+      if (slab == TNB - 1) {
+        float dv = (valid && col >= TV) ? acc[q] : -INFINITY;
+        int di = (valid && col >= TV) ? col - TV : 0x7fffffff;
+#pragma unroll
+        for (int sh = 16; sh > 0; sh >>= 1) {
+          const float ov = __shfl_xor(dv, sh);
+          const int oi = __shfl_xor(di, sh);
+          if (better(ov, oi, dv, di)) {
+            dv = ov;
+            di = oi;
+          }
+        }
+        if (act[q] && c == 0) {
+          st.dv[w] = dv;
+          st.di[w] = di;
+        }
+      }
+    } else if (act[q]) {
+      st.pp[(size_t)w * TH + col] = acc[q];
+      const TdtWin s = st.win[w];
+      if (s.t < s.T) {
+        const float v = frames[(size_t)(s.off + s.t) * TH + col] + acc[q];
+        st.j[(size_t)w * TH + col] = v > 0.0f ? v : 0.0f;
       }
     }
   }
@@ -219,113 +399,60 @@ __global__ __launch_bounds__(64) void tdt_update_kernel(TdtState st, int cap) {
   }
 }
 
-// Gate pre-activations of one LSTM layer for the windows that emitted:
+// Gate pre-activations of one LSTM layer for the windows that emitted,
 // z[r] = ((b[r] + b[4H + r]) + W[r]·x) + R[r]·h.  The reference's dot keeps
-// four lane sums (k = l mod 4, k ascending) added as ((s0 + s1) + s2) + s3, so
-// each lane sum is one thread here: thread = (gate row r, lane l), 64 rows x
-// 4 lanes per block, a group of windows per block (x and h staged in LDS); W
-// and R are stored k-major (WT[k][r]) so the loads of a k are contiguous
-// across rows.  Layer 0 reads x = embed[last token], layer 1 x = the layer-0
+// four lane sums (k = l mod 4, k ascending) added as ((s0 + s1) + s2) + s3;
+// each lane sum of each matrix is one chain here: block = 64 gate rows (one
+// per thread) x one (matrix, lane l) x a group of ZG emitting windows, so a
+// wave's weight loads (W and R stored k-major, WT[k][r]) are one contiguous
+// row segment and its x / h operands are LDS broadcasts.  The partial sums
+// go to zp[w][matrix][l][4H]; the cell kernel adds them in the reference's
+// order.  Layer 0 reads x = embed[last token], layer 1 x = the layer-0
 // candidate hidden state.
-__global__ __launch_bounds__(256) void tdt_z_kernel(const float *__restrict__ WT, const float *__restrict__ RT, const float *__restrict__ B,
-                                                    const float *__restrict__ embed, int layer, TdtState st, int n) {
-  __shared__ float xs[TG][TH], hsm[TG][TH];
-  __shared__ float part[2][TG][64][4];
-  const int l = threadIdx.x & 3, rl = threadIdx.x >> 2, r = blockIdx.x * 64 + rl;  // 40 blocks
-  const int w0 = blockIdx.y * TG;
-  bool any = false;
-  for (int g = 0; g < TG && w0 + g < n; g++) any |= st.win[w0 + g].emit != 0;
-  if (!any) return;
-  for (int e = threadIdx.x; e < TG * TH; e += 256) {
-    const int g = e / TH, k = e % TH, w = w0 + g;
-    float xv = 0.f, hv = 0.f;
-    if (w < n && st.win[w].emit) {
-      const int cur = st.win[w].cur;
-      xv = layer == 0 ? embed[(size_t)st.win[w].last * TH + k] : st.h[(((size_t)w * 2 + (cur ^ 1)) * 2 + 0) * TH + k];
-      hv = st.h[(((size_t)w * 2 + cur) * 2 + layer) * TH + k];
-    }
-    xs[g][k] = xv;
-    hsm[g][k] = hv;
+template <int ZG>
+__global__ __launch_bounds__(64) void tdt_z_kernel(const float *__restrict__ WT, const float *__restrict__ RT, const float *__restrict__ embed,
+                                                   int layer, TdtState st, int n) {
+  __shared__ int lst[ZG];
+  __shared__ float xs[ZG][TH / 4];
+  const int tid = threadIdx.x, l = blockIdx.x & 3, mat = (blockIdx.x >> 2) & 1, r = (blockIdx.x >> 3) * 64 + tid;
+  const bool em = tid < n && st.win[tid].emit != 0;
+  const int cnt = tdt_group(em, blockIdx.y * ZG, ZG, lst);
+  if (cnt == 0) return;
+  for (int e = tid; e < ZG * (TH / 4); e += 64) {
+    const int g = e / (TH / 4), i = e % (TH / 4), w = lst[g < cnt ? g : 0];
+    const TdtWin s = st.win[w];
+    const float *src = mat == 1 ? st.h + (((size_t)w * 2 + s.cur) * 2 + layer) * TH
+                                : (layer == 0 ? embed + (size_t)s.last * TH : st.h + (((size_t)w * 2 + (s.cur ^ 1)) * 2 + 0) * TH);
+    xs[g][i] = src[4 * i + l];
   }
   __syncthreads();
-  float aw[TG], ar[TG];
+  const __amdgpu_buffer_rsrc_t rm = tdt_rsrc(mat == 0 ? WT : RT, (size_t)4 * TH * TH);
+  const int voff = (l * 4 * TH + r) * 4;  // row k = 4 i + l
+  float acc[ZG];
 #pragma unroll
-  for (int g = 0; g < TG; g++) aw[g] = ar[g] = 0.f;
-  for (int i0 = 0; i0 < TH / 4; i0 += 32) {
-    float wv[32], rv[32];
+  for (int g = 0; g < ZG; g++) acc[g] = 0.f;
+  chain_dot<TH / 4, 40, ZG>(acc, [&](int i) { return tdt_ld(rm, voff, i * 16 * TH * 4); }, [&](int g, int i) { return xs[g][i]; });
 #pragma unroll
-    for (int u = 0; u < 32; u++) {
-      const int k = 4 * (i0 + u) + l;
-      wv[u] = WT[(size_t)k * 4 * TH + r];
-      rv[u] = RT[(size_t)k * 4 * TH + r];
-    }
-#pragma unroll
-    for (int u = 0; u < 32; u++) {
-      const int k = 4 * (i0 + u) + l;
-#pragma unroll
-      for (int g = 0; g < TG; g++) {
-        aw[g] = aw[g] + wv[u] * xs[g][k];
-        ar[g] = ar[g] + rv[u] * hsm[g][k];
-      }
-    }
-  }
-#pragma unroll
-  for (int g = 0; g < TG; g++) {
-    part[0][g][rl][l] = aw[g];
-    part[1][g][rl][l] = ar[g];
-  }
-  __syncthreads();
-  if (l == 0) {
-    const float b = B[r] + B[4 * TH + r];
-    for (int g = 0; g < TG; g++) {
-      const int w = w0 + g;
-      if (w < n && st.win[w].emit) {
-        const float *pw = part[0][g][rl], *pr = part[1][g][rl];
-        const float dw = pw[0] + pw[1] + pw[2] + pw[3];
-        const float dr = pr[0] + pr[1] + pr[2] + pr[3];
-        st.z[(size_t)w * 4 * TH + r] = b + dw + dr;
-      }
-    }
-  }
+  for (int g = 0; g < ZG; g++)
+    if (g < cnt) st.z[(((size_t)lst[g] * 2 + mat) * 4 + l) * 4 * TH + r] = acc[g];
 }
 
 // LSTM cell of one layer: thread = (hidden unit, window).
-__global__ __launch_bounds__(256) void tdt_gates_kernel(int layer, TdtState st) {
+__global__ __launch_bounds__(256) void tdt_gates_kernel(const float *__restrict__ B, int layer, TdtState st) {
   const int w = blockIdx.y, g = blockIdx.x * 256 + threadIdx.x;
   if (g >= TH || !st.win[w].emit) return;
-  const float *z = st.z + (size_t)w * 4 * TH;
-  const float zi = z[g], zo = z[TH + g], zf = z[2 * TH + g], zc = z[3 * TH + g];
+  const float *zp = st.z + (size_t)w * 8 * 4 * TH;
+  auto zrow = [&](int r) {
+    const float dw = ((zp[r] + zp[4 * TH + r]) + zp[8 * TH + r]) + zp[12 * TH + r];
+    const float dr = ((zp[16 * TH + r] + zp[20 * TH + r]) + zp[24 * TH + r]) + zp[28 * TH + r];
+    return ((B[r] + B[4 * TH + r]) + dw) + dr;
+  };
+  const float zi = zrow(g), zo = zrow(TH + g), zf = zrow(2 * TH + g), zc = zrow(3 * TH + g);
   const int cur = st.win[w].cur;
   const size_t o = (((size_t)w * 2 + cur) * 2 + layer) * TH + g, on = (((size_t)w * 2 + (cur ^ 1)) * 2 + layer) * TH + g;
   const float cc = tdt_sigmoid(zf) * st.c[o] + tdt_sigmoid(zi) * tdt_tanhf(zc);
   st.c[on] = cc;
   st.h[on] = tdt_sigmoid(zo) * tdt_tanhf(cc);
-}
-
-// Pred projection of one window if it emitted (pp[n] = b[n] + Σ_k dec[k] w[k][n],
-// k in order; dec arrives as scalar loads), then its next joint input
-// j = relu(frame[t] + pp) if it is still active.  Block = 64 output units x one
-// window (10 x n blocks); weight loads issued ahead of the adds.
-__global__ __launch_bounds__(64) void tdt_proj_kernel(const float *__restrict__ pw, const float *__restrict__ pb, const float *__restrict__ frames,
-                                                      const float *__restrict__ hs, TdtState st) {
-  const int u = blockIdx.x * 64 + threadIdx.x, w = blockIdx.y;
-  const TdtWin s = st.win[w];
-  if (__builtin_amdgcn_readfirstlane(s.emit)) {  // uniform
-    const float *dec = hs + (((size_t)w * 2 + (__builtin_amdgcn_readfirstlane(s.cur) ^ 1)) * 2 + 1) * TH;
-    float acc = pb[u];
-    for (int k0 = 0; k0 < TH; k0 += 64) {
-      float wv[64];
-#pragma unroll
-      for (int q = 0; q < 64; q++) wv[q] = pw[(size_t)(k0 + q) * TH + u];
-#pragma unroll
-      for (int q = 0; q < 64; q++) acc = acc + dec[k0 + q] * wv[q];
-    }
-    st.pp[(size_t)w * TH + u] = acc;
-  }
-  if (s.t < s.T) {
-    const float v = frames[(size_t)(s.off + s.t) * TH + u] + st.pp[(size_t)w * TH + u];
-    st.j[(size_t)w * TH + u] = v > 0.0f ? v : 0.0f;
-  }
 }
 
 }  // namespace fa
@@ -350,8 +477,13 @@ int fa_tdt_load(fa_ctx *ctx, const float *const *w, fa_tdt **out) {
   fa_tdt *d = new fa_tdt();
   d->ctx = ctx;
   float **dst[11] = {&d->embed, &d->lw[0], &d->lr[0], &d->lb[0], &d->lw[1], &d->lr[1], &d->lb[1], &d->pred_w, &d->pred_b, &d->out_w, &d->out_b};
+  // device sizes: the joint matrix rows are padded to TLP columns (zeros), so
+  // every row is 16-byte aligned and every 32-column slab lies inside it
+  size_t dsz[11];
+  for (int i = 0; i < 11; i++) dsz[i] = sizes[i];
+  dsz[9] = (size_t)TH * TLP;
   for (int i = 0; i < 11; i++) {
-    float *p = (float *)dev_alloc(ctx, sizes[i] * 4);
+    float *p = (float *)dev_alloc(ctx, dsz[i] * 4);
     if (!p) {
       fa_tdt_destroy(d);
       return FA_E_OOM;
@@ -365,7 +497,12 @@ int fa_tdt_load(fa_ctx *ctx, const float *const *w, fa_tdt **out) {
         for (int k = 0; k < TH; k++) tr[(size_t)k * 4 * TH + r] = src[(size_t)r * TH + k];
       src = tr.data();
     }
-    if (hipMemcpy(p, src, sizes[i] * 4, hipMemcpyHostToDevice) != hipSuccess) {
+    if (i == 9) {  // joint [H][TL] -> [H][TLP]
+      tr.assign(dsz[i], 0.f);
+      for (int k = 0; k < TH; k++) memcpy(&tr[(size_t)k * TLP], src + (size_t)k * TL, TL * 4);
+      src = tr.data();
+    }
+    if (hipMemcpy(p, src, dsz[i] * 4, hipMemcpyHostToDevice) != hipSuccess) {
       fa_tdt_destroy(d);
       return set_err(ctx, FA_E_DEVICE, "tdtLoad: upload of weight %d failed", i);
     }
@@ -409,7 +546,7 @@ int fa_tdt_decode(fa_tdt *d, fa_tensor frames, const int32_t *lens, int n, int c
     o += (bytes + 255) & ~(size_t)255;
     return at;
   };
-  const size_t o_win = take(sizeof(TdtWin) * n), o_h = take(4ul * n * 4 * TH), o_c = take(4ul * n * 4 * TH), o_pp = take(4ul * n * TH), o_j = take(4ul * n * TH), o_z = take(4ul * n * 4 * TH),
+  const size_t o_win = take(sizeof(TdtWin) * n), o_h = take(4ul * n * 4 * TH), o_c = take(4ul * n * 4 * TH), o_pp = take(4ul * n * TH), o_j = take(4ul * n * TH), o_z = take(4ul * n * 8 * 4 * TH),
                o_pv = take(4ul * n * TNB), o_pi = take(4ul * n * TNB), o_dv = take(4ul * n), o_di = take(4ul * n), o_ids = take(4ul * n * cap),
                o_frs = take(4ul * n * cap), o_act = take(4ul * n);
   if (d->state_bytes < o) {
@@ -439,21 +576,22 @@ int fa_tdt_decode(fa_tdt *d, fa_tensor frames, const int32_t *lens, int n, int c
   st.alive = (int *)(base + o_act);
   rf = get(ctx, frames);
   const float *fr = (const float *)rf->ptr;
-  const int ng = (n + TG - 1) / TG;  // window groups
+  constexpr int zg = 2;  // emitting windows per LSTM block (measured: 2 < 4 < 8)
   FA_HIP(ctx, hipMemsetAsync(base + o_h, 0, o_pp - o_h, ctx->stream));  // both state slots = 0
   FA_HIP(ctx, hipMemcpyAsync(st.win, win.data(), sizeof(TdtWin) * n, hipMemcpyHostToDevice, ctx->stream));
   auto predict = [&]() -> int {  // candidate state + pred projection for windows with emit set
     for (int layer = 0; layer < 2; layer++) {
       {
         ProfScope ps(ctx, "tdt_lstm_z");
-        FA_LAUNCH(ps, tdt_z_kernel, dim3(4 * TH / 64, ng), dim3(256), 0, ctx->stream, d->lw[layer], d->lr[layer], d->lb[layer], d->embed, layer,
+        FA_LAUNCH(ps, tdt_z_kernel<zg>, dim3(4 * TH / 64 * 8, cdiv(n, zg)), dim3(64), 0, ctx->stream, d->lw[layer], d->lr[layer], d->embed, layer,
                   st, n);
       }
       ProfScope ps(ctx, "tdt_lstm_cell");
-      FA_LAUNCH(ps, tdt_gates_kernel, dim3(cdiv(TH, 256), n), dim3(256), 0, ctx->stream, layer, st);
+      FA_LAUNCH(ps, tdt_gates_kernel, dim3(cdiv(TH, 256), n), dim3(256), 0, ctx->stream, d->lb[layer], layer, st);
     }
     ProfScope ps(ctx, "tdt_proj");
-    FA_LAUNCH(ps, tdt_proj_kernel, dim3(TH / 64, n), dim3(64), 0, ctx->stream, d->pred_w, d->pred_b, fr, (const float *)st.h, st);
+    FA_LAUNCH(ps, tdt_rowsum_kernel<1>, dim3(TH / TJB, cdiv(n, RS_SLOTS) + 1), dim3(256), 0, ctx->stream, d->pred_w, TH, TH, d->pred_b,
+              (const float *)st.h, fr, st, n);
     return check_launch(ctx, "tdt_predict");
   };
   FA_TRY(predict());  // predict(BLANK) from the zero state, then j for t = 0
@@ -467,7 +605,8 @@ int fa_tdt_decode(fa_tdt *d, fa_tensor frames, const int32_t *lens, int n, int c
     for (int k = 0; k < kChunk; k++) {
       {
         ProfScope ps(ctx, "tdt_joint");
-        FA_LAUNCH(ps, tdt_joint_kernel, dim3(TNB, ng), dim3(64), 0, ctx->stream, d->out_w, d->out_b, (const float *)st.j, st, n);
+        FA_LAUNCH(ps, tdt_rowsum_kernel<0>, dim3(TNB, cdiv(n, RS_SLOTS)), dim3(256), 0, ctx->stream, d->out_w, TLP, TL, d->out_b,
+                  (const float *)st.j, fr, st, n);
       }
       {
         ProfScope ps(ctx, "tdt_update");
