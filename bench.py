@@ -206,6 +206,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="encoder", choices=["encoder", "layer", "ragged", "quant", "quant4", "gemv", "copy", "mel", "decode"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--windows", type=int, default=16, help="decode workload: windows per decode call (1..64)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); multi-GPU runs are not part of it", file=sys.stderr)
@@ -345,7 +346,7 @@ def bench_decode(args, fa, ctx):
     value = audio-s (16 x 15 s) / wall-s of the whole decode call (steps in
     lock-step on the GPU, results copied to the host)."""
     dec_w = fa.synth.make_decoder_weights(1)
-    n_win, T = 16, 188
+    n_win, T = args.windows, 188
     frames_h = np.concatenate([fa.synth.make_projected_frames(T, seed=100 + i) for i in range(n_win)])
     frames = ctx.upload(frames_h, frames_h.shape[0], 640)
     dec = fa.TdtDecoder(ctx, dec_w)
@@ -375,7 +376,7 @@ def bench_decode(args, fa, ctx):
     line = {"metric": "greedy TDT decode audio-s/wall-s at 1 GPU", "value": round(audio_s / wall, 1), "unit": "audio-s/wall-s", "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 3), "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic projected frames ~N(0,1), synthetic decoder weights (seed 1)",
-            "config": {"workload": "configs[2] encoder output: 16 windows x 188 frames, greedy TDT (durations 0..4, <= 10 symbols/frame)",
+            "config": {"workload": f"configs[2] encoder output: {n_win} windows x 188 frames, greedy TDT (durations 0..4, <= 10 symbols/frame)",
                        "windows": n_win, "frames": n_win * T, "tokens": tokens, "decode_steps": j["launches"]},
             "roofline": {"bound": "hbm", "achieved": round(jbytes / max(j["avg_us"], 1e-9) * 1e-3, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(jbytes / max(j["avg_us"], 1e-9) * 1e-3 / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "tdt_joint",

@@ -58,7 +58,7 @@ struct TdtState {
   float *dv;               // [n]
   int *di;                 // [n]
   int *ids, *frs;          // [n][cap]
-  int *alive;              // [n] window still has frames
+  int *alive;              // [n] window still has frames (-1: no finite joint maximum)
 };
 
 __device__ __forceinline__ float tdt_floorf(float x) {
@@ -359,7 +359,7 @@ __global__ __launch_bounds__(64) void tdt_update_kernel(TdtState st, int cap) {
   if (s.t >= s.T) {  // uniform
     if (tid == 0) {
       st.win[w].emit = 0;
-      st.alive[w] = 0;
+      if (st.alive[w] > 0) st.alive[w] = 0;  // a -1 flag stays
     }
     return;
   }
@@ -376,6 +376,14 @@ __global__ __launch_bounds__(64) void tdt_update_kernel(TdtState st, int cap) {
   if (tid == 0) {
     const int step = st.di[w];
     s.emit = 0;
+    if (tok < 0 || tok >= TV || step < 0 || step >= TL - TV) {
+      // no finite maximum (non-finite logits): end the window and flag it, so
+      // a bad value can never become an embedding row index
+      s.t = s.T;
+      st.win[w] = s;
+      st.alive[w] = -1;
+      return;
+    }
     if (tok != TBLANK) {
       if (s.n_out < cap) {
         st.ids[(size_t)w * cap + s.n_out] = tok;
@@ -578,6 +586,7 @@ int fa_tdt_decode(fa_tdt *d, fa_tensor frames, const int32_t *lens, int n, int c
   const float *fr = (const float *)rf->ptr;
   constexpr int zg = 2;  // emitting windows per LSTM block (measured: 2 < 4 < 8)
   FA_HIP(ctx, hipMemsetAsync(base + o_h, 0, o_pp - o_h, ctx->stream));  // both state slots = 0
+  FA_HIP(ctx, hipMemsetAsync(st.alive, 0, 4ul * n, ctx->stream));
   FA_HIP(ctx, hipMemcpyAsync(st.win, win.data(), sizeof(TdtWin) * n, hipMemcpyHostToDevice, ctx->stream));
   auto predict = [&]() -> int {  // candidate state + pred projection for windows with emit set
     for (int layer = 0; layer < 2; layer++) {
@@ -617,7 +626,10 @@ int fa_tdt_decode(fa_tdt *d, fa_tensor frames, const int32_t *lens, int n, int c
     FA_HIP(ctx, hipMemcpyAsync(alive.data(), st.alive, 4ul * n, hipMemcpyDeviceToHost, ctx->stream));
     FA_HIP(ctx, hipStreamSynchronize(ctx->stream));
     active = 0;
-    for (int i = 0; i < n; i++) active += alive[i];
+    for (int i = 0; i < n; i++) {
+      if (alive[i] < 0) return set_err(ctx, FA_E_DEVICE, "tdtDecode: window %d: joint logits without a finite maximum", i);
+      active += alive[i];
+    }
   }
   if (active) return set_err(ctx, FA_E_DEVICE, "tdtDecode: windows still active after %ld steps", max_steps);
   std::vector<TdtWin> fin(n);

@@ -79,3 +79,28 @@ def test_capacity_and_validation(ctx, fa, orc, dec_w, tdt):
         tdt.decodeBatch(bad, [10])
     with pytest.raises(fa.FaError):
         tdt.decodeBatch(ctx.upload(np.zeros((10, H), np.float32), 10, H), [11])
+
+
+def test_many_windows_match_oracle(ctx, fa, orc, dec_w, tdt):
+    """More windows than one block's 16 window slots (several window groups per
+    kernel, ragged lengths, empty windows): every window equals the oracle."""
+    rng = np.random.default_rng(7)
+    lens = [int(x) for x in rng.integers(1, 120, 40)]
+    lens[3] = 0
+    lens[17] = 188
+    frames = [fa.synth.make_projected_frames(T, seed=300 + i) for i, T in enumerate(lens)]
+    got = tdt.decodeBatch(frames)
+    for i, f in enumerate(frames):
+        ids, fr = orc.tdt_decode(dec_w, f) if len(f) else (np.zeros(0, np.int32), np.zeros(0, np.int32))
+        assert got[i]["ids"] == ids.tolist() and got[i]["idFrames"] == fr.tolist(), (i, lens[i])
+
+
+def test_full_batch_equals_small_batches(ctx, fa, tdt):
+    """64 windows in one call (the maximum) = the same windows 8 at a time."""
+    frames = [fa.synth.make_projected_frames(96, seed=500 + i) for i in range(64)]
+    big = tdt.decodeBatch(frames)
+    small = []
+    for b in range(0, 64, 8):
+        small += tdt.decodeBatch(frames[b:b + 8])
+    for i in range(64):
+        assert big[i]["ids"] == small[i]["ids"] and big[i]["idFrames"] == small[i]["idFrames"], i
