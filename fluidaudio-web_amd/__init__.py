@@ -15,6 +15,8 @@ from .encoder import FusedEncoder, inferConfig, loadParakeetEncoder, parakeetEnc
 from .mel import JsPreprocessor, ParakeetMel
 from .decoder import TdtDecoder
 from . import synth, windowing
+from .pipeline import createStitcher, transcribeWindowed
 
 __all__ = ["ACT", "FaError", "lib", "HipContext", "HipTensor", "PackedBytes", "createContext", "FusedEncoder", "inferConfig",
-           "loadParakeetEncoder", "parakeetEncodeBatch", "posEncoding", "tsub", "synth", "windowing", "JsPreprocessor", "ParakeetMel", "TdtDecoder"]
+           "loadParakeetEncoder", "parakeetEncodeBatch", "posEncoding", "tsub", "synth", "windowing", "JsPreprocessor", "ParakeetMel", "TdtDecoder",
+           "createStitcher", "transcribeWindowed"]

@@ -108,3 +108,23 @@ def make_decoder_weights(seed: int = 1, blank_bias: float = 4.5, hid: int = 640,
 def make_projected_frames(T: int, seed: int = 1, hid: int = 640) -> np.ndarray:
     """Encoder frames after the joint's encoder projection, [T, hid] ~ N(0, 1)."""
     return np.random.default_rng(seed).standard_normal((T, hid)).astype(np.float32)
+
+
+def make_pcm(seconds: float, seed: int = 1, sr: int = 16000) -> np.ndarray:
+    """Speech-like synthetic mono audio: a gliding harmonic tone with syllable-
+    rate amplitude modulation plus noise, f32 in [-1, 1]."""
+    rng = np.random.default_rng(seed)
+    n = int(round(seconds * sr))
+    t = np.arange(n, dtype=np.float64) / sr
+    f0 = 140 + 40 * np.sin(2 * np.pi * 0.3 * t)
+    ph = 2 * np.pi * np.cumsum(f0) / sr
+    env = 0.5 + 0.5 * np.sin(2 * np.pi * 3.7 * t) ** 2
+    x = env * (0.25 * np.sin(ph) + 0.12 * np.sin(2 * ph) + 0.06 * np.sin(3 * ph)) + 0.02 * rng.standard_normal(n)
+    return x.astype(np.float32)
+
+
+def make_joint_projection(seed: int = 1, D: int = 1024, hid: int = 640) -> tuple:
+    """The joint network's encoder projection (decoder manifest encW [D, hid],
+    encB [hid]; pipeline.js:57-61), scaled so projected frames are O(1)."""
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal((D, hid)) * (2.0 / np.sqrt(D))).astype(np.float32), (rng.standard_normal(hid) * 0.1).astype(np.float32)
