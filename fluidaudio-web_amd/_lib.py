@@ -74,6 +74,7 @@ SIGNATURES = [
     ("fa_bmm_pv", I, [P, T, T, I, I, I, C.POINTER(T)]),
     ("fa_rel_shift", I, [P, T, C.POINTER(T)]),
     ("fa_rel_shift_b", I, [P, T, I, C.POINTER(T)]),
+    ("fa_rel_shift_stream", I, [P, T, I, I, I, I, I, I, I, I, I, C.POINTER(T)]),
     ("fa_attn_fused", I, [P, T, T, T, T, T, T, I, I, I, C.POINTER(T)]),
     ("fa_ewise", I, [P, T, T, I, C.POINTER(T)]),
     ("fa_scale", I, [P, T, C.c_float, C.POINTER(T)]),

@@ -13,7 +13,7 @@ code written against GpuContext/WasmContext reads the same:
   - misuse raises FaError (the reference throws Error).
 Methods that belong to the TTS and decoder engines (lstm, snake, adain,
 convTranspose1d, im2col, conv1dGemm/conv1dFast*, gatherCols, leakyRelu,
-jbatch, argmaxRows, jointArgmax, relShiftStream) are outside this backend's
+jbatch, argmaxRows, jointArgmax) are outside this backend's
 scope and raise NotImplementedError naming the op.
 """
 from __future__ import annotations
@@ -62,7 +62,7 @@ class StagedRead:
 
 
 _UNSUPPORTED = ("lstm", "snake", "adain", "convTranspose1d", "im2col", "conv1dGemm", "conv1dFast", "conv1dFastF16", "gatherCols",
-                "leakyRelu", "jbatch", "argmaxRows", "jointArgmax", "relShiftStream")
+                "leakyRelu", "jbatch", "argmaxRows", "jointArgmax")
 
 
 def _f32(a):
@@ -309,6 +309,14 @@ class HipContext:
     def relShiftB(self, x, H):
         o = self._out()
         check(self._p, lib().fa_rel_shift_b(self._p, x.h, H, C.byref(o)))
+        return self._t(o.value)
+
+    def relShiftStream(self, x, opts=None, **kw):
+        """compute.js relShiftStream(x, {H, n, Lk, dMax, Lc, subT, C, left, right})."""
+        o_ = dict(opts or {}, **kw)
+        o = self._out()
+        check(self._p, lib().fa_rel_shift_stream(self._p, x.h, *(int(o_[k]) for k in ("H", "n", "Lk", "dMax", "Lc", "subT", "C", "left", "right")),
+                                                 C.byref(o)))
         return self._t(o.value)
 
     def attnFused(self, q, k, v, pos, pbu, pbv, H, HD, W):

@@ -235,6 +235,27 @@ __global__ void relshift_kernel(const float *x, float *y, int t, int H) {
   }
 }
 
+// Streaming rel_shift + chunked-causal mask (compute.js:689-703,
+// wasm-context.js:509-524): n new queries at absolute positions q = subT + i
+// against Lk keys at k = subT - Lc + j; x holds each query's bd term over a
+// truncated positional table whose column pi is relative distance dMax - pi.
+// y = x[row, clamp(dMax - (q - k), 0, P - 1)], or -1e4 when k lies outside
+// the query's chunk window [cs - left, cs + C - 1 + right], cs = C * (q / C).
+__global__ void relshift_stream_kernel(const float *x, float *y, long total, int n, int Lk, int P, int dMax, int Lc, int subT, int C, int left,
+                                       int right) {
+  for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += (long)gridDim.x * blockDim.x) {
+    const long r = idx / Lk;
+    const int j = (int)(idx - r * Lk), i = (int)(r % n);
+    const int q = subT + i, cs = C * (q / C), k = subT - Lc + j;
+    float v = -10000.0f;
+    if (k >= cs - left && k <= cs + C - 1 + right) {
+      const int d = min(P - 1, max(0, dMax - (q - k)));
+      v = x[r * P + d];
+    }
+    y[idx] = v;
+  }
+}
+
 // ── quantised-weight helpers ──────────────────────────────────────────────
 __global__ void repack_i8_kernel(const int8_t *src, int8_t *dst, int K, int N) {  // [K][N] -> [N][K]
   __shared__ int8_t tile[64][65];
@@ -751,6 +772,27 @@ int fa_rel_shift_b(fa_ctx *ctx, fa_tensor x, int H, fa_tensor *out) {
 }
 
 int fa_rel_shift(fa_ctx *ctx, fa_tensor x, fa_tensor *out) { return fa_rel_shift_b(ctx, x, 1, out); }
+
+int fa_rel_shift_stream(fa_ctx *ctx, fa_tensor x, int H, int n, int Lk, int dMax, int Lc, int subT, int C, int left, int right, fa_tensor *out) {
+  TensorRec *rx;
+  FA_TRY(need(ctx, x, &rx, "relShiftStream"));
+  if (rx->kind != S_F32) return set_err(ctx, FA_E_INVALID, "relShiftStream: x must be f32");
+  if (H <= 0 || n <= 0 || (long)H * n != rx->rows) return set_err(ctx, FA_E_INVALID, "relShiftStream: x has %d rows, H*n = %d*%d", rx->rows, H, n);
+  if (Lk < 0 || C <= 0 || subT < 0 || left < 0 || right < 0 || rx->cols <= 0)
+    return set_err(ctx, FA_E_INVALID, "relShiftStream: Lk %d, C %d, subT %d, left %d, right %d", Lk, C, subT, left, right);
+  fa_tensor o;
+  TensorRec *ro;
+  const long total = (long)H * n * Lk;
+  FA_TRY(new_tensor(ctx, H * n, Lk, S_F32, (size_t)total * 4, &o, &ro));
+  rx = get(ctx, x);
+  ProfScope ps(ctx, "relShiftStream");
+  if (total)
+    FA_LAUNCH(ps, relshift_stream_kernel, dim3(gs(total)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), total, n, Lk, rx->cols, dMax, Lc, subT, C,
+              left, right);
+  FA_TRY(check_launch(ctx, "relShiftStream"));
+  *out = o;
+  return FA_OK;
+}
 
 int fa_attn_fused(fa_ctx *ctx, fa_tensor q, fa_tensor k, fa_tensor v, fa_tensor pos, fa_tensor pbu, fa_tensor pbv, int H, int HD, int W, fa_tensor *out) {
   TensorRec *rq, *rk, *rv, *rp, *ru, *rw;

@@ -249,6 +249,7 @@ FN(js_bmm_qk, 8, RET_T(fa_bmm_qk(c, T(1), T(2), T(3), I(4), I(5), I(6), I(7), &_
 FN(js_bmm_pv, 6, RET_T(fa_bmm_pv(c, T(1), T(2), I(3), I(4), I(5), &_o)))
 FN(js_rel_shift, 2, RET_T(fa_rel_shift(c, T(1), &_o)))
 FN(js_rel_shift_b, 3, RET_T(fa_rel_shift_b(c, T(1), I(2), &_o)))
+FN(js_rel_shift_stream, 11, RET_T(fa_rel_shift_stream(c, T(1), I(2), I(3), I(4), I(5), I(6), I(7), I(8), I(9), I(10), &_o)))
 FN(js_attn_fused, 10, RET_T(fa_attn_fused(c, T(1), T(2), T(3), T(4), T(5), T(6), I(7), I(8), I(9), &_o)))
 FN(js_ewise, 4, RET_T(fa_ewise(c, T(1), T(2), I(3), &_o)))
 FN(js_scale, 3, RET_T(fa_scale(c, T(1), (float)f64(env, a[2]), &_o)))
@@ -474,7 +475,7 @@ static napi_value init(napi_env env, napi_value exports) {
       EXPORT("beginBatch", js_begin_batch), EXPORT("endBatch", js_end_batch), EXPORT("matmul", js_matmul), EXPORT("matmulInt8", js_matmul_int8),
       EXPORT("matmulNBits", js_matmul_nbits), EXPORT("layernorm", js_layernorm), EXPORT("softmax", js_softmax), EXPORT("conv1d", js_conv1d),
       EXPORT("conv2d", js_conv2d), EXPORT("bmmQK", js_bmm_qk), EXPORT("bmmPV", js_bmm_pv), EXPORT("relShift", js_rel_shift),
-      EXPORT("relShiftB", js_rel_shift_b), EXPORT("attnFused", js_attn_fused), EXPORT("ewise", js_ewise), EXPORT("scale", js_scale),
+      EXPORT("relShiftB", js_rel_shift_b), EXPORT("relShiftStream", js_rel_shift_stream), EXPORT("attnFused", js_attn_fused), EXPORT("ewise", js_ewise), EXPORT("scale", js_scale),
       EXPORT("silu", js_silu), EXPORT("relu", js_relu), EXPORT("glu", js_glu), EXPORT("transpose", js_transpose),
       EXPORT("sliceCols", js_slice_cols), EXPORT("setCols", js_set_cols), EXPORT("sliceRows", js_slice_rows), EXPORT("copyRows", js_copy_rows),
       EXPORT("concatRows", js_concat_rows), EXPORT("subReshape", js_sub_reshape), EXPORT("rowBiasAct", js_row_bias_act),

@@ -166,6 +166,10 @@ class HipContext {
   relShiftB(x, H) {
     return this._info(addon.relShiftB(this.ctx, x.h, H));
   }
+  /** compute.js relShiftStream(x, {H, n, Lk, dMax, Lc, subT, C, left, right}). */
+  relShiftStream(x, { H, n, Lk, dMax, Lc, subT, C, left, right }) {
+    return this._info(addon.relShiftStream(this.ctx, x.h, H, n, Lk, dMax, Lc, subT, C, left, right));
+  }
   attnFused(q, k, v, pos, pbu, pbv, H, HD, W) {
     return this._info(addon.attnFused(this.ctx, q.h, k.h, v.h, pos.h, pbu.h, pbv.h, H, HD, W));
   }

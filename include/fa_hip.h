@@ -127,6 +127,10 @@ int fa_bmm_qk(fa_ctx *ctx, fa_tensor q, fa_tensor b, fa_tensor qb, int H, int HD
 int fa_bmm_pv(fa_ctx *ctx, fa_tensor p, fa_tensor v, int H, int HD, int W, fa_tensor *out);                          /* bmmPV */
 int fa_rel_shift(fa_ctx *ctx, fa_tensor x, fa_tensor *out);                                                           /* relShift */
 int fa_rel_shift_b(fa_ctx *ctx, fa_tensor x, int H, fa_tensor *out);                                                  /* relShiftB */
+/* relShiftStream (compute.js:689-703, wasm-context.js:509-524): x [H*n, P] -> [H*n, Lk],
+ * y[h*n+i, j] = x[h*n+i, clamp(dMax - (q - k), 0, P-1)], q = subT + i, k = subT - Lc + j;
+ * -1e4 where k is outside [C*floor(q/C) - left, C*floor(q/C) + C - 1 + right]. */
+int fa_rel_shift_stream(fa_ctx *ctx, fa_tensor x, int H, int n, int Lk, int dMax, int Lc, int subT, int C, int left, int right, fa_tensor *out);
 /* attnFused (compute.d.ts:248): fused rel-pos attention over W windows of T
  * rows; q/k/v [W*T, H*HD], pos [2T-1, H*HD], pbu/pbv [1, H*HD].  Unlike the
  * reference (T <= 256, compute.js:680) any T up to 1024 is accepted. */

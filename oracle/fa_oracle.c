@@ -342,6 +342,20 @@ void or_relshift_b(const float *x, float *out, int rows, int H) {
       }
 }
 
+/* wctx:509-524 — streaming rel_shift + chunked-causal mask: x [H*n, P] -> [H*n, Lk]. */
+void or_relshift_stream(const float *x, float *out, int H, int n, int Lk, int P, int dMax, int Lc, int subT, int C, int left, int right) {
+  for (int r = 0; r < H * n; r++) {
+    const int i = r % n, q = subT + i, cs = C * (int)floor((double)q / C);
+    for (int j = 0; j < Lk; j++) {
+      const int k = subT - Lc + j;
+      int d = dMax - (q - k);
+      if (d < 0) d = 0;
+      if (d > P - 1) d = P - 1;
+      out[(size_t)r * Lk + j] = (k < cs - left || k > cs + C - 1 + right) ? -10000.0f : x[(size_t)r * P + d];
+    }
+  }
+}
+
 /* enc:163-174 — sinusoidal table over 2T-1 relative positions T-1 .. -(T-1). */
 void or_pos_encoding(int T, int D, float *pe) {
   const double lg = log(10000.0) / D;

@@ -75,6 +75,7 @@ def _declare(L):
     L.or_bmm_qk.argtypes = [f32p, I, f32p, I, vp, f32p, I, I, I, I]
     L.or_bmm_pv.argtypes = [f32p, I, f32p, I, f32p, I, I, I]
     L.or_relshift_b.argtypes = [f32p, f32p, I, I]
+    L.or_relshift_stream.argtypes = [f32p, f32p] + [I] * 10
     L.or_pos_encoding.argtypes = [I, I, f32p]
     L.or_quantize_int8_cols.argtypes = [f32p, I, I, i8p, f32p]
     L.or_dequant_int8_cols.argtypes = [i8p, f32p, I, I, f32p]
@@ -234,6 +235,14 @@ def bmm_pv(p, v, H, HD, W=1):
     Tq = p.shape[0] // (W * H)
     out = np.empty((W * Tq, H * HD), np.float32)
     lib().or_bmm_pv(p, p.shape[0], v, v.shape[0], out, H, HD, W)
+    return out
+
+
+def relshift_stream(x, H, n, Lk, dMax, Lc, subT, C, left, right):
+    """wasm-context.js:509-524: streaming rel_shift + chunked-causal mask."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty((H * n, Lk), np.float32)
+    lib().or_relshift_stream(x, out, H, n, Lk, x.shape[1], dMax, Lc, subT, C, left, right)
     return out
 
 

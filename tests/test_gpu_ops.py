@@ -163,3 +163,16 @@ def test_bmm_and_fused_attention(ctx, orc):
     fused = dl(ctx, ctx.attnFused(tq, tk, tv, tp, tu, tvb, H, HD, W))
     rel = np.linalg.norm(fused - ref) / np.linalg.norm(ref)
     assert rel < 1e-2, rel
+
+
+def test_rel_shift_stream_matches_oracle(ctx, orc):
+    """relShiftStream (the streaming encoder's chunked-causal rel_shift) vs the
+    oracle, bit for bit: negative key positions, clamped distances on both
+    sides, right context, and a streaming position mid-stream."""
+    rng = np.random.default_rng(3)
+    for H, n, Lk, P, dMax, Lc, subT, C, left, right in [(8, 4, 74, 77, 73, 70, 140, 4, 70, 0), (2, 5, 30, 9, 3, 20, 7, 3, 6, 2),
+                                                        (1, 1, 1, 1, 0, 0, 0, 1, 0, 0), (4, 16, 100, 120, 119, 84, 0, 16, 70, 3)]:
+        x = rng.standard_normal((H * n, P)).astype(np.float32)
+        opts = dict(H=H, n=n, Lk=Lk, dMax=dMax, Lc=Lc, subT=subT, C=C, left=left, right=right)
+        got = dl(ctx, ctx.relShiftStream(ctx.upload(x, H * n, P), opts))
+        assert np.array_equal(got, orc.relshift_stream(x, H, n, Lk, dMax, Lc, subT, C, left, right)), opts
