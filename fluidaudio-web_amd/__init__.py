@@ -16,7 +16,9 @@ from .mel import JsPreprocessor, ParakeetMel
 from .decoder import TdtDecoder
 from . import synth, windowing
 from .pipeline import createStitcher, transcribeWindowed
+from .streaming import createEncodeStream, disposeEncodeStream, encodeStreamFlush, encodeStreamPush
 
 __all__ = ["ACT", "FaError", "lib", "HipContext", "HipTensor", "PackedBytes", "createContext", "FusedEncoder", "inferConfig",
            "loadParakeetEncoder", "parakeetEncodeBatch", "posEncoding", "tsub", "synth", "windowing", "JsPreprocessor", "ParakeetMel", "TdtDecoder",
-           "createStitcher", "transcribeWindowed"]
+           "createStitcher", "transcribeWindowed",
+           "createEncodeStream", "encodeStreamPush", "encodeStreamFlush", "disposeEncodeStream"]

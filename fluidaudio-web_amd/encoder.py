@@ -39,11 +39,15 @@ def _f32(a):
 
 
 # ── op-by-op restatement ────────────────────────────────────────────────────
-def loadParakeetEncoder(ctx: HipContext, man: dict, weights: str = "f16", layers: int | None = None) -> dict:
+def loadParakeetEncoder(ctx: HipContext, man: dict, weights: str = "f16", layers: int | None = None, cfg: dict | None = None) -> dict:
     """Upload weights with the reference's load-time folds (raw-encoder.js:
     124-156): q·1/√HD, pos_bias·1/√HD, FF linear2·0.5; pointwise convs as
-    transposed [cin, cout] matrices.  weights: "f16" (uploadF16) or "f32"."""
-    cfg = inferConfig(man)
+    transposed [cin, cout] matrices.  weights: "f16" (uploadF16) or "f32".
+    cfg adds the streaming-model fields the manifest does not carry
+    (eou-parakeet/config.js: melBins, subPad {t, b, l, r}, convCausal,
+    attChunk, attLeft, attRight); layers with bnw / bnb get the conv-module
+    LayerNorm (raw-encoder.js:151,361-364)."""
+    cfg = dict(inferConfig(man), **(cfg or {}))
     if layers is not None:
         cfg["layers"] = layers
     INV = 1.0 / math.sqrt(cfg["HD"])
@@ -86,6 +90,7 @@ def loadParakeetEncoder(ctx: HipContext, man: dict, weights: str = "f16", layers
             "ff2w1": mat(g("ff2w1")), "ff2w2": mat(g("ff2w2"), 0.5),
             "ff2b1": vec_opt(g("ff2b1")), "ff2b2": vec_opt(g("ff2b2"), 0.5),
             "lnout": [vec(g("lnout_w")), vec(g("lnout_b"))],
+            "bn": [vec(g("bnw")), vec(g("bnb"))] if g("bnw") in man else None,
         })
     return {"sub": sub, "layers": Ls, "cfg": cfg}
 
@@ -100,6 +105,23 @@ def posEncoding(Tsub: int, D: int) -> np.ndarray:
     return pe
 
 
+def SUB_CONVS(Csub):
+    """The dw-striding stack (raw-encoder.js:187-193): (cout, cin, k, stride, groups, act, stride-2)."""
+    return [(Csub, 1, 3, 2, 1, "relu", True), (Csub, Csub, 3, 2, Csub, "none", True), (Csub, Csub, 1, 1, 1, "relu", False),
+            (Csub, Csub, 3, 2, Csub, "none", True), (Csub, Csub, 1, 1, 1, "relu", False)]
+
+
+def chunkMask(cfg: dict, T: int) -> np.ndarray:
+    """raw-encoder.js:256-276: 0 where query i may see key j (j in
+    [cs - left, cs + C - 1 + right], cs = C*floor(i/C)), -10000 elsewhere."""
+    Cc, left, right = cfg["attChunk"], cfg.get("attLeft", 70), cfg.get("attRight", 0)
+    i = np.arange(T)[:, None]
+    j = np.arange(T)[None, :]
+    cs = Cc * (i // Cc)
+    lo, hi = np.maximum(0, cs - left), np.minimum(T - 1, cs + Cc - 1 + right)
+    return np.where((j >= lo) & (j <= hi), 0.0, -10000.0).astype(np.float32)
+
+
 def _pre_encode(ctx, enc, mel):
     """raw-encoder.js:177-222 for one window; mel [melBins, T] channel-major."""
     cfg = enc["cfg"]
@@ -107,21 +129,21 @@ def _pre_encode(ctx, enc, mel):
     T = mel.shape[1]
     s = ctx.upload(np.ascontiguousarray(_f32(mel).T), 1, T * mb)
     Hh, Wd = T, mb
-    conv = [(Csub, 1, 3, 2, 1, "relu", True), (Csub, Csub, 3, 2, Csub, "none", True), (Csub, Csub, 1, 1, 1, "relu", False),
-            (Csub, Csub, 3, 2, Csub, "none", True), (Csub, Csub, 1, 1, 1, "relu", False)]
-    for i, (cout, cin, k, st, gr, act, s2) in enumerate(conv):
-        p = 1 if s2 else 0
+    sp = cfg.get("subPad") or {"t": 1, "b": 1, "l": 1, "r": 1}
+    for i, (cout, cin, k, st, gr, act, s2) in enumerate(SUB_CONVS(Csub)):
+        pt, pb, pl, pr = (sp["t"], sp["b"], sp["l"], sp["r"]) if s2 else (0, 0, 0, 0)
         s = ctx.conv2d(s, enc["sub"]["conv"][i]["w"], cout, cin, Hh, Wd, k, k, bias=enc["sub"]["conv"][i]["b"], strideH=st, strideW=st,
-                       padTop=p, padBottom=p, padLeft=p, padRight=p, groups=gr, act=act)
-        Hh = (Hh + 2 * p - k) // st + 1
-        Wd = (Wd + 2 * p - k) // st + 1
+                       padTop=pt, padBottom=pb, padLeft=pl, padRight=pr, groups=gr, act=act)
+        Hh = (Hh + pt + pb - k) // st + 1
+        Wd = (Wd + pl + pr - k) // st + 1
     flat = ctx.subReshape(s, Csub, Hh, Wd)
     return ctx.matmul(flat, enc["sub"]["linw"], bias=enc["sub"]["linb"]), Hh
 
 
 def parakeetEncodeBatch(ctx: HipContext, enc: dict, mels: list) -> tuple:
-    """raw-encoder.js:235-386 (no chunk mask, Parakeet BN-folded conv module).
-    Returns (frames [W*Tsub, D] tensor, Tsub)."""
+    """raw-encoder.js:235-386, including the streaming models' options
+    (chunk-limited attention mask, causal depthwise conv, conv-module
+    LayerNorm).  Returns (frames [W*Tsub, D] tensor, Tsub)."""
     cfg = enc["cfg"]
     D, H, HD, K = cfg["D"], cfg["H"], cfg["HD"], cfg["dwK"]
     W = len(mels)
@@ -133,7 +155,11 @@ def parakeetEncodeBatch(ctx: HipContext, enc: dict, mels: list) -> tuple:
     peT = ctx.upload(posEncoding(Tsub, D), 2 * Tsub - 1, D)
     ln = lambda t, lp: ctx.layernorm(t, lp[0], lp[1])
     ff = lambda t, lp, w1, w2, b1, b2: ctx.matmul(ctx.matmul(ln(t, lp), w1, bias=b1, act="silu"), w2, bias=b2, add=t)
-    pad = (K - 1) >> 1
+    padL, padR = (K - 1, 0) if cfg.get("convCausal") else ((K - 1) >> 1, (K - 1) >> 1)
+    maskT = None
+    if cfg.get("attChunk"):
+        m = np.tile(chunkMask(cfg, Tsub), (W * H, 1))
+        maskT = ctx.upload(m, W * H * Tsub, Tsub)
 
     def run():
         nonlocal x
@@ -147,18 +173,24 @@ def parakeetEncodeBatch(ctx: HipContext, enc: dict, mels: list) -> tuple:
             p = ctx.matmul(peT, w["pos"])
             ac = ctx.bmmQK(q, k, w["pbuAll"], H, HD, W)
             bd = ctx.relShiftB(ctx.bmmQK(q, p, w["pbvAll"], H, HD, W, True), W * H)
-            probs = ctx.softmax(ctx.add(ac, bd))
+            sc = ctx.add(ac, bd)
+            if maskT is not None:
+                sc = ctx.add(sc, maskT)
+            probs = ctx.softmax(sc)
             outc = ctx.bmmPV(probs, v, H, HD, W)
             x = ctx.matmul(outc, w["out"], bias=w["outb"], add=x)
             pre1 = ctx.matmul(ln(x, w["lnconv"]), w["pw1T"], bias=w["pw1b"])
             glu = ctx.glu(ctx.transpose(pre1))
+            act = "none" if w["bn"] is not None else "silu"
             if W == 1:
-                dwo = ctx.conv1d(glu, w["dw"], D, K, groups=D, padLeft=pad, padRight=pad, bias=w["dwb"], act="silu")
+                dwo = ctx.conv1d(glu, w["dw"], D, K, groups=D, padLeft=padL, padRight=padR, bias=w["dwb"], act=act)
             else:
                 dwo = ctx.alloc(D, W * Tsub)
                 for wi in range(W):
-                    ctx.setCols(dwo, ctx.conv1d(ctx.sliceCols(glu, wi * Tsub, Tsub), w["dw"], D, K, groups=D, padLeft=pad, padRight=pad,
-                                                bias=w["dwb"], act="silu"), wi * Tsub)
+                    ctx.setCols(dwo, ctx.conv1d(ctx.sliceCols(glu, wi * Tsub, Tsub), w["dw"], D, K, groups=D, padLeft=padL, padRight=padR,
+                                                bias=w["dwb"], act=act), wi * Tsub)
+            if w["bn"] is not None:  # EOU: depthwise -> LayerNorm over channels -> SiLU
+                dwo = ctx.transpose(ctx.silu(ln(ctx.transpose(dwo), w["bn"])))
             x = ctx.matmul(ctx.transpose(dwo), w["pw2T"], bias=w["pw2b"], add=x)
             x = ff(x, w["lnff2"], w["ff2w1"], w["ff2w2"], w["ff2b1"], w["ff2b2"])
             x = ln(x, w["lnout"])

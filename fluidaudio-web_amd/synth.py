@@ -26,6 +26,14 @@ import numpy as np
 PARAKEET_CFG = dict(D=1024, DFF=4096, H=8, HD=128, layers=24, dwK=9, Csub=256, Fsub=16, melBins=128)
 
 
+def tiny_stream_cfg(layers=2, right=0, chunk=2):
+    """Small streaming (EOU-style) model: eou-parakeet/config.js's subsampling
+    pads and options at reduced dims.  With subPad l=2, r=1 the frequency axis
+    32 -> 17 -> 9 -> 5 gives Fsub 5 (not melBins / 8)."""
+    return dict(D=64, DFF=256, H=2, HD=32, layers=layers, dwK=9, Csub=8, Fsub=5, melBins=32, subPad={"t": 2, "b": 1, "l": 2, "r": 1},
+                convCausal=True, attChunk=chunk, attLeft=8, attRight=right)
+
+
 def tiny_cfg(layers=2):
     """Small config for CPU cross-checks (same structure, reduced dims)."""
     return dict(D=64, DFF=256, H=2, HD=32, layers=layers, dwK=9, Csub=8, Fsub=4, melBins=32)
@@ -64,6 +72,8 @@ def make_weights(cfg: dict, seed: int = 1, layers: int | None = None, biases: bo
         m[g("pw2")] = _f16r(n((D, D, 1), 0.02))
         m[g("dw")] = _f16r(n((D, 1, K), np.sqrt(1 / 3)))
         m[g("dwb")] = n(D, 0.02)
+        if cfg.get("convCausal"):  # streaming models normalise the depthwise output with a LayerNorm
+            m[g("bnw")], m[g("bnb")] = (1 + n(D, 0.02)).astype(np.float32), n(D, 0.02)
         if biases:
             for k in ("ff1b1", "ff2b1", "pw1b"):
                 m[g(k)] = n(DFF if k != "pw1b" else 2 * D, 0.02)

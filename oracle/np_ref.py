@@ -53,13 +53,16 @@ def pos_encoding(T: int, D: int) -> torch.Tensor:
 
 
 def subsample(cfg, man, mel):
-    """mel [melBins, T] -> [Tsub, D]."""
+    """mel [melBins, T] -> [Tsub, D].  cfg["subPad"] {t, b, l, r} pads the three
+    stride-2 convs asymmetrically (streaming models); default 1 on every side."""
     C = cfg["Csub"]
+    sp = cfg.get("subPad") or {"t": 1, "b": 1, "l": 1, "r": 1}
+    pad = lambda x: F.pad(x, (sp["l"], sp["r"], sp["t"], sp["b"]))  # noqa: E731
     x = _t(mel).T.unsqueeze(0).unsqueeze(0)  # [1, 1, T, melBins] (time = H, freq = W)
-    x = F.relu(F.conv2d(x, _t(man["c0w"]).reshape(C, 1, 3, 3), _t(man["c0b"]), stride=2, padding=1))
-    x = F.conv2d(x, _t(man["c1w"]).reshape(C, 1, 3, 3), _t(man["c1b"]), stride=2, padding=1, groups=C)
+    x = F.relu(F.conv2d(pad(x), _t(man["c0w"]).reshape(C, 1, 3, 3), _t(man["c0b"]), stride=2))
+    x = F.conv2d(pad(x), _t(man["c1w"]).reshape(C, 1, 3, 3), _t(man["c1b"]), stride=2, groups=C)
     x = F.relu(F.conv2d(x, _t(man["c2w"]).reshape(C, C, 1, 1), _t(man["c2b"])))
-    x = F.conv2d(x, _t(man["c3w"]).reshape(C, 1, 3, 3), _t(man["c3b"]), stride=2, padding=1, groups=C)
+    x = F.conv2d(pad(x), _t(man["c3w"]).reshape(C, 1, 3, 3), _t(man["c3b"]), stride=2, groups=C)
     x = F.relu(F.conv2d(x, _t(man["c4w"]).reshape(C, C, 1, 1), _t(man["c4b"])))
     b, c, t, f = x.shape
     x = x.transpose(1, 2).reshape(t, c * f)
@@ -92,7 +95,14 @@ def layer(cfg, man, L, x, W, T):
     vb = _t(man[g("pbv")]).reshape(1, H, 1, HD)
     ac = (q + u) @ k.transpose(-1, -2)
     bd = rel_shift_nemo((q + vb) @ p.unsqueeze(0).transpose(-1, -2))
-    att = torch.softmax((ac + bd) / math.sqrt(HD), dim=-1)
+    sc = (ac + bd) / math.sqrt(HD)
+    if cfg.get("attChunk"):  # chunk-limited attention: query i sees keys [cs - left, cs + C - 1 + right]
+        Cc, left, right = cfg["attChunk"], cfg.get("attLeft", 70), cfg.get("attRight", 0)
+        i = torch.arange(T).unsqueeze(1)
+        j = torch.arange(T).unsqueeze(0)
+        cs = Cc * torch.div(i, Cc, rounding_mode="floor")
+        sc = sc + torch.where((j >= cs - left) & (j <= cs + Cc - 1 + right), 0.0, -10000.0).to(sc.dtype)
+    att = torch.softmax(sc, dim=-1)
     o = (att @ v).transpose(1, 2).reshape(W * T, D)
     x = x + _lin(o, man, g("out"), g("outb"))
     # conv module
@@ -103,7 +113,10 @@ def layer(cfg, man, L, x, W, T):
         h = h + _t(man[g("pw1b")])
     h = F.glu(h, dim=-1)  # [W*T, D]
     h = h.reshape(W, T, D).transpose(1, 2)  # [W, D, T]
-    h = F.conv1d(h, _t(man[g("dw")]).reshape(D, 1, K), _t(man[g("dwb")]), padding=(K - 1) // 2, groups=D)
+    h = F.pad(h, (K - 1, 0) if cfg.get("convCausal") else ((K - 1) // 2, (K - 1) // 2))
+    h = F.conv1d(h, _t(man[g("dw")]).reshape(D, 1, K), _t(man[g("dwb")]), groups=D)
+    if man.get(g("bnw")) is not None:  # streaming conv module: LayerNorm over channels before SiLU
+        h = F.layer_norm(h.transpose(1, 2), (D,), _t(man[g("bnw")]), _t(man[g("bnb")]), eps=1e-5).transpose(1, 2)
     h = F.silu(h).transpose(1, 2).reshape(W * T, D)
     h = h @ _t(man[g("pw2")]).reshape(D, D).T
     if man.get(g("pw2b")) is not None:

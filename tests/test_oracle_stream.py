@@ -2,7 +2,19 @@
 or_relshift_stream, restating src/gpu/wasm-context.js:509-524): reduction to
 the offline rel_shift (itself pinned against NeMo's pad-reshape), a hand-worked
 known answer with mask and clamp, and the per-row count of unmasked keys."""
+import os
+import sys
+
 import numpy as np
+import pytest
+
+
+@pytest.fixture(scope="module")
+def npref():
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "oracle"))
+    import np_ref
+
+    return np_ref
 
 
 def test_full_context_equals_offline_rel_shift(orc):
@@ -36,3 +48,35 @@ def test_unmasked_key_count(orc):
             cs = C * (q // C)
             lo, hi = max(cs - left, subT - Lc), min(cs + C - 1 + right, subT - Lc + Lk - 1)
             assert int((y[r] != -1e4).sum()) == max(0, hi - lo + 1)
+
+
+def _stream_model(fa, layers=2, right=0, chunk=2):
+    cfg = fa.synth.tiny_stream_cfg(layers=layers, right=right, chunk=chunk)
+    return cfg, fa.synth.make_weights(cfg, seed=11)
+
+
+def test_np_ref_mask_wider_than_sequence_is_identity(fa, npref):
+    np_ref = npref
+    cfg, man = _stream_model(fa)
+    mel = fa.synth.make_features(cfg["melBins"], 160, seed=3)[0]
+    wide = dict(cfg, attChunk=64, attLeft=64)  # one chunk covers all 20 frames
+    free = {k: v for k, v in cfg.items() if k not in ("attChunk", "attLeft", "attRight")}
+    assert np.array_equal(np_ref.encode(wide, man, [mel]), np_ref.encode(free, man, [mel]))
+
+
+def test_np_ref_streaming_model_is_causal_up_to_its_chunk(fa, npref):
+    """With right context 0 (causal depthwise conv, top-padded subsampling,
+    chunk-limited attention) output frame s depends on mel frames up to 8 e
+    only, e = the last frame of s's chunk: later mel frames change nothing
+    before e + 1, and do change later frames."""
+    np_ref = npref
+    cfg, man = _stream_model(fa, chunk=2)
+    T = 240
+    mel = fa.synth.make_features(cfg["melBins"], T, seed=4)[0]
+    base = np_ref.encode(cfg, man, [mel])
+    for e in (5, 13):  # ends of chunks (chunk 2: frames 4..5 and 12..13)
+        pert = mel.copy()
+        pert[:, 8 * e + 1:] += np.random.default_rng(e).standard_normal(pert[:, 8 * e + 1:].shape).astype(np.float32)
+        out = np_ref.encode(cfg, man, [pert])
+        assert np.array_equal(out[:e + 1], base[:e + 1]), e
+        assert np.abs(out[e + 1:] - base[e + 1:]).max() > 1e-3, e
