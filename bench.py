@@ -204,7 +204,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="encoder", choices=["encoder", "layer", "ragged", "quant", "quant4", "gemv", "copy", "mel", "decode", "e2e"])
+    ap.add_argument("--workload", default="encoder", choices=["encoder", "layer", "ragged", "quant", "quant4", "gemv", "copy", "mel", "decode", "e2e", "stream"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--windows", type=int, default=16, help="decode workload: windows per decode call (1..64)")
     ap.add_argument("--audio-sec", type=float, default=3600.0, help="e2e workload: seconds of synthetic audio")
@@ -225,6 +225,8 @@ def main():
         return bench_decode(args, fa, ctx)
     if args.workload == "e2e":
         return bench_e2e(args, fa, ctx)
+    if args.workload == "stream":
+        return bench_stream(args, fa, ctx)
     cfg = dict(FULL)
     layout = "packed"
     if args.workload in ("encoder", "quant", "quant4"):
@@ -463,6 +465,57 @@ def bench_e2e(args, fa, ctx):
                                           f"(preEncode + 1 layer scaled to 24) + decode {t_dec:.2f} s, oracle/fa_oracle.c single thread"}
     dec.close()
     enc.close()
+    print(json.dumps(line), flush=True)
+
+
+def bench_stream(args, fa, ctx):
+    """Streaming encode (streaming.py, the op path) of 30 s of synthetic log-mel
+    pushed 160 ms at a time (16 mel frames = one chunk of 2 encoder frames),
+    with this path's Parakeet shapes (24 layers, d_model 1024, f16 weights) and
+    the EOU streaming config (eou-parakeet/config.js: chunk 2, left 70, causal
+    conv with LayerNorm, subsampling pads t2 b1 l2 r1).  value = audio-s /
+    wall-s of one stream; per-chunk latency in the config."""
+    cfg = dict(FULL, subPad={"t": 2, "b": 1, "l": 2, "r": 1}, convCausal=True, attChunk=2, attLeft=70, Fsub=17)
+    man = fa.synth.make_weights(cfg, seed=1)
+    enc = fa.loadParakeetEncoder(ctx, man, weights="f16", cfg=cfg)
+    seconds, piece = 30.0, 16
+    mel = fa.synth.make_features(128, int(seconds * 100), seed=2)[0]
+
+    def run():
+        st = fa.createEncodeStream(ctx, enc)
+        n = 0
+        for t in range(0, mel.shape[1], piece):
+            o = fa.encodeStreamPush(ctx, st, mel[:, t:t + piece])
+            n += 0 if o is None else o.shape[0]
+        o = fa.encodeStreamFlush(ctx, st)
+        n += 0 if o is None else o.shape[0]
+        fa.disposeEncodeStream(ctx, st)
+        return n
+
+    for _ in range(args.warmup):
+        frames = run()
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        frames = run()
+    wall = (time.perf_counter() - t0) / args.steps
+    chunks = mel.shape[1] // piece
+    line = {"metric": "streaming encode audio-s/wall-s per stream at 1 GPU", "value": round(seconds / wall, 1), "unit": "audio-s/wall-s",
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 2), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f16-weights/f32", "data": "synthetic log-mel ~N(0,1), random-init weights",
+            "config": {"workload": "30 s pushed in 160 ms pieces, 24 layers d_model 1024, chunk 2 / left 70 (EOU streaming config), op path",
+                       "frames": frames, "chunks": chunks, "ms_per_chunk": round(wall * 1e3 / chunks, 3)}}
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import np_ref
+        import torch
+        torch.set_num_threads(1)
+        seg = mel[:, :300]  # 3 s
+        t0 = time.perf_counter()
+        np_ref.encode(cfg, man, [seg])
+        cw = time.perf_counter() - t0
+        line["cpu_baseline"] = {"value": round(3.0 / cw, 2), "unit": "audio-s/wall-s", "cores": 1, "kind": "port",
+                                "sample": "3 s offline chunked-causal encode (the function the stream computes) through oracle/np_ref.py, float64 torch, 1 thread"}
     print(json.dumps(line), flush=True)
 
 
