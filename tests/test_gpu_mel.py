@@ -1,5 +1,5 @@
-"""Log-mel front end on the GPU (fa_mel_windows, the SURVEY's next-row mel
-frontend) vs the CPU oracle's restatement of the reference's JsPreprocessor
+"""Log-mel front end on the GPU (fa_mel_windows, the features in front of the
+encoder) vs the CPU oracle's restatement of the reference's JsPreprocessor
 (nemotron-mel.js:451-603, Parakeet settings parakeet-mel.js:8-22).  Both run
 the same f64 operation sequence with host-computed constants, so outputs agree
 bit for bit except where the device log rounds differently from the host's in

@@ -1,5 +1,5 @@
-"""Greedy TDT decoding on the GPU (fa_tdt_decode, the SURVEY's next-row GPU
-decode) vs the CPU oracle's restatement of rust/parakeet-decoder decode_proj.
+"""Greedy TDT decoding on the GPU (fa_tdt_decode, the step after the encoder)
+vs the CPU oracle's restatement of rust/parakeet-decoder decode_proj.
 Both compute the reference's f32 operation sequence (its polynomial expf,
 lane-ordered dots, in-order joint sums; no fused multiply-add), so the bar is
 identical token ids and frame indices for every window."""
