@@ -238,12 +238,18 @@ __global__ __launch_bounds__(256) void enc_ln_kernel(const float *__restrict__ x
   if (row >= rows) return;
   const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)row * D);
   float4 v[V];
+  f4 gv[V], bv[V];
+#pragma unroll
+  for (int t = 0; t < V; t++) {  // gamma / beta loaded with the row: their latency overlaps the reductions
+    v[t] = xr[lane + 64 * t];
+    gv[t] = reinterpret_cast<const f4 *>(gamma)[lane + 64 * t];
+    bv[t] = reinterpret_cast<const f4 *>(beta)[lane + 64 * t];
+  }
+#pragma unroll
+  for (int t = 0; t < V; t++) asm volatile("" : "+v"(gv[t]), "+v"(bv[t]));  // loads issued here, not sunk below the reductions
   float s = 0.f;
 #pragma unroll
-  for (int t = 0; t < V; t++) {
-    v[t] = xr[lane + 64 * t];
-    s += v[t].x + v[t].y + v[t].z + v[t].w;
-  }
+  for (int t = 0; t < V; t++) s += v[t].x + v[t].y + v[t].z + v[t].w;
   const float mean = wave_sum(s) * (1.f / D);
   float q = 0.f;
 #pragma unroll
@@ -255,7 +261,7 @@ __global__ __launch_bounds__(256) void enc_ln_kernel(const float *__restrict__ x
 #pragma unroll
   for (int t = 0; t < V; t++) {
     const int j = lane + 64 * t;
-    const float4 gm = reinterpret_cast<const float4 *>(gamma)[j], bt = reinterpret_cast<const float4 *>(beta)[j];
+    const f4 gm = gv[t], bt = bv[t];
     const float o[4] = {(v[t].x - mean) * inv * gm.x + bt.x, (v[t].y - mean) * inv * gm.y + bt.y, (v[t].z - mean) * inv * gm.z + bt.z,
                         (v[t].w - mean) * inv * gm.w + bt.w};
     h4 hi, lo;
