@@ -364,55 +364,62 @@ __global__ __launch_bounds__(256) void enc_ln2_kernel(float *__restrict__ x, con
 
 // Conv module depthwise conv over time, k taps, symmetric pad (k-1)/2,
 // + bias (BatchNorm folded) + SiLU (raw-encoder.js:365-367), per window.
-// Thread = 8 channels x TT consecutive frames; the TT+k-1 input rows are
-// loaded once into registers.  One wavefront covers 512 channels.
+// Thread = CPT channels x TT consecutive frames; the TT+k-1 input rows are
+// loaded once into registers (each input row is read (TT+k-1)/TT times).
 // TI = float: the GLU output arrives in f32; ylo (optional) receives the exact
 // f16 remainder of each output for a two-plane GEMM operand.
-template <int KT, int TT, typename TI>
+template <int KT, int TT, int CPT, typename TI>
 __global__ __launch_bounds__(64) void dwconv_silu_kernel(const TI *__restrict__ x, _Float16 *__restrict__ y, _Float16 *__restrict__ ylo,
                                                           const float *__restrict__ wt, const float *__restrict__ b, int D, WinStage st) {
+  static_assert(CPT == 4 || CPT == 8, "4 or 8 channels per thread");
+  typedef _Float16 hv __attribute__((ext_vector_type(CPT)));
   const int win = blockIdx.y;
   const int T = st.len[win];
   const int t0 = blockIdx.x * TT;
   if (t0 >= T) return;
-  const int c0 = (blockIdx.z * blockDim.x + threadIdx.x) * 8;
+  const int c0 = (blockIdx.z * blockDim.x + threadIdx.x) * CPT;
   if (c0 >= D) return;
   constexpr int PAD = (KT - 1) / 2;
   const TI *xb = x + (size_t)st.off[win] * D + c0;
   _Float16 *yb = y + (size_t)st.off[win] * D + c0;
-  float in[TT + KT - 1][8];
+  float in[TT + KT - 1][CPT];
 #pragma unroll
   for (int r = 0; r < TT + KT - 1; r++) {
     const int t = t0 - PAD + r;
     if (t >= 0 && t < T) {
       if constexpr (sizeof(TI) == 2) {
-        const h8 v = *reinterpret_cast<const h8 *>(xb + (size_t)t * D);
+        const hv v = *reinterpret_cast<const hv *>(xb + (size_t)t * D);
 #pragma unroll
-        for (int e = 0; e < 8; e++) in[r][e] = (float)v[e];
+        for (int e = 0; e < CPT; e++) in[r][e] = (float)v[e];
       } else {
-        const float4 a = reinterpret_cast<const float4 *>(xb + (size_t)t * D)[0], bq = reinterpret_cast<const float4 *>(xb + (size_t)t * D)[1];
-        in[r][0] = a.x; in[r][1] = a.y; in[r][2] = a.z; in[r][3] = a.w;
-        in[r][4] = bq.x; in[r][5] = bq.y; in[r][6] = bq.z; in[r][7] = bq.w;
+#pragma unroll
+        for (int q = 0; q < CPT / 4; q++) {
+          const float4 a4 = reinterpret_cast<const float4 *>(xb + (size_t)t * D)[q];
+          in[r][4 * q] = a4.x;
+          in[r][4 * q + 1] = a4.y;
+          in[r][4 * q + 2] = a4.z;
+          in[r][4 * q + 3] = a4.w;
+        }
       }
     } else {
 #pragma unroll
-      for (int e = 0; e < 8; e++) in[r][e] = 0.f;
+      for (int e = 0; e < CPT; e++) in[r][e] = 0.f;
     }
   }
-  float wk[KT][8];
+  float wk[KT][CPT];
 #pragma unroll
   for (int k = 0; k < KT; k++)
 #pragma unroll
-    for (int e = 0; e < 8; e++) wk[k][e] = wt[k * D + c0 + e];
-  float bb[8];
+    for (int e = 0; e < CPT; e++) wk[k][e] = wt[k * D + c0 + e];
+  float bb[CPT];
 #pragma unroll
-  for (int e = 0; e < 8; e++) bb[e] = b[c0 + e];
+  for (int e = 0; e < CPT; e++) bb[e] = b[c0 + e];
 #pragma unroll
   for (int t = 0; t < TT; t++) {
     if (t0 + t >= T) break;
-    h8 o, ol;
+    hv o, ol;
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
+    for (int e = 0; e < CPT; e++) {
       float acc = 0.f;
 #pragma unroll
       for (int k = 0; k < KT; k++) acc += in[t + k][e] * wk[k][e];
@@ -420,8 +427,8 @@ __global__ __launch_bounds__(64) void dwconv_silu_kernel(const TI *__restrict__ 
       o[e] = (_Float16)r;
       ol[e] = (_Float16)(r - (float)o[e]);
     }
-    *reinterpret_cast<h8 *>(yb + (size_t)(t0 + t) * D) = o;
-    if (ylo) *reinterpret_cast<h8 *>(ylo + (size_t)st.off[win] * D + c0 + (size_t)(t0 + t) * D) = ol;
+    *reinterpret_cast<hv *>(yb + (size_t)(t0 + t) * D) = o;
+    if (ylo) *reinterpret_cast<hv *>(ylo + (size_t)st.off[win] * D + c0 + (size_t)(t0 + t) * D) = ol;
   }
 }
 
@@ -1155,12 +1162,14 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
       _Float16 *dlo = (ex & FA_EXACT_DW_OUT) ? alo : nullptr;
       {
         ProfScope ps(ctx, glu32 ? (dlo ? "dwconv_x" : "dwconv_f32") : (dlo ? "dwconv_lo" : "dwconv"));
-        const int thr = std::min(64, D / 8);
-        const dim3 grid(cdiv(mx[3], 4), n, cdiv(D / 8, thr));
+        // 4 channels x 16 frames per thread: inputs read 1.5x (24 rows per 16
+        // outputs); measured 9.6 us against 10.9 for 8 channels x 4 frames (3x)
+        const int thr = std::min(64, D / 4);
+        const dim3 grid(cdiv(mx[3], 16), n, cdiv(D / 4, thr));
         if (glu32)
-          FA_LAUNCH(ps, (dwconv_silu_kernel<9, 4, float>), grid, dim3(thr), 0, ctx->stream, (const float *)g32, a, dlo, Ly.dww, Ly.dwb, D, s3);
+          FA_LAUNCH(ps, (dwconv_silu_kernel<9, 16, 4, float>), grid, dim3(thr), 0, ctx->stream, (const float *)g32, a, dlo, Ly.dww, Ly.dwb, D, s3);
         else
-          FA_LAUNCH(ps, (dwconv_silu_kernel<9, 4, _Float16>), grid, dim3(thr), 0, ctx->stream, (const _Float16 *)gg, a, dlo, Ly.dww, Ly.dwb, D, s3);
+          FA_LAUNCH(ps, (dwconv_silu_kernel<9, 16, 4, _Float16>), grid, dim3(thr), 0, ctx->stream, (const _Float16 *)gg, a, dlo, Ly.dww, Ly.dwb, D, s3);
         FA_TRY(check_launch(ctx, "dwconv"));
       }
       FA_TRY(gemm(a, dlo, D, Ly.pw2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, dlo ? "pw2_x" : "pw2"));
