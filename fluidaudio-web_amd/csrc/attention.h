@@ -32,6 +32,7 @@ struct AttnArgs {
 int relpos_attention(fa_ctx *ctx, const AttnArgs &a, int in_f32, int out_f32, int Tmax, const char *label);
 // f16 q/k/v/pos/out (the fused encoder): transposes V into vt (capacity
 // W * H * 128 * round_up(Tmax, 64) halfs), then the LDS-staged kernel.
-int relpos_attention_f16(fa_ctx *ctx, const AttnArgs &a, int Tmax, _Float16 *vt, const char *label);
+// transpose = 0: vt already holds V (written by the q|k|v GEMM's epilogue)
+int relpos_attention_f16(fa_ctx *ctx, const AttnArgs &a, int Tmax, _Float16 *vt, const char *label, bool transpose = true);
 
 }  // namespace fa

@@ -457,7 +457,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(NWV > 
     }
 }
 
-int relpos_attention_f16(fa_ctx *ctx, const AttnArgs &a, int Tmax, _Float16 *vt, const char *label) {
+int relpos_attention_f16(fa_ctx *ctx, const AttnArgs &a, int Tmax, _Float16 *vt, const char *label, bool transpose) {
   const int W = a.win.n;
   if (a.HD != 128) return set_err(ctx, FA_E_UNSUPPORTED, "%s: head dim %d (kernel is specialised for 128)", label, a.HD);
   if (Tmax <= 0 || W <= 0) return FA_OK;
@@ -466,7 +466,7 @@ int relpos_attention_f16(fa_ctx *ctx, const AttnArgs &a, int Tmax, _Float16 *vt,
     if (a.win.len[i] > Tmax || a.pcenter - (a.win.len[i] - 1) < 0 || a.pcenter + a.win.len[i] - 1 >= a.prows)
       return set_err(ctx, FA_E_INVALID, "%s: window %d length %d outside the positional table", label, i, a.win.len[i]);
   const int Tp = (Tmax + 63) / 64 * 64;  // v_transpose_kernel tiles of 64 keys; the attention reads 32 at a time
-  {
+  if (transpose) {
     ProfScope ps(ctx, "v_transpose");
     FA_LAUNCH(ps, v_transpose_kernel, dim3(Tp / 64, a.H, W), dim3(256), 0, ctx->stream, reinterpret_cast<const _Float16 *>(a.v), a.ldv, a.win, a.H,
               Tp, vt);

@@ -148,12 +148,17 @@ __global__ __launch_bounds__(256) void sub_c01_kernel(const float *__restrict__ 
 // c3: depthwise conv2d 3x3, stride 2, pad 1, + bias (raw-encoder.js:191) over
 // the c2 GEMM's f32 pre-activation output, applying c2's ReLU on load.
 // wt [9][C] (tap-major).  Output hi/lo pairs like sub_c01_kernel.
+// With vrow set it also writes the encoder's row map for the transposed V
+// buffer: vrow[out.off[win] + to] = win * vstride + to for the window's
+// frames, -1 for the padding rows of a padded layout (to < vpad).
 template <int CPL>
 __global__ __launch_bounds__(256) void sub_dw_kernel(const float *__restrict__ x, WinStage in, int Fin, WinStage out, int Fout,
-                                                     const float *__restrict__ wt, const float *__restrict__ b, _Float16 *__restrict__ y) {
+                                                     const float *__restrict__ wt, const float *__restrict__ b, _Float16 *__restrict__ y,
+                                                     int *__restrict__ vrow, int vstride, int vpad) {
   constexpr int C = 64 * CPL;
   const int lane = threadIdx.x & 63, win = blockIdx.y;
   const int to = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (vrow && lane == 0 && (to < out.len[win] || to < vpad)) vrow[out.off[win] + to] = to < out.len[win] ? win * vstride + to : -1;
   if (to >= out.len[win]) return;
   float wr[9][CPL], br[CPL];
 #pragma unroll
@@ -217,8 +222,8 @@ static int launch_c01(fa_ctx *ctx, ProfScope &ps, dim3 grid, const float *mel, i
   return FA_OK;
 }
 static int launch_dw(fa_ctx *ctx, ProfScope &ps, dim3 grid, const float *x, WinStage in, int Fin, WinStage out, int Fout, const float *wt,
-                     const float *b, _Float16 *y, int C) {
-#define FA_DW(K) FA_LAUNCH(ps, sub_dw_kernel<K>, grid, dim3(256), 0, ctx->stream, x, in, Fin, out, Fout, wt, b, y)
+                     const float *b, _Float16 *y, int C, int *vrow, int vstride, int vpad) {
+#define FA_DW(K) FA_LAUNCH(ps, sub_dw_kernel<K>, grid, dim3(256), 0, ctx->stream, x, in, Fin, out, Fout, wt, b, y, vrow, vstride, vpad)
   FA_CPL_SWITCH(C, FA_DW)
 #undef FA_DW
   return FA_OK;
@@ -489,9 +494,10 @@ struct fa_encoder {
   };
   std::vector<Captured> graphs;
   uint64_t ws_gen = 0, graph_clock = 0;
+  bool vt_fuse = true;  // q|k|v epilogue writes the transposed V (FA_VT_FUSE=0 at load: v_transpose_kernel)
   // workspace (grow-only)
-  void *hlo = nullptr, *ulo = nullptr, *alo = nullptr, *g32 = nullptr, *vt = nullptr, *s2 = nullptr, *s2p = nullptr, *s3 = nullptr, *s3p = nullptr, *h = nullptr, *u = nullptr, *a = nullptr, *g = nullptr;
-  size_t cap_hlo = 0, cap_ulo = 0, cap_alo = 0, cap_g32 = 0, cap_vt = 0, cap_s2 = 0, cap_s2p = 0, cap_s3 = 0, cap_s3p = 0, cap_m = 0, cap_u = 0;
+  void *hlo = nullptr, *ulo = nullptr, *alo = nullptr, *g32 = nullptr, *vt = nullptr, *vrow = nullptr, *s2 = nullptr, *s2p = nullptr, *s3 = nullptr, *s3p = nullptr, *h = nullptr, *u = nullptr, *a = nullptr, *g = nullptr;
+  size_t cap_hlo = 0, cap_ulo = 0, cap_alo = 0, cap_g32 = 0, cap_vt = 0, cap_vrow = 0, cap_s2 = 0, cap_s2p = 0, cap_s3 = 0, cap_s3p = 0, cap_m = 0, cap_u = 0;
 };
 
 namespace fa {
@@ -684,7 +690,7 @@ void fa_encoder_destroy(fa_encoder *enc) {
   for (void *p : enc->allocs) (void)hipFree(p);
   for (auto &g : enc->graphs)
     if (g.exec) (void)hipGraphExecDestroy(g.exec);
-  for (void *p : {enc->hlo, enc->ulo, enc->alo, enc->g32, enc->vt, enc->s2, enc->s2p, enc->s3, enc->s3p, enc->h, enc->u, enc->a, enc->g})
+  for (void *p : {enc->hlo, enc->ulo, enc->alo, enc->g32, enc->vt, enc->vrow, enc->s2, enc->s2p, enc->s3, enc->s3p, enc->h, enc->u, enc->a, enc->g})
     if (p) (void)hipFree(p);
   delete enc;
 }
@@ -740,6 +746,7 @@ int fa_encoder_load(fa_ctx *ctx, const fa_encoder_cfg *cfg, int n, const char *c
   e->cfg = c;
   e->format = format;
   e->maxT = max_T;
+  if (const char *vf = getenv("FA_VT_FUSE")) e->vt_fuse = vf[0] != '0';
   auto fail = [&](int st) {
     fa_encoder_destroy(e);
     return st;
@@ -1046,7 +1053,17 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
     if (any & (FA_EXACT_ATTN_OUT | FA_EXACT_DW_OUT)) FA_TRY(grow(e, &e->alo, &e->cap_alo, (size_t)M * D * 2));
     if (any & FA_EXACT_GLU) FA_TRY(grow(e, &e->g32, &e->cap_g32, (size_t)M * D * 4));
   }
-  FA_TRY(grow(e, &e->vt, &e->cap_vt, (size_t)n * c.H * c.HD * ((mx[3] + 63) / 64 * 64) * 2));  // transposed V per (window, head)
+  const int Tp = (mx[3] + 63) / 64 * 64;  // key stride of the transposed V buffer
+  {
+    // transposed V per (window, head), written by the q|k|v GEMM's epilogue
+    // (or v_transpose_kernel).  Keys past a window's end are never written:
+    // the buffer starts zeroed and afterwards holds only finite V values of
+    // earlier forwards there, which the attention weights by exactly 0.
+    const uint64_t gen = e->ws_gen;
+    FA_TRY(grow(e, &e->vt, &e->cap_vt, (size_t)n * c.H * c.HD * Tp * 2));
+    if (e->ws_gen != gen) FA_HIP(ctx, hipMemsetAsync(e->vt, 0, e->cap_vt, ctx->stream));
+    FA_TRY(grow(e, &e->vrow, &e->cap_vrow, (size_t)M * 4));
+  }
   fa_tensor ox;
   TensorRec *rx;
   FA_TRY(new_tensor(ctx, M, D, S_F32, (size_t)M * D * 4, &ox, &rx));
@@ -1075,7 +1092,8 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
     }
     {
       ProfScope ps(ctx, "sub_dw3");
-      FA_TRY(launch_dw(ctx, ps, dim3(cdiv(mx[3], 4), n), (const float *)e->s2p, s2, F2, s3, F3, e->c3w, e->c3b, (_Float16 *)e->s3, C));
+      FA_TRY(launch_dw(ctx, ps, dim3(cdiv(mx[3], 4), n), (const float *)e->s2p, s2, F2, s3, F3, e->c3w, e->c3b, (_Float16 *)e->s3, C, (int *)e->vrow,
+                       c.H * c.HD * Tp, layout == 1 ? mx[3] : 0));
       FA_TRY(check_launch(ctx, "sub_dw3"));
     }
     {
@@ -1148,12 +1166,26 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
       FA_TRY(gemm(u, ul, c.DFF, Ly.ff1w2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, ul ? "ff1_w2_x" : "ff1_w2"));
       // attention
       FA_TRY(ln(1, Ly, hl ? "ln_att_x" : "ln_att"));
-      FA_TRY(gemm(h, hl, D, Ly.qkv, u, nullptr, 3 * D, 1, FA_ACT_NONE, nullptr, 0, hl ? "qkv_x" : "qkv"));
+      bool vt_fused = false;
+      {
+        // q|k|v; V goes straight to the attention's transposed buffer when
+        // the direct-to-LDS route runs it (FA_VT_FUSE=0 at load keeps v_transpose)
+        GemmArgs p;
+        p.A = h; p.Alo = hl; p.lda = D; p.akind = A_F16;
+        set_gemm_b(p, Ly.qkv);
+        p.C = u; p.ldc = 3 * D; p.out_f16 = 1;
+        p.M = M;
+        if (c.HD == 128 && e->vt_fuse && gemm_takes_direct(ctx, p)) {
+          p.vt = (_Float16 *)e->vt; p.vrow = (const int *)e->vrow; p.vcol0 = 2 * D; p.vtp = Tp;
+          vt_fused = true;
+        }
+        FA_TRY(gemm_mfma(ctx, p, hl ? "qkv_x" : "qkv"));
+      }
       at.pos = Ly.P;
       at.pbu = Ly.pbu;
       at.pbv = Ly.pbv;
       at.out_lo = (ex & FA_EXACT_ATTN_OUT) ? alo : nullptr;
-      FA_TRY(relpos_attention_f16(ctx, at, mx[3], (_Float16 *)e->vt, at.out_lo ? "attention_x" : "attention"));
+      FA_TRY(relpos_attention_f16(ctx, at, mx[3], (_Float16 *)e->vt, at.out_lo ? "attention_x" : "attention", !vt_fused));
       FA_TRY(gemm(a, at.out_lo, D, Ly.out, x, nullptr, D, 0, FA_ACT_NONE, x, 0, at.out_lo ? "attn_out_x" : "attn_out"));
       // conv module: pw1 + GLU (f16, or f32 when exact) -> depthwise + SiLU -> pw2
       FA_TRY(ln(2, Ly, hl ? "ln_conv_x" : "ln_conv"));

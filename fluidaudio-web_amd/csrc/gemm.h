@@ -31,8 +31,16 @@ struct GemmArgs {
   int act = 0;
   int glu = 0;   // GLU-pair epilogue (see gemm.hip), out [M, N/2] f16
   int hilo = 0;  // ReLU then an exact f16 pair per value: out [M, 2N] f16, (hi, lo) at columns 2n, 2n+1
+  // f16 epilogue only: columns >= vcol0 go transposed to vt[vrow[row] + (col - vcol0) * vtp]
+  // instead of C (rows with vrow < 0 are dropped); the direct-to-LDS route only
+  _Float16 *vt = nullptr;
+  const int *vrow = nullptr;
+  int vcol0 = 0, vtp = 0;
   int M = 0, N = 0, K = 0;
 };
+
+// 1 when gemm_mfma runs p on the direct-to-LDS route (the one that honours vt)
+int gemm_takes_direct(fa_ctx *ctx, const GemmArgs &p);
 
 int gemm_mfma(fa_ctx *ctx, const GemmArgs &p, const char *label);
 int gemm_f32(fa_ctx *ctx, const float *A, const float *B, float *C, const float *bias, const float *add, int M, int N, int K, int act,

@@ -351,10 +351,23 @@ __device__ __forceinline__ void epilogue_direct(const GemmArgs &p, f4 (&acc)[TI]
   for (int i = 0; i < TI; i++) {
     const int row = r0 + 16 * i + (lane & 15);
     if (row >= p.M) continue;
+    int vr = -1;  // transposed-V destination of this row
+    if constexpr (EPI == EPI_F16)
+      if (p.vt) vr = p.vrow[row];
 #pragma unroll
     for (int j = 0; j < TJ; j++) {
       const int col = c0 + 16 * j + cl;
       f4 v = scaled ? acc[i][j] : acc[i][j] + bv[j];
+      if constexpr (EPI == EPI_F16) {
+        if (p.vt && col >= p.vcol0) {  // 16 lanes = 16 consecutive keys: 32-byte runs per column
+          if (vr >= 0) {
+            _Float16 *dst = p.vt + vr + (size_t)(col - p.vcol0) * p.vtp;
+#pragma unroll
+            for (int e = 0; e < 4; e++) dst[(size_t)e * p.vtp] = to_f16(v[e]);
+          }
+          continue;
+        }
+      }
       if constexpr (EPI == EPI_F32) {
         if (p.add) v += *reinterpret_cast<const f4 *>(p.add + (size_t)row * p.ldadd + col);
         *reinterpret_cast<f4 *>(reinterpret_cast<float *>(p.C) + (size_t)row * p.ldc + col) = v;
@@ -889,7 +902,17 @@ static int launch_kind(fa_ctx *ctx, const GemmArgs &p, const char *label) {
   }
 }
 
+int gemm_takes_direct(fa_ctx *ctx, const GemmArgs &p) {
+  if (p.akind != A_F16 || epi_of(p) == EPI_GENERIC || pick_dma(ctx, p) < 0) return 0;
+  if (p.bkind == B_F16) return 1;
+  if (p.bkind == B_I8) return !p.Alo;
+  if (p.bkind == B_I4) return !p.Alo && !p.bzp && !p.bscale_f32;
+  return 0;
+}
+
 int gemm_mfma(fa_ctx *ctx, const GemmArgs &p, const char *label) {
+  if (p.vt && (epi_of(p) != EPI_F16 || !gemm_takes_direct(ctx, p)))
+    return set_err(ctx, FA_E_UNSUPPORTED, "%s: transposed-V output needs the f16 epilogue of the direct-to-LDS route", label);
   if (p.M <= 0 || p.N <= 0) return FA_OK;
   if (p.K % 64 != 0) return set_err(ctx, FA_E_UNSUPPORTED, "%s: K=%d must be a multiple of 64", label, p.K);
   if (p.glu && p.N % 16 != 0) return set_err(ctx, FA_E_UNSUPPORTED, "%s: GLU epilogue needs N%%16==0", label);

@@ -123,6 +123,36 @@ def test_quantized_direct_to_lds_route_matches_staged_route(ctx, fa, small, monk
     assert np.array_equal(fast, staged), float(np.abs(fast - staged).max())
 
 
+@pytest.mark.parametrize("layout", ["packed", "padded"])
+def test_transposed_v_epilogue_matches_v_transpose(ctx, fa, small, monkeypatch, layout):
+    """The q|k|v GEMM writing V straight into the attention's transposed
+    [window][head][d][key] buffer (through the row map the front end's last
+    kernel writes) gives the bits of the separate v_transpose pass: same f16
+    values, same attention.  Ragged windows ending mid-tile, graph replay and
+    eager runs, every operand plane (the two-plane q|k|v route included), and
+    a second, smaller batch over the same buffers (keys past a window's end
+    then hold the first batch's values, which the attention weights by 0)."""
+    big = [fa.synth.make_features(128, t, seed=60 + i)[0] for i, t in enumerate((1500, 777, 1001))]
+    little = [fa.synth.make_features(128, t, seed=70 + i)[0] for i, t in enumerate((403, 911))]
+    monkeypatch.setenv("FA_VT_FUSE", "0")
+    ref_enc = fa.FusedEncoder(ctx, small, "f16", max_T=188)
+    monkeypatch.delenv("FA_VT_FUSE")
+    enc = fa.FusedEncoder(ctx, small, "f16", max_T=188)
+    for mask in (None, 31):
+        if mask is not None:
+            ref_enc.setExact(mask)
+            enc.setExact(mask)
+        for mels in (big, little, big):
+            want = ref_enc.encode(mels, layout)
+            for graph in ("1", "0"):
+                monkeypatch.setenv("FA_GRAPH", graph)
+                got = enc.encode(mels, layout)
+                assert all(np.array_equal(g, w) for g, w in zip(got, want)), (mask, graph, [t.shape for t in got])
+            monkeypatch.delenv("FA_GRAPH")
+    enc.close()
+    ref_enc.close()
+
+
 def test_attention_workgroup_shapes_agree(ctx, fa, small, monkeypatch):
     """The two rel-pos attention workgroup shapes (default: 96 queries as 6
     waves x 1 row tile; FA_ATTN=1: 128 queries as 4 waves x 2 row tiles) give
