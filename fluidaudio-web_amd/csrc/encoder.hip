@@ -1268,6 +1268,7 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
       size_t lru = 0;
       for (size_t i = 1; i < e->graphs.size(); i++)
         if (e->graphs[i].used < e->graphs[lru].used) lru = i;
+      (void)hipStreamSynchronize(ctx->stream);  // the evicted graph may still be running on this stream
       (void)hipGraphExecDestroy(e->graphs[lru].exec);
       e->graphs.erase(e->graphs.begin() + lru);
     }
