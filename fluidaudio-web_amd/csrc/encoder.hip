@@ -73,14 +73,29 @@ __device__ __forceinline__ void store_hilo(_Float16 *dst, const float (&v)[CPL])
 // the c0 map never reaches memory.  c0 outputs outside [0,T1) x [0,F1) are
 // c1's zero padding.  w0 [C][9], b0 [C]; w1 [9][C] (tap-major), b1 [C].
 // Output: [rows of stage 2][F2][C] as hi/lo pairs (2C halfs per position).
-template <int CPL>
+// LM = true (MB <= kC01MelMax): the wave's 7 mel rows (4*t2-3 .. 4*t2+3) are
+// staged in LDS once, zero-padded in time and by one bin on either side, and
+// the c0 taps are LDS broadcasts instead of per-tap global loads.
+constexpr int kC01MelMax = 128, kC01MelStride = kC01MelMax + 4;
+template <int CPL, bool LM = false>
 __global__ __launch_bounds__(256) void sub_c01_kernel(const float *__restrict__ mel, int MB, WinStage s0, WinStage s1, int F1, WinStage s2, int F2,
                                                       const float *__restrict__ w0, const float *__restrict__ b0, const float *__restrict__ w1,
                                                       const float *__restrict__ b1, _Float16 *__restrict__ y) {
   constexpr int C = 64 * CPL;
-  const int lane = threadIdx.x & 63, win = blockIdx.y;
-  const int t2 = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  __shared__ float smel[LM ? 4 : 1][LM ? 7 : 1][LM ? kC01MelStride : 1];
+  const int lane = threadIdx.x & 63, win = blockIdx.y, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int t2 = blockIdx.x * 4 + wave;
   if (t2 >= s2.len[win]) return;
+  if constexpr (LM) {  // slot j holds bin j - 1; rows outside the window are zero
+    const int T0w = s0.len[win];
+    const float *mw = mel + (size_t)s0.off[win] * MB;
+    for (int idx = lane; idx < 7 * kC01MelStride; idx += 64) {
+      const int r = idx / kC01MelStride, j = idx - r * kC01MelStride, ti = 4 * t2 - 3 + r, fi = j - 1;
+      smel[wave][r][j] = (ti >= 0 && ti < T0w && fi >= 0 && fi < MB) ? mw[(size_t)ti * MB + fi] : 0.f;
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): wave-private rows, written by this wave
+    __builtin_amdgcn_wave_barrier();
+  }
   float k0[CPL][9], c0b[CPL], k1[9][CPL], c1b[CPL];
 #pragma unroll
   for (int e = 0; e < CPL; e++) {
@@ -109,7 +124,10 @@ __global__ __launch_bounds__(256) void sub_c01_kernel(const float *__restrict__ 
 #pragma unroll
       for (int bb = 0; bb < 3; bb++) {
         const int fi = 2 * f1 - 1 + bb;
-        x[a * 3 + bb] = (ti >= 0 && ti < T0 && fi >= 0 && fi < MB) ? m[(size_t)ti * MB + fi] : 0.f;
+        if constexpr (LM)
+          x[a * 3 + bb] = smel[wave][ti - (4 * t2 - 3)][fi + 1];
+        else
+          x[a * 3 + bb] = (ti >= 0 && ti < T0 && fi >= 0 && fi < MB) ? m[(size_t)ti * MB + fi] : 0.f;
       }
     }
 #pragma unroll
@@ -215,7 +233,13 @@ __global__ __launch_bounds__(256) void sub_dw_kernel(const float *__restrict__ x
     default: return set_err(ctx, FA_E_UNSUPPORTED, "Csub=%d", (C)); \
   }
 static int launch_c01(fa_ctx *ctx, ProfScope &ps, dim3 grid, const float *mel, int MB, WinStage s0, WinStage s1, int F1, WinStage s2, int F2,
-                      const float *w0, const float *b0, const float *w1, const float *b1, _Float16 *y, int C) {
+                      const float *w0, const float *b0, const float *w1, const float *b1, _Float16 *y, int C, bool lds_mel) {
+  if (MB <= kC01MelMax && lds_mel) {
+#define FA_C01(K) FA_LAUNCH(ps, (sub_c01_kernel<K, true>), grid, dim3(256), 0, ctx->stream, mel, MB, s0, s1, F1, s2, F2, w0, b0, w1, b1, y)
+    FA_CPL_SWITCH(C, FA_C01)
+#undef FA_C01
+    return FA_OK;
+  }
 #define FA_C01(K) FA_LAUNCH(ps, sub_c01_kernel<K>, grid, dim3(256), 0, ctx->stream, mel, MB, s0, s1, F1, s2, F2, w0, b0, w1, b1, y)
   FA_CPL_SWITCH(C, FA_C01)
 #undef FA_C01
@@ -494,7 +518,8 @@ struct fa_encoder {
   };
   std::vector<Captured> graphs;
   uint64_t ws_gen = 0, graph_clock = 0;
-  bool vt_fuse = true;  // q|k|v epilogue writes the transposed V (FA_VT_FUSE=0 at load: v_transpose_kernel)
+  bool vt_fuse = true;
+  bool c01_lds = true;  // front end stages mel rows in LDS (FA_C01_LDS=0 at load: per-tap global loads)  // q|k|v epilogue writes the transposed V (FA_VT_FUSE=0 at load: v_transpose_kernel)
   // workspace (grow-only)
   void *hlo = nullptr, *ulo = nullptr, *alo = nullptr, *g32 = nullptr, *vt = nullptr, *vrow = nullptr, *s2 = nullptr, *s2p = nullptr, *s3 = nullptr, *s3p = nullptr, *h = nullptr, *u = nullptr, *a = nullptr, *g = nullptr;
   size_t cap_hlo = 0, cap_ulo = 0, cap_alo = 0, cap_g32 = 0, cap_vt = 0, cap_vrow = 0, cap_s2 = 0, cap_s2p = 0, cap_s3 = 0, cap_s3p = 0, cap_m = 0, cap_u = 0;
@@ -747,6 +772,7 @@ int fa_encoder_load(fa_ctx *ctx, const fa_encoder_cfg *cfg, int n, const char *c
   e->format = format;
   e->maxT = max_T;
   if (const char *vf = getenv("FA_VT_FUSE")) e->vt_fuse = vf[0] != '0';
+  if (const char *cl = getenv("FA_C01_LDS")) e->c01_lds = cl[0] != '0';
   auto fail = [&](int st) {
     fa_encoder_destroy(e);
     return st;
@@ -1079,7 +1105,7 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
     {
       ProfScope ps(ctx, "sub_c01");
       FA_TRY(launch_c01(ctx, ps, dim3(cdiv(mx[2], 4), n), (const float *)rm->ptr, MB, s0, s1, F1, s2, F2, e->c0w, e->c0b, e->c1w, e->c1b,
-                        (_Float16 *)e->s2, C));
+                        (_Float16 *)e->s2, C, e->c01_lds));
       FA_TRY(check_launch(ctx, "sub_c01"));
     }
     {

@@ -123,6 +123,22 @@ def test_quantized_direct_to_lds_route_matches_staged_route(ctx, fa, small, monk
     assert np.array_equal(fast, staged), float(np.abs(fast - staged).max())
 
 
+def test_front_end_lds_mel_rows_match_global_taps(ctx, fa, small, monkeypatch):
+    """The front end's c0/c1 kernel reading its 7 mel rows per output row from
+    LDS (zero-padded in time and by one bin each side) gives the bits of the
+    per-tap global loads with explicit bounds checks: ragged windows whose
+    lengths leave partial first and last c0 rows, and a 1-frame window."""
+    mels = [fa.synth.make_features(128, t, seed=80 + i)[0] for i, t in enumerate((1500, 777, 1001, 9, 1))]
+    monkeypatch.setenv("FA_C01_LDS", "0")
+    ref_enc = fa.FusedEncoder(ctx, small, "f16", max_T=188)
+    monkeypatch.delenv("FA_C01_LDS")
+    enc = fa.FusedEncoder(ctx, small, "f16", max_T=188)
+    want, got = ref_enc.encode(mels), enc.encode(mels)
+    enc.close()
+    ref_enc.close()
+    assert all(np.array_equal(g, w) for g, w in zip(got, want))
+
+
 @pytest.mark.parametrize("layout", ["packed", "padded"])
 def test_transposed_v_epilogue_matches_v_transpose(ctx, fa, small, monkeypatch, layout):
     """The q|k|v GEMM writing V straight into the attention's transposed
