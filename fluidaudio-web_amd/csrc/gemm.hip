@@ -555,6 +555,13 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
   const int sw8 = ((lane & 15) >> 1) & 3;  // int8 B rows: (row >> 1) & 3
   const int sw4 = ((lane & 15) >> 2) & 1;  // int4 B rows: (row >> 2) & 1
   h8 af[2][TI], bf[2][TJ], al[2][LO ? TI : 1];
+  // int4 B: raw fragments (4 bytes + block scale) are kept as read and
+  // widened right before their MFMAs, so the LDS read of the next half-step
+  // is not waited for before this half-step's MFMAs issue (measured: int4
+  // encoder 10.10 -> 9.57 ms; int8, whose widening is cheaper, was 1 % slower
+  // this way and widens at the read)
+  uint2 bq[2][B4 ? TJ : 1];
+  _Float16 bs[2][B4 ? TJ : 1];
   // int4 block scales of the K tile being read, two sets by tile parity
   uint32_t scs[2][B4 ? TJ : 1];
   auto ldscale = [&](int set, int kt) {
@@ -586,8 +593,8 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
 #pragma unroll
       for (int j = 0; j < TJ; j++) {
         const uint32_t sw2 = scs[set][j];
-        const _Float16 sc = __builtin_bit_cast(_Float16, (uint16_t)(ks ? (sw2 >> 16) : (sw2 & 0xffffu)));
-        bf[slot][j] = i4x8_to_h8(*reinterpret_cast<const uint32_t *>(base + bbase + j * 16 * RBB + so4), sc);
+        bs[slot][j] = __builtin_bit_cast(_Float16, (uint16_t)(ks ? (sw2 >> 16) : (sw2 & 0xffffu)));
+        bq[slot][j].x = *reinterpret_cast<const uint32_t *>(base + bbase + j * 16 * RBB + so4);
       }
     } else {
 #pragma unroll
@@ -595,6 +602,10 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
     }
   };
   auto mma = [&](int slot) {
+    if constexpr (B4) {
+#pragma unroll
+      for (int j = 0; j < TJ; j++) bf[slot][j] = i4x8_to_h8(bq[slot][j].x, bs[slot][j]);
+    }
 #pragma unroll
     for (int i = 0; i < TI; i++)
 #pragma unroll
