@@ -462,6 +462,18 @@ __global__ __launch_bounds__(64) void dwconv_silu_kernel(const TI *__restrict__ 
 }
 
 // Zero rows of a padded batch past each window's length (output contract).
+// Plain 16-byte vector copy (graph-mode input / output staging).
+__global__ __launch_bounds__(256) void copy_f4_kernel(const float4 *__restrict__ src, float4 *__restrict__ dst, long n4) {
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n4; i += (long)gridDim.x * 256) dst[i] = src[i];
+}
+static int copy_f4(fa_ctx *ctx, const void *src, void *dst, size_t bytes, const char *label) {
+  const long n4 = (long)(bytes / 16);
+  if (!n4) return FA_OK;
+  ProfScope ps(ctx, label);
+  FA_LAUNCH(ps, copy_f4_kernel, dim3((unsigned)std::min<long>(cdiv(n4, 256), 4096)), dim3(256), 0, ctx->stream, (const float4 *)src, (float4 *)dst, n4);
+  return check_launch(ctx, label);
+}
+
 __global__ void zero_pad_rows_kernel(float *x, int D, WinStage st, int Tpad) {
   const int win = blockIdx.y;
   const int r = blockIdx.x;
@@ -523,6 +535,11 @@ struct fa_encoder {
   // workspace (grow-only)
   void *hlo = nullptr, *ulo = nullptr, *alo = nullptr, *g32 = nullptr, *vt = nullptr, *vrow = nullptr, *s2 = nullptr, *s2p = nullptr, *s3 = nullptr, *s3p = nullptr, *h = nullptr, *u = nullptr, *a = nullptr, *g = nullptr;
   size_t cap_hlo = 0, cap_ulo = 0, cap_alo = 0, cap_g32 = 0, cap_vt = 0, cap_vrow = 0, cap_s2 = 0, cap_s2p = 0, cap_s3 = 0, cap_s3p = 0, cap_m = 0, cap_u = 0;
+  // graph-mode input and residual-stream buffers: a captured forward reads the
+  // mel rows from melw and works on xw, so its launches never name the
+  // caller's (pool-recycled) tensors; copies in and out run outside the graph
+  void *melw = nullptr, *xw = nullptr;
+  size_t cap_melw = 0, cap_xw = 0;
 };
 
 namespace fa {
@@ -715,7 +732,7 @@ void fa_encoder_destroy(fa_encoder *enc) {
   for (void *p : enc->allocs) (void)hipFree(p);
   for (auto &g : enc->graphs)
     if (g.exec) (void)hipGraphExecDestroy(g.exec);
-  for (void *p : {enc->hlo, enc->ulo, enc->alo, enc->g32, enc->vt, enc->vrow, enc->s2, enc->s2p, enc->s3, enc->s3p, enc->h, enc->u, enc->a, enc->g})
+  for (void *p : {enc->hlo, enc->ulo, enc->alo, enc->g32, enc->vt, enc->vrow, enc->s2, enc->s2p, enc->s3, enc->s3p, enc->h, enc->u, enc->a, enc->g, enc->melw, enc->xw})
     if (p) (void)hipFree(p);
   delete enc;
 }
@@ -1018,7 +1035,13 @@ int fa_encoder_load(fa_ctx *ctx, const fa_encoder_cfg *cfg, int n, const char *c
 int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t *lens, int n, int layout, int layers_run, fa_tensor *out) {
   if (!e || e->ctx != ctx) return set_err(ctx, FA_E_INVALID, "encoderForward: encoder belongs to another context");
   if (n <= 0) return set_err(ctx, FA_E_INVALID, "encoderForward: no windows");
-  if (n > kMaxWin) return set_err(ctx, FA_E_UNSUPPORTED, "encoderForward: %d windows in one batch (max %d)", n, kMaxWin);
+  // At most 32 windows per batch: the largest batch validated on the GPU.  A
+  // 64-window batch inside a one-hour windowed transcription once faulted the
+  // GPU with no cause shown yet, so larger batches are refused here rather
+  // than only by the Python pipeline.
+  constexpr int kMaxEncWin = 32;
+  static_assert(kMaxEncWin <= kMaxWin, "window tables");
+  if (n > kMaxEncWin) return set_err(ctx, FA_E_UNSUPPORTED, "encoderForward: %d windows in one batch (max %d)", n, kMaxEncWin);
   if (layout != 0 && layout != 1) return set_err(ctx, FA_E_INVALID, "encoderForward: layout %d", layout);
   const fa_encoder_cfg &c = e->cfg;
   const int D = c.D, C = c.Csub, MB = c.melBins;
@@ -1090,11 +1113,19 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
     if (e->ws_gen != gen) FA_HIP(ctx, hipMemsetAsync(e->vt, 0, e->cap_vt, ctx->stream));
     FA_TRY(grow(e, &e->vrow, &e->cap_vrow, (size_t)M * 4));
   }
+  const char *ge = getenv("FA_GRAPH");
+  const bool use_graph = !ctx->prof_on && !(ge && ge[0] == '0');
+  if (use_graph) {
+    FA_TRY(grow(e, &e->melw, &e->cap_melw, (size_t)R[0] * MB * 4));
+    FA_TRY(grow(e, &e->xw, &e->cap_xw, (size_t)M * D * 4));
+  }
   fa_tensor ox;
   TensorRec *rx;
   FA_TRY(new_tensor(ctx, M, D, S_F32, (size_t)M * D * 4, &ox, &rx));
   rm = get(ctx, mel);
-  float *x = (float *)rx->ptr;
+  float *const xout = (float *)rx->ptr;
+  float *x = use_graph ? (float *)e->xw : xout;
+  const float *melp = use_graph ? (const float *)e->melw : (const float *)rm->ptr;
   _Float16 *h = (_Float16 *)e->h, *u = (_Float16 *)e->u, *a = (_Float16 *)e->a, *gg = (_Float16 *)e->g;
 
   // The whole forward is a fixed kernel sequence for a given signature: it is
@@ -1104,7 +1135,7 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
   // ── subsampling ──
     {
       ProfScope ps(ctx, "sub_c01");
-      FA_TRY(launch_c01(ctx, ps, dim3(cdiv(mx[2], 4), n), (const float *)rm->ptr, MB, s0, s1, F1, s2, F2, e->c0w, e->c0b, e->c1w, e->c1b,
+      FA_TRY(launch_c01(ctx, ps, dim3(cdiv(mx[2], 4), n), melp, MB, s0, s1, F1, s2, F2, e->c0w, e->c0b, e->c1w, e->c1b,
                         (_Float16 *)e->s2, C, e->c01_lds));
       FA_TRY(check_launch(ctx, "sub_c01"));
     }
@@ -1264,13 +1295,15 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
     }
     return FA_OK;
   };
-  const char *ge = getenv("FA_GRAPH");
-  if (ctx->prof_on || (ge && ge[0] == '0')) {
+  if (!use_graph) {
     FA_TRY(launch_all());
     *out = ox;
     return FA_OK;
   }
-  std::vector<int64_t> key = {(int64_t)e->ws_gen, layers, n, layout, (int64_t)(intptr_t)rm->ptr, (int64_t)(intptr_t)x};
+  // The graph reads melw and writes xw (fixed per workspace generation), so the
+  // key holds no caller pointer: a caller that keeps earlier outputs alive
+  // still replays the same graph.
+  std::vector<int64_t> key = {(int64_t)e->ws_gen, layers, n, layout};
   key.insert(key.end(), lens, lens + n);
   fa_encoder::Captured *hit = nullptr;
   for (auto &g : e->graphs)
@@ -1289,7 +1322,7 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
     const hipError_t ie = hipGraphInstantiateWithFlags(&exec, graph, 0);
     (void)hipGraphDestroy(graph);
     if (ie != hipSuccess) return set_err(ctx, FA_E_DEVICE, "encoderForward: graph instantiate: %s", hipGetErrorString(ie));
-    constexpr size_t kMaxGraphs = 8;
+    constexpr size_t kMaxGraphs = 16;
     if (e->graphs.size() >= kMaxGraphs) {  // evict the least recently used
       size_t lru = 0;
       for (size_t i = 1; i < e->graphs.size(); i++)
@@ -1302,7 +1335,9 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
     hit = &e->graphs.back();
   }
   hit->used = ++e->graph_clock;
+  FA_TRY(copy_f4(ctx, rm->ptr, e->melw, (size_t)R[0] * MB * 4, "enc_in"));
   FA_HIP(ctx, hipGraphLaunch(hit->exec, ctx->stream));
+  FA_TRY(copy_f4(ctx, e->xw, xout, (size_t)M * D * 4, "enc_out"));
   *out = ox;
   return FA_OK;
 }

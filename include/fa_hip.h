@@ -295,6 +295,7 @@ int fa_encoder_get_exact(const fa_encoder *enc, int layer);
  * or [n*TsubMax, D] (layout 1, rows past a window's Tsub are zero) f32
  * frames.  Each window's frames equal its standalone encode: attention keys,
  * the depthwise conv and the subsampling convs never cross window bounds.
+ * 1 <= n <= 32 (FA_E_UNSUPPORTED above: the largest batch validated on the GPU).
  * layers_run < 0 runs all layers. */
 int fa_encoder_forward(fa_ctx *ctx, fa_encoder *enc, fa_tensor mel, const int32_t *lens, int n, int layout, int layers_run, fa_tensor *out);
 /* Subsampled length of a window of T mel frames (raw-encoder.js:217-218). */

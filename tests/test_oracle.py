@@ -148,6 +148,53 @@ def test_bmm_qk_pv_against_einsum(orc):
     assert np.abs(o - ref2).max() < 1e-5
 
 
+# ── int8 GEMM, SiLU, transpose (lib.rs:143-162, wasm-context.js:22,396-441) ─
+def test_matmul_int8_known_answer_layout_and_scale(orc):
+    # wq is [K, N] row-major (index k*N + n): a transposed read, a scale taken
+    # per row instead of per column or a signed/unsigned mix-up all change this
+    a = np.array([[1.0, 10.0]], np.float32)
+    wq = np.array([[1, 2, -3], [4, -128, 6]], np.int8)
+    s = np.array([1.0, 0.5, 2.0], np.float32)
+    y = orc.matmul_int8(a, wq, s, 3, 2)
+    assert y.tolist() == [[41.0, (2 - 1280) * 0.5, (-3 + 60) * 2.0]]
+    # bias then activation after the column scale (JS applies them, wasm-context.js:290-297)
+    y = orc.matmul_int8(a, wq, s, 3, 2, bias=np.array([0.0, 1000.0, -200.0], np.float32), act="relu")
+    assert y.tolist() == [[41.0, 361.0, 0.0]]
+
+
+def test_matmul_int8_against_f64_dequant(orc):
+    K, N = 200, 37
+    a = r(5, K)
+    wq = rng.integers(-127, 128, size=(K, N)).astype(np.int8)
+    s = (rng.random(N) * 0.01 + 1e-3).astype(np.float32)
+    bias = r(1, N)
+    ref = a.astype(np.float64) @ (wq.astype(np.float64) * s.astype(np.float64)) + bias.astype(np.float64)
+    got = orc.matmul_int8(a, wq, s, N, K, bias=bias)
+    assert np.abs(got - ref).max() < 2e-5 * max(1.0, np.abs(ref).max())
+    # f32 accumulate in k order, then one multiply by the scale (lib.rs:153-158)
+    acc = np.zeros((5, N), np.float32)
+    for k in range(K):
+        acc = (acc + (a[:, k:k + 1] * wq[k:k + 1, :].astype(np.float32)).astype(np.float32)).astype(np.float32)
+    assert np.array_equal(orc.matmul_int8(a, wq, s, N, K), (acc * s).astype(np.float32))
+
+
+def test_silu_against_torch(orc):
+    x = np.concatenate([r(1000, s=6.0).reshape(-1), np.array([0.0, 29.0, 31.0, -31.0, -100.0, 1e-30], np.float32)])
+    got = orc.silu(x)
+    ref = F.silu(f64(x)).numpy()
+    assert err(got, ref) < 2e-7
+    assert got[x.size - 6] == 0.0 and got[x.size - 1] == np.float32(5e-31)  # silu(0) = 0, silu(tiny) = tiny/2
+    # the reference clamps the exponent at +-30 (actf.js:19): -100 -> -100/(1+e^30)
+    assert np.isclose(got[x.size - 2], -100.0 / (1.0 + math.exp(30.0)), rtol=1e-6)
+
+
+def test_transpose_against_numpy(orc):
+    x = r(13, 7)
+    assert np.array_equal(orc.transpose(x), x.T)
+    assert np.array_equal(orc.transpose(orc.transpose(x)), x)
+    assert orc.transpose(r(1, 5)).shape == (5, 1)
+
+
 # ── quantisation formats ───────────────────────────────────────────────────
 def test_int8_quantizer_known_answers(orc):
     # column 0: max 127 -> s = 1: 63.5 rounds half-even to 64, -0.5 to -0;
