@@ -742,8 +742,6 @@ int fa_encoder_set_exact(fa_encoder *enc, int first_layer, int last_layer, unsig
   const int nl = (int)enc->L.size();
   if (first_layer < 0 || last_layer >= nl || first_layer > last_layer) return set_err(enc->ctx, FA_E_INVALID, "setExact: layers [%d, %d] of %d", first_layer, last_layer, nl);
   if (mask & ~31u) return set_err(enc->ctx, FA_E_INVALID, "setExact: unknown bits 0x%x", mask);
-  if ((mask & ~(unsigned)FA_EXACT_GLU) && enc->format != FA_W_F16)
-    return set_err(enc->ctx, FA_E_UNSUPPORTED, "setExact: two-plane operands need the f16 weight format");
   if ((mask & FA_EXACT_LN_OUT) && (enc->cfg.D % 256 || enc->cfg.D > 2048))
     return set_err(enc->ctx, FA_E_UNSUPPORTED, "setExact: exact LayerNorm output needs D a multiple of 256 (<= 2048)");
   for (int l = first_layer; l <= last_layer; l++) enc->L[l].exact = mask;
@@ -1020,7 +1018,7 @@ int fa_encoder_load(fa_ctx *ctx, const fa_encoder_cfg *cfg, int n, const char *c
   (void)hipFree(pe_d);
   (void)hipFree(ptmp);
   if (!e->c0w || !e->c0b || !e->c1w || !e->c1b || !e->c3w || !e->c3b) return fail(set_err(ctx, FA_E_OOM, "encoder load: front end"));
-  if (format == FA_W_F16) {  // default operand precision (see fa_encoder_set_exact)
+  {  // default operand precision, every weight format (see fa_encoder_set_exact)
     const int nl = (int)e->L.size();
     for (int li = 0; li < nl; li++) {
       unsigned m = li >= nl - kExactTail ? kAllExact : kCheapExact;

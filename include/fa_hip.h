@@ -276,8 +276,9 @@ void fa_encoder_destroy(fa_encoder *enc);
  * an exact f16 pair (hi = f16(v), lo = f16(v - hi)) feeding two MFMAs per
  * weight fragment, or (FA_EXACT_GLU) keeps it f32.  No counterpart in the
  * reference (its f16 route keeps f16 partial sums, gemm.js:380-391); this is
- * how the f16 encoder holds the fp32 path's frame-wise decisions.  Masks other
- * than FA_EXACT_GLU need the f16 weight format.  Layers [first, last] get `mask`. */
+ * how the f16 encoder holds the fp32 path's frame-wise decisions.  Every
+ * weight format takes every mask; the default is the same for all formats.
+ * Layers [first, last] get `mask`. */
 enum fa_exact_bits {
   FA_EXACT_LN_OUT = 1,    /* LayerNorm outputs -> FF W1, q|k|v, pw1 */
   FA_EXACT_FF_HIDDEN = 2, /* FF hidden (after SiLU) -> FF W2 */

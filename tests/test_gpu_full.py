@@ -83,12 +83,12 @@ def test_set_exact_validation(ctx, fa, full_weights):
     with pytest.raises(fa.FaError):
         enc.setExact(1, 1, 5)
     enc.close()
-    q = fa.FusedEncoder(ctx, lw, "int8", max_T=64)
-    assert q.exact(0) == 0
-    with pytest.raises(fa.FaError):
+    for fmt in ("int8", "int4"):  # quantised weights take the same masks and default
+        q = fa.FusedEncoder(ctx, lw, fmt, max_T=64)
+        assert q.exact(0) == 31 and q.exact(1) == 31
         q.setExact(1)
-    q.setExact(8)  # f32 GLU output needs no f16 weights
-    q.close()
+        assert q.exact(0) == 1
+        q.close()
 
 
 def test_config4_ragged_batch_equals_standalone(ctx, fa, full_weights):
