@@ -98,6 +98,7 @@ SIGNATURES = [
     ("fa_gemv_quant", I, [P, T, T, T, I, I, I, C.POINTER(T)]),
     ("fa_pack_windows", I, [P, T, I32P, I32P, I, I, C.POINTER(T)]),
     ("fa_mel_windows", I, [P, T, I32P, I32P, I, I, C.c_double, I, C.POINTER(T)]),
+    ("fa_mel_windows_static", I, [P, C.c_void_p, C.c_int64, I32P, I32P, I, I, C.c_double, I, C.c_void_p, C.c_int64]),
     ("fa_tdt_load", I, [P, C.POINTER(C.POINTER(C.c_float)), C.POINTER(P)]),
     ("fa_tdt_destroy", None, [P]),
     ("fa_tdt_decode", I, [P, T, I32P, I, I, I32P, I32P, I32P]),

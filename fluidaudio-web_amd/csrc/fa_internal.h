@@ -132,6 +132,10 @@ struct ProfScope {
   } while (0)
 int check_launch(fa_ctx *ctx, const char *what);
 
+// Looks up the allocation-free mel path's static device array for ctx->device
+// (once per device; mel.hip).  Called by fa_ctx_create with the device current.
+int mel_static_init(fa_ctx *ctx);
+
 inline unsigned cdiv(long a, long b) { return (unsigned)((a + b - 1) / b); }
 
 }  // namespace fa

@@ -23,6 +23,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "fa_internal.h"
@@ -289,6 +290,114 @@ static int ensure_tables(fa_ctx *ctx, int nmels) {
   return FA_OK;
 }
 
+// Launch the three stages for n windows; tab / fb / bounds are the constant
+// tables for n_mels, stats holds 2 doubles per (window, bin) for up to kMaxWin
+// windows (every slot the normalisation reads is written by mel_stats first).
+static int mel_launch(fa_ctx *ctx, const float *pcm, long nsamp, const int32_t *starts, const int32_t *lens, int n, int n_mels, double log_guard,
+                      int normalize, long total, float *y, const MelTab *tab, const float *fb, const int *bounds, double *stats) {
+  long acc = 0;
+  for (int w0 = 0; w0 < n; w0 += kMaxWin) {
+    WinTable src{}, dst{};
+    src.n = dst.n = std::min(kMaxWin, n - w0);
+    int wmx = 0;
+    for (int i = 0; i < src.n; i++) {
+      src.off[i] = starts[w0 + i];
+      src.len[i] = lens[w0 + i];
+      dst.off[i] = (int)acc;
+      dst.len[i] = lens[w0 + i] / kHop;
+      acc += dst.len[i];
+      wmx = std::max(wmx, dst.len[i]);
+    }
+    if (wmx == 0) continue;
+    {
+      ProfScope ps(ctx, "mel_frames");
+      FA_LAUNCH(ps, mel_frames_kernel, dim3(wmx, src.n), dim3(64), 0, ctx->stream, pcm, nsamp, src, dst, tab, fb, bounds, n_mels, log_guard, total, y);
+      FA_TRY(check_launch(ctx, "mel_frames"));
+    }
+    if (normalize) {
+      {
+        ProfScope ps(ctx, "mel_stats");
+        FA_LAUNCH(ps, mel_stats_kernel, dim3(cdiv(n_mels, kStatRows), dst.n), dim3(256), 0, ctx->stream, (const float *)y, dst, n_mels, total, stats);
+        FA_TRY(check_launch(ctx, "mel_stats"));
+      }
+      ProfScope ps(ctx, "mel_norm");
+      FA_LAUNCH(ps, mel_norm_kernel, dim3(cdiv(wmx, 256), n_mels, dst.n), dim3(256), 0, ctx->stream, y, dst, n_mels, total, (const double *)stats);
+      FA_TRY(check_launch(ctx, "mel_norm"));
+    }
+  }
+  return FA_OK;
+}
+
+// Window / bin / size checks shared by both entry points; returns the output
+// column count in *total.
+static int mel_check(fa_ctx *ctx, long nsamp, const int32_t *starts, const int32_t *lens, int n, int n_mels, double log_guard, long *total) {
+  if (n <= 0) return set_err(ctx, FA_E_INVALID, "melWindows: no windows");
+  if (!starts || !lens) return set_err(ctx, FA_E_INVALID, "melWindows: null window arrays");
+  if (n_mels < 1 || n_mels > kMaxMels) return set_err(ctx, FA_E_INVALID, "melWindows: %d mel bins (1..%d)", n_mels, kMaxMels);
+  if (!(log_guard >= 0)) return set_err(ctx, FA_E_INVALID, "melWindows: log guard must be >= 0");
+  long t = 0;
+  for (int i = 0; i < n; i++) {
+    if (lens[i] < 0 || starts[i] < 0 || (long)starts[i] + lens[i] > nsamp)
+      return set_err(ctx, FA_E_INVALID, "melWindows: window %d [%d, +%d) outside the %ld-sample stream", i, starts[i], lens[i], nsamp);
+    t += lens[i] / kHop;
+  }
+  if (t > 0x7fffffff / kMaxMels) return set_err(ctx, FA_E_INVALID, "melWindows: %ld frames in one call", t);
+  *total = t;
+  return FA_OK;
+}
+
+// ── allocation-free variant: one static device array per GPU ─────────────────
+// Layout: the constant tables sized for kMaxMels bins (MelTab, filterbank,
+// bounds), then the statistics of kMaxWin windows x kMaxMels bins.
+constexpr size_t kStaticTabBytes = (kTabFb + (size_t)kMaxMels * kBins * 4 + 2 * kMaxMels * 4 + 255) / 256 * 256;
+constexpr size_t kStaticStatBytes = (size_t)kMaxWin * kMaxMels * 2 * sizeof(double);
+constexpr size_t kScratchBytes = kStaticTabBytes + kStaticStatBytes;
+static_assert(kScratchBytes == 273920, "static scratch size (documented in fa_hip.h)");
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+// Per device: the array's device address (from hipGetSymbolAddress with that
+// device current; the array's host-side name is not a device address) and the
+// bin count its tables currently hold.
+constexpr int kMaxDevices = 64;
+struct StaticScratch {
+  char *ptr = nullptr;
+  int tab_mels = 0;
+};
+static StaticScratch g_static[kMaxDevices];
+static std::mutex g_static_mu;
+
+static int upload_static_tables(fa_ctx *ctx, StaticScratch &ss, int nmels) {
+  MelTab t;
+  std::vector<float> fb;
+  std::vector<int> bounds;
+  build_tables(nmels, t, fb, bounds);
+  std::vector<char> host(kTabFb + fb.size() * 4 + bounds.size() * 4);
+  std::memcpy(host.data(), &t, kTabFb);
+  std::memcpy(host.data() + kTabFb, fb.data(), fb.size() * 4);
+  std::memcpy(host.data() + kTabFb + fb.size() * 4, bounds.data(), bounds.size() * 4);
+  // earlier calls may still read the tables being replaced
+  FA_HIP(ctx, hipDeviceSynchronize());
+  FA_HIP(ctx, hipMemcpy(ss.ptr, host.data(), host.size(), hipMemcpyHostToDevice));
+  ss.tab_mels = nmels;
+  return FA_OK;
+}
+
+// Called by fa_ctx_create with ctx->device current: looks the array up once
+// per device and fills its tables for 128 bins (Parakeet's front end).
+int mel_static_init(fa_ctx *ctx) {
+  if (ctx->device < 0 || ctx->device >= kMaxDevices) return set_err(ctx, FA_E_UNSUPPORTED, "device %d beyond %d", ctx->device, kMaxDevices);
+  std::lock_guard<std::mutex> lk(g_static_mu);
+  StaticScratch &ss = g_static[ctx->device];
+  if (!ss.ptr) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return set_err(ctx, FA_E_DEVICE, "hipGetSymbolAddress(mel scratch): %s", hipGetErrorString(e));
+    ss.ptr = (char *)p;
+    FA_TRY(upload_static_tables(ctx, ss, kMaxMels));
+  }
+  return FA_OK;
+}
+
 }  // namespace fa
 
 using namespace fa;
@@ -300,19 +409,9 @@ int fa_mel_windows(fa_ctx *ctx, fa_tensor pcm, const int32_t *starts, const int3
   TensorRec *rp;
   FA_TRY(need(ctx, pcm, &rp, "melWindows"));
   if (rp->kind != S_F32) return set_err(ctx, FA_E_INVALID, "melWindows: PCM must be an f32 tensor");
-  if (n <= 0) return set_err(ctx, FA_E_INVALID, "melWindows: no windows");
-  if (n_mels < 1 || n_mels > kMaxMels) return set_err(ctx, FA_E_INVALID, "melWindows: %d mel bins (1..%d)", n_mels, kMaxMels);
-  if (!(log_guard >= 0)) return set_err(ctx, FA_E_INVALID, "melWindows: log guard must be >= 0");
   const long nsamp = (long)rp->rows * rp->cols;
   long total = 0;
-  int mx = 0;
-  for (int i = 0; i < n; i++) {
-    if (lens[i] < 0 || starts[i] < 0 || (long)starts[i] + lens[i] > nsamp)
-      return set_err(ctx, FA_E_INVALID, "melWindows: window %d [%d, +%d) outside the %ld-sample stream", i, starts[i], lens[i], nsamp);
-    total += lens[i] / kHop;
-    mx = std::max(mx, lens[i] / kHop);
-  }
-  if (total > 0x7fffffff / kMaxMels) return set_err(ctx, FA_E_INVALID, "melWindows: %ld frames in one call", total);
+  FA_TRY(mel_check(ctx, nsamp, starts, lens, n, n_mels, log_guard, &total));
   FA_TRY(ensure_tables(ctx, n_mels));
   fa_tensor o;
   TensorRec *ro;
@@ -336,41 +435,33 @@ int fa_mel_windows(fa_ctx *ctx, fa_tensor pcm, const int32_t *starts, const int3
   const MelTab *tab = (const MelTab *)ctx->mel_tab;
   const float *fb = (const float *)((const char *)ctx->mel_tab + kTabFb);
   const int *bounds = (const int *)((const char *)ctx->mel_tab + kTabFb + (size_t)n_mels * kBins * 4);
-  float *y = (float *)ro->ptr;
-  long acc = 0;
-  for (int w0 = 0; w0 < n; w0 += kMaxWin) {
-    WinTable src{}, dst{};
-    src.n = dst.n = std::min(kMaxWin, n - w0);
-    int wmx = 0;
-    for (int i = 0; i < src.n; i++) {
-      src.off[i] = starts[w0 + i];
-      src.len[i] = lens[w0 + i];
-      dst.off[i] = (int)acc;
-      dst.len[i] = lens[w0 + i] / kHop;
-      acc += dst.len[i];
-      wmx = std::max(wmx, dst.len[i]);
-    }
-    if (wmx == 0) continue;
-    {
-      ProfScope ps(ctx, "mel_frames");
-      FA_LAUNCH(ps, mel_frames_kernel, dim3(wmx, src.n), dim3(64), 0, ctx->stream, (const float *)rp->ptr, nsamp, src, dst, tab, fb, bounds, n_mels,
-                log_guard, total, y);
-      FA_TRY(check_launch(ctx, "mel_frames"));
-    }
-    if (normalize) {
-      double *st = (double *)ctx->mel_scratch;
-      {
-        ProfScope ps(ctx, "mel_stats");
-        FA_LAUNCH(ps, mel_stats_kernel, dim3(cdiv(n_mels, kStatRows), dst.n), dim3(256), 0, ctx->stream, (const float *)y, dst, n_mels, total, st);
-        FA_TRY(check_launch(ctx, "mel_stats"));
-      }
-      ProfScope ps(ctx, "mel_norm");
-      FA_LAUNCH(ps, mel_norm_kernel, dim3(cdiv(wmx, 256), n_mels, dst.n), dim3(256), 0, ctx->stream, y, dst, n_mels, total, (const double *)st);
-      FA_TRY(check_launch(ctx, "mel_norm"));
-    }
-  }
+  FA_TRY(mel_launch(ctx, (const float *)rp->ptr, nsamp, starts, lens, n, n_mels, log_guard, normalize, total, (float *)ro->ptr, tab, fb, bounds,
+                    (double *)ctx->mel_scratch));
   *out = o;
   return FA_OK;
+}
+
+int fa_mel_windows_static(fa_ctx *ctx, const float *pcm, int64_t nsamp, const int32_t *starts, const int32_t *lens, int n, int n_mels,
+                          double log_guard, int normalize, float *out, int64_t out_cols) {
+  if (!ctx) return FA_E_INVALID;
+  if (!pcm || !out) return set_err(ctx, FA_E_INVALID, "melWindowsStatic: null device pointer");
+  if (n > kMaxWin) return set_err(ctx, FA_E_UNSUPPORTED, "melWindowsStatic: %d windows in one call (the static scratch holds %d)", n, kMaxWin);
+  long total = 0;
+  FA_TRY(mel_check(ctx, (long)nsamp, starts, lens, n, n_mels, log_guard, &total));
+  if (total != out_cols) return set_err(ctx, FA_E_INVALID, "melWindowsStatic: the windows give %ld frames, out has %lld columns", total, (long long)out_cols);
+  if (ctx->device < 0 || ctx->device >= kMaxDevices || !g_static[ctx->device].ptr)
+    return set_err(ctx, FA_E_STATE, "melWindowsStatic: static scratch not set up for device %d", ctx->device);
+  StaticScratch &ss = g_static[ctx->device];
+  if (ss.tab_mels != n_mels) {  // another bin count: synchronous table upload (not capturable)
+    std::lock_guard<std::mutex> lk(g_static_mu);
+    if (ss.tab_mels != n_mels) FA_TRY(upload_static_tables(ctx, ss, n_mels));
+  }
+  if (total == 0) return FA_OK;
+  const MelTab *tab = (const MelTab *)ss.ptr;
+  const float *fb = (const float *)(ss.ptr + kTabFb);
+  const int *bounds = (const int *)(ss.ptr + kTabFb + (size_t)n_mels * kBins * 4);
+  double *stats = (double *)(ss.ptr + kStaticTabBytes);
+  return mel_launch(ctx, pcm, (long)nsamp, starts, lens, n, n_mels, log_guard, normalize, total, out, tab, fb, bounds, stats);
 }
 
 }  // extern "C"

@@ -246,6 +246,11 @@ int fa_ctx_create(int device, fa_ctx **out) {
     delete ctx;
     return FA_E_DEVICE;
   }
+  if (const int st = fa::mel_static_init(ctx)) {
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return st;
+  }
   *out = ctx;
   return FA_OK;
 }

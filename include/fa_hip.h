@@ -243,6 +243,21 @@ int fa_tdt_decode(fa_tdt *dec, fa_tensor frames, const int32_t *lens, int n, int
  * normalize 0 (Nemotron's raw log-mel, its first floor(len/160) frames). */
 int fa_mel_windows(fa_ctx *ctx, fa_tensor pcm, const int32_t *starts, const int32_t *lens, int n, int n_mels, double log_guard, int normalize,
                    fa_tensor *out);
+/* fa_mel_windows for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, hosts that forbid hipMalloc).  No
+ * counterpart in the reference.  Same arguments and results as
+ * fa_mel_windows, but the PCM (nsamp f32 samples) and the output
+ * (f32 [n_mels][out_cols], out_cols = Σ floor(lens[i]/160)) are device
+ * pointers the caller owns, and nothing is allocated: the constant tables and
+ * the per-(window, bin) statistics live in one static device array of
+ * 273,920 bytes per GPU (held until the process ends), set up by
+ * fa_ctx_create.  Limits: n <= 64 windows per call (FA_E_UNSUPPORTED above),
+ * n_mels <= 128.  The first call with an n_mels other than 128 on a device
+ * uploads that bin count's tables with a synchronous copy (make it outside
+ * graph capture).  Every call on a GPU shares the array: calls that overlap
+ * on one GPU (two streams, two contexts) race. */
+int fa_mel_windows_static(fa_ctx *ctx, const float *pcm, int64_t nsamp, const int32_t *starts, const int32_t *lens, int n, int n_mels,
+                          double log_guard, int normalize, float *out, int64_t out_cols);
 /* Row -> window index map of a batch (the index map every window-aware kernel
  * uses), computed on the device and copied to host_map: entry r is the window
  * owning row r, or -1 for a padding row.  stage 0 = mel frames, 1..3 = after
