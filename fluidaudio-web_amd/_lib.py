@@ -98,6 +98,16 @@ SIGNATURES = [
     ("fa_gemv_quant", I, [P, T, T, T, I, I, I, C.POINTER(T)]),
     ("fa_pack_windows", I, [P, T, I32P, I32P, I, I, C.POINTER(T)]),
     ("fa_mel_windows", I, [P, T, I32P, I32P, I, I, C.c_double, I, C.POINTER(T)]),
+    ("fa_leaky_relu", I, [P, T, C.c_double, C.POINTER(T)]),
+    ("fa_snake", I, [P, T, T, C.POINTER(T)]),
+    ("fa_adain", I, [P, T, T, T, C.c_double, C.POINTER(T)]),
+    ("fa_im2col", I, [P, T, I, I, I, I, C.POINTER(T)]),
+    ("fa_conv_transpose1d", I, [P, T, T, I, I, T, I, I, I, I, I, I, C.POINTER(T)]),
+    ("fa_gather_cols", I, [P, T, C.POINTER(C.c_uint32), I, C.POINTER(T)]),
+    ("fa_lstm", I, [P, T, T, T, T, I, C.POINTER(T)]),
+    ("fa_jbatch", I, [P, T, I, I, T, I, C.POINTER(T)]),
+    ("fa_argmax_rows", I, [P, T, I, I, I, C.POINTER(T)]),
+    ("fa_joint_argmax", I, [P, T, I, I, T, T, T, I, I, I, C.POINTER(T)]),
     ("fa_mel_windows_static", I, [P, C.c_void_p, C.c_int64, I32P, I32P, I, I, C.c_double, I, C.c_void_p, C.c_int64]),
     ("fa_tdt_load", I, [P, C.POINTER(C.POINTER(C.c_float)), C.POINTER(P)]),
     ("fa_tdt_destroy", None, [P]),

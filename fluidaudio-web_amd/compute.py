@@ -11,10 +11,10 @@ code written against GpuContext/WasmContext reads the same:
     (buffer-pool.js:49-126);
   - beginBatch() nests -> error; stageDownload().read() is single-use;
   - misuse raises FaError (the reference throws Error).
-Methods that belong to the TTS and decoder engines (lstm, snake, adain,
-convTranspose1d, im2col, conv1dGemm/conv1dFast*, gatherCols, leakyRelu,
-jbatch, argmaxRows, jointArgmax) are outside this backend's
-scope and raise NotImplementedError naming the op.
+Every required member of the d.ts is implemented; the TTS and decoder-side
+ops (lstm, snake, adain, convTranspose1d, im2col, conv1dGemm/conv1dFast*,
+gatherCols, leakyRelu, jbatch, argmaxRows, jointArgmax) are plain kernels with
+the CPU backend's arithmetic (wasm-context.js), off the encoder's hot path.
 """
 from __future__ import annotations
 
@@ -59,10 +59,6 @@ class StagedRead:
         out = np.empty(self._n, np.float32)
         check(self._ctx._p, lib().fa_staged_read(self._ctx._p, self._h, out.ctypes.data_as(L.F32P)))
         return out
-
-
-_UNSUPPORTED = ("lstm", "snake", "adain", "convTranspose1d", "im2col", "conv1dGemm", "conv1dFast", "conv1dFastF16", "gatherCols",
-                "leakyRelu", "jbatch", "argmaxRows", "jointArgmax")
 
 
 def _f32(a):
@@ -394,6 +390,67 @@ class HipContext:
         check(self._p, lib().fa_row_bias_act(self._p, x.h, bias.h, ACT[act], C.byref(o)))
         return HipTensor(self, o.value, x.rows, x.cols)
 
+    # ── TTS / decoder-side members (compute.d.ts:174-234) ──────────────────
+    def leakyRelu(self, x, slope=0.2):
+        return self._unary(lib().fa_leaky_relu, x, C.c_double(slope))
+
+    def snake(self, x, alpha):
+        return self._unary(lib().fa_snake, x, alpha.h)
+
+    def adain(self, x, scale, shift, eps=1e-5):
+        return self._unary(lib().fa_adain, x, scale.h, shift.h, C.c_double(eps))
+
+    def im2col(self, x, k, stride=1, pad=0, dilation=1):
+        o = self._out()
+        check(self._p, lib().fa_im2col(self._p, x.h, k, stride, pad, dilation, C.byref(o)))
+        return self._t(o.value)
+
+    def conv1dGemm(self, x, wRows, cout, k, stride=1, pad=0, dilation=1, act="none"):
+        """wasm-context.js:286-288: matmul(wRows [Cout, Cin*k], im2col(x))."""
+        cols = self.im2col(x, k, stride=stride, pad=pad, dilation=dilation)
+        y = self.matmul(wRows, cols, act=act)
+        self.freeTensor(cols)
+        return y
+
+    def conv1dFast(self, x, wRows, cout, k, **opts):
+        """wasm-context.js:265-267: conv1d with wRows as the [Cout, Cin*k] weight."""
+        return self.conv1d(x, wRows, cout, k, **opts)
+
+    def conv1dFastF16(self, x, wRows, cout, k, **opts):
+        return self.conv1d(x, wRows, cout, k, **opts)
+
+    def convTranspose1d(self, x, w, cout, k, bias=None, stride=1, pad=0, dilation=1, groups=1, outputPadding=0, act="none"):
+        o = self._out()
+        check(self._p, lib().fa_conv_transpose1d(self._p, x.h, w.h, cout, k, self._h(bias), stride, pad, dilation, groups, outputPadding,
+                                                 ACT[act], C.byref(o)))
+        return self._t(o.value)
+
+    def gatherCols(self, x, idxMap):
+        idx = np.ascontiguousarray(idxMap, np.uint32)
+        o = self._out()
+        check(self._p, lib().fa_gather_cols(self._p, x.h, idx.ctypes.data_as(C.POINTER(C.c_uint32)), len(idx), C.byref(o)))
+        return HipTensor(self, o.value, x.rows, len(idx))
+
+    def lstm(self, x, w, r, b, hid):
+        o = self._out()
+        check(self._p, lib().fa_lstm(self._p, x.h, w.h, r.h, b.h, hid, C.byref(o)))
+        return HipTensor(self, o.value, x.rows, 2 * hid)
+
+    def jbatch(self, encProj, base, B, predProj, hid):
+        o = self._out()
+        check(self._p, lib().fa_jbatch(self._p, encProj.h, base, B, predProj.h, hid, C.byref(o)))
+        return HipTensor(self, o.value, B, hid)
+
+    def argmaxRows(self, x, B, vocab, logits):
+        o = self._out()
+        check(self._p, lib().fa_argmax_rows(self._p, x.h, B, vocab, logits, C.byref(o)))
+        return HipTensor(self, o.value, B, 4)
+
+    def jointArgmax(self, encProj, frame, count, predProj, outW, outB, hidden, vocab, logits):
+        o = self._out()
+        check(self._p, lib().fa_joint_argmax(self._p, encProj.h, frame, count, predProj.h, outW.h, outB.h, hidden, vocab, logits, C.byref(o)))
+        return HipTensor(self, o.value, count, 4)
+
     # ── profiling (compute.d.ts:250-251) ──────────────────────────────────
     def startProfile(self, maxOps=4096, only=None):
         """Bracket launches with HIP events; `only` restricts it to a comma-separated
@@ -456,10 +513,6 @@ class HipContext:
         check(self._p, lib().fa_window_row_map(self._p, l.ctypes.data_as(L.I32P), len(l), lay, stage, m.ctypes.data_as(L.I32P), C.byref(rows)))
         return m
 
-    def __getattr__(self, name):
-        if name in _UNSUPPORTED:
-            raise NotImplementedError(f"HipContext.{name}: TTS/decoder op outside this backend's encoder scope")
-        raise AttributeError(name)
 
 
 def createContext(backend: str = "hip", device: int = 0) -> HipContext:

@@ -10,7 +10,4 @@ int layernorm_launch(fa_ctx *ctx, const float *x, const float *g, const float *b
                      float eps, const char *label);
 int gemv_quant_launch(fa_ctx *ctx, const float *A, const void *W, const void *scales, int format, int M, int N, int K, float *Y, const float *bias,
                       int act, const char *label);
-int gemv_nbits_launch(fa_ctx *ctx, const float *A, const uint8_t *bq, const float *scales, const uint8_t *zp, int zpb, int M, int N, int K, float *Y,
-                      const char *label);
-
 }  // namespace fa

@@ -286,6 +286,31 @@ __global__ void dequant_i4_kernel(const uint8_t *bq, const _Float16 *s, float *w
   }
 }
 
+// f16 tensor -> f32 row-major [rows, cols]: row-major (allocF16) or K-major
+// (uploadF16: element (r, c) at c * rows + r).
+__global__ void f16_to_f32_rows_kernel(const _Float16 *src, float *dst, int rows, int cols, int kmajor) {
+  const long n = (long)rows * cols;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
+    const int r = (int)(i / cols), c = (int)(i % cols);
+    dst[i] = (float)src[kmajor ? (size_t)c * rows + r : (size_t)i];
+  }
+}
+
+// ONNX MatMulNBits weights (bits 4, block 32; gemm.js:893-919) -> f32 [K, N]:
+// (q - zp) * s exactly as the reference kernel dequantises in f32.
+__global__ void nbits_dequant_f32_kernel(const uint8_t *bq, const float *scales, const uint8_t *zp, int zpb, int K, int N, float *w) {
+  const long n_el = (long)K * N;
+  const int nblk = (K + 31) / 32;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n_el; i += (long)gridDim.x * 256) {
+    const int k = (int)(i / N), n = (int)(i % N), b = k >> 5, t = k & 31;
+    const uint8_t byte = bq[((size_t)n * nblk + b) * 16 + (t >> 1)];
+    const float q = (float)((t & 1) ? (byte >> 4) : (byte & 0xf));
+    const uint8_t zb = zp[(size_t)n * zpb + (b >> 1)];
+    const float z = (float)((b & 1) ? (zb >> 4) : (zb & 0xf));
+    w[i] = (q - z) * scales[(size_t)n * nblk + b];
+  }
+}
+
 static inline unsigned gs(long n) {
   long b = (n + 255) / 256;
   return (unsigned)(b < 1 ? 1 : (b > 65535 * 4 ? 65535 * 4 : b));
@@ -304,9 +329,44 @@ static int need_f32(fa_ctx *ctx, TensorRec *r, const char *what) {
   return FA_OK;
 }
 
+// An f32 view of an operand for the ops whose kernels read f32: f16 tensors
+// (uploadF16 / allocF16, the reference's f16-storage tensors) are widened
+// into a pooled temporary (*tmp, freed by the caller after its launch).
+static int as_f32(fa_ctx *ctx, fa_tensor t, fa_tensor *use, fa_tensor *tmp, const char *what) {
+  TensorRec *r;
+  *tmp = 0;
+  *use = t;
+  FA_TRY(need(ctx, t, &r, what));
+  if (r->kind == S_F32) return FA_OK;
+  if (r->kind != S_F16KM && r->kind != S_F16RM) return set_err(ctx, FA_E_INVALID, "%s: expected an f32 or f16 tensor", what);
+  TensorRec *ro;
+  FA_TRY(new_tensor(ctx, r->rows, r->cols, S_F32, (size_t)r->rows * r->cols * 4, tmp, &ro));
+  r = get(ctx, t);
+  const long n = (long)r->rows * r->cols;
+  if (n) hipLaunchKernelGGL(f16_to_f32_rows_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, (const _Float16 *)r->ptr, F32(ro), r->rows, r->cols,
+                           r->kind == S_F16KM ? 1 : 0);
+  FA_TRY(check_launch(ctx, what));
+  *use = *tmp;
+  return FA_OK;
+}
+
 extern "C" {
 
+static int matmul_impl(fa_ctx *ctx, fa_tensor a, fa_tensor b, fa_tensor bias, int act, fa_tensor add, fa_tensor *out);
 int fa_matmul(fa_ctx *ctx, fa_tensor a, fa_tensor b, fa_tensor bias, int act, fa_tensor add, fa_tensor *out) {
+  TensorRec *ra;
+  FA_TRY(need(ctx, a, &ra, "matmul"));
+  if (ra->kind != S_F16KM) return matmul_impl(ctx, a, b, bias, act, add, out);
+  // A uploaded as an f16 weight (matmulF16 with f16 a, compute.d.ts:164):
+  // widened to f32 rows, then the route of its B
+  fa_tensor a32, tmp;
+  FA_TRY(as_f32(ctx, a, &a32, &tmp, "matmul A"));
+  const int st = matmul_impl(ctx, a32, b, bias, act, add, out);
+  (void)fa_free_tensor(ctx, tmp);
+  return st;
+}
+
+static int matmul_impl(fa_ctx *ctx, fa_tensor a, fa_tensor b, fa_tensor bias, int act, fa_tensor add, fa_tensor *out) {
   TensorRec *ra, *rb, *rbias, *radd;
   FA_TRY(need(ctx, a, &ra, "matmul"));
   FA_TRY(need(ctx, b, &rb, "matmul"));
@@ -428,19 +488,23 @@ int fa_matmul_nbits(fa_ctx *ctx, fa_tensor a, fa_tensor bq, fa_tensor scales, fa
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, M, N, S_F32, (size_t)M * N * 4, &o, &ro));
-  ra = get(ctx, a); rq = get(ctx, bq); rs = get(ctx, scales); rz = get(ctx, zp);
-  if (M <= 64 || K % 64 != 0) {
-    FA_TRY(gemv_nbits_launch(ctx, F32(ra), (const uint8_t *)rq->ptr, F32(rs), (const uint8_t *)rz->ptr, zpb, M, N, K, F32(ro), "matmulNBits_gemv"));
-  } else {
-    GemmArgs p;
-    p.A = ra->ptr; p.lda = K; p.akind = A_F32;
-    p.B = rq->ptr; p.bkind = B_I4;
-    p.bscale = rs->ptr; p.bscale_f32 = 1;
-    p.bzp = (const uint8_t *)rz->ptr; p.zpb = zpb;
-    p.C = ro->ptr; p.ldc = N;
-    p.M = M; p.N = N; p.K = K;
-    FA_TRY(gemm_mfma(ctx, p, "matmulNBits"));
+  if ((long)rs->rows * rs->cols < (long)N * nblk || rz->bytes < (size_t)N * zpb) return set_err(ctx, FA_E_INVALID, "matmulNBits: scales / zero points too small");
+  // The reference's kernel dequantises in f32 (arbitrary f32 block scales and
+  // zero points): the weights are expanded to f32 [K, N] once per call and
+  // multiplied on the fp32 MFMA route, so results carry f32 accuracy.  (The
+  // encoder's own int4 format runs fused in its f16 GEMMs instead.)
+  fa_tensor tw;
+  TensorRec *rw;
+  FA_TRY(new_tensor(ctx, K, N, S_F32, (size_t)K * N * 4, &tw, &rw));
+  ra = get(ctx, a); rq = get(ctx, bq); rs = get(ctx, scales); rz = get(ctx, zp); ro = get(ctx, o);
+  {
+    ProfScope ps(ctx, "matmulNBits_dequant");
+    FA_LAUNCH(ps, nbits_dequant_f32_kernel, dim3(gs((long)K * N)), dim3(256), 0, ctx->stream, (const uint8_t *)rq->ptr, F32(rs), (const uint8_t *)rz->ptr,
+              zpb, K, N, F32(rw));
+    FA_TRY(check_launch(ctx, "matmulNBits_dequant"));
   }
+  FA_TRY(gemm_f32(ctx, F32(ra), F32(rw), F32(ro), nullptr, nullptr, M, N, K, 0, "matmulNBits"));
+  FA_TRY(fa_free_tensor(ctx, tw));
   *out = o;
   return FA_OK;
 }
@@ -667,8 +731,22 @@ int fa_row_bias_act(fa_ctx *ctx, fa_tensor x, fa_tensor bias, int act, fa_tensor
   return FA_OK;
 }
 
+static int conv1d_impl(fa_ctx *ctx, fa_tensor x, fa_tensor w, int cout, int k, fa_tensor bias, int stride, int pad_left, int pad_right, int dilation,
+                       int groups, int act, fa_tensor *out);
 int fa_conv1d(fa_ctx *ctx, fa_tensor x, fa_tensor w, int cout, int k, fa_tensor bias, int stride, int pad_left, int pad_right, int dilation,
               int groups, int act, fa_tensor *out) {
+  // f16-storage operands (conv1dFastF16 with uploadF16 tensors) are widened to f32
+  fa_tensor x32, w32, tx, tw;
+  FA_TRY(as_f32(ctx, x, &x32, &tx, "conv1d x"));
+  int st = as_f32(ctx, w, &w32, &tw, "conv1d w");
+  if (!st) st = conv1d_impl(ctx, x32, w32, cout, k, bias, stride, pad_left, pad_right, dilation, groups, act, out);
+  if (tx) (void)fa_free_tensor(ctx, tx);
+  if (tw) (void)fa_free_tensor(ctx, tw);
+  return st;
+}
+
+static int conv1d_impl(fa_ctx *ctx, fa_tensor x, fa_tensor w, int cout, int k, fa_tensor bias, int stride, int pad_left, int pad_right, int dilation,
+                       int groups, int act, fa_tensor *out) {
   TensorRec *rx, *rw, *rb;
   FA_TRY(need(ctx, x, &rx, "conv1d"));
   FA_TRY(need(ctx, w, &rw, "conv1d w"));

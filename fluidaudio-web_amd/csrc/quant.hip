@@ -212,11 +212,6 @@ int gemv_quant_launch(fa_ctx *ctx, const float *A, const void *W, const void *sc
   return gemv_launch(ctx, p, format, label);
 }
 
-int gemv_nbits_launch(fa_ctx *ctx, const float *A, const uint8_t *bq, const float *scales, const uint8_t *zp, int zpb, int M, int N, int K, float *Y,
-                      const char *label) {
-  GemvArgs p{A, M, K, N, bq, scales, zp, zpb, Y, nullptr, 0};
-  return gemv_launch(ctx, p, 3, label);
-}
 
 }  // namespace fa
 

@@ -87,6 +87,19 @@ static void *typed(napi_env env, napi_value v, size_t *len_bytes) {
   return data;
 }
 
+/* A TypedArray of exactly the expected element type (NULL otherwise): the
+ * C ABI reinterprets the bytes, so an Int32Array passed where floats are
+ * expected must be refused, not reinterpreted. */
+static void *typed_as(napi_env env, napi_value v, napi_typedarray_type want, size_t *len_bytes) {
+  napi_typedarray_type t;
+  size_t len, off;
+  void *data;
+  napi_value ab;
+  if (napi_get_typedarray_info(env, v, &t, &len, &data, &ab, &off) != napi_ok || t != want) return NULL;
+  if (len_bytes) *len_bytes = len * (want == napi_float64_array ? 8 : (want == napi_uint8_array || want == napi_int8_array) ? 1 : 4);
+  return data;
+}
+
 /* ── lifecycle ──────────────────────────────────────────────────────────── */
 static napi_value js_ctx_create(napi_env env, napi_callback_info info) {
   napi_value a[MAXA];
@@ -124,7 +137,7 @@ static napi_value up_common(napi_env env, napi_callback_info info, int f16) {
   if (!args(env, info, 4, a)) return NULL;
   fa_ctx *c = ext(env, a[0]);
   size_t nb = 0;
-  float *d = typed(env, a[1], &nb);
+  float *d = typed_as(env, a[1], napi_float32_array, &nb);
   int rows = i32(env, a[2]), cols = i32(env, a[3]);
   if (!d || nb < (size_t)rows * cols * 4) {
     napi_throw_range_error(env, NULL, "upload: Float32Array shorter than rows*cols");
@@ -264,6 +277,32 @@ FN(js_copy_rows, 4, RET_VOID(fa_copy_rows(c, T(1), T(2), I(3))))
 FN(js_sub_reshape, 5, RET_T(fa_sub_reshape(c, T(1), I(2), I(3), I(4), &_o)))
 FN(js_row_bias_act, 4, RET_T(fa_row_bias_act(c, T(1), T(2), I(3), &_o)))
 FN(js_profile_start, 2, RET_VOID(fa_profile_start(c, I(1))))
+/* the remaining required ComputeContext members (compute.d.ts:174-234) */
+FN(js_leaky_relu, 3, RET_T(fa_leaky_relu(c, T(1), f64(env, a[2]), &_o)))
+FN(js_snake, 3, RET_T(fa_snake(c, T(1), T(2), &_o)))
+FN(js_adain, 5, RET_T(fa_adain(c, T(1), T(2), T(3), f64(env, a[4]), &_o)))
+FN(js_im2col, 6, RET_T(fa_im2col(c, T(1), I(2), I(3), I(4), I(5), &_o)))
+FN(js_conv_transpose1d, 12, RET_T(fa_conv_transpose1d(c, T(1), T(2), I(3), I(4), T(5), I(6), I(7), I(8), I(9), I(10), I(11), &_o)))
+FN(js_lstm, 6, RET_T(fa_lstm(c, T(1), T(2), T(3), T(4), I(5), &_o)))
+FN(js_jbatch, 6, RET_T(fa_jbatch(c, T(1), I(2), I(3), T(4), I(5), &_o)))
+FN(js_argmax_rows, 5, RET_T(fa_argmax_rows(c, T(1), I(2), I(3), I(4), &_o)))
+FN(js_joint_argmax, 10, RET_T(fa_joint_argmax(c, T(1), I(2), I(3), T(4), T(5), T(6), I(7), I(8), I(9), &_o)))
+
+/* gatherCols(ctx, x, Uint32Array idx) */
+static napi_value js_gather_cols(napi_env env, napi_callback_info info) {
+  napi_value a[MAXA];
+  if (!args(env, info, 3, a)) return NULL;
+  CTX;
+  size_t nb = 0;
+  const uint32_t *idx = typed_as(env, a[2], napi_uint32_array, &nb);
+  if (!idx) {
+    napi_throw_type_error(env, NULL, "gatherCols: idxMap must be a Uint32Array");
+    return NULL;
+  }
+  fa_tensor o = 0;
+  int st = fa_gather_cols(c, T(1), idx, (int)(nb / 4), &o);
+  return st ? throw_status(env, c, st) : mkbig(env, o);
+}
 
 static napi_value js_concat_rows(napi_env env, napi_callback_info info) {
   napi_value a[MAXA];
@@ -318,7 +357,7 @@ static napi_value js_pack_windows(napi_env env, napi_callback_info info) {
   if (!args(env, info, 5, a)) return NULL;
   CTX;
   size_t nb1 = 0, nb2 = 0;
-  int32_t *starts = typed(env, a[2], &nb1), *lens = typed(env, a[3], &nb2);
+  int32_t *starts = typed_as(env, a[2], napi_int32_array, &nb1), *lens = typed_as(env, a[3], napi_int32_array, &nb2);
   if (!starts || !lens || nb1 != nb2) {
     napi_throw_type_error(env, NULL, "packWindows: starts/lens must be Int32Arrays of one length");
     return NULL;
@@ -334,7 +373,7 @@ static napi_value js_mel_windows(napi_env env, napi_callback_info info) {
   if (!args(env, info, 7, a)) return NULL;
   CTX;
   size_t nb1 = 0, nb2 = 0;
-  int32_t *starts = typed(env, a[2], &nb1), *lens = typed(env, a[3], &nb2);
+  int32_t *starts = typed_as(env, a[2], napi_int32_array, &nb1), *lens = typed_as(env, a[3], napi_int32_array, &nb2);
   if (!starts || !lens || nb1 != nb2) {
     napi_throw_type_error(env, NULL, "melWindows: starts/lens must be Int32Arrays of one length");
     return NULL;
@@ -354,11 +393,20 @@ static napi_value js_tdt_load(napi_env env, napi_callback_info info) {
   napi_value a[MAXA];
   if (!args(env, info, 2, a)) return NULL;
   CTX;
+  /* element counts fa_tdt_load reads (the decoder manifest's shapes) */
+  static const size_t want[11] = {8193u * 640, 2560u * 640, 2560u * 640, 5120, 2560u * 640, 2560u * 640, 5120, 640u * 640, 640, 640u * 8198, 8198};
   const float *w[11];
   for (uint32_t i = 0; i < 11; i++) {
     napi_value d;
     NA(napi_get_element(env, a[1], i, &d));
-    w[i] = typed(env, d, NULL);
+    size_t nb = 0;
+    w[i] = typed_as(env, d, napi_float32_array, &nb);
+    if (!w[i] || nb != want[i] * 4) {
+      char m[160];
+      snprintf(m, sizeof m, "tdtLoad: weight %u must be a Float32Array of %zu values", i, want[i]);
+      napi_throw_type_error(env, NULL, m);
+      return NULL;
+    }
   }
   fa_tdt *dec = NULL;
   int st = fa_tdt_load(c, w, &dec);
@@ -374,7 +422,8 @@ static napi_value js_tdt_decode(napi_env env, napi_callback_info info) {
   if (!args(env, info, 8, a)) return NULL;
   CTX;
   size_t nl = 0, ni = 0, nf = 0, nc = 0;
-  int32_t *lens = typed(env, a[3], &nl), *ids = typed(env, a[5], &ni), *fr = typed(env, a[6], &nf), *cnt = typed(env, a[7], &nc);
+  int32_t *lens = typed_as(env, a[3], napi_int32_array, &nl), *ids = typed_as(env, a[5], napi_int32_array, &ni), *fr = typed_as(env, a[6], napi_int32_array, &nf),
+          *cnt = typed_as(env, a[7], napi_int32_array, &nc);
   const int n = (int)(nl / 4), cap = I(4);
   if (!lens || !ids || !fr || !cnt || cap <= 0 || ni < (size_t)n * cap * 4 || nf < ni || nc < (size_t)n * 4) {
     napi_throw_type_error(env, NULL, "tdtDecode: lens / ids / frameIdx / counts must be Int32Arrays of n, n*cap, n*cap, n");
@@ -407,7 +456,12 @@ static napi_value js_encoder_load(napi_env env, napi_callback_info info) {
   napi_value a[MAXA];
   if (!args(env, info, 6, a)) return NULL;
   CTX;
-  int32_t *cf = typed(env, a[1], NULL);
+  size_t cfb = 0;
+  int32_t *cf = typed_as(env, a[1], napi_int32_array, &cfb);
+  if (!cf || cfb < 9 * 4) {
+    napi_throw_type_error(env, NULL, "encoderLoad: cfg must be an Int32Array of 9 values");
+    return NULL;
+  }
   fa_encoder_cfg cfg = {cf[0], cf[1], cf[2], cf[3], cf[4], cf[5], cf[6], cf[7], cf[8]};
   uint32_t n = 0;
   NA(napi_get_array_length(env, a[2], &n));
@@ -422,8 +476,16 @@ static napi_value js_encoder_load(napi_env env, napi_callback_info info) {
     names[i] = malloc(len + 1);
     NA(napi_get_value_string_utf8(env, s, names[i], len + 1, &len));
     NA(napi_get_element(env, a[3], i, &d));
-    data[i] = typed(env, d, &nb);
+    data[i] = typed_as(env, d, napi_float32_array, &nb);
     counts[i] = (int64_t)(nb / 4);
+    if (!data[i]) {
+      for (uint32_t j = 0; j <= i; j++) free(names[j]);
+      free(names);
+      free(data);
+      free(counts);
+      napi_throw_type_error(env, NULL, "encoderLoad: every weight must be a Float32Array");
+      return NULL;
+    }
   }
   fa_encoder *e = NULL;
   int st = fa_encoder_load(c, &cfg, (int)n, (const char *const *)names, data, counts, I(4), I(5), &e);
@@ -443,7 +505,11 @@ static napi_value js_encoder_forward(napi_env env, napi_callback_info info) {
   if (!args(env, info, 6, a)) return NULL;
   CTX;
   size_t nb = 0;
-  int32_t *lens = typed(env, a[3], &nb);
+  int32_t *lens = typed_as(env, a[3], napi_int32_array, &nb);
+  if (!lens) {
+    napi_throw_type_error(env, NULL, "encoderForward: lens must be an Int32Array");
+    return NULL;
+  }
   fa_tensor o = 0;
   int st = fa_encoder_forward(c, ext(env, a[1]), T(2), lens, (int)(nb / 4), I(4), I(5), &o);
   return st ? throw_status(env, c, st) : mkbig(env, o);
@@ -482,6 +548,9 @@ static napi_value init(napi_env env, napi_value exports) {
       EXPORT("profileStart", js_profile_start), EXPORT("profileEnd", js_profile_end), EXPORT("packWindows", js_pack_windows), EXPORT("melWindows", js_mel_windows),
       EXPORT("encoderLoad", js_encoder_load), EXPORT("encoderForward", js_encoder_forward), EXPORT("encoderDestroy", js_encoder_destroy),
       EXPORT("encoderTsub", js_encoder_tsub), EXPORT("tdtLoad", js_tdt_load), EXPORT("tdtDecode", js_tdt_decode), EXPORT("tdtDestroy", js_tdt_destroy),
+      EXPORT("leakyRelu", js_leaky_relu), EXPORT("snake", js_snake), EXPORT("adain", js_adain), EXPORT("im2col", js_im2col),
+      EXPORT("convTranspose1d", js_conv_transpose1d), EXPORT("gatherCols", js_gather_cols), EXPORT("lstm", js_lstm), EXPORT("jbatch", js_jbatch),
+      EXPORT("argmaxRows", js_argmax_rows), EXPORT("jointArgmax", js_joint_argmax),
   };
   napi_define_properties(env, exports, sizeof d / sizeof d[0], d);
   return exports;

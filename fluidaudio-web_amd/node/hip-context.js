@@ -221,6 +221,51 @@ class HipContext {
   rowBiasAct(x, bias, act = "none") {
     return this._t(addon.rowBiasAct(this.ctx, x.h, bias.h, ACT[act]), x.rows, x.cols);
   }
+  // ── TTS / decoder-side members (compute.d.ts:174-234) ──
+  leakyRelu(x, slope = 0.2) {
+    return this._t(addon.leakyRelu(this.ctx, x.h, slope), x.rows, x.cols);
+  }
+  snake(x, alpha) {
+    return this._t(addon.snake(this.ctx, x.h, alpha.h), x.rows, x.cols);
+  }
+  adain(x, scale, shift, eps = 1e-5) {
+    return this._t(addon.adain(this.ctx, x.h, scale.h, shift.h, eps), x.rows, x.cols);
+  }
+  im2col(x, k, { stride = 1, pad = 0, dilation = 1 } = {}) {
+    return this._info(addon.im2col(this.ctx, x.h, k, stride, pad, dilation));
+  }
+  /** matmul(wRows [Cout, Cin*k], im2col(x)) (wasm-context.js:286-288). */
+  conv1dGemm(x, wRows, cout, k, { stride = 1, pad = 0, dilation = 1, act = "none" } = {}) {
+    const cols = this.im2col(x, k, { stride, pad, dilation });
+    const y = this.matmul(wRows, cols, { act });
+    this.freeTensor(cols);
+    return y;
+  }
+  conv1dFast(x, wRows, cout, k, opts = {}) {
+    return this.conv1d(x, wRows, Object.assign({}, opts, { cout, k }));
+  }
+  conv1dFastF16(x, wRows, cout, k, opts = {}) {
+    return this.conv1d(x, wRows, Object.assign({}, opts, { cout, k }));
+  }
+  convTranspose1d(x, w, { cout, k, bias = null, stride = 1, pad = 0, dilation = 1, groups = 1, outputPadding = 0, act = "none" } = {}) {
+    return this._info(addon.convTranspose1d(this.ctx, x.h, w.h, cout, k, h(bias), stride, pad, dilation, groups, outputPadding, ACT[act]));
+  }
+  gatherCols(x, idxMap) {
+    const idx = idxMap instanceof Uint32Array ? idxMap : Uint32Array.from(idxMap);
+    return this._t(addon.gatherCols(this.ctx, x.h, idx), x.rows, idx.length);
+  }
+  lstm(x, w, r, b, hid) {
+    return this._t(addon.lstm(this.ctx, x.h, w.h, r.h, b.h, hid), x.rows, 2 * hid);
+  }
+  jbatch(encProj, base, B, predProj, hid) {
+    return this._t(addon.jbatch(this.ctx, encProj.h, base, B, predProj.h, hid), B, hid);
+  }
+  argmaxRows(x, B, vocab, logits) {
+    return this._t(addon.argmaxRows(this.ctx, x.h, B, vocab, logits), B, 4);
+  }
+  jointArgmax(encProj, frame, count, predProj, outW, outB, hidden, vocab, logits) {
+    return this._t(addon.jointArgmax(this.ctx, encProj.h, frame, count, predProj.h, outW.h, outB.h, hidden, vocab, logits), count, 4);
+  }
   // ── profiling ──
   startProfile(maxOps = 4096) {
     addon.profileStart(this.ctx, maxOps);
@@ -228,16 +273,16 @@ class HipContext {
   async endProfile() {
     return addon.profileEnd(this.ctx);
   }
-  // ── fused encoder (one native call per window batch) ──
+  // ── fused encoder (one native call per window batch; backend-private, so _-prefixed) ──
   /** man: {name: {data: Float32Array, dims}} in the reference manifest naming. */
-  loadFusedEncoder(man, cfg, { format = "f16", maxT = 512 } = {}) {
+  _loadFusedEncoder(man, cfg, { format = "f16", maxT = 512 } = {}) {
     const names = Object.keys(man);
     const c = Int32Array.from(["D", "DFF", "H", "HD", "layers", "dwK", "Csub", "Fsub", "melBins"].map((k) => cfg[k]));
     const enc = addon.encoderLoad(this.ctx, c, names, names.map((k) => man[k].data), { f16: 0, int8: 1, int4: 2 }[format], maxT);
     return { enc, cfg };
   }
   /** Encode windows (list of Float32Array [melBins*T] channel-major) -> frames tensor [ΣTsub, D]. */
-  encodeFused(fused, mels, layout = "packed") {
+  _encodeFused(fused, mels, layout = "packed") {
     const mb = fused.cfg.melBins;
     const lens = Int32Array.from(mels.map((m) => m.length / mb));
     const total = lens.reduce((a, b) => a + b, 0);
@@ -285,7 +330,7 @@ class HipContext {
   _destroyTdtDecoder(d) {
     addon.tdtDestroy(d.dec);
   }
-  destroyFusedEncoder(fused) {
+  _destroyFusedEncoder(fused) {
     addon.encoderDestroy(fused.enc);
   }
 }

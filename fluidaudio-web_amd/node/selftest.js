@@ -90,15 +90,15 @@ const check = (name, d, tol) => {
   add_("L0_pw2", 256 * 256, 0.04);
   add_("L0_dw", 256 * 9, 1);
   add_("L0_dwb", 256, 0.04);
-  const fused = ctx.loadFusedEncoder(man, cfg, { maxT: 64 });
+  const fused = ctx._loadFusedEncoder(man, cfg, { maxT: 64 });
   const mels = [mk(128 * 300, 2), mk(128 * 97, 2)];
-  const batch = await ctx.download(ctx.encodeFused(fused, mels));
+  const batch = await ctx.download(ctx._encodeFused(fused, mels));
   const t0 = encoderTsub(300);
-  const alone0 = await ctx.download(ctx.encodeFused(fused, [mels[0]]));
-  const alone1 = await ctx.download(ctx.encodeFused(fused, [mels[1]]));
+  const alone0 = await ctx.download(ctx._encodeFused(fused, [mels[0]]));
+  const alone1 = await ctx.download(ctx._encodeFused(fused, [mels[1]]));
   check("fused encoder window 0 packed == alone", maxdiff(batch.subarray(0, t0 * 256), alone0), 1e-4);
   check("fused encoder window 1 packed == alone", maxdiff(batch.subarray(t0 * 256), alone1), 1e-4);
-  ctx.destroyFusedEncoder(fused);
+  ctx._destroyFusedEncoder(fused);
   // log-mel front end: windows of one stream == each window alone; silence -> 0
   const pcmH = mk(16000 * 3, 0.2);
   const pcm = ctx.upload(pcmH, 1, pcmH.length);

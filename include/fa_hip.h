@@ -152,6 +152,35 @@ int fa_concat_rows(fa_ctx *ctx, const fa_tensor *ts, int n, fa_tensor *out);
 int fa_sub_reshape(fa_ctx *ctx, fa_tensor x, int C, int Tsub, int F, fa_tensor *out); /* subReshape */
 int fa_row_bias_act(fa_ctx *ctx, fa_tensor x, fa_tensor bias, int act, fa_tensor *out); /* rowBiasAct (compute.d.ts:249) */
 
+/* ── the other required members: compute.d.ts:174-234, with the CPU backend's
+ * arithmetic (src/gpu/wasm-context.js; JS doubles, f32 stores).  Not on the
+ * encoder's path: plain kernels so the backend is a complete ComputeContext. */
+int fa_leaky_relu(fa_ctx *ctx, fa_tensor x, double slope, fa_tensor *out);             /* leakyRelu (wasm-context.js:406-413) */
+int fa_snake(fa_ctx *ctx, fa_tensor x, fa_tensor alpha, fa_tensor *out);              /* snake: x + sin^2(a x)/(a + 1e-9), a per row (:414-427) */
+int fa_adain(fa_ctx *ctx, fa_tensor x, fa_tensor scale, fa_tensor shift, double eps, fa_tensor *out); /* adain: per-row instance norm + affine (:344-362) */
+/* im2col: x [Cin, L] -> [Cin*k, Lout], Lout = (L + 2 pad - dilation (k-1) - 1)/stride + 1 (:271-285).
+ * conv1dGemm / conv1dFast / conv1dFastF16 are compositions of im2col, matmul
+ * and conv1d in the host layer, as in the CPU backend (:265-288). */
+int fa_im2col(fa_ctx *ctx, fa_tensor x, int k, int stride, int pad, int dilation, fa_tensor *out);
+/* convTranspose1d: x [Cin, L], w = Cin*(Cout/groups)*k, out [Cout, Lout],
+ * Lout = (L-1) stride - 2 pad + dilation (k-1) + output_padding + 1 (:686-741). */
+int fa_conv_transpose1d(fa_ctx *ctx, fa_tensor x, fa_tensor w, int cout, int k, fa_tensor bias, int stride, int pad, int dilation, int groups,
+                        int output_padding, int act, fa_tensor *out);
+/* gatherCols: out [C, n_idx], out[r, f] = x[r, idx[f]] (host index array; :453-460). */
+int fa_gather_cols(fa_ctx *ctx, fa_tensor x, const uint32_t *idx, int n_idx, fa_tensor *out);
+/* lstm: bidirectional, batch 1, ONNX gate order i,o,f,c; x [seq, inp],
+ * w [2,4H,inp], r [2,4H,H], b [2,8H] -> [seq, 2H]; H <= 256 (:742-776). */
+int fa_lstm(fa_ctx *ctx, fa_tensor x, fa_tensor w, fa_tensor r, fa_tensor b, int hid, fa_tensor *out);
+/* jbatch: out [B, hid] = relu(enc[base+i, :] + pred) (:564-572). */
+int fa_jbatch(fa_ctx *ctx, fa_tensor enc, int base, int B, fa_tensor pred, int hid, fa_tensor *out);
+/* argmaxRows: x [B, logits] -> [B, 4] = (token index, token max, duration
+ * index, duration max); tokens are columns < vocab, first maximum wins (:573-598). */
+int fa_argmax_rows(fa_ctx *ctx, fa_tensor x, int B, int vocab, int logits, fa_tensor *out);
+/* jointArgmax: for frames [frame, frame+count): relu(enc + pred) @ outW [hidden, logits]
+ * + outB, then argmaxRows -> [count, 4] (:599-633). */
+int fa_joint_argmax(fa_ctx *ctx, fa_tensor enc, int frame, int count, fa_tensor pred, fa_tensor outW, fa_tensor outB, int hidden, int vocab,
+                    int logits, fa_tensor *out);
+
 /* ── profiling: startProfile/endProfile (compute.d.ts:250-251) ──────────────────
  * While a profile is open every kernel launch is bracketed by HIP events on
  * the context stream.  fa_profile_end waits, then returns up to `cap` records

@@ -95,3 +95,15 @@ def test_infer_config_and_determinism(fa):
     assert all(np.array_equal(m1[k], m2[k]) for k in m1)
     assert fa.inferConfig(m1) == cfg
     assert all(np.array_equal(m1[k].astype(np.float16).astype(np.float32), m1[k]) for k in ("L0_q", "L1_ff2w1", "linw"))
+
+
+def test_python_host_implements_every_required_member(fa):
+    """The Python HipContext carries every required ComputeContext method
+    (the list node/conformance.js checks the Node class against)."""
+    import re
+
+    src = open(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "fluidaudio-web_amd", "node", "conformance.js")).read()
+    req = re.findall(r'"(\w+)"', src[src.index("const REQUIRED"):src.index("const OPTIONAL")])
+    assert len(req) == 63
+    missing = [m for m in req if not callable(getattr(fa.HipContext, m, None))]
+    assert not missing, missing
