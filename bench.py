@@ -562,15 +562,16 @@ def bench_e2e(args, fa, ctx):
 
 
 def bench_stream(args, fa, ctx):
-    """Streaming encode (streaming.py, the op path) of 30 s of synthetic log-mel
-    pushed 160 ms at a time (16 mel frames = one chunk of 2 encoder frames),
-    with this path's Parakeet shapes (24 layers, d_model 1024, f16 weights) and
-    the EOU streaming config (eou-parakeet/config.js: chunk 2, left 70, causal
-    conv with LayerNorm, subsampling pads t2 b1 l2 r1).  value = audio-s /
-    wall-s of one stream; per-chunk latency in the config."""
+    """Streaming encode (the native stream: fa_stream_* over the fused encoder,
+    device-resident K/V and conv caches) of 30 s of synthetic log-mel pushed
+    160 ms at a time (16 mel frames = one chunk of 2 encoder frames), with
+    this path's Parakeet shapes (24 layers, d_model 1024, f16 weights) and the
+    EOU streaming config (eou-parakeet/config.js: chunk 2, left 70, causal conv
+    with LayerNorm, subsampling pads t2 b1 l2 r1).  value = audio-s / wall-s
+    of one stream; per-chunk latency in the config."""
     cfg = dict(FULL, subPad={"t": 2, "b": 1, "l": 2, "r": 1}, convCausal=True, attChunk=2, attLeft=70, Fsub=17)
     man = fa.synth.make_weights(cfg, seed=1)
-    enc = fa.loadParakeetEncoder(ctx, man, weights="f16", cfg=cfg)
+    enc = fa.FusedEncoder(ctx, man, "f16", max_T=128, cfg=cfg)
     seconds, piece = 30.0, 16
     mel = fa.synth.make_features(128, int(seconds * 100), seed=2)[0]
 
@@ -595,8 +596,8 @@ def bench_stream(args, fa, ctx):
     chunks = mel.shape[1] // piece
     line = {"metric": "streaming encode audio-s/wall-s per stream at 1 GPU", "value": round(seconds / wall, 1), "unit": "audio-s/wall-s",
             "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 2), "higher_is_better": True,
-            "scaling": "weak", "vs_baseline": None, "dtype": "f16-weights/f32", "data": "synthetic log-mel ~N(0,1), random-init weights",
-            "config": {"workload": "30 s pushed in 160 ms pieces, 24 layers d_model 1024, chunk 2 / left 70 (EOU streaming config), op path",
+            "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic log-mel ~N(0,1), random-init weights",
+            "config": {"workload": "30 s pushed in 160 ms pieces, 24 layers d_model 1024, chunk 2 / left 70 (EOU streaming config), native fused stream",
                        "frames": frames, "chunks": chunks, "ms_per_chunk": round(wall * 1e3 / chunks, 3)}}
     if not args.no_cpu:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -609,6 +610,7 @@ def bench_stream(args, fa, ctx):
         cw = time.perf_counter() - t0
         line["cpu_baseline"] = {"value": round(3.0 / cw, 2), "unit": "audio-s/wall-s", "cores": 1, "kind": "port",
                                 "sample": "3 s offline chunked-causal encode (the function the stream computes) through oracle/np_ref.py, float64 torch, 1 thread"}
+    enc.close()
     print(json.dumps(line), flush=True)
 
 

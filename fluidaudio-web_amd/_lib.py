@@ -27,6 +27,10 @@ class EncoderCfg(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("D", "DFF", "H", "HD", "layers", "dwK", "Csub", "Fsub", "melBins")]
 
 
+class EncoderOpts(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("sub_pad_t", "sub_pad_b", "sub_pad_l", "sub_pad_r", "conv_causal", "att_chunk", "att_left", "att_right")]
+
+
 _lib = None
 
 T = C.c_uint64  # fa_tensor / fa_arena / fa_staged
@@ -117,8 +121,15 @@ SIGNATURES = [
     ("fa_encoder_destroy", None, [P]),
     ("fa_encoder_set_exact", I, [P, I, I, C.c_uint]),
     ("fa_encoder_get_exact", I, [P, I]),
+    ("fa_encoder_load_opts", I, [P, C.POINTER(EncoderCfg), C.POINTER(EncoderOpts), I, C.POINTER(C.c_char_p), C.POINTER(F32P), C.POINTER(C.c_int64), I, I,
+                                 C.POINTER(P)]),
     ("fa_encoder_forward", I, [P, P, T, I32P, I, I, I, C.POINTER(T)]),
     ("fa_encoder_tsub", I, [I]),
+    ("fa_encoder_tsub_of", I, [P, I]),
+    ("fa_stream_create", I, [P, P, I, I, C.POINTER(P)]),
+    ("fa_stream_push", I, [P, F32P, I, C.POINTER(T)]),
+    ("fa_stream_flush", I, [P, C.POINTER(T)]),
+    ("fa_stream_destroy", None, [P]),
 ]
 
 

@@ -26,6 +26,7 @@ struct AttnArgs {
   void *out_lo = nullptr;     // f16 route, optional: exact remainder plane f16(o - f16(o)), [rows, ldo]
   int ldo = 0;
   WinTable win;               // window row offsets / lengths (by value: no device table)
+  int chunk = 0, left = 0, right = 0;  // chunk > 0: query i sees keys [cs - left, cs + chunk - 1 + right], cs = chunk * floor(i / chunk)
   int H = 0, HD = 0;
 };
 

@@ -299,7 +299,16 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(NWV > 
       }
     }
   }
-  issue(0, 0);
+  // key blocks this workgroup's queries can see (all keys, or the union of
+  // their chunk windows when attention is chunk-limited)
+  int jlo = 0, jhi = T;
+  if (a.chunk > 0) {
+    const int qlast = min(T, q0 + QB) - 1;
+    jlo = max(0, a.chunk * (q0 / a.chunk) - a.left);
+    jhi = min(T, a.chunk * (qlast / a.chunk) + a.chunk + a.right);
+  }
+  const int kb0 = jlo / KB, nkb = (jhi + KB - 1) / KB;
+  issue(0, kb0 * KB);
 
   f4 o[RT][8];
 #pragma unroll
@@ -316,9 +325,8 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(NWV > 
     }
   const int lbw = QB - 16 * RT - wave * 16 * RT;  // band row of this wave's union tile 0 (= the last row tile's first band row)
 
-  const int nkb = (T + KB - 1) / KB;
-  for (int kb = 0; kb < nkb; kb++) {
-    const int j0 = kb * KB, cur = kb & 1;
+  for (int kb = kb0; kb < nkb; kb++) {
+    const int j0 = kb * KB, cur = (kb - kb0) & 1;
     __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0): this stage's copies landed
     __syncthreads();                                    // ... for every wave; the other stage is free
     if (kb + 1 < nkb) issue(cur ^ 1, j0 + KB);
@@ -388,8 +396,14 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(NWV > 
         const int ri = g * 4 + r;
         float v0 = sc[rt][0][r] + strip[ri * SW + c16 + 15 - ri];
         float v1 = sc[rt][1][r] + strip[ri * SW + 16 + c16 + 15 - ri];
-        v0 = (j0 + c16 < T) ? v0 : -INFINITY;
-        v1 = (j0 + 16 + c16 < T) ? v1 : -INFINITY;
+        int klo = 0, khi = T - 1;  // keys this query sees
+        if (a.chunk > 0) {
+          const int i = iw + rt * 16 + ri, cs = a.chunk * (i / a.chunk);
+          klo = max(klo, cs - a.left);
+          khi = min(khi, cs + a.chunk - 1 + a.right);
+        }
+        v0 = (j0 + c16 >= klo && j0 + c16 <= khi) ? v0 : -INFINITY;
+        v1 = (j0 + 16 + c16 >= klo && j0 + 16 + c16 <= khi) ? v1 : -INFINITY;
         sv[rt][r][0] = v0;
         sv[rt][r][1] = v1;
         need |= fmaxf(v0, v1) > mrow[rt][r] + kLazy;
@@ -416,7 +430,9 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(NWV > 
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int ri = g * 4 + r;
-        const float p0 = __expf(sv[rt][r][0] - mrow[rt][r]), p1 = __expf(sv[rt][r][1] - mrow[rt][r]);
+        // masked keys give 0 (also while a row has seen no visible key yet: -inf - -inf)
+        const float p0 = sv[rt][r][0] == -INFINITY ? 0.f : __expf(sv[rt][r][0] - mrow[rt][r]);
+        const float p1 = sv[rt][r][1] == -INFINITY ? 0.f : __expf(sv[rt][r][1] - mrow[rt][r]);
         pb[ri * PBS + c16] = (_Float16)p0;
         pb[ri * PBS + 16 + c16] = (_Float16)p1;
         lrow[rt][r] += p0 + p1;  // per-lane partial; rows reduced once after the last key block

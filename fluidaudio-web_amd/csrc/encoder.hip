@@ -22,6 +22,7 @@
 // pw2 + x -> LN -> FF2 -> LN.  Residual adds ride the GEMM epilogues (as the
 // reference's `add` option, raw-encoder.js:282-284).
 #include <cmath>
+#include <functional>
 #include <cstring>
 #include <string>
 #include <unordered_map>
@@ -32,11 +33,12 @@
 #include "gemm.h"
 #include "attention.h"
 #include "ops.h"
+#include "encoder_impl.h"
 
 namespace fa {
 
-// One stage's window table: rows [off[w], off[w]+len[w]) belong to window w.
-typedef WinTable WinStage;
+// One stage's window table: rows [off[w], off[w]+len[w]) belong to window w
+// (WinStage, encoder_impl.h).
 
 // ── subsampling kernels (channels-last) ──────────────────────────────────
 // One wavefront per output row (window, t) sweeping the frequency axis; lane l
@@ -68,29 +70,35 @@ __device__ __forceinline__ void store_hilo(_Float16 *dst, const float (&v)[CPL])
   }
 }
 
-// c0 (conv2d 1 -> C, 3x3, stride 2, pad 1, + bias, ReLU; raw-encoder.js:188)
-// fused into c1 (depthwise 3x3, stride 2, pad 1, + bias; raw-encoder.js:189):
-// the c0 map never reaches memory.  c0 outputs outside [0,T1) x [0,F1) are
-// c1's zero padding.  w0 [C][9], b0 [C]; w1 [9][C] (tap-major), b1 [C].
-// Output: [rows of stage 2][F2][C] as hi/lo pairs (2C halfs per position).
-// LM = true (MB <= kC01MelMax): the wave's 7 mel rows (4*t2-3 .. 4*t2+3) are
-// staged in LDS once, zero-padded in time and by one bin on either side, and
-// the c0 taps are LDS broadcasts instead of per-tap global loads.
-constexpr int kC01MelMax = 128, kC01MelStride = kC01MelMax + 4;
+// c0 (conv2d 1 -> C, 3x3, stride 2, + bias, ReLU; raw-encoder.js:188) fused
+// into c1 (depthwise 3x3, stride 2, + bias; raw-encoder.js:189): the c0 map
+// never reaches memory.  Both convs pad pt rows on top and pl bins on the
+// left (Parakeet: 1 and 1; the streaming models' subPad, raw-encoder.js:187-219);
+// the bottom / right pads are implied by the stage lengths the host computes.
+// c0 outputs outside [0,T1) x [0,F1) are c1's zero padding.  w0 [C][9], b0
+// [C]; w1 [9][C] (tap-major), b1 [C].  Output: [rows of stage 2][F2][C] as
+// hi/lo pairs (2C halfs per position).
+// LM = true (melBins + both frequency pads <= kC01MelStride): the wave's 7
+// mel rows are staged in LDS once, zero-padded in time and frequency, and the
+// c0 taps are LDS broadcasts instead of per-tap global loads.
+constexpr int kC01MelStride = 132;  // LDS row: melBins + both frequency pads
 template <int CPL, bool LM = false>
 __global__ __launch_bounds__(256) void sub_c01_kernel(const float *__restrict__ mel, int MB, WinStage s0, WinStage s1, int F1, WinStage s2, int F2,
                                                       const float *__restrict__ w0, const float *__restrict__ b0, const float *__restrict__ w1,
-                                                      const float *__restrict__ b1, _Float16 *__restrict__ y) {
+                                                      const float *__restrict__ b1, _Float16 *__restrict__ y, int pt, int pl) {
   constexpr int C = 64 * CPL;
   __shared__ float smel[LM ? 4 : 1][LM ? 7 : 1][LM ? kC01MelStride : 1];
   const int lane = threadIdx.x & 63, win = blockIdx.y, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int t2 = blockIdx.x * 4 + wave;
   if (t2 >= s2.len[win]) return;
-  if constexpr (LM) {  // slot j holds bin j - 1; rows outside the window are zero
+  // mel rows 4*t2 - 3*pt .. +6 feed this output row (c1 row t2 reads c0 rows
+  // 2*t2 - pt .. +2, each reading mel rows 2*t1 - pt .. +2)
+  const int rbase = 4 * t2 - 3 * pt;
+  if constexpr (LM) {  // slot j holds bin j - pl; rows outside the window are zero
     const int T0w = s0.len[win];
     const float *mw = mel + (size_t)s0.off[win] * MB;
     for (int idx = lane; idx < 7 * kC01MelStride; idx += 64) {
-      const int r = idx / kC01MelStride, j = idx - r * kC01MelStride, ti = 4 * t2 - 3 + r, fi = j - 1;
+      const int r = idx / kC01MelStride, j = idx - r * kC01MelStride, ti = rbase + r, fi = j - pl;
       smel[wave][r][j] = (ti >= 0 && ti < T0w && fi >= 0 && fi < MB) ? mw[(size_t)ti * MB + fi] : 0.f;
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): wave-private rows, written by this wave
@@ -120,12 +128,12 @@ __global__ __launch_bounds__(256) void sub_c01_kernel(const float *__restrict__ 
     float x[9];
 #pragma unroll
     for (int a = 0; a < 3; a++) {
-      const int ti = 2 * t1 - 1 + a;
+      const int ti = 2 * t1 - pt + a;
 #pragma unroll
       for (int bb = 0; bb < 3; bb++) {
-        const int fi = 2 * f1 - 1 + bb;
+        const int fi = 2 * f1 - pl + bb;
         if constexpr (LM)
-          x[a * 3 + bb] = smel[wave][ti - (4 * t2 - 3)][fi + 1];
+          x[a * 3 + bb] = smel[wave][ti - rbase][fi + pl];
         else
           x[a * 3 + bb] = (ti >= 0 && ti < T0 && fi >= 0 && fi < MB) ? m[(size_t)ti * MB + fi] : 0.f;
       }
@@ -138,9 +146,9 @@ __global__ __launch_bounds__(256) void sub_c01_kernel(const float *__restrict__ 
       o[e] = fmaxf(acc, 0.f);
     }
   };
-  float left[3][CPL];  // c0 column 2*f2-1 of rows 2*t2-1 .. 2*t2+1 (the previous step's right column)
+  float left[3][CPL];  // c0 column 2*f2-pl of rows 2*t2-pt .. 2*t2-pt+2 (the previous step's right column)
 #pragma unroll
-  for (int a = 0; a < 3; a++) c0(2 * t2 - 1 + a, -1, left[a]);
+  for (int a = 0; a < 3; a++) c0(2 * t2 - pt + a, -pl, left[a]);
   _Float16 *yr = y + (size_t)(s2.off[win] + t2) * F2 * 2 * C + 2 * CPL * lane;
   for (int f2 = 0; f2 < F2; f2++) {
     float o[CPL];
@@ -149,8 +157,8 @@ __global__ __launch_bounds__(256) void sub_c01_kernel(const float *__restrict__ 
 #pragma unroll
     for (int a = 0; a < 3; a++) {
       float mid[CPL], right[CPL];
-      c0(2 * t2 - 1 + a, 2 * f2, mid);
-      c0(2 * t2 - 1 + a, 2 * f2 + 1, right);
+      c0(2 * t2 - pt + a, 2 * f2 - pl + 1, mid);
+      c0(2 * t2 - pt + a, 2 * f2 - pl + 2, right);
 #pragma unroll
       for (int e = 0; e < CPL; e++) {
         o[e] += left[a][e] * k1[a * 3][e];
@@ -163,7 +171,7 @@ __global__ __launch_bounds__(256) void sub_c01_kernel(const float *__restrict__ 
   }
 }
 
-// c3: depthwise conv2d 3x3, stride 2, pad 1, + bias (raw-encoder.js:191) over
+// c3: depthwise conv2d 3x3, stride 2, pads pt / pl, + bias (raw-encoder.js:191) over
 // the c2 GEMM's f32 pre-activation output, applying c2's ReLU on load.
 // wt [9][C] (tap-major).  Output hi/lo pairs like sub_c01_kernel.
 // With vrow set it also writes the encoder's row map for the transposed V
@@ -172,7 +180,7 @@ __global__ __launch_bounds__(256) void sub_c01_kernel(const float *__restrict__ 
 template <int CPL>
 __global__ __launch_bounds__(256) void sub_dw_kernel(const float *__restrict__ x, WinStage in, int Fin, WinStage out, int Fout,
                                                      const float *__restrict__ wt, const float *__restrict__ b, _Float16 *__restrict__ y,
-                                                     int *__restrict__ vrow, int vstride, int vpad) {
+                                                     int *__restrict__ vrow, int vstride, int vpad, int pt, int pl) {
   constexpr int C = 64 * CPL;
   const int lane = threadIdx.x & 63, win = blockIdx.y;
   const int to = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -197,9 +205,9 @@ __global__ __launch_bounds__(256) void sub_dw_kernel(const float *__restrict__ x
       for (int e = 0; e < CPL; e++) v[e] = 0.f;
     }
   };
-  float left[3][CPL];  // input column 2*fo-1 of rows 2*to-1 .. 2*to+1
+  float left[3][CPL];  // input column 2*fo-pl of rows 2*to-pt .. 2*to-pt+2
 #pragma unroll
-  for (int a = 0; a < 3; a++) ld(2 * to - 1 + a, -1, left[a]);
+  for (int a = 0; a < 3; a++) ld(2 * to - pt + a, -pl, left[a]);
   _Float16 *yr = y + (size_t)(out.off[win] + to) * Fout * 2 * C + 2 * CPL * lane;
   for (int fo = 0; fo < Fout; fo++) {
     float o[CPL];
@@ -207,10 +215,10 @@ __global__ __launch_bounds__(256) void sub_dw_kernel(const float *__restrict__ x
     for (int e = 0; e < CPL; e++) o[e] = br[e];
 #pragma unroll
     for (int a = 0; a < 3; a++) {
-      const int ti = 2 * to - 1 + a;
+      const int ti = 2 * to - pt + a;
       float mid[CPL], right[CPL];
-      ld(ti, 2 * fo, mid);
-      ld(ti, 2 * fo + 1, right);
+      ld(ti, 2 * fo - pl + 1, mid);
+      ld(ti, 2 * fo - pl + 2, right);
 #pragma unroll
       for (int e = 0; e < CPL; e++) {
         o[e] += left[a][e] * wr[a * 3][e];
@@ -233,21 +241,21 @@ __global__ __launch_bounds__(256) void sub_dw_kernel(const float *__restrict__ x
     default: return set_err(ctx, FA_E_UNSUPPORTED, "Csub=%d", (C)); \
   }
 static int launch_c01(fa_ctx *ctx, ProfScope &ps, dim3 grid, const float *mel, int MB, WinStage s0, WinStage s1, int F1, WinStage s2, int F2,
-                      const float *w0, const float *b0, const float *w1, const float *b1, _Float16 *y, int C, bool lds_mel) {
-  if (MB <= kC01MelMax && lds_mel) {
-#define FA_C01(K) FA_LAUNCH(ps, (sub_c01_kernel<K, true>), grid, dim3(256), 0, ctx->stream, mel, MB, s0, s1, F1, s2, F2, w0, b0, w1, b1, y)
+                      const float *w0, const float *b0, const float *w1, const float *b1, _Float16 *y, int C, bool lds_mel, int pt, int pl, int pr) {
+  if (MB + pl + pr <= kC01MelStride && lds_mel) {
+#define FA_C01(K) FA_LAUNCH(ps, (sub_c01_kernel<K, true>), grid, dim3(256), 0, ctx->stream, mel, MB, s0, s1, F1, s2, F2, w0, b0, w1, b1, y, pt, pl)
     FA_CPL_SWITCH(C, FA_C01)
 #undef FA_C01
     return FA_OK;
   }
-#define FA_C01(K) FA_LAUNCH(ps, sub_c01_kernel<K>, grid, dim3(256), 0, ctx->stream, mel, MB, s0, s1, F1, s2, F2, w0, b0, w1, b1, y)
+#define FA_C01(K) FA_LAUNCH(ps, sub_c01_kernel<K>, grid, dim3(256), 0, ctx->stream, mel, MB, s0, s1, F1, s2, F2, w0, b0, w1, b1, y, pt, pl)
   FA_CPL_SWITCH(C, FA_C01)
 #undef FA_C01
   return FA_OK;
 }
 static int launch_dw(fa_ctx *ctx, ProfScope &ps, dim3 grid, const float *x, WinStage in, int Fin, WinStage out, int Fout, const float *wt,
-                     const float *b, _Float16 *y, int C, int *vrow, int vstride, int vpad) {
-#define FA_DW(K) FA_LAUNCH(ps, sub_dw_kernel<K>, grid, dim3(256), 0, ctx->stream, x, in, Fin, out, Fout, wt, b, y, vrow, vstride, vpad)
+                     const float *b, _Float16 *y, int C, int *vrow, int vstride, int vpad, int pt, int pl) {
+#define FA_DW(K) FA_LAUNCH(ps, sub_dw_kernel<K>, grid, dim3(256), 0, ctx->stream, x, in, Fin, out, Fout, wt, b, y, vrow, vstride, vpad, pt, pl)
   FA_CPL_SWITCH(C, FA_DW)
 #undef FA_DW
   return FA_OK;
@@ -259,7 +267,9 @@ static int launch_dw(fa_ctx *ctx, ProfScope &ps, dim3 grid, const float *x, WinS
 // with `lo` also the exact remainder plane lo = f16(y - f16(y)).  Statistics
 // as the reference's layernorm (compute.js:519-529): mean, then the mean of
 // squared deviations, eps inside the rsqrt.
-template <int V>
+// SILU = true: SiLU after the affine (the streaming models' conv-module
+// LayerNorm of the depthwise output, raw-encoder.js:361-364).
+template <int V, bool SILU = false>
 __global__ __launch_bounds__(256) void enc_ln_kernel(const float *__restrict__ x, const float *__restrict__ gamma, const float *__restrict__ beta,
                                                      _Float16 *__restrict__ y, _Float16 *__restrict__ ylo, int rows, float eps) {
   constexpr int D = 256 * V;
@@ -291,8 +301,12 @@ __global__ __launch_bounds__(256) void enc_ln_kernel(const float *__restrict__ x
   for (int t = 0; t < V; t++) {
     const int j = lane + 64 * t;
     const f4 gm = gv[t], bt = bv[t];
-    const float o[4] = {(v[t].x - mean) * inv * gm.x + bt.x, (v[t].y - mean) * inv * gm.y + bt.y, (v[t].z - mean) * inv * gm.z + bt.z,
-                        (v[t].w - mean) * inv * gm.w + bt.w};
+    float o[4] = {(v[t].x - mean) * inv * gm.x + bt.x, (v[t].y - mean) * inv * gm.y + bt.y, (v[t].z - mean) * inv * gm.z + bt.z,
+                  (v[t].w - mean) * inv * gm.w + bt.w};
+    if constexpr (SILU) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) o[e] = silu_f(o[e]);
+    }
     h4 hi, lo;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
@@ -461,6 +475,168 @@ __global__ __launch_bounds__(64) void dwconv_silu_kernel(const TI *__restrict__ 
   }
 }
 
+// Depthwise conv over time (k = 9) for the streaming models and stream
+// passes: causal (pad k-1 on the left, raw-encoder.js:279-280) or symmetric,
+// + bias; taps before a window's first frame read `cache` when one is given
+// (a stream pass: the k-1 GLU rows ahead of the pass, window 0 only) and zeros
+// otherwise.  Then either SiLU into f16 (+ exact lo plane), or the raw f32
+// value into y32 when the layer normalises the depthwise output first.
+// Thread = 4 channels of one frame.
+template <typename TI>
+__global__ __launch_bounds__(64) void dwconv_gen_kernel(const TI *__restrict__ x, const float *__restrict__ cache, WinStage st, int causal,
+                                                        const float *__restrict__ wt, const float *__restrict__ b, int D, _Float16 *__restrict__ y,
+                                                        _Float16 *__restrict__ ylo, float *__restrict__ y32) {
+  constexpr int KT = 9;
+  const int win = blockIdx.y, t = blockIdx.x, T = st.len[win];
+  if (t >= T) return;
+  const int c0 = (blockIdx.z * 64 + threadIdx.x) * 4;
+  if (c0 >= D) return;
+  const int pad = causal ? KT - 1 : (KT - 1) / 2;
+  const size_t base = (size_t)st.off[win] * D + c0;
+  float acc[4];
+#pragma unroll
+  for (int e = 0; e < 4; e++) acc[e] = 0.f;
+#pragma unroll
+  for (int k = 0; k < KT; k++) {
+    const int ti = t - pad + k;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (ti >= 0 && ti < T) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[e] = (float)x[base + (size_t)ti * D + e];
+    } else if (ti < 0 && cache && win == 0) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[e] = cache[(size_t)(KT - 1 + ti) * D + c0 + e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) acc[e] += v[e] * wt[k * D + c0 + e];
+  }
+  h4 hi, lo;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const float r = acc[e] + b[c0 + e];
+    if (y32) {
+      y32[base + (size_t)t * D + e] = r;
+    } else {
+      const float sv = silu_f(r);
+      hi[e] = (_Float16)sv;
+      lo[e] = (_Float16)(sv - (float)hi[e]);
+    }
+  }
+  if (!y32) {
+    *reinterpret_cast<h4 *>(y + base + (size_t)t * D) = hi;
+    if (ylo) *reinterpret_cast<h4 *>(ylo + base + (size_t)t * D) = lo;
+  }
+}
+
+// Stream-pass K / V caches: row r < keep of the next caches is row
+// Lc + nemit - keep + r of [this layer's cached rows (Lc) ; this pass's rows],
+// the keys of the last `keep` emitted frames (streaming-encoder.js:254-257
+// keeps the same rows).  u holds q|k|v rows (K at column D, V at 2D).
+__global__ __launch_bounds__(256) void stream_kv_cache_kernel(const _Float16 *__restrict__ kc_in, const _Float16 *__restrict__ vc_in,
+                                                              const _Float16 *__restrict__ u, int ldu, int D, int Lc, int nemit, int keep,
+                                                              _Float16 *__restrict__ kc_out, _Float16 *__restrict__ vc_out) {
+  const int r = blockIdx.x, src = Lc + nemit - keep + r;
+  for (int c = threadIdx.x * 8; c < D; c += 256 * 8) {
+    h8 k, v;
+    if (src < Lc) {
+      k = *reinterpret_cast<const h8 *>(kc_in + (size_t)src * D + c);
+      v = *reinterpret_cast<const h8 *>(vc_in + (size_t)src * D + c);
+    } else {
+      k = *reinterpret_cast<const h8 *>(u + (size_t)(src - Lc) * ldu + D + c);
+      v = *reinterpret_cast<const h8 *>(u + (size_t)(src - Lc) * ldu + 2 * D + c);
+    }
+    *reinterpret_cast<h8 *>(kc_out + (size_t)r * D + c) = k;
+    *reinterpret_cast<h8 *>(vc_out + (size_t)r * D + c) = v;
+  }
+}
+
+// Stream-pass depthwise-conv cache: row r < k-1 of the next cache is row
+// nemit + r of [cache (k-1 rows) ; this pass's GLU rows] -- the k-1 GLU
+// outputs ahead of the next pass's first frame.
+template <typename TI>
+__global__ __launch_bounds__(256) void stream_conv_cache_kernel(const float *__restrict__ cc_in, const TI *__restrict__ g, int D, int nemit,
+                                                                float *__restrict__ cc_out) {
+  constexpr int KT = 9;
+  const int r = blockIdx.x, src = nemit + r;
+  for (int c = threadIdx.x; c < D; c += 256)
+    cc_out[(size_t)r * D + c] = src < KT - 1 ? cc_in[(size_t)src * D + c] : (float)g[(size_t)(src - (KT - 1)) * D + c];
+}
+
+// Attention of a stream pass (relShiftStream + softmax + bmmPV,
+// compute.js:689-703, streaming-encoder.js:241-254): query i of the pass
+// attends key j of [this layer's Lc cached keys ; the pass's nq keys], key j
+// at position j - Lc relative to the pass's first frame (the pass starts on a
+// chunk boundary); key j is visible iff j - Lc lies in [cs - left,
+// cs + chunk - 1 + right], cs = chunk * floor(i / chunk), and its positional
+// term uses table row clamp(dMax - (i - (j - Lc)), 0, Pn - 1).  One wave per
+// (query, head): lanes over keys for the f32 scores of f16 rows, wave
+// reductions for the softmax, lanes over head dims for P·V.  Lk <= 256.
+__global__ __launch_bounds__(256) void stream_attn_kernel(const _Float16 *__restrict__ u, int ldu, const _Float16 *__restrict__ kc,
+                                                          const _Float16 *__restrict__ vc, int Lc, int nq, int D, const _Float16 *__restrict__ P, int Pn,
+                                                          int dMax, const float *__restrict__ pbu, const float *__restrict__ pbv, int chunk, int left,
+                                                          int right, _Float16 *__restrict__ out, _Float16 *__restrict__ out_lo) {
+  constexpr int HD = 128, MAXK = 256;
+  __shared__ float qs[4][2][HD];
+  __shared__ float ps[4][MAXK];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = blockIdx.y;
+  const int i = blockIdx.x * 4 + wave;
+  if (i >= nq) return;
+  const int Lk = Lc + nq;
+#pragma unroll
+  for (int e = 0; e < 2; e++) {
+    const int d = lane + 64 * e;
+    const float q = (float)u[(size_t)i * ldu + h * HD + d];
+    qs[wave][0][d] = q + pbu[h * HD + d];
+    qs[wave][1][d] = q + pbv[h * HD + d];
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+  const int cs = chunk * (i / chunk);
+  float mx = -INFINITY;
+  for (int j = lane; j < Lk; j += 64) {
+    const int rel = j - Lc;
+    float sc = -INFINITY;
+    if (rel >= cs - left && rel <= cs + chunk - 1 + right) {
+      const _Float16 *kr = j < Lc ? kc + (size_t)j * D + h * HD : u + (size_t)(j - Lc) * ldu + D + h * HD;
+      const int pr = min(max(dMax - (i - rel), 0), Pn - 1);
+      const _Float16 *pp = P + (size_t)pr * D + h * HD;
+      float acc = 0.f;
+      for (int d = 0; d < HD; d += 8) {
+        const h8 kv = *reinterpret_cast<const h8 *>(kr + d), pv = *reinterpret_cast<const h8 *>(pp + d);
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc += qs[wave][0][d + e] * (float)kv[e] + qs[wave][1][d + e] * (float)pv[e];
+      }
+      sc = acc;
+    }
+    ps[wave][j] = sc;
+    mx = fmaxf(mx, sc);
+  }
+  mx = wave_max(mx);  // finite: a query always sees its own chunk
+  float sum = 0.f;
+  for (int j = lane; j < Lk; j += 64) {
+    const float p = __expf(ps[wave][j] - mx);  // masked keys: exp(-inf) = 0
+    ps[wave][j] = p;
+    sum += p;
+  }
+  sum = wave_sum(sum);
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+  const float inv = 1.f / sum;
+#pragma unroll
+  for (int e = 0; e < 2; e++) {
+    const int d = lane + 64 * e;
+    float o = 0.f;
+    for (int j = 0; j < Lk; j++) {
+      const float p = ps[wave][j];
+      if (p != 0.f) o += p * (float)(j < Lc ? vc[(size_t)j * D + h * HD + d] : u[(size_t)(j - Lc) * ldu + 2 * D + h * HD + d]);
+    }
+    o *= inv;
+    const _Float16 hi = (_Float16)o;
+    out[(size_t)i * D + h * HD + d] = hi;
+    if (out_lo) out_lo[(size_t)i * D + h * HD + d] = (_Float16)(o - (float)hi);
+  }
+}
+
 // Zero rows of a padded batch past each window's length (output contract).
 // Plain 16-byte vector copy (graph-mode input / output staging).
 __global__ __launch_bounds__(256) void copy_f4_kernel(const float4 *__restrict__ src, float4 *__restrict__ dst, long n4) {
@@ -491,56 +667,7 @@ __global__ void f32_to_f16_kernel(const float *x, _Float16 *y, long n) {
 static uint16_t h_f32_to_f16(float f) { return __half_as_ushort(__float2half_rn(f)); }
 static float h_f16_to_f32(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 
-// A linear's device weights in one of the three storage formats.
-struct Lin {
-  void *w = nullptr;          // f16 [N][K] | int8 [N][K] | int4 [N][K/32][16 B]
-  void *scales = nullptr;     // int4: f16 bits [N][K/32]
-  float *colscale = nullptr;  // int8: s[n]·fold[n]; int4: fold[n] (null when all 1)
-  float *bias = nullptr;      // [N] (folded), or null
-  int bkind = B_F16;
-  int N = 0, K = 0;
-};
-
 }  // namespace fa
-
-struct fa_encoder {
-  fa_ctx *ctx = nullptr;
-  fa_encoder_cfg cfg{};
-  int format = FA_W_F16;
-  int maxT = 0;
-  std::vector<void *> allocs;
-  // front end
-  float *c0w = nullptr, *c0b = nullptr, *c1w = nullptr, *c1b = nullptr, *c3w = nullptr, *c3b = nullptr;
-  fa::Lin c2, c4, lin;
-  struct Layer {
-    float *ln[5][2];
-    fa::Lin ff1w1, ff1w2, qkv, out, pw1, pw2, ff2w1, ff2w2;
-    float *pbu = nullptr, *pbv = nullptr, *dww = nullptr, *dwb = nullptr;
-    _Float16 *P = nullptr;  // [2*maxT-1, D]
-    unsigned exact = 0;     // FA_EXACT_* operands carried as exact f16 hi/lo pairs
-  };
-  std::vector<Layer> L;
-  // captured forwards (hipGraph), keyed by everything baked into the launch
-  // arguments; ws_gen moves whenever a workspace buffer or a precision mask
-  // changes, so stale graphs never match again
-  struct Captured {
-    std::vector<int64_t> key;
-    hipGraphExec_t exec = nullptr;
-    uint64_t used = 0;
-  };
-  std::vector<Captured> graphs;
-  uint64_t ws_gen = 0, graph_clock = 0;
-  bool vt_fuse = true;
-  bool c01_lds = true;  // front end stages mel rows in LDS (FA_C01_LDS=0 at load: per-tap global loads)  // q|k|v epilogue writes the transposed V (FA_VT_FUSE=0 at load: v_transpose_kernel)
-  // workspace (grow-only)
-  void *hlo = nullptr, *ulo = nullptr, *alo = nullptr, *g32 = nullptr, *vt = nullptr, *vrow = nullptr, *s2 = nullptr, *s2p = nullptr, *s3 = nullptr, *s3p = nullptr, *h = nullptr, *u = nullptr, *a = nullptr, *g = nullptr;
-  size_t cap_hlo = 0, cap_ulo = 0, cap_alo = 0, cap_g32 = 0, cap_vt = 0, cap_vrow = 0, cap_s2 = 0, cap_s2p = 0, cap_s3 = 0, cap_s3p = 0, cap_m = 0, cap_u = 0;
-  // graph-mode input and residual-stream buffers: a captured forward reads the
-  // mel rows from melw and works on xw, so its launches never name the
-  // caller's (pool-recycled) tensors; copies in and out run outside the graph
-  void *melw = nullptr, *xw = nullptr;
-  size_t cap_melw = 0, cap_xw = 0;
-};
 
 namespace fa {
 
@@ -701,6 +828,369 @@ static const unsigned kAllExact = 31u;
 static const int kExactTail = 8;
 
 static inline int stride2_len(int T) { return T <= 0 ? 0 : (T - 1) / 2 + 1; }
+// Output length of a k=3 stride-2 conv with pads p0 / p1: floor((T + p0 + p1 - 3) / 2) + 1.
+static inline int stride2_out(int T, int p0, int p1) {
+  if (T <= 0) return 0;
+  const int q = T + p0 + p1 - 3;
+  const int o = (q >= 0 ? q / 2 : -((1 - q) / 2)) + 1;
+  return o > 0 ? o : 0;
+}
+static inline int enc_tsub(const fa_encoder_opts &o, int T) {
+  for (int i = 0; i < 3; i++) T = stride2_out(T, o.sub_pad_t, o.sub_pad_b);
+  return T;
+}
+
+// Replay the captured graph for `key`, capturing `launch` first when the key
+// is new (least recently used graphs are evicted past 16); `pre` runs on the
+// stream just before the replay (input staging).
+int encoder_graph_run(fa_ctx *ctx, fa_encoder *e, const std::vector<int64_t> &key, const std::function<int()> &launch,
+                      const std::function<int()> &pre) {
+  fa_encoder::Captured *hit = nullptr;
+  for (auto &gr : e->graphs)
+    if (gr.key == key) hit = &gr;
+  if (!hit) {
+    FA_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    const int st = launch();
+    hipGraph_t graph = nullptr;
+    const hipError_t ce = hipStreamEndCapture(ctx->stream, &graph);
+    if (st != FA_OK) {
+      if (graph) (void)hipGraphDestroy(graph);
+      return st;
+    }
+    if (ce != hipSuccess) return set_err(ctx, FA_E_DEVICE, "encoder: graph capture: %s", hipGetErrorString(ce));
+    hipGraphExec_t exec = nullptr;
+    const hipError_t ie = hipGraphInstantiateWithFlags(&exec, graph, 0);
+    (void)hipGraphDestroy(graph);
+    if (ie != hipSuccess) return set_err(ctx, FA_E_DEVICE, "encoder: graph instantiate: %s", hipGetErrorString(ie));
+    constexpr size_t kMaxGraphs = 16;
+    if (e->graphs.size() >= kMaxGraphs) {  // evict the least recently used
+      size_t lru = 0;
+      for (size_t i = 1; i < e->graphs.size(); i++)
+        if (e->graphs[i].used < e->graphs[lru].used) lru = i;
+      (void)hipStreamSynchronize(ctx->stream);  // the evicted graph may still be running on this stream
+      (void)hipGraphExecDestroy(e->graphs[lru].exec);
+      e->graphs.erase(e->graphs.begin() + lru);
+    }
+    e->graphs.push_back({key, exec, 0});
+    hit = &e->graphs.back();
+  }
+  hit->used = ++e->graph_clock;
+  if (pre) FA_TRY(pre());
+  FA_HIP(ctx, hipGraphLaunch(hit->exec, ctx->stream));
+  return FA_OK;
+}
+
+int encoder_grow(fa_encoder *e, void **buf, size_t *cap, size_t need) { return grow(e, buf, cap, need); }
+int encoder_copy_f4(fa_ctx *ctx, const void *src, void *dst, size_t bytes, const char *label) { return copy_f4(ctx, src, dst, bytes, label); }
+
+int pass_geometry(fa_ctx *ctx, const fa_encoder *e, const int32_t *lens, int n, int layout, int pt, int pb, PassGeom *g) {
+  const fa_encoder_cfg &c = e->cfg;
+  const fa_encoder_opts &o = e->opts;
+  if (n <= 0 || n > kMaxWin) return set_err(ctx, FA_E_INVALID, "encoder pass: %d windows", n);
+  g->n = n;
+  g->layout = layout;
+  g->pt = pt;
+  g->pb = pb;
+  g->F[0] = c.melBins;
+  for (int s = 1; s < 4; s++) g->F[s] = stride2_out(g->F[s - 1], o.sub_pad_l, o.sub_pad_r);
+  if (g->F[3] != c.Fsub) return set_err(ctx, FA_E_INVALID, "encoder pass: melBins %d gives %d freq bins, manifest has %d", c.melBins, g->F[3], c.Fsub);
+  for (int s = 0; s < 4; s++) {
+    g->s[s] = WinStage{};
+    g->s[s].n = n;
+    g->mx[s] = 0;
+  }
+  for (int i = 0; i < n; i++) {
+    if (lens[i] <= 0) return set_err(ctx, FA_E_INVALID, "encoder pass: window %d has length %d", i, lens[i]);
+    g->s[0].len[i] = lens[i];
+    for (int s = 1; s < 4; s++) g->s[s].len[i] = stride2_out(g->s[s - 1].len[i], pt, pb);
+    if (g->s[3].len[i] <= 0) return set_err(ctx, FA_E_INVALID, "encoder pass: window %d (%d mel frames) subsamples to no frame", i, lens[i]);
+    if (g->s[3].len[i] > e->maxT) return set_err(ctx, FA_E_INVALID, "encoder pass: window %d subsamples to %d frames > max_T %d", i, g->s[3].len[i], e->maxT);
+    for (int s = 0; s < 4; s++) g->mx[s] = std::max(g->mx[s], g->s[s].len[i]);
+  }
+  for (int s = 0; s < 4; s++) {
+    int acc = 0;
+    for (int i = 0; i < n; i++) {
+      g->s[s].off[i] = layout == 0 ? acc : i * g->mx[s];
+      acc += layout == 0 ? g->s[s].len[i] : g->mx[s];
+    }
+    g->R[s] = acc;
+  }
+  g->M = g->R[3];
+  return FA_OK;
+}
+
+int pass_workspace(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, int layers, bool stream) {
+  const fa_encoder_cfg &c = e->cfg;
+  const int D = c.D, C = c.Csub, M = g.M;
+  FA_TRY(grow(e, &e->s2, &e->cap_s2, (size_t)g.R[2] * g.F[2] * 2 * C * 2));  // hi/lo f16
+  FA_TRY(grow(e, &e->s2p, &e->cap_s2p, (size_t)g.R[2] * g.F[2] * C * 4));    // f32 pre-ReLU
+  FA_TRY(grow(e, &e->s3, &e->cap_s3, (size_t)g.R[3] * g.F[3] * 2 * C * 2));  // hi/lo f16
+  FA_TRY(grow(e, &e->s3p, &e->cap_s3p, (size_t)g.R[3] * g.F[3] * 2 * C * 2));  // hi/lo f16
+  const size_t need_m = (size_t)M * D * 2, need_u = (size_t)M * std::max(c.DFF, 3 * D) * 2;
+  if (need_m > e->cap_m) {
+    size_t c1 = 0, c2 = 0, c3 = 0;
+    if (e->h) { (void)hipStreamSynchronize(ctx->stream); (void)hipFree(e->h); (void)hipFree(e->a); (void)hipFree(e->g); e->h = e->a = e->g = nullptr; e->ws_gen++; }
+    FA_TRY(grow(e, &e->h, &c1, need_m));
+    FA_TRY(grow(e, &e->a, &c2, need_m));
+    FA_TRY(grow(e, &e->g, &c3, need_m));
+    e->cap_m = need_m;
+  }
+  FA_TRY(grow(e, &e->u, &e->cap_u, need_u));
+  unsigned any = 0;
+  bool cln = false;
+  for (int li = 0; li < layers; li++) {
+    any |= e->L[li].exact;
+    cln |= e->L[li].cln[0] != nullptr;
+  }
+  if (any & FA_EXACT_LN_OUT) FA_TRY(grow(e, &e->hlo, &e->cap_hlo, (size_t)M * D * 2));
+  if (any & FA_EXACT_FF_HIDDEN) FA_TRY(grow(e, &e->ulo, &e->cap_ulo, (size_t)M * c.DFF * 2));
+  if (any & (FA_EXACT_ATTN_OUT | FA_EXACT_DW_OUT)) FA_TRY(grow(e, &e->alo, &e->cap_alo, (size_t)M * D * 2));
+  if (any & FA_EXACT_GLU) FA_TRY(grow(e, &e->g32, &e->cap_g32, (size_t)M * D * 4));
+  if (cln) FA_TRY(grow(e, &e->dw32, &e->cap_dw32, (size_t)M * D * 4));
+  if (!stream) {
+    // transposed V per (window, head), written by the q|k|v GEMM's epilogue
+    // (or v_transpose_kernel).  Keys past a window's end are never written:
+    // the buffer starts zeroed and afterwards holds only finite V values of
+    // earlier forwards there, which the attention weights by exactly 0.
+    const int Tp = (g.mx[3] + 63) / 64 * 64;
+    const uint64_t gen = e->ws_gen;
+    FA_TRY(grow(e, &e->vt, &e->cap_vt, (size_t)g.n * c.H * c.HD * Tp * 2));
+    if (e->ws_gen != gen) FA_HIP(ctx, hipMemsetAsync(e->vt, 0, e->cap_vt, ctx->stream));
+    FA_TRY(grow(e, &e->vrow, &e->cap_vrow, (size_t)M * 4));
+  }
+  return FA_OK;
+}
+
+// The whole forward of one pass as a fixed kernel sequence (captured into a
+// hipGraph by the callers when it repeats).  mel: [R0, melBins] time-major
+// rows; x: [M, D] f32, the residual stream and the pass's output.
+int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp, float *x, int layers, const StreamPass *sp) {
+  const fa_encoder_cfg &c = e->cfg;
+  const fa_encoder_opts &o = e->opts;
+  const int D = c.D, C = c.Csub, MB = c.melBins, M = g.M, n = g.n, layout = g.layout;
+  const int F1 = g.F[1], F2 = g.F[2], F3 = g.F[3];
+  const WinStage &s0 = g.s[0], &s1 = g.s[1], &s2 = g.s[2], &s3 = g.s[3];
+  const int *mx = g.mx, *R = g.R;
+  const int Tp = (mx[3] + 63) / 64 * 64;
+  _Float16 *h = (_Float16 *)e->h, *u = (_Float16 *)e->u, *a = (_Float16 *)e->a, *gg = (_Float16 *)e->g;
+  // ── subsampling ──
+  {
+    ProfScope ps(ctx, "sub_c01");
+    FA_TRY(launch_c01(ctx, ps, dim3(cdiv(mx[2], 4), n), melp, MB, s0, s1, F1, s2, F2, e->c0w, e->c0b, e->c1w, e->c1b, (_Float16 *)e->s2, C, e->c01_lds,
+                      g.pt, o.sub_pad_l, o.sub_pad_r));
+    FA_TRY(check_launch(ctx, "sub_c01"));
+  }
+  {
+    GemmArgs p;  // c2 (1x1) + bias; its ReLU is applied by the c3 kernel's loads
+    p.A = e->s2; p.lda = 2 * C; p.akind = A_F16;
+    set_gemm_b(p, e->c2);
+    p.C = e->s2p; p.ldc = C;
+    p.M = R[2] * F2;
+    FA_TRY(gemm_mfma(ctx, p, "sub_pw2"));
+  }
+  {
+    ProfScope ps(ctx, "sub_dw3");
+    FA_TRY(launch_dw(ctx, ps, dim3(cdiv(mx[3], 4), n), (const float *)e->s2p, s2, F2, s3, F3, e->c3w, e->c3b, (_Float16 *)e->s3, C,
+                     sp ? nullptr : (int *)e->vrow, c.H * c.HD * Tp, layout == 1 ? mx[3] : 0, g.pt, o.sub_pad_l));
+    FA_TRY(check_launch(ctx, "sub_dw3"));
+  }
+  {
+    GemmArgs p;  // c4 (1x1) + bias + ReLU, written as hi/lo pairs for the linear
+    p.A = e->s3; p.lda = 2 * C; p.akind = A_F16;
+    set_gemm_b(p, e->c4);
+    p.C = e->s3p; p.ldc = 2 * C; p.out_f16 = 1; p.hilo = 1;
+    p.M = R[3] * F3;
+    FA_TRY(gemm_mfma(ctx, p, "sub_pw4"));
+  }
+  {
+    GemmArgs p;
+    p.A = e->s3p; p.lda = 2 * C * F3; p.akind = A_F16;
+    set_gemm_b(p, e->lin);
+    p.C = x; p.ldc = D;
+    p.M = M;
+    FA_TRY(gemm_mfma(ctx, p, "sub_linear"));
+  }
+
+  // ── conformer layers ──
+  // A operand (with an optional exact lo plane) -> C (with an optional lo plane)
+  auto gemm = [&](const void *A, const void *Alo, int lda, const Lin &L, void *Cp, void *Clo, int ldc, int out_f16, int act, const float *add, int glu,
+                  const char *label) {
+    GemmArgs p;
+    p.A = A; p.Alo = Alo; p.lda = lda; p.akind = A_F16;
+    set_gemm_b(p, L);
+    p.C = Cp; p.Clo = Clo; p.ldc = ldc; p.out_f16 = out_f16; p.act = act;
+    p.add = add; p.ldadd = ldc; p.glu = glu;
+    p.M = M;
+    return gemm_mfma(ctx, p, label);
+  };
+  _Float16 *hlo = (_Float16 *)e->hlo, *ulo = (_Float16 *)e->ulo, *alo = (_Float16 *)e->alo;
+  float *g32 = (float *)e->g32;
+  // LayerNorm of rows `src` into the f16 operand dst (+ lo plane); silu: the conv-module LayerNorm
+  auto ln_into = [&](const float *src, const float *gm, const float *bt, _Float16 *dst, _Float16 *lo, bool silu, const char *label) -> int {
+    if (D % 256 == 0 && D <= 2048) {
+      ProfScope ps(ctx, label);
+      const dim3 grid(cdiv(M, 4));
+#define FA_LNK(V)                                                                                                                       \
+  do {                                                                                                                                  \
+    if (silu)                                                                                                                           \
+      FA_LAUNCH(ps, (enc_ln_kernel<V, true>), grid, dim3(256), 0, ctx->stream, src, gm, bt, dst, lo, M, 1e-5f);                        \
+    else                                                                                                                                \
+      FA_LAUNCH(ps, (enc_ln_kernel<V, false>), grid, dim3(256), 0, ctx->stream, src, gm, bt, dst, lo, M, 1e-5f);                       \
+  } while (0)
+      switch (D / 256) {
+        case 1: FA_LNK(1); break;
+        case 2: FA_LNK(2); break;
+        case 4: FA_LNK(4); break;
+        case 8: FA_LNK(8); break;
+        default: silu = false; break;
+      }
+#undef FA_LNK
+      if (D / 256 == 1 || D / 256 == 2 || D / 256 == 4 || D / 256 == 8) return check_launch(ctx, label);
+    }
+    if (silu) return set_err(ctx, FA_E_UNSUPPORTED, "%s: conv-module LayerNorm needs D a multiple of 256 (<= 2048)", label);
+    return layernorm_launch(ctx, src, gm, bt, dst, 1, M, D, D, D, 1e-5f, label);
+  };
+  auto ln = [&](int which, const fa_encoder::Layer &Ly, const char *label) -> int {
+    return ln_into(x, Ly.ln[which][0], Ly.ln[which][1], h, (Ly.exact & FA_EXACT_LN_OUT) ? hlo : nullptr, false, label);
+  };
+  AttnArgs at;
+  at.q = u; at.k = u + D; at.v = u + 2 * D;
+  at.ldq = at.ldk = at.ldv = 3 * D;
+  at.ldp = D; at.prows = 2 * e->maxT - 1; at.pcenter = e->maxT - 1;
+  at.out = a; at.ldo = D;
+  at.H = c.H; at.HD = c.HD;
+  at.chunk = o.att_chunk; at.left = o.att_left; at.right = o.att_right;
+  at.win.n = n;
+  for (int i = 0; i < n; i++) {
+    at.win.off[i] = s3.off[i];
+    at.win.len[i] = s3.len[i];
+  }
+  const bool fuse_ln = D == 256 || D == 512 || D == 1024 || D == 2048;  // norm_out + the next layer's norm_ff1 in one pass
+  const bool plain_dw = !o.conv_causal && !sp;  // the offline symmetric depthwise conv (BatchNorm folded)
+  for (int li = 0; li < layers; li++) {
+    auto &Ly = e->L[li];
+    const unsigned ex = Ly.exact;
+    const void *hl = (ex & FA_EXACT_LN_OUT) ? hlo : nullptr;
+    void *ul = (ex & FA_EXACT_FF_HIDDEN) ? ulo : nullptr;
+    // FF1 (its LayerNorm ran with the previous layer's norm_out)
+    if (li == 0 || !fuse_ln) FA_TRY(ln(0, Ly, hl ? "ln_ff1_x" : "ln_ff1"));
+    FA_TRY(gemm(h, hl, D, Ly.ff1w1, u, ul, c.DFF, 1, FA_ACT_SILU, nullptr, 0, hl ? "ff1_w1_x" : (ul ? "ff1_w1_u" : "ff1_w1")));
+    FA_TRY(gemm(u, ul, c.DFF, Ly.ff1w2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, ul ? "ff1_w2_x" : "ff1_w2"));
+    // attention
+    FA_TRY(ln(1, Ly, hl ? "ln_att_x" : "ln_att"));
+    bool vt_fused = false;
+    {
+      // q|k|v; offline, V goes straight to the attention's transposed buffer
+      // when the direct-to-LDS route runs it (FA_VT_FUSE=0 at load keeps v_transpose)
+      GemmArgs p;
+      p.A = h; p.Alo = hl; p.lda = D; p.akind = A_F16;
+      set_gemm_b(p, Ly.qkv);
+      p.C = u; p.ldc = 3 * D; p.out_f16 = 1;
+      p.M = M;
+      if (!sp && c.HD == 128 && e->vt_fuse && gemm_takes_direct(ctx, p)) {
+        p.vt = (_Float16 *)e->vt; p.vrow = (const int *)e->vrow; p.vcol0 = 2 * D; p.vtp = Tp;
+        vt_fused = true;
+      }
+      FA_TRY(gemm_mfma(ctx, p, hl ? "qkv_x" : "qkv"));
+    }
+    _Float16 *olo = (ex & FA_EXACT_ATTN_OUT) ? alo : nullptr;
+    if (!sp) {
+      at.pos = Ly.P;
+      at.pbu = Ly.pbu;
+      at.pbv = Ly.pbv;
+      at.out_lo = olo;
+      FA_TRY(relpos_attention_f16(ctx, at, mx[3], (_Float16 *)e->vt, olo ? "attention_x" : "attention", !vt_fused));
+    } else {
+      const size_t kvo = (size_t)li * sp->kv_ld * D;
+      {
+        ProfScope ps(ctx, "stream_attention");
+        FA_LAUNCH(ps, stream_attn_kernel, dim3(cdiv(M, 4), c.H), dim3(256), 0, ctx->stream, u, 3 * D, sp->kc_in + kvo, sp->vc_in + kvo, sp->Lc, M, D,
+                  Ly.P + (size_t)(e->maxT - 1 - sp->dMax) * D, sp->Pn, sp->dMax, Ly.pbu, Ly.pbv, sp->chunk, sp->left, sp->right, a, olo);
+        FA_TRY(check_launch(ctx, "stream_attention"));
+      }
+      if (sp->keep > 0) {
+        ProfScope ps(ctx, "stream_kv_cache");
+        FA_LAUNCH(ps, stream_kv_cache_kernel, dim3(sp->keep), dim3(256), 0, ctx->stream, sp->kc_in + kvo, sp->vc_in + kvo, u, 3 * D, D, sp->Lc, sp->nemit,
+                  sp->keep, sp->kc_out + kvo, sp->vc_out + kvo);
+        FA_TRY(check_launch(ctx, "stream_kv_cache"));
+      }
+    }
+    FA_TRY(gemm(a, olo, D, Ly.out, x, nullptr, D, 0, FA_ACT_NONE, x, 0, olo ? "attn_out_x" : "attn_out"));
+    // conv module: pw1 + GLU (f16, or f32 when exact) -> depthwise (+ LayerNorm) + SiLU -> pw2
+    FA_TRY(ln(2, Ly, hl ? "ln_conv_x" : "ln_conv"));
+    const bool glu32 = ex & FA_EXACT_GLU;
+    FA_TRY(gemm(h, hl, D, Ly.pw1, glu32 ? (void *)g32 : (void *)gg, nullptr, D, glu32 ? 0 : 1, FA_ACT_NONE, nullptr, 1,
+                hl ? "pw1_glu_x" : (glu32 ? "pw1_glu_f32" : "pw1_glu")));
+    _Float16 *dlo = (ex & FA_EXACT_DW_OUT) ? alo : nullptr;
+    if (plain_dw && !Ly.cln[0]) {
+      ProfScope ps(ctx, glu32 ? (dlo ? "dwconv_x" : "dwconv_f32") : (dlo ? "dwconv_lo" : "dwconv"));
+      // 4 channels x 16 frames per thread: inputs read 1.5x (24 rows per 16
+      // outputs); measured 9.6 us against 10.9 for 8 channels x 4 frames (3x)
+      const int thr = std::min(64, D / 4);
+      const dim3 grid(cdiv(mx[3], 16), n, cdiv(D / 4, thr));
+      if (glu32)
+        FA_LAUNCH(ps, (dwconv_silu_kernel<9, 16, 4, float>), grid, dim3(thr), 0, ctx->stream, (const float *)g32, a, dlo, Ly.dww, Ly.dwb, D, s3);
+      else
+        FA_LAUNCH(ps, (dwconv_silu_kernel<9, 16, 4, _Float16>), grid, dim3(thr), 0, ctx->stream, (const _Float16 *)gg, a, dlo, Ly.dww, Ly.dwb, D, s3);
+      FA_TRY(check_launch(ctx, "dwconv"));
+    } else {
+      const float *cache = sp ? sp->cc_in + (size_t)li * 8 * D : nullptr;
+      float *y32 = Ly.cln[0] ? (float *)e->dw32 : nullptr;
+      {
+        ProfScope ps(ctx, "dwconv_gen");
+        const dim3 grid(mx[3], n, cdiv(D / 4, 64));
+        if (glu32)
+          FA_LAUNCH(ps, dwconv_gen_kernel<float>, grid, dim3(64), 0, ctx->stream, (const float *)g32, cache, s3, o.conv_causal, Ly.dww, Ly.dwb, D, a, dlo, y32);
+        else
+          FA_LAUNCH(ps, dwconv_gen_kernel<_Float16>, grid, dim3(64), 0, ctx->stream, (const _Float16 *)gg, cache, s3, o.conv_causal, Ly.dww, Ly.dwb, D, a, dlo,
+                    y32);
+        FA_TRY(check_launch(ctx, "dwconv_gen"));
+      }
+      if (y32) FA_TRY(ln_into(y32, Ly.cln[0], Ly.cln[1], a, dlo, true, "conv_ln_silu"));
+      if (sp) {
+        ProfScope ps(ctx, "stream_conv_cache");
+        float *cco = sp->cc_out + (size_t)li * 8 * D;
+        if (glu32)
+          FA_LAUNCH(ps, stream_conv_cache_kernel<float>, dim3(8), dim3(256), 0, ctx->stream, cache, (const float *)g32, D, sp->nemit, cco);
+        else
+          FA_LAUNCH(ps, stream_conv_cache_kernel<_Float16>, dim3(8), dim3(256), 0, ctx->stream, cache, (const _Float16 *)gg, D, sp->nemit, cco);
+        FA_TRY(check_launch(ctx, "stream_conv_cache"));
+      }
+    }
+    FA_TRY(gemm(a, dlo, D, Ly.pw2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, dlo ? "pw2_x" : "pw2"));
+    // FF2 + norm_out
+    FA_TRY(ln(3, Ly, hl ? "ln_ff2_x" : "ln_ff2"));
+    FA_TRY(gemm(h, hl, D, Ly.ff2w1, u, ul, c.DFF, 1, FA_ACT_SILU, nullptr, 0, hl ? "ff2_w1_x" : (ul ? "ff2_w1_u" : "ff2_w1")));
+    FA_TRY(gemm(u, ul, c.DFF, Ly.ff2w2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, ul ? "ff2_w2_x" : "ff2_w2"));
+    if (fuse_ln && li + 1 < layers) {
+      const auto &Ln = e->L[li + 1];
+      _Float16 *nlo = (Ln.exact & FA_EXACT_LN_OUT) ? hlo : nullptr;
+      const char *lab = nlo ? "ln_out_ff1_x" : "ln_out_ff1";
+      ProfScope ps(ctx, lab);
+      const dim3 grid(cdiv(M, 4));
+      switch (D / 256) {
+        case 1: FA_LAUNCH(ps, enc_ln2_kernel<1>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[4][0], Ly.ln[4][1], Ln.ln[0][0], Ln.ln[0][1], h, nlo, M, 1e-5f); break;
+        case 2: FA_LAUNCH(ps, enc_ln2_kernel<2>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[4][0], Ly.ln[4][1], Ln.ln[0][0], Ln.ln[0][1], h, nlo, M, 1e-5f); break;
+        case 4: FA_LAUNCH(ps, enc_ln2_kernel<4>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[4][0], Ly.ln[4][1], Ln.ln[0][0], Ln.ln[0][1], h, nlo, M, 1e-5f); break;
+        case 8: FA_LAUNCH(ps, enc_ln2_kernel<8>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[4][0], Ly.ln[4][1], Ln.ln[0][0], Ln.ln[0][1], h, nlo, M, 1e-5f); break;
+        default: return set_err(ctx, FA_E_UNSUPPORTED, "fused LayerNorm: D = %d", D);
+      }
+      FA_TRY(check_launch(ctx, lab));
+    } else if (D == 1024) {
+      ProfScope ps(ctx, "ln_out");
+      FA_LAUNCH(ps, enc_ln_f32_kernel<4>, dim3(cdiv(M, 4)), dim3(256), 0, ctx->stream, x, Ly.ln[4][0], Ly.ln[4][1], M, 1e-5f);
+      FA_TRY(check_launch(ctx, "ln_out"));
+    } else {
+      FA_TRY(layernorm_launch(ctx, x, Ly.ln[4][0], Ly.ln[4][1], x, 0, M, D, D, D, 1e-5f, "ln_out"));
+    }
+  }
+  if (layout == 1) {
+    ProfScope ps(ctx, "zero_pad");
+    FA_LAUNCH(ps, zero_pad_rows_kernel, dim3(mx[3], n), dim3(256), 0, ctx->stream, x, D, s3, mx[3]);
+    FA_TRY(check_launch(ctx, "zero_pad"));
+  }
+  return FA_OK;
+}
 
 }  // namespace fa
 
@@ -709,6 +1199,7 @@ using namespace fa;
 extern "C" {
 
 int fa_encoder_tsub(int T) { return stride2_len(stride2_len(stride2_len(T))); }
+int fa_encoder_tsub_of(const fa_encoder *enc, int T) { return enc ? enc_tsub(enc->opts, T) : -1; }
 
 int fa_quantize_weights(int format, const float *w, int K, int N, void *q_out, void *scales_out) {
   if (!w || !q_out || !scales_out || K <= 0 || N <= 0) return FA_E_INVALID;
@@ -732,7 +1223,7 @@ void fa_encoder_destroy(fa_encoder *enc) {
   for (void *p : enc->allocs) (void)hipFree(p);
   for (auto &g : enc->graphs)
     if (g.exec) (void)hipGraphExecDestroy(g.exec);
-  for (void *p : {enc->hlo, enc->ulo, enc->alo, enc->g32, enc->vt, enc->vrow, enc->s2, enc->s2p, enc->s3, enc->s3p, enc->h, enc->u, enc->a, enc->g, enc->melw, enc->xw})
+  for (void *p : {enc->hlo, enc->ulo, enc->alo, enc->g32, enc->vt, enc->vrow, enc->s2, enc->s2p, enc->s3, enc->s3p, enc->h, enc->u, enc->a, enc->g, enc->melw, enc->xw, enc->dw32})
     if (p) (void)hipFree(p);
   delete enc;
 }
@@ -756,12 +1247,26 @@ int fa_encoder_get_exact(const fa_encoder *enc, int layer) {
 
 int fa_encoder_load(fa_ctx *ctx, const fa_encoder_cfg *cfg, int n, const char *const *names, const float *const *data, const int64_t *counts,
                     int format, int max_T, fa_encoder **out) {
+  return fa_encoder_load_opts(ctx, cfg, nullptr, n, names, data, counts, format, max_T, out);
+}
+
+int fa_encoder_load_opts(fa_ctx *ctx, const fa_encoder_cfg *cfg, const fa_encoder_opts *opts, int n, const char *const *names,
+                         const float *const *data, const int64_t *counts, int format, int max_T, fa_encoder **out) {
   if (!ctx || !cfg || !out) return FA_E_INVALID;
   *out = nullptr;
   const fa_encoder_cfg c = *cfg;
+  const fa_encoder_opts o = opts ? *opts : fa_encoder_opts{1, 1, 1, 1, 0, 0, 0, 0};
+  if (o.sub_pad_t < 0 || o.sub_pad_b < 0 || o.sub_pad_l < 0 || o.sub_pad_r < 0 || o.sub_pad_t > 2 || o.sub_pad_l > 2 || o.sub_pad_b > 2 || o.sub_pad_r > 2)
+    return set_err(ctx, FA_E_UNSUPPORTED, "encoder: subsampling pads t%d b%d l%d r%d (0..2 supported)", o.sub_pad_t, o.sub_pad_b, o.sub_pad_l, o.sub_pad_r);
+  if (o.att_chunk < 0 || o.att_left < 0 || o.att_right < 0) return set_err(ctx, FA_E_INVALID, "encoder: negative attention chunk / context");
   if (c.HD != 128 || c.H * c.HD != c.D) return set_err(ctx, FA_E_UNSUPPORTED, "encoder: needs HD=128 and H*HD=D (got H=%d HD=%d D=%d)", c.H, c.HD, c.D);
-  if (c.D % 64 || c.DFF % 64 || c.Csub % 64 || c.melBins != 8 * c.Fsub || (c.Csub * c.Fsub) % 64)
-    return set_err(ctx, FA_E_UNSUPPORTED, "encoder: D, DFF, Csub must be multiples of 64 and melBins = 8*Fsub");
+  {
+    int F = c.melBins;
+    for (int i = 0; i < 3; i++) F = stride2_out(F, o.sub_pad_l, o.sub_pad_r);
+    if (c.D % 64 || c.DFF % 64 || c.Csub % 64 || F != c.Fsub || (c.Csub * c.Fsub) % 32 || c.melBins + o.sub_pad_l + o.sub_pad_r > 4096)
+      return set_err(ctx, FA_E_UNSUPPORTED, "encoder: D, DFF, Csub must be multiples of 64 and melBins must subsample to Fsub (%d bins -> %d, Fsub %d)",
+                     c.melBins, F, c.Fsub);
+  }
   if (c.Csub != 64 && c.Csub != 128 && c.Csub != 256 && c.Csub != 512) return set_err(ctx, FA_E_UNSUPPORTED, "encoder: Csub must be 64, 128, 256 or 512");
   if (c.dwK != 9) return set_err(ctx, FA_E_UNSUPPORTED, "encoder: depthwise kernel %d (9 supported)", c.dwK);
   if (max_T <= 0 || max_T > 1024) return set_err(ctx, FA_E_INVALID, "encoder: max_T %d outside 1..1024", max_T);
@@ -784,6 +1289,7 @@ int fa_encoder_load(fa_ctx *ctx, const fa_encoder_cfg *cfg, int n, const char *c
   fa_encoder *e = new fa_encoder();
   e->ctx = ctx;
   e->cfg = c;
+  e->opts = o;
   e->format = format;
   e->maxT = max_T;
   if (const char *vf = getenv("FA_VT_FUSE")) e->vt_fuse = vf[0] != '0';
@@ -882,6 +1388,16 @@ int fa_encoder_load(fa_ctx *ctx, const fa_encoder_cfg *cfg, int n, const char *c
       if ((st = get(g(lnk[j]) + "_w", D, false, &gw)) || (st = get(g(lnk[j]) + "_b", D, false, &gb))) return fail(st);
       Ly.ln[j][0] = dupload(e, gw, D);
       Ly.ln[j][1] = dupload(e, gb, D);
+    }
+    {  // conv-module LayerNorm (streaming models; raw-encoder.js:361-364), when present
+      const float *bw, *bb;
+      if ((st = get(g("bnw"), D, true, &bw)) || (st = get(g("bnb"), D, true, &bb))) return fail(st);
+      if ((bw == nullptr) != (bb == nullptr)) return fail(set_err(ctx, FA_E_INVALID, "encoder load: layer %d has only one of bnw / bnb", li));
+      if (bw) {
+        if (D % 256 || D > 2048) return fail(set_err(ctx, FA_E_UNSUPPORTED, "encoder load: conv-module LayerNorm needs D a multiple of 256 (<= 2048)"));
+        Ly.cln[0] = dupload(e, bw, D);
+        Ly.cln[1] = dupload(e, bb, D);
+      }
     }
     auto kn_to_bt = [](const float *w, int K, int N) {
       std::vector<float> bt((size_t)N * K);
@@ -1042,79 +1558,20 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
   if (n > kMaxEncWin) return set_err(ctx, FA_E_UNSUPPORTED, "encoderForward: %d windows in one batch (max %d)", n, kMaxEncWin);
   if (layout != 0 && layout != 1) return set_err(ctx, FA_E_INVALID, "encoderForward: layout %d", layout);
   const fa_encoder_cfg &c = e->cfg;
-  const int D = c.D, C = c.Csub, MB = c.melBins;
-  const int F1 = stride2_len(MB), F2 = stride2_len(F1), F3 = stride2_len(F2);
-  if (F3 != c.Fsub) return set_err(ctx, FA_E_INVALID, "encoderForward: melBins %d gives %d freq bins, manifest has %d", MB, F3, c.Fsub);
+  const int D = c.D, MB = c.melBins;
   TensorRec *rm;
   FA_TRY(need(ctx, mel, &rm, "encoderForward mel"));
   if (rm->kind != S_F32 || rm->cols != MB) return set_err(ctx, FA_E_INVALID, "encoderForward: mel must be f32 [rows, %d]", MB);
-  // per-stage window tables
-  WinStage s0{}, s1{}, s2{}, s3{};
-  s0.n = s1.n = s2.n = s3.n = n;
-  int mx[4] = {0, 0, 0, 0};
-  for (int i = 0; i < n; i++) {
-    if (lens[i] <= 0) return set_err(ctx, FA_E_INVALID, "encoderForward: window %d has length %d", i, lens[i]);
-    s0.len[i] = lens[i];
-    s1.len[i] = stride2_len(lens[i]);
-    s2.len[i] = stride2_len(s1.len[i]);
-    s3.len[i] = stride2_len(s2.len[i]);
-    if (s3.len[i] > e->maxT) return set_err(ctx, FA_E_INVALID, "encoderForward: window %d subsamples to %d frames > max_T %d", i, s3.len[i], e->maxT);
-    mx[0] = std::max(mx[0], s0.len[i]);
-    mx[1] = std::max(mx[1], s1.len[i]);
-    mx[2] = std::max(mx[2], s2.len[i]);
-    mx[3] = std::max(mx[3], s3.len[i]);
-  }
-  WinStage *ss[4] = {&s0, &s1, &s2, &s3};
-  int R[4];
-  for (int s = 0; s < 4; s++) {
-    int acc = 0;
-    for (int i = 0; i < n; i++) {
-      ss[s]->off[i] = layout == 0 ? acc : i * mx[s];
-      acc += layout == 0 ? ss[s]->len[i] : mx[s];
-    }
-    R[s] = acc;
-  }
-  if (rm->rows < R[0]) return set_err(ctx, FA_E_INVALID, "encoderForward: mel has %d rows, windows need %d", rm->rows, R[0]);
-  const int M = R[3];
+  PassGeom g;
+  FA_TRY(pass_geometry(ctx, e, lens, n, layout, e->opts.sub_pad_t, e->opts.sub_pad_b, &g));
+  if (rm->rows < g.R[0]) return set_err(ctx, FA_E_INVALID, "encoderForward: mel has %d rows, windows need %d", rm->rows, g.R[0]);
+  const int M = g.M;
   const int layers = layers_run < 0 ? c.layers : std::min(layers_run, c.layers);
-  // workspace
-  FA_TRY(grow(e, &e->s2, &e->cap_s2, (size_t)R[2] * F2 * 2 * C * 2));  // hi/lo f16
-  FA_TRY(grow(e, &e->s2p, &e->cap_s2p, (size_t)R[2] * F2 * C * 4));    // f32 pre-ReLU
-  FA_TRY(grow(e, &e->s3, &e->cap_s3, (size_t)R[3] * F3 * 2 * C * 2));  // hi/lo f16
-  FA_TRY(grow(e, &e->s3p, &e->cap_s3p, (size_t)R[3] * F3 * 2 * C * 2));  // hi/lo f16
-  const size_t need_m = (size_t)M * D * 2, need_u = (size_t)M * std::max(c.DFF, 3 * D) * 2;
-  if (need_m > e->cap_m) {
-    size_t c1 = 0, c2 = 0, c3 = 0;
-    if (e->h) { (void)hipStreamSynchronize(ctx->stream); (void)hipFree(e->h); (void)hipFree(e->a); (void)hipFree(e->g); e->h = e->a = e->g = nullptr; e->ws_gen++; }
-    FA_TRY(grow(e, &e->h, &c1, need_m));
-    FA_TRY(grow(e, &e->a, &c2, need_m));
-    FA_TRY(grow(e, &e->g, &c3, need_m));
-    e->cap_m = need_m;
-  }
-  FA_TRY(grow(e, &e->u, &e->cap_u, need_u));
-  {
-    unsigned any = 0;
-    for (int li = 0; li < layers; li++) any |= e->L[li].exact;
-    if (any & FA_EXACT_LN_OUT) FA_TRY(grow(e, &e->hlo, &e->cap_hlo, (size_t)M * D * 2));
-    if (any & FA_EXACT_FF_HIDDEN) FA_TRY(grow(e, &e->ulo, &e->cap_ulo, (size_t)M * c.DFF * 2));
-    if (any & (FA_EXACT_ATTN_OUT | FA_EXACT_DW_OUT)) FA_TRY(grow(e, &e->alo, &e->cap_alo, (size_t)M * D * 2));
-    if (any & FA_EXACT_GLU) FA_TRY(grow(e, &e->g32, &e->cap_g32, (size_t)M * D * 4));
-  }
-  const int Tp = (mx[3] + 63) / 64 * 64;  // key stride of the transposed V buffer
-  {
-    // transposed V per (window, head), written by the q|k|v GEMM's epilogue
-    // (or v_transpose_kernel).  Keys past a window's end are never written:
-    // the buffer starts zeroed and afterwards holds only finite V values of
-    // earlier forwards there, which the attention weights by exactly 0.
-    const uint64_t gen = e->ws_gen;
-    FA_TRY(grow(e, &e->vt, &e->cap_vt, (size_t)n * c.H * c.HD * Tp * 2));
-    if (e->ws_gen != gen) FA_HIP(ctx, hipMemsetAsync(e->vt, 0, e->cap_vt, ctx->stream));
-    FA_TRY(grow(e, &e->vrow, &e->cap_vrow, (size_t)M * 4));
-  }
+  FA_TRY(pass_workspace(ctx, e, g, layers, false));
   const char *ge = getenv("FA_GRAPH");
   const bool use_graph = !ctx->prof_on && !(ge && ge[0] == '0');
   if (use_graph) {
-    FA_TRY(grow(e, &e->melw, &e->cap_melw, (size_t)R[0] * MB * 4));
+    FA_TRY(grow(e, &e->melw, &e->cap_melw, (size_t)g.R[0] * MB * 4));
     FA_TRY(grow(e, &e->xw, &e->cap_xw, (size_t)M * D * 4));
   }
   fa_tensor ox;
@@ -1122,219 +1579,20 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t 
   FA_TRY(new_tensor(ctx, M, D, S_F32, (size_t)M * D * 4, &ox, &rx));
   rm = get(ctx, mel);
   float *const xout = (float *)rx->ptr;
-  float *x = use_graph ? (float *)e->xw : xout;
-  const float *melp = use_graph ? (const float *)e->melw : (const float *)rm->ptr;
-  _Float16 *h = (_Float16 *)e->h, *u = (_Float16 *)e->u, *a = (_Float16 *)e->a, *gg = (_Float16 *)e->g;
-
-  // The whole forward is a fixed kernel sequence for a given signature: it is
-  // captured once into a hipGraph and replayed (one submission instead of
-  // ~700 launches).  Profiling runs eagerly (its events are per launch).
-  auto launch_all = [&]() -> int {
-  // ── subsampling ──
-    {
-      ProfScope ps(ctx, "sub_c01");
-      FA_TRY(launch_c01(ctx, ps, dim3(cdiv(mx[2], 4), n), melp, MB, s0, s1, F1, s2, F2, e->c0w, e->c0b, e->c1w, e->c1b,
-                        (_Float16 *)e->s2, C, e->c01_lds));
-      FA_TRY(check_launch(ctx, "sub_c01"));
-    }
-    {
-      GemmArgs p;  // c2 (1x1) + bias; its ReLU is applied by the c3 kernel's loads
-      p.A = e->s2; p.lda = 2 * C; p.akind = A_F16;
-      set_gemm_b(p, e->c2);
-      p.C = e->s2p; p.ldc = C;
-      p.M = R[2] * F2;
-      FA_TRY(gemm_mfma(ctx, p, "sub_pw2"));
-    }
-    {
-      ProfScope ps(ctx, "sub_dw3");
-      FA_TRY(launch_dw(ctx, ps, dim3(cdiv(mx[3], 4), n), (const float *)e->s2p, s2, F2, s3, F3, e->c3w, e->c3b, (_Float16 *)e->s3, C, (int *)e->vrow,
-                       c.H * c.HD * Tp, layout == 1 ? mx[3] : 0));
-      FA_TRY(check_launch(ctx, "sub_dw3"));
-    }
-    {
-      GemmArgs p;  // c4 (1x1) + bias + ReLU, written as hi/lo pairs for the linear
-      p.A = e->s3; p.lda = 2 * C; p.akind = A_F16;
-      set_gemm_b(p, e->c4);
-      p.C = e->s3p; p.ldc = 2 * C; p.out_f16 = 1; p.hilo = 1;
-      p.M = R[3] * F3;
-      FA_TRY(gemm_mfma(ctx, p, "sub_pw4"));
-    }
-    {
-      GemmArgs p;
-      p.A = e->s3p; p.lda = 2 * C * F3; p.akind = A_F16;
-      set_gemm_b(p, e->lin);
-      p.C = x; p.ldc = D;
-      p.M = M;
-      FA_TRY(gemm_mfma(ctx, p, "sub_linear"));
-    }
-  
-    // ── conformer layers ──
-    // A operand (with an optional exact lo plane) -> C (with an optional lo plane)
-    auto gemm = [&](const void *A, const void *Alo, int lda, const Lin &L, void *Cp, void *Clo, int ldc, int out_f16, int act, const float *add, int glu,
-                    const char *label) {
-      GemmArgs p;
-      p.A = A; p.Alo = Alo; p.lda = lda; p.akind = A_F16;
-      set_gemm_b(p, L);
-      p.C = Cp; p.Clo = Clo; p.ldc = ldc; p.out_f16 = out_f16; p.act = act;
-      p.add = add; p.ldadd = ldc; p.glu = glu;
-      p.M = M;
-      return gemm_mfma(ctx, p, label);
-    };
-    _Float16 *hlo = (_Float16 *)e->hlo, *ulo = (_Float16 *)e->ulo, *alo = (_Float16 *)e->alo;
-    float *g32 = (float *)e->g32;
-    auto ln = [&](int which, const fa_encoder::Layer &Ly, const char *label) -> int {
-      _Float16 *lo = (Ly.exact & FA_EXACT_LN_OUT) ? hlo : nullptr;
-      if (D % 256 == 0 && D <= 2048) {
-        ProfScope ps(ctx, label);
-        const dim3 grid(cdiv(M, 4));
-        switch (D / 256) {
-          case 1: FA_LAUNCH(ps, enc_ln_kernel<1>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[which][0], Ly.ln[which][1], h, lo, M, 1e-5f); break;
-          case 2: FA_LAUNCH(ps, enc_ln_kernel<2>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[which][0], Ly.ln[which][1], h, lo, M, 1e-5f); break;
-          case 4: FA_LAUNCH(ps, enc_ln_kernel<4>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[which][0], Ly.ln[which][1], h, lo, M, 1e-5f); break;
-          case 8: FA_LAUNCH(ps, enc_ln_kernel<8>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[which][0], Ly.ln[which][1], h, lo, M, 1e-5f); break;
-          default: return layernorm_launch(ctx, x, Ly.ln[which][0], Ly.ln[which][1], h, 1, M, D, D, D, 1e-5f, label);
-        }
-        return check_launch(ctx, label);
-      }
-      return layernorm_launch(ctx, x, Ly.ln[which][0], Ly.ln[which][1], h, 1, M, D, D, D, 1e-5f, label);
-    };
-    AttnArgs at;
-    at.q = u; at.k = u + D; at.v = u + 2 * D;
-    at.ldq = at.ldk = at.ldv = 3 * D;
-    at.ldp = D; at.prows = 2 * e->maxT - 1; at.pcenter = e->maxT - 1;
-    at.out = a; at.ldo = D;
-    at.H = c.H; at.HD = c.HD;
-    at.win.n = n;
-    for (int i = 0; i < n; i++) {
-      at.win.off[i] = s3.off[i];
-      at.win.len[i] = s3.len[i];
-    }
-    const bool fuse_ln = D == 256 || D == 512 || D == 1024 || D == 2048;  // norm_out + the next layer's norm_ff1 in one pass
-    for (int li = 0; li < layers; li++) {
-      auto &Ly = e->L[li];
-      const unsigned ex = Ly.exact;
-      const void *hl = (ex & FA_EXACT_LN_OUT) ? hlo : nullptr;
-      void *ul = (ex & FA_EXACT_FF_HIDDEN) ? ulo : nullptr;
-      // FF1 (its LayerNorm ran with the previous layer's norm_out)
-      if (li == 0 || !fuse_ln) FA_TRY(ln(0, Ly, hl ? "ln_ff1_x" : "ln_ff1"));
-      FA_TRY(gemm(h, hl, D, Ly.ff1w1, u, ul, c.DFF, 1, FA_ACT_SILU, nullptr, 0, hl ? "ff1_w1_x" : (ul ? "ff1_w1_u" : "ff1_w1")));
-      FA_TRY(gemm(u, ul, c.DFF, Ly.ff1w2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, ul ? "ff1_w2_x" : "ff1_w2"));
-      // attention
-      FA_TRY(ln(1, Ly, hl ? "ln_att_x" : "ln_att"));
-      bool vt_fused = false;
-      {
-        // q|k|v; V goes straight to the attention's transposed buffer when
-        // the direct-to-LDS route runs it (FA_VT_FUSE=0 at load keeps v_transpose)
-        GemmArgs p;
-        p.A = h; p.Alo = hl; p.lda = D; p.akind = A_F16;
-        set_gemm_b(p, Ly.qkv);
-        p.C = u; p.ldc = 3 * D; p.out_f16 = 1;
-        p.M = M;
-        if (c.HD == 128 && e->vt_fuse && gemm_takes_direct(ctx, p)) {
-          p.vt = (_Float16 *)e->vt; p.vrow = (const int *)e->vrow; p.vcol0 = 2 * D; p.vtp = Tp;
-          vt_fused = true;
-        }
-        FA_TRY(gemm_mfma(ctx, p, hl ? "qkv_x" : "qkv"));
-      }
-      at.pos = Ly.P;
-      at.pbu = Ly.pbu;
-      at.pbv = Ly.pbv;
-      at.out_lo = (ex & FA_EXACT_ATTN_OUT) ? alo : nullptr;
-      FA_TRY(relpos_attention_f16(ctx, at, mx[3], (_Float16 *)e->vt, at.out_lo ? "attention_x" : "attention", !vt_fused));
-      FA_TRY(gemm(a, at.out_lo, D, Ly.out, x, nullptr, D, 0, FA_ACT_NONE, x, 0, at.out_lo ? "attn_out_x" : "attn_out"));
-      // conv module: pw1 + GLU (f16, or f32 when exact) -> depthwise + SiLU -> pw2
-      FA_TRY(ln(2, Ly, hl ? "ln_conv_x" : "ln_conv"));
-      const bool glu32 = ex & FA_EXACT_GLU;
-      FA_TRY(gemm(h, hl, D, Ly.pw1, glu32 ? (void *)g32 : (void *)gg, nullptr, D, glu32 ? 0 : 1, FA_ACT_NONE, nullptr, 1, hl ? "pw1_glu_x" : (glu32 ? "pw1_glu_f32" : "pw1_glu")));
-      _Float16 *dlo = (ex & FA_EXACT_DW_OUT) ? alo : nullptr;
-      {
-        ProfScope ps(ctx, glu32 ? (dlo ? "dwconv_x" : "dwconv_f32") : (dlo ? "dwconv_lo" : "dwconv"));
-        // 4 channels x 16 frames per thread: inputs read 1.5x (24 rows per 16
-        // outputs); measured 9.6 us against 10.9 for 8 channels x 4 frames (3x)
-        const int thr = std::min(64, D / 4);
-        const dim3 grid(cdiv(mx[3], 16), n, cdiv(D / 4, thr));
-        if (glu32)
-          FA_LAUNCH(ps, (dwconv_silu_kernel<9, 16, 4, float>), grid, dim3(thr), 0, ctx->stream, (const float *)g32, a, dlo, Ly.dww, Ly.dwb, D, s3);
-        else
-          FA_LAUNCH(ps, (dwconv_silu_kernel<9, 16, 4, _Float16>), grid, dim3(thr), 0, ctx->stream, (const _Float16 *)gg, a, dlo, Ly.dww, Ly.dwb, D, s3);
-        FA_TRY(check_launch(ctx, "dwconv"));
-      }
-      FA_TRY(gemm(a, dlo, D, Ly.pw2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, dlo ? "pw2_x" : "pw2"));
-      // FF2 + norm_out
-      FA_TRY(ln(3, Ly, hl ? "ln_ff2_x" : "ln_ff2"));
-      FA_TRY(gemm(h, hl, D, Ly.ff2w1, u, ul, c.DFF, 1, FA_ACT_SILU, nullptr, 0, hl ? "ff2_w1_x" : (ul ? "ff2_w1_u" : "ff2_w1")));
-      FA_TRY(gemm(u, ul, c.DFF, Ly.ff2w2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, ul ? "ff2_w2_x" : "ff2_w2"));
-      if (fuse_ln && li + 1 < layers) {
-        const auto &Ln = e->L[li + 1];
-        _Float16 *nlo = (Ln.exact & FA_EXACT_LN_OUT) ? hlo : nullptr;
-        const char *lab = nlo ? "ln_out_ff1_x" : "ln_out_ff1";
-        ProfScope ps(ctx, lab);
-        const dim3 grid(cdiv(M, 4));
-        switch (D / 256) {
-          case 1: FA_LAUNCH(ps, enc_ln2_kernel<1>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[4][0], Ly.ln[4][1], Ln.ln[0][0], Ln.ln[0][1], h, nlo, M, 1e-5f); break;
-          case 2: FA_LAUNCH(ps, enc_ln2_kernel<2>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[4][0], Ly.ln[4][1], Ln.ln[0][0], Ln.ln[0][1], h, nlo, M, 1e-5f); break;
-          case 4: FA_LAUNCH(ps, enc_ln2_kernel<4>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[4][0], Ly.ln[4][1], Ln.ln[0][0], Ln.ln[0][1], h, nlo, M, 1e-5f); break;
-          case 8: FA_LAUNCH(ps, enc_ln2_kernel<8>, grid, dim3(256), 0, ctx->stream, x, Ly.ln[4][0], Ly.ln[4][1], Ln.ln[0][0], Ln.ln[0][1], h, nlo, M, 1e-5f); break;
-          default: return set_err(ctx, FA_E_UNSUPPORTED, "fused LayerNorm: D = %d", D);
-        }
-        FA_TRY(check_launch(ctx, lab));
-      } else if (D == 1024) {
-        ProfScope ps(ctx, "ln_out");
-        FA_LAUNCH(ps, enc_ln_f32_kernel<4>, dim3(cdiv(M, 4)), dim3(256), 0, ctx->stream, x, Ly.ln[4][0], Ly.ln[4][1], M, 1e-5f);
-        FA_TRY(check_launch(ctx, "ln_out"));
-      } else {
-        FA_TRY(layernorm_launch(ctx, x, Ly.ln[4][0], Ly.ln[4][1], x, 0, M, D, D, D, 1e-5f, "ln_out"));
-      }
-    }
-    if (layout == 1) {
-      ProfScope ps(ctx, "zero_pad");
-      FA_LAUNCH(ps, zero_pad_rows_kernel, dim3(mx[3], n), dim3(256), 0, ctx->stream, x, D, s3, mx[3]);
-      FA_TRY(check_launch(ctx, "zero_pad"));
-    }
-    return FA_OK;
-  };
-  if (!use_graph) {
-    FA_TRY(launch_all());
+  if (!use_graph) {  // profiling (its events are per launch) or FA_GRAPH=0
+    FA_TRY(pass_launch(ctx, e, g, (const float *)rm->ptr, xout, layers, nullptr));
     *out = ox;
     return FA_OK;
   }
-  // The graph reads melw and writes xw (fixed per workspace generation), so the
-  // key holds no caller pointer: a caller that keeps earlier outputs alive
-  // still replays the same graph.
+  // The whole forward is a fixed kernel sequence for a given signature: it is
+  // captured once into a hipGraph and replayed (one submission instead of
+  // ~700 launches).  The graph reads melw and writes xw (fixed per workspace
+  // generation), so the key holds no caller pointer: a caller that keeps
+  // earlier outputs alive still replays the same graph.
   std::vector<int64_t> key = {(int64_t)e->ws_gen, layers, n, layout};
   key.insert(key.end(), lens, lens + n);
-  fa_encoder::Captured *hit = nullptr;
-  for (auto &g : e->graphs)
-    if (g.key == key) hit = &g;
-  if (!hit) {
-    FA_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
-    const int st = launch_all();
-    hipGraph_t graph = nullptr;
-    const hipError_t ce = hipStreamEndCapture(ctx->stream, &graph);
-    if (st != FA_OK) {
-      if (graph) (void)hipGraphDestroy(graph);
-      return st;
-    }
-    if (ce != hipSuccess) return set_err(ctx, FA_E_DEVICE, "encoderForward: graph capture: %s", hipGetErrorString(ce));
-    hipGraphExec_t exec = nullptr;
-    const hipError_t ie = hipGraphInstantiateWithFlags(&exec, graph, 0);
-    (void)hipGraphDestroy(graph);
-    if (ie != hipSuccess) return set_err(ctx, FA_E_DEVICE, "encoderForward: graph instantiate: %s", hipGetErrorString(ie));
-    constexpr size_t kMaxGraphs = 16;
-    if (e->graphs.size() >= kMaxGraphs) {  // evict the least recently used
-      size_t lru = 0;
-      for (size_t i = 1; i < e->graphs.size(); i++)
-        if (e->graphs[i].used < e->graphs[lru].used) lru = i;
-      (void)hipStreamSynchronize(ctx->stream);  // the evicted graph may still be running on this stream
-      (void)hipGraphExecDestroy(e->graphs[lru].exec);
-      e->graphs.erase(e->graphs.begin() + lru);
-    }
-    e->graphs.push_back({key, exec, 0});
-    hit = &e->graphs.back();
-  }
-  hit->used = ++e->graph_clock;
-  FA_TRY(copy_f4(ctx, rm->ptr, e->melw, (size_t)R[0] * MB * 4, "enc_in"));
-  FA_HIP(ctx, hipGraphLaunch(hit->exec, ctx->stream));
+  FA_TRY(encoder_graph_run(ctx, e, key, [&]() { return pass_launch(ctx, e, g, (const float *)e->melw, (float *)e->xw, layers, nullptr); },
+                           [&]() { return copy_f4(ctx, rm->ptr, e->melw, (size_t)g.R[0] * MB * 4, "enc_in"); }));
   FA_TRY(copy_f4(ctx, e->xw, xout, (size_t)M * D * 4, "enc_out"));
   *out = ox;
   return FA_OK;

@@ -1,0 +1,108 @@
+// The fused encoder's internal state, shared by encoder.hip (load, offline
+// forward) and stream.hip (chunk-by-chunk streaming passes).
+#pragma once
+#include <cstdint>
+#include <functional>
+#include <vector>
+
+#include "fa_internal.h"
+#include "attention.h"
+#include "gemm.h"
+
+namespace fa {
+
+typedef WinTable WinStage;
+
+// A linear's device weights in one of the three storage formats.
+struct Lin {
+  void *w = nullptr;          // f16 [N][K] | int8 [N][K] | int4 [N][K/32][16 B]
+  void *scales = nullptr;     // int4: f16 bits [N][K/32]
+  float *colscale = nullptr;  // int8: s[n]·fold[n]; int4: fold[n] (null when all 1)
+  float *bias = nullptr;      // [N] (folded), or null
+  int bkind = B_F16;
+  int N = 0, K = 0;
+};
+
+}  // namespace fa
+
+struct fa_encoder {
+  fa_ctx *ctx = nullptr;
+  fa_encoder_cfg cfg{};
+  fa_encoder_opts opts{1, 1, 1, 1, 0, 0, 0, 0};
+  int format = FA_W_F16;
+  int maxT = 0;
+  std::vector<void *> allocs;
+  // front end
+  float *c0w = nullptr, *c0b = nullptr, *c1w = nullptr, *c1b = nullptr, *c3w = nullptr, *c3b = nullptr;
+  fa::Lin c2, c4, lin;
+  struct Layer {
+    float *ln[5][2];
+    fa::Lin ff1w1, ff1w2, qkv, out, pw1, pw2, ff2w1, ff2w2;
+    float *pbu = nullptr, *pbv = nullptr, *dww = nullptr, *dwb = nullptr;
+    _Float16 *P = nullptr;  // [2*maxT-1, D]
+    float *cln[2] = {nullptr, nullptr};  // conv-module LayerNorm of the depthwise output (streaming models), or none
+    unsigned exact = 0;     // FA_EXACT_* operands carried as exact f16 hi/lo pairs
+  };
+  std::vector<Layer> L;
+  // captured forwards (hipGraph), keyed by everything baked into the launch
+  // arguments; ws_gen moves whenever a workspace buffer or a precision mask
+  // changes, so stale graphs never match again
+  struct Captured {
+    std::vector<int64_t> key;
+    hipGraphExec_t exec = nullptr;
+    uint64_t used = 0;
+  };
+  std::vector<Captured> graphs;
+  uint64_t ws_gen = 0, graph_clock = 0;
+  bool vt_fuse = true;  // q|k|v epilogue writes the transposed V (FA_VT_FUSE=0 at load: v_transpose_kernel)
+  bool c01_lds = true;  // front end stages mel rows in LDS (FA_C01_LDS=0 at load: per-tap global loads)
+  // workspace (grow-only)
+  void *hlo = nullptr, *ulo = nullptr, *alo = nullptr, *g32 = nullptr, *vt = nullptr, *vrow = nullptr, *s2 = nullptr, *s2p = nullptr, *s3 = nullptr, *s3p = nullptr, *h = nullptr, *u = nullptr, *a = nullptr, *g = nullptr;
+  size_t cap_hlo = 0, cap_ulo = 0, cap_alo = 0, cap_g32 = 0, cap_vt = 0, cap_vrow = 0, cap_s2 = 0, cap_s2p = 0, cap_s3 = 0, cap_s3p = 0, cap_m = 0, cap_u = 0;
+  // graph-mode input and residual-stream buffers: a captured forward reads the
+  // mel rows from melw and works on xw, so its launches never name the
+  // caller's (pool-recycled) tensors; copies in and out run outside the graph
+  void *melw = nullptr, *xw = nullptr;
+  size_t cap_melw = 0, cap_xw = 0;
+  void *dw32 = nullptr;  // f32 depthwise output ahead of the conv-module LayerNorm
+  size_t cap_dw32 = 0;
+};
+
+namespace fa {
+
+// One pass of the encoder over a batch of windows: stage tables for the four
+// time resolutions (mel, after each stride-2 conv), frequency bins per stage,
+// and the time pads of this pass (offline: the model's; a streaming pass pads
+// only at the stream's edges).
+struct PassGeom {
+  int n = 0, layout = 0, pt = 0, pb = 0;
+  WinStage s[4];
+  int mx[4] = {0, 0, 0, 0}, R[4] = {0, 0, 0, 0}, F[4] = {0, 0, 0, 0};
+  int M = 0;
+};
+
+// A streaming chunk pass: the frames of this pass attend to `Lc` cached keys
+// of earlier passes followed by their own; the first `nemit` frames are
+// emitted, and their keys / depthwise inputs become the next pass's caches.
+struct StreamPass {
+  int Lc = 0, nemit = 0, keep = 0;
+  int chunk = 0, left = 0, right = 0;
+  const _Float16 *kc_in = nullptr, *vc_in = nullptr;  // [layers][left][D]
+  _Float16 *kc_out = nullptr, *vc_out = nullptr;
+  const float *cc_in = nullptr;  // [layers][dwK-1][D], GLU outputs ahead of the pass
+  float *cc_out = nullptr;
+  // positional term: distance dMax - r at row r of the layer's table (the
+  // offline table's rows maxT-1-dMax ..), Pn = dMax - dMin + 1 rows
+  int Pn = 0, dMax = 0;
+  int kv_ld = 0;  // rows per layer slice of the K/V caches (= left)
+};
+
+int pass_geometry(fa_ctx *ctx, const fa_encoder *e, const int32_t *lens, int n, int layout, int pt, int pb, PassGeom *g);
+int pass_workspace(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, int layers, bool stream);
+int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *mel, float *x, int layers, const StreamPass *sp);
+int encoder_grow(fa_encoder *e, void **buf, size_t *cap, size_t need);
+int encoder_copy_f4(fa_ctx *ctx, const void *src, void *dst, size_t bytes, const char *label);
+int encoder_graph_run(fa_ctx *ctx, fa_encoder *e, const std::vector<int64_t> &key, const std::function<int()> &launch,
+                      const std::function<int()> &pre);
+
+}  // namespace fa

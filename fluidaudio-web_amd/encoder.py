@@ -214,8 +214,11 @@ def tsub(T: int) -> int:
 class FusedEncoder:
     """Native whole-encoder forward (fa_encoder_load / fa_encoder_forward)."""
 
-    def __init__(self, ctx: HipContext, man: dict, fmt: str = "f16", max_T: int = 512, layers: int | None = None):
-        cfg = inferConfig(man)
+    def __init__(self, ctx: HipContext, man: dict, fmt: str = "f16", max_T: int = 512, layers: int | None = None, cfg: dict | None = None):
+        """cfg: the streaming models' fields the manifest does not carry
+        (melBins, subPad {t, b, l, r}, convCausal, attChunk, attLeft,
+        attRight; eou-parakeet/config.js), as loadParakeetEncoder takes them."""
+        cfg = dict(inferConfig(man), **(cfg or {}))
         if layers is not None:
             cfg["layers"] = min(layers, cfg["layers"])
         self.ctx, self.cfg, self.fmt, self.max_T = ctx, cfg, fmt, max_T
@@ -226,8 +229,12 @@ class FusedEncoder:
         arr_data = (L.F32P * len(names))(*[keep[n].ctypes.data_as(L.F32P) for n in names])
         arr_cnt = (C.c_int64 * len(names))(*[keep[n].size for n in names])
         c = L.EncoderCfg(*(cfg[k] for k in ("D", "DFF", "H", "HD", "layers", "dwK", "Csub", "Fsub", "melBins")))
+        sp = cfg.get("subPad") or {"t": 1, "b": 1, "l": 1, "r": 1}
+        o = L.EncoderOpts(sp["t"], sp["b"], sp["l"], sp["r"], int(bool(cfg.get("convCausal"))), int(cfg.get("attChunk") or 0),
+                          int(cfg.get("attLeft", 70)) if cfg.get("attChunk") else 0, int(cfg.get("attRight", 0)) if cfg.get("attChunk") else 0)
         p = L.P()
-        check(ctx._p, lib().fa_encoder_load(ctx._p, C.byref(c), len(names), arr_names, arr_data, arr_cnt, FORMATS[fmt], max_T, C.byref(p)))
+        check(ctx._p, lib().fa_encoder_load_opts(ctx._p, C.byref(c), C.byref(o), len(names), arr_names, arr_data, arr_cnt, FORMATS[fmt], max_T,
+                                                 C.byref(p)))
         self._p = p
         ctx._children.add(self)
 
@@ -242,6 +249,10 @@ class FusedEncoder:
 
     def exact(self, layer: int) -> int:
         return int(lib().fa_encoder_get_exact(self._p, layer))
+
+    def tsub(self, T: int) -> int:
+        """Encoder frames of a window of T mel frames (this model's subsampling pads)."""
+        return int(lib().fa_encoder_tsub_of(self._p, int(T)))
 
     def close(self):
         if getattr(self, "_p", None):
@@ -277,7 +288,7 @@ class FusedEncoder:
         finally:
             self.ctx.popArena(arena)
             self.ctx.freeTensor(feats)
-        ts = [tsub(t) for t in lens]
+        ts = [self.tsub(t) for t in lens]
         res, off = [], 0
         tmax = max(ts)
         for i, t in enumerate(ts):

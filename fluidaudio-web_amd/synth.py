@@ -34,6 +34,13 @@ def tiny_stream_cfg(layers=2, right=0, chunk=2):
                 convCausal=True, attChunk=chunk, attLeft=8, attRight=right)
 
 
+def small_stream_cfg(layers=2, right=0, chunk=2, left=8):
+    """Streaming (EOU-style) model at dims the fused encoder takes (HD 128):
+    subPad t2 b1 l2 r1 takes 128 mel bins 128 -> 65 -> 33 -> 17 (Fsub 17)."""
+    return dict(D=256, DFF=1024, H=2, HD=128, layers=layers, dwK=9, Csub=64, Fsub=17, melBins=128, subPad={"t": 2, "b": 1, "l": 2, "r": 1},
+                convCausal=True, attChunk=chunk, attLeft=left, attRight=right)
+
+
 def tiny_cfg(layers=2):
     """Small config for CPU cross-checks (same structure, reduced dims)."""
     return dict(D=64, DFF=256, H=2, HD=32, layers=layers, dwK=9, Csub=8, Fsub=4, melBins=32)

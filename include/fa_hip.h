@@ -300,6 +300,22 @@ typedef struct fa_encoder_cfg {
   int D, DFF, H, HD, layers, dwK, Csub, Fsub, melBins;
 } fa_encoder_cfg;
 
+/* Model options of the streaming FastConformer variants (EOU / Nemotron
+ * configs, src/engines/asr-parakeet/raw-encoder.js:187-219,250-280,361-364):
+ *   sub_pad_*    pads of the three stride-2 subsampling convs (Parakeet: 1,1,1,1;
+ *                EOU: t2 b1 l2 r1); the frequency bins after the front end
+ *                follow from melBins and the left/right pads;
+ *   conv_causal  depthwise conv padded (K-1, 0) instead of ((K-1)/2, (K-1)/2);
+ *   att_chunk    > 0: query i sees keys [cs - att_left, cs + att_chunk - 1 +
+ *                att_right], cs = att_chunk * floor(i / att_chunk) (0 = all keys).
+ * A layer whose manifest has "L<i>_bnw" / "L<i>_bnb" normalises the depthwise
+ * output with that LayerNorm before its SiLU (raw-encoder.js:361-364). */
+typedef struct fa_encoder_opts {
+  int sub_pad_t, sub_pad_b, sub_pad_l, sub_pad_r;
+  int conv_causal;
+  int att_chunk, att_left, att_right;
+} fa_encoder_opts;
+
 /* Weight storage formats for the encoder's linears. */
 enum fa_weight_format { FA_W_F16 = 0, FA_W_INT8 = 1, FA_W_INT4 = 2 };
 
@@ -313,6 +329,11 @@ enum fa_weight_format { FA_W_F16 = 0, FA_W_INT8 = 1, FA_W_INT4 = 2 };
  * the 8x front end) the encoder will accept (<= 1024). */
 int fa_encoder_load(fa_ctx *ctx, const fa_encoder_cfg *cfg, int n, const char *const *names, const float *const *data, const int64_t *counts,
                     int format, int max_T, fa_encoder **out);
+/* fa_encoder_load with model options (NULL = the offline Parakeet defaults:
+ * pads 1, symmetric depthwise conv, full attention).  The options shape every
+ * forward of the encoder and the streams created on it. */
+int fa_encoder_load_opts(fa_ctx *ctx, const fa_encoder_cfg *cfg, const fa_encoder_opts *opts, int n, const char *const *names,
+                         const float *const *data, const int64_t *counts, int format, int max_T, fa_encoder **out);
 void fa_encoder_destroy(fa_encoder *enc);
 
 /* Operand precision per conformer layer.  The f16 route rounds five kinds of
@@ -345,6 +366,29 @@ int fa_encoder_get_exact(const fa_encoder *enc, int layer);
 int fa_encoder_forward(fa_ctx *ctx, fa_encoder *enc, fa_tensor mel, const int32_t *lens, int n, int layout, int layers_run, fa_tensor *out);
 /* Subsampled length of a window of T mel frames (raw-encoder.js:217-218). */
 int fa_encoder_tsub(int T);
+/* The same for this encoder's subsampling pads. */
+int fa_encoder_tsub_of(const fa_encoder *enc, int T);
+
+/* ── streaming encoder: createEncodeStream / encodeStreamPush /
+ * encodeStreamFlush / disposeEncodeStream
+ * (src/engines/asr-parakeet/streaming-encoder.js:33-182) ──────────────────
+ * A stream runs chunk passes of the fused encoder with the K / V and
+ * depthwise-conv caches kept on the device; its frames are those of the
+ * offline chunked-causal encoder (fa_encoder_forward on the same encoder).
+ * enc: loaded with att_chunk > 0, conv_causal and sub_pad_t 2 (the streaming
+ * models), max_T > att_left + att_chunk.  lookahead_chunks: provisional
+ * right-context chunks recomputed each pass (>= 1 when att_right > 0; error
+ * against offline frames shrinks as it grows).  max_chunk: frames per pass
+ * (att_chunk .. 128).
+ * fa_stream_push: mel = host f32 [melBins][count] (mel-major); runs every pass
+ * the buffered frames allow; *out = the new frames [n, D] (f32), or 0 when
+ * none are final yet.  fa_stream_flush: encodes the tail with the bottom pad;
+ * the stream accepts no push afterwards (FA_E_STATE). */
+typedef struct fa_stream fa_stream;
+int fa_stream_create(fa_ctx *ctx, fa_encoder *enc, int lookahead_chunks, int max_chunk, fa_stream **out);
+int fa_stream_push(fa_stream *st, const float *mel, int count, fa_tensor *out);
+int fa_stream_flush(fa_stream *st, fa_tensor *out);
+void fa_stream_destroy(fa_stream *st);
 
 #ifdef __cplusplus
 }
