@@ -19,7 +19,6 @@ the CPU backend's arithmetic (wasm-context.js), off the encoder's hot path.
 from __future__ import annotations
 
 import ctypes as C
-import weakref
 from contextlib import contextmanager
 
 import numpy as np
@@ -65,6 +64,22 @@ def _f32(a):
     return np.ascontiguousarray(np.asarray(a, dtype=np.float32))
 
 
+class NativeHandle:
+    """One native object's pointer and destructor; released at most once,
+    by its owner's close() or by the context's destroy(), whichever is first."""
+
+    __slots__ = ("_owner", "p", "_destroy")
+
+    def __init__(self, owner, p, destroy):
+        self._owner, self.p, self._destroy = owner, p, destroy
+
+    def release(self):
+        if self.p:
+            p, self.p = self.p, None
+            self._owner._owned.pop(id(self), None)
+            self._destroy(p)
+
+
 class HipContext:
     """ComputeContext on one gfx950 GPU (one HIP stream, in-order)."""
 
@@ -78,13 +93,23 @@ class HipContext:
             raise FaError(st, f"fa_ctx_create(device={device}) failed with status {st} (no gfx950 GPU visible?)")
         self._p = p
         self._destroyed = False
-        self._children = weakref.WeakSet()  # native objects bound to this context (encoders)
+        self._owned = {}  # id -> NativeHandle: objects that free device memory through this context
+
+    def _own(self, ptr, destroy) -> "NativeHandle":
+        """Register a native object (encoder, decoder, stream) created on this
+        context; destroy() releases every one still live before the context.
+        The registry holds plain cells, not weak references, so interpreter
+        shutdown (which clears weak references before running finalizers)
+        cannot destroy the context ahead of its objects."""
+        h = NativeHandle(self, ptr, destroy)
+        self._owned[id(h)] = h
+        return h
 
     # ── lifecycle ─────────────────────────────────────────────────────────
     def destroy(self):
         if not self._destroyed:
-            for c in list(self._children):  # they free device memory through the context
-                c.close()
+            for h in reversed(list(self._owned.values())):  # newest first (a stream before its encoder); they free device memory through the context
+                h.release()
             lib().fa_ctx_destroy(self._p)
             self._destroyed = True
 

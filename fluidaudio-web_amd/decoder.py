@@ -31,13 +31,17 @@ class TdtDecoder:
         ptrs = (C.POINTER(C.c_float) * len(arrs))(*[a.ctypes.data_as(C.POINTER(C.c_float)) for a in arrs])
         p = L.P()
         check(ctx._p, lib().fa_tdt_load(ctx._p, ptrs, C.byref(p)))
-        self._p = p
-        ctx._children.add(self)
+        self._h = ctx._own(p, lib().fa_tdt_destroy)
+
+    @property
+    def _p(self):
+        h = getattr(self, "_h", None)
+        return h.p if h is not None else None
 
     def close(self):
-        if getattr(self, "_p", None):
-            lib().fa_tdt_destroy(self._p)
-            self._p = None
+        h = getattr(self, "_h", None)
+        if h is not None:
+            h.release()
 
     def __del__(self):
         try:

@@ -235,8 +235,7 @@ class FusedEncoder:
         p = L.P()
         check(ctx._p, lib().fa_encoder_load_opts(ctx._p, C.byref(c), C.byref(o), len(names), arr_names, arr_data, arr_cnt, FORMATS[fmt], max_T,
                                                  C.byref(p)))
-        self._p = p
-        ctx._children.add(self)
+        self._h = ctx._own(p, lib().fa_encoder_destroy)
 
     # operand-precision bits (fa_encoder_set_exact)
     EXACT = dict(ln_out=1, ff_hidden=2, attn_out=4, glu=8, dw_out=16)
@@ -254,10 +253,15 @@ class FusedEncoder:
         """Encoder frames of a window of T mel frames (this model's subsampling pads)."""
         return int(lib().fa_encoder_tsub_of(self._p, int(T)))
 
+    @property
+    def _p(self):
+        h = getattr(self, "_h", None)
+        return h.p if h is not None else None
+
     def close(self):
-        if getattr(self, "_p", None):
-            lib().fa_encoder_destroy(self._p)
-            self._p = None
+        h = getattr(self, "_h", None)
+        if h is not None:
+            h.release()
 
     def __del__(self):
         try:

@@ -25,7 +25,7 @@ class EncodeStream:
         self.ctx, self.enc, self.proj = ctx, enc, proj
         p = L.P()
         check(ctx._p, lib().fa_stream_create(ctx._p, enc._p, int(lookaheadChunks), int(maxChunk), C.byref(p)))
-        self._p = p
+        self._h = ctx._own(p, lib().fa_stream_destroy)
 
     def _frames(self, h: int):
         if not h:
@@ -39,10 +39,15 @@ class EncodeStream:
         self.ctx.freeTensor(t)
         return out
 
+    @property
+    def _p(self):
+        h = getattr(self, "_h", None)
+        return h.p if h is not None else None
+
     def close(self):
-        if getattr(self, "_p", None):
-            lib().fa_stream_destroy(self._p)
-            self._p = None
+        h = getattr(self, "_h", None)
+        if h is not None:
+            h.release()
 
     def __del__(self):
         try:

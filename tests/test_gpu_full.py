@@ -77,7 +77,7 @@ def test_exact_operands_track_fp32_path(ctx, fa, full_weights):
 def test_set_exact_validation(ctx, fa, full_weights):
     lw = {k: v for k, v in full_weights.items() if not (k.startswith("L") and int(k[1:k.index("_")]) >= 2)}
     enc = fa.FusedEncoder(ctx, lw, "f16", max_T=64)
-    assert enc.exact(1) == 31 and enc.exact(5) == -1  # default tail covers both layers of a 2-layer model
+    assert enc.exact(1) == 29 and enc.exact(5) == -1  # default tail (all but FF hidden) covers both layers of a 2-layer model
     with pytest.raises(fa.FaError):
         enc.setExact(64)
     with pytest.raises(fa.FaError):
@@ -85,7 +85,7 @@ def test_set_exact_validation(ctx, fa, full_weights):
     enc.close()
     for fmt in ("int8", "int4"):  # quantised weights take the same masks and default
         q = fa.FusedEncoder(ctx, lw, fmt, max_T=64)
-        assert q.exact(0) == 31 and q.exact(1) == 31
+        assert q.exact(0) == 29 and q.exact(1) == 29
         q.setExact(1)
         assert q.exact(0) == 1
         q.close()
