@@ -24,6 +24,8 @@
 #include "fa_device.h"
 #include "attention.h"
 
+#include <type_traits>
+
 namespace fa {
 
 template <typename T>
@@ -219,71 +221,113 @@ __device__ __forceinline__ void attn_dma16(const void *g, uint32_t lds_addr) {
 }
 #pragma clang diagnostic pop
 
-// Workgroup = QB = 16·RT·NWV queries of one (window, head): NWV waves, each
-// owning RT 16-row MFMA tiles (with RT = 2 every K / V / band fragment read
-// from LDS feeds two MFMAs; with RT = 1 more waves share a CU).  Keys advance
-// 32 per stage, two stages in flight:
-//   K   [32 keys][128 d]        (256 B rows, 16-byte chunk c at slot c ^ (row & 7))
-//   Vt  [128 d][32 keys]        (64 B rows,  chunk c at slot c ^ ((row >> 1) & 3))
-//   band [QB+32 rows][128 d]    table rows pbase .. , pbase = pc - (q0 + QB - 1) + j0
-// A query i and key j use band row (j - j0) + (q0 + QB - 1 - i).
-template <int RT, int NWV>
-__global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(NWV > 4 ? 2 : 1, NWV > 4 ? 2 : 1))) void relpos_attn_lds_kernel(
+// Workgroup = QB = 16·NWV queries of one (window, head), one 16-query row
+// tile per wave: every product is computed with keys / band rows as
+// the MFMA's M side and the wave's 16 queries as N, so each lane owns ONE
+// query (column c16) and the softmax state (reference max, partial sum,
+// rescale factor) is per lane.  Keys advance 32 per block; S blocks of
+// copies are in flight (global_load_lds_dwordx4, tracked with vmcnt):
+//   K   [32 keys][128 d]   (256 B rows, 16-byte chunk c at slot c ^ ((row >> 1) & 7):
+//                           the 8 rows 2 m + kt one read phase touches hit distinct banks)
+//   Vt  [128 d][32 keys]   (64 B rows,  chunk c at slot c ^ ((row >> 1) & 3))
+// The positional band of a key block is table rows pbase0 + j0 + [0, BR),
+// BR = QB + 32 (query i and key j use band row (j - j0) + (q0 + QB - 1 - i)).
+// Consecutive blocks' bands overlap in BR - 32 rows, so the band lives in a
+// ring of RS table rows (row x at slot x % RS, chunk c at c ^ (slot & 7)):
+// the first block copies its BR rows, every later block only the 32 it adds.
+//   * Key tile kt (0, 1) of a 32-key block reads K rows 2 m + kt for MFMA row
+//     m, so output row g*4 + r of tile kt is key 8 g + 2 r + kt: lane (g, c16)
+//     holds keys 8 g .. 8 g + 7 of its query, in order.  Its probabilities
+//     are then directly the B operand of O^T += Vt · P^T (B[k][n], k = 8 g ..
+//     8 g + 7): no LDS round trip for P.
+//   * The positional band is computed as band^T (rows = table rows, columns =
+//     queries) and stored per query column, 4 rows per ds_write_b128; the key
+//     (r, kt) of lane (g, c16) uses band offset 8 g + 15 - c16 + 2 r + kt:
+//     8 consecutive floats of the lane's own column.
+//   * Scores are carried in log2 units (scaled by log2 e once summed), so a
+//     probability is one v_exp_f32.
+//   * Keys are masked only in blocks that reach past the window or when the
+//     attention is chunk-limited (per-lane key range computed once).
+template <int NWV, int S>
+__global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu((NWV + 3) / 4, (NWV + 3) / 4))) void relpos_attn_t_kernel(
     AttnArgs a, const _Float16 *__restrict__ vt, int Tp) {
-  constexpr int HD = 128, QB = 16 * RT * NWV, KB = 32, BR = QB + 32, UT = RT + 2;  // UT: band tiles per wave
-  constexpr int IT = 16 + BR / 4, IW = IT / NWV;                                  // 1 KB copies per stage / per wave
-  static_assert(IT % NWV == 0, "copies per wave");
-  constexpr int KBYTES = KB * 256, VBYTES = HD * 64, PBYTES = BR * 256;
-  constexpr int STG = KBYTES + VBYTES + PBYTES;  // 56 KB
-  constexpr int SW = 48 + 4, PBS = KB + 8;         // strip row stride (floats), probability row stride (halfs)
-  __shared__ __attribute__((aligned(1024))) char st0[STG];
-  __shared__ __attribute__((aligned(1024))) char st1[STG];
-  __shared__ float sStrip[NWV][RT][16 * SW];
-  __shared__ __attribute__((aligned(16))) _Float16 sP[NWV][RT][16 * PBS];
+  constexpr int HD = 128, QB = 16 * NWV, KB = 32, BR = QB + 32;
+  constexpr int RS = BR + (S - 1) * KB <= 128 ? 128 : 256;  // band ring rows (power of two)
+  static_assert(BR + (S - 1) * KB <= RS, "band ring holds the current band and the prefetched blocks' rows");
+  constexpr int IT0 = 16 + BR / 4, IT1 = 16 + KB / 4;
+  constexpr int IW0 = (IT0 + NWV - 1) / NWV, IW1 = (IT1 + NWV - 1) / NWV;
+  static_assert(IT1 % NWV == 0, "equal copy counts per wave (vmcnt accounting)");
+  constexpr int KBYTES = KB * 256, VBYTES = HD * 64, KVB = KBYTES + VBYTES;
+  constexpr int SW = 48 + 4;  // band strip: [16 query columns][SW floats]
+  constexpr float L2E = 1.4426950408889634f, kLazy = 11.f;  // lazy rescale threshold (log2 units)
+  __shared__ __attribute__((aligned(1024))) char kvs[S][KVB];
+  __shared__ __attribute__((aligned(1024))) char ring[RS * 256];
+  __shared__ __attribute__((aligned(16))) float sStrip[NWV][16 * SW];
 
   const int w = blockIdx.z, h = blockIdx.y, q0 = blockIdx.x * QB;
   const int T = a.win.len[w], off = a.win.off[w];
   if (q0 >= T) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, c16 = lane & 15;
-  const int iw = q0 + wave * 16 * RT;  // this wave's first query (window-local); row tile rt covers iw + 16 rt ..
+  const int iw = q0 + wave * 16;  // this wave's first query (window-local)
+  const int qi = iw + c16;        // this lane's query
   const _Float16 *Q = reinterpret_cast<const _Float16 *>(a.q) + (size_t)off * a.ldq + h * HD;
   const _Float16 *Kp = reinterpret_cast<const _Float16 *>(a.k) + (size_t)off * a.ldk + h * HD;
   const _Float16 *Pp = reinterpret_cast<const _Float16 *>(a.pos) + h * HD;
   const _Float16 *Vt = vt + ((size_t)(w * a.H + h) * HD) * Tp;
-  const uint32_t sadr[2] = {(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)st0),
-                            (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)st1)};
+  const uint32_t sadr0 = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)kvs[0]);
+  const uint32_t radr = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)ring);
   const int pbase0 = a.pcenter - (q0 + QB - 1);
 
-  // 56 copies of 1 KB per stage, 14 per wave: K (8: 4 rows each), Vt (8: 16
-  // rows each), band (40: 4 rows each).
-  auto issue = [&](int sidx, int j0) {
-    const uint32_t base = sadr[sidx];
+  auto issue = [&](int sidx, int j0, int rb, auto first) {
+    constexpr bool F = decltype(first)::value;
+    constexpr int IT = F ? IT0 : IT1, IW = F ? IW0 : IW1, R0 = F ? 0 : BR - KB;
+    const uint32_t base = sadr0 + (uint32_t)sidx * KVB;
 #pragma unroll
     for (int i = 0; i < IW; i++) {
-      const int ins = wave + i * NWV;  // 0..IT-1
+      const int ins = wave + i * NWV;
+      if (IT % NWV != 0 && ins >= IT) break;
       const void *src;
+      uint32_t dst;
       if (ins < 8) {
-        const int r = ins * 4 + (lane >> 4), ch = (lane & 15) ^ (r & 7);
+        const int r = ins * 4 + (lane >> 4), ch = (lane & 15) ^ ((r >> 1) & 7);
         src = Kp + (size_t)min(j0 + r, T - 1) * a.ldk + ch * 8;
+        dst = base + ins * 1024;
       } else if (ins < 16) {
         const int r = (ins - 8) * 16 + (lane >> 2), ch = (lane & 3) ^ ((r >> 1) & 3);
         src = Vt + (size_t)r * Tp + j0 + ch * 8;
+        dst = base + ins * 1024;
       } else {
-        const int r = (ins - 16) * 4 + (lane >> 4), ch = (lane & 15) ^ (r & 7);
-        const int pr = min(max(pbase0 + j0 + r, 0), a.prows - 1);
+        const int x = rb + R0 + (ins - 16) * 4, sl = (x + (lane >> 4)) & (RS - 1), ch = (lane & 15) ^ (sl & 7);
+        const int pr = min(max(pbase0 + j0 - rb + x + (lane >> 4), 0), a.prows - 1);
         src = Pp + (size_t)pr * a.ldp + ch * 8;
+        dst = radr + (uint32_t)(x & (RS - 1)) * 256;
       }
-      attn_dma16(src, base + ins * 1024);
+      attn_dma16(src, dst);
     }
   };
 
-  // A operands: (q+u) and (q+v) for rows iw + 16 rt + c16, d = s*32 + g*8 .. +8
-  h8 qu[RT][4], qv[RT][4];
+  // keys this lane's query sees, and the key blocks the workgroup needs
+  int klo = 0, khi = T - 1, jlo = 0, jhi = T;
+  if (a.chunk > 0) {
+    const int cs = a.chunk * (qi / a.chunk);
+    klo = max(0, cs - a.left);
+    khi = min(T - 1, cs + a.chunk - 1 + a.right);
+    const int qlast = min(T, q0 + QB) - 1;
+    jlo = max(0, a.chunk * (q0 / a.chunk) - a.left);
+    jhi = min(T, a.chunk * (qlast / a.chunk) + a.chunk + a.right);
+  }
+  const int kb0 = jlo / KB, nkb = (jhi + KB - 1) / KB;
+  issue(0, kb0 * KB, 0, std::true_type{});
 #pragma unroll
-  for (int rt = 0; rt < RT; rt++) {
-    const int qi = min(iw + rt * 16 + c16, T - 1);
-    const _Float16 *qr = Q + (size_t)qi * a.ldq;
+  for (int p = 1; p < S - 1; p++)
+    if (kb0 + p < nkb) issue(p, (kb0 + p) * KB, p * KB, std::false_type{});
+
+  // the first blocks' copies are in flight while q is loaded and biased
+  // B operands: (q+u) and (q+v) of this lane's query, d = s*32 + g*8 .. +8
+  h8 qu[4], qv[4];
+  {
+    const _Float16 *qr = Q + (size_t)min(qi, T - 1) * a.ldq;
 #pragma unroll
     for (int s = 0; s < 4; s++) {
       const int d = s * 32 + g * 8;
@@ -294,78 +338,58 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(NWV > 
 #pragma unroll
       for (int e = 0; e < 8; e++) {
         const float xv = (float)x[e];
-        qu[rt][s][e] = (_Float16)(xv + ub[e]);
-        qv[rt][s][e] = (_Float16)(xv + vb[e]);
+        qu[s][e] = (_Float16)(xv + ub[e]);
+        qv[s][e] = (_Float16)(xv + vb[e]);
       }
     }
   }
-  // key blocks this workgroup's queries can see (all keys, or the union of
-  // their chunk windows when attention is chunk-limited)
-  int jlo = 0, jhi = T;
-  if (a.chunk > 0) {
-    const int qlast = min(T, q0 + QB) - 1;
-    jlo = max(0, a.chunk * (q0 / a.chunk) - a.left);
-    jhi = min(T, a.chunk * (qlast / a.chunk) + a.chunk + a.right);
-  }
-  const int kb0 = jlo / KB, nkb = (jhi + KB - 1) / KB;
-  issue(0, kb0 * KB);
 
-  f4 o[RT][8];
+  f4 o[8];  // O^T tiles: d rows t*16 + g*4 + r, query column c16
 #pragma unroll
-  for (int rt = 0; rt < RT; rt++)
-#pragma unroll
-    for (int t = 0; t < 8; t++) o[rt][t] = f4{0.f, 0.f, 0.f, 0.f};
-  float mrow[RT][4], lrow[RT][4];
-#pragma unroll
-  for (int rt = 0; rt < RT; rt++)
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      mrow[rt][r] = -INFINITY;
-      lrow[rt][r] = 0.f;
-    }
-  const int lbw = QB - 16 * RT - wave * 16 * RT;  // band row of this wave's union tile 0 (= the last row tile's first band row)
+  for (int t = 0; t < 8; t++) o[t] = f4{0.f, 0.f, 0.f, 0.f};
+  float mref = -INFINITY, lpart = 0.f;
+  const int lbw = QB - 16 - wave * 16;  // band offset of this wave's union tile 0
+  float *strip = sStrip[wave];
 
   for (int kb = kb0; kb < nkb; kb++) {
-    const int j0 = kb * KB, cur = (kb - kb0) & 1;
-    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0): this stage's copies landed
-    __syncthreads();                                    // ... for every wave; the other stage is free
-    if (kb + 1 < nkb) issue(cur ^ 1, j0 + KB);
-    const char *Ks = cur ? st1 : st0, *Vs = Ks + KBYTES, *Ps = Ks + KBYTES + VBYTES;
+    const int j0 = kb * KB, cur = (kb - kb0) % S;
+    // this block's copies landed: at most min(S - 2, blocks after it) later blocks' copies outstanding
+    const int ahead = min(S - 2, nkb - 1 - kb);
+    if (S > 2 && ahead >= 2) __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8) | (((2 * IW1) & 15) | (((2 * IW1) >> 4) << 14)));
+    else if (S > 2 && ahead == 1) __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8) | ((IW1 & 15) | ((IW1 >> 4) << 14)));
+    else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+    __syncthreads();
+    const int rb = (kb - kb0) * KB;
+    if (kb + S - 1 < nkb) issue((cur + S - 1) % S, j0 + (S - 1) * KB, rb + (S - 1) * KB, std::false_type{});
+    const char *Ks = kvs[cur], *Vs = Ks + KBYTES;
 
-    // fragment reads: K (2 key tiles x 4 k-steps), band (4 union tiles x 4)
-    h8 kf[2][4], pf[UT][4];
+    h8 kf[2][4], pf[3][4];
 #pragma unroll
     for (int kt = 0; kt < 2; kt++) {
-      const int r = kt * 16 + c16;
+      const int r = 2 * c16 + kt;  // MFMA row c16 of key tile kt = key 2 c16 + kt
 #pragma unroll
-      for (int s = 0; s < 4; s++) kf[kt][s] = *reinterpret_cast<const h8 *>(Ks + r * 256 + (((s * 4 + g) ^ (r & 7)) * 16));
+      for (int s = 0; s < 4; s++) kf[kt][s] = *reinterpret_cast<const h8 *>(Ks + r * 256 + (((s * 4 + g) ^ ((r >> 1) & 7)) * 16));
     }
 #pragma unroll
-    for (int u = 0; u < UT; u++) {
-      const int r = lbw + u * 16 + c16;
+    for (int u = 0; u < 3; u++) {
+      const int sl = (rb + lbw + u * 16 + c16) & (RS - 1);
 #pragma unroll
-      for (int s = 0; s < 4; s++) pf[u][s] = *reinterpret_cast<const h8 *>(Ps + r * 256 + (((s * 4 + g) ^ (r & 7)) * 16));
+      for (int s = 0; s < 4; s++) pf[u][s] = *reinterpret_cast<const h8 *>(ring + sl * 256 + (((s * 4 + g) ^ (sl & 7)) * 16));
     }
     __builtin_amdgcn_sched_barrier(0);
-    // row tile rt uses band union tiles (RT - 1 - rt) .. (RT + 1 - rt)
-    f4 sc[RT][2], bd[RT][3];
+    f4 sc[2], bd[3];
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++) {
+    for (int kt = 0; kt < 2; kt++) sc[kt] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kt = 0; kt < 2; kt++) sc[rt][kt] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < 3; u++) bd[u] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ct = 0; ct < 3; ct++) bd[rt][ct] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < 4; s++) {
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++) sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[kt][s], qu[s], sc[kt], 0, 0, 0);
+#pragma unroll
+      for (int u = 0; u < 3; u++) bd[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[u][s], qv[s], bd[u], 0, 0, 0);
     }
-#pragma unroll
-    for (int s = 0; s < 4; s++)
-#pragma unroll
-      for (int rt = 0; rt < RT; rt++) {
-#pragma unroll
-        for (int kt = 0; kt < 2; kt++) sc[rt][kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qu[rt][s], kf[kt][s], sc[rt][kt], 0, 0, 0);
-#pragma unroll
-        for (int ct = 0; ct < 3; ct++) bd[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qv[rt][s], pf[RT - 1 - rt + ct][s], bd[rt][ct], 0, 0, 0);
-      }
-    // V fragments (d rows t*16 + c16, keys g*8 .. +8), read now to hide behind the softmax
+    // Vt fragments (d rows t*16 + c16, keys g*8 .. +8), read now to hide behind the softmax
     h8 vf[8];
 #pragma unroll
     for (int t = 0; t < 8; t++) {
@@ -373,104 +397,70 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(NWV > 
       vf[t] = *reinterpret_cast<const h8 *>(Vs + d * 64 + ((g ^ ((d >> 1) & 3)) * 16));
     }
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++)
-#pragma unroll
-      for (int ct = 0; ct < 3; ct++)
-#pragma unroll
-        for (int rr = 0; rr < 4; rr++) sStrip[wave][rt][(g * 4 + rr) * SW + ct * 16 + c16] = bd[rt][ct][rr];
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): strip writes done (wave-private strips)
+    for (int u = 0; u < 3; u++) *reinterpret_cast<f4 *>(strip + c16 * SW + u * 16 + g * 4) = bd[u];
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): strip written (wave-private)
     __builtin_amdgcn_wave_barrier();
-    // S = ac + band[i][jj + 15 - (i - ib)], keys >= T masked, online softmax.
-    // Lazy rescaling: probabilities are taken against a per-row reference
-    // max mref that only moves (rescaling l and O) when some row's running
-    // max exceeds it by more than kLazy nats, decided wave-wide; p <= e^kLazy
-    // stays well inside f16 range with unchanged relative precision.
-    constexpr float kLazy = 8.f;
-    float sv[RT][4][2];
-    bool need = false;
+    float sv[8];  // keys 8 g + e of this lane's query (e = 2 r + kt)
+    {
+      const float *bp = strip + c16 * SW + 8 * g + 15 - c16;
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++) {
-      const float *strip = sStrip[wave][rt];
+      for (int r = 0; r < 4; r++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int ri = g * 4 + r;
-        float v0 = sc[rt][0][r] + strip[ri * SW + c16 + 15 - ri];
-        float v1 = sc[rt][1][r] + strip[ri * SW + 16 + c16 + 15 - ri];
-        int klo = 0, khi = T - 1;  // keys this query sees
-        if (a.chunk > 0) {
-          const int i = iw + rt * 16 + ri, cs = a.chunk * (i / a.chunk);
-          klo = max(klo, cs - a.left);
-          khi = min(khi, cs + a.chunk - 1 + a.right);
-        }
-        v0 = (j0 + c16 >= klo && j0 + c16 <= khi) ? v0 : -INFINITY;
-        v1 = (j0 + 16 + c16 >= klo && j0 + 16 + c16 <= khi) ? v1 : -INFINITY;
-        sv[rt][r][0] = v0;
-        sv[rt][r][1] = v1;
-        need |= fmaxf(v0, v1) > mrow[rt][r] + kLazy;
+        for (int kt = 0; kt < 2; kt++) sv[2 * r + kt] = (sc[kt][r] + bp[2 * r + kt]) * L2E;
+    }
+    if (j0 + KB > T || a.chunk > 0) {
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const int j = j0 + 8 * g + e;
+        sv[e] = (j >= klo && j <= khi) ? sv[e] : -INFINITY;
       }
     }
-    if (__builtin_amdgcn_ballot_w64(need)) {
+    float mx = sv[0];
 #pragma unroll
-      for (int rt = 0; rt < RT; rt++)
+    for (int e = 1; e < 8; e++) mx = fmaxf(mx, sv[e]);
+    if (__builtin_amdgcn_ballot_w64(mx > mref + kLazy)) {
+      // new reference max for every query whose running max moved: the
+      // query's 4 lane groups agree through the xor-16 / xor-32 exchange
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      if (mx > mref) {
+        const float corr = __builtin_amdgcn_exp2f(mref - mx);  // 0 on the first visible block (mref = -inf)
+        lpart *= corr;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const float mx = row16_max(fmaxf(sv[rt][r][0], sv[rt][r][1]));
-          if (mx > mrow[rt][r]) {
-            const float corr = __expf(mrow[rt][r] - mx);  // 0 on the first key block (mref = -inf)
-            lrow[rt][r] *= corr;  // per-lane partial sums scale with their row
-#pragma unroll
-            for (int t = 0; t < 8; t++) o[rt][t][r] *= corr;
-            mrow[rt][r] = mx;
-          }
-        }
-    }
-#pragma unroll
-    for (int rt = 0; rt < RT; rt++) {
-      _Float16 *pb = sP[wave][rt];
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int ri = g * 4 + r;
-        // masked keys give 0 (also while a row has seen no visible key yet: -inf - -inf)
-        const float p0 = sv[rt][r][0] == -INFINITY ? 0.f : __expf(sv[rt][r][0] - mrow[rt][r]);
-        const float p1 = sv[rt][r][1] == -INFINITY ? 0.f : __expf(sv[rt][r][1] - mrow[rt][r]);
-        pb[ri * PBS + c16] = (_Float16)p0;
-        pb[ri * PBS + 16 + c16] = (_Float16)p1;
-        lrow[rt][r] += p0 + p1;  // per-lane partial; rows reduced once after the last key block
+        for (int t = 0; t < 8; t++) o[t] *= corr;
+        mref = mx;
       }
     }
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
-    // O += P·V
+    h8 pb;
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++) {
-      const h8 pa = *reinterpret_cast<const h8 *>(&sP[wave][rt][c16 * PBS + g * 8]);
-#pragma unroll
-      for (int t = 0; t < 8; t++) o[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vf[t], o[rt][t], 0, 0, 0);
+    for (int e = 0; e < 8; e++) {
+      // masked keys give 0 (also while the query has seen no visible key: -inf - -inf)
+      const float p = sv[e] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sv[e] - mref);
+      lpart += p;
+      pb[e] = (_Float16)p;
     }
+#pragma unroll
+    for (int t = 0; t < 8; t++) o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[t], pb, o[t], 0, 0, 0);
   }
 
-  _Float16 *O = reinterpret_cast<_Float16 *>(a.out) + (size_t)off * a.ldo + h * HD;
-  _Float16 *Olo = a.out_lo ? reinterpret_cast<_Float16 *>(a.out_lo) + (size_t)off * a.ldo + h * HD : nullptr;
-  float lsum[RT][4];  // row sums, reduced with every lane active
+  float lsum = lpart + __shfl_xor(lpart, 16);
+  lsum += __shfl_xor(lsum, 32);
+  if (qi >= T) return;
+  const float inv = 1.f / lsum;
+  _Float16 *O = reinterpret_cast<_Float16 *>(a.out) + (size_t)(off + qi) * a.ldo + h * HD + g * 4;
+  _Float16 *Olo = a.out_lo ? reinterpret_cast<_Float16 *>(a.out_lo) + (size_t)(off + qi) * a.ldo + h * HD + g * 4 : nullptr;
 #pragma unroll
-  for (int rt = 0; rt < RT; rt++)
-#pragma unroll
-    for (int r = 0; r < 4; r++) lsum[rt][r] = row16_sum(lrow[rt][r]);
-#pragma unroll
-  for (int rt = 0; rt < RT; rt++)
+  for (int t = 0; t < 8; t++) {
+    h4 hi, lo;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-      const int i = iw + rt * 16 + g * 4 + r;
-      if (i >= T) continue;
-      const float inv = 1.f / lsum[rt][r];
-#pragma unroll
-      for (int t = 0; t < 8; t++) {
-        const float v = o[rt][t][r] * inv;
-        const _Float16 hi = (_Float16)v;
-        O[(size_t)i * a.ldo + t * 16 + c16] = hi;
-        if (Olo) Olo[(size_t)i * a.ldo + t * 16 + c16] = (_Float16)(v - (float)hi);
-      }
+      const float v = o[t][r] * inv;
+      hi[r] = (_Float16)v;
+      lo[r] = (_Float16)(v - (float)hi[r]);
     }
+    *reinterpret_cast<h4 *>(O + t * 16) = hi;
+    if (Olo) *reinterpret_cast<h4 *>(Olo + t * 16) = lo;
+  }
 }
 
 int relpos_attention_f16(fa_ctx *ctx, const AttnArgs &a, int Tmax, _Float16 *vt, const char *label, bool transpose) {
@@ -489,14 +479,9 @@ int relpos_attention_f16(fa_ctx *ctx, const AttnArgs &a, int Tmax, _Float16 *vt,
     FA_TRY(check_launch(ctx, "v_transpose"));
   }
   ProfScope ps(ctx, label);
-  // FA_ATTN=1: 128-query workgroups (4 waves x 2 row tiles); default: 96-query
-  // workgroups (6 waves x 1 row tile, 1.5 waves per SIMD, and a 188-frame
-  // window splits 96 + 92 instead of 128 + 60)
-  const char *ev = getenv("FA_ATTN");
-  if (ev && ev[0] == '1')
-    FA_LAUNCH(ps, (relpos_attn_lds_kernel<2, 4>), dim3(cdiv(Tmax, 128), a.H, W), dim3(256), 0, ctx->stream, a, (const _Float16 *)vt, Tp);
-  else
-    FA_LAUNCH(ps, (relpos_attn_lds_kernel<1, 6>), dim3(cdiv(Tmax, 96), a.H, W), dim3(384), 0, ctx->stream, a, (const _Float16 *)vt, Tp);
+  // 96-query workgroups (6 waves, 1.5 per SIMD; a 188-frame window splits
+  // 96 + 92), K / Vt / band copies one block ahead
+  FA_LAUNCH(ps, (relpos_attn_t_kernel<6, 2>), dim3(cdiv(Tmax, 96), a.H, W), dim3(384), 0, ctx->stream, a, (const _Float16 *)vt, Tp);
   return check_launch(ctx, label);
 }
 
@@ -517,3 +502,4 @@ int relpos_attention(fa_ctx *ctx, const AttnArgs &a, int in_f32, int out_f32, in
 }
 
 }  // namespace fa
+

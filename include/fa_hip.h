@@ -342,7 +342,9 @@ void fa_encoder_destroy(fa_encoder *enc);
  * weight fragment, or (FA_EXACT_GLU) keeps it f32.  No counterpart in the
  * reference (its f16 route keeps f16 partial sums, gemm.js:380-391); this is
  * how the f16 encoder holds the fp32 path's frame-wise decisions.  Every
- * weight format takes every mask; the default is the same for all formats.
+ * weight format takes every mask.  Default: attention / GLU / depthwise
+ * outputs exact in every layer; in the last 8 layers also the LayerNorm
+ * outputs, and for int8 / int4 weights the FF hidden state too.
  * Layers [first, last] get `mask`. */
 enum fa_exact_bits {
   FA_EXACT_LN_OUT = 1,    /* LayerNorm outputs -> FF W1, q|k|v, pw1 */

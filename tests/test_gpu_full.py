@@ -83,9 +83,9 @@ def test_set_exact_validation(ctx, fa, full_weights):
     with pytest.raises(fa.FaError):
         enc.setExact(1, 1, 5)
     enc.close()
-    for fmt in ("int8", "int4"):  # quantised weights take the same masks and default
+    for fmt in ("int8", "int4"):  # quantised weights take the same masks; their default tail is all-exact
         q = fa.FusedEncoder(ctx, lw, fmt, max_T=64)
-        assert q.exact(0) == 29 and q.exact(1) == 29
+        assert q.exact(0) == 31 and q.exact(1) == 31
         q.setExact(1)
         assert q.exact(0) == 1
         q.close()
