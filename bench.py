@@ -636,7 +636,11 @@ def bench_copy(args, fa, ctx):
 
 def bench_gemv(args, fa, ctx):
     """configs[4] GEMV: M in {1,4,16} x K=1024 x N=4096, int8 / int4 weights,
-    distinct weight buffers rotated (> 256 MB total) so the MALL cannot serve them."""
+    distinct weight buffers rotated (> 256 MB total) so the MALL cannot serve
+    them: one call per buffer (fa_gemv_quant), and all buffers in one batched
+    call (fa_gemv_quant_batch, launches of <= 48 buffers).  gbs = algorithmic
+    bytes (weights + scales + activations + outputs) / kernel time; wall_gbs
+    over the host-timed calls."""
     K, N = 1024, 4096
     rng = np.random.default_rng(1)
     out = {}
@@ -673,6 +677,29 @@ def bench_gemv(args, fa, ctx):
             out[f"{fmt}_M{M}"] = {"avg_us": round(avg * 1e3, 2), "gbs": round(by / (avg * 1e-3) / 1e9, 1),
                                   "frac": round(by / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                                   "wall_us_per_call": round(wall / (reps * nbuf) * 1e6, 2), "buffers": nbuf}
+            # all buffers in one batched call (launches of <= 48 weight buffers)
+            alist = [a] * nbuf
+
+            def bcall():
+                ar = ctx.pushArena()
+                ctx.gemvQuantBatch(alist, ws, ss, code, N, K)
+                ctx.popArena(ar)
+
+            bcall()
+            ctx.sync()
+            ctx.startProfile(100000)
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                bcall()
+            ctx.sync()
+            bwall = time.perf_counter() - t0
+            prof = ctx.endProfile()
+            kms = sum(r["ms"] for r in prof if r["label"].startswith("gemv_batch"))
+            nl = sum(1 for r in prof if r["label"].startswith("gemv_batch"))
+            btot = by * nbuf * reps
+            out[f"{fmt}_M{M}_batched"] = {"launches_per_call": nl // reps, "kernel_us_per_launch": round(kms / nl * 1e3, 2),
+                                          "gbs": round(btot / (kms * 1e-3) / 1e9, 1), "frac": round(btot / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                          "wall_gbs": round(btot / bwall / 1e9, 1), "buffers": nbuf}
     print(json.dumps({"metric": "weight-only quantised GEMV HBM GB/s", "workload": "configs[4] GEMV K=1024 N=4096", "results": out}), flush=True)
 
 

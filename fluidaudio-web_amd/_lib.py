@@ -100,6 +100,7 @@ SIGNATURES = [
     ("fa_dequant_int4", I, [P, T, T, I, I, C.POINTER(T)]),
     ("fa_quantize_weights", I, [I, F32P, I, I, C.c_void_p, C.c_void_p]),
     ("fa_gemv_quant", I, [P, T, T, T, I, I, I, C.POINTER(T)]),
+    ("fa_gemv_quant_batch", I, [P, I, C.POINTER(T), C.POINTER(T), C.POINTER(T), I, I, I, C.POINTER(T)]),
     ("fa_pack_windows", I, [P, T, I32P, I32P, I, I, C.POINTER(T)]),
     ("fa_mel_windows", I, [P, T, I32P, I32P, I, I, C.c_double, I, C.POINTER(T)]),
     ("fa_leaky_relu", I, [P, T, C.c_double, C.POINTER(T)]),

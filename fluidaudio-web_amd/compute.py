@@ -509,6 +509,17 @@ class HipContext:
         check(self._p, lib().fa_gemv_quant(self._p, a.h, w.h, scales.h, fmt, N, K, C.byref(o)))
         return HipTensor(self, o.value, a.rows, N)
 
+    def gemvQuantBatch(self, a_list, w_list, s_list, fmt, N, K):
+        """len(w_list) independent GEMVs in one launch per 48 items; returns
+        [count*M, N] (item i at rows i*M ..)."""
+        n = len(w_list)
+        if not (len(a_list) == len(s_list) == n):
+            raise ValueError("gemvQuantBatch: one a, w and scales per item")
+        arr = lambda xs: (L.T * n)(*[x.h for x in xs])
+        o = self._out()
+        check(self._p, lib().fa_gemv_quant_batch(self._p, n, arr(a_list), arr(w_list), arr(s_list), fmt, N, K, C.byref(o)))
+        return HipTensor(self, o.value, n * a_list[0].rows, N)
+
     # ── ragged windows ────────────────────────────────────────────────────
     def packWindows(self, feats, starts, lens, layout="packed"):
         s = np.ascontiguousarray(starts, np.int32)

@@ -84,4 +84,32 @@ __device__ __forceinline__ int xcd_remap(int bid, int n) {
   return base + local;
 }
 
+// int8 weights -> f16 pairs, exactly: with x = w ^ 0x80808080 each byte is
+// b + 128, and the f16 with bits 0x64XX is 1024 + XX, so two byte_perms and a
+// packed f16 subtract of 1152 give b for four bytes.
+__device__ __forceinline__ h8 i8x8_to_h8(uint2 w) {
+  const uint32_t x0 = w.x ^ 0x80808080u, x1 = w.y ^ 0x80808080u;
+  const h2 off = h2{(_Float16)1152.f, (_Float16)1152.f};
+  const h2 a = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u)) - off;
+  const h2 b = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, x0, 0x04030402u)) - off;
+  const h2 c = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u)) - off;
+  const h2 d = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u)) - off;
+  return h8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// 8 int4 weights (low nibble = even k) of one group-32 block -> f16
+// (q - 8) * s, rounded once: nibbles are placed under an 0x64 high byte
+// (f16 1024 + q), 1032 is subtracted exactly and the packed f16 multiply by
+// the block scale rounds the exact product -- the value the register-staged
+// route computes in f32 and rounds.
+__device__ __forceinline__ h8 i4x8_to_h8(uint32_t u, _Float16 s) {
+  const uint32_t lo = u & 0x0F0F0F0Fu, hi = (u >> 4) & 0x0F0F0F0Fu;
+  const h2 off = h2{(_Float16)1032.f, (_Float16)1032.f}, sc = h2{s, s};
+  const h2 a = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(hi, lo, 0x0C040C00u) | 0x64006400u) - off) * sc;
+  const h2 b = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(hi, lo, 0x0C050C01u) | 0x64006400u) - off) * sc;
+  const h2 c = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(hi, lo, 0x0C060C02u) | 0x64006400u) - off) * sc;
+  const h2 d = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(hi, lo, 0x0C070C03u) | 0x64006400u) - off) * sc;
+  return h8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
 }  // namespace fa

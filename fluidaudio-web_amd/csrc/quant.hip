@@ -38,104 +38,123 @@ struct GemvArgs {
   int act;
 };
 
-// 16 output columns per workgroup; wave w takes the 64-k chunks w, w+4, ...
-// All of a lane's weight loads (16 k of its column per chunk) are issued
-// before any MFMA so the workgroup's whole weight slice is in flight at once;
-// the activations are read straight from global (L1/L2: every workgroup reads
-// the same M x K block) as MFMA A fragments, rows >= M being register zeros.
-template <int FMT>
-__device__ __forceinline__ void gemv_dequant(const GemvArgs &p, int n, int kb, const uint4 &u8, const uint2 &u4, h8 &b0, h8 &b1) {
-  if constexpr (FMT == 1) {
-    const uint32_t w[4] = {u8.x, u8.y, u8.z, u8.w};
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-      b0[e] = (_Float16)(float)(int8_t)((w[e >> 2] >> (8 * (e & 3))) & 0xff);
-      b1[e] = (_Float16)(float)(int8_t)((w[2 + (e >> 2)] >> (8 * (e & 3))) & 0xff);
-    }
-  } else {
-    const int blk = kb >> 5, nblk = p.K >> 5;
-    float s, zp = 8.f;
-    if constexpr (FMT == 2) {
-      s = (float)reinterpret_cast<const _Float16 *>(p.scales)[(size_t)n * nblk + blk];
-    } else {
-      s = reinterpret_cast<const float *>(p.scales)[(size_t)n * nblk + blk];
-      const uint8_t zb = p.zp[(size_t)n * p.zpb + (blk >> 1)];
-      zp = (float)((blk & 1) ? (zb >> 4) : (zb & 0xf));
-    }
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-      b0[e] = (_Float16)(((float)((u4.x >> (4 * e)) & 0xf) - zp) * s);
-      b1[e] = (_Float16)(((float)((u4.y >> (4 * e)) & 0xf) - zp) * s);
-    }
-  }
-}
-
-__device__ __forceinline__ h8 gemv_a8(const float *a) {
-  const float4 x = reinterpret_cast<const float4 *>(a)[0], y = reinterpret_cast<const float4 *>(a)[1];
-  return h8{(_Float16)x.x, (_Float16)x.y, (_Float16)x.z, (_Float16)x.w, (_Float16)y.x, (_Float16)y.y, (_Float16)y.z, (_Float16)y.w};
-}
-
-template <int FMT>
-__global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs p) {
-  constexpr int CB = 4;  // chunks per wave held in flight together
-  __shared__ f4 sPart[4][64];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n0 = blockIdx.x * 16;
+// Workgroup = NWB x KS waves: NWB column groups of 16 output columns, each
+// K range split over KS waves (partial sums reduced through LDS).  The
+// activations (M <= 16 rows) are staged once per workgroup in LDS as f16
+// ([16][K + 8]), so every MFMA A fragment is one
+// ds_read_b128.  Lane (g, c16) of a wave streams 64 contiguous weight bytes
+// of its column per chunk together with the other three lanes of the
+// column: int8 16 B = 16 k (chunk = 64 k), int4 16 B = 32 k, one group-32
+// block with one scale (chunk = 128 k).  The k order inside a chunk is
+// permuted identically for weights and activations (lane g's k values feed
+// MFMA k slots g*8 .. g*8 + 7 of successive MFMAs).  Chunks go in groups of
+// CB whose loads are all issued before the group's first MFMA (the first
+// group's while the activations are staged).  Dequantisation is exact and
+// the same as the GEMM route's (i8x8_to_h8, i4x8_to_h8: (q - 8)·s rounded
+// once to f16); the int8 column scale is applied to the f32 sum.
+template <int FMT, int NWB, int KS>
+__device__ __forceinline__ void gemv_tile(const GemvArgs &p, int n0, _Float16 *sA) {
+  constexpr int CB = FMT == 1 ? 16 : 8;   // chunks per load group
+  constexpr int CK = FMT == 1 ? 64 : 128;  // k per chunk
+  constexpr int NM = FMT == 1 ? 2 : 4;     // MFMAs per chunk
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wc = wave % NWB, wk = wave / NWB;
   const int c16 = lane & 15, g = lane >> 4;
-  const int n = min(n0 + c16, p.N - 1);
-  const bool arow = c16 < p.M;
-  const float *arow_p = p.A + (size_t)min(c16, p.M - 1) * p.K;
-  f4 acc = f4{0.f, 0.f, 0.f, 0.f};
-  const int nch = p.K / 64;
-  for (int c0 = wave; c0 < nch; c0 += 4 * CB) {
-    uint4 w8[CB];
-    uint2 w4[CB];
+  const int K = p.K, KP = K + 8, nch = K / CK, nblk = K >> 5;
+  const int cb = wk * nch / KS, ce = (wk + 1) * nch / KS;  // this wave's chunks
+  const int n = min(n0 + wc * 16 + c16, p.N - 1);
+  const uint8_t *Wc = reinterpret_cast<const uint8_t *>(p.W) + (size_t)n * (FMT == 1 ? K : K >> 1) + g * 16;
+  const _Float16 *S4 = reinterpret_cast<const _Float16 *>(p.scales) + (size_t)n * nblk + g;
+  uint4 w[CB];
+  _Float16 s4[CB];
+  auto load = [&](int c0) {
 #pragma unroll
     for (int i = 0; i < CB; i++) {
-      const int ch = c0 + 4 * i;
-      if (ch < nch) {
-        const int kb = ch * 64 + g * 16;
-        if constexpr (FMT == 1)
-          w8[i] = *reinterpret_cast<const uint4 *>(reinterpret_cast<const int8_t *>(p.W) + (size_t)n * p.K + kb);
-        else
-          w4[i] = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint8_t *>(p.W) + (size_t)n * (p.K >> 1) + (kb >> 1));
-      }
+      const int ch = min(c0 + i, ce - 1);  // past the range: a repeat, never used
+      w[i] = *reinterpret_cast<const uint4 *>(Wc + ch * 64);
+      if constexpr (FMT == 2) s4[i] = S4[ch * 4];
     }
-#pragma unroll
-    for (int i = 0; i < CB; i++) {
-      const int ch = c0 + 4 * i;
-      if (ch < nch) {
-        const int kb = ch * 64 + g * 16;
-        h8 b0, b1;
-        gemv_dequant<FMT>(p, n, kb, w8[i], w4[i], b0, b1);
-        h8 a0 = h8{0, 0, 0, 0, 0, 0, 0, 0}, a1 = a0;
-        if (arow) {
-          a0 = gemv_a8(arow_p + kb);
-          a1 = gemv_a8(arow_p + kb + 8);
-        }
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b0, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b1, acc, 0, 0, 0);
-      }
-    }
+  };
+  if (cb < ce) load(cb);  // the first group's weights stream while the activations are staged
+  // f32 [M][K] -> f16 rows of [16][KP]; rows >= M stay unwritten: they only
+  // feed MFMA output rows >= M, which are never stored
+  for (int idx = tid; idx < p.M * (K / 4); idx += 64 * NWB * KS) {
+    const int r = idx / (K / 4), c = (idx - r * (K / 4)) * 4;
+    const float4 v = *reinterpret_cast<const float4 *>(p.A + (size_t)r * K + c);
+    *reinterpret_cast<h4 *>(sA + r * KP + c) = h4{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
   }
-  sPart[wave][lane] = acc;
   __syncthreads();
-  if (wave != 0) return;
-  f4 t = sPart[0][lane];
+  f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+  const _Float16 *arow = sA + c16 * KP + g * (CK / 4);
+  for (int c0 = cb; c0 < ce; c0 += CB) {
+    if (c0 > cb) load(c0);
 #pragma unroll
-  for (int w = 1; w < 4; w++) {
-    const f4 o = sPart[w][lane];
-    t[0] += o[0]; t[1] += o[1]; t[2] += o[2]; t[3] += o[3];
+    for (int i = 0; i < CB; i++) {
+      const int ch = c0 + i;
+      if (ch < ce) {
+        const uint32_t u[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+#pragma unroll
+        for (int j = 0; j < NM; j++) {
+          const h8 b = FMT == 1 ? i8x8_to_h8(uint2{u[2 * j], u[2 * j + 1]}) : i4x8_to_h8(u[j], s4[i]);
+          const h8 a = *reinterpret_cast<const h8 *>(arow + ch * CK + j * 8);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
+        }
+      }
+    }
   }
-  const int col = n0 + c16;
+  if constexpr (KS > 1) {  // partial sums of the K splits -> wave row wk = 0
+    f4 *part = reinterpret_cast<f4 *>(sA + 16 * KP);
+    if (wk > 0) part[((wk - 1) * NWB + wc) * 64 + lane] = acc;
+    __syncthreads();
+    if (wk > 0) return;
+#pragma unroll
+    for (int k = 1; k < KS; k++) {
+      const f4 o = part[((k - 1) * NWB + wc) * 64 + lane];
+      acc[0] += o[0]; acc[1] += o[1]; acc[2] += o[2]; acc[3] += o[3];
+    }
+  }
+  const int col = n0 + wc * 16 + c16;
   if (col >= p.N) return;
   const float cs = FMT == 1 ? reinterpret_cast<const float *>(p.scales)[col] : 1.f;
   const float bv = p.bias ? p.bias[col] : 0.f;
 #pragma unroll
   for (int r = 0; r < 4; r++) {
     const int m = g * 4 + r;
-    if (m < p.M) p.Y[(size_t)m * p.N + col] = act_apply(t[r] * cs + bv, p.act);
+    if (m < p.M) p.Y[(size_t)m * p.N + col] = act_apply(acc[r] * cs + bv, p.act);
   }
+}
+
+// one product: 16 columns per workgroup, K split over 4 waves (N / 16
+// workgroups fill the chip for the encoder's widths)
+template <int FMT>
+__global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs p) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 gemv_sA[];
+  gemv_tile<FMT, 1, 4>(p, blockIdx.x * 16, gemv_sA);
+}
+
+constexpr int kGemvWaves = 8;  // batched: 128 columns per workgroup, whole K per wave
+// Many independent products of one shape in one launch (blockIdx.y = item):
+// the weight streams of all items are in flight together, so the launch runs
+// at the HBM rate instead of one small matrix's latency.
+constexpr int kGemvBatchItems = 48;
+struct GemvItem {
+  const float *A;
+  const void *W;
+  const void *scales;
+  float *Y;
+};
+struct GemvBatch {
+  GemvItem it[kGemvBatchItems];
+};
+template <int FMT>
+__global__ __launch_bounds__(64 * kGemvWaves) void gemv_batch_kernel(GemvArgs base, GemvBatch b) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 gemv_sA[];
+  const GemvItem &it = b.it[blockIdx.y];
+  GemvArgs p = base;
+  p.A = it.A;
+  p.W = it.W;
+  p.scales = it.scales;
+  p.Y = it.Y;
+  gemv_tile<FMT, kGemvWaves, 1>(p, blockIdx.x * 16 * kGemvWaves, gemv_sA);
 }
 
 // any-shape fallback: one thread per output, f32 math
@@ -171,37 +190,46 @@ __global__ void gemv_naive_kernel(GemvArgs p, int fmt) {
   p.Y[idx] = act_apply(acc, p.act);
 }
 
+static inline bool gemv_mfma_ok(int fmt, int M, int K) { return (fmt == 1 || fmt == 2) && M <= 64 && K % 128 == 0 && K <= 4096; }
+static inline size_t gemv_lds(int K) { return (size_t)16 * (K + 8) * 2 + 3 * 64 * 16; }  // + the K-split partial sums
+// the staged activations take up to 16 x 4104 halfs (131 KB) of dynamic LDS,
+// beyond the default 64 KB launch limit: raise it once per process
+static int gemv_prepare(fa_ctx *ctx) {
+  static int st = -1;
+  if (st < 0) {
+    const int lim = 160 * 1024;
+    st = (hipFuncSetAttribute((const void *)gemv_mfma_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize, lim) == hipSuccess &&
+          hipFuncSetAttribute((const void *)gemv_mfma_kernel<2>, hipFuncAttributeMaxDynamicSharedMemorySize, lim) == hipSuccess &&
+          hipFuncSetAttribute((const void *)gemv_batch_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize, lim) == hipSuccess &&
+          hipFuncSetAttribute((const void *)gemv_batch_kernel<2>, hipFuncAttributeMaxDynamicSharedMemorySize, lim) == hipSuccess)
+             ? 1
+             : 0;
+  }
+  return st ? FA_OK : set_err(ctx, FA_E_DEVICE, "gemv: raising the dynamic LDS limit failed");
+}
+
 static int gemv_launch(fa_ctx *ctx, const GemvArgs &p, int fmt, const char *label) {
   if (p.M <= 0 || p.N <= 0) return FA_OK;
-  const bool single = !(p.M > 16 && p.M <= 64 && p.K % 64 == 0);
-  ProfScope ps(ctx, label, single);
-  if (p.M <= 16 && p.K % 64 == 0) {
-    const size_t shm = 0;
+  if (gemv_mfma_ok(fmt, p.M, p.K)) {
+    FA_TRY(gemv_prepare(ctx));
+    // 16-row slabs (one launch for M <= 16)
     const dim3 grid(cdiv(p.N, 16));
-    if (fmt == 1)
-      FA_LAUNCH(ps, gemv_mfma_kernel<1>, grid, dim3(256), shm, ctx->stream, p);
-    else if (fmt == 2)
-      FA_LAUNCH(ps, gemv_mfma_kernel<2>, grid, dim3(256), shm, ctx->stream, p);
-    else
-      FA_LAUNCH(ps, gemv_mfma_kernel<3>, grid, dim3(256), shm, ctx->stream, p);
-  } else if (p.M <= 64 && p.K % 64 == 0) {
-    // M in (16, 64]: run 16-row slabs
     for (int m0 = 0; m0 < p.M; m0 += 16) {
       GemvArgs q = p;
       q.A = p.A + (size_t)m0 * p.K;
       q.Y = p.Y + (size_t)m0 * p.N;
       q.M = p.M - m0 < 16 ? p.M - m0 : 16;
-      const size_t shm = 0;
+      ProfScope ps(ctx, label, true);
       if (fmt == 1)
-        hipLaunchKernelGGL(gemv_mfma_kernel<1>, dim3(cdiv(p.N, 16)), dim3(256), shm, ctx->stream, q);
-      else if (fmt == 2)
-        hipLaunchKernelGGL(gemv_mfma_kernel<2>, dim3(cdiv(p.N, 16)), dim3(256), shm, ctx->stream, q);
+        FA_LAUNCH(ps, gemv_mfma_kernel<1>, grid, dim3(256), gemv_lds(p.K), ctx->stream, q);
       else
-        hipLaunchKernelGGL(gemv_mfma_kernel<3>, dim3(cdiv(p.N, 16)), dim3(256), shm, ctx->stream, q);
+        FA_LAUNCH(ps, gemv_mfma_kernel<2>, grid, dim3(256), gemv_lds(p.K), ctx->stream, q);
+      FA_TRY(check_launch(ctx, label));
     }
-  } else {
-    FA_LAUNCH(ps, gemv_naive_kernel, dim3(cdiv((long)p.M * p.N, 256)), dim3(256), 0, ctx->stream, p, fmt);
+    return FA_OK;
   }
+  ProfScope ps(ctx, label, true);
+  FA_LAUNCH(ps, gemv_naive_kernel, dim3(cdiv((long)p.M * p.N, 256)), dim3(256), 0, ctx->stream, p, fmt);
   return check_launch(ctx, label);
 }
 
@@ -233,6 +261,51 @@ extern "C" int fa_gemv_quant(fa_ctx *ctx, fa_tensor a, fa_tensor w, fa_tensor sc
   FA_TRY(new_tensor(ctx, M, N, S_F32, (size_t)M * N * 4, &o, &ro));
   ra = get(ctx, a); rw = get(ctx, w); rs = get(ctx, scales);
   FA_TRY(gemv_quant_launch(ctx, (const float *)ra->ptr, rw->ptr, rs->ptr, format, M, N, K, (float *)ro->ptr, nullptr, 0, format == 1 ? "gemv_int8" : "gemv_int4"));
+  *out = o;
+  return FA_OK;
+}
+
+extern "C" int fa_gemv_quant_batch(fa_ctx *ctx, int count, const fa_tensor *a, const fa_tensor *w, const fa_tensor *scales, int format, int N, int K,
+                                   fa_tensor *out) {
+  if (!ctx || !out || count <= 0 || !a || !w || !scales) return ctx ? set_err(ctx, FA_E_INVALID, "gemvQuantBatch: %d items", count) : FA_E_INVALID;
+  if (format != 1 && format != 2) return set_err(ctx, FA_E_INVALID, "gemvQuantBatch: format %d", format);
+  if (K % 128 != 0 || K > 4096 || N <= 0) return set_err(ctx, FA_E_UNSUPPORTED, "gemvQuantBatch: K=%d must be a multiple of 128, <= 4096", K);
+  const size_t wbytes = format == 1 ? (size_t)N * K : (size_t)N * (K / 32) * 16;
+  const size_t sbytes = format == 1 ? (size_t)N * 4 : (size_t)N * (K / 32) * 2;
+  int M = -1;
+  for (int i = 0; i < count; i++) {
+    TensorRec *ra, *rw, *rs;
+    FA_TRY(need(ctx, a[i], &ra, "gemvQuantBatch a"));
+    FA_TRY(need(ctx, w[i], &rw, "gemvQuantBatch w"));
+    FA_TRY(need(ctx, scales[i], &rs, "gemvQuantBatch scales"));
+    if (ra->kind != S_F32 || ra->cols != K || (M >= 0 && ra->rows != M))
+      return set_err(ctx, FA_E_INVALID, "gemvQuantBatch: item %d: a must be f32 [M,%d] with one M for all items", i, K);
+    M = ra->rows;
+    if (rw->bytes < wbytes || rs->bytes < sbytes) return set_err(ctx, FA_E_INVALID, "gemvQuantBatch: item %d: weight / scale buffer too small", i);
+  }
+  if (M < 1 || M > 16) return set_err(ctx, FA_E_UNSUPPORTED, "gemvQuantBatch: M=%d (1..16)", M);
+  FA_TRY(gemv_prepare(ctx));
+  fa_tensor o;
+  TensorRec *ro;
+  FA_TRY(new_tensor(ctx, count * M, N, S_F32, (size_t)count * M * N * 4, &o, &ro));
+  float *Y = (float *)ro->ptr;
+  GemvArgs base{nullptr, M, K, N, nullptr, nullptr, nullptr, 0, nullptr, nullptr, 0};
+  const char *label = format == 1 ? "gemv_batch_int8" : "gemv_batch_int4";
+  for (int i0 = 0; i0 < count; i0 += kGemvBatchItems) {
+    const int nb = std::min(kGemvBatchItems, count - i0);
+    GemvBatch b{};
+    for (int j = 0; j < nb; j++) {
+      const int i = i0 + j;
+      b.it[j] = {(const float *)get(ctx, a[i])->ptr, get(ctx, w[i])->ptr, get(ctx, scales[i])->ptr, Y + (size_t)i * M * N};
+    }
+    ProfScope ps(ctx, label);
+    const dim3 grid(cdiv(N, 16 * kGemvWaves), nb);
+    if (format == 1)
+      FA_LAUNCH(ps, gemv_batch_kernel<1>, grid, dim3(64 * kGemvWaves), gemv_lds(K), ctx->stream, base, b);
+    else
+      FA_LAUNCH(ps, gemv_batch_kernel<2>, grid, dim3(64 * kGemvWaves), gemv_lds(K), ctx->stream, base, b);
+    FA_TRY(check_launch(ctx, label));
+  }
   *out = o;
   return FA_OK;
 }

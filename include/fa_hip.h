@@ -221,6 +221,16 @@ int fa_quantize_weights(int format, const float *w, int K, int N, void *q_out, v
  * int8 ([N][K] K-major bytes), 2 = int4 (bq [N][K/32][16 B]).  The weight
  * layouts are the ones the fused encoder stores (see fa_encoder_load). */
 int fa_gemv_quant(fa_ctx *ctx, fa_tensor a, fa_tensor w, fa_tensor scales, int format, int N, int K, fa_tensor *out);
+/* `count` independent GEMVs of one shape in one launch per 48 items: item i
+ * computes a[i] [M,K] @ W_i (format and layouts as fa_gemv_quant; one M in
+ * 1..16 for all items, K a multiple of 128, <= 4096) into rows [i*M, (i+1)*M) of out
+ * [count*M, N].  No reference counterpart (the reference issues one matmul
+ * per weight, gemm.js:697-706 / 893-919): for callers with many weight
+ * buffers ready at once (the q / k / v / FF linears of several streams or
+ * layers' independent projections), whose weight streams then run at the
+ * HBM rate together instead of one small matrix's launch latency each. */
+int fa_gemv_quant_batch(fa_ctx *ctx, int count, const fa_tensor *a, const fa_tensor *w, const fa_tensor *scales, int format, int N, int K,
+                        fa_tensor *out);
 
 /* ── ragged window packing (the new batched-window path) ──────────────────────
  * Cuts n windows [start_i, start_i+len_i) out of a channel-major feature

@@ -56,6 +56,40 @@ def test_gemv_quant(ctx, fa, orc, M, fmt):
     assert rel(got, ref) < (1e-2 if fmt == 1 else 2e-3)
 
 
+@pytest.mark.parametrize("M", [1, 16])
+@pytest.mark.parametrize("fmt", [1, 2])
+def test_gemv_quant_batch_equals_single_calls(ctx, fa, M, fmt):
+    """One launch over 50 items (two launches of <= 48) gives each item's
+    single-call result (checked against the oracle in test_gemv_quant) up to
+    f32 summation order: the batched tile runs the whole K in one wave, the
+    single call splits it over four."""
+    K, N, n = 1024, 512, 50
+    items = []
+    for i in range(n):
+        w = (rng.standard_normal((K, N)) * 0.02).astype(np.float32)
+        q, s = lib_quant(fa, w, fmt)
+        st = ctx.upload(s, 1, N) if fmt == 1 else ctx.uploadBytes(s)
+        items.append((ctx.upload(rng.standard_normal((M, K)).astype(np.float32), M, K), ctx.uploadBytes(q), st))
+    got = ctx.download(ctx.gemvQuantBatch([t[0] for t in items], [t[1] for t in items], [t[2] for t in items], fmt, N, K)).reshape(n, M, N)
+    for i, (a, q, st) in enumerate(items):
+        one = ctx.download(ctx.gemvQuant(a, q, st, fmt, N, K)).reshape(M, N)
+        assert np.abs(got[i] - one).max() <= 1e-5 * max(1.0, np.abs(one).max()), i
+
+
+def test_gemv_quant_batch_rejects(ctx, fa):
+    K, N = 1024, 256
+    q = ctx.uploadBytes(np.zeros(K * N, np.uint8))
+    s = ctx.upload(np.ones(N, np.float32), 1, N)
+    a1, a2 = ctx.upload(np.zeros((1, K), np.float32), 1, K), ctx.upload(np.zeros((2, K), np.float32), 2, K)
+    with pytest.raises(fa.FaError):
+        ctx.gemvQuantBatch([a1, a2], [q, q], [s, s], 1, N, K)  # mixed M
+    with pytest.raises(fa.FaError):
+        ctx.gemvQuantBatch([a1], [q], [s], 1, N, 1000)  # K not a multiple of 64
+    small = ctx.uploadBytes(np.zeros(16, np.uint8))
+    with pytest.raises(fa.FaError):
+        ctx.gemvQuantBatch([a1], [small], [s], 1, N, K)
+
+
 @pytest.mark.parametrize("M", [3, 300])
 def test_matmul_int8_reference_layout(ctx, orc, M):
     K, N = 256, 192
