@@ -35,6 +35,8 @@
 #include "ops.h"
 #include "encoder_impl.h"
 
+#include <array>
+
 namespace fa {
 
 // One stage's window table: rows [off[w], off[w]+len[w]) belong to window w
@@ -925,6 +927,62 @@ int pass_geometry(fa_ctx *ctx, const fa_encoder *e, const int32_t *lens, int n, 
   return FA_OK;
 }
 
+// Quantised weights at large batches: the fused-dequant GEMM routes widen
+// every B fragment in each wave that reads it, which costs more VALU than the
+// MFMAs they feed once M fills the chip.  From kDequantRows rows on, each
+// layer's linears are first widened once into an f16 [N][K] scratch (the
+// exact values the fused routes compute: q for int8, with the column scale
+// left to the epilogue; f16((q - 8)·s) for int4) and the f16 GEMM runs on
+// them; the scratch is L2 / MALL-hot when the GEMM reads it.
+constexpr int kDequantRows = 512;
+
+// One launch per layer widens all its quantised linears: one 16-byte unit of
+// packed weights per thread (int8 16 values; int4 one group-32 block, 32
+// values, with its scale); item i covers units [end[i-1], end[i]).
+constexpr int kWdqMax = 8;
+struct WdqList {
+  const uint8_t *w[kWdqMax];
+  const _Float16 *s[kWdqMax];
+  _Float16 *out[kWdqMax];
+  long end[kWdqMax];
+  int n, i4;
+};
+__global__ __launch_bounds__(256) void wdq_kernel(WdqList L) {
+  long u = (long)blockIdx.x * 256 + threadIdx.x;
+  if (u >= L.end[L.n - 1]) return;
+  int i = 0;
+  while (u >= L.end[i]) i++;
+  if (i > 0) u -= L.end[i - 1];
+  const uint4 v = reinterpret_cast<const uint4 *>(L.w[i])[u];
+  if (L.i4) {
+    const _Float16 sc = L.s[i][u];
+    h8 *o = reinterpret_cast<h8 *>(L.out[i] + u * 32);
+    o[0] = i4x8_to_h8(v.x, sc);
+    o[1] = i4x8_to_h8(v.y, sc);
+    o[2] = i4x8_to_h8(v.z, sc);
+    o[3] = i4x8_to_h8(v.w, sc);
+  } else {
+    h8 *o = reinterpret_cast<h8 *>(L.out[i] + u * 16);
+    o[0] = i8x8_to_h8(uint2{v.x, v.y});
+    o[1] = i8x8_to_h8(uint2{v.z, v.w});
+  }
+}
+
+static inline std::array<const Lin *, kWdqMax> layer_lins(const fa_encoder::Layer &Ly) {
+  return {&Ly.ff1w1, &Ly.ff1w2, &Ly.qkv, &Ly.out, &Ly.pw1, &Ly.pw2, &Ly.ff2w1, &Ly.ff2w2};
+}
+
+static size_t wdq_bytes(const fa_encoder *e) {
+  size_t mx = 0;
+  for (const auto &Ly : e->L) {
+    size_t t = 0;
+    for (const Lin *L : layer_lins(Ly))
+      if (L->bkind != B_F16) t += (size_t)L->N * L->K * 2;
+    mx = std::max(mx, t);
+  }
+  return mx;
+}
+
 int pass_workspace(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, int layers, bool stream) {
   const fa_encoder_cfg &c = e->cfg;
   const int D = c.D, C = c.Csub, M = g.M;
@@ -953,6 +1011,7 @@ int pass_workspace(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, int layers, bo
   if (any & (FA_EXACT_ATTN_OUT | FA_EXACT_DW_OUT)) FA_TRY(grow(e, &e->alo, &e->cap_alo, (size_t)M * D * 2));
   if (any & FA_EXACT_GLU) FA_TRY(grow(e, &e->g32, &e->cap_g32, (size_t)M * D * 4));
   if (cln) FA_TRY(grow(e, &e->dw32, &e->cap_dw32, (size_t)M * D * 4));
+  if (e->format != FA_W_F16 && M >= kDequantRows) FA_TRY(grow(e, &e->wdq, &e->cap_wdq, wdq_bytes(e)));
   if (!stream) {
     // transposed V per (window, head), written by the q|k|v GEMM's epilogue
     // (or v_transpose_kernel).  Keys past a window's end are never written:
@@ -1019,11 +1078,50 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
 
   // ── conformer layers ──
   // A operand (with an optional exact lo plane) -> C (with an optional lo plane)
+  // quantised weights, batches of >= kDequantRows rows: each layer's linears
+  // are widened (one launch) right before the layer runs.  Widening the next
+  // layer on a second stream during the current one was measured slower
+  // (int8 7.84 -> 8.59 ms per configs[4] batch): the copy competes with the
+  // GEMMs for HBM and CU slots and the GEMMs lose more than the copy takes.
+  const bool dq = e->format != FA_W_F16 && M >= kDequantRows;
+  WdqList wdq{};
+  const Lin *wdq_src[kWdqMax] = {};
+  auto dequant_layer = [&](const fa_encoder::Layer &Ly) -> int {
+    WdqList &W = wdq;
+    W = WdqList{};
+    _Float16 *dst = (_Float16 *)e->wdq;
+    long units = 0;
+    for (const Lin *L : layer_lins(Ly)) {
+      if (L->bkind == B_F16) continue;
+      const int i4 = L->bkind == B_I4;
+      W.w[W.n] = (const uint8_t *)L->w;
+      W.s[W.n] = (const _Float16 *)L->scales;
+      W.out[W.n] = dst;
+      units += (long)L->N * L->K / (i4 ? 32 : 16);
+      W.end[W.n] = units;
+      W.i4 = i4;
+      wdq_src[W.n++] = L;
+      dst += (size_t)L->N * L->K;
+    }
+    if (!W.n) return FA_OK;
+    ProfScope ps(ctx, "dequant_w");
+    FA_LAUNCH(ps, wdq_kernel, dim3(cdiv(units, 256)), dim3(256), 0, ctx->stream, W);
+    return check_launch(ctx, "dequant_w");
+  };
   auto gemm = [&](const void *A, const void *Alo, int lda, const Lin &L, void *Cp, void *Clo, int ldc, int out_f16, int act, const float *add, int glu,
                   const char *label) {
     GemmArgs p;
     p.A = A; p.Alo = Alo; p.lda = lda; p.akind = A_F16;
     set_gemm_b(p, L);
+    if (L.bkind != B_F16 && M >= kDequantRows) {  // the layer's widened copy (dequant_layer), f16 route
+      const _Float16 *wf = nullptr;
+      for (int i = 0; i < wdq.n; i++)
+        if (wdq_src[i] == &L) wf = wdq.out[i];
+      if (!wf) return set_err(ctx, FA_E_STATE, "%s: quantised weights were not widened for this layer", label);
+      p.B = wf;
+      p.bkind = B_F16;
+      p.bscale = nullptr;
+    }
     p.C = Cp; p.Clo = Clo; p.ldc = ldc; p.out_f16 = out_f16; p.act = act;
     p.add = add; p.ldadd = ldc; p.glu = glu;
     p.M = M;
@@ -1075,6 +1173,7 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
   const bool plain_dw = !o.conv_causal && !sp;  // the offline symmetric depthwise conv (BatchNorm folded)
   for (int li = 0; li < layers; li++) {
     auto &Ly = e->L[li];
+    if (dq) FA_TRY(dequant_layer(Ly));
     const unsigned ex = Ly.exact;
     const void *hl = (ex & FA_EXACT_LN_OUT) ? hlo : nullptr;
     void *ul = (ex & FA_EXACT_FF_HIDDEN) ? ulo : nullptr;
@@ -1229,7 +1328,7 @@ void fa_encoder_destroy(fa_encoder *enc) {
   for (void *p : enc->allocs) (void)hipFree(p);
   for (auto &g : enc->graphs)
     if (g.exec) (void)hipGraphExecDestroy(g.exec);
-  for (void *p : {enc->hlo, enc->ulo, enc->alo, enc->g32, enc->vt, enc->vrow, enc->s2, enc->s2p, enc->s3, enc->s3p, enc->h, enc->u, enc->a, enc->g, enc->melw, enc->xw, enc->dw32})
+  for (void *p : {enc->hlo, enc->ulo, enc->alo, enc->g32, enc->vt, enc->vrow, enc->s2, enc->s2p, enc->s3, enc->s3p, enc->h, enc->u, enc->a, enc->g, enc->melw, enc->xw, enc->dw32, enc->wdq})
     if (p) (void)hipFree(p);
   delete enc;
 }

@@ -66,6 +66,8 @@ struct fa_encoder {
   size_t cap_melw = 0, cap_xw = 0;
   void *dw32 = nullptr;  // f32 depthwise output ahead of the conv-module LayerNorm
   size_t cap_dw32 = 0;
+  void *wdq = nullptr;  // quantised formats, batches of >= kDequantRows rows: one layer's linears widened to f16
+  size_t cap_wdq = 0;
 };
 
 namespace fa {
