@@ -16,31 +16,34 @@
 
 namespace fa {
 
-// Block = (64-frame tile, window).  Reads feats[c][start + t] coalesced along
-// t, transposes through LDS, writes out[row][c] coalesced along c.
+// Block = (64-frame tile, 64-channel tile, window).  The 16 loads of a
+// thread (feats[c][start + t], coalesced along t) are all issued before the
+// tile goes through LDS; the transposed rows leave as float4 stores of four
+// channels (coalesced along c).
 __global__ __launch_bounds__(256) void pack_windows_kernel(const float *__restrict__ feats, long Ttot, int MB, WinTable dst, WinTable src, int Tpad,
                                                            float *__restrict__ out) {
   __shared__ float tile[64][65];
-  const int w = blockIdx.y, t0 = blockIdx.x * 64;
+  const int w = blockIdx.z, t0 = blockIdx.x * 64, c0 = blockIdx.y * 64;
   const int len = dst.len[w];
   const int rows = Tpad > 0 ? Tpad : len;  // padded batches also write zero rows
   if (t0 >= rows) return;
   const long start = src.off[w];
-  for (int c0 = 0; c0 < MB; c0 += 64) {
-    for (int e = threadIdx.x; e < 64 * 64; e += 256) {
-      const int cc = e / 64, tt = e % 64;
-      const int c = c0 + cc, t = t0 + tt;
-      float v = 0.f;
-      if (c < MB && t < len && start + t < Ttot) v = feats[(size_t)c * Ttot + start + t];
-      tile[cc][tt] = v;
-    }
-    __syncthreads();
-    for (int e = threadIdx.x; e < 64 * 64; e += 256) {
-      const int tt = e / 64, cc = e % 64;
-      const int c = c0 + cc, t = t0 + tt;
-      if (c < MB && t < rows) out[(size_t)(dst.off[w] + t) * MB + c] = tile[cc][tt];
-    }
-    __syncthreads();
+  const int tt = threadIdx.x & 63, cq = threadIdx.x >> 6;
+  float v[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const int c = c0 + cq + 4 * i, t = t0 + tt;
+    v[i] = (c < MB && t < len && start + t < Ttot) ? feats[(size_t)c * Ttot + start + t] : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < 16; i++) tile[cq + 4 * i][tt] = v[i];
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int e = threadIdx.x + 256 * i, r = e >> 4, c4 = (e & 15) * 4;  // frame t0 + r, channels c0 + c4 .. + 3
+    const int c = c0 + c4, t = t0 + r;
+    if (c < MB && t < rows)
+      *reinterpret_cast<float4 *>(out + (size_t)(dst.off[w] + t) * MB + c) = make_float4(tile[c4][r], tile[c4 + 1][r], tile[c4 + 2][r], tile[c4 + 3][r]);
   }
 }
 
@@ -65,6 +68,7 @@ int fa_pack_windows(fa_ctx *ctx, fa_tensor feats, const int32_t *starts, const i
   TensorRec *rf;
   FA_TRY(need(ctx, feats, &rf, "packWindows"));
   if (rf->kind != S_F32) return set_err(ctx, FA_E_INVALID, "packWindows: features must be f32 [melBins, T]");
+  if (rf->rows % 4) return set_err(ctx, FA_E_UNSUPPORTED, "packWindows: melBins %d must be a multiple of 4", rf->rows);
   if (n <= 0) return set_err(ctx, FA_E_INVALID, "packWindows: no windows");
   if (layout != 0 && layout != 1) return set_err(ctx, FA_E_INVALID, "packWindows: layout %d", layout);
   const int MB = rf->rows;
@@ -97,7 +101,7 @@ int fa_pack_windows(fa_ctx *ctx, fa_tensor feats, const int32_t *starts, const i
       src.len[i] = lens[wi];
       acc += lens[wi];
     }
-    FA_LAUNCH(ps, pack_windows_kernel, dim3(cdiv(mx, 64), dst.n), dim3(256), 0, ctx->stream, (const float *)rf->ptr, Ttot, MB, dst, src,
+    FA_LAUNCH(ps, pack_windows_kernel, dim3(cdiv(mx, 64), cdiv(MB, 64), dst.n), dim3(256), 0, ctx->stream, (const float *)rf->ptr, Ttot, MB, dst, src,
                        layout == 1 ? mx : 0, (float *)ro->ptr);
     FA_TRY(check_launch(ctx, "pack_windows"));
   }
