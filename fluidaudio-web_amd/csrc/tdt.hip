@@ -13,9 +13,9 @@
 // frames equal the reference's.
 //
 // The windows advance in lock-step, one decoding step per kernel sequence:
-//   tdt_rowsum_kernel<0>  joint logits: a 32-column slab of the joint matrix
-//                       streamed through LDS once per step for up to 16 live
-//                       windows; per-slab argmax per window
+//   tdt_joint_kernel    joint logits: a 64-column slab of the joint matrix
+//                       streamed through LDS once per step for up to 8 live
+//                       windows (a wave each); per-slab argmax per window
 //   tdt_update_kernel   per window: final argmax, token record, TDT advance,
 //                       emit flag; the candidate state becomes the committed one
 //                       when a token was emitted
@@ -24,7 +24,7 @@
 //                       emitting windows)
 //   tdt_gates_kernel    lane sums -> gate pre-activations -> LSTM cell ->
 //                       candidate state
-//   tdt_rowsum_kernel<1>  pred projection (emitting windows) and the next joint
+//   tdt_proj_kernel     pred projection (emitting windows) and the next joint
 //                       input relu(frame + pred) (every active window)
 // The reference's GPU decoder (src/engines/asr-parakeet/gpu-decoder.js) runs one
 // workgroup per window that streams the whole joint matrix per step; batching
@@ -39,8 +39,8 @@
 namespace fa {
 
 constexpr int TH = 640, TV = 8193, TL = 8198, TBLANK = 8192, TMAXSYM = 10;
-constexpr int TJB = 32;                    // joint / projection columns per block
-constexpr int TNB = (TL + TJB - 1) / TJB;  // joint column slabs (257)
+constexpr int TJB = 64;                    // joint / projection columns per block (one per lane)
+constexpr int TNB = (TL + TJB - 1) / TJB;  // joint column slabs (129)
 constexpr int TLP = TNB * TJB;             // padded row stride of the joint matrix on the device
 
 struct TdtWin {
@@ -193,33 +193,26 @@ __device__ __forceinline__ void tdt_wait_vmcnt() {  // gfx9 s_waitcnt: vmcnt [3:
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-constexpr int RS_KC = 64, RS_S = 4, RS_SLOTS = 16, RS_WPL = 2;  // rows per chunk, chunks in flight, windows per block / per lane
+constexpr int RS_KC = 64, RS_S = 4, RS_SLOTS = 8;  // rows per chunk, chunks in flight, windows (waves) per block
 
-// EPI 0: joint (selected = windows with frames left; per-slab token maximum,
-// and the duration maximum in the last slab).  EPI 1: pred projection
-// (selected = windows that emitted; pp and the next joint input j =
-// relu(frame[t] + pp)); the last grid row instead refreshes j of the active
-// windows that did not emit.
-template <int EPI>
-__global__ __launch_bounds__(256) void tdt_rowsum_kernel(const float *__restrict__ W, int ldw, int ncols, const float *__restrict__ bias,
-                                                         const float *__restrict__ xsrc, const float *__restrict__ frames, TdtState st, int n) {
+// Wave = one selected window, lane = one column of a 64-column slab: every
+// lane runs one in-order chain over the 640 hidden units.  The window's input
+// vector is wave-uniform and is read with scalar loads (SGPR operands of the
+// multiplies; measured 18.7 us per step against 29.0 with the vector staged
+// in LDS and read as broadcasts); the slab's rows are streamed global->LDS by
+// global_load_lds_dwordx4 in chunks of 64 rows, RS_S chunks in flight, and
+// shared by the block's 8 windows.  W rows must be 16-byte aligned and the
+// slab must lie inside every row.
+// Selected = windows with frames left; per-slab token maximum, and the
+// duration maximum in the last slab.
+__global__ __launch_bounds__(64 * RS_SLOTS) void tdt_joint_kernel(const float *__restrict__ W, int ldw, int ncols, const float *__restrict__ bias,
+                                                                  const float *__restrict__ xsrc, TdtState st, int n) {
   __shared__ __attribute__((aligned(1024))) float ws[RS_S][RS_KC][TJB];
-  __shared__ __attribute__((aligned(16))) float xs[RS_SLOTS][TH];
   __shared__ int lst[RS_SLOTS], lcnt;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int c = lane & 31, h = lane >> 5, slab = blockIdx.x, col = slab * TJB + c;
-  if (EPI == 1 && (int)blockIdx.y == (int)gridDim.y - 1) {
-    for (int w = tid >> 5; w < n; w += 8) {
-      const TdtWin s = st.win[w];
-      if (!s.emit && s.t < s.T) {
-        const float v = frames[(size_t)(s.off + s.t) * TH + col] + st.pp[(size_t)w * TH + col];
-        st.j[(size_t)w * TH + col] = v > 0.0f ? v : 0.0f;
-      }
-    }
-    return;
-  }
+  const int slab = blockIdx.x, col = slab * TJB + lane;
   if (wave == 0) {
-    const bool sel = lane < n && (EPI == 0 ? st.win[lane].t < st.win[lane].T : st.win[lane].emit != 0);
+    const bool sel = lane < n && st.win[lane].t < st.win[lane].T;
     const unsigned long long m = __ballot(sel);
     const int first = blockIdx.y * RS_SLOTS, rank = __popcll(m & ((1ull << lane) - 1ull));
     if (sel && rank >= first && rank < first + RS_SLOTS) lst[rank - first] = lane;
@@ -229,37 +222,23 @@ __global__ __launch_bounds__(256) void tdt_rowsum_kernel(const float *__restrict
   const int cnt = lcnt;
   if (cnt == 0) return;  // uniform
   const uint32_t sb = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)&ws[0][0][0]);
-  const float *wsrc = W + (size_t)(lane >> 3) * ldw + slab * TJB + (lane & 7) * 4;
-  auto issue = [&](int ch) {  // 64 rows x 128 B = 8 copies of 1 KB, two per wave
+  // a chunk is 64 rows x 256 B = 16 copies of 1 KB (4 rows each), two per wave
+  const float *wsrc = W + (size_t)(lane >> 4) * ldw + slab * TJB + (lane & 15) * 4;
+  auto issue = [&](int ch) {
 #pragma unroll
     for (int i = 0; i < 2; i++) {
       const int ins = wave * 2 + i;
-      tdt_dma16(wsrc + (size_t)(ch * RS_KC + ins * 8) * ldw, sb + (ch % RS_S) * (RS_KC * TJB * 4) + ins * 1024);
+      tdt_dma16(wsrc + (size_t)(ch * RS_KC + ins * 4) * ldw, sb + (ch % RS_S) * (RS_KC * TJB * 4) + ins * 1024);
     }
   };
   constexpr int NCH = TH / RS_KC;
 #pragma unroll
   for (int ch = 0; ch < RS_S - 1; ch++) issue(ch);
-  // x vectors of the block's windows
-  for (int e = tid; e < cnt * TH; e += 256) {
-    const int sl = e / TH, k = e - sl * TH, w = lst[sl];
-    const float *src = EPI == 0 ? xsrc + (size_t)w * TH : xsrc + (((size_t)w * 2 + (st.win[w].cur ^ 1)) * 2 + 1) * TH;
-    xs[sl][k] = src[k];
-  }
-  int slot[RS_WPL];
-  bool act[RS_WPL];
-#pragma unroll
-  for (int q = 0; q < RS_WPL; q++) {
-    const int sl = wave + 4 * h + 8 * q;
-    act[q] = sl < cnt;
-    slot[q] = act[q] ? sl : 0;
-  }
-  const bool work = wave < cnt;  // the wave's smallest slot
+  const bool work = wave < cnt;
+  const int w = __builtin_amdgcn_readfirstlane(lst[work ? wave : 0]);
+  const float *xw = xsrc + (size_t)w * TH;  // wave-uniform: scalar loads, SGPR operands
   const bool valid = col < ncols;
-  const float b0 = valid ? bias[col] : 0.f;
-  float acc[RS_WPL];
-#pragma unroll
-  for (int q = 0; q < RS_WPL; q++) acc[q] = b0;
+  float acc = valid ? bias[col] : 0.f;
   for (int ch = 0; ch < NCH; ch++) {
     const int newer = min(RS_S - 2, NCH - 1 - ch);  // copies issued after chunk ch, per wave: 2 each
     if (newer >= 2) tdt_wait_vmcnt<4>();
@@ -268,26 +247,18 @@ __global__ __launch_bounds__(256) void tdt_rowsum_kernel(const float *__restrict
     __syncthreads();  // chunk ch visible to every wave; the stage of chunk ch - 1 is free
     if (ch + RS_S - 1 < NCH) issue(ch + RS_S - 1);
     if (work) {
-      // 16-row groups in two register sets: the LDS reads of group g + 1 are
-      // issued before group g is summed (reads issued next to their use would
-      // expose the LDS latency at every row)
-      const float *wr = &ws[ch % RS_S][0][c];
+      const float *wr = &ws[ch % RS_S][0][lane];
       const int k0 = ch * RS_KC;
-      float wA[16], wB[16];
-      float4 xA[RS_WPL][4], xB[RS_WPL][4];
-      auto ld = [&](int kk, float(&wv)[16], float4(&xv)[RS_WPL][4]) {
+      float wA[16], wB[16], xA[16], xB[16];
+      auto ld = [&](int kk, float(&wv)[16], float(&xv)[16]) {
 #pragma unroll
         for (int u = 0; u < 16; u++) wv[u] = wr[(kk + u) * TJB];
 #pragma unroll
-        for (int q = 0; q < RS_WPL; q++)
-#pragma unroll
-          for (int v = 0; v < 4; v++) xv[q][v] = *reinterpret_cast<const float4 *>(&xs[slot[q]][k0 + kk + 4 * v]);
+        for (int u = 0; u < 16; u++) xv[u] = xw[k0 + kk + u];
       };
-      auto sum = [&](const float(&wv)[16], const float4(&xv)[RS_WPL][4]) {
+      auto sum = [&](const float(&wv)[16], const float(&xv)[16]) {
 #pragma unroll
-        for (int u = 0; u < 16; u++)
-#pragma unroll
-          for (int q = 0; q < RS_WPL; q++) acc[q] = acc[q] + xv[q][u >> 2][u & 3] * wv[u];
+        for (int u = 0; u < 16; u++) acc = acc + xv[u] * wv[u];
       };
       ld(0, wA, xA);
       ld(16, wB, xB);
@@ -300,49 +271,141 @@ __global__ __launch_bounds__(256) void tdt_rowsum_kernel(const float *__restrict
     }
   }
   if (!work) return;
+  {
+    float bv = (valid && col < TV) ? acc : -INFINITY;
+    int bi = (valid && col < TV) ? col : 0x7fffffff;
 #pragma unroll
-  for (int q = 0; q < RS_WPL; q++) {
-    const int w = lst[slot[q]];
-    if (EPI == 0) {
-      float bv = (valid && col < TV) ? acc[q] : -INFINITY;
-      int bi = (valid && col < TV) ? col : 0x7fffffff;
+    for (int sh = 32; sh > 0; sh >>= 1) {
+      const float ov = __shfl_xor(bv, sh);
+      const int oi = __shfl_xor(bi, sh);
+      if (better(ov, oi, bv, bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (lane == 0) {
+      st.pv[w * TNB + slab] = bv;
+      st.pi[w * TNB + slab] = bi;
+    }
+    if (slab == TNB - 1) {
+      float dv = (valid && col >= TV) ? acc : -INFINITY;
+      int di = (valid && col >= TV) ? col - TV : 0x7fffffff;
 #pragma unroll
-      for (int sh = 16; sh > 0; sh >>= 1) {  // within the 32-lane half
-        const float ov = __shfl_xor(bv, sh);
-        const int oi = __shfl_xor(bi, sh);
-        if (better(ov, oi, bv, bi)) {
-          bv = ov;
-          bi = oi;
+      for (int sh = 32; sh > 0; sh >>= 1) {
+        const float ov = __shfl_xor(dv, sh);
+        const int oi = __shfl_xor(di, sh);
+        if (better(ov, oi, dv, di)) {
+          dv = ov;
+          di = oi;
         }
       }
-      if (act[q] && c == 0) {
-        st.pv[w * TNB + slab] = bv;
-        st.pi[w * TNB + slab] = bi;
+      if (lane == 0) {
+        st.dv[w] = dv;
+        st.di[w] = di;
       }
-      if (slab == TNB - 1) {
-        float dv = (valid && col >= TV) ? acc[q] : -INFINITY;
-        int di = (valid && col >= TV) ? col - TV : 0x7fffffff;
-#pragma unroll
-        for (int sh = 16; sh > 0; sh >>= 1) {
-          const float ov = __shfl_xor(dv, sh);
-          const int oi = __shfl_xor(di, sh);
-          if (better(ov, oi, dv, di)) {
-            dv = ov;
-            di = oi;
-          }
-        }
-        if (act[q] && c == 0) {
-          st.dv[w] = dv;
-          st.di[w] = di;
-        }
-      }
-    } else if (act[q]) {
-      st.pp[(size_t)w * TH + col] = acc[q];
+    }
+  }
+}
+
+// Pred projection of the windows that emitted, pp = pred_b + h1 · pred_w
+// (in-order sums over the 640 hidden units), and the next joint input
+// j = relu(frame[t] + pp).  Block = one wave = ZG emitting windows x 64
+// columns.  pred_w is stored column-major on the device (WT[col][k]), so a
+// lane's float4 load brings 4 consecutive k of its column: 160 loads per
+// chain instead of 640, streamed with two register buffers of PB loads.  The
+// windows' h vectors are staged in LDS and read as broadcasts (in-order LDS
+// returns let the reads run ahead of their use; scalar loads would each be
+// waited for in full); each lane runs ZG chains sharing its weight loads.  The last grid row refreshes
+// j of the active windows that did not emit.
+template <int ZG>
+__global__ __launch_bounds__(64) void tdt_proj_kernel(const float *__restrict__ WT, const float *__restrict__ bias, const float *__restrict__ hsrc,
+                                                      const float *__restrict__ frames, TdtState st, int n) {
+  constexpr int PB = 20, NI = TH / 4;
+  static_assert(NI % (2 * PB) == 0, "whole buffer pairs");
+  __shared__ int lst[ZG];
+  __shared__ __attribute__((aligned(16))) float xs[ZG][TH];
+  const int tid = threadIdx.x, col = blockIdx.x * 64 + tid;
+  if ((int)blockIdx.y == (int)gridDim.y - 1) {
+    for (int w = 0; w < n; w++) {
       const TdtWin s = st.win[w];
-      if (s.t < s.T) {
-        const float v = frames[(size_t)(s.off + s.t) * TH + col] + acc[q];
+      if (!s.emit && s.t < s.T) {
+        const float v = frames[(size_t)(s.off + s.t) * TH + col] + st.pp[(size_t)w * TH + col];
         st.j[(size_t)w * TH + col] = v > 0.0f ? v : 0.0f;
       }
+    }
+    return;
+  }
+  const bool em = tid < n && st.win[tid].emit != 0;
+  const int cnt = tdt_group(em, blockIdx.y * ZG, ZG, lst);
+  if (cnt == 0) return;
+  const float4 *wc = reinterpret_cast<const float4 *>(WT + (size_t)col * TH);
+  float acc[ZG];
+  const float b0 = bias[col];
+#pragma unroll
+  for (int g = 0; g < ZG; g++) acc[g] = b0;
+  float4 wa[PB], wb[PB];
+#pragma unroll
+  for (int u = 0; u < PB; u++) wa[u] = wc[u];
+  // the windows' h vectors -> LDS (read back as broadcasts)
+  for (int e = tid; e < ZG * TH; e += 64) {
+    const int g = e / TH, k = e - g * TH, w = lst[g < cnt ? g : 0];
+    xs[g][k] = hsrc[(((size_t)w * 2 + (st.win[w].cur ^ 1)) * 2 + 1) * TH + k];
+  }
+  __syncthreads();
+  // x in groups of 4 float4 (16 k) per window, two register sets: the LDS
+  // reads of group q + 1 are issued before group q is summed
+  auto ldx = [&](int i, float4(&xv)[ZG][4]) {
+#pragma unroll
+    for (int g = 0; g < ZG; g++)
+#pragma unroll
+      for (int v = 0; v < 4; v++) xv[g][v] = *reinterpret_cast<const float4 *>(&xs[g][4 * (i + v)]);
+  };
+  auto sum4 = [&](const float4(&wv)[PB], int u0, const float4(&xv)[ZG][4]) {
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const float we[4] = {wv[u0 + v].x, wv[u0 + v].y, wv[u0 + v].z, wv[u0 + v].w};
+#pragma unroll
+      for (int g = 0; g < ZG; g++) {
+        const float xe[4] = {xv[g][v].x, xv[g][v].y, xv[g][v].z, xv[g][v].w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) acc[g] = acc[g] + xe[e] * we[e];
+      }
+    }
+  };
+  auto sum = [&](const float4(&wv)[PB], int i0) {
+    static_assert(PB % 4 == 0, "groups of 4");
+    float4 xA[ZG][4], xB[ZG][4];
+    ldx(i0, xA);
+#pragma unroll
+    for (int q = 0; q < PB / 4; q += 2) {
+      if (q + 1 < PB / 4) ldx(i0 + 4 * (q + 1), xB);
+      sum4(wv, 4 * q, xA);
+      if (q + 1 < PB / 4) {
+        if (q + 2 < PB / 4) ldx(i0 + 4 * (q + 2), xA);
+        sum4(wv, 4 * (q + 1), xB);
+      }
+    }
+  };
+
+#pragma unroll 1
+  for (int i0 = 0; i0 < NI; i0 += 2 * PB) {
+#pragma unroll
+    for (int u = 0; u < PB; u++) wb[u] = wc[i0 + PB + u];
+    sum(wa, i0);
+    const int nx = i0 + 2 * PB < NI ? i0 + 2 * PB : NI - PB;  // last step: a harmless reload
+#pragma unroll
+    for (int u = 0; u < PB; u++) wa[u] = wc[nx + u];
+    sum(wb, i0 + PB);
+  }
+#pragma unroll
+  for (int g = 0; g < ZG; g++) {
+    if (g >= cnt) break;
+    const int w = lst[g];
+    st.pp[(size_t)w * TH + col] = acc[g];
+    const TdtWin s = st.win[w];
+    if (s.t < s.T) {
+      const float v = frames[(size_t)(s.off + s.t) * TH + col] + acc[g];
+      st.j[(size_t)w * TH + col] = v > 0.0f ? v : 0.0f;
     }
   }
 }
@@ -505,6 +568,12 @@ int fa_tdt_load(fa_ctx *ctx, const float *const *w, fa_tdt **out) {
         for (int k = 0; k < TH; k++) tr[(size_t)k * 4 * TH + r] = src[(size_t)r * TH + k];
       src = tr.data();
     }
+    if (i == 7) {  // pred projection [H][H] (k-major) -> column-major [col][k]
+      tr.resize(sizes[i]);
+      for (int k = 0; k < TH; k++)
+        for (int m = 0; m < TH; m++) tr[(size_t)m * TH + k] = src[(size_t)k * TH + m];
+      src = tr.data();
+    }
     if (i == 9) {  // joint [H][TL] -> [H][TLP]
       tr.assign(dsz[i], 0.f);
       for (int k = 0; k < TH; k++) memcpy(&tr[(size_t)k * TLP], src + (size_t)k * TL, TL * 4);
@@ -599,8 +668,7 @@ int fa_tdt_decode(fa_tdt *d, fa_tensor frames, const int32_t *lens, int n, int c
       FA_LAUNCH(ps, tdt_gates_kernel, dim3(cdiv(TH, 256), n), dim3(256), 0, ctx->stream, d->lb[layer], layer, st);
     }
     ProfScope ps(ctx, "tdt_proj");
-    FA_LAUNCH(ps, tdt_rowsum_kernel<1>, dim3(TH / TJB, cdiv(n, RS_SLOTS) + 1), dim3(256), 0, ctx->stream, d->pred_w, TH, TH, d->pred_b,
-              (const float *)st.h, fr, st, n);
+    FA_LAUNCH(ps, tdt_proj_kernel<2>, dim3(TH / 64, cdiv(n, 2) + 1), dim3(64), 0, ctx->stream, d->pred_w, d->pred_b, (const float *)st.h, fr, st, n);
     return check_launch(ctx, "tdt_predict");
   };
   FA_TRY(predict());  // predict(BLANK) from the zero state, then j for t = 0
@@ -614,8 +682,8 @@ int fa_tdt_decode(fa_tdt *d, fa_tensor frames, const int32_t *lens, int n, int c
     for (int k = 0; k < kChunk; k++) {
       {
         ProfScope ps(ctx, "tdt_joint");
-        FA_LAUNCH(ps, tdt_rowsum_kernel<0>, dim3(TNB, cdiv(n, RS_SLOTS)), dim3(256), 0, ctx->stream, d->out_w, TLP, TL, d->out_b,
-                  (const float *)st.j, fr, st, n);
+        FA_LAUNCH(ps, tdt_joint_kernel, dim3(TNB, cdiv(n, RS_SLOTS)), dim3(64 * RS_SLOTS), 0, ctx->stream, d->out_w, TLP, TL, d->out_b,
+                  (const float *)st.j, st, n);
       }
       {
         ProfScope ps(ctx, "tdt_update");
