@@ -170,3 +170,22 @@ def test_config4_quantized_encoder_vs_fp32_path(ctx, fa, orc, full_weights, fmt)
     print(f"configs[4] {fmt} encoder, 24 layers x 16 x 15 s: rel-L2 vs fp32 path (dequantised weights) {r:.2e}, "
           f"argmax disagreements {f}/{len(got)}")
     assert r <= 1e-2 and f <= 0.001 * len(got)
+
+
+@pytest.mark.parametrize("fmt", ["int8", "int4"])
+def test_quantized_widened_route_equals_fused_route(ctx, fa, full_weights, fmt):
+    """Batches of >= 512 encoder rows widen each layer's quantised weights to
+    f16 once and run the f16 GEMMs; smaller batches dequantise inside the GEMM
+    tiles.  Both compute the same f16 weight values and the same K-ordered
+    sums, so two windows encoded alone (376 rows, fused route) equal the same
+    windows inside a 4-window batch (752 rows, widened route)."""
+    lw = {k: v for k, v in full_weights.items() if not (k.startswith("L") and int(k[1:k.index("_")]) >= 4)}
+    mels = fa.synth.make_features(128, 1500, seed=21, W=4)
+    enc = fa.FusedEncoder(ctx, lw, fmt, max_T=188)
+    small = enc.encode(mels[:2])
+    big = enc.encode(mels)
+    enc.close()
+    for a, b in zip(small, big[:2]):
+        d = float(np.abs(a - b).max() / np.abs(b).max())
+        print(f"{fmt}: fused vs widened route, max rel diff {d:.2e}")
+        assert d <= 1e-5
