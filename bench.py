@@ -594,11 +594,32 @@ def bench_stream(args, fa, ctx):
         frames = run()
     wall = (time.perf_counter() - t0) / args.steps
     chunks = mel.shape[1] // piece
+    # per-kernel GPU time of steady-state chunk passes, eager under HIP events
+    # (a profiled pass is not graph-replayed)
+    st = fa.createEncodeStream(ctx, enc)
+    for t in range(0, 64 * piece, piece):  # past the first pass and the cache fill
+        fa.encodeStreamPush(ctx, st, mel[:, t:t + piece])
+    ctx.sync()
+    ctx.startProfile(200000)
+    prof_chunks = 8
+    for t in range(64 * piece, (64 + prof_chunks) * piece, piece):
+        fa.encodeStreamPush(ctx, st, mel[:, t:t + piece])
+    prof = ctx.endProfile()
+    fa.disposeEncodeStream(ctx, st)
+    kern = {}
+    for r in prof:
+        k = kern.setdefault(r["label"], {"launches": 0, "ms": 0.0})
+        k["launches"] += 1
+        k["ms"] += r["ms"]
+    kern = {lab: {"launches_per_chunk": v["launches"] // prof_chunks, "us_per_chunk": round(v["ms"] * 1e3 / prof_chunks, 1)}
+            for lab, v in sorted(kern.items(), key=lambda kv: -kv[1]["ms"])}
     line = {"metric": "streaming encode audio-s/wall-s per stream at 1 GPU", "value": round(seconds / wall, 1), "unit": "audio-s/wall-s",
             "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 2), "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic log-mel ~N(0,1), random-init weights",
             "config": {"workload": "30 s pushed in 160 ms pieces, 24 layers d_model 1024, chunk 2 / left 70 (EOU streaming config), native fused stream",
-                       "frames": frames, "chunks": chunks, "ms_per_chunk": round(wall * 1e3 / chunks, 3)}}
+                       "frames": frames, "chunks": chunks, "ms_per_chunk": round(wall * 1e3 / chunks, 3)},
+            "kernels_eager_per_chunk": kern,
+            "kernel_us_per_chunk_eager": round(sum(v["us_per_chunk"] for v in kern.values()), 1)}
     if not args.no_cpu:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import np_ref

@@ -572,7 +572,10 @@ __global__ __launch_bounds__(256) void stream_conv_cache_kernel(const float *__r
 // cs + chunk - 1 + right], cs = chunk * floor(i / chunk), and its positional
 // term uses table row clamp(dMax - (i - (j - Lc)), 0, Pn - 1).  One wave per
 // (query, head): lanes over keys for the f32 scores of f16 rows, wave
-// reductions for the softmax, lanes over head dims for P·V.  Lk <= 256.
+// reductions for the softmax, lanes over head dims for P·V out of the head's
+// V rows, staged in LDS once per block (4 queries) with every row load in
+// flight at once (reading them from global one key after another cost
+// ~76 us per layer).  Lk <= 256.
 __global__ __launch_bounds__(256) void stream_attn_kernel(const _Float16 *__restrict__ u, int ldu, const _Float16 *__restrict__ kc,
                                                           const _Float16 *__restrict__ vc, int Lc, int nq, int D, const _Float16 *__restrict__ P, int Pn,
                                                           int dMax, const float *__restrict__ pbu, const float *__restrict__ pbv, int chunk, int left,
@@ -580,10 +583,17 @@ __global__ __launch_bounds__(256) void stream_attn_kernel(const _Float16 *__rest
   constexpr int HD = 128, MAXK = 256;
   __shared__ float qs[4][2][HD];
   __shared__ float ps[4][MAXK];
+  __shared__ __attribute__((aligned(16))) _Float16 vs[MAXK][HD];  // the head's V rows, shared by the block's 4 queries
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = blockIdx.y;
   const int i = blockIdx.x * 4 + wave;
-  if (i >= nq) return;
   const int Lk = Lc + nq;
+  for (int idx = threadIdx.x; idx < Lk * (HD / 8); idx += 256) {  // all row loads in flight at once
+    const int j = idx >> 4, c8 = (idx & 15) * 8;
+    const _Float16 *src = j < Lc ? vc + (size_t)j * D + h * HD + c8 : u + (size_t)(j - Lc) * ldu + 2 * D + h * HD + c8;
+    *reinterpret_cast<h8 *>(&vs[j][c8]) = *reinterpret_cast<const h8 *>(src);
+  }
+  __syncthreads();
+  if (i >= nq) return;
 #pragma unroll
   for (int e = 0; e < 2; e++) {
     const int d = lane + 64 * e;
@@ -628,10 +638,8 @@ __global__ __launch_bounds__(256) void stream_attn_kernel(const _Float16 *__rest
   for (int e = 0; e < 2; e++) {
     const int d = lane + 64 * e;
     float o = 0.f;
-    for (int j = 0; j < Lk; j++) {
-      const float p = ps[wave][j];
-      if (p != 0.f) o += p * (float)(j < Lc ? vc[(size_t)j * D + h * HD + d] : u[(size_t)(j - Lc) * ldu + 2 * D + h * HD + d]);
-    }
+#pragma unroll 8
+    for (int j = 0; j < Lk; j++) o += ps[wave][j] * (float)vs[j][d];  // masked keys carry p = 0
     o *= inv;
     const _Float16 hi = (_Float16)o;
     out[(size_t)i * D + h * HD + d] = hi;

@@ -719,8 +719,112 @@ static int launch_dma(fa_ctx *ctx, const GemmArgs &p, const char *label) {
   return check_launch(ctx, label);
 }
 
+// Skinny route (M <= 16 TI rows, f16 A with an optional exact lo plane, f16
+// B): the streaming passes' GEMMs, whose few rows leave a tiled kernel with a
+// handful of workgroups streaming the whole weight matrix.  Workgroup = 16
+// output columns x KS waves, wave w summing the K slice [w K/KS, (w+1) K/KS)
+// with its B (16 columns) and A fragments loaded straight from global, G
+// 32-deep steps of loads in flight; the slices' partial tiles are added
+// through LDS in wave order and wave 0 runs the direct epilogue.
+template <int TI, int KS, int EPI, int LO>
+__global__ __launch_bounds__(64 * KS) void gemm_skinny_kernel(GemmArgs p) {
+  constexpr int G = 8;
+  __shared__ f4 part[KS > 1 ? KS - 1 : 1][TI][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c16 = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int ks = p.K / KS, kb = wave * ks, nst = ks / 32;
+  const _Float16 *B = reinterpret_cast<const _Float16 *>(p.B) + (size_t)(n0 + c16) * p.K + kb + g * 8;
+  const _Float16 *A[TI], *Al[TI];
+#pragma unroll
+  for (int i = 0; i < TI; i++) {
+    const size_t ro = (size_t)min(16 * i + c16, p.M - 1) * p.lda + kb + g * 8;
+    A[i] = reinterpret_cast<const _Float16 *>(p.A) + ro;
+    Al[i] = LO ? reinterpret_cast<const _Float16 *>(p.Alo) + ro : nullptr;
+  }
+  f4 acc[TI][1];
+#pragma unroll
+  for (int i = 0; i < TI; i++) acc[i][0] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < nst; s0 += G) {
+    h8 bf[G], af[G][TI], al[G][LO ? TI : 1];
+#pragma unroll
+    for (int u = 0; u < G; u++) {
+      const int st = min(s0 + u, nst - 1) * 32;  // past the slice: a repeat, never used
+      bf[u] = *reinterpret_cast<const h8 *>(B + st);
+#pragma unroll
+      for (int i = 0; i < TI; i++) {
+        af[u][i] = *reinterpret_cast<const h8 *>(A[i] + st);
+        if constexpr (LO) al[u][i] = *reinterpret_cast<const h8 *>(Al[i] + st);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < G; u++) {
+      if (s0 + u < nst) {
+#pragma unroll
+        for (int i = 0; i < TI; i++) {
+          acc[i][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[u], af[u][i], acc[i][0], 0, 0, 0);  // C^T tile
+          if constexpr (LO) acc[i][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[u], al[u][i], acc[i][0], 0, 0, 0);
+        }
+      }
+    }
+  }
+  if constexpr (KS > 1) {
+    if (wave > 0)
+#pragma unroll
+      for (int i = 0; i < TI; i++) part[wave - 1][i][lane] = acc[i][0];
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int w = 0; w < KS - 1; w++)
+#pragma unroll
+      for (int i = 0; i < TI; i++) acc[i][0] += part[w][i][lane];
+  }
+  epilogue_direct<TI, 1, EPI>(p, acc, 0, n0, lane);
+}
+
+// K split per workgroup: 8 waves up to N = 2048, 4 above (16 measured slower
+// at N = 1024: 8.8 against 6.0 us for the 1024 x 1024 two-plane product).
+static inline int skinny_ks(int N) { return N <= 2048 ? 8 : 4; }
+
+template <int EPI>
+static int launch_skinny(fa_ctx *ctx, const GemmArgs &p, const char *label) {
+  const int ks = skinny_ks(p.N);
+  const int ti = p.M <= 16 ? 1 : 2;
+  ProfScope ps(ctx, label);
+  const dim3 grid(p.N / 16);
+#define FA_SK(TI, KS)                                                                                \
+  do {                                                                                               \
+    if (p.Alo)                                                                                       \
+      FA_LAUNCH(ps, (gemm_skinny_kernel<TI, KS, EPI, 1>), grid, dim3(64 * KS), 0, ctx->stream, p); \
+    else                                                                                             \
+      FA_LAUNCH(ps, (gemm_skinny_kernel<TI, KS, EPI, 0>), grid, dim3(64 * KS), 0, ctx->stream, p); \
+  } while (0)
+  if (ti == 1) {
+    if (ks == 4) FA_SK(1, 4);
+    else FA_SK(1, 8);
+  } else {
+    if (ks == 4) FA_SK(2, 4);
+    else FA_SK(2, 8);
+  }
+#undef FA_SK
+  return check_launch(ctx, label);
+}
+
+// The skinny route takes f16 x f16 products of at most 32 rows with K a
+// multiple of 32 x its K split, N a multiple of 16, 16-byte aligned operands.
+static inline bool takes_skinny(const GemmArgs &p) {
+  const char *e = getenv("FA_GEMM_SKINNY");
+  if (e && e[0] == '0') return false;
+  const int ks = skinny_ks(p.N);
+  return p.M <= 32 && p.akind == A_F16 && p.bkind == B_F16 && !p.vt && epi_of(p) != EPI_GENERIC && p.N % 16 == 0 && p.K % (32 * ks) == 0 &&
+         p.lda % 8 == 0 && p.ldc % 8 == 0 && !((uintptr_t)p.A & 15) && !((uintptr_t)p.Alo & 15) && !((uintptr_t)p.B & 15) && !((uintptr_t)p.C & 15) &&
+         !((uintptr_t)p.Clo & 15) && !((uintptr_t)p.add & 15) && p.ldadd % 4 == 0;
+}
+
 template <int AK, int BKND, int EPI>
 static int launch_tile(fa_ctx *ctx, const GemmArgs &p, const char *label) {
+  if constexpr (AK == A_F16 && BKND == B_F16 && EPI != EPI_GENERIC)
+    if (takes_skinny(p)) return launch_skinny<EPI>(ctx, p, label);
   if constexpr (AK == A_F16 && BKND == B_F16 && EPI != EPI_GENERIC) {
     if (p.Alo) {
       switch (pick_dma(ctx, p)) {
