@@ -530,26 +530,78 @@ __global__ __launch_bounds__(64) void dwconv_gen_kernel(const TI *__restrict__ x
   }
 }
 
-// Stream-pass K / V caches: row r < keep of the next caches is row
-// Lc + nemit - keep + r of [this layer's cached rows (Lc) ; this pass's rows],
-// the keys of the last `keep` emitted frames (streaming-encoder.js:254-257
-// keeps the same rows).  u holds q|k|v rows (K at column D, V at 2D).
-__global__ __launch_bounds__(256) void stream_kv_cache_kernel(const _Float16 *__restrict__ kc_in, const _Float16 *__restrict__ vc_in,
-                                                              const _Float16 *__restrict__ u, int ldu, int D, int Lc, int nemit, int keep,
-                                                              _Float16 *__restrict__ kc_out, _Float16 *__restrict__ vc_out) {
-  const int r = blockIdx.x, src = Lc + nemit - keep + r;
-  for (int c = threadIdx.x * 8; c < D; c += 256 * 8) {
-    h8 k, v;
-    if (src < Lc) {
-      k = *reinterpret_cast<const h8 *>(kc_in + (size_t)src * D + c);
-      v = *reinterpret_cast<const h8 *>(vc_in + (size_t)src * D + c);
-    } else {
-      k = *reinterpret_cast<const h8 *>(u + (size_t)(src - Lc) * ldu + D + c);
-      v = *reinterpret_cast<const h8 *>(u + (size_t)(src - Lc) * ldu + 2 * D + c);
+// Depthwise conv (k = 9, causal or symmetric, taps before the window's first
+// frame from `cache` in a stream pass) + bias, then the conv-module LayerNorm
+// (streaming models, raw-encoder.js:361-364) + SiLU into f16 (+ exact lo
+// plane): block = one frame (256 threads x 4 channels, D <= 1024), the row
+// statistics reduced over the block (mean, then mean of squared deviations,
+// eps inside the rsqrt, as enc_ln_kernel).  In a stream pass block (0, 0)
+// also writes the next pass's conv cache (rows nemit .. nemit + 7 of
+// [cache ; GLU rows]).
+template <typename TI>
+__global__ __launch_bounds__(256) void dwconv_ln_kernel(const TI *__restrict__ x, const float *__restrict__ cache, WinStage st, int causal,
+                                                        const float *__restrict__ wt, const float *__restrict__ b, const float *__restrict__ gamma,
+                                                        const float *__restrict__ beta, int D, _Float16 *__restrict__ y, _Float16 *__restrict__ ylo,
+                                                        float *__restrict__ cc_out, int nemit) {
+  constexpr int KT = 9;
+  __shared__ float red[2][4];
+  const int win = blockIdx.y, t = blockIdx.x, T = st.len[win];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c0 = tid * 4;
+  const bool act = c0 < D;
+  if (cc_out && t == 0 && win == 0 && act) {
+    for (int r = 0; r < KT - 1; r++) {
+      const int src = nemit + r;
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        cc_out[(size_t)r * D + c0 + e] = src < KT - 1 ? cache[(size_t)src * D + c0 + e] : (float)x[(size_t)st.off[0] * D + (size_t)(src - (KT - 1)) * D + c0 + e];
     }
-    *reinterpret_cast<h8 *>(kc_out + (size_t)r * D + c) = k;
-    *reinterpret_cast<h8 *>(vc_out + (size_t)r * D + c) = v;
   }
+  if (t >= T) return;  // uniform per block
+  const int pad = causal ? KT - 1 : (KT - 1) / 2;
+  const size_t base = (size_t)st.off[win] * D + c0;
+  float r[4] = {0.f, 0.f, 0.f, 0.f};
+  if (act) {
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < KT; k++) {
+      const int ti = t - pad + k;
+      float v[4] = {0.f, 0.f, 0.f, 0.f};
+      if (ti >= 0 && ti < T) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] = (float)x[base + (size_t)ti * D + e];
+      } else if (ti < 0 && cache && win == 0) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] = cache[(size_t)(KT - 1 + ti) * D + c0 + e];
+      }
+#pragma unroll
+      for (int e = 0; e < 4; e++) acc[e] += v[e] * wt[k * D + c0 + e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) r[e] = acc[e] + b[c0 + e];
+  }
+  auto block_sum = [&](float v, int slot) {
+    v = wave_sum(v);
+    if (lane == 0) red[slot][wave] = v;
+    __syncthreads();
+    return (red[slot][0] + red[slot][1]) + (red[slot][2] + red[slot][3]);
+  };
+  const float mean = block_sum(act ? r[0] + r[1] + r[2] + r[3] : 0.f, 0) * (1.f / D);
+  float q = 0.f;
+  if (act)
+#pragma unroll
+    for (int e = 0; e < 4; e++) q += (r[e] - mean) * (r[e] - mean);
+  const float inv = rsqrtf(block_sum(q, 1) * (1.f / D) + 1e-5f);
+  if (!act) return;
+  h4 hi, lo;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const float o = silu_f((r[e] - mean) * inv * gamma[c0 + e] + beta[c0 + e]);
+    hi[e] = (_Float16)o;
+    lo[e] = (_Float16)(o - (float)hi[e]);
+  }
+  *reinterpret_cast<h4 *>(y + base + (size_t)t * D) = hi;
+  if (ylo) *reinterpret_cast<h4 *>(ylo + base + (size_t)t * D) = lo;
 }
 
 // Stream-pass depthwise-conv cache: row r < k-1 of the next cache is row
@@ -571,28 +623,42 @@ __global__ __launch_bounds__(256) void stream_conv_cache_kernel(const float *__r
 // chunk boundary); key j is visible iff j - Lc lies in [cs - left,
 // cs + chunk - 1 + right], cs = chunk * floor(i / chunk), and its positional
 // term uses table row clamp(dMax - (i - (j - Lc)), 0, Pn - 1).  One wave per
-// (query, head): lanes over keys for the f32 scores of f16 rows, wave
-// reductions for the softmax, lanes over head dims for P·V out of the head's
-// V rows, staged in LDS once per block (4 queries) with every row load in
-// flight at once (reading them from global one key after another cost
-// ~76 us per layer).  Lk <= 256.
+// (query, head): lanes over keys for the f32 scores, wave reductions for the
+// softmax, lanes over head dims for P·V.  The head's K and V rows are staged
+// in LDS once per block (4 queries) with every row load in flight at once
+// (reading V from global one key after another cost ~76 us per layer); the
+// first query block of each head also writes the head's part of the next
+// pass's K / V caches from them.  Lk <= 256.
 __global__ __launch_bounds__(256) void stream_attn_kernel(const _Float16 *__restrict__ u, int ldu, const _Float16 *__restrict__ kc,
                                                           const _Float16 *__restrict__ vc, int Lc, int nq, int D, const _Float16 *__restrict__ P, int Pn,
                                                           int dMax, const float *__restrict__ pbu, const float *__restrict__ pbv, int chunk, int left,
-                                                          int right, _Float16 *__restrict__ out, _Float16 *__restrict__ out_lo) {
-  constexpr int HD = 128, MAXK = 256;
+                                                          int right, _Float16 *__restrict__ out, _Float16 *__restrict__ out_lo, int nemit, int keep,
+                                                          _Float16 *__restrict__ kc_out, _Float16 *__restrict__ vc_out) {
+  constexpr int HD = 128, MAXK = 256, KS = HD + 8;  // K rows padded: lanes read different keys' rows
   __shared__ float qs[4][2][HD];
   __shared__ float ps[4][MAXK];
   __shared__ __attribute__((aligned(16))) _Float16 vs[MAXK][HD];  // the head's V rows, shared by the block's 4 queries
+  __shared__ __attribute__((aligned(16))) _Float16 ks[MAXK][KS];  // and its K rows
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = blockIdx.y;
   const int i = blockIdx.x * 4 + wave;
   const int Lk = Lc + nq;
   for (int idx = threadIdx.x; idx < Lk * (HD / 8); idx += 256) {  // all row loads in flight at once
     const int j = idx >> 4, c8 = (idx & 15) * 8;
-    const _Float16 *src = j < Lc ? vc + (size_t)j * D + h * HD + c8 : u + (size_t)(j - Lc) * ldu + 2 * D + h * HD + c8;
-    *reinterpret_cast<h8 *>(&vs[j][c8]) = *reinterpret_cast<const h8 *>(src);
+    const _Float16 *vsrc = j < Lc ? vc + (size_t)j * D + h * HD + c8 : u + (size_t)(j - Lc) * ldu + 2 * D + h * HD + c8;
+    const _Float16 *ksrc = j < Lc ? kc + (size_t)j * D + h * HD + c8 : u + (size_t)(j - Lc) * ldu + D + h * HD + c8;
+    *reinterpret_cast<h8 *>(&vs[j][c8]) = *reinterpret_cast<const h8 *>(vsrc);
+    *reinterpret_cast<h8 *>(&ks[j][c8]) = *reinterpret_cast<const h8 *>(ksrc);
   }
   __syncthreads();
+  if (blockIdx.x == 0 && kc_out) {
+    // the next pass's caches for this head: rows Lc + nemit - keep .. of [cached ; new]
+    // (the keys of the last `keep` emitted frames, streaming-encoder.js:254-257)
+    for (int idx = threadIdx.x; idx < keep * (HD / 8); idx += 256) {
+      const int r = idx >> 4, c8 = (idx & 15) * 8, src = Lc + nemit - keep + r;
+      *reinterpret_cast<h8 *>(kc_out + (size_t)r * D + h * HD + c8) = *reinterpret_cast<const h8 *>(&ks[src][c8]);
+      *reinterpret_cast<h8 *>(vc_out + (size_t)r * D + h * HD + c8) = *reinterpret_cast<const h8 *>(&vs[src][c8]);
+    }
+  }
   if (i >= nq) return;
 #pragma unroll
   for (int e = 0; e < 2; e++) {
@@ -609,12 +675,11 @@ __global__ __launch_bounds__(256) void stream_attn_kernel(const _Float16 *__rest
     const int rel = j - Lc;
     float sc = -INFINITY;
     if (rel >= cs - left && rel <= cs + chunk - 1 + right) {
-      const _Float16 *kr = j < Lc ? kc + (size_t)j * D + h * HD : u + (size_t)(j - Lc) * ldu + D + h * HD;
       const int pr = min(max(dMax - (i - rel), 0), Pn - 1);
       const _Float16 *pp = P + (size_t)pr * D + h * HD;
       float acc = 0.f;
       for (int d = 0; d < HD; d += 8) {
-        const h8 kv = *reinterpret_cast<const h8 *>(kr + d), pv = *reinterpret_cast<const h8 *>(pp + d);
+        const h8 kv = *reinterpret_cast<const h8 *>(&ks[j][d]), pv = *reinterpret_cast<const h8 *>(pp + d);
 #pragma unroll
         for (int e = 0; e < 8; e++) acc += qs[wave][0][d + e] * (float)kv[e] + qs[wave][1][d + e] * (float)pv[e];
       }
@@ -1218,14 +1283,9 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
       {
         ProfScope ps(ctx, "stream_attention");
         FA_LAUNCH(ps, stream_attn_kernel, dim3(cdiv(M, 4), c.H), dim3(256), 0, ctx->stream, u, 3 * D, sp->kc_in + kvo, sp->vc_in + kvo, sp->Lc, M, D,
-                  Ly.P + (size_t)(e->maxT - 1 - sp->dMax) * D, sp->Pn, sp->dMax, Ly.pbu, Ly.pbv, sp->chunk, sp->left, sp->right, a, olo);
+                  Ly.P + (size_t)(e->maxT - 1 - sp->dMax) * D, sp->Pn, sp->dMax, Ly.pbu, Ly.pbv, sp->chunk, sp->left, sp->right, a, olo, sp->nemit,
+                  sp->keep, sp->keep > 0 ? sp->kc_out + kvo : nullptr, sp->vc_out + kvo);
         FA_TRY(check_launch(ctx, "stream_attention"));
-      }
-      if (sp->keep > 0) {
-        ProfScope ps(ctx, "stream_kv_cache");
-        FA_LAUNCH(ps, stream_kv_cache_kernel, dim3(sp->keep), dim3(256), 0, ctx->stream, sp->kc_in + kvo, sp->vc_in + kvo, u, 3 * D, D, sp->Lc, sp->nemit,
-                  sp->keep, sp->kc_out + kvo, sp->vc_out + kvo);
-        FA_TRY(check_launch(ctx, "stream_kv_cache"));
       }
     }
     FA_TRY(gemm(a, olo, D, Ly.out, x, nullptr, D, 0, FA_ACT_NONE, x, 0, olo ? "attn_out_x" : "attn_out"));
@@ -1249,25 +1309,39 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
     } else {
       const float *cache = sp ? sp->cc_in + (size_t)li * 8 * D : nullptr;
       float *y32 = Ly.cln[0] ? (float *)e->dw32 : nullptr;
-      {
-        ProfScope ps(ctx, "dwconv_gen");
-        const dim3 grid(mx[3], n, cdiv(D / 4, 64));
+      if (y32 && D % 4 == 0 && D <= 1024) {  // depthwise + conv-module LayerNorm + SiLU (+ the stream's conv cache) in one kernel
+        ProfScope ps(ctx, "dwconv_ln");
+        float *cco = sp ? sp->cc_out + (size_t)li * 8 * D : nullptr;
+        const dim3 grid(mx[3], n);
         if (glu32)
-          FA_LAUNCH(ps, dwconv_gen_kernel<float>, grid, dim3(64), 0, ctx->stream, (const float *)g32, cache, s3, o.conv_causal, Ly.dww, Ly.dwb, D, a, dlo, y32);
+          FA_LAUNCH(ps, dwconv_ln_kernel<float>, grid, dim3(256), 0, ctx->stream, (const float *)g32, cache, s3, o.conv_causal, Ly.dww, Ly.dwb, Ly.cln[0],
+                    Ly.cln[1], D, a, dlo, cco, sp ? sp->nemit : 0);
         else
-          FA_LAUNCH(ps, dwconv_gen_kernel<_Float16>, grid, dim3(64), 0, ctx->stream, (const _Float16 *)gg, cache, s3, o.conv_causal, Ly.dww, Ly.dwb, D, a, dlo,
-                    y32);
-        FA_TRY(check_launch(ctx, "dwconv_gen"));
-      }
-      if (y32) FA_TRY(ln_into(y32, Ly.cln[0], Ly.cln[1], a, dlo, true, "conv_ln_silu"));
-      if (sp) {
-        ProfScope ps(ctx, "stream_conv_cache");
-        float *cco = sp->cc_out + (size_t)li * 8 * D;
-        if (glu32)
-          FA_LAUNCH(ps, stream_conv_cache_kernel<float>, dim3(8), dim3(256), 0, ctx->stream, cache, (const float *)g32, D, sp->nemit, cco);
-        else
-          FA_LAUNCH(ps, stream_conv_cache_kernel<_Float16>, dim3(8), dim3(256), 0, ctx->stream, cache, (const _Float16 *)gg, D, sp->nemit, cco);
-        FA_TRY(check_launch(ctx, "stream_conv_cache"));
+          FA_LAUNCH(ps, dwconv_ln_kernel<_Float16>, grid, dim3(256), 0, ctx->stream, (const _Float16 *)gg, cache, s3, o.conv_causal, Ly.dww, Ly.dwb,
+                    Ly.cln[0], Ly.cln[1], D, a, dlo, cco, sp ? sp->nemit : 0);
+        FA_TRY(check_launch(ctx, "dwconv_ln"));
+      } else {
+        {
+          ProfScope ps(ctx, "dwconv_gen");
+          const dim3 grid(mx[3], n, cdiv(D / 4, 64));
+          if (glu32)
+            FA_LAUNCH(ps, dwconv_gen_kernel<float>, grid, dim3(64), 0, ctx->stream, (const float *)g32, cache, s3, o.conv_causal, Ly.dww, Ly.dwb, D, a, dlo,
+                      y32);
+          else
+            FA_LAUNCH(ps, dwconv_gen_kernel<_Float16>, grid, dim3(64), 0, ctx->stream, (const _Float16 *)gg, cache, s3, o.conv_causal, Ly.dww, Ly.dwb, D, a,
+                      dlo, y32);
+          FA_TRY(check_launch(ctx, "dwconv_gen"));
+        }
+        if (y32) FA_TRY(ln_into(y32, Ly.cln[0], Ly.cln[1], a, dlo, true, "conv_ln_silu"));
+        if (sp) {
+          ProfScope ps(ctx, "stream_conv_cache");
+          float *cco = sp->cc_out + (size_t)li * 8 * D;
+          if (glu32)
+            FA_LAUNCH(ps, stream_conv_cache_kernel<float>, dim3(8), dim3(256), 0, ctx->stream, cache, (const float *)g32, D, sp->nemit, cco);
+          else
+            FA_LAUNCH(ps, stream_conv_cache_kernel<_Float16>, dim3(8), dim3(256), 0, ctx->stream, cache, (const _Float16 *)gg, D, sp->nemit, cco);
+          FA_TRY(check_launch(ctx, "stream_conv_cache"));
+        }
       }
     }
     FA_TRY(gemm(a, dlo, D, Ly.pw2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, dlo ? "pw2_x" : "pw2"));
