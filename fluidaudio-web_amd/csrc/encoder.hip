@@ -1123,7 +1123,7 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
     p.A = e->s2; p.lda = 2 * C; p.akind = A_F16;
     set_gemm_b(p, e->c2);
     p.C = e->s2p; p.ldc = C;
-    p.M = R[2] * F2;
+    p.M = R[2] * F2; p.allow_skinny = sp != nullptr;
     FA_TRY(gemm_mfma(ctx, p, "sub_pw2"));
   }
   {
@@ -1137,7 +1137,7 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
     p.A = e->s3; p.lda = 2 * C; p.akind = A_F16;
     set_gemm_b(p, e->c4);
     p.C = e->s3p; p.ldc = 2 * C; p.out_f16 = 1; p.hilo = 1;
-    p.M = R[3] * F3;
+    p.M = R[3] * F3; p.allow_skinny = sp != nullptr;
     FA_TRY(gemm_mfma(ctx, p, "sub_pw4"));
   }
   {
@@ -1145,7 +1145,7 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
     p.A = e->s3p; p.lda = 2 * C * F3; p.akind = A_F16;
     set_gemm_b(p, e->lin);
     p.C = x; p.ldc = D;
-    p.M = M;
+    p.M = M; p.allow_skinny = sp != nullptr;
     FA_TRY(gemm_mfma(ctx, p, "sub_linear"));
   }
 
@@ -1197,7 +1197,7 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
     }
     p.C = Cp; p.Clo = Clo; p.ldc = ldc; p.out_f16 = out_f16; p.act = act;
     p.add = add; p.ldadd = ldc; p.glu = glu;
-    p.M = M;
+    p.M = M; p.allow_skinny = sp != nullptr;
     return gemm_mfma(ctx, p, label);
   };
   _Float16 *hlo = (_Float16 *)e->hlo, *ulo = (_Float16 *)e->ulo, *alo = (_Float16 *)e->alo;
@@ -1264,7 +1264,7 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
       p.A = h; p.Alo = hl; p.lda = D; p.akind = A_F16;
       set_gemm_b(p, Ly.qkv);
       p.C = u; p.ldc = 3 * D; p.out_f16 = 1;
-      p.M = M;
+      p.M = M; p.allow_skinny = sp != nullptr;
       if (!sp && c.HD == 128 && e->vt_fuse && gemm_takes_direct(ctx, p)) {
         p.vt = (_Float16 *)e->vt; p.vrow = (const int *)e->vrow; p.vcol0 = 2 * D; p.vtp = Tp;
         vt_fused = true;

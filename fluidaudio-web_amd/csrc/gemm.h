@@ -25,6 +25,10 @@ struct GemmArgs {
   int ldc = 0;
   int out_f16 = 0;
   const float *colscale = nullptr;  // int8 per-output-column scale
+  // the skinny route (<= 32 rows: K split over waves, so its sums are ordered
+  // differently from the tiled kernels'); set by the streaming passes only, so
+  // an offline batch's frames do not depend on how many windows it holds
+  int allow_skinny = 0;
   const float *bias = nullptr;      // [N]
   const float *add = nullptr;       // f32 residual [M, ldadd]; may alias C
   int ldadd = 0;

@@ -816,7 +816,7 @@ static inline bool takes_skinny(const GemmArgs &p) {
   const char *e = getenv("FA_GEMM_SKINNY");
   if (e && e[0] == '0') return false;
   const int ks = skinny_ks(p.N);
-  return p.M <= 32 && p.akind == A_F16 && p.bkind == B_F16 && !p.vt && epi_of(p) != EPI_GENERIC && p.N % 16 == 0 && p.K % (32 * ks) == 0 &&
+  return p.allow_skinny && p.M <= 32 && p.akind == A_F16 && p.bkind == B_F16 && !p.vt && epi_of(p) != EPI_GENERIC && p.N % 16 == 0 && p.K % (32 * ks) == 0 &&
          p.lda % 8 == 0 && p.ldc % 8 == 0 && !((uintptr_t)p.A & 15) && !((uintptr_t)p.Alo & 15) && !((uintptr_t)p.B & 15) && !((uintptr_t)p.C & 15) &&
          !((uintptr_t)p.Clo & 15) && !((uintptr_t)p.add & 15) && p.ldadd % 4 == 0;
 }
