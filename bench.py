@@ -3,8 +3,8 @@
 Default workload: the full 24-layer encoder with
 the dw-striding 8x front end over 16 windows of 15 s (1500 log-mel frames,
 128 bins, ~N(0,1), seed 1), random-init f16 weights (seed 1).  One step =
-pack the 16 windows out of the resident feature stream + the whole encoder
-forward.  value = audio-s / wall-s over the K timed steps (inputs resident in
+the whole encoder forward over the 16 windows, read in place from the
+resident channel-major feature stream (no packed copy).  value = audio-s / wall-s over the K timed steps (inputs resident in
 HBM, output left on the device).
 
 The JSON line also carries
@@ -96,7 +96,7 @@ def kernel_work(cfg, lens, layout):
         "v_transpose": ("byte", M * D * 2 * 2),
         "attention": ("flop", att), "attention_x": ("flop", att),
         "dwconv": ("byte", M * D * 4), "dwconv_f32": ("byte", M * D * 6), "dwconv_lo": ("byte", M * D * 6), "dwconv_x": ("byte", M * D * 8),
-        "zero_pad": ("byte", 0), "enc_in": ("byte", R0 * MB * 8), "enc_out": ("byte", M * D * 8),
+        "zero_pad": ("byte", 0), "enc_src": ("byte", 0), "enc_in": ("byte", R0 * MB * 8), "enc_out": ("byte", M * D * 8),
     }
     for ln in ("ln_ff1", "ln_att", "ln_conv", "ln_ff2"):
         w[ln] = ("byte", M * D * 6)       # f32 in, f16 out
@@ -212,7 +212,8 @@ def cpu_baseline():
 
 def run_encoder(args, fa, ctx, cfg, batches, feats_h, layout, fmt="f16", seed=1):
     """batches: list of (starts, lens) into the resident feature stream feats_h
-    [melBins, T].  One step = pack + encode every batch."""
+    [melBins, T].  One step = encode every batch, its windows read in place
+    from the stream (fa_encoder_forward_stream)."""
     man = fa.synth.make_weights(cfg, seed=seed)
     log(f"[bench] weights generated ({sum(v.size for v in man.values()) / 1e6:.0f} M values); loading {fmt}")
     max_T = max(fa.tsub(int(t)) for _, ln in batches for t in ln)
@@ -224,8 +225,7 @@ def run_encoder(args, fa, ctx, cfg, batches, feats_h, layout, fmt="f16", seed=1)
 
     def run_batch(st, ln):
         a = ctx.pushArena()
-        mel = ctx.packWindows(feats, st, ln, layout)
-        enc.forward(mel, ln, layout)
+        enc.forwardStream(feats, st, ln, layout)
         ctx.popArena(a)
 
     def step():
@@ -319,15 +319,15 @@ def main():
             workload = "configs[1]-shaped: one FastConformer layer (plus front end), 8 windows x 188 frames"
         else:
             workload = ("configs[2]: 24-layer FastConformer encoder + dw-striding 8x subsampling, 16 windows x 15 s "
-                        "(1500 mel frames), packed on-GPU")
+                        "(1500 mel frames), read in place from the feature stream")
     else:
         total = 360000
         starts, lens = fa.windowing.planRaggedWindows(total, 200, 3000, 100, seed=1)
         feats_h = rng.standard_normal((cfg["melBins"], total), dtype=np.float32)
         batches = [(starts[b], lens[b]) for b in (np.asarray(g) for g in fa.windowing.packBatches(lens, 32))]
         audio_s = total * 0.01  # the stream's span: overlaps are not counted twice
-        workload = (f"configs[3]: 3600 s stream cut into {len(lens)} ragged windows (2-30 s, 1 s overlap), packed on-GPU "
-                    f"into {len(batches)} batches of <= 32 (sorted by length), 24 layers")
+        workload = (f"configs[3]: 3600 s stream cut into {len(lens)} ragged windows (2-30 s, 1 s overlap), read in place "
+                    f"as {len(batches)} batches of <= 32 (sorted by length), 24 layers")
     fmt = {"quant": "int8", "quant4": "int4"}.get(args.workload, "f16")
     r = run_encoder(args, fa, ctx, cfg, batches, feats_h, layout, fmt)
     kern = summarize(r["recs"], 1)

@@ -125,6 +125,7 @@ SIGNATURES = [
     ("fa_encoder_load_opts", I, [P, C.POINTER(EncoderCfg), C.POINTER(EncoderOpts), I, C.POINTER(C.c_char_p), C.POINTER(F32P), C.POINTER(C.c_int64), I, I,
                                  C.POINTER(P)]),
     ("fa_encoder_forward", I, [P, P, T, I32P, I, I, I, C.POINTER(T)]),
+    ("fa_encoder_forward_stream", I, [P, P, T, I32P, I32P, I, I, I, C.POINTER(T)]),
     ("fa_encoder_tsub", I, [I]),
     ("fa_encoder_tsub_of", I, [P, I]),
     ("fa_stream_create", I, [P, P, I, I, C.POINTER(P)]),

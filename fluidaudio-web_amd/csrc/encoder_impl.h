@@ -64,6 +64,9 @@ struct fa_encoder {
   // caller's (pool-recycled) tensors; copies in and out run outside the graph
   void *melw = nullptr, *xw = nullptr;
   size_t cap_melw = 0, cap_xw = 0;
+  // device MelSrc of the channel-major forward (fa_encoder_forward_stream)
+  void *msrc = nullptr;
+  size_t cap_msrc = 0;
   void *dw32 = nullptr;  // f32 depthwise output ahead of the conv-module LayerNorm
   size_t cap_dw32 = 0;
   void *wdq = nullptr;  // quantised formats, batches of >= kDequantRows rows: one layer's linears widened to f16
@@ -71,6 +74,16 @@ struct fa_encoder {
 };
 
 namespace fa {
+
+// Where the channel-major feature stream [melBins, ttot] lives and where each
+// window starts in it (column).  Kept in device memory so that a captured
+// forward reads it at replay time: a new stream or new window starts need no
+// recapture, only a refresh of these bytes before the launch.
+struct MelSrc {
+  const float *ptr;
+  long ttot;
+  int start[kMaxWin];
+};
 
 // One pass of the encoder over a batch of windows: stage tables for the four
 // time resolutions (mel, after each stride-2 conv), frequency bins per stage,
@@ -81,6 +94,9 @@ struct PassGeom {
   WinStage s[4];
   int mx[4] = {0, 0, 0, 0}, R[4] = {0, 0, 0, 0}, F[4] = {0, 0, 0, 0};
   int M = 0;
+  // set: the front end reads the channel-major feature stream this device
+  // descriptor names (MelSrc) instead of time-major rows at s[0].off
+  const MelSrc *mel_src = nullptr;
 };
 
 // A streaming chunk pass: the frames of this pass attend to `Lc` cached keys

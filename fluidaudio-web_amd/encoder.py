@@ -278,6 +278,20 @@ class FusedEncoder:
                                                     0 if layout == "packed" else 1, layers, C.byref(o)))
         return self.ctx._t(o.value)
 
+    def forwardStream(self, feats: HipTensor, starts, lens, layout: str = "packed", layers: int = -1) -> HipTensor:
+        """Windows [starts[i], starts[i]+lens[i]) of the channel-major feature
+        stream feats [melBins, T] (melWindows' output), encoded without a
+        packed copy (fa_encoder_forward_stream); frames as forward() returns
+        them for packWindows(feats, starts, lens, layout)."""
+        s = np.ascontiguousarray(starts, np.int32)
+        l = np.ascontiguousarray(lens, np.int32)
+        if len(s) != len(l):
+            raise ValueError("forwardStream: %d starts for %d windows" % (len(s), len(l)))
+        o = L.T()
+        check(self.ctx._p, lib().fa_encoder_forward_stream(self.ctx._p, self._p, feats.h, s.ctypes.data_as(L.I32P), l.ctypes.data_as(L.I32P),
+                                                           len(l), 0 if layout == "packed" else 1, layers, C.byref(o)))
+        return self.ctx._t(o.value)
+
     def encode(self, mels: list, layout: str = "packed", layers: int = -1) -> np.ndarray:
         """Convenience: list of [melBins, T_i] windows -> list of [Tsub_i, D] arrays."""
         lens = [m.shape[1] for m in mels]
@@ -286,8 +300,7 @@ class FusedEncoder:
         feats = self.ctx.upload(stream, stream.shape[0], stream.shape[1])
         arena = self.ctx.pushArena()
         try:
-            packed = self.ctx.packWindows(feats, starts, lens, layout)
-            y = self.forward(packed, lens, layout, layers)
+            y = self.forwardStream(feats, starts, lens, layout, layers)
             out = self.ctx.download(y).reshape(y.rows, y.cols)
         finally:
             self.ctx.popArena(arena)

@@ -515,6 +515,22 @@ static napi_value js_encoder_forward(napi_env env, napi_callback_info info) {
   return st ? throw_status(env, c, st) : mkbig(env, o);
 }
 
+static napi_value js_encoder_forward_stream(napi_env env, napi_callback_info info) {
+  /* (ctx, enc, feats, Int32Array starts, Int32Array lens, layout, layers) */
+  napi_value a[MAXA];
+  if (!args(env, info, 7, a)) return NULL;
+  CTX;
+  size_t nb1 = 0, nb2 = 0;
+  int32_t *starts = typed_as(env, a[3], napi_int32_array, &nb1), *lens = typed_as(env, a[4], napi_int32_array, &nb2);
+  if (!starts || !lens || nb1 != nb2) {
+    napi_throw_type_error(env, NULL, "encoderForwardStream: starts/lens must be Int32Arrays of one length");
+    return NULL;
+  }
+  fa_tensor o = 0;
+  int st = fa_encoder_forward_stream(c, ext(env, a[1]), T(2), starts, lens, (int)(nb2 / 4), I(5), I(6), &o);
+  return st ? throw_status(env, c, st) : mkbig(env, o);
+}
+
 static napi_value js_encoder_destroy(napi_env env, napi_callback_info info) {
   napi_value a[MAXA];
   if (!args(env, info, 1, a)) return NULL;
@@ -546,7 +562,8 @@ static napi_value init(napi_env env, napi_value exports) {
       EXPORT("sliceCols", js_slice_cols), EXPORT("setCols", js_set_cols), EXPORT("sliceRows", js_slice_rows), EXPORT("copyRows", js_copy_rows),
       EXPORT("concatRows", js_concat_rows), EXPORT("subReshape", js_sub_reshape), EXPORT("rowBiasAct", js_row_bias_act),
       EXPORT("profileStart", js_profile_start), EXPORT("profileEnd", js_profile_end), EXPORT("packWindows", js_pack_windows), EXPORT("melWindows", js_mel_windows),
-      EXPORT("encoderLoad", js_encoder_load), EXPORT("encoderForward", js_encoder_forward), EXPORT("encoderDestroy", js_encoder_destroy),
+      EXPORT("encoderLoad", js_encoder_load), EXPORT("encoderForward", js_encoder_forward),
+      EXPORT("encoderForwardStream", js_encoder_forward_stream), EXPORT("encoderDestroy", js_encoder_destroy),
       EXPORT("encoderTsub", js_encoder_tsub), EXPORT("tdtLoad", js_tdt_load), EXPORT("tdtDecode", js_tdt_decode), EXPORT("tdtDestroy", js_tdt_destroy),
       EXPORT("leakyRelu", js_leaky_relu), EXPORT("snake", js_snake), EXPORT("adain", js_adain), EXPORT("im2col", js_im2col),
       EXPORT("convTranspose1d", js_conv_transpose1d), EXPORT("gatherCols", js_gather_cols), EXPORT("lstm", js_lstm), EXPORT("jbatch", js_jbatch),

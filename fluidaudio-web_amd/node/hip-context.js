@@ -296,8 +296,7 @@ class HipContext {
     const starts = new Int32Array(lens.length);
     for (let i = 1; i < lens.length; i++) starts[i] = starts[i - 1] + lens[i - 1];
     const feats = this.upload(stream, mb, total);
-    const mel = addon.packWindows(this.ctx, feats.h, starts, lens, layout === "packed" ? 0 : 1);
-    const out = this._info(addon.encoderForward(this.ctx, fused.enc, mel, lens, layout === "packed" ? 0 : 1, -1));
+    const out = this._info(addon.encoderForwardStream(this.ctx, fused.enc, feats.h, starts, lens, layout === "packed" ? 0 : 1, -1));
     this.freeTensor(feats);
     return out;
   }

@@ -9,7 +9,7 @@ The reference overlaps three stages across CPU and GPU (mel and the WASM
 decode on the CPU, the encoder on the GPU).  Here every stage runs on the GPU
 on the context's stream, so the host only plans windows and stitches tokens:
   PCM (uploaded once) -> fa_mel_windows (all windows of a group)
-    -> fa_pack_windows -> fa_encoder_forward (ragged batch)
+    -> fa_encoder_forward_stream (ragged batch read in place from the stream)
     -> matmul(projW, projB) -> fa_tdt_decode (all windows in lock-step)
     -> tokens back to the host -> stitch.
 Projected frames never leave the device.  A group holds up to `wb` windows
@@ -107,8 +107,7 @@ def transcribeWindowed(ctx, enc, dec, projW, projB, samples, sampleRate: int = 1
             arena = ctx.pushArena()
             try:
                 feats = ctx.melWindows(pcm, st, ln)
-                packed = ctx.packWindows(feats, offs, T)
-                y = enc.forward(packed, T)
+                y = enc.forwardStream(feats, offs, T)
                 proj = ctx.matmul(y, projW, bias=projB)
                 ts = [tsub(t) for t in T]
                 res = dec.decodeBatch(proj, ts)

@@ -376,6 +376,15 @@ int fa_encoder_get_exact(const fa_encoder *enc, int layer);
  * 1 <= n <= 32 (FA_E_UNSUPPORTED above: the largest batch validated on the GPU).
  * layers_run < 0 runs all layers. */
 int fa_encoder_forward(fa_ctx *ctx, fa_encoder *enc, fa_tensor mel, const int32_t *lens, int n, int layout, int layers_run, fa_tensor *out);
+/* The same encode with the windows read in place from the channel-major
+ * feature stream feats [melBins, T] (fa_mel_windows' output, the layout
+ * fa_pack_windows reads): window i = columns [starts[i], starts[i]+lens[i]).
+ * out equals fa_encoder_forward(fa_pack_windows(feats, starts, lens, layout))
+ * bit for bit, with no packed copy made.  Replaces the per-window transpose
+ * + encoder call of the reference's encode path (raw-encoder.js:181-182,
+ * pipeline.js:74).  Windows may overlap; starts/lens are host arrays. */
+int fa_encoder_forward_stream(fa_ctx *ctx, fa_encoder *enc, fa_tensor feats, const int32_t *starts, const int32_t *lens, int n, int layout,
+                              int layers_run, fa_tensor *out);
 /* Subsampled length of a window of T mel frames (raw-encoder.js:217-218). */
 int fa_encoder_tsub(int T);
 /* The same for this encoder's subsampling pads. */

@@ -183,3 +183,45 @@ def test_attention_workgroup_shapes_agree(ctx, fa, small, monkeypatch):
     b = np.concatenate(enc.encode(mels))
     enc.close()
     assert rel_l2(a, b) < 2e-3, rel_l2(a, b)
+
+
+@pytest.mark.parametrize("lds", ["1", "0"])
+@pytest.mark.parametrize("layout", ["packed", "padded"])
+def test_forward_stream_equals_pack_then_forward(ctx, fa, small, monkeypatch, layout, lds):
+    """Windows read in place from the channel-major feature stream
+    (fa_encoder_forward_stream) give the bits of fa_pack_windows followed by
+    fa_encoder_forward: overlapping windows, one ending on the stream's last
+    frame, a 1-frame window, ragged first / last c0 rows; the front end's LDS
+    mel staging and its per-tap global loads; eager and graph replays, the
+    replays moving the same window lengths to other starts (the captured
+    forward reads the starts from device memory refreshed per call)."""
+    monkeypatch.setenv("FA_C01_LDS", lds)
+    enc = fa.FusedEncoder(ctx, small, "f16", max_T=188)
+    T = 4000
+    stream = fa.synth.make_features(128, T, seed=90)[0]
+    f = ctx.upload(stream, 128, T)
+    lens = np.array([1500, 777, 1, 1001, 9], np.int32)
+    for rep, starts in enumerate(([0, 700, 3999, T - 1001, 13], [5, 0, 17, 2999, 3991], [2500, 1200, 0, 1, 3000])):
+        starts = np.asarray(starts, np.int32)
+        for graph in ("0", "1"):
+            monkeypatch.setenv("FA_GRAPH", graph)
+            y0 = enc.forward(ctx.packWindows(f, starts, lens, layout), lens, layout)
+            y1 = enc.forwardStream(f, starts, lens, layout)
+            a = ctx.download(y0).reshape(y0.rows, y0.cols)
+            b = ctx.download(y1).reshape(y1.rows, y1.cols)
+            assert a.shape == b.shape
+            assert np.array_equal(a, b), f"starts set {rep}, graph {graph}: max diff {np.abs(a - b).max()}"
+    ctx.freeTensor(f)
+    enc.close()
+
+
+def test_forward_stream_rejects_windows_outside_the_stream(ctx, fa, small):
+    enc = fa.FusedEncoder(ctx, small, "f16", max_T=64)
+    f = ctx.upload(np.zeros((128, 100), np.float32), 128, 100)
+    for starts, lens in (([0, 90], [50, 11]), ([-1], [10]), ([0], [101])):
+        with pytest.raises(Exception, match="outside the 100-frame stream"):
+            enc.forwardStream(f, starts, lens)
+    with pytest.raises(Exception, match="features must be f32"):
+        enc.forwardStream(ctx.upload(np.zeros((64, 100), np.float32), 64, 100), [0], [50])
+    ctx.freeTensor(f)
+    enc.close()
