@@ -126,6 +126,7 @@ SIGNATURES = [
                                  C.POINTER(P)]),
     ("fa_encoder_forward", I, [P, P, T, I32P, I, I, I, C.POINTER(T)]),
     ("fa_encoder_forward_stream", I, [P, P, T, I32P, I32P, I, I, I, C.POINTER(T)]),
+    ("fa_encoder_forward_stream_batches", I, [P, P, T, I, I32P, I32P, I32P, I, I, C.POINTER(T)]),
     ("fa_encoder_tsub", I, [I]),
     ("fa_encoder_tsub_of", I, [P, I]),
     ("fa_stream_create", I, [P, P, I, I, C.POINTER(P)]),

@@ -897,7 +897,7 @@ static int grow(fa_encoder *e, void **buf, size_t *cap, size_t need) {
   if (need <= *cap) return FA_OK;
   e->ws_gen++;
   if (*buf) {
-    (void)hipStreamSynchronize(e->ctx->stream);
+    (void)hipDeviceSynchronize();  // the buffer may be in use on the context stream or a lane stream
     (void)hipFree(*buf);
     *buf = nullptr;
     *cap = 0;
@@ -944,8 +944,8 @@ static inline int enc_tsub(const fa_encoder_opts &o, int T) {
 // stream just before the replay (input staging).
 int encoder_graph_run(fa_ctx *ctx, fa_encoder *e, const std::vector<int64_t> &key, const std::function<int()> &launch,
                       const std::function<int()> &pre) {
-  fa_encoder::Captured *hit = nullptr;
-  for (auto &gr : e->graphs)
+  EncWs::Captured *hit = nullptr;
+  for (auto &gr : e->W().graphs)
     if (gr.key == key) hit = &gr;
   if (!hit) {
     FA_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
@@ -962,18 +962,18 @@ int encoder_graph_run(fa_ctx *ctx, fa_encoder *e, const std::vector<int64_t> &ke
     (void)hipGraphDestroy(graph);
     if (ie != hipSuccess) return set_err(ctx, FA_E_DEVICE, "encoder: graph instantiate: %s", hipGetErrorString(ie));
     constexpr size_t kMaxGraphs = 16;
-    if (e->graphs.size() >= kMaxGraphs) {  // evict the least recently used
+    if (e->W().graphs.size() >= kMaxGraphs) {  // evict the least recently used
       size_t lru = 0;
-      for (size_t i = 1; i < e->graphs.size(); i++)
-        if (e->graphs[i].used < e->graphs[lru].used) lru = i;
-      (void)hipStreamSynchronize(ctx->stream);  // the evicted graph may still be running on this stream
-      (void)hipGraphExecDestroy(e->graphs[lru].exec);
-      e->graphs.erase(e->graphs.begin() + lru);
+      for (size_t i = 1; i < e->W().graphs.size(); i++)
+        if (e->W().graphs[i].used < e->W().graphs[lru].used) lru = i;
+      (void)hipDeviceSynchronize();  // the evicted graph may still be running (context or lane stream)
+      (void)hipGraphExecDestroy(e->W().graphs[lru].exec);
+      e->W().graphs.erase(e->W().graphs.begin() + lru);
     }
-    e->graphs.push_back({key, exec, 0});
-    hit = &e->graphs.back();
+    e->W().graphs.push_back({key, exec, 0});
+    hit = &e->W().graphs.back();
   }
-  hit->used = ++e->graph_clock;
+  hit->used = ++e->W().graph_clock;
   if (pre) FA_TRY(pre());
   FA_HIP(ctx, hipGraphLaunch(hit->exec, ctx->stream));
   return FA_OK;
@@ -1077,32 +1077,32 @@ static size_t wdq_bytes(const fa_encoder *e) {
 int pass_workspace(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, int layers, bool stream) {
   const fa_encoder_cfg &c = e->cfg;
   const int D = c.D, C = c.Csub, M = g.M;
-  FA_TRY(grow(e, &e->s2, &e->cap_s2, (size_t)g.R[2] * g.F[2] * 2 * C * 2));  // hi/lo f16
-  FA_TRY(grow(e, &e->s2p, &e->cap_s2p, (size_t)g.R[2] * g.F[2] * C * 4));    // f32 pre-ReLU
-  FA_TRY(grow(e, &e->s3, &e->cap_s3, (size_t)g.R[3] * g.F[3] * 2 * C * 2));  // hi/lo f16
-  FA_TRY(grow(e, &e->s3p, &e->cap_s3p, (size_t)g.R[3] * g.F[3] * 2 * C * 2));  // hi/lo f16
+  FA_TRY(grow(e, &e->W().s2, &e->W().cap_s2, (size_t)g.R[2] * g.F[2] * 2 * C * 2));  // hi/lo f16
+  FA_TRY(grow(e, &e->W().s2p, &e->W().cap_s2p, (size_t)g.R[2] * g.F[2] * C * 4));    // f32 pre-ReLU
+  FA_TRY(grow(e, &e->W().s3, &e->W().cap_s3, (size_t)g.R[3] * g.F[3] * 2 * C * 2));  // hi/lo f16
+  FA_TRY(grow(e, &e->W().s3p, &e->W().cap_s3p, (size_t)g.R[3] * g.F[3] * 2 * C * 2));  // hi/lo f16
   const size_t need_m = (size_t)M * D * 2, need_u = (size_t)M * std::max(c.DFF, 3 * D) * 2;
-  if (need_m > e->cap_m) {
+  if (need_m > e->W().cap_m) {
     size_t c1 = 0, c2 = 0, c3 = 0;
-    if (e->h) { (void)hipStreamSynchronize(ctx->stream); (void)hipFree(e->h); (void)hipFree(e->a); (void)hipFree(e->g); e->h = e->a = e->g = nullptr; e->ws_gen++; }
-    FA_TRY(grow(e, &e->h, &c1, need_m));
-    FA_TRY(grow(e, &e->a, &c2, need_m));
-    FA_TRY(grow(e, &e->g, &c3, need_m));
-    e->cap_m = need_m;
+    if (e->W().h) { (void)hipDeviceSynchronize(); (void)hipFree(e->W().h); (void)hipFree(e->W().a); (void)hipFree(e->W().g); e->W().h = e->W().a = e->W().g = nullptr; e->ws_gen++; }
+    FA_TRY(grow(e, &e->W().h, &c1, need_m));
+    FA_TRY(grow(e, &e->W().a, &c2, need_m));
+    FA_TRY(grow(e, &e->W().g, &c3, need_m));
+    e->W().cap_m = need_m;
   }
-  FA_TRY(grow(e, &e->u, &e->cap_u, need_u));
+  FA_TRY(grow(e, &e->W().u, &e->W().cap_u, need_u));
   unsigned any = 0;
   bool cln = false;
   for (int li = 0; li < layers; li++) {
     any |= e->L[li].exact;
     cln |= e->L[li].cln[0] != nullptr;
   }
-  if (any & FA_EXACT_LN_OUT) FA_TRY(grow(e, &e->hlo, &e->cap_hlo, (size_t)M * D * 2));
-  if (any & FA_EXACT_FF_HIDDEN) FA_TRY(grow(e, &e->ulo, &e->cap_ulo, (size_t)M * c.DFF * 2));
-  if (any & (FA_EXACT_ATTN_OUT | FA_EXACT_DW_OUT)) FA_TRY(grow(e, &e->alo, &e->cap_alo, (size_t)M * D * 2));
-  if (any & FA_EXACT_GLU) FA_TRY(grow(e, &e->g32, &e->cap_g32, (size_t)M * D * 4));
-  if (cln) FA_TRY(grow(e, &e->dw32, &e->cap_dw32, (size_t)M * D * 4));
-  if (e->format != FA_W_F16 && M >= kDequantRows) FA_TRY(grow(e, &e->wdq, &e->cap_wdq, wdq_bytes(e)));
+  if (any & FA_EXACT_LN_OUT) FA_TRY(grow(e, &e->W().hlo, &e->W().cap_hlo, (size_t)M * D * 2));
+  if (any & FA_EXACT_FF_HIDDEN) FA_TRY(grow(e, &e->W().ulo, &e->W().cap_ulo, (size_t)M * c.DFF * 2));
+  if (any & (FA_EXACT_ATTN_OUT | FA_EXACT_DW_OUT)) FA_TRY(grow(e, &e->W().alo, &e->W().cap_alo, (size_t)M * D * 2));
+  if (any & FA_EXACT_GLU) FA_TRY(grow(e, &e->W().g32, &e->W().cap_g32, (size_t)M * D * 4));
+  if (cln) FA_TRY(grow(e, &e->W().dw32, &e->W().cap_dw32, (size_t)M * D * 4));
+  if (e->format != FA_W_F16 && M >= kDequantRows) FA_TRY(grow(e, &e->W().wdq, &e->W().cap_wdq, wdq_bytes(e)));
   if (!stream) {
     // transposed V per (window, head), written by the q|k|v GEMM's epilogue
     // (or v_transpose_kernel).  Keys past a window's end are never written:
@@ -1110,9 +1110,9 @@ int pass_workspace(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, int layers, bo
     // earlier forwards there, which the attention weights by exactly 0.
     const int Tp = (g.mx[3] + 63) / 64 * 64;
     const uint64_t gen = e->ws_gen;
-    FA_TRY(grow(e, &e->vt, &e->cap_vt, (size_t)g.n * c.H * c.HD * Tp * 2));
-    if (e->ws_gen != gen) FA_HIP(ctx, hipMemsetAsync(e->vt, 0, e->cap_vt, ctx->stream));
-    FA_TRY(grow(e, &e->vrow, &e->cap_vrow, (size_t)M * 4));
+    FA_TRY(grow(e, &e->W().vt, &e->W().cap_vt, (size_t)g.n * c.H * c.HD * Tp * 2));
+    if (e->ws_gen != gen) FA_HIP(ctx, hipMemsetAsync(e->W().vt, 0, e->W().cap_vt, ctx->stream));
+    FA_TRY(grow(e, &e->W().vrow, &e->W().cap_vrow, (size_t)M * 4));
   }
   return FA_OK;
 }
@@ -1128,39 +1128,39 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
   const WinStage &s0 = g.s[0], &s1 = g.s[1], &s2 = g.s[2], &s3 = g.s[3];
   const int *mx = g.mx, *R = g.R;
   const int Tp = (mx[3] + 63) / 64 * 64;
-  _Float16 *h = (_Float16 *)e->h, *u = (_Float16 *)e->u, *a = (_Float16 *)e->a, *gg = (_Float16 *)e->g;
+  _Float16 *h = (_Float16 *)e->W().h, *u = (_Float16 *)e->W().u, *a = (_Float16 *)e->W().a, *gg = (_Float16 *)e->W().g;
   // ── subsampling ──
   {
     ProfScope ps(ctx, "sub_c01");
-    FA_TRY(launch_c01(ctx, ps, dim3(cdiv(mx[2], 4), n), melp, MB, s0, s1, F1, s2, F2, e->c0w, e->c0b, e->c1w, e->c1b, (_Float16 *)e->s2, C, e->c01_lds,
+    FA_TRY(launch_c01(ctx, ps, dim3(cdiv(mx[2], 4), n), melp, MB, s0, s1, F1, s2, F2, e->c0w, e->c0b, e->c1w, e->c1b, (_Float16 *)e->W().s2, C, e->c01_lds,
                       g.pt, o.sub_pad_l, o.sub_pad_r, g.mel_src));
     FA_TRY(check_launch(ctx, "sub_c01"));
   }
   {
     GemmArgs p;  // c2 (1x1) + bias; its ReLU is applied by the c3 kernel's loads
-    p.A = e->s2; p.lda = 2 * C; p.akind = A_F16;
+    p.A = e->W().s2; p.lda = 2 * C; p.akind = A_F16;
     set_gemm_b(p, e->c2);
-    p.C = e->s2p; p.ldc = C;
+    p.C = e->W().s2p; p.ldc = C;
     p.M = R[2] * F2; p.allow_skinny = sp != nullptr;
     FA_TRY(gemm_mfma(ctx, p, "sub_pw2"));
   }
   {
     ProfScope ps(ctx, "sub_dw3");
-    FA_TRY(launch_dw(ctx, ps, dim3(cdiv(mx[3], 4), n), (const float *)e->s2p, s2, F2, s3, F3, e->c3w, e->c3b, (_Float16 *)e->s3, C,
-                     sp ? nullptr : (int *)e->vrow, c.H * c.HD * Tp, layout == 1 ? mx[3] : 0, g.pt, o.sub_pad_l));
+    FA_TRY(launch_dw(ctx, ps, dim3(cdiv(mx[3], 4), n), (const float *)e->W().s2p, s2, F2, s3, F3, e->c3w, e->c3b, (_Float16 *)e->W().s3, C,
+                     sp ? nullptr : (int *)e->W().vrow, c.H * c.HD * Tp, layout == 1 ? mx[3] : 0, g.pt, o.sub_pad_l));
     FA_TRY(check_launch(ctx, "sub_dw3"));
   }
   {
     GemmArgs p;  // c4 (1x1) + bias + ReLU, written as hi/lo pairs for the linear
-    p.A = e->s3; p.lda = 2 * C; p.akind = A_F16;
+    p.A = e->W().s3; p.lda = 2 * C; p.akind = A_F16;
     set_gemm_b(p, e->c4);
-    p.C = e->s3p; p.ldc = 2 * C; p.out_f16 = 1; p.hilo = 1;
+    p.C = e->W().s3p; p.ldc = 2 * C; p.out_f16 = 1; p.hilo = 1;
     p.M = R[3] * F3; p.allow_skinny = sp != nullptr;
     FA_TRY(gemm_mfma(ctx, p, "sub_pw4"));
   }
   {
     GemmArgs p;
-    p.A = e->s3p; p.lda = 2 * C * F3; p.akind = A_F16;
+    p.A = e->W().s3p; p.lda = 2 * C * F3; p.akind = A_F16;
     set_gemm_b(p, e->lin);
     p.C = x; p.ldc = D;
     p.M = M; p.allow_skinny = sp != nullptr;
@@ -1180,7 +1180,7 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
   auto dequant_layer = [&](const fa_encoder::Layer &Ly) -> int {
     WdqList &W = wdq;
     W = WdqList{};
-    _Float16 *dst = (_Float16 *)e->wdq;
+    _Float16 *dst = (_Float16 *)e->W().wdq;
     long units = 0;
     for (const Lin *L : layer_lins(Ly)) {
       if (L->bkind == B_F16) continue;
@@ -1218,8 +1218,8 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
     p.M = M; p.allow_skinny = sp != nullptr;
     return gemm_mfma(ctx, p, label);
   };
-  _Float16 *hlo = (_Float16 *)e->hlo, *ulo = (_Float16 *)e->ulo, *alo = (_Float16 *)e->alo;
-  float *g32 = (float *)e->g32;
+  _Float16 *hlo = (_Float16 *)e->W().hlo, *ulo = (_Float16 *)e->W().ulo, *alo = (_Float16 *)e->W().alo;
+  float *g32 = (float *)e->W().g32;
   // LayerNorm of rows `src` into the f16 operand dst (+ lo plane); silu: the conv-module LayerNorm
   auto ln_into = [&](const float *src, const float *gm, const float *bt, _Float16 *dst, _Float16 *lo, bool silu, const char *label) -> int {
     if (D % 256 == 0 && D <= 2048) {
@@ -1284,7 +1284,7 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
       p.C = u; p.ldc = 3 * D; p.out_f16 = 1;
       p.M = M; p.allow_skinny = sp != nullptr;
       if (!sp && c.HD == 128 && e->vt_fuse && gemm_takes_direct(ctx, p)) {
-        p.vt = (_Float16 *)e->vt; p.vrow = (const int *)e->vrow; p.vcol0 = 2 * D; p.vtp = Tp;
+        p.vt = (_Float16 *)e->W().vt; p.vrow = (const int *)e->W().vrow; p.vcol0 = 2 * D; p.vtp = Tp;
         vt_fused = true;
       }
       FA_TRY(gemm_mfma(ctx, p, hl ? "qkv_x" : "qkv"));
@@ -1295,7 +1295,7 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
       at.pbu = Ly.pbu;
       at.pbv = Ly.pbv;
       at.out_lo = olo;
-      FA_TRY(relpos_attention_f16(ctx, at, mx[3], (_Float16 *)e->vt, olo ? "attention_x" : "attention", !vt_fused));
+      FA_TRY(relpos_attention_f16(ctx, at, mx[3], (_Float16 *)e->W().vt, olo ? "attention_x" : "attention", !vt_fused));
     } else {
       const size_t kvo = (size_t)li * sp->kv_ld * D;
       {
@@ -1326,7 +1326,7 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
       FA_TRY(check_launch(ctx, "dwconv"));
     } else {
       const float *cache = sp ? sp->cc_in + (size_t)li * 8 * D : nullptr;
-      float *y32 = Ly.cln[0] ? (float *)e->dw32 : nullptr;
+      float *y32 = Ly.cln[0] ? (float *)e->W().dw32 : nullptr;
       if (y32 && D % 4 == 0 && D <= 1024) {  // depthwise + conv-module LayerNorm + SiLU (+ the stream's conv cache) in one kernel
         ProfScope ps(ctx, "dwconv_ln");
         float *cco = sp ? sp->cc_out + (size_t)li * 8 * D : nullptr;
@@ -1451,12 +1451,12 @@ static int encoder_forward_impl(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const
   const char *ge = getenv("FA_GRAPH");
   const bool use_graph = !ctx->prof_on && !(ge && ge[0] == '0');
   if (stream) {
-    FA_TRY(grow(e, &e->msrc, &e->cap_msrc, sizeof(MelSrc)));
-    g.mel_src = (const MelSrc *)e->msrc;
+    FA_TRY(grow(e, &e->W().msrc, &e->W().cap_msrc, sizeof(MelSrc)));
+    g.mel_src = (const MelSrc *)e->W().msrc;
   }
   if (use_graph) {
-    if (!stream) FA_TRY(grow(e, &e->melw, &e->cap_melw, (size_t)g.R[0] * MB * 4));
-    FA_TRY(grow(e, &e->xw, &e->cap_xw, (size_t)M * D * 4));
+    if (!stream) FA_TRY(grow(e, &e->W().melw, &e->W().cap_melw, (size_t)g.R[0] * MB * 4));
+    FA_TRY(grow(e, &e->W().xw, &e->W().cap_xw, (size_t)M * D * 4));
   }
   fa_tensor ox;
   TensorRec *rx;
@@ -1466,7 +1466,7 @@ static int encoder_forward_impl(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const
   auto set_src = [&]() -> int {
     src.ptr = (const float *)rm->ptr;
     ProfScope ps(ctx, "enc_src");
-    FA_LAUNCH(ps, set_mel_src_kernel, dim3(1), dim3(64), 0, ctx->stream, src, (MelSrc *)e->msrc);
+    FA_LAUNCH(ps, set_mel_src_kernel, dim3(1), dim3(64), 0, ctx->stream, src, (MelSrc *)e->W().msrc);
     return check_launch(ctx, "enc_src");
   };
   if (!use_graph) {  // profiling (its events are per launch) or FA_GRAPH=0
@@ -1486,9 +1486,9 @@ static int encoder_forward_impl(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const
   key.insert(key.end(), lens, lens + n);
   FA_TRY(encoder_graph_run(
       ctx, e, key,
-      [&]() { return pass_launch(ctx, e, g, stream ? nullptr : (const float *)e->melw, (float *)e->xw, layers, nullptr); },
-      [&]() { return stream ? set_src() : copy_f4(ctx, rm->ptr, e->melw, (size_t)g.R[0] * MB * 4, "enc_in"); }));
-  FA_TRY(copy_f4(ctx, e->xw, xout, (size_t)M * D * 4, "enc_out"));
+      [&]() { return pass_launch(ctx, e, g, stream ? nullptr : (const float *)e->W().melw, (float *)e->W().xw, layers, nullptr); },
+      [&]() { return stream ? set_src() : copy_f4(ctx, rm->ptr, e->W().melw, (size_t)g.R[0] * MB * 4, "enc_in"); }));
+  FA_TRY(copy_f4(ctx, e->W().xw, xout, (size_t)M * D * 4, "enc_out"));
   *out = ox;
   return FA_OK;
 }
@@ -1516,12 +1516,19 @@ int fa_quantize_weights(int format, const float *w, int K, int N, void *q_out, v
 
 void fa_encoder_destroy(fa_encoder *enc) {
   if (!enc) return;
-  (void)hipStreamSynchronize(enc->ctx->stream);
+  (void)hipDeviceSynchronize();  // the context stream and the lane streams
   for (void *p : enc->allocs) (void)hipFree(p);
-  for (auto &g : enc->graphs)
-    if (g.exec) (void)hipGraphExecDestroy(g.exec);
-  for (void *p : {enc->hlo, enc->ulo, enc->alo, enc->g32, enc->vt, enc->vrow, enc->s2, enc->s2p, enc->s3, enc->s3p, enc->h, enc->u, enc->a, enc->g, enc->melw, enc->xw, enc->dw32, enc->wdq, enc->msrc})
-    if (p) (void)hipFree(p);
+  for (auto &w : enc->ws) {
+    for (auto &g : w.graphs)
+      if (g.exec) (void)hipGraphExecDestroy(g.exec);
+    for (void *p : {w.hlo, w.ulo, w.alo, w.g32, w.vt, w.vrow, w.s2, w.s2p, w.s3, w.s3p, w.h, w.u, w.a, w.g, w.melw, w.xw, w.dw32, w.wdq, w.msrc})
+      if (p) (void)hipFree(p);
+  }
+  for (int l = 0; l < fa_encoder::kLanes; l++) {
+    if (enc->lane_done[l]) (void)hipEventDestroy(enc->lane_done[l]);
+    if (enc->lane_stream[l]) (void)hipStreamDestroy(enc->lane_stream[l]);
+  }
+  if (enc->lanes_in) (void)hipEventDestroy(enc->lanes_in);
   delete enc;
 }
 
@@ -1851,6 +1858,54 @@ int fa_encoder_forward_stream(fa_ctx *ctx, fa_encoder *e, fa_tensor feats, const
                               int layers_run, fa_tensor *out) {
   if (!starts) return set_err(ctx, FA_E_INVALID, "encoderForwardStream: no window starts");
   return encoder_forward_impl(ctx, e, feats, starts, 0, lens, n, layout, layers_run, out, "encoderForwardStream");
+}
+
+// Several batches of one feature stream, each exactly as fa_encoder_forward_stream
+// computes it, with consecutive batches on two workspace lanes that run on
+// streams of their own: while one batch's kernel tails and end-of-kernel
+// write-backs drain, the other batch's kernels fill the idle CUs (measured
+// two 16-window batches in 13.4 ms against 2 x 7.5 ms).  The lanes
+// start after the work already queued on the context stream, and the context
+// stream waits for both before anything queued after this call.
+int fa_encoder_forward_stream_batches(fa_ctx *ctx, fa_encoder *e, fa_tensor feats, int nb, const int32_t *starts, const int32_t *lens,
+                                      const int32_t *counts, int layout, int layers_run, fa_tensor *outs) {
+  const char *who = "encoderForwardStreamBatches";
+  if (!e || e->ctx != ctx) return set_err(ctx, FA_E_INVALID, "%s: encoder belongs to another context", who);
+  if (nb <= 0 || !starts || !lens || !counts || !outs) return set_err(ctx, FA_E_INVALID, "%s: no batches", who);
+  for (int b = 0; b < nb; b++)
+    if (counts[b] <= 0) return set_err(ctx, FA_E_INVALID, "%s: batch %d has %d windows", who, b, counts[b]);
+  if (nb == 1) return encoder_forward_impl(ctx, e, feats, starts, 0, lens, counts[0], layout, layers_run, outs, who);
+  for (int l = 0; l < fa_encoder::kLanes; l++) {
+    if (!e->lane_stream[l]) FA_HIP(ctx, hipStreamCreateWithFlags(&e->lane_stream[l], hipStreamNonBlocking));
+    if (!e->lane_done[l]) FA_HIP(ctx, hipEventCreateWithFlags(&e->lane_done[l], hipEventDisableTiming));
+  }
+  if (!e->lanes_in) FA_HIP(ctx, hipEventCreateWithFlags(&e->lanes_in, hipEventDisableTiming));
+  FA_HIP(ctx, hipEventRecord(e->lanes_in, ctx->stream));
+  const hipStream_t home = ctx->stream;
+  int st = FA_OK;
+  bool used[fa_encoder::kLanes] = {false, false};
+  long off = 0;
+  for (int b = 0; b < nb && st == FA_OK; b++) {
+    const int l = b % fa_encoder::kLanes;
+    if (!used[l]) {
+      st = hipStreamWaitEvent(e->lane_stream[l], e->lanes_in, 0) == hipSuccess ? FA_OK : set_err(ctx, FA_E_DEVICE, "%s: stream wait", who);
+      used[l] = true;
+    }
+    if (st != FA_OK) break;
+    // the batch's launches (and the tensors' pool bookkeeping) go to the lane's stream
+    ctx->stream = e->lane_stream[l];
+    e->lane = l;
+    st = encoder_forward_impl(ctx, e, feats, starts + off, 0, lens + off, counts[b], layout, layers_run, &outs[b], who);
+    e->lane = 0;
+    ctx->stream = home;
+    off += counts[b];
+  }
+  for (int l = 0; l < fa_encoder::kLanes; l++)
+    if (used[l]) {
+      (void)hipEventRecord(e->lane_done[l], e->lane_stream[l]);
+      (void)hipStreamWaitEvent(home, e->lane_done[l], 0);
+    }
+  return st;
 }
 
 }  // extern "C"

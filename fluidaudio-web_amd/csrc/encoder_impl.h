@@ -23,6 +23,36 @@ struct Lin {
   int N = 0, K = 0;
 };
 
+// One workspace lane of the fused encoder: grow-only device buffers and the
+// forwards captured on them.
+struct EncWs {
+  // captured forwards (hipGraph), keyed by everything baked into the launch
+  // arguments; ws_gen moves whenever a workspace buffer or a precision mask
+  // changes (the encoder's ws_gen), so stale graphs never match again
+  struct Captured {
+    std::vector<int64_t> key;
+    hipGraphExec_t exec = nullptr;
+    uint64_t used = 0;
+  };
+  std::vector<Captured> graphs;
+  uint64_t graph_clock = 0;
+  // workspace (grow-only)
+  void *hlo = nullptr, *ulo = nullptr, *alo = nullptr, *g32 = nullptr, *vt = nullptr, *vrow = nullptr, *s2 = nullptr, *s2p = nullptr, *s3 = nullptr, *s3p = nullptr, *h = nullptr, *u = nullptr, *a = nullptr, *g = nullptr;
+  size_t cap_hlo = 0, cap_ulo = 0, cap_alo = 0, cap_g32 = 0, cap_vt = 0, cap_vrow = 0, cap_s2 = 0, cap_s2p = 0, cap_s3 = 0, cap_s3p = 0, cap_m = 0, cap_u = 0;
+  // graph-mode input and residual-stream buffers: a captured forward reads the
+  // mel rows from melw and works on xw, so its launches never name the
+  // caller's (pool-recycled) tensors; copies in and out run outside the graph
+  void *melw = nullptr, *xw = nullptr;
+  size_t cap_melw = 0, cap_xw = 0;
+  // device MelSrc of the channel-major forward (fa_encoder_forward_stream)
+  void *msrc = nullptr;
+  size_t cap_msrc = 0;
+  void *dw32 = nullptr;  // f32 depthwise output ahead of the conv-module LayerNorm
+  size_t cap_dw32 = 0;
+  void *wdq = nullptr;  // quantised formats, batches of >= kDequantRows rows: one layer's linears widened to f16
+  size_t cap_wdq = 0;
+};
+
 }  // namespace fa
 
 struct fa_encoder {
@@ -44,33 +74,19 @@ struct fa_encoder {
     unsigned exact = 0;     // FA_EXACT_* operands carried as exact f16 hi/lo pairs
   };
   std::vector<Layer> L;
-  // captured forwards (hipGraph), keyed by everything baked into the launch
-  // arguments; ws_gen moves whenever a workspace buffer or a precision mask
-  // changes, so stale graphs never match again
-  struct Captured {
-    std::vector<int64_t> key;
-    hipGraphExec_t exec = nullptr;
-    uint64_t used = 0;
-  };
-  std::vector<Captured> graphs;
-  uint64_t ws_gen = 0, graph_clock = 0;
+  uint64_t ws_gen = 0;
   bool vt_fuse = true;  // q|k|v epilogue writes the transposed V (FA_VT_FUSE=0 at load: v_transpose_kernel)
   bool c01_lds = true;  // front end stages mel rows in LDS (FA_C01_LDS=0 at load: per-tap global loads)
-  // workspace (grow-only)
-  void *hlo = nullptr, *ulo = nullptr, *alo = nullptr, *g32 = nullptr, *vt = nullptr, *vrow = nullptr, *s2 = nullptr, *s2p = nullptr, *s3 = nullptr, *s3p = nullptr, *h = nullptr, *u = nullptr, *a = nullptr, *g = nullptr;
-  size_t cap_hlo = 0, cap_ulo = 0, cap_alo = 0, cap_g32 = 0, cap_vt = 0, cap_vrow = 0, cap_s2 = 0, cap_s2p = 0, cap_s3 = 0, cap_s3p = 0, cap_m = 0, cap_u = 0;
-  // graph-mode input and residual-stream buffers: a captured forward reads the
-  // mel rows from melw and works on xw, so its launches never name the
-  // caller's (pool-recycled) tensors; copies in and out run outside the graph
-  void *melw = nullptr, *xw = nullptr;
-  size_t cap_melw = 0, cap_xw = 0;
-  // device MelSrc of the channel-major forward (fa_encoder_forward_stream)
-  void *msrc = nullptr;
-  size_t cap_msrc = 0;
-  void *dw32 = nullptr;  // f32 depthwise output ahead of the conv-module LayerNorm
-  size_t cap_dw32 = 0;
-  void *wdq = nullptr;  // quantised formats, batches of >= kDequantRows rows: one layer's linears widened to f16
-  size_t cap_wdq = 0;
+  // Workspace lanes: a forward works in ws[lane] on that lane's stream.  Lane
+  // 0 runs on the context stream; fa_encoder_forward_stream_batches puts
+  // consecutive batches on two lanes with streams of their own, so one batch's
+  // kernel tails and end-of-kernel write-backs overlap the other's work.
+  static constexpr int kLanes = 2;
+  fa::EncWs ws[kLanes];
+  int lane = 0;
+  hipStream_t lane_stream[kLanes] = {nullptr, nullptr};
+  hipEvent_t lane_done[kLanes] = {nullptr, nullptr}, lanes_in = nullptr;
+  fa::EncWs &W() { return ws[lane]; }
 };
 
 namespace fa {

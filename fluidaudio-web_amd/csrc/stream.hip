@@ -48,7 +48,7 @@ struct fa_stream {
   float *mel_dev = nullptr, *x_dev = nullptr;
   size_t mel_cap = 0, x_cap = 0;
   uint64_t buf_gen = 0;  // moves when mel_dev / x_dev are reallocated
-  std::vector<fa_encoder::Captured> graphs;
+  std::vector<EncWs::Captured> graphs;
   uint64_t graph_clock = 0;
 };
 
@@ -109,7 +109,7 @@ int run_pass(fa_stream *st, int m, int pt, int pb, int nComp, int nemit, std::ve
   const bool steady = st->Lc == st->left && pb == 0 && pt == 0;
   if (steady && !ctx->prof_on && !(ge && ge[0] == '0')) {
     std::vector<int64_t> key = {(int64_t)e->ws_gen, (int64_t)st->buf_gen, m, nComp, nemit, st->cur};
-    fa_encoder::Captured *hit = nullptr;
+    EncWs::Captured *hit = nullptr;
     for (auto &gr : st->graphs)
       if (gr.key == key) hit = &gr;
     if (!hit) {

@@ -292,6 +292,28 @@ class FusedEncoder:
                                                            len(l), 0 if layout == "packed" else 1, layers, C.byref(o)))
         return self.ctx._t(o.value)
 
+    def forwardStreamBatches(self, feats: HipTensor, batches, layout: str = "packed", layers: int = -1) -> list:
+        """Several batches [(starts, lens), ...] of one feature stream; outputs
+        equal forwardStream of each batch, bit for bit.  Consecutive batches
+        run on two workspace lanes with streams of their own, so they overlap
+        on the GPU (fa_encoder_forward_stream_batches); the windowed
+        transcription's loop over groups (pipeline.js:66-80) in one call."""
+        if not batches:
+            return []
+        st = [np.ascontiguousarray(b[0], np.int32) for b in batches]
+        ln = [np.ascontiguousarray(b[1], np.int32) for b in batches]
+        for s_, l_ in zip(st, ln):
+            if len(s_) != len(l_) or len(l_) == 0:
+                raise ValueError("forwardStreamBatches: %d starts for %d windows" % (len(s_), len(l_)))
+        s = np.ascontiguousarray(np.concatenate(st), np.int32)
+        l = np.ascontiguousarray(np.concatenate(ln), np.int32)
+        cnt = np.array([len(x) for x in ln], np.int32)
+        outs = (L.T * len(batches))()
+        check(self.ctx._p, lib().fa_encoder_forward_stream_batches(self.ctx._p, self._p, feats.h, len(batches), s.ctypes.data_as(L.I32P),
+                                                                   l.ctypes.data_as(L.I32P), cnt.ctypes.data_as(L.I32P),
+                                                                   0 if layout == "packed" else 1, layers, outs))
+        return [self.ctx._t(o) for o in outs]
+
     def encode(self, mels: list, layout: str = "packed", layers: int = -1) -> np.ndarray:
         """Convenience: list of [melBins, T_i] windows -> list of [Tsub_i, D] arrays."""
         lens = [m.shape[1] for m in mels]

@@ -385,6 +385,15 @@ int fa_encoder_forward(fa_ctx *ctx, fa_encoder *enc, fa_tensor mel, const int32_
  * pipeline.js:74).  Windows may overlap; starts/lens are host arrays. */
 int fa_encoder_forward_stream(fa_ctx *ctx, fa_encoder *enc, fa_tensor feats, const int32_t *starts, const int32_t *lens, int n, int layout,
                               int layers_run, fa_tensor *out);
+/* nb batches of one feature stream: batch b = the next counts[b] windows of
+ * starts/lens, outs[b] = fa_encoder_forward_stream of that batch, bit for bit.
+ * Consecutive batches run on two workspace lanes with streams of their own,
+ * so one batch's kernel tails and write-backs overlap the next batch's
+ * kernels; the lanes start after the work queued on the context stream and
+ * the context stream waits for both.  Replaces the loop over window groups
+ * of the reference's windowed transcription (pipeline.js:66-80). */
+int fa_encoder_forward_stream_batches(fa_ctx *ctx, fa_encoder *enc, fa_tensor feats, int nb, const int32_t *starts, const int32_t *lens,
+                                      const int32_t *counts, int layout, int layers_run, fa_tensor *outs);
 /* Subsampled length of a window of T mel frames (raw-encoder.js:217-218). */
 int fa_encoder_tsub(int T);
 /* The same for this encoder's subsampling pads. */

@@ -225,3 +225,44 @@ def test_forward_stream_rejects_windows_outside_the_stream(ctx, fa, small):
         enc.forwardStream(ctx.upload(np.zeros((64, 100), np.float32), 64, 100), [0], [50])
     ctx.freeTensor(f)
     enc.close()
+
+
+@pytest.mark.parametrize("graph", ["1", "0"])
+def test_forward_stream_batches_equal_one_batch_at_a_time(ctx, fa, small, monkeypatch, graph):
+    """fa_encoder_forward_stream_batches (consecutive batches on two workspace
+    lanes with streams of their own) gives every batch the bits of
+    fa_encoder_forward_stream: five ragged batches of different window counts
+    (so the two lanes hold different workspace sizes and captured forwards),
+    called twice in a row (graph replays on the lanes), then a single-batch
+    call and a plain forward on the context stream reading the same buffers'
+    lane 0 afterwards."""
+    monkeypatch.setenv("FA_GRAPH", graph)
+    enc = fa.FusedEncoder(ctx, small, "f16", max_T=188)
+    T = 6000
+    stream = fa.synth.make_features(128, T, seed=91)[0]
+    f = ctx.upload(stream, 128, T)
+    rng = np.random.default_rng(5)
+    batches = []
+    for n in (3, 1, 5, 2, 4):
+        lens = rng.integers(1, 1501, n).astype(np.int32)
+        starts = np.array([rng.integers(0, T - l + 1) for l in lens], np.int32)
+        batches.append((starts, lens))
+    want = []
+    for st, ln in batches:
+        y = enc.forwardStream(f, st, ln)
+        want.append(ctx.download(y).reshape(y.rows, y.cols))
+    for call in range(2):
+        outs = enc.forwardStreamBatches(f, batches)
+        assert len(outs) == len(batches)
+        for b, (y, w) in enumerate(zip(outs, want)):
+            got = ctx.download(y).reshape(y.rows, y.cols)
+            assert got.shape == w.shape
+            assert np.array_equal(got, w), f"call {call}, batch {b}: max diff {np.abs(got - w).max()}"
+    one = enc.forwardStreamBatches(f, batches[2:3])[0]
+    assert np.array_equal(ctx.download(one).reshape(one.rows, one.cols), want[2])
+    y = enc.forwardStream(f, *batches[4])
+    assert np.array_equal(ctx.download(y).reshape(y.rows, y.cols), want[4])
+    with pytest.raises(Exception, match="no batches|windows"):
+        enc.forwardStreamBatches(f, [(np.array([], np.int32), np.array([], np.int32))])
+    ctx.freeTensor(f)
+    enc.close()
