@@ -1598,6 +1598,7 @@ int fa_encoder_load_opts(fa_ctx *ctx, const fa_encoder_cfg *cfg, const fa_encode
   e->maxT = max_T;
   if (const char *vf = getenv("FA_VT_FUSE")) e->vt_fuse = vf[0] != '0';
   if (const char *cl = getenv("FA_C01_LDS")) e->c01_lds = cl[0] != '0';
+  if (const char *nl = getenv("FA_ENC_LANES")) e->nlanes = std::max(1, std::min(fa_encoder::kLanes, atoi(nl)));
   auto fail = [&](int st) {
     fa_encoder_destroy(e);
     return st;
@@ -1875,7 +1876,7 @@ int fa_encoder_forward_stream_batches(fa_ctx *ctx, fa_encoder *e, fa_tensor feat
   for (int b = 0; b < nb; b++)
     if (counts[b] <= 0) return set_err(ctx, FA_E_INVALID, "%s: batch %d has %d windows", who, b, counts[b]);
   if (nb == 1) return encoder_forward_impl(ctx, e, feats, starts, 0, lens, counts[0], layout, layers_run, outs, who);
-  for (int l = 0; l < fa_encoder::kLanes; l++) {
+  for (int l = 0; l < e->nlanes; l++) {
     if (!e->lane_stream[l]) FA_HIP(ctx, hipStreamCreateWithFlags(&e->lane_stream[l], hipStreamNonBlocking));
     if (!e->lane_done[l]) FA_HIP(ctx, hipEventCreateWithFlags(&e->lane_done[l], hipEventDisableTiming));
   }
@@ -1883,10 +1884,10 @@ int fa_encoder_forward_stream_batches(fa_ctx *ctx, fa_encoder *e, fa_tensor feat
   FA_HIP(ctx, hipEventRecord(e->lanes_in, ctx->stream));
   const hipStream_t home = ctx->stream;
   int st = FA_OK;
-  bool used[fa_encoder::kLanes] = {false, false};
+  bool used[fa_encoder::kLanes] = {};
   long off = 0;
   for (int b = 0; b < nb && st == FA_OK; b++) {
-    const int l = b % fa_encoder::kLanes;
+    const int l = b % e->nlanes;
     if (!used[l]) {
       st = hipStreamWaitEvent(e->lane_stream[l], e->lanes_in, 0) == hipSuccess ? FA_OK : set_err(ctx, FA_E_DEVICE, "%s: stream wait", who);
       used[l] = true;
@@ -1900,7 +1901,7 @@ int fa_encoder_forward_stream_batches(fa_ctx *ctx, fa_encoder *e, fa_tensor feat
     ctx->stream = home;
     off += counts[b];
   }
-  for (int l = 0; l < fa_encoder::kLanes; l++)
+  for (int l = 0; l < e->nlanes; l++)
     if (used[l]) {
       (void)hipEventRecord(e->lane_done[l], e->lane_stream[l]);
       (void)hipStreamWaitEvent(home, e->lane_done[l], 0);

@@ -81,11 +81,12 @@ struct fa_encoder {
   // 0 runs on the context stream; fa_encoder_forward_stream_batches puts
   // consecutive batches on two lanes with streams of their own, so one batch's
   // kernel tails and end-of-kernel write-backs overlap the other's work.
-  static constexpr int kLanes = 2;
+  static constexpr int kLanes = 4;  // capacity; nlanes in use (FA_ENC_LANES at load, default 2)
+  int nlanes = 2;
   fa::EncWs ws[kLanes];
   int lane = 0;
-  hipStream_t lane_stream[kLanes] = {nullptr, nullptr};
-  hipEvent_t lane_done[kLanes] = {nullptr, nullptr}, lanes_in = nullptr;
+  hipStream_t lane_stream[kLanes] = {};
+  hipEvent_t lane_done[kLanes] = {}, lanes_in = nullptr;
   fa::EncWs &W() { return ws[lane]; }
 };
 
