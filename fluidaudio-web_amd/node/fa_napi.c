@@ -531,6 +531,42 @@ static napi_value js_encoder_forward_stream(napi_env env, napi_callback_info inf
   return st ? throw_status(env, c, st) : mkbig(env, o);
 }
 
+static napi_value js_encoder_forward_stream_batches(napi_env env, napi_callback_info info) {
+  /* (ctx, enc, feats, Int32Array starts, Int32Array lens, Int32Array counts, layout, layers) -> [BigInt tensor per batch] */
+  napi_value a[MAXA];
+  if (!args(env, info, 8, a)) return NULL;
+  CTX;
+  size_t nb1 = 0, nb2 = 0, nb3 = 0;
+  int32_t *starts = typed_as(env, a[3], napi_int32_array, &nb1), *lens = typed_as(env, a[4], napi_int32_array, &nb2);
+  int32_t *counts = typed_as(env, a[5], napi_int32_array, &nb3);
+  if (!starts || !lens || !counts || nb1 != nb2 || nb3 == 0) {
+    napi_throw_type_error(env, NULL, "encoderForwardStreamBatches: starts/lens/counts must be Int32Arrays (starts, lens of one length)");
+    return NULL;
+  }
+  const int nb = (int)(nb3 / 4);
+  long total = 0;
+  for (int b = 0; b < nb; b++) total += counts[b];
+  if (total != (long)(nb2 / 4)) {
+    napi_throw_type_error(env, NULL, "encoderForwardStreamBatches: counts must sum to the number of windows");
+    return NULL;
+  }
+  fa_tensor *outs = (fa_tensor *)calloc((size_t)nb, sizeof(fa_tensor));
+  if (!outs) {
+    napi_throw_error(env, NULL, "encoderForwardStreamBatches: out of host memory");
+    return NULL;
+  }
+  int st = fa_encoder_forward_stream_batches(c, ext(env, a[1]), T(2), nb, starts, lens, counts, I(6), I(7), outs);
+  if (st) {
+    free(outs);
+    return throw_status(env, c, st);
+  }
+  napi_value arr;
+  NA(napi_create_array_with_length(env, (size_t)nb, &arr));
+  for (int b = 0; b < nb; b++) NA(napi_set_element(env, arr, (uint32_t)b, mkbig(env, outs[b])));
+  free(outs);
+  return arr;
+}
+
 static napi_value js_encoder_destroy(napi_env env, napi_callback_info info) {
   napi_value a[MAXA];
   if (!args(env, info, 1, a)) return NULL;
@@ -563,7 +599,8 @@ static napi_value init(napi_env env, napi_value exports) {
       EXPORT("concatRows", js_concat_rows), EXPORT("subReshape", js_sub_reshape), EXPORT("rowBiasAct", js_row_bias_act),
       EXPORT("profileStart", js_profile_start), EXPORT("profileEnd", js_profile_end), EXPORT("packWindows", js_pack_windows), EXPORT("melWindows", js_mel_windows),
       EXPORT("encoderLoad", js_encoder_load), EXPORT("encoderForward", js_encoder_forward),
-      EXPORT("encoderForwardStream", js_encoder_forward_stream), EXPORT("encoderDestroy", js_encoder_destroy),
+      EXPORT("encoderForwardStream", js_encoder_forward_stream), EXPORT("encoderForwardStreamBatches", js_encoder_forward_stream_batches),
+      EXPORT("encoderDestroy", js_encoder_destroy),
       EXPORT("encoderTsub", js_encoder_tsub), EXPORT("tdtLoad", js_tdt_load), EXPORT("tdtDecode", js_tdt_decode), EXPORT("tdtDestroy", js_tdt_destroy),
       EXPORT("leakyRelu", js_leaky_relu), EXPORT("snake", js_snake), EXPORT("adain", js_adain), EXPORT("im2col", js_im2col),
       EXPORT("convTranspose1d", js_conv_transpose1d), EXPORT("gatherCols", js_gather_cols), EXPORT("lstm", js_lstm), EXPORT("jbatch", js_jbatch),

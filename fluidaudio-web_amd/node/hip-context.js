@@ -300,6 +300,17 @@ class HipContext {
     this.freeTensor(feats);
     return out;
   }
+  /** Several batches [{starts, lens}] of one resident feature stream [melBins, T]:
+   * each output equals encoderForwardStream of that batch, bit for bit, with
+   * consecutive batches in flight on the encoder's two workspace lanes
+   * (fa_encoder_forward_stream_batches); the group loop of pipeline.js:66-80. */
+  _encodeFusedStreamBatches(fused, feats, batches, layout = "packed") {
+    const counts = Int32Array.from(batches.map((b) => b.lens.length));
+    const starts = Int32Array.from([].concat(...batches.map((b) => Array.from(b.starts))));
+    const lens = Int32Array.from([].concat(...batches.map((b) => Array.from(b.lens))));
+    const hs = addon.encoderForwardStreamBatches(this.ctx, fused.enc, feats.h, starts, lens, counts, layout === "packed" ? 0 : 1, -1);
+    return hs.map((h) => this._info(h));
+  }
   /** Log-mel features (ParakeetMel.process semantics, parakeet-mel.js:14-22) of
    * windows [starts[i], starts[i]+lens[i]) of a resident f32 sample tensor ->
    * f32 tensor [nMels, Σ floor(lens[i]/160)] in the stream layout packWindows
