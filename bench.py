@@ -633,11 +633,34 @@ def bench_stream(args, fa, ctx):
         k["ms"] += r["ms"]
     kern = {lab: {"launches_per_chunk": v["launches"] // prof_chunks, "us_per_chunk": round(v["ms"] * 1e3 / prof_chunks, 1)}
             for lab, v in sorted(kern.items(), key=lambda kv: -kv[1]["ms"])}
+    # several streams in flight: each 160 ms tick pushes one piece to every
+    # stream in one fa_stream_push_many call (each stream's passes on a HIP
+    # stream of its own)
+    def run_many(n):
+        sts = [fa.createEncodeStream(ctx, enc) for _ in range(n)]
+        for t in range(0, mel.shape[1], piece):
+            fa.encodeStreamsPush(ctx, sts, [mel[:, t:t + piece]] * n)
+        for st in sts:
+            fa.encodeStreamFlush(ctx, st)
+            fa.disposeEncodeStream(ctx, st)
+
+    concurrent = {}
+    for n in (4, 8, 16):
+        run_many(n)
+        ctx.sync()
+        t0 = time.perf_counter()
+        run_many(n)
+        ctx.sync()
+        wn = time.perf_counter() - t0
+        concurrent[str(n)] = {"aggregate_audio_s_per_wall_s": round(n * seconds / wn, 1), "per_stream_x_real_time": round(seconds / wn, 1),
+                              "ms_per_tick": round(wn * 1e3 / chunks, 3)}
+        log(f"[bench] {n} streams: {concurrent[str(n)]}")
     line = {"metric": "streaming encode audio-s/wall-s per stream at 1 GPU", "value": round(seconds / wall, 1), "unit": "audio-s/wall-s",
             "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 2), "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic log-mel ~N(0,1), random-init weights",
             "config": {"workload": "30 s pushed in 160 ms pieces, 24 layers d_model 1024, chunk 2 / left 70 (EOU streaming config), native fused stream",
                        "frames": frames, "chunks": chunks, "ms_per_chunk": round(wall * 1e3 / chunks, 3)},
+            "concurrent_streams": concurrent,
             "kernels_eager_per_chunk": kern,
             "kernel_us_per_chunk_eager": round(sum(v["us_per_chunk"] for v in kern.values()), 1)}
     if not args.no_cpu:

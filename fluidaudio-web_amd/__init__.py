@@ -16,9 +16,9 @@ from .mel import JsPreprocessor, ParakeetMel
 from .decoder import TdtDecoder
 from . import synth, windowing
 from .pipeline import createStitcher, transcribeWindowed
-from .streaming import createEncodeStream, disposeEncodeStream, encodeStreamFlush, encodeStreamPush
+from .streaming import createEncodeStream, disposeEncodeStream, encodeStreamFlush, encodeStreamPush, encodeStreamsPush
 
 __all__ = ["ACT", "FaError", "lib", "HipContext", "HipTensor", "PackedBytes", "createContext", "FusedEncoder", "inferConfig",
            "loadParakeetEncoder", "parakeetEncodeBatch", "posEncoding", "tsub", "synth", "windowing", "JsPreprocessor", "ParakeetMel", "TdtDecoder",
            "createStitcher", "transcribeWindowed",
-           "createEncodeStream", "encodeStreamPush", "encodeStreamFlush", "disposeEncodeStream"]
+           "createEncodeStream", "encodeStreamPush", "encodeStreamFlush", "disposeEncodeStream", "encodeStreamsPush"]

@@ -131,6 +131,7 @@ SIGNATURES = [
     ("fa_encoder_tsub_of", I, [P, I]),
     ("fa_stream_create", I, [P, P, I, I, C.POINTER(P)]),
     ("fa_stream_push", I, [P, F32P, I, C.POINTER(T)]),
+    ("fa_stream_push_many", I, [I, C.POINTER(P), C.POINTER(F32P), C.POINTER(I), C.POINTER(T)]),
     ("fa_stream_flush", I, [P, C.POINTER(T)]),
     ("fa_stream_destroy", None, [P]),
 ]

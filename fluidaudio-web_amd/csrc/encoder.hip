@@ -980,6 +980,14 @@ int encoder_graph_run(fa_ctx *ctx, fa_encoder *e, const std::vector<int64_t> &ke
 }
 
 int encoder_grow(fa_encoder *e, void **buf, size_t *cap, size_t need) { return grow(e, buf, cap, need); }
+void encoder_ws_free(EncWs &w) {
+  for (auto &g : w.graphs)
+    if (g.exec) (void)hipGraphExecDestroy(g.exec);
+  w.graphs.clear();
+  for (void *p : {w.hlo, w.ulo, w.alo, w.g32, w.vt, w.vrow, w.s2, w.s2p, w.s3, w.s3p, w.h, w.u, w.a, w.g, w.melw, w.xw, w.dw32, w.wdq, w.msrc})
+    if (p) (void)hipFree(p);
+  w = EncWs();
+}
 int encoder_copy_f4(fa_ctx *ctx, const void *src, void *dst, size_t bytes, const char *label) { return copy_f4(ctx, src, dst, bytes, label); }
 
 int pass_geometry(fa_ctx *ctx, const fa_encoder *e, const int32_t *lens, int n, int layout, int pt, int pb, PassGeom *g) {
@@ -1518,12 +1526,7 @@ void fa_encoder_destroy(fa_encoder *enc) {
   if (!enc) return;
   (void)hipDeviceSynchronize();  // the context stream and the lane streams
   for (void *p : enc->allocs) (void)hipFree(p);
-  for (auto &w : enc->ws) {
-    for (auto &g : w.graphs)
-      if (g.exec) (void)hipGraphExecDestroy(g.exec);
-    for (void *p : {w.hlo, w.ulo, w.alo, w.g32, w.vt, w.vrow, w.s2, w.s2p, w.s3, w.s3p, w.h, w.u, w.a, w.g, w.melw, w.xw, w.dw32, w.wdq, w.msrc})
-      if (p) (void)hipFree(p);
-  }
+  for (auto &w : enc->ws) encoder_ws_free(w);
   for (int l = 0; l < fa_encoder::kLanes; l++) {
     if (enc->lane_done[l]) (void)hipEventDestroy(enc->lane_done[l]);
     if (enc->lane_stream[l]) (void)hipStreamDestroy(enc->lane_stream[l]);

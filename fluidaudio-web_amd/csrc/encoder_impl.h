@@ -87,7 +87,9 @@ struct fa_encoder {
   int lane = 0;
   hipStream_t lane_stream[kLanes] = {};
   hipEvent_t lane_done[kLanes] = {}, lanes_in = nullptr;
-  fa::EncWs &W() { return ws[lane]; }
+  // a streaming encoder's pass works in the stream's own workspace
+  fa::EncWs *ws_ovr = nullptr;
+  fa::EncWs &W() { return ws_ovr ? *ws_ovr : ws[lane]; }
 };
 
 namespace fa {
@@ -136,6 +138,8 @@ int pass_geometry(fa_ctx *ctx, const fa_encoder *e, const int32_t *lens, int n, 
 int pass_workspace(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, int layers, bool stream);
 int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *mel, float *x, int layers, const StreamPass *sp);
 int encoder_grow(fa_encoder *e, void **buf, size_t *cap, size_t need);
+// frees a workspace's buffers and captured forwards (the device must be idle for them)
+void encoder_ws_free(EncWs &w);
 int encoder_copy_f4(fa_ctx *ctx, const void *src, void *dst, size_t bytes, const char *label);
 int encoder_graph_run(fa_ctx *ctx, fa_encoder *e, const std::vector<int64_t> &key, const std::function<int()> &launch,
                       const std::function<int()> &pre);

@@ -50,6 +50,14 @@ struct fa_stream {
   uint64_t buf_gen = 0;  // moves when mel_dev / x_dev are reallocated
   std::vector<EncWs::Captured> graphs;
   uint64_t graph_clock = 0;
+  // Each stream's passes run on a HIP stream of its own with a workspace of
+  // its own, so several streams' passes (fa_stream_push_many) are in flight
+  // together.  A push starts after the work queued on the context stream
+  // (event `in`) and the context stream waits for it (event `done`), so its
+  // frames are ordinary context tensors.
+  EncWs ws;
+  hipStream_t hs = nullptr;
+  hipEvent_t in = nullptr, done = nullptr;
 };
 
 namespace {
@@ -71,9 +79,27 @@ int grow_buf(fa_stream *st, void **buf, size_t *cap, size_t need) {
   return FA_OK;
 }
 
+// While a pass is queued, the context's launches go to the stream's HIP stream
+// and the encoder's workspace is the stream's.
+struct PassScope {
+  fa_ctx *c;
+  fa_encoder *e;
+  hipStream_t s0;
+  EncWs *w0;
+  explicit PassScope(fa_stream *st) : c(st->ctx), e(st->enc), s0(st->ctx->stream), w0(st->enc->ws_ovr) {
+    c->stream = st->hs;
+    e->ws_ovr = &st->ws;
+  }
+  ~PassScope() {
+    c->stream = s0;
+    e->ws_ovr = w0;
+  }
+};
+
 // One pass over m mel rows at the FIFO head: nComp frames computed, the first
 // nemit emitted (appended to `outs` as a [nemit, D] tensor) and cached.
 int run_pass(fa_stream *st, int m, int pt, int pb, int nComp, int nemit, std::vector<fa_tensor> &outs) {
+  PassScope scope(st);
   fa_ctx *ctx = st->ctx;
   fa_encoder *e = st->enc;
   const fa_encoder_cfg &c = e->cfg;
@@ -164,6 +190,39 @@ int emit(fa_stream *st, std::vector<fa_tensor> &outs, fa_tensor *out) {
   return rc;
 }
 
+
+// The passes a push of `count` mel-major frames makes ready, queued on the
+// stream's HIP stream; their frames are appended to outs.
+int push_passes(fa_stream *st, const float *mel, int count, std::vector<fa_tensor> &outs) {
+  const int MB = st->enc->cfg.melBins;
+  // mel-major [melBins][count] -> frame-major FIFO rows
+  const size_t old = st->fifo.size() / MB;
+  st->fifo.resize((old + count) * MB);
+  for (int t = 0; t < count; t++)
+    for (int ch = 0; ch < MB; ch++) st->fifo[(old + t) * MB + ch] = mel[(size_t)ch * count + t];
+  for (;;) {
+    const int M = (int)(st->fifo.size() / MB);
+    // frames a pass can finish: the first pass reads 8*nComp - 7 rows (top
+    // padded), later passes 8*nComp + 7 (14 rows of look-back); nComp
+    // includes the provisional lookahead B, and n is a whole number of chunks
+    int n = st->subT == 0 ? (M + 7) / 8 - st->B : (M - 7 >= 0 ? (M - 7) / 8 : -1) - st->B;
+    n = std::min(n, st->max_chunk);
+    n -= ((n % st->C) + st->C) % st->C;
+    if (n < st->C) break;
+    const int nComp = n + st->B;
+    const int m = st->subT == 0 ? 8 * nComp - 7 : 8 * nComp + 7;
+    const int pt = st->subT == 0 ? st->enc->opts.sub_pad_t : 0;
+    FA_TRY(run_pass(st, m, pt, 0, nComp, n, outs));
+    // keep the look-back of the next pass's first frame
+    st->subT += n;
+    const long keep_from = 8L * st->subT - kLookback;
+    const long drop = keep_from - st->fifo_start;
+    st->fifo.erase(st->fifo.begin(), st->fifo.begin() + (size_t)drop * MB);
+    st->fifo_start = keep_from;
+  }
+  return FA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -202,6 +261,11 @@ int fa_stream_create(fa_ctx *ctx, fa_encoder *enc, int lookahead_chunks, int max
       return FA_E_OOM;
     }
   }
+  if (hipStreamCreateWithFlags(&st->hs, hipStreamNonBlocking) != hipSuccess || hipEventCreateWithFlags(&st->in, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&st->done, hipEventDisableTiming) != hipSuccess) {
+    fa_stream_destroy(st);
+    return set_err(ctx, FA_E_DEVICE, "createEncodeStream: creating the stream's HIP stream failed");
+  }
   // the first pass sees a zero depthwise-conv history (the offline causal pad)
   if (hipMemsetAsync(st->cc[0], 0, cb, ctx->stream) != hipSuccess) {
     fa_stream_destroy(st);
@@ -213,42 +277,48 @@ int fa_stream_create(fa_ctx *ctx, fa_encoder *enc, int lookahead_chunks, int max
 
 int fa_stream_push(fa_stream *st, const float *mel, int count, fa_tensor *out) {
   if (!st || !out) return FA_E_INVALID;
-  fa_ctx *ctx = st->ctx;
-  *out = 0;
-  if (st->flushed) return set_err(ctx, FA_E_STATE, "encodeStreamPush: stream already flushed; create a new stream");
-  if (count < 0 || (count > 0 && !mel)) return set_err(ctx, FA_E_INVALID, "encodeStreamPush: %d frames", count);
-  const int MB = st->enc->cfg.melBins;
-  // mel-major [melBins][count] -> frame-major FIFO rows
-  const size_t old = st->fifo.size() / MB;
-  st->fifo.resize((old + count) * MB);
-  for (int t = 0; t < count; t++)
-    for (int ch = 0; ch < MB; ch++) st->fifo[(old + t) * MB + ch] = mel[(size_t)ch * count + t];
-  std::vector<fa_tensor> outs;
-  for (;;) {
-    const int M = (int)(st->fifo.size() / MB);
-    // frames a pass can finish: the first pass reads 8*nComp - 7 rows (top
-    // padded), later passes 8*nComp + 7 (14 rows of look-back); nComp
-    // includes the provisional lookahead B, and n is a whole number of chunks
-    int n = st->subT == 0 ? (M + 7) / 8 - st->B : (M - 7 >= 0 ? (M - 7) / 8 : -1) - st->B;
-    n = std::min(n, st->max_chunk);
-    n -= ((n % st->C) + st->C) % st->C;
-    if (n < st->C) break;
-    const int nComp = n + st->B;
-    const int m = st->subT == 0 ? 8 * nComp - 7 : 8 * nComp + 7;
-    const int pt = st->subT == 0 ? st->enc->opts.sub_pad_t : 0;
-    const int rc = run_pass(st, m, pt, 0, nComp, n, outs);
-    if (rc) {
-      for (fa_tensor t : outs) (void)fa_free_tensor(ctx, t);
-      return rc;
-    }
-    // keep the look-back of the next pass's first frame
-    st->subT += n;
-    const long keep_from = 8L * st->subT - kLookback;
-    const long drop = keep_from - st->fifo_start;
-    st->fifo.erase(st->fifo.begin(), st->fifo.begin() + (size_t)drop * MB);
-    st->fifo_start = keep_from;
+  return fa_stream_push_many(1, &st, &mel, &count, out);
+}
+
+int fa_stream_push_many(int n, fa_stream *const *sts, const float *const *mels, const int *counts, fa_tensor *outs) {
+  if (n <= 0 || !sts || !mels || !counts || !outs) return FA_E_INVALID;
+  for (int i = 0; i < n; i++) {
+    if (!sts[i]) return FA_E_INVALID;
+    outs[i] = 0;
   }
-  return emit(st, outs, out);
+  fa_ctx *ctx = sts[0]->ctx;
+  for (int i = 0; i < n; i++) {
+    fa_stream *st = sts[i];
+    if (st->ctx != ctx) return set_err(ctx, FA_E_INVALID, "encodeStreamPush: streams of different contexts in one call");
+    for (int j = 0; j < i; j++)
+      if (sts[j] == st) return set_err(ctx, FA_E_INVALID, "encodeStreamPush: stream %d repeats stream %d in one call", i, j);
+    if (st->flushed) return set_err(ctx, FA_E_STATE, "encodeStreamPush: stream already flushed; create a new stream");
+    if (counts[i] < 0 || (counts[i] > 0 && !mels[i])) return set_err(ctx, FA_E_INVALID, "encodeStreamPush: %d frames", counts[i]);
+  }
+  // every stream's passes start after the work already queued on the context stream
+  FA_HIP(ctx, hipEventRecord(sts[0]->in, ctx->stream));
+  for (int i = 0; i < n; i++) FA_HIP(ctx, hipStreamWaitEvent(sts[i]->hs, sts[0]->in, 0));
+  std::vector<std::vector<fa_tensor>> frames(n);
+  int rc = FA_OK;
+  for (int i = 0; i < n && rc == FA_OK; i++) rc = push_passes(sts[i], mels[i], counts[i], frames[i]);
+  // the context stream waits for every stream (also after an error, so later work stays ordered)
+  for (int i = 0; i < n; i++) {
+    (void)hipEventRecord(sts[i]->done, sts[i]->hs);
+    (void)hipStreamWaitEvent(ctx->stream, sts[i]->done, 0);
+  }
+  for (int i = 0; i < n; i++) {
+    if (rc == FA_OK)
+      rc = emit(sts[i], frames[i], &outs[i]);
+    else
+      for (fa_tensor t : frames[i]) (void)fa_free_tensor(ctx, t);
+  }
+  if (rc != FA_OK)
+    for (int i = 0; i < n; i++)
+      if (outs[i]) {
+        (void)fa_free_tensor(ctx, outs[i]);
+        outs[i] = 0;
+      }
+  return rc;
 }
 
 int fa_stream_flush(fa_stream *st, fa_tensor *out) {
@@ -270,7 +340,15 @@ int fa_stream_flush(fa_stream *st, fa_tensor *out) {
   if (T <= 0) return FA_OK;
   if (T > st->enc->maxT) return set_err(ctx, FA_E_UNSUPPORTED, "encodeStreamFlush: %d tail frames > max_T", T);
   std::vector<fa_tensor> outs;
-  FA_TRY(run_pass(st, M, pt, pb, T, T, outs));
+  FA_HIP(ctx, hipEventRecord(st->in, ctx->stream));
+  FA_HIP(ctx, hipStreamWaitEvent(st->hs, st->in, 0));
+  const int rc = run_pass(st, M, pt, pb, T, T, outs);
+  (void)hipEventRecord(st->done, st->hs);
+  (void)hipStreamWaitEvent(ctx->stream, st->done, 0);
+  if (rc != FA_OK) {
+    for (fa_tensor t : outs) (void)fa_free_tensor(ctx, t);
+    return rc;
+  }
   st->fifo.clear();
   return emit(st, outs, out);
 }
@@ -278,6 +356,8 @@ int fa_stream_flush(fa_stream *st, fa_tensor *out) {
 void fa_stream_destroy(fa_stream *st) {
   if (!st) return;
   (void)hipStreamSynchronize(st->ctx->stream);
+  if (st->hs) (void)hipStreamSynchronize(st->hs);
+  encoder_ws_free(st->ws);
   for (auto &g : st->graphs)
     if (g.exec) (void)hipGraphExecDestroy(g.exec);
   for (int i = 0; i < 2; i++)
@@ -285,6 +365,9 @@ void fa_stream_destroy(fa_stream *st) {
       if (p) (void)hipFree(p);
   if (st->mel_dev) (void)hipFree(st->mel_dev);
   if (st->x_dev) (void)hipFree(st->x_dev);
+  if (st->in) (void)hipEventDestroy(st->in);
+  if (st->done) (void)hipEventDestroy(st->done);
+  if (st->hs) (void)hipStreamDestroy(st->hs);
   delete st;
 }
 

@@ -71,6 +71,24 @@ def encodeStreamPush(ctx, st: EncodeStream, mel):
     return st._frames(o.value)
 
 
+def encodeStreamsPush(ctx, streams: list, mels: list) -> list:
+    """encodeStreamPush for several distinct streams at once (fa_stream_push_many):
+    each stream's chunk passes run on a HIP stream of its own, so the streams'
+    passes are in flight together.  Returns each stream's new frames (or None)."""
+    if len(streams) != len(mels):
+        raise ValueError("encodeStreamsPush: %d streams, %d mel blocks" % (len(streams), len(mels)))
+    n = len(streams)
+    if n == 0:
+        return []
+    ms = [np.ascontiguousarray(m, np.float32) for m in mels]
+    hs = (L.P * n)(*[s._p for s in streams])
+    ps = (L.F32P * n)(*[m.ctypes.data_as(L.F32P) for m in ms])
+    cn = (C.c_int * n)(*[int(m.shape[1]) if m.ndim == 2 else 0 for m in ms])
+    outs = (L.T * n)()
+    check(ctx._p, lib().fa_stream_push_many(n, hs, ps, cn, outs))
+    return [s._frames(o) for s, o in zip(streams, outs)]
+
+
 def encodeStreamFlush(ctx, st: EncodeStream):
     """Encode the final partial chunk (bottom-padded); the stream accepts no
     push afterwards."""

@@ -138,3 +138,48 @@ def test_stream_errors(ctx, fa):
         fa.createEncodeStream(ctx, enc_r, lookaheadChunks=0)
     enc_r.close()
     enc.close()
+
+
+@pytest.mark.parametrize("graph", ["1", "0"])
+def test_streams_pushed_together_equal_streams_pushed_alone(ctx, fa, monkeypatch, graph):
+    """fa_stream_push_many: four streams of one encoder, each with its own mel
+    and its own piece pattern (so they run different pass counts and shapes
+    per call, and one ends long before the others), pushed together on their
+    own HIP streams, give every stream the bits of pushing it alone; a
+    repeated stream and a flushed stream in one call are refused."""
+    monkeypatch.setenv("FA_GRAPH", graph)
+    cfg, man, enc = _model(ctx, fa)
+    mels = [fa.synth.make_features(cfg["melBins"], n, seed=30 + i)[0] for i, n in enumerate((600, 480, 200, 640))]
+    patterns = [[16] * 38, [37, 100, 5, 64, 95, 179], [8] * 25, [24] * 27]
+    alone = [_stream(ctx, fa, enc, m, p) for m, p in zip(mels, patterns)]
+    sts = [fa.createEncodeStream(ctx, enc) for _ in mels]
+    got = [[] for _ in mels]
+    pos = [0] * len(mels)
+    for step in range(max(len(p) for p in patterns)):
+        live = [i for i, p in enumerate(patterns) if step < len(p)]
+        blocks = []
+        for i in live:
+            n = patterns[i][step]
+            blocks.append(mels[i][:, pos[i]:pos[i] + n])
+            pos[i] += n
+        for i, o in zip(live, fa.encodeStreamsPush(ctx, [sts[i] for i in live], blocks)):
+            if o is not None:
+                got[i].append(o)
+        for i in range(len(mels)):
+            if step == len(patterns[i]) - 1:
+                o = fa.encodeStreamFlush(ctx, sts[i])
+                if o is not None:
+                    got[i].append(o)
+    for i, (g, a) in enumerate(zip(got, alone)):
+        g = np.concatenate(g, 0)
+        assert g.shape == a.shape, (i, g.shape, a.shape)
+        assert np.array_equal(g, a), f"stream {i}: max diff {np.abs(g - a).max()}"
+    fresh = fa.createEncodeStream(ctx, enc)
+    with pytest.raises(fa.FaError, match="repeats"):
+        fa.encodeStreamsPush(ctx, [fresh, fresh], [mels[0][:, :8]] * 2)
+    with pytest.raises(fa.FaError, match="flushed"):
+        fa.encodeStreamsPush(ctx, [fresh, sts[1]], [mels[0][:, :8], mels[1][:, :8]])
+    fa.disposeEncodeStream(ctx, fresh)
+    for st in sts:
+        fa.disposeEncodeStream(ctx, st)
+    enc.close()
