@@ -503,12 +503,13 @@ __global__ __launch_bounds__(64) void dwconv_silu_kernel(const TI *__restrict__ 
 // value into y32 when the layer normalises the depthwise output first.
 // Thread = 4 channels of one frame.
 template <typename TI>
-__global__ __launch_bounds__(64) void dwconv_gen_kernel(const TI *__restrict__ x, const float *__restrict__ cache, WinStage st, int causal,
+__global__ __launch_bounds__(64) void dwconv_gen_kernel(const TI *__restrict__ x, const StreamSlots *__restrict__ slots, size_t cco, WinStage st, int causal,
                                                         const float *__restrict__ wt, const float *__restrict__ b, int D, _Float16 *__restrict__ y,
                                                         _Float16 *__restrict__ ylo, float *__restrict__ y32) {
   constexpr int KT = 9;
   const int win = blockIdx.y, t = blockIdx.x, T = st.len[win];
   if (t >= T) return;
+  const float *cache = slots ? slots->cc_in[win] + cco : nullptr;  // a stream pass: taps before the window's first frame
   const int c0 = (blockIdx.z * 64 + threadIdx.x) * 4;
   if (c0 >= D) return;
   const int pad = causal ? KT - 1 : (KT - 1) / 2;
@@ -523,7 +524,7 @@ __global__ __launch_bounds__(64) void dwconv_gen_kernel(const TI *__restrict__ x
     if (ti >= 0 && ti < T) {
 #pragma unroll
       for (int e = 0; e < 4; e++) v[e] = (float)x[base + (size_t)ti * D + e];
-    } else if (ti < 0 && cache && win == 0) {
+    } else if (ti < 0 && cache) {
 #pragma unroll
       for (int e = 0; e < 4; e++) v[e] = cache[(size_t)(KT - 1 + ti) * D + c0 + e];
     }
@@ -557,22 +558,24 @@ __global__ __launch_bounds__(64) void dwconv_gen_kernel(const TI *__restrict__ x
 // also writes the next pass's conv cache (rows nemit .. nemit + 7 of
 // [cache ; GLU rows]).
 template <typename TI>
-__global__ __launch_bounds__(256) void dwconv_ln_kernel(const TI *__restrict__ x, const float *__restrict__ cache, WinStage st, int causal,
+__global__ __launch_bounds__(256) void dwconv_ln_kernel(const TI *__restrict__ x, const StreamSlots *__restrict__ slots, size_t cco, WinStage st, int causal,
                                                         const float *__restrict__ wt, const float *__restrict__ b, const float *__restrict__ gamma,
-                                                        const float *__restrict__ beta, int D, _Float16 *__restrict__ y, _Float16 *__restrict__ ylo,
-                                                        float *__restrict__ cc_out, int nemit) {
+                                                        const float *__restrict__ beta, int D, _Float16 *__restrict__ y, _Float16 *__restrict__ ylo, int nemit) {
   constexpr int KT = 9;
   __shared__ float red[2][4];
   const int win = blockIdx.y, t = blockIdx.x, T = st.len[win];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c0 = tid * 4;
   const bool act = c0 < D;
-  if (cc_out && t == 0 && win == 0 && act) {
+  // a stream pass: this window's stream caches (taps before its first frame, and the next pass's)
+  const float *cache = slots ? slots->cc_in[win] + cco : nullptr;
+  float *cc_out = slots ? slots->cc_out[win] + cco : nullptr;
+  if (cc_out && t == 0 && act) {
     for (int r = 0; r < KT - 1; r++) {
       const int src = nemit + r;
 #pragma unroll
       for (int e = 0; e < 4; e++)
-        cc_out[(size_t)r * D + c0 + e] = src < KT - 1 ? cache[(size_t)src * D + c0 + e] : (float)x[(size_t)st.off[0] * D + (size_t)(src - (KT - 1)) * D + c0 + e];
+        cc_out[(size_t)r * D + c0 + e] = src < KT - 1 ? cache[(size_t)src * D + c0 + e] : (float)x[(size_t)st.off[win] * D + (size_t)(src - (KT - 1)) * D + c0 + e];
     }
   }
   if (t >= T) return;  // uniform per block
@@ -588,7 +591,7 @@ __global__ __launch_bounds__(256) void dwconv_ln_kernel(const TI *__restrict__ x
       if (ti >= 0 && ti < T) {
 #pragma unroll
         for (int e = 0; e < 4; e++) v[e] = (float)x[base + (size_t)ti * D + e];
-      } else if (ti < 0 && cache && win == 0) {
+      } else if (ti < 0 && cache) {
 #pragma unroll
         for (int e = 0; e < 4; e++) v[e] = cache[(size_t)(KT - 1 + ti) * D + c0 + e];
       }
@@ -626,10 +629,13 @@ __global__ __launch_bounds__(256) void dwconv_ln_kernel(const TI *__restrict__ x
 // nemit + r of [cache (k-1 rows) ; this pass's GLU rows] -- the k-1 GLU
 // outputs ahead of the next pass's first frame.
 template <typename TI>
-__global__ __launch_bounds__(256) void stream_conv_cache_kernel(const float *__restrict__ cc_in, const TI *__restrict__ g, int D, int nemit,
-                                                                float *__restrict__ cc_out) {
+__global__ __launch_bounds__(256) void stream_conv_cache_kernel(const StreamSlots *__restrict__ slots, size_t cco, const TI *__restrict__ g, int D, int nemit,
+                                                                int nq) {
   constexpr int KT = 9;
-  const int r = blockIdx.x, src = nemit + r;
+  const int r = blockIdx.x, w = blockIdx.y, src = nemit + r;  // row r of window (stream) w's next cache
+  const float *cc_in = slots->cc_in[w] + cco;
+  float *cc_out = slots->cc_out[w] + cco;
+  g += (size_t)w * nq * D;
   for (int c = threadIdx.x; c < D; c += 256)
     cc_out[(size_t)r * D + c] = src < KT - 1 ? cc_in[(size_t)src * D + c] : (float)g[(size_t)(src - (KT - 1)) * D + c];
 }
@@ -647,17 +653,22 @@ __global__ __launch_bounds__(256) void stream_conv_cache_kernel(const float *__r
 // (reading V from global one key after another cost ~76 us per layer); the
 // first query block of each head also writes the head's part of the next
 // pass's K / V caches from them.  Lk <= 256.
-__global__ __launch_bounds__(256) void stream_attn_kernel(const _Float16 *__restrict__ u, int ldu, const _Float16 *__restrict__ kc,
-                                                          const _Float16 *__restrict__ vc, int Lc, int nq, int D, const _Float16 *__restrict__ P, int Pn,
-                                                          int dMax, const float *__restrict__ pbu, const float *__restrict__ pbv, int chunk, int left,
-                                                          int right, _Float16 *__restrict__ out, _Float16 *__restrict__ out_lo, int nemit, int keep,
-                                                          _Float16 *__restrict__ kc_out, _Float16 *__restrict__ vc_out) {
+__global__ __launch_bounds__(256) void stream_attn_kernel(const _Float16 *__restrict__ u, int ldu, const StreamSlots *__restrict__ slots, size_t kvo,
+                                                          int Lc, int nq, int D, const _Float16 *__restrict__ P, int Pn, int dMax,
+                                                          const float *__restrict__ pbu, const float *__restrict__ pbv, int chunk, int left, int right,
+                                                          _Float16 *__restrict__ out, _Float16 *__restrict__ out_lo, int nemit, int keep) {
   constexpr int HD = 128, MAXK = 256, KS = HD + 8;  // K rows padded: lanes read different keys' rows
   __shared__ float qs[4][2][HD];
   __shared__ float ps[4][MAXK];
   __shared__ __attribute__((aligned(16))) _Float16 vs[MAXK][HD];  // the head's V rows, shared by the block's 4 queries
   __shared__ __attribute__((aligned(16))) _Float16 ks[MAXK][KS];  // and its K rows
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = blockIdx.y, w = blockIdx.z;
+  // window w = stream w of the batched pass: its nq rows of u / out, its caches
+  u += (size_t)w * nq * ldu;
+  out += (size_t)w * nq * D;
+  if (out_lo) out_lo += (size_t)w * nq * D;
+  const _Float16 *kc = slots->kc_in[w] + kvo, *vc = slots->vc_in[w] + kvo;
+  _Float16 *kc_out = keep > 0 ? slots->kc_out[w] + kvo : nullptr, *vc_out = slots->vc_out[w] + kvo;
   const int i = blockIdx.x * 4 + wave;
   const int Lk = Lc + nq;
   for (int idx = threadIdx.x; idx < Lk * (HD / 8); idx += 256) {  // all row loads in flight at once
@@ -1306,11 +1317,12 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
       FA_TRY(relpos_attention_f16(ctx, at, mx[3], (_Float16 *)e->W().vt, olo ? "attention_x" : "attention", !vt_fused));
     } else {
       const size_t kvo = (size_t)li * sp->kv_ld * D;
+      const int nq = M / n;  // frames per window (stream)
       {
         ProfScope ps(ctx, "stream_attention");
-        FA_LAUNCH(ps, stream_attn_kernel, dim3(cdiv(M, 4), c.H), dim3(256), 0, ctx->stream, u, 3 * D, sp->kc_in + kvo, sp->vc_in + kvo, sp->Lc, M, D,
+        FA_LAUNCH(ps, stream_attn_kernel, dim3(cdiv(nq, 4), c.H, n), dim3(256), 0, ctx->stream, u, 3 * D, sp->slots, kvo, sp->Lc, nq, D,
                   Ly.P + (size_t)(e->maxT - 1 - sp->dMax) * D, sp->Pn, sp->dMax, Ly.pbu, Ly.pbv, sp->chunk, sp->left, sp->right, a, olo, sp->nemit,
-                  sp->keep, sp->keep > 0 ? sp->kc_out + kvo : nullptr, sp->vc_out + kvo);
+                  sp->keep);
         FA_TRY(check_launch(ctx, "stream_attention"));
       }
     }
@@ -1333,39 +1345,38 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
         FA_LAUNCH(ps, (dwconv_silu_kernel<9, 16, 4, _Float16>), grid, dim3(thr), 0, ctx->stream, (const _Float16 *)gg, a, dlo, Ly.dww, Ly.dwb, D, s3);
       FA_TRY(check_launch(ctx, "dwconv"));
     } else {
-      const float *cache = sp ? sp->cc_in + (size_t)li * 8 * D : nullptr;
+      const StreamSlots *slots = sp ? sp->slots : nullptr;  // a stream pass: per-window conv caches
+      const size_t cco = (size_t)li * 8 * D;
       float *y32 = Ly.cln[0] ? (float *)e->W().dw32 : nullptr;
       if (y32 && D % 4 == 0 && D <= 1024) {  // depthwise + conv-module LayerNorm + SiLU (+ the stream's conv cache) in one kernel
         ProfScope ps(ctx, "dwconv_ln");
-        float *cco = sp ? sp->cc_out + (size_t)li * 8 * D : nullptr;
         const dim3 grid(mx[3], n);
         if (glu32)
-          FA_LAUNCH(ps, dwconv_ln_kernel<float>, grid, dim3(256), 0, ctx->stream, (const float *)g32, cache, s3, o.conv_causal, Ly.dww, Ly.dwb, Ly.cln[0],
-                    Ly.cln[1], D, a, dlo, cco, sp ? sp->nemit : 0);
+          FA_LAUNCH(ps, dwconv_ln_kernel<float>, grid, dim3(256), 0, ctx->stream, (const float *)g32, slots, cco, s3, o.conv_causal, Ly.dww, Ly.dwb, Ly.cln[0],
+                    Ly.cln[1], D, a, dlo, sp ? sp->nemit : 0);
         else
-          FA_LAUNCH(ps, dwconv_ln_kernel<_Float16>, grid, dim3(256), 0, ctx->stream, (const _Float16 *)gg, cache, s3, o.conv_causal, Ly.dww, Ly.dwb,
-                    Ly.cln[0], Ly.cln[1], D, a, dlo, cco, sp ? sp->nemit : 0);
+          FA_LAUNCH(ps, dwconv_ln_kernel<_Float16>, grid, dim3(256), 0, ctx->stream, (const _Float16 *)gg, slots, cco, s3, o.conv_causal, Ly.dww, Ly.dwb,
+                    Ly.cln[0], Ly.cln[1], D, a, dlo, sp ? sp->nemit : 0);
         FA_TRY(check_launch(ctx, "dwconv_ln"));
       } else {
         {
           ProfScope ps(ctx, "dwconv_gen");
           const dim3 grid(mx[3], n, cdiv(D / 4, 64));
           if (glu32)
-            FA_LAUNCH(ps, dwconv_gen_kernel<float>, grid, dim3(64), 0, ctx->stream, (const float *)g32, cache, s3, o.conv_causal, Ly.dww, Ly.dwb, D, a, dlo,
+            FA_LAUNCH(ps, dwconv_gen_kernel<float>, grid, dim3(64), 0, ctx->stream, (const float *)g32, slots, cco, s3, o.conv_causal, Ly.dww, Ly.dwb, D, a, dlo,
                       y32);
           else
-            FA_LAUNCH(ps, dwconv_gen_kernel<_Float16>, grid, dim3(64), 0, ctx->stream, (const _Float16 *)gg, cache, s3, o.conv_causal, Ly.dww, Ly.dwb, D, a,
+            FA_LAUNCH(ps, dwconv_gen_kernel<_Float16>, grid, dim3(64), 0, ctx->stream, (const _Float16 *)gg, slots, cco, s3, o.conv_causal, Ly.dww, Ly.dwb, D, a,
                       dlo, y32);
           FA_TRY(check_launch(ctx, "dwconv_gen"));
         }
         if (y32) FA_TRY(ln_into(y32, Ly.cln[0], Ly.cln[1], a, dlo, true, "conv_ln_silu"));
         if (sp) {
           ProfScope ps(ctx, "stream_conv_cache");
-          float *cco = sp->cc_out + (size_t)li * 8 * D;
           if (glu32)
-            FA_LAUNCH(ps, stream_conv_cache_kernel<float>, dim3(8), dim3(256), 0, ctx->stream, cache, (const float *)g32, D, sp->nemit, cco);
+            FA_LAUNCH(ps, stream_conv_cache_kernel<float>, dim3(8, n), dim3(256), 0, ctx->stream, slots, cco, (const float *)g32, D, sp->nemit, M / n);
           else
-            FA_LAUNCH(ps, stream_conv_cache_kernel<_Float16>, dim3(8), dim3(256), 0, ctx->stream, cache, (const _Float16 *)gg, D, sp->nemit, cco);
+            FA_LAUNCH(ps, stream_conv_cache_kernel<_Float16>, dim3(8, n), dim3(256), 0, ctx->stream, slots, cco, (const _Float16 *)gg, D, sp->nemit, M / n);
           FA_TRY(check_launch(ctx, "stream_conv_cache"));
         }
       }
@@ -1527,6 +1538,7 @@ void fa_encoder_destroy(fa_encoder *enc) {
   (void)hipDeviceSynchronize();  // the context stream and the lane streams
   for (void *p : enc->allocs) (void)hipFree(p);
   for (auto &w : enc->ws) encoder_ws_free(w);
+  stream_lanes_free(enc);
   for (int l = 0; l < fa_encoder::kLanes; l++) {
     if (enc->lane_done[l]) (void)hipEventDestroy(enc->lane_done[l]);
     if (enc->lane_stream[l]) (void)hipStreamDestroy(enc->lane_stream[l]);

@@ -87,8 +87,9 @@ struct fa_encoder {
   int lane = 0;
   hipStream_t lane_stream[kLanes] = {};
   hipEvent_t lane_done[kLanes] = {}, lanes_in = nullptr;
-  // a streaming encoder's pass works in the stream's own workspace
+  // a stream pass works in its stream lane's workspace (stream.hip)
   fa::EncWs *ws_ovr = nullptr;
+  struct StreamLane *slane[kLanes] = {};
   fa::EncWs &W() { return ws_ovr ? *ws_ovr : ws[lane]; }
 };
 
@@ -118,16 +119,27 @@ struct PassGeom {
   const MelSrc *mel_src = nullptr;
 };
 
-// A streaming chunk pass: the frames of this pass attend to `Lc` cached keys
-// of earlier passes followed by their own; the first `nemit` frames are
-// emitted, and their keys / depthwise inputs become the next pass's caches.
+// The caches of the streams in one batched stream pass, window w = stream w:
+// its layer-0 K / V caches ([layers][left][D] f16) and depthwise-conv cache
+// ([layers][8][D] f32), the set the pass reads and the set it writes.  Kept
+// in device memory (refreshed before each pass), so a captured pass serves
+// any set of streams.
+constexpr int kMaxStreamGroup = 32;
+struct StreamSlots {
+  const _Float16 *kc_in[kMaxStreamGroup], *vc_in[kMaxStreamGroup];
+  _Float16 *kc_out[kMaxStreamGroup], *vc_out[kMaxStreamGroup];
+  const float *cc_in[kMaxStreamGroup];
+  float *cc_out[kMaxStreamGroup];
+};
+
+// A streaming chunk pass over g.n streams (windows of nq = g.M / g.n frames
+// each): the frames of a window attend to `Lc` cached keys of its stream's
+// earlier passes followed by their own; the first `nemit` frames are emitted,
+// and their keys / depthwise inputs become the next pass's caches.
 struct StreamPass {
   int Lc = 0, nemit = 0, keep = 0;
   int chunk = 0, left = 0, right = 0;
-  const _Float16 *kc_in = nullptr, *vc_in = nullptr;  // [layers][left][D]
-  _Float16 *kc_out = nullptr, *vc_out = nullptr;
-  const float *cc_in = nullptr;  // [layers][dwK-1][D], GLU outputs ahead of the pass
-  float *cc_out = nullptr;
+  const StreamSlots *slots = nullptr;  // device table, one entry per window
   // positional term: distance dMax - r at row r of the layer's table (the
   // offline table's rows maxT-1-dMax ..), Pn = dMax - dMin + 1 rows
   int Pn = 0, dMax = 0;
@@ -140,6 +152,8 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *mel,
 int encoder_grow(fa_encoder *e, void **buf, size_t *cap, size_t need);
 // frees a workspace's buffers and captured forwards (the device must be idle for them)
 void encoder_ws_free(EncWs &w);
+// the stream lanes of an encoder (stream.hip), at encoder destruction
+void stream_lanes_free(fa_encoder *e);
 int encoder_copy_f4(fa_ctx *ctx, const void *src, void *dst, size_t bytes, const char *label);
 int encoder_graph_run(fa_ctx *ctx, fa_encoder *e, const std::vector<int64_t> &key, const std::function<int()> &launch,
                       const std::function<int()> &pre);

@@ -21,11 +21,21 @@
 // The caches live on the device and are double-buffered: a pass reads one
 // set and writes the next (K / V of the last `left` emitted frames per layer
 // in f16, the depthwise conv's k-1 input rows per layer in f32), so nothing
-// is copied back to the host but the emitted frames.  Steady-state passes
-// (full key cache, same chunk size) repeat one of two kernel sequences and
-// are replayed from captured hipGraphs.
+// is copied back to the host but the emitted frames.
+//
+// Several streams of one encoder (fa_stream_push_many) whose next passes have
+// the same shape (rows, pads, cached keys) run as ONE batched pass: window w
+// of the pass is stream w, its caches named by a device table (StreamSlots),
+// so the weights are read once for all of them (a pass over a few frames is
+// bound by reading the ~1.2 GB of f16 weights).  Passes run on the encoder's
+// stream lanes (a HIP stream, workspace and staging buffers each); groups of
+// different shapes run on different lanes at once.  Steady-state passes (full
+// key caches, no pads) are replayed from captured hipGraphs keyed by their
+// shape; the cache table is refreshed before each replay.
 #include <algorithm>
 #include <cstring>
+#include <map>
+#include <tuple>
 #include <vector>
 
 #include "fa_internal.h"
@@ -45,19 +55,21 @@ struct fa_stream {
   _Float16 *kc[2] = {nullptr, nullptr}, *vc[2] = {nullptr, nullptr};  // [layers][left][D]
   float *cc[2] = {nullptr, nullptr};                                  // [layers][8][D]
   int cur = 0, Lc = 0;
+};
+
+// One lane of stream passes: HIP stream, workspace, the pass's mel rows and
+// output frames, the device cache table, captured passes.
+struct StreamLane {
+  EncWs ws;
+  hipStream_t hs = nullptr;
+  hipEvent_t done = nullptr, in = nullptr;
   float *mel_dev = nullptr, *x_dev = nullptr;
   size_t mel_cap = 0, x_cap = 0;
+  StreamSlots *slots = nullptr;
   uint64_t buf_gen = 0;  // moves when mel_dev / x_dev are reallocated
   std::vector<EncWs::Captured> graphs;
   uint64_t graph_clock = 0;
-  // Each stream's passes run on a HIP stream of its own with a workspace of
-  // its own, so several streams' passes (fa_stream_push_many) are in flight
-  // together.  A push starts after the work queued on the context stream
-  // (event `in`) and the context stream waits for it (event `done`), so its
-  // frames are ordinary context tensors.
-  EncWs ws;
-  hipStream_t hs = nullptr;
-  hipEvent_t in = nullptr, done = nullptr;
+  std::vector<float> stage;  // host staging of a pass's mel rows
 };
 
 namespace {
@@ -65,30 +77,48 @@ namespace {
 constexpr int kLookback = 14;  // mel rows before 8*subT the next pass's first frame reads (three k=3 stride-2 convs)
 constexpr int kKT = 9;
 
-int grow_buf(fa_stream *st, void **buf, size_t *cap, size_t need) {
+__global__ void set_slots_kernel(StreamSlots v, StreamSlots *dst) {
+  if (threadIdx.x == 0) *dst = v;
+}
+
+int lane_grow(fa_ctx *ctx, StreamLane *L, void **buf, size_t *cap, size_t need) {
   if (need <= *cap) return FA_OK;
   if (*buf) {
-    (void)hipStreamSynchronize(st->ctx->stream);
+    (void)hipStreamSynchronize(L->hs);
     (void)hipFree(*buf);
     *buf = nullptr;
   }
-  *buf = dev_alloc(st->ctx, need);
+  *buf = dev_alloc(ctx, need);
   if (!*buf) return FA_E_OOM;
   *cap = need;
-  st->buf_gen++;
+  L->buf_gen++;
   return FA_OK;
 }
 
-// While a pass is queued, the context's launches go to the stream's HIP stream
-// and the encoder's workspace is the stream's.
+int get_lane(fa_ctx *ctx, fa_encoder *e, int l, StreamLane **out) {
+  if (!e->slane[l]) {
+    StreamLane *L = new StreamLane();
+    e->slane[l] = L;
+    if (hipStreamCreateWithFlags(&L->hs, hipStreamNonBlocking) != hipSuccess || hipEventCreateWithFlags(&L->done, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&L->in, hipEventDisableTiming) != hipSuccess)
+      return set_err(ctx, FA_E_DEVICE, "encodeStreamPush: creating a stream lane failed");
+    L->slots = (StreamSlots *)dev_alloc(ctx, sizeof(StreamSlots));
+    if (!L->slots) return FA_E_OOM;
+  }
+  *out = e->slane[l];
+  return FA_OK;
+}
+
+// While a pass is queued, the context's launches go to the lane's HIP stream
+// and the encoder's workspace is the lane's.
 struct PassScope {
   fa_ctx *c;
   fa_encoder *e;
   hipStream_t s0;
   EncWs *w0;
-  explicit PassScope(fa_stream *st) : c(st->ctx), e(st->enc), s0(st->ctx->stream), w0(st->enc->ws_ovr) {
-    c->stream = st->hs;
-    e->ws_ovr = &st->ws;
+  PassScope(fa_ctx *ctx, fa_encoder *enc, StreamLane *L) : c(ctx), e(enc), s0(ctx->stream), w0(enc->ws_ovr) {
+    c->stream = L->hs;
+    e->ws_ovr = &L->ws;
   }
   ~PassScope() {
     c->stream = s0;
@@ -96,47 +126,94 @@ struct PassScope {
   }
 };
 
-// One pass over m mel rows at the FIFO head: nComp frames computed, the first
-// nemit emitted (appended to `outs` as a [nemit, D] tensor) and cached.
-int run_pass(fa_stream *st, int m, int pt, int pb, int nComp, int nemit, std::vector<fa_tensor> &outs) {
-  PassScope scope(st);
-  fa_ctx *ctx = st->ctx;
-  fa_encoder *e = st->enc;
+// The shape of a stream's next pass: m mel rows at the FIFO head, pads,
+// nComp frames computed, the first nemit emitted.
+struct PassPlan {
+  int m = 0, pt = 0, pb = 0, nComp = 0, nemit = 0;
+};
+
+// The next chunk pass the buffered frames allow (false: none yet).
+bool next_pass(const fa_stream *st, PassPlan *p) {
+  const int MB = st->enc->cfg.melBins;
+  const int M = (int)(st->fifo.size() / MB);
+  // frames a pass can finish: the first pass reads 8*nComp - 7 rows (top
+  // padded), later passes 8*nComp + 7 (14 rows of look-back); nComp
+  // includes the provisional lookahead B, and n is a whole number of chunks
+  int n = st->subT == 0 ? (M + 7) / 8 - st->B : (M - 7 >= 0 ? (M - 7) / 8 : -1) - st->B;
+  n = std::min(n, st->max_chunk);
+  n -= ((n % st->C) + st->C) % st->C;
+  if (n < st->C) return false;
+  p->nComp = n + st->B;
+  p->nemit = n;
+  p->m = st->subT == 0 ? 8 * p->nComp - 7 : 8 * p->nComp + 7;
+  p->pt = st->subT == 0 ? st->enc->opts.sub_pad_t : 0;
+  p->pb = 0;
+  return true;
+}
+
+// After a chunk pass: drop the FIFO rows the next pass no longer reads.
+void advance_fifo(fa_stream *st, int nemit) {
+  const int MB = st->enc->cfg.melBins;
+  st->subT += nemit;
+  const long keep_from = 8L * st->subT - kLookback;
+  const long drop = keep_from - st->fifo_start;
+  st->fifo.erase(st->fifo.begin(), st->fifo.begin() + (size_t)drop * MB);
+  st->fifo_start = keep_from;
+}
+
+// One pass of n streams with the same plan and the same cached-key count, on
+// lane L: window w = sts[w]; its emitted frames are appended to outs[w].
+int run_group(fa_ctx *ctx, fa_encoder *e, StreamLane *L, fa_stream *const *sts, int n, const PassPlan &pl, std::vector<fa_tensor> *const *outs) {
+  PassScope scope(ctx, e, L);
   const fa_encoder_cfg &c = e->cfg;
-  const int MB = c.melBins, D = c.D;
-  const int32_t len = m;
+  const int MB = c.melBins, D = c.D, m = pl.m, nComp = pl.nComp, nemit = pl.nemit;
+  fa_stream *s0 = sts[0];
+  if (n < 1 || n > kMaxStreamGroup) return set_err(ctx, FA_E_INVALID, "stream pass: %d streams in one pass", n);
+  std::vector<int32_t> lens(n, m);
   PassGeom g;
-  FA_TRY(pass_geometry(ctx, e, &len, 1, 0, pt, pb, &g));
-  if (g.M != nComp) return set_err(ctx, FA_E_STATE, "stream pass: %d mel rows give %d frames, expected %d", m, g.M, nComp);
-  if (st->Lc + nComp > 256) return set_err(ctx, FA_E_UNSUPPORTED, "stream pass: %d cached + %d new keys (at most 256)", st->Lc, nComp);
+  FA_TRY(pass_geometry(ctx, e, lens.data(), n, 0, pl.pt, pl.pb, &g));
+  if (g.M != n * nComp) return set_err(ctx, FA_E_STATE, "stream pass: %d mel rows give %d frames, expected %d", m, g.M / n, nComp);
+  if (s0->Lc + nComp > 256) return set_err(ctx, FA_E_UNSUPPORTED, "stream pass: %d cached + %d new keys (at most 256)", s0->Lc, nComp);
   FA_TRY(pass_workspace(ctx, e, g, c.layers, true));
-  FA_TRY(grow_buf(st, (void **)&st->mel_dev, &st->mel_cap, (size_t)m * MB * 4));
-  FA_TRY(grow_buf(st, (void **)&st->x_dev, &st->x_cap, (size_t)nComp * D * 4));
-  FA_HIP(ctx, hipMemcpyAsync(st->mel_dev, st->fifo.data(), (size_t)m * MB * 4, hipMemcpyHostToDevice, ctx->stream));
-  FA_HIP(ctx, hipStreamSynchronize(ctx->stream));  // the FIFO is edited once this pass is queued
+  FA_TRY(lane_grow(ctx, L, (void **)&L->mel_dev, &L->mel_cap, (size_t)n * m * MB * 4));
+  FA_TRY(lane_grow(ctx, L, (void **)&L->x_dev, &L->x_cap, (size_t)n * nComp * D * 4));
+  L->stage.resize((size_t)n * m * MB);
+  for (int w = 0; w < n; w++) std::memcpy(L->stage.data() + (size_t)w * m * MB, sts[w]->fifo.data(), (size_t)m * MB * 4);
+  FA_HIP(ctx, hipMemcpyAsync(L->mel_dev, L->stage.data(), (size_t)n * m * MB * 4, hipMemcpyHostToDevice, L->hs));
+  FA_HIP(ctx, hipStreamSynchronize(L->hs));  // the staging buffer and FIFOs are edited once this pass is queued
+  StreamSlots tab{};
+  for (int w = 0; w < n; w++) {
+    fa_stream *st = sts[w];
+    tab.kc_in[w] = st->kc[st->cur];
+    tab.vc_in[w] = st->vc[st->cur];
+    tab.kc_out[w] = st->kc[st->cur ^ 1];
+    tab.vc_out[w] = st->vc[st->cur ^ 1];
+    tab.cc_in[w] = st->cc[st->cur];
+    tab.cc_out[w] = st->cc[st->cur ^ 1];
+  }
+  {
+    ProfScope ps(ctx, "stream_slots");
+    FA_LAUNCH(ps, set_slots_kernel, dim3(1), dim3(64), 0, ctx->stream, tab, L->slots);
+    FA_TRY(check_launch(ctx, "stream_slots"));
+  }
   StreamPass sp;
-  sp.Lc = st->Lc;
+  sp.Lc = s0->Lc;
   sp.nemit = nemit;
-  sp.keep = std::min(st->left, st->Lc + nemit);
-  sp.chunk = st->C;
-  sp.left = st->left;
-  sp.right = st->right;
-  sp.kc_in = st->kc[st->cur];
-  sp.vc_in = st->vc[st->cur];
-  sp.kc_out = st->kc[st->cur ^ 1];
-  sp.vc_out = st->vc[st->cur ^ 1];
-  sp.cc_in = st->cc[st->cur];
-  sp.cc_out = st->cc[st->cur ^ 1];
-  sp.Pn = st->Pn;
-  sp.dMax = st->dMax;
-  sp.kv_ld = st->left;
-  auto launch = [&]() { return pass_launch(ctx, e, g, st->mel_dev, st->x_dev, c.layers, &sp); };
+  sp.keep = std::min(s0->left, s0->Lc + nemit);
+  sp.chunk = s0->C;
+  sp.left = s0->left;
+  sp.right = s0->right;
+  sp.slots = L->slots;
+  sp.Pn = s0->Pn;
+  sp.dMax = s0->dMax;
+  sp.kv_ld = s0->left;
+  auto launch = [&]() { return pass_launch(ctx, e, g, L->mel_dev, L->x_dev, c.layers, &sp); };
   const char *ge = getenv("FA_GRAPH");
-  const bool steady = st->Lc == st->left && pb == 0 && pt == 0;
+  const bool steady = s0->Lc == s0->left && pl.pb == 0 && pl.pt == 0;
   if (steady && !ctx->prof_on && !(ge && ge[0] == '0')) {
-    std::vector<int64_t> key = {(int64_t)e->ws_gen, (int64_t)st->buf_gen, m, nComp, nemit, st->cur};
+    std::vector<int64_t> key = {(int64_t)e->ws_gen, (int64_t)L->buf_gen, n, m, nComp, nemit};
     EncWs::Captured *hit = nullptr;
-    for (auto &gr : st->graphs)
+    for (auto &gr : L->graphs)
       if (gr.key == key) hit = &gr;
     if (!hit) {
       FA_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
@@ -152,29 +229,32 @@ int run_pass(fa_stream *st, int m, int pt, int pb, int nComp, int nemit, std::ve
       const hipError_t ie = hipGraphInstantiateWithFlags(&exec, graph, 0);
       (void)hipGraphDestroy(graph);
       if (ie != hipSuccess) return set_err(ctx, FA_E_DEVICE, "stream pass: graph instantiate: %s", hipGetErrorString(ie));
-      if (st->graphs.size() >= 4) {  // a stream repeats at most a few signatures
+      if (L->graphs.size() >= 8) {  // a few group sizes and chunk shapes repeat
         size_t lru = 0;
-        for (size_t i = 1; i < st->graphs.size(); i++)
-          if (st->graphs[i].used < st->graphs[lru].used) lru = i;
+        for (size_t i = 1; i < L->graphs.size(); i++)
+          if (L->graphs[i].used < L->graphs[lru].used) lru = i;
         (void)hipStreamSynchronize(ctx->stream);
-        (void)hipGraphExecDestroy(st->graphs[lru].exec);
-        st->graphs.erase(st->graphs.begin() + lru);
+        (void)hipGraphExecDestroy(L->graphs[lru].exec);
+        L->graphs.erase(L->graphs.begin() + lru);
       }
-      st->graphs.push_back({key, exec, 0});
-      hit = &st->graphs.back();
+      L->graphs.push_back({key, exec, 0});
+      hit = &L->graphs.back();
     }
-    hit->used = ++st->graph_clock;
+    hit->used = ++L->graph_clock;
     FA_HIP(ctx, hipGraphLaunch(hit->exec, ctx->stream));
   } else {
     FA_TRY(launch());
   }
-  st->cur ^= 1;
-  st->Lc = sp.keep;
-  fa_tensor o;
-  TensorRec *ro;
-  FA_TRY(new_tensor(ctx, nemit, D, S_F32, (size_t)nemit * D * 4, &o, &ro));
-  FA_TRY(encoder_copy_f4(ctx, st->x_dev, ro->ptr, (size_t)nemit * D * 4, "stream_out"));
-  outs.push_back(o);
+  for (int w = 0; w < n; w++) {
+    fa_stream *st = sts[w];
+    st->cur ^= 1;
+    st->Lc = sp.keep;
+    fa_tensor o;
+    TensorRec *ro;
+    FA_TRY(new_tensor(ctx, nemit, D, S_F32, (size_t)nemit * D * 4, &o, &ro));
+    FA_TRY(encoder_copy_f4(ctx, L->x_dev + (size_t)w * nComp * D, ro->ptr, (size_t)nemit * D * 4, "stream_out"));
+    outs[w]->push_back(o);
+  }
   return FA_OK;
 }
 
@@ -190,40 +270,98 @@ int emit(fa_stream *st, std::vector<fa_tensor> &outs, fa_tensor *out) {
   return rc;
 }
 
-
-// The passes a push of `count` mel-major frames makes ready, queued on the
-// stream's HIP stream; their frames are appended to outs.
-int push_passes(fa_stream *st, const float *mel, int count, std::vector<fa_tensor> &outs) {
-  const int MB = st->enc->cfg.melBins;
-  // mel-major [melBins][count] -> frame-major FIFO rows
-  const size_t old = st->fifo.size() / MB;
-  st->fifo.resize((old + count) * MB);
-  for (int t = 0; t < count; t++)
-    for (int ch = 0; ch < MB; ch++) st->fifo[(old + t) * MB + ch] = mel[(size_t)ch * count + t];
-  for (;;) {
-    const int M = (int)(st->fifo.size() / MB);
-    // frames a pass can finish: the first pass reads 8*nComp - 7 rows (top
-    // padded), later passes 8*nComp + 7 (14 rows of look-back); nComp
-    // includes the provisional lookahead B, and n is a whole number of chunks
-    int n = st->subT == 0 ? (M + 7) / 8 - st->B : (M - 7 >= 0 ? (M - 7) / 8 : -1) - st->B;
-    n = std::min(n, st->max_chunk);
-    n -= ((n % st->C) + st->C) % st->C;
-    if (n < st->C) break;
-    const int nComp = n + st->B;
-    const int m = st->subT == 0 ? 8 * nComp - 7 : 8 * nComp + 7;
-    const int pt = st->subT == 0 ? st->enc->opts.sub_pad_t : 0;
-    FA_TRY(run_pass(st, m, pt, 0, nComp, n, outs));
-    // keep the look-back of the next pass's first frame
-    st->subT += n;
-    const long keep_from = 8L * st->subT - kLookback;
-    const long drop = keep_from - st->fifo_start;
-    st->fifo.erase(st->fifo.begin(), st->fifo.begin() + (size_t)drop * MB);
-    st->fifo_start = keep_from;
+// Queue rounds of passes until no stream has a pass ready: in each round the
+// streams with a ready pass are grouped by (plan, cached keys), each group is
+// one batched pass, groups go round-robin to the lanes; a round starts after
+// the previous one (a stream's passes follow each other through its caches).
+// Lanes start after the work queued on the context stream, and the context
+// stream waits for every lane used.
+int run_rounds(fa_ctx *ctx, fa_encoder *e, std::vector<fa_stream *> &sts, std::vector<std::vector<fa_tensor>> &frames, const PassPlan *flush) {
+  const int nl = std::max(1, e->nlanes);
+  StreamLane *L0;
+  FA_TRY(get_lane(ctx, e, 0, &L0));
+  FA_HIP(ctx, hipEventRecord(L0->in, ctx->stream));
+  std::vector<bool> used(nl, false);
+  int rc = FA_OK;
+  for (int round = 0; rc == FA_OK; round++) {
+    // (plan, Lc) -> member indices
+    std::map<std::tuple<int, int, int, int, int, int>, std::vector<int>> groups;
+    for (int i = 0; i < (int)sts.size(); i++) {
+      PassPlan p;
+      if (flush) {
+        if (round > 0) continue;
+        p = *flush;
+      } else if (!next_pass(sts[i], &p)) {
+        continue;
+      }
+      groups[std::make_tuple(p.m, p.pt, p.pb, p.nComp, p.nemit, sts[i]->Lc)].push_back(i);
+    }
+    if (groups.empty()) break;
+    std::vector<bool> wait_prev(nl, round > 0);
+    int k = 0;
+    for (auto &kv : groups) {
+      const auto &key = kv.first;
+      PassPlan p;
+      p.m = std::get<0>(key);
+      p.pt = std::get<1>(key);
+      p.pb = std::get<2>(key);
+      p.nComp = std::get<3>(key);
+      p.nemit = std::get<4>(key);
+      const std::vector<int> &mem = kv.second;
+      for (size_t b0 = 0; b0 < mem.size() && rc == FA_OK; b0 += kMaxStreamGroup, k++) {
+        const int nb = (int)std::min<size_t>(kMaxStreamGroup, mem.size() - b0);
+        const int l = k % nl;
+        StreamLane *L;
+        if ((rc = get_lane(ctx, e, l, &L)) != FA_OK) break;
+        if (!used[l]) {
+          if (hipStreamWaitEvent(L->hs, L0->in, 0) != hipSuccess) rc = set_err(ctx, FA_E_DEVICE, "stream pass: lane wait");
+          used[l] = true;
+        }
+        if (wait_prev[l]) {  // after every lane's previous round
+          for (int j = 0; j < nl; j++)
+            if (e->slane[j] && j != l) (void)hipStreamWaitEvent(L->hs, e->slane[j]->done, 0);
+          wait_prev[l] = false;
+        }
+        if (rc != FA_OK) break;
+        std::vector<fa_stream *> g(nb);
+        std::vector<std::vector<fa_tensor> *> o(nb);
+        for (int w = 0; w < nb; w++) {
+          g[w] = sts[mem[b0 + w]];
+          o[w] = &frames[mem[b0 + w]];
+        }
+        rc = run_group(ctx, e, L, g.data(), nb, p, o.data());
+        if (rc == FA_OK && !flush)
+          for (int w = 0; w < nb; w++) advance_fifo(g[w], p.nemit);
+      }
+      if (rc != FA_OK) break;
+    }
+    for (int l = 0; l < nl; l++)
+      if (used[l]) (void)hipEventRecord(e->slane[l]->done, e->slane[l]->hs);
+    if (flush) break;
   }
-  return FA_OK;
+  for (int l = 0; l < nl; l++)
+    if (used[l]) (void)hipStreamWaitEvent(ctx->stream, e->slane[l]->done, 0);
+  return rc;
 }
 
 }  // namespace
+
+void fa::stream_lanes_free(fa_encoder *e) {
+  for (auto &L : e->slane) {
+    if (!L) continue;
+    if (L->hs) (void)hipStreamSynchronize(L->hs);
+    for (auto &g : L->graphs)
+      if (g.exec) (void)hipGraphExecDestroy(g.exec);
+    encoder_ws_free(L->ws);
+    for (void *p : {(void *)L->mel_dev, (void *)L->x_dev, (void *)L->slots})
+      if (p) (void)hipFree(p);
+    if (L->done) (void)hipEventDestroy(L->done);
+    if (L->in) (void)hipEventDestroy(L->in);
+    if (L->hs) (void)hipStreamDestroy(L->hs);
+    delete L;
+    L = nullptr;
+  }
+}
 
 extern "C" {
 
@@ -261,11 +399,6 @@ int fa_stream_create(fa_ctx *ctx, fa_encoder *enc, int lookahead_chunks, int max
       return FA_E_OOM;
     }
   }
-  if (hipStreamCreateWithFlags(&st->hs, hipStreamNonBlocking) != hipSuccess || hipEventCreateWithFlags(&st->in, hipEventDisableTiming) != hipSuccess ||
-      hipEventCreateWithFlags(&st->done, hipEventDisableTiming) != hipSuccess) {
-    fa_stream_destroy(st);
-    return set_err(ctx, FA_E_DEVICE, "createEncodeStream: creating the stream's HIP stream failed");
-  }
   // the first pass sees a zero depthwise-conv history (the offline causal pad)
   if (hipMemsetAsync(st->cc[0], 0, cb, ctx->stream) != hipSuccess) {
     fa_stream_destroy(st);
@@ -287,25 +420,27 @@ int fa_stream_push_many(int n, fa_stream *const *sts, const float *const *mels, 
     outs[i] = 0;
   }
   fa_ctx *ctx = sts[0]->ctx;
+  fa_encoder *e = sts[0]->enc;
   for (int i = 0; i < n; i++) {
     fa_stream *st = sts[i];
-    if (st->ctx != ctx) return set_err(ctx, FA_E_INVALID, "encodeStreamPush: streams of different contexts in one call");
+    if (st->ctx != ctx || st->enc != e) return set_err(ctx, FA_E_INVALID, "encodeStreamPush: streams of different encoders in one call");
     for (int j = 0; j < i; j++)
       if (sts[j] == st) return set_err(ctx, FA_E_INVALID, "encodeStreamPush: stream %d repeats stream %d in one call", i, j);
     if (st->flushed) return set_err(ctx, FA_E_STATE, "encodeStreamPush: stream already flushed; create a new stream");
     if (counts[i] < 0 || (counts[i] > 0 && !mels[i])) return set_err(ctx, FA_E_INVALID, "encodeStreamPush: %d frames", counts[i]);
   }
-  // every stream's passes start after the work already queued on the context stream
-  FA_HIP(ctx, hipEventRecord(sts[0]->in, ctx->stream));
-  for (int i = 0; i < n; i++) FA_HIP(ctx, hipStreamWaitEvent(sts[i]->hs, sts[0]->in, 0));
-  std::vector<std::vector<fa_tensor>> frames(n);
-  int rc = FA_OK;
-  for (int i = 0; i < n && rc == FA_OK; i++) rc = push_passes(sts[i], mels[i], counts[i], frames[i]);
-  // the context stream waits for every stream (also after an error, so later work stays ordered)
-  for (int i = 0; i < n; i++) {
-    (void)hipEventRecord(sts[i]->done, sts[i]->hs);
-    (void)hipStreamWaitEvent(ctx->stream, sts[i]->done, 0);
+  const int MB = e->cfg.melBins;
+  std::vector<fa_stream *> v(sts, sts + n);
+  for (int i = 0; i < n; i++) {  // mel-major [melBins][count] -> frame-major FIFO rows
+    fa_stream *st = sts[i];
+    const size_t old = st->fifo.size() / MB;
+    const int count = counts[i];
+    st->fifo.resize((old + count) * MB);
+    for (int t = 0; t < count; t++)
+      for (int ch = 0; ch < MB; ch++) st->fifo[(old + t) * MB + ch] = mels[i][(size_t)ch * count + t];
   }
+  std::vector<std::vector<fa_tensor>> frames(n);
+  int rc = run_rounds(ctx, e, v, frames, nullptr);
   for (int i = 0; i < n; i++) {
     if (rc == FA_OK)
       rc = emit(sts[i], frames[i], &outs[i]);
@@ -339,35 +474,29 @@ int fa_stream_flush(fa_stream *st, fa_tensor *out) {
   }
   if (T <= 0) return FA_OK;
   if (T > st->enc->maxT) return set_err(ctx, FA_E_UNSUPPORTED, "encodeStreamFlush: %d tail frames > max_T", T);
-  std::vector<fa_tensor> outs;
-  FA_HIP(ctx, hipEventRecord(st->in, ctx->stream));
-  FA_HIP(ctx, hipStreamWaitEvent(st->hs, st->in, 0));
-  const int rc = run_pass(st, M, pt, pb, T, T, outs);
-  (void)hipEventRecord(st->done, st->hs);
-  (void)hipStreamWaitEvent(ctx->stream, st->done, 0);
+  PassPlan p;
+  p.m = M;
+  p.pt = pt;
+  p.pb = pb;
+  p.nComp = T;
+  p.nemit = T;
+  std::vector<fa_stream *> v{st};
+  std::vector<std::vector<fa_tensor>> frames(1);
+  const int rc = run_rounds(ctx, st->enc, v, frames, &p);
   if (rc != FA_OK) {
-    for (fa_tensor t : outs) (void)fa_free_tensor(ctx, t);
+    for (fa_tensor t : frames[0]) (void)fa_free_tensor(ctx, t);
     return rc;
   }
   st->fifo.clear();
-  return emit(st, outs, out);
+  return emit(st, frames[0], out);
 }
 
 void fa_stream_destroy(fa_stream *st) {
   if (!st) return;
-  (void)hipStreamSynchronize(st->ctx->stream);
-  if (st->hs) (void)hipStreamSynchronize(st->hs);
-  encoder_ws_free(st->ws);
-  for (auto &g : st->graphs)
-    if (g.exec) (void)hipGraphExecDestroy(g.exec);
+  (void)hipStreamSynchronize(st->ctx->stream);  // the context stream waits for every pass of the stream's pushes
   for (int i = 0; i < 2; i++)
     for (void *p : {(void *)st->kc[i], (void *)st->vc[i], (void *)st->cc[i]})
       if (p) (void)hipFree(p);
-  if (st->mel_dev) (void)hipFree(st->mel_dev);
-  if (st->x_dev) (void)hipFree(st->x_dev);
-  if (st->in) (void)hipEventDestroy(st->in);
-  if (st->done) (void)hipEventDestroy(st->done);
-  if (st->hs) (void)hipStreamDestroy(st->hs);
   delete st;
 }
 

@@ -141,16 +141,25 @@ def test_stream_errors(ctx, fa):
 
 
 @pytest.mark.parametrize("graph", ["1", "0"])
-def test_streams_pushed_together_equal_streams_pushed_alone(ctx, fa, monkeypatch, graph):
-    """fa_stream_push_many: four streams of one encoder, each with its own mel
-    and its own piece pattern (so they run different pass counts and shapes
-    per call, and one ends long before the others), pushed together on their
-    own HIP streams, give every stream the bits of pushing it alone; a
-    repeated stream and a flushed stream in one call are refused."""
+@pytest.mark.parametrize("aligned", [False, True])
+def test_streams_pushed_together_equal_streams_pushed_alone(ctx, fa, monkeypatch, graph, aligned):
+    """fa_stream_push_many: four streams of one encoder, each with its own mel,
+    pushed together give every stream the bits of pushing it alone.  Aligned:
+    every stream gets the same piece pattern, so each push runs one batched
+    pass of all four (window w = stream w, caches from the device table);
+    otherwise each has its own pattern (different pass counts and shapes per
+    call, one ends long before the others), so passes group only when their
+    shapes and cached-key counts meet and the rest run as separate passes on
+    the lanes.  A repeated stream and a flushed stream in one call are
+    refused."""
     monkeypatch.setenv("FA_GRAPH", graph)
     cfg, man, enc = _model(ctx, fa)
-    mels = [fa.synth.make_features(cfg["melBins"], n, seed=30 + i)[0] for i, n in enumerate((600, 480, 200, 640))]
-    patterns = [[16] * 38, [37, 100, 5, 64, 95, 179], [8] * 25, [24] * 27]
+    if aligned:
+        mels = [fa.synth.make_features(cfg["melBins"], 608, seed=40 + i)[0] for i in range(4)]
+        patterns = [[16] * 38] * 4
+    else:
+        mels = [fa.synth.make_features(cfg["melBins"], n, seed=30 + i)[0] for i, n in enumerate((600, 480, 200, 640))]
+        patterns = [[16] * 38, [37, 100, 5, 64, 95, 179], [8] * 25, [24] * 27]
     alone = [_stream(ctx, fa, enc, m, p) for m, p in zip(mels, patterns)]
     sts = [fa.createEncodeStream(ctx, enc) for _ in mels]
     got = [[] for _ in mels]
