@@ -503,13 +503,13 @@ __global__ __launch_bounds__(64) void dwconv_silu_kernel(const TI *__restrict__ 
 // value into y32 when the layer normalises the depthwise output first.
 // Thread = 4 channels of one frame.
 template <typename TI>
-__global__ __launch_bounds__(64) void dwconv_gen_kernel(const TI *__restrict__ x, const StreamSlots *__restrict__ slots, size_t cco, WinStage st, int causal,
+__global__ __launch_bounds__(64) void dwconv_gen_kernel(const TI *__restrict__ x, const CcSlots slots, int use_slots, size_t cco, WinStage st, int causal,
                                                         const float *__restrict__ wt, const float *__restrict__ b, int D, _Float16 *__restrict__ y,
                                                         _Float16 *__restrict__ ylo, float *__restrict__ y32) {
   constexpr int KT = 9;
   const int win = blockIdx.y, t = blockIdx.x, T = st.len[win];
   if (t >= T) return;
-  const float *cache = slots ? slots->cc_in[win] + cco : nullptr;  // a stream pass: taps before the window's first frame
+  const float *cache = use_slots ? slots.cc_in[win] + cco : nullptr;  // a stream pass: taps before the window's first frame
   const int c0 = (blockIdx.z * 64 + threadIdx.x) * 4;
   if (c0 >= D) return;
   const int pad = causal ? KT - 1 : (KT - 1) / 2;
@@ -558,7 +558,7 @@ __global__ __launch_bounds__(64) void dwconv_gen_kernel(const TI *__restrict__ x
 // also writes the next pass's conv cache (rows nemit .. nemit + 7 of
 // [cache ; GLU rows]).
 template <typename TI>
-__global__ __launch_bounds__(256) void dwconv_ln_kernel(const TI *__restrict__ x, const StreamSlots *__restrict__ slots, size_t cco, WinStage st, int causal,
+__global__ __launch_bounds__(256) void dwconv_ln_kernel(const TI *__restrict__ x, const CcSlots slots, int use_slots, size_t cco, WinStage st, int causal,
                                                         const float *__restrict__ wt, const float *__restrict__ b, const float *__restrict__ gamma,
                                                         const float *__restrict__ beta, int D, _Float16 *__restrict__ y, _Float16 *__restrict__ ylo, int nemit) {
   constexpr int KT = 9;
@@ -568,15 +568,24 @@ __global__ __launch_bounds__(256) void dwconv_ln_kernel(const TI *__restrict__ x
   const int c0 = tid * 4;
   const bool act = c0 < D;
   // a stream pass: this window's stream caches (taps before its first frame, and the next pass's)
-  const float *cache = slots ? slots->cc_in[win] + cco : nullptr;
-  float *cc_out = slots ? slots->cc_out[win] + cco : nullptr;
+  const float *cache = use_slots ? slots.cc_in[win] + cco : nullptr;
+  float *cc_out = use_slots ? slots.cc_out[win] + cco : nullptr;
   if (cc_out && t == 0 && act) {
+    // every load issued before the first store (the stores could alias them for all the compiler knows)
+    const TI *xw = x + (size_t)st.off[win] * D + c0;
+    float4 rows[KT - 1];
+#pragma unroll
     for (int r = 0; r < KT - 1; r++) {
       const int src = nemit + r;
-#pragma unroll
-      for (int e = 0; e < 4; e++)
-        cc_out[(size_t)r * D + c0 + e] = src < KT - 1 ? cache[(size_t)src * D + c0 + e] : (float)x[(size_t)st.off[win] * D + (size_t)(src - (KT - 1)) * D + c0 + e];
+      if (src < KT - 1) {
+        rows[r] = *reinterpret_cast<const float4 *>(cache + (size_t)src * D + c0);
+      } else {
+        const TI *xr = xw + (size_t)(src - (KT - 1)) * D;
+        rows[r] = make_float4((float)xr[0], (float)xr[1], (float)xr[2], (float)xr[3]);
+      }
     }
+#pragma unroll
+    for (int r = 0; r < KT - 1; r++) *reinterpret_cast<float4 *>(cc_out + (size_t)r * D + c0) = rows[r];
   }
   if (t >= T) return;  // uniform per block
   const int pad = causal ? KT - 1 : (KT - 1) / 2;
@@ -629,12 +638,12 @@ __global__ __launch_bounds__(256) void dwconv_ln_kernel(const TI *__restrict__ x
 // nemit + r of [cache (k-1 rows) ; this pass's GLU rows] -- the k-1 GLU
 // outputs ahead of the next pass's first frame.
 template <typename TI>
-__global__ __launch_bounds__(256) void stream_conv_cache_kernel(const StreamSlots *__restrict__ slots, size_t cco, const TI *__restrict__ g, int D, int nemit,
+__global__ __launch_bounds__(256) void stream_conv_cache_kernel(const CcSlots slots, size_t cco, const TI *__restrict__ g, int D, int nemit,
                                                                 int nq) {
   constexpr int KT = 9;
   const int r = blockIdx.x, w = blockIdx.y, src = nemit + r;  // row r of window (stream) w's next cache
-  const float *cc_in = slots->cc_in[w] + cco;
-  float *cc_out = slots->cc_out[w] + cco;
+  const float *cc_in = slots.cc_in[w] + cco;
+  float *cc_out = slots.cc_out[w] + cco;
   g += (size_t)w * nq * D;
   for (int c = threadIdx.x; c < D; c += 256)
     cc_out[(size_t)r * D + c] = src < KT - 1 ? cc_in[(size_t)src * D + c] : (float)g[(size_t)(src - (KT - 1)) * D + c];
@@ -653,7 +662,7 @@ __global__ __launch_bounds__(256) void stream_conv_cache_kernel(const StreamSlot
 // (reading V from global one key after another cost ~76 us per layer); the
 // first query block of each head also writes the head's part of the next
 // pass's K / V caches from them.  Lk <= 256.
-__global__ __launch_bounds__(256) void stream_attn_kernel(const _Float16 *__restrict__ u, int ldu, const StreamSlots *__restrict__ slots, size_t kvo,
+__global__ __launch_bounds__(256) void stream_attn_kernel(const _Float16 *__restrict__ u, int ldu, const KvSlots slots, size_t kvo,
                                                           int Lc, int nq, int D, const _Float16 *__restrict__ P, int Pn, int dMax,
                                                           const float *__restrict__ pbu, const float *__restrict__ pbv, int chunk, int left, int right,
                                                           _Float16 *__restrict__ out, _Float16 *__restrict__ out_lo, int nemit, int keep) {
@@ -667,8 +676,8 @@ __global__ __launch_bounds__(256) void stream_attn_kernel(const _Float16 *__rest
   u += (size_t)w * nq * ldu;
   out += (size_t)w * nq * D;
   if (out_lo) out_lo += (size_t)w * nq * D;
-  const _Float16 *kc = slots->kc_in[w] + kvo, *vc = slots->vc_in[w] + kvo;
-  _Float16 *kc_out = keep > 0 ? slots->kc_out[w] + kvo : nullptr, *vc_out = slots->vc_out[w] + kvo;
+  const _Float16 *kc = slots.kc_in[w] + kvo, *vc = slots.vc_in[w] + kvo;
+  _Float16 *kc_out = keep > 0 ? slots.kc_out[w] + kvo : nullptr, *vc_out = slots.vc_out[w] + kvo;
   const int i = blockIdx.x * 4 + wave;
   const int Lk = Lc + nq;
   for (int idx = threadIdx.x; idx < Lk * (HD / 8); idx += 256) {  // all row loads in flight at once
@@ -1320,7 +1329,7 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
       const int nq = M / n;  // frames per window (stream)
       {
         ProfScope ps(ctx, "stream_attention");
-        FA_LAUNCH(ps, stream_attn_kernel, dim3(cdiv(nq, 4), c.H, n), dim3(256), 0, ctx->stream, u, 3 * D, sp->slots, kvo, sp->Lc, nq, D,
+        FA_LAUNCH(ps, stream_attn_kernel, dim3(cdiv(nq, 4), c.H, n), dim3(256), 0, ctx->stream, u, 3 * D, sp->kv, kvo, sp->Lc, nq, D,
                   Ly.P + (size_t)(e->maxT - 1 - sp->dMax) * D, sp->Pn, sp->dMax, Ly.pbu, Ly.pbv, sp->chunk, sp->left, sp->right, a, olo, sp->nemit,
                   sp->keep);
         FA_TRY(check_launch(ctx, "stream_attention"));
@@ -1345,17 +1354,19 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
         FA_LAUNCH(ps, (dwconv_silu_kernel<9, 16, 4, _Float16>), grid, dim3(thr), 0, ctx->stream, (const _Float16 *)gg, a, dlo, Ly.dww, Ly.dwb, D, s3);
       FA_TRY(check_launch(ctx, "dwconv"));
     } else {
-      const StreamSlots *slots = sp ? sp->slots : nullptr;  // a stream pass: per-window conv caches
+      static const CcSlots no_slots{};
+      const CcSlots &slots = sp ? sp->cc : no_slots;  // a stream pass: per-window conv caches
+      const int use_slots = sp != nullptr;
       const size_t cco = (size_t)li * 8 * D;
       float *y32 = Ly.cln[0] ? (float *)e->W().dw32 : nullptr;
       if (y32 && D % 4 == 0 && D <= 1024) {  // depthwise + conv-module LayerNorm + SiLU (+ the stream's conv cache) in one kernel
         ProfScope ps(ctx, "dwconv_ln");
         const dim3 grid(mx[3], n);
         if (glu32)
-          FA_LAUNCH(ps, dwconv_ln_kernel<float>, grid, dim3(256), 0, ctx->stream, (const float *)g32, slots, cco, s3, o.conv_causal, Ly.dww, Ly.dwb, Ly.cln[0],
+          FA_LAUNCH(ps, dwconv_ln_kernel<float>, grid, dim3(256), 0, ctx->stream, (const float *)g32, slots, use_slots, cco, s3, o.conv_causal, Ly.dww, Ly.dwb, Ly.cln[0],
                     Ly.cln[1], D, a, dlo, sp ? sp->nemit : 0);
         else
-          FA_LAUNCH(ps, dwconv_ln_kernel<_Float16>, grid, dim3(256), 0, ctx->stream, (const _Float16 *)gg, slots, cco, s3, o.conv_causal, Ly.dww, Ly.dwb,
+          FA_LAUNCH(ps, dwconv_ln_kernel<_Float16>, grid, dim3(256), 0, ctx->stream, (const _Float16 *)gg, slots, use_slots, cco, s3, o.conv_causal, Ly.dww, Ly.dwb,
                     Ly.cln[0], Ly.cln[1], D, a, dlo, sp ? sp->nemit : 0);
         FA_TRY(check_launch(ctx, "dwconv_ln"));
       } else {
@@ -1363,10 +1374,10 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
           ProfScope ps(ctx, "dwconv_gen");
           const dim3 grid(mx[3], n, cdiv(D / 4, 64));
           if (glu32)
-            FA_LAUNCH(ps, dwconv_gen_kernel<float>, grid, dim3(64), 0, ctx->stream, (const float *)g32, slots, cco, s3, o.conv_causal, Ly.dww, Ly.dwb, D, a, dlo,
+            FA_LAUNCH(ps, dwconv_gen_kernel<float>, grid, dim3(64), 0, ctx->stream, (const float *)g32, slots, use_slots, cco, s3, o.conv_causal, Ly.dww, Ly.dwb, D, a, dlo,
                       y32);
           else
-            FA_LAUNCH(ps, dwconv_gen_kernel<_Float16>, grid, dim3(64), 0, ctx->stream, (const _Float16 *)gg, slots, cco, s3, o.conv_causal, Ly.dww, Ly.dwb, D, a,
+            FA_LAUNCH(ps, dwconv_gen_kernel<_Float16>, grid, dim3(64), 0, ctx->stream, (const _Float16 *)gg, slots, use_slots, cco, s3, o.conv_causal, Ly.dww, Ly.dwb, D, a,
                       dlo, y32);
           FA_TRY(check_launch(ctx, "dwconv_gen"));
         }

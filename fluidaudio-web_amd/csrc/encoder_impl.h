@@ -121,13 +121,16 @@ struct PassGeom {
 
 // The caches of the streams in one batched stream pass, window w = stream w:
 // its layer-0 K / V caches ([layers][left][D] f16) and depthwise-conv cache
-// ([layers][8][D] f32), the set the pass reads and the set it writes.  Kept
-// in device memory (refreshed before each pass), so a captured pass serves
-// any set of streams.
-constexpr int kMaxStreamGroup = 32;
-struct StreamSlots {
+// ([layers][8][D] f32), the set the pass reads and the set it writes.  Passed
+// by value to the kernels that use them (a table in device memory cost each
+// of those kernels a dependent pointer load), so a captured pass is keyed by
+// the table.
+constexpr int kMaxStreamGroup = 16;
+struct KvSlots {
   const _Float16 *kc_in[kMaxStreamGroup], *vc_in[kMaxStreamGroup];
   _Float16 *kc_out[kMaxStreamGroup], *vc_out[kMaxStreamGroup];
+};
+struct CcSlots {
   const float *cc_in[kMaxStreamGroup];
   float *cc_out[kMaxStreamGroup];
 };
@@ -139,7 +142,8 @@ struct StreamSlots {
 struct StreamPass {
   int Lc = 0, nemit = 0, keep = 0;
   int chunk = 0, left = 0, right = 0;
-  const StreamSlots *slots = nullptr;  // device table, one entry per window
+  KvSlots kv{};  // one entry per window
+  CcSlots cc{};
   // positional term: distance dMax - r at row r of the layer's table (the
   // offline table's rows maxT-1-dMax ..), Pn = dMax - dMin + 1 rows
   int Pn = 0, dMax = 0;

@@ -25,13 +25,13 @@
 //
 // Several streams of one encoder (fa_stream_push_many) whose next passes have
 // the same shape (rows, pads, cached keys) run as ONE batched pass: window w
-// of the pass is stream w, its caches named by a device table (StreamSlots),
+// of the pass is stream w, its caches named by tables (KvSlots, CcSlots),
 // so the weights are read once for all of them (a pass over a few frames is
 // bound by reading the ~1.2 GB of f16 weights).  Passes run on the encoder's
 // stream lanes (a HIP stream, workspace and staging buffers each); groups of
 // different shapes run on different lanes at once.  Steady-state passes (full
 // key caches, no pads) are replayed from captured hipGraphs keyed by their
-// shape; the cache table is refreshed before each replay.
+// shape and cache table.
 #include <algorithm>
 #include <cstring>
 #include <map>
@@ -65,11 +65,15 @@ struct StreamLane {
   hipEvent_t done = nullptr, in = nullptr;
   float *mel_dev = nullptr, *x_dev = nullptr;
   size_t mel_cap = 0, x_cap = 0;
-  StreamSlots *slots = nullptr;
   uint64_t buf_gen = 0;  // moves when mel_dev / x_dev are reallocated
   std::vector<EncWs::Captured> graphs;
   uint64_t graph_clock = 0;
-  std::vector<float> stage;  // host staging of a pass's mel rows
+  // pinned host staging of a pass's mel rows, two buffers used in turn (a
+  // buffer is rewritten only after its previous copy has completed)
+  float *stage[2] = {nullptr, nullptr};
+  size_t stage_cap[2] = {0, 0};
+  hipEvent_t staged[2] = {nullptr, nullptr};
+  int next_stage = 0;
 };
 
 namespace {
@@ -77,8 +81,17 @@ namespace {
 constexpr int kLookback = 14;  // mel rows before 8*subT the next pass's first frame reads (three k=3 stride-2 convs)
 constexpr int kKT = 9;
 
-__global__ void set_slots_kernel(StreamSlots v, StreamSlots *dst) {
-  if (threadIdx.x == 0) *dst = v;
+// The emitted frames of every window of a batched pass: rows [w nq, w nq +
+// nemit) of x to window w's output tensor.
+struct OutRows {
+  float *dst[kMaxStreamGroup];
+};
+__global__ __launch_bounds__(256) void stream_out_kernel(const float4 *__restrict__ x, int nq, int nemit, int D4, OutRows o) {
+  const int w = blockIdx.y;
+  const long n4 = (long)nemit * D4;
+  const float4 *src = x + (size_t)w * nq * D4;
+  float4 *dst = reinterpret_cast<float4 *>(o.dst[w]);
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n4; i += (long)gridDim.x * 256) dst[i] = src[i];
 }
 
 int lane_grow(fa_ctx *ctx, StreamLane *L, void **buf, size_t *cap, size_t need) {
@@ -100,10 +113,9 @@ int get_lane(fa_ctx *ctx, fa_encoder *e, int l, StreamLane **out) {
     StreamLane *L = new StreamLane();
     e->slane[l] = L;
     if (hipStreamCreateWithFlags(&L->hs, hipStreamNonBlocking) != hipSuccess || hipEventCreateWithFlags(&L->done, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&L->in, hipEventDisableTiming) != hipSuccess)
+        hipEventCreateWithFlags(&L->in, hipEventDisableTiming) != hipSuccess || hipEventCreateWithFlags(&L->staged[0], hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&L->staged[1], hipEventDisableTiming) != hipSuccess)
       return set_err(ctx, FA_E_DEVICE, "encodeStreamPush: creating a stream lane failed");
-    L->slots = (StreamSlots *)dev_alloc(ctx, sizeof(StreamSlots));
-    if (!L->slots) return FA_E_OOM;
   }
   *out = e->slane[l];
   return FA_OK;
@@ -177,24 +189,32 @@ int run_group(fa_ctx *ctx, fa_encoder *e, StreamLane *L, fa_stream *const *sts, 
   FA_TRY(pass_workspace(ctx, e, g, c.layers, true));
   FA_TRY(lane_grow(ctx, L, (void **)&L->mel_dev, &L->mel_cap, (size_t)n * m * MB * 4));
   FA_TRY(lane_grow(ctx, L, (void **)&L->x_dev, &L->x_cap, (size_t)n * nComp * D * 4));
-  L->stage.resize((size_t)n * m * MB);
-  for (int w = 0; w < n; w++) std::memcpy(L->stage.data() + (size_t)w * m * MB, sts[w]->fifo.data(), (size_t)m * MB * 4);
-  FA_HIP(ctx, hipMemcpyAsync(L->mel_dev, L->stage.data(), (size_t)n * m * MB * 4, hipMemcpyHostToDevice, L->hs));
-  FA_HIP(ctx, hipStreamSynchronize(L->hs));  // the staging buffer and FIFOs are edited once this pass is queued
-  StreamSlots tab{};
+  {  // the windows' mel rows, copied from the FIFOs into pinned staging, then to the device
+    const int b = L->next_stage;
+    L->next_stage ^= 1;
+    const size_t bytes = (size_t)n * m * MB * 4;
+    FA_HIP(ctx, hipEventSynchronize(L->staged[b]));  // this buffer's previous copy (two passes back) is done
+    if (bytes > L->stage_cap[b]) {
+      if (L->stage[b]) FA_HIP(ctx, hipHostFree(L->stage[b]));
+      L->stage[b] = nullptr;
+      L->stage_cap[b] = 0;
+      FA_HIP(ctx, hipHostMalloc((void **)&L->stage[b], bytes, hipHostMallocDefault));
+      L->stage_cap[b] = bytes;
+    }
+    for (int w = 0; w < n; w++) std::memcpy(L->stage[b] + (size_t)w * m * MB, sts[w]->fifo.data(), (size_t)m * MB * 4);
+    FA_HIP(ctx, hipMemcpyAsync(L->mel_dev, L->stage[b], bytes, hipMemcpyHostToDevice, L->hs));
+    FA_HIP(ctx, hipEventRecord(L->staged[b], L->hs));
+  }
+  KvSlots kv{};
+  CcSlots cc{};
   for (int w = 0; w < n; w++) {
     fa_stream *st = sts[w];
-    tab.kc_in[w] = st->kc[st->cur];
-    tab.vc_in[w] = st->vc[st->cur];
-    tab.kc_out[w] = st->kc[st->cur ^ 1];
-    tab.vc_out[w] = st->vc[st->cur ^ 1];
-    tab.cc_in[w] = st->cc[st->cur];
-    tab.cc_out[w] = st->cc[st->cur ^ 1];
-  }
-  {
-    ProfScope ps(ctx, "stream_slots");
-    FA_LAUNCH(ps, set_slots_kernel, dim3(1), dim3(64), 0, ctx->stream, tab, L->slots);
-    FA_TRY(check_launch(ctx, "stream_slots"));
+    kv.kc_in[w] = st->kc[st->cur];
+    kv.vc_in[w] = st->vc[st->cur];
+    kv.kc_out[w] = st->kc[st->cur ^ 1];
+    kv.vc_out[w] = st->vc[st->cur ^ 1];
+    cc.cc_in[w] = st->cc[st->cur];
+    cc.cc_out[w] = st->cc[st->cur ^ 1];
   }
   StreamPass sp;
   sp.Lc = s0->Lc;
@@ -203,7 +223,8 @@ int run_group(fa_ctx *ctx, fa_encoder *e, StreamLane *L, fa_stream *const *sts, 
   sp.chunk = s0->C;
   sp.left = s0->left;
   sp.right = s0->right;
-  sp.slots = L->slots;
+  sp.kv = kv;
+  sp.cc = cc;
   sp.Pn = s0->Pn;
   sp.dMax = s0->dMax;
   sp.kv_ld = s0->left;
@@ -211,7 +232,15 @@ int run_group(fa_ctx *ctx, fa_encoder *e, StreamLane *L, fa_stream *const *sts, 
   const char *ge = getenv("FA_GRAPH");
   const bool steady = s0->Lc == s0->left && pl.pb == 0 && pl.pt == 0;
   if (steady && !ctx->prof_on && !(ge && ge[0] == '0')) {
+    // the cache tables are baked into the launches, so every pointer in them
+    // is part of the key (a new stream may get a freed stream's address for
+    // one cache and not for another); a stable set of streams alternates
+    // between two captured passes (the caches' double buffers)
     std::vector<int64_t> key = {(int64_t)e->ws_gen, (int64_t)L->buf_gen, n, m, nComp, nemit};
+    for (int w = 0; w < n; w++)
+      for (const void *p : {(const void *)kv.kc_in[w], (const void *)kv.vc_in[w], (const void *)kv.kc_out[w], (const void *)kv.vc_out[w],
+                            (const void *)cc.cc_in[w], (const void *)cc.cc_out[w]})
+        key.push_back((int64_t)(uintptr_t)p);
     EncWs::Captured *hit = nullptr;
     for (auto &gr : L->graphs)
       if (gr.key == key) hit = &gr;
@@ -229,7 +258,7 @@ int run_group(fa_ctx *ctx, fa_encoder *e, StreamLane *L, fa_stream *const *sts, 
       const hipError_t ie = hipGraphInstantiateWithFlags(&exec, graph, 0);
       (void)hipGraphDestroy(graph);
       if (ie != hipSuccess) return set_err(ctx, FA_E_DEVICE, "stream pass: graph instantiate: %s", hipGetErrorString(ie));
-      if (L->graphs.size() >= 8) {  // a few group sizes and chunk shapes repeat
+      if (L->graphs.size() >= 16) {  // two per stable set of streams and chunk shape
         size_t lru = 0;
         for (size_t i = 1; i < L->graphs.size(); i++)
           if (L->graphs[i].used < L->graphs[lru].used) lru = i;
@@ -245,6 +274,7 @@ int run_group(fa_ctx *ctx, fa_encoder *e, StreamLane *L, fa_stream *const *sts, 
   } else {
     FA_TRY(launch());
   }
+  OutRows orows{};
   for (int w = 0; w < n; w++) {
     fa_stream *st = sts[w];
     st->cur ^= 1;
@@ -252,8 +282,16 @@ int run_group(fa_ctx *ctx, fa_encoder *e, StreamLane *L, fa_stream *const *sts, 
     fa_tensor o;
     TensorRec *ro;
     FA_TRY(new_tensor(ctx, nemit, D, S_F32, (size_t)nemit * D * 4, &o, &ro));
-    FA_TRY(encoder_copy_f4(ctx, L->x_dev + (size_t)w * nComp * D, ro->ptr, (size_t)nemit * D * 4, "stream_out"));
+    orows.dst[w] = (float *)ro->ptr;
     outs[w]->push_back(o);
+  }
+  if (D % 4) return set_err(ctx, FA_E_UNSUPPORTED, "stream pass: D %d not a multiple of 4", D);
+  {
+    ProfScope ps(ctx, "stream_out");
+    const long n4 = (long)nemit * (D / 4);
+    FA_LAUNCH(ps, stream_out_kernel, dim3((unsigned)std::max<long>(1, std::min<long>(cdiv(n4, 256), 64)), n), dim3(256), 0, ctx->stream,
+              (const float4 *)L->x_dev, nComp, nemit, D / 4, orows);
+    FA_TRY(check_launch(ctx, "stream_out"));
   }
   return FA_OK;
 }
@@ -353,8 +391,12 @@ void fa::stream_lanes_free(fa_encoder *e) {
     for (auto &g : L->graphs)
       if (g.exec) (void)hipGraphExecDestroy(g.exec);
     encoder_ws_free(L->ws);
-    for (void *p : {(void *)L->mel_dev, (void *)L->x_dev, (void *)L->slots})
+    for (void *p : {(void *)L->mel_dev, (void *)L->x_dev})
       if (p) (void)hipFree(p);
+    for (int b = 0; b < 2; b++) {
+      if (L->stage[b]) (void)hipHostFree(L->stage[b]);
+      if (L->staged[b]) (void)hipEventDestroy(L->staged[b]);
+    }
     if (L->done) (void)hipEventDestroy(L->done);
     if (L->in) (void)hipEventDestroy(L->in);
     if (L->hs) (void)hipStreamDestroy(L->hs);
