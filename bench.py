@@ -634,8 +634,8 @@ def bench_stream(args, fa, ctx):
     kern = {lab: {"launches_per_chunk": v["launches"] // prof_chunks, "us_per_chunk": round(v["ms"] * 1e3 / prof_chunks, 1)}
             for lab, v in sorted(kern.items(), key=lambda kv: -kv[1]["ms"])}
     # several streams in flight: each 160 ms tick pushes one piece to every
-    # stream in one fa_stream_push_many call (each stream's passes on a HIP
-    # stream of its own)
+    # stream in one fa_stream_push_many call; streams at the same point run as
+    # one batched pass (up to 16 per pass, passes on the encoder's lanes)
     def run_many(n):
         sts = [fa.createEncodeStream(ctx, enc) for _ in range(n)]
         for t in range(0, mel.shape[1], piece):
@@ -645,7 +645,7 @@ def bench_stream(args, fa, ctx):
             fa.disposeEncodeStream(ctx, st)
 
     concurrent = {}
-    for n in (4, 8, 16):
+    for n in (4, 8, 16, 32):
         run_many(n)
         ctx.sync()
         t0 = time.perf_counter()
