@@ -74,7 +74,7 @@ def traffic_for(cls):
         return None
 
 
-def kernel_work(cfg, lens, layout):
+def kernel_work(cfg, lens, layout, fmt="f16"):
     """label -> (kind, amount per launch); kind 'flop' (MFMA) or 'byte' (HBM).
     Python ints throughout (numpy int32 lengths would overflow the products)."""
     lens = [int(t) for t in lens]
@@ -102,6 +102,9 @@ def kernel_work(cfg, lens, layout):
         "dwconv": ("byte", M * D * 4), "dwconv_f32": ("byte", M * D * 6), "dwconv_lo": ("byte", M * D * 6), "dwconv_x": ("byte", M * D * 8),
         "zero_pad": ("byte", 0), "enc_src": ("byte", 0), "enc_in": ("byte", R0 * MB * 8), "enc_out": ("byte", M * D * 8),
     }
+    if fmt in ("int8", "int4"):  # one layer's linears widened to f16: packed weights (+ int4 scales) in, f16 out
+        nw = 4 * D * DFF + 3 * D * D + D * D + 2 * D * D + D * D
+        w["dequant_w"] = ("byte", nw * 2 + (nw if fmt == "int8" else nw // 2 + nw // 32 * 2))
     for ln in ("ln_ff1", "ln_att", "ln_conv", "ln_ff2"):
         w[ln] = ("byte", M * D * 6)       # f32 in, f16 out
         w[ln + "_x"] = ("byte", M * D * 8)  # f32 in, f16 hi + lo planes out
@@ -225,7 +228,7 @@ def run_encoder(args, fa, ctx, cfg, batches, feats_h, layout, fmt="f16", seed=1)
     del man
     feats = ctx.upload(feats_h, feats_h.shape[0], feats_h.shape[1])
     batches = [(np.asarray(st, np.int32), np.asarray(ln, np.int32)) for st, ln in batches]
-    works = [kernel_work(cfg, ln, layout) for _, ln in batches]
+    works = [kernel_work(cfg, ln, layout, fmt) for _, ln in batches]
 
     def run_batch(st, ln):
         a = ctx.pushArena()

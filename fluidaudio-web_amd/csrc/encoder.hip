@@ -1055,35 +1055,54 @@ int pass_geometry(fa_ctx *ctx, const fa_encoder *e, const int32_t *lens, int n, 
 // them; the scratch is L2 / MALL-hot when the GEMM reads it.
 constexpr int kDequantRows = 512;
 
-// One launch per layer widens all its quantised linears: one 16-byte unit of
-// packed weights per thread (int8 16 values; int4 one group-32 block, 32
-// values, with its scale); item i covers units [end[i-1], end[i]).
+// One launch per layer widens all its quantised linears: blockIdx.y = the
+// linear, each lane one 8-value chunk (int8: 8 bytes; int4: one 4-byte word
+// of a group-32 block, with the block's scale) -> 16 contiguous output bytes,
+// so a wave's stores cover 1 KB without gaps; four chunks per lane, every
+// load issued before the first store.  item i has chunks[i] chunks.
 constexpr int kWdqMax = 8;
 struct WdqList {
   const uint8_t *w[kWdqMax];
   const _Float16 *s[kWdqMax];
   _Float16 *out[kWdqMax];
-  long end[kWdqMax];
+  long chunks[kWdqMax];
   int n, i4;
 };
+constexpr int kWdqPer = 4;  // chunks per lane
 __global__ __launch_bounds__(256) void wdq_kernel(WdqList L) {
-  long u = (long)blockIdx.x * 256 + threadIdx.x;
-  if (u >= L.end[L.n - 1]) return;
-  int i = 0;
-  while (u >= L.end[i]) i++;
-  if (i > 0) u -= L.end[i - 1];
-  const uint4 v = reinterpret_cast<const uint4 *>(L.w[i])[u];
+  const int i = blockIdx.y;
+  const long n8 = L.chunks[i];
+  const long c0 = (long)blockIdx.x * 256 * kWdqPer + threadIdx.x;
+  if (c0 >= n8) return;
+  h8 o[kWdqPer];
   if (L.i4) {
-    const _Float16 sc = L.s[i][u];
-    h8 *o = reinterpret_cast<h8 *>(L.out[i] + u * 32);
-    o[0] = i4x8_to_h8(v.x, sc);
-    o[1] = i4x8_to_h8(v.y, sc);
-    o[2] = i4x8_to_h8(v.z, sc);
-    o[3] = i4x8_to_h8(v.w, sc);
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(L.w[i]);
+    uint32_t v[kWdqPer];
+    _Float16 sc[kWdqPer];
+#pragma unroll
+    for (int r = 0; r < kWdqPer; r++) {
+      const long c = c0 + r * 256;
+      v[r] = c < n8 ? w[c] : 0u;
+      sc[r] = c < n8 ? L.s[i][c >> 2] : (_Float16)0.f;  // a group-32 block is 4 chunks
+    }
+#pragma unroll
+    for (int r = 0; r < kWdqPer; r++) o[r] = i4x8_to_h8(v[r], sc[r]);
   } else {
-    h8 *o = reinterpret_cast<h8 *>(L.out[i] + u * 16);
-    o[0] = i8x8_to_h8(uint2{v.x, v.y});
-    o[1] = i8x8_to_h8(uint2{v.z, v.w});
+    const uint2 *w = reinterpret_cast<const uint2 *>(L.w[i]);
+    uint2 v[kWdqPer];
+#pragma unroll
+    for (int r = 0; r < kWdqPer; r++) {
+      const long c = c0 + r * 256;
+      v[r] = c < n8 ? w[c] : uint2{0u, 0u};
+    }
+#pragma unroll
+    for (int r = 0; r < kWdqPer; r++) o[r] = i8x8_to_h8(v[r]);
+  }
+  h8 *out = reinterpret_cast<h8 *>(L.out[i]);
+#pragma unroll
+  for (int r = 0; r < kWdqPer; r++) {
+    const long c = c0 + r * 256;
+    if (c < n8) out[c] = o[r];
   }
 }
 
@@ -1209,22 +1228,21 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
     WdqList &W = wdq;
     W = WdqList{};
     _Float16 *dst = (_Float16 *)e->W().wdq;
-    long units = 0;
+    long mx = 0;
     for (const Lin *L : layer_lins(Ly)) {
       if (L->bkind == B_F16) continue;
-      const int i4 = L->bkind == B_I4;
       W.w[W.n] = (const uint8_t *)L->w;
       W.s[W.n] = (const _Float16 *)L->scales;
       W.out[W.n] = dst;
-      units += (long)L->N * L->K / (i4 ? 32 : 16);
-      W.end[W.n] = units;
-      W.i4 = i4;
+      W.chunks[W.n] = (long)L->N * L->K / 8;
+      mx = std::max(mx, W.chunks[W.n]);
+      W.i4 = L->bkind == B_I4;
       wdq_src[W.n++] = L;
       dst += (size_t)L->N * L->K;
     }
     if (!W.n) return FA_OK;
     ProfScope ps(ctx, "dequant_w");
-    FA_LAUNCH(ps, wdq_kernel, dim3(cdiv(units, 256)), dim3(256), 0, ctx->stream, W);
+    FA_LAUNCH(ps, wdq_kernel, dim3(cdiv(mx, 256 * kWdqPer), W.n), dim3(256), 0, ctx->stream, W);
     return check_launch(ctx, "dequant_w");
   };
   auto gemm = [&](const void *A, const void *Alo, int lda, const Lin &L, void *Cp, void *Clo, int ldc, int out_f16, int act, const float *add, int glu,
