@@ -3,6 +3,7 @@
 // then the fused encoder's packed-vs-standalone equality.  Exit code 0 = pass.
 "use strict";
 const { HipContext, version, encoderTsub } = require("./hip-context.js");
+const addonRef = require("./fa_hip.node");
 
 let seed = 0x5eed; // mulberry32, as scripts/backend-conformance.mjs:46-54
 const rand = () => {
@@ -98,6 +99,22 @@ const check = (name, d, tol) => {
   const alone1 = await ctx.download(ctx._encodeFused(fused, [mels[1]]));
   check("fused encoder window 0 packed == alone", maxdiff(batch.subarray(0, t0 * 256), alone0), 1e-4);
   check("fused encoder window 1 packed == alone", maxdiff(batch.subarray(t0 * 256), alone1), 1e-4);
+  // several batches of one resident feature stream on the encoder's two lanes == one batch at a time
+  {
+    const T = 900, feats = mk(128 * T, 2);
+    const fs = ctx.upload(feats, 128, T);
+    const batches = [{ starts: [0, 300], lens: [300, 97] }, { starts: [150], lens: [64] }, { starts: [500, 10, 800], lens: [400, 33, 100] }];
+    const outs = ctx._encodeFusedStreamBatches(fused, fs, batches);
+    let md2 = 0;
+    for (let b = 0; b < batches.length; b++) {
+      const got = await ctx.download(outs[b]);
+      const ref = await ctx.download(ctx._info(addonRef.encoderForwardStream(ctx.ctx, fused.enc, fs.h, Int32Array.from(batches[b].starts),
+                                                                              Int32Array.from(batches[b].lens), 0, -1)));
+      md2 = Math.max(md2, got.length === ref.length ? maxdiff(got, ref) : Infinity);
+    }
+    check("fused encoder stream batches == one batch at a time", md2, 0);
+    ctx.freeTensor(fs);
+  }
   ctx._destroyFusedEncoder(fused);
   // log-mel front end: windows of one stream == each window alone; silence -> 0
   const pcmH = mk(16000 * 3, 0.2);
