@@ -321,8 +321,9 @@ __global__ __launch_bounds__(256) void enc_ln_kernel(const float *__restrict__ x
   for (int t = 0; t < V; t++) {
     const int j = lane + 64 * t;
     const f4 gm = gv[t], bt = bv[t];
-    float o[4] = {(v[t].x - mean) * inv * gm.x + bt.x, (v[t].y - mean) * inv * gm.y + bt.y, (v[t].z - mean) * inv * gm.z + bt.z,
-                  (v[t].w - mean) * inv * gm.w + bt.w};
+    // one rounding for the affine (fma), as the skinny GEMM's folded LayerNorm computes it
+    float o[4] = {__builtin_fmaf((v[t].x - mean) * inv, gm.x, bt.x), __builtin_fmaf((v[t].y - mean) * inv, gm.y, bt.y),
+                  __builtin_fmaf((v[t].z - mean) * inv, gm.z, bt.z), __builtin_fmaf((v[t].w - mean) * inv, gm.w, bt.w)};
     if constexpr (SILU) {
 #pragma unroll
       for (int e = 0; e < 4; e++) o[e] = silu_f(o[e]);
@@ -330,6 +331,7 @@ __global__ __launch_bounds__(256) void enc_ln_kernel(const float *__restrict__ x
     h4 hi, lo;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
+      asm("" : "+v"(o[e]));  // the f32 value rounded once to f16 (no fma-with-conversion), as the folded skinny GEMM does
       hi[e] = (_Float16)o[e];
       lo[e] = (_Float16)(o[e] - (float)hi[e]);
     }
@@ -1245,10 +1247,27 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
     FA_LAUNCH(ps, wdq_kernel, dim3(cdiv(mx, 256 * kWdqPer), W.n), dim3(256), 0, ctx->stream, W);
     return check_launch(ctx, "dequant_w");
   };
+  // stream passes of <= 16 rows: the LayerNorm ahead of the q|k|v, pw1 and
+  // FF2 W1 products is folded into their skinny GEMM (A built from the
+  // residual rows in the kernel), one launch fewer each (FA_LN_FOLD=0: off).
+  // Measured per 160 ms chunk, 24 layers: one stream 2.34 -> 2.22 ms; at 32
+  // rows (16 batched streams) every workgroup's row statistics cost more
+  // than the launch saved (617 -> 608 aggregate audio-s/wall-s), so not there.
+  const char *lf = getenv("FA_LN_FOLD");
+  const bool fold_ln = sp && M <= 16 && D == 1024 && e->format == FA_W_F16 && !(lf && lf[0] == '0');
+  struct {
+    const float *g = nullptr, *b = nullptr;
+    bool lo = false;
+  } lnf;
   auto gemm = [&](const void *A, const void *Alo, int lda, const Lin &L, void *Cp, void *Clo, int ldc, int out_f16, int act, const float *add, int glu,
                   const char *label) {
     GemmArgs p;
     p.A = A; p.Alo = Alo; p.lda = lda; p.akind = A_F16;
+    if (lnf.g) {  // A = LayerNorm(x) (+ its lo plane), built in the GEMM
+      p.A = nullptr; p.Alo = nullptr;
+      p.ln_x = x; p.ln_g = lnf.g; p.ln_b = lnf.b; p.ln_eps = 1e-5f; p.ln_lo = lnf.lo;
+      lnf.g = lnf.b = nullptr;
+    }
     set_gemm_b(p, L);
     if (L.bkind != B_F16 && M >= kDequantRows) {  // the layer's widened copy (dequant_layer), f16 route
       const _Float16 *wf = nullptr;
@@ -1319,7 +1338,7 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
     FA_TRY(gemm(h, hl, D, Ly.ff1w1, u, ul, c.DFF, 1, FA_ACT_SILU, nullptr, 0, hl ? "ff1_w1_x" : (ul ? "ff1_w1_u" : "ff1_w1")));
     FA_TRY(gemm(u, ul, c.DFF, Ly.ff1w2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, ul ? "ff1_w2_x" : "ff1_w2"));
     // attention
-    FA_TRY(ln(1, Ly, hl ? "ln_att_x" : "ln_att"));
+    if (!fold_ln) FA_TRY(ln(1, Ly, hl ? "ln_att_x" : "ln_att"));
     bool vt_fused = false;
     {
       // q|k|v; offline, V goes straight to the attention's transposed buffer
@@ -1329,6 +1348,10 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
       set_gemm_b(p, Ly.qkv);
       p.C = u; p.ldc = 3 * D; p.out_f16 = 1;
       p.M = M; p.allow_skinny = sp != nullptr;
+      if (fold_ln) {  // norm_att folded in
+        p.A = nullptr; p.Alo = nullptr;
+        p.ln_x = x; p.ln_g = Ly.ln[1][0]; p.ln_b = Ly.ln[1][1]; p.ln_eps = 1e-5f; p.ln_lo = hl != nullptr;
+      }
       if (!sp && c.HD == 128 && e->vt_fuse && gemm_takes_direct(ctx, p)) {
         p.vt = (_Float16 *)e->W().vt; p.vrow = (const int *)e->W().vrow; p.vcol0 = 2 * D; p.vtp = Tp;
         vt_fused = true;
@@ -1355,7 +1378,10 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
     }
     FA_TRY(gemm(a, olo, D, Ly.out, x, nullptr, D, 0, FA_ACT_NONE, x, 0, olo ? "attn_out_x" : "attn_out"));
     // conv module: pw1 + GLU (f16, or f32 when exact) -> depthwise (+ LayerNorm) + SiLU -> pw2
-    FA_TRY(ln(2, Ly, hl ? "ln_conv_x" : "ln_conv"));
+    if (fold_ln)  // norm_conv folded into pw1
+      lnf = {Ly.ln[2][0], Ly.ln[2][1], hl != nullptr};
+    else
+      FA_TRY(ln(2, Ly, hl ? "ln_conv_x" : "ln_conv"));
     const bool glu32 = ex & FA_EXACT_GLU;
     FA_TRY(gemm(h, hl, D, Ly.pw1, glu32 ? (void *)g32 : (void *)gg, nullptr, D, glu32 ? 0 : 1, FA_ACT_NONE, nullptr, 1,
                 hl ? "pw1_glu_x" : (glu32 ? "pw1_glu_f32" : "pw1_glu")));
@@ -1412,7 +1438,10 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
     }
     FA_TRY(gemm(a, dlo, D, Ly.pw2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, dlo ? "pw2_x" : "pw2"));
     // FF2 + norm_out
-    FA_TRY(ln(3, Ly, hl ? "ln_ff2_x" : "ln_ff2"));
+    if (fold_ln)  // norm_ff2 folded into FF2 W1
+      lnf = {Ly.ln[3][0], Ly.ln[3][1], hl != nullptr};
+    else
+      FA_TRY(ln(3, Ly, hl ? "ln_ff2_x" : "ln_ff2"));
     FA_TRY(gemm(h, hl, D, Ly.ff2w1, u, ul, c.DFF, 1, FA_ACT_SILU, nullptr, 0, hl ? "ff2_w1_x" : (ul ? "ff2_w1_u" : "ff2_w1")));
     FA_TRY(gemm(u, ul, c.DFF, Ly.ff2w2, x, nullptr, D, 0, FA_ACT_NONE, x, 0, ul ? "ff2_w2_x" : "ff2_w2"));
     if (fuse_ln && li + 1 < layers) {

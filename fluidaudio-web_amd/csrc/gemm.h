@@ -29,6 +29,12 @@ struct GemmArgs {
   // differently from the tiled kernels'); set by the streaming passes only, so
   // an offline batch's frames do not depend on how many windows it holds
   int allow_skinny = 0;
+  // skinny route only: A = LayerNorm(ln_x) computed in the GEMM (f32 rows
+  // [M, K], gamma / beta [K], K = 1024), the LayerNorm kernel's arithmetic;
+  // ln_lo: also its exact lo plane (A ignored)
+  const float *ln_x = nullptr, *ln_g = nullptr, *ln_b = nullptr;
+  float ln_eps = 0.f;
+  int ln_lo = 0;
   const float *bias = nullptr;      // [N]
   const float *add = nullptr;       // f32 residual [M, ldadd]; may alias C
   int ldadd = 0;

@@ -782,6 +782,111 @@ __global__ __launch_bounds__(64 * KS) void gemm_skinny_kernel(GemmArgs p) {
   epilogue_direct<TI, 1, EPI>(p, acc, 0, n0, lane);
 }
 
+// The skinny route with the LayerNorm of its A rows folded in (stream
+// passes: the norm_att / norm_conv / norm_ff2 launches disappear).  The
+// workgroup first computes each row's mean and 1/std exactly as
+// enc_ln_kernel does (one wave per row, float4 per lane at lane + 64 t, the
+// same sums), then every A fragment is built from the f32 rows as
+// f16(fma((x - mean) * inv, gamma, beta)) (+ its exact lo plane), the values
+// the LayerNorm kernel stores.  K = 1024.
+__device__ __forceinline__ float ln_affine(float x, float mean, float inv, float g, float b) { return __builtin_fmaf((x - mean) * inv, g, b); }
+
+template <int TI, int KS, int EPI, int LO>
+__global__ __launch_bounds__(64 * KS) void gemm_skinny_ln_kernel(GemmArgs p) {
+  constexpr int G = 4, D = 1024;
+  __shared__ f4 part[KS > 1 ? KS - 1 : 1][TI][64];
+  __shared__ float stat[2][32];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c16 = lane & 15, g = lane >> 4;
+  for (int r = wave; r < p.M; r += KS) {  // row statistics
+    const float4 *xr = reinterpret_cast<const float4 *>(p.ln_x + (size_t)r * D);
+    float4 v[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) v[t] = xr[lane + 64 * t];
+    float s = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; t++) s += v[t].x + v[t].y + v[t].z + v[t].w;
+    const float mean = wave_sum(s) * (1.f / D);
+    float q = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const float a = v[t].x - mean, b = v[t].y - mean, c = v[t].z - mean, d = v[t].w - mean;
+      q += a * a + b * b + c * c + d * d;
+    }
+    const float inv = rsqrtf(wave_sum(q) * (1.f / D) + p.ln_eps);
+    if (lane == 0) {
+      stat[0][r] = mean;
+      stat[1][r] = inv;
+    }
+  }
+  __syncthreads();
+  const int n0 = blockIdx.x * 16;
+  const int ks = p.K / KS, kb = wave * ks, nst = ks / 32;
+  const _Float16 *B = reinterpret_cast<const _Float16 *>(p.B) + (size_t)(n0 + c16) * p.K + kb + g * 8;
+  const float *X[TI];
+  float mean[TI], inv[TI];
+#pragma unroll
+  for (int i = 0; i < TI; i++) {
+    const int r = min(16 * i + c16, p.M - 1);
+    X[i] = p.ln_x + (size_t)r * p.K + kb + g * 8;
+    mean[i] = stat[0][r];
+    inv[i] = stat[1][r];
+  }
+  const float *Gm = p.ln_g + kb + g * 8, *Bt = p.ln_b + kb + g * 8;
+  f4 acc[TI][1];
+#pragma unroll
+  for (int i = 0; i < TI; i++) acc[i][0] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < nst; s0 += G) {
+    h8 bf[G];
+    float4 xv[G][TI][2], gv[G][2], bv[G][2];
+#pragma unroll
+    for (int u = 0; u < G; u++) {
+      const int st = min(s0 + u, nst - 1) * 32;  // past the slice: a repeat, never used
+      bf[u] = *reinterpret_cast<const h8 *>(B + st);
+#pragma unroll
+      for (int e = 0; e < 2; e++) {
+        gv[u][e] = reinterpret_cast<const float4 *>(Gm + st)[e];
+        bv[u][e] = reinterpret_cast<const float4 *>(Bt + st)[e];
+#pragma unroll
+        for (int i = 0; i < TI; i++) xv[u][i][e] = reinterpret_cast<const float4 *>(X[i] + st)[e];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < G; u++) {
+      if (s0 + u < nst) {
+        const float gg[8] = {gv[u][0].x, gv[u][0].y, gv[u][0].z, gv[u][0].w, gv[u][1].x, gv[u][1].y, gv[u][1].z, gv[u][1].w};
+        const float bb[8] = {bv[u][0].x, bv[u][0].y, bv[u][0].z, bv[u][0].w, bv[u][1].x, bv[u][1].y, bv[u][1].z, bv[u][1].w};
+#pragma unroll
+        for (int i = 0; i < TI; i++) {
+          const float xx[8] = {xv[u][i][0].x, xv[u][i][0].y, xv[u][i][0].z, xv[u][i][0].w, xv[u][i][1].x, xv[u][i][1].y, xv[u][i][1].z, xv[u][i][1].w};
+          h8 hi, lo;
+#pragma unroll
+          for (int e = 0; e < 8; e++) {
+            float o = ln_affine(xx[e], mean[i], inv[i], gg[e], bb[e]);
+            asm("" : "+v"(o));  // rounded once to f16, as enc_ln_kernel stores it
+            hi[e] = (_Float16)o;
+            lo[e] = (_Float16)(o - (float)hi[e]);
+          }
+          acc[i][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[u], hi, acc[i][0], 0, 0, 0);  // C^T tile
+          if constexpr (LO) acc[i][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[u], lo, acc[i][0], 0, 0, 0);
+        }
+      }
+    }
+  }
+  if constexpr (KS > 1) {
+    if (wave > 0)
+#pragma unroll
+      for (int i = 0; i < TI; i++) part[wave - 1][i][lane] = acc[i][0];
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int w = 0; w < KS - 1; w++)
+#pragma unroll
+      for (int i = 0; i < TI; i++) acc[i][0] += part[w][i][lane];
+  }
+  epilogue_direct<TI, 1, EPI>(p, acc, 0, n0, lane);
+}
+
 // K split per workgroup: 8 waves up to N = 2048, 4 above (16 measured slower
 // at N = 1024: 8.8 against 6.0 us for the 1024 x 1024 two-plane product).
 static inline int skinny_ks(int N) { return N <= 2048 ? 8 : 4; }
@@ -792,6 +897,24 @@ static int launch_skinny(fa_ctx *ctx, const GemmArgs &p, const char *label) {
   const int ti = p.M <= 16 ? 1 : 2;
   ProfScope ps(ctx, label);
   const dim3 grid(p.N / 16);
+  if (p.ln_x) {  // A = LayerNorm(ln_x), built in the kernel
+#define FA_SKL(TI, KS)                                                                                   \
+  do {                                                                                                  \
+    if (p.ln_lo)                                                                                        \
+      FA_LAUNCH(ps, (gemm_skinny_ln_kernel<TI, KS, EPI, 1>), grid, dim3(64 * KS), 0, ctx->stream, p);  \
+    else                                                                                                \
+      FA_LAUNCH(ps, (gemm_skinny_ln_kernel<TI, KS, EPI, 0>), grid, dim3(64 * KS), 0, ctx->stream, p);  \
+  } while (0)
+    if (ti == 1) {
+      if (ks == 4) FA_SKL(1, 4);
+      else FA_SKL(1, 8);
+    } else {
+      if (ks == 4) FA_SKL(2, 4);
+      else FA_SKL(2, 8);
+    }
+#undef FA_SKL
+    return check_launch(ctx, label);
+  }
 #define FA_SK(TI, KS)                                                                                \
   do {                                                                                               \
     if (p.Alo)                                                                                       \
@@ -816,6 +939,7 @@ static inline bool takes_skinny(const GemmArgs &p) {
   const char *e = getenv("FA_GEMM_SKINNY");
   if (e && e[0] == '0') return false;
   const int ks = skinny_ks(p.N);
+  if (p.ln_x && (p.K != 1024 || p.Alo || ((uintptr_t)p.ln_x & 15) || ((uintptr_t)p.ln_g & 15) || ((uintptr_t)p.ln_b & 15))) return false;
   return p.allow_skinny && p.M <= 32 && p.akind == A_F16 && p.bkind == B_F16 && !p.vt && epi_of(p) != EPI_GENERIC && p.N % 16 == 0 && p.K % (32 * ks) == 0 &&
          p.lda % 8 == 0 && p.ldc % 8 == 0 && !((uintptr_t)p.A & 15) && !((uintptr_t)p.Alo & 15) && !((uintptr_t)p.B & 15) && !((uintptr_t)p.C & 15) &&
          !((uintptr_t)p.Clo & 15) && !((uintptr_t)p.add & 15) && p.ldadd % 4 == 0;
@@ -825,6 +949,7 @@ template <int AK, int BKND, int EPI>
 static int launch_tile(fa_ctx *ctx, const GemmArgs &p, const char *label) {
   if constexpr (AK == A_F16 && BKND == B_F16 && EPI != EPI_GENERIC)
     if (takes_skinny(p)) return launch_skinny<EPI>(ctx, p, label);
+  if (p.ln_x) return set_err(ctx, FA_E_UNSUPPORTED, "%s: a LayerNorm-folded A needs the skinny route (<= 32 rows, K = 1024)", label);
   if constexpr (AK == A_F16 && BKND == B_F16 && EPI != EPI_GENERIC) {
     if (p.Alo) {
       switch (pick_dma(ctx, p)) {

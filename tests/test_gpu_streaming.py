@@ -192,3 +192,26 @@ def test_streams_pushed_together_equal_streams_pushed_alone(ctx, fa, monkeypatch
     for st in sts:
         fa.disposeEncodeStream(ctx, st)
     enc.close()
+
+
+@pytest.mark.parametrize("exact", [False, True])
+def test_layernorm_folded_into_skinny_gemms_is_bit_identical(ctx, fa, monkeypatch, exact):
+    """Stream passes fold norm_att / norm_conv / norm_ff2 into the skinny GEMMs
+    that consume them (the A rows normalised in the kernel with the
+    LayerNorm kernel's own sums and fma): the streamed frames are the bits of
+    the separate LayerNorm launches (FA_LN_FOLD=0), also with every operand
+    exact (the folded GEMM then builds the lo plane too)."""
+    cfg = fa.synth.small_stream_cfg(layers=2, right=0, chunk=2, left=8)
+    cfg = dict(cfg, D=1024, DFF=4096, H=8, HD=128)  # the fold needs K = D = 1024
+    man = fa.synth.make_weights(cfg, seed=13)
+    enc = fa.FusedEncoder(ctx, man, "f16", max_T=128, cfg=cfg)
+    if exact:
+        enc.setExact(31)
+    mel = fa.synth.make_features(cfg["melBins"], 320, seed=14)[0]
+    outs = []
+    for fold in ("1", "0"):
+        monkeypatch.setenv("FA_LN_FOLD", fold)
+        outs.append(_stream(ctx, fa, enc, mel, [16] * 20))
+    enc.close()
+    assert outs[0].shape == outs[1].shape
+    assert np.array_equal(outs[0], outs[1]), f"max diff {np.abs(outs[0] - outs[1]).max()}"
