@@ -321,9 +321,8 @@ __global__ __launch_bounds__(256) void enc_ln_kernel(const float *__restrict__ x
   for (int t = 0; t < V; t++) {
     const int j = lane + 64 * t;
     const f4 gm = gv[t], bt = bv[t];
-    // one rounding for the affine (fma), as the skinny GEMM's folded LayerNorm computes it
-    float o[4] = {__builtin_fmaf((v[t].x - mean) * inv, gm.x, bt.x), __builtin_fmaf((v[t].y - mean) * inv, gm.y, bt.y),
-                  __builtin_fmaf((v[t].z - mean) * inv, gm.z, bt.z), __builtin_fmaf((v[t].w - mean) * inv, gm.w, bt.w)};
+    float o[4] = {(v[t].x - mean) * inv * gm.x + bt.x, (v[t].y - mean) * inv * gm.y + bt.y, (v[t].z - mean) * inv * gm.z + bt.z,
+                  (v[t].w - mean) * inv * gm.w + bt.w};
     if constexpr (SILU) {
 #pragma unroll
       for (int e = 0; e < 4; e++) o[e] = silu_f(o[e]);
@@ -331,7 +330,6 @@ __global__ __launch_bounds__(256) void enc_ln_kernel(const float *__restrict__ x
     h4 hi, lo;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-      asm("" : "+v"(o[e]));  // the f32 value rounded once to f16 (no fma-with-conversion), as the folded skinny GEMM does
       hi[e] = (_Float16)o[e];
       lo[e] = (_Float16)(o[e] - (float)hi[e]);
     }

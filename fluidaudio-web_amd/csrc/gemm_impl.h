@@ -786,10 +786,10 @@ __global__ __launch_bounds__(64 * KS) void gemm_skinny_kernel(GemmArgs p) {
 // passes: the norm_att / norm_conv / norm_ff2 launches disappear).  The
 // workgroup first computes each row's mean and 1/std exactly as
 // enc_ln_kernel does (one wave per row, float4 per lane at lane + 64 t, the
-// same sums), then every A fragment is built from the f32 rows as
-// f16(fma((x - mean) * inv, gamma, beta)) (+ its exact lo plane), the values
-// the LayerNorm kernel stores.  K = 1024.
-__device__ __forceinline__ float ln_affine(float x, float mean, float inv, float g, float b) { return __builtin_fmaf((x - mean) * inv, g, b); }
+// same sums), then every A fragment is built from the f32 rows with the
+// LayerNorm kernel's expression f16((x - mean) * inv * gamma + beta) (+ its
+// exact lo plane).  K = 1024.
+__device__ __forceinline__ float ln_affine(float x, float mean, float inv, float g, float b) { return (x - mean) * inv * g + b; }
 
 template <int TI, int KS, int EPI, int LO>
 __global__ __launch_bounds__(64 * KS) void gemm_skinny_ln_kernel(GemmArgs p) {
@@ -862,8 +862,7 @@ __global__ __launch_bounds__(64 * KS) void gemm_skinny_ln_kernel(GemmArgs p) {
           h8 hi, lo;
 #pragma unroll
           for (int e = 0; e < 8; e++) {
-            float o = ln_affine(xx[e], mean[i], inv[i], gg[e], bb[e]);
-            asm("" : "+v"(o));  // rounded once to f16, as enc_ln_kernel stores it
+            const float o = ln_affine(xx[e], mean[i], inv[i], gg[e], bb[e]);  // enc_ln_kernel's expression
             hi[e] = (_Float16)o;
             lo[e] = (_Float16)(o - (float)hi[e]);
           }
