@@ -561,9 +561,13 @@ static napi_value js_encoder_forward_stream_batches(napi_env env, napi_callback_
     return throw_status(env, c, st);
   }
   napi_value arr;
-  NA(napi_create_array_with_length(env, (size_t)nb, &arr));
-  for (int b = 0; b < nb; b++) NA(napi_set_element(env, arr, (uint32_t)b, mkbig(env, outs[b])));
+  napi_status ok = napi_create_array_with_length(env, (size_t)nb, &arr);
+  for (int b = 0; b < nb && ok == napi_ok; b++) ok = napi_set_element(env, arr, (uint32_t)b, mkbig(env, outs[b]));
   free(outs);
+  if (ok != napi_ok) {
+    napi_throw_error(env, NULL, "encoderForwardStreamBatches: building the result array failed");
+    return NULL;
+  }
   return arr;
 }
 
