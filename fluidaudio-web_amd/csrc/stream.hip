@@ -154,7 +154,10 @@ bool next_pass(const fa_stream *st, PassPlan *p) {
   int n = st->subT == 0 ? (M + 7) / 8 - st->B : (M - 7 >= 0 ? (M - 7) / 8 : -1) - st->B;
   n = std::min(n, st->max_chunk);
   n -= ((n % st->C) + st->C) % st->C;
-  if (n < st->C) return false;
+  // the next pass reads kLookback mel rows before 8 * subT, so the first pass
+  // emits at least two frames (matters for one-frame chunks only; frames do not
+  // depend on where passes split the stream)
+  if (n < (st->subT == 0 ? std::max(st->C, 2) : st->C)) return false;
   p->nComp = n + st->B;
   p->nemit = n;
   p->m = st->subT == 0 ? 8 * p->nComp - 7 : 8 * p->nComp + 7;
@@ -168,7 +171,7 @@ void advance_fifo(fa_stream *st, int nemit) {
   const int MB = st->enc->cfg.melBins;
   st->subT += nemit;
   const long keep_from = 8L * st->subT - kLookback;
-  const long drop = keep_from - st->fifo_start;
+  const long drop = keep_from - st->fifo_start;  // >= 0: subT >= 2 after the first pass
   st->fifo.erase(st->fifo.begin(), st->fifo.begin() + (size_t)drop * MB);
   st->fifo_start = keep_from;
 }
@@ -181,6 +184,7 @@ int run_group(fa_ctx *ctx, fa_encoder *e, StreamLane *L, fa_stream *const *sts, 
   const int MB = c.melBins, D = c.D, m = pl.m, nComp = pl.nComp, nemit = pl.nemit;
   fa_stream *s0 = sts[0];
   if (n < 1 || n > kMaxStreamGroup) return set_err(ctx, FA_E_INVALID, "stream pass: %d streams in one pass", n);
+  if (D % 4) return set_err(ctx, FA_E_UNSUPPORTED, "stream pass: D %d not a multiple of 4", D);
   std::vector<int32_t> lens(n, m);
   PassGeom g;
   FA_TRY(pass_geometry(ctx, e, lens.data(), n, 0, pl.pt, pl.pb, &g));
@@ -274,18 +278,19 @@ int run_group(fa_ctx *ctx, fa_encoder *e, StreamLane *L, fa_stream *const *sts, 
   } else {
     FA_TRY(launch());
   }
+  // the pass is queued: every window's caches moved to the other buffer half
+  for (int w = 0; w < n; w++) {
+    sts[w]->cur ^= 1;
+    sts[w]->Lc = sp.keep;
+  }
   OutRows orows{};
   for (int w = 0; w < n; w++) {
-    fa_stream *st = sts[w];
-    st->cur ^= 1;
-    st->Lc = sp.keep;
     fa_tensor o;
     TensorRec *ro;
     FA_TRY(new_tensor(ctx, nemit, D, S_F32, (size_t)nemit * D * 4, &o, &ro));
     orows.dst[w] = (float *)ro->ptr;
     outs[w]->push_back(o);
   }
-  if (D % 4) return set_err(ctx, FA_E_UNSUPPORTED, "stream pass: D %d not a multiple of 4", D);
   {
     ProfScope ps(ctx, "stream_out");
     const long n4 = (long)nemit * (D / 4);

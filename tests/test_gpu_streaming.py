@@ -79,9 +79,11 @@ def test_offline_chunked_causal_matches_np_ref(ctx, fa, npref):
     assert r_exact < 1e-4 and r_plain > 2 * r_exact
 
 
-@pytest.mark.parametrize("pieces", [[601], [37, 100, 5, 64, 95, 300], [16] * 38, [8] * 76])
-def test_stream_reproduces_offline_frames(ctx, fa, npref, pieces):
-    cfg, man, enc = _model(ctx, fa)
+@pytest.mark.parametrize("chunk,pieces", [(2, [601]), (2, [37, 100, 5, 64, 95, 300]), (2, [16] * 38), (2, [8] * 76), (1, [8] * 76), (1, [3, 9, 8, 200, 381])])
+def test_stream_reproduces_offline_frames(ctx, fa, npref, chunk, pieces):
+    """chunk 1 with 8-frame pieces: a first pass could finish one frame, and the
+    next pass reads 14 mel rows back; the stream waits for two."""
+    cfg, man, enc = _model(ctx, fa, chunk=chunk)
     mel = fa.synth.make_features(cfg["melBins"], sum(pieces), seed=6)[0]
     off = enc.encode([mel])[0]
     got = _stream(ctx, fa, enc, mel, pieces)
