@@ -1540,6 +1540,14 @@ static int encoder_forward_impl(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const
   fa_tensor ox;
   TensorRec *rx;
   FA_TRY(new_tensor(ctx, M, D, S_F32, (size_t)M * D * 4, &ox, &rx));
+  struct ReleaseOnError {  // the output is released unless the forward was queued
+    fa_ctx *c;
+    fa_tensor t;
+    bool keep = false;
+    ~ReleaseOnError() {
+      if (!keep) (void)fa_free_tensor(c, t);
+    }
+  } out_guard{ctx, ox};
   rm = get(ctx, mel);
   float *const xout = (float *)rx->ptr;
   auto set_src = [&]() -> int {
@@ -1551,6 +1559,7 @@ static int encoder_forward_impl(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const
   if (!use_graph) {  // profiling (its events are per launch) or FA_GRAPH=0
     if (stream) FA_TRY(set_src());
     FA_TRY(pass_launch(ctx, e, g, (const float *)rm->ptr, xout, layers, nullptr));
+    out_guard.keep = true;
     *out = ox;
     return FA_OK;
   }
@@ -1568,6 +1577,7 @@ static int encoder_forward_impl(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const
       [&]() { return pass_launch(ctx, e, g, stream ? nullptr : (const float *)e->W().melw, (float *)e->W().xw, layers, nullptr); },
       [&]() { return stream ? set_src() : copy_f4(ctx, rm->ptr, e->W().melw, (size_t)g.R[0] * MB * 4, "enc_in"); }));
   FA_TRY(copy_f4(ctx, e->W().xw, xout, (size_t)M * D * 4, "enc_out"));
+  out_guard.keep = true;
   *out = ox;
   return FA_OK;
 }
@@ -1950,6 +1960,7 @@ int fa_encoder_forward_stream_batches(fa_ctx *ctx, fa_encoder *e, fa_tensor feat
   const char *who = "encoderForwardStreamBatches";
   if (!e || e->ctx != ctx) return set_err(ctx, FA_E_INVALID, "%s: encoder belongs to another context", who);
   if (nb <= 0 || !starts || !lens || !counts || !outs) return set_err(ctx, FA_E_INVALID, "%s: no batches", who);
+  for (int b = 0; b < nb; b++) outs[b] = 0;
   for (int b = 0; b < nb; b++)
     if (counts[b] <= 0) return set_err(ctx, FA_E_INVALID, "%s: batch %d has %d windows", who, b, counts[b]);
   if (nb == 1) return encoder_forward_impl(ctx, e, feats, starts, 0, lens, counts[0], layout, layers_run, outs, who);
@@ -1983,6 +1994,12 @@ int fa_encoder_forward_stream_batches(fa_ctx *ctx, fa_encoder *e, fa_tensor feat
       (void)hipEventRecord(e->lane_done[l], e->lane_stream[l]);
       (void)hipStreamWaitEvent(home, e->lane_done[l], 0);
     }
+  if (st != FA_OK)  // no partial result: the batches already encoded are released
+    for (int b = 0; b < nb; b++)
+      if (outs[b]) {
+        (void)fa_free_tensor(ctx, outs[b]);
+        outs[b] = 0;
+      }
   return st;
 }
 

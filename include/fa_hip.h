@@ -390,7 +390,8 @@ int fa_encoder_forward_stream(fa_ctx *ctx, fa_encoder *enc, fa_tensor feats, con
  * Consecutive batches run on two workspace lanes with streams of their own,
  * so one batch's kernel tails and write-backs overlap the next batch's
  * kernels; the lanes start after the work queued on the context stream and
- * the context stream waits for both.  Replaces the loop over window groups
+ * the context stream waits for both.  On failure every outs[b] is 0 (batches
+ * already encoded are released).  Replaces the loop over window groups
  * of the reference's windowed transcription (pipeline.js:66-80). */
 int fa_encoder_forward_stream_batches(fa_ctx *ctx, fa_encoder *enc, fa_tensor feats, int nb, const int32_t *starts, const int32_t *lens,
                                       const int32_t *counts, int layout, int layers_run, fa_tensor *outs);

@@ -264,5 +264,18 @@ def test_forward_stream_batches_equal_one_batch_at_a_time(ctx, fa, small, monkey
     assert np.array_equal(ctx.download(y).reshape(y.rows, y.cols), want[4])
     with pytest.raises(Exception, match="no batches|windows"):
         enc.forwardStreamBatches(f, [(np.array([], np.int32), np.array([], np.int32))])
+    # a failing later batch releases the batches already encoded: repeated
+    # failing calls create no new buffers
+    # (inside an arena, where outputs come from the buffer pool)
+    bad = [batches[0], (np.array([T - 5], np.int32), np.array([10], np.int32))]
+    arena = ctx.pushArena()
+    with pytest.raises(Exception, match="outside"):
+        enc.forwardStreamBatches(f, bad)
+    ctx.memStatsStart()
+    for _ in range(3):
+        with pytest.raises(Exception, match="outside"):
+            enc.forwardStreamBatches(f, bad)
+    assert ctx.memStats()["created"] == 0
+    ctx.popArena(arena)
     ctx.freeTensor(f)
     enc.close()
