@@ -1540,14 +1540,7 @@ static int encoder_forward_impl(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const
   fa_tensor ox;
   TensorRec *rx;
   FA_TRY(new_tensor(ctx, M, D, S_F32, (size_t)M * D * 4, &ox, &rx));
-  struct ReleaseOnError {  // the output is released unless the forward was queued
-    fa_ctx *c;
-    fa_tensor t;
-    bool keep = false;
-    ~ReleaseOnError() {
-      if (!keep) (void)fa_free_tensor(c, t);
-    }
-  } out_guard{ctx, ox};
+  TensorGuard og(ctx, ox);  // released unless the forward is queued
   rm = get(ctx, mel);
   float *const xout = (float *)rx->ptr;
   auto set_src = [&]() -> int {
@@ -1559,8 +1552,7 @@ static int encoder_forward_impl(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const
   if (!use_graph) {  // profiling (its events are per launch) or FA_GRAPH=0
     if (stream) FA_TRY(set_src());
     FA_TRY(pass_launch(ctx, e, g, (const float *)rm->ptr, xout, layers, nullptr));
-    out_guard.keep = true;
-    *out = ox;
+    *out = og.release();
     return FA_OK;
   }
   // The whole forward is a fixed kernel sequence for a given signature: it is
@@ -1577,8 +1569,7 @@ static int encoder_forward_impl(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const
       [&]() { return pass_launch(ctx, e, g, stream ? nullptr : (const float *)e->W().melw, (float *)e->W().xw, layers, nullptr); },
       [&]() { return stream ? set_src() : copy_f4(ctx, rm->ptr, e->W().melw, (size_t)g.R[0] * MB * 4, "enc_in"); }));
   FA_TRY(copy_f4(ctx, e->W().xw, xout, (size_t)M * D * 4, "enc_out"));
-  out_guard.keep = true;
-  *out = ox;
+  *out = og.release();
   return FA_OK;
 }
 

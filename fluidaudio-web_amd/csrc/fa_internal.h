@@ -109,6 +109,25 @@ int new_tensor(fa_ctx *ctx, int rows, int cols, int kind, size_t bytes, fa_tenso
 int new_persistent(fa_ctx *ctx, int rows, int cols, int kind, size_t bytes, fa_tensor *out, TensorRec **rec = nullptr);
 void *dev_alloc(fa_ctx *ctx, size_t bytes);  // raw hipMalloc, nullptr on failure (error set)
 
+// A freshly allocated output tensor, freed when the scope ends unless
+// release() handed it to the caller: an op that fails after allocating its
+// output leaves nothing behind.
+struct TensorGuard {
+  fa_ctx *ctx;
+  fa_tensor t;
+  TensorGuard(fa_ctx *c, fa_tensor x) : ctx(c), t(x) {}
+  TensorGuard(const TensorGuard &) = delete;
+  TensorGuard &operator=(const TensorGuard &) = delete;
+  ~TensorGuard() {
+    if (t) (void)fa_free_tensor(ctx, t);
+  }
+  fa_tensor release() {
+    const fa_tensor r = t;
+    t = 0;
+    return r;
+  }
+};
+
 // ── launch bracketing for the profiler ────────────────────────────────────
 // A ProfScope opened around a launch claims a (start, stop) event pair when a
 // profile is open for its label.  FA_LAUNCH hands the pair to

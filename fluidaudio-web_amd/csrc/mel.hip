@@ -416,9 +416,10 @@ int fa_mel_windows(fa_ctx *ctx, fa_tensor pcm, const int32_t *starts, const int3
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, n_mels, (int)total, S_F32, (size_t)n_mels * total * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rp = get(ctx, pcm);
   if (total == 0) {
-    *out = o;
+    *out = og.release();
     return FA_OK;
   }
   const size_t sbytes = (size_t)std::min(n, kMaxWin) * n_mels * 2 * sizeof(double);
@@ -437,7 +438,7 @@ int fa_mel_windows(fa_ctx *ctx, fa_tensor pcm, const int32_t *starts, const int3
   const int *bounds = (const int *)((const char *)ctx->mel_tab + kTabFb + (size_t)n_mels * kBins * 4);
   FA_TRY(mel_launch(ctx, (const float *)rp->ptr, nsamp, starts, lens, n, n_mels, log_guard, normalize, total, (float *)ro->ptr, tab, fb, bounds,
                     (double *)ctx->mel_scratch));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 

@@ -381,6 +381,7 @@ static int matmul_impl(fa_ctx *ctx, fa_tensor a, fa_tensor b, fa_tensor bias, in
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, M, N, S_F32, (size_t)M * N * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   ra = get(ctx, a); rb = get(ctx, b); rbias = bias ? get(ctx, bias) : nullptr; radd = add ? get(ctx, add) : nullptr;  // recs may move
   if (ra->kind == S_F16RM && (rb->kind != S_F16KM || K % 64)) return set_err(ctx, FA_E_UNSUPPORTED, "matmul: f16 A needs an f16 B and K %% 64 == 0");
   if (rb->kind == S_F16KM) {
@@ -400,7 +401,7 @@ static int matmul_impl(fa_ctx *ctx, fa_tensor a, fa_tensor b, fa_tensor bias, in
   } else {
     return set_err(ctx, FA_E_INVALID, "matmul: B must be an f32 or f16 tensor");
   }
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -421,6 +422,7 @@ int fa_matmul_pair(fa_ctx *ctx, fa_tensor a_hi, fa_tensor a_lo, fa_tensor b, fa_
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, M, N, S_F32, (size_t)M * N * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rh = get(ctx, a_hi); rl = get(ctx, a_lo); rb = get(ctx, b); rbias = bias ? get(ctx, bias) : nullptr; radd = add ? get(ctx, add) : nullptr;
   GemmArgs p;
   p.A = rh->ptr; p.Alo = rl->ptr; p.lda = K; p.akind = A_F16;
@@ -429,7 +431,7 @@ int fa_matmul_pair(fa_ctx *ctx, fa_tensor a_hi, fa_tensor a_lo, fa_tensor b, fa_
   p.bias = CF32(rbias); p.add = CF32(radd); p.ldadd = N;
   p.M = M; p.N = N; p.K = K;
   FA_TRY(gemm_mfma(ctx, p, "matmul_pair"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -457,6 +459,7 @@ int fa_matmul_int8(fa_ctx *ctx, fa_tensor a, fa_tensor wq, fa_tensor scale, int 
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, M, N, S_F32, (size_t)M * N * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   ra = get(ctx, a); rw = get(ctx, wq); rs = get(ctx, scale); rbias = bias ? get(ctx, bias) : nullptr;
   if (M <= 64 || K % 64 != 0) {
     FA_TRY(gemv_quant_launch(ctx, F32(ra), rw->aux, F32(rs), 1, M, N, K, F32(ro), CF32(rbias), act, "matmulInt8_gemv"));
@@ -470,7 +473,7 @@ int fa_matmul_int8(fa_ctx *ctx, fa_tensor a, fa_tensor wq, fa_tensor scale, int 
     p.M = M; p.N = N; p.K = K;
     FA_TRY(gemm_mfma(ctx, p, "matmulInt8"));
   }
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -488,6 +491,7 @@ int fa_matmul_nbits(fa_ctx *ctx, fa_tensor a, fa_tensor bq, fa_tensor scales, fa
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, M, N, S_F32, (size_t)M * N * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   if ((long)rs->rows * rs->cols < (long)N * nblk || rz->bytes < (size_t)N * zpb) return set_err(ctx, FA_E_INVALID, "matmulNBits: scales / zero points too small");
   // The reference's kernel dequantises in f32 (arbitrary f32 block scales and
   // zero points): the weights are expanded to f32 [K, N] once per call and
@@ -496,6 +500,7 @@ int fa_matmul_nbits(fa_ctx *ctx, fa_tensor a, fa_tensor bq, fa_tensor scales, fa
   fa_tensor tw;
   TensorRec *rw;
   FA_TRY(new_tensor(ctx, K, N, S_F32, (size_t)K * N * 4, &tw, &rw));
+  TensorGuard tg(ctx, tw);  // the f32 weights live for this call only
   ra = get(ctx, a); rq = get(ctx, bq); rs = get(ctx, scales); rz = get(ctx, zp); ro = get(ctx, o);
   {
     ProfScope ps(ctx, "matmulNBits_dequant");
@@ -504,8 +509,7 @@ int fa_matmul_nbits(fa_ctx *ctx, fa_tensor a, fa_tensor bq, fa_tensor scales, fa
     FA_TRY(check_launch(ctx, "matmulNBits_dequant"));
   }
   FA_TRY(gemm_f32(ctx, F32(ra), F32(rw), F32(ro), nullptr, nullptr, M, N, K, 0, "matmulNBits"));
-  FA_TRY(fa_free_tensor(ctx, tw));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -520,9 +524,10 @@ int fa_layernorm(fa_ctx *ctx, fa_tensor x, fa_tensor gamma, fa_tensor beta, floa
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, R, Cc, S_F32, (size_t)R * Cc * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rx = get(ctx, x); rg = get(ctx, gamma); rb = get(ctx, beta);
   FA_TRY(layernorm_launch(ctx, F32(rx), F32(rg), F32(rb), ro->ptr, 0, R, Cc, Cc, Cc, eps, "layernorm"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -534,11 +539,12 @@ int fa_softmax(fa_ctx *ctx, fa_tensor x, fa_tensor *out) {
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, R, Cc, S_F32, (size_t)R * Cc * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rx = get(ctx, x);
   ProfScope ps(ctx, "softmax");
   if (R) FA_LAUNCH(ps, softmax_kernel, dim3(cdiv(R, 4)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), R, Cc);
   FA_TRY(check_launch(ctx, "softmax"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -550,11 +556,12 @@ static int unary(fa_ctx *ctx, fa_tensor x, int kind, float s, fa_tensor *out, co
   TensorRec *ro;
   const long n = (long)rx->rows * rx->cols;
   FA_TRY(new_tensor(ctx, rx->rows, rx->cols, S_F32, (size_t)n * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rx = get(ctx, x);
   ProfScope ps(ctx, name);
   if (n) FA_LAUNCH(ps, unary_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), n, kind, s);
   FA_TRY(check_launch(ctx, name));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 int fa_scale(fa_ctx *ctx, fa_tensor x, float s, fa_tensor *out) { return unary(ctx, x, 0, s, out, "scale"); }
@@ -574,11 +581,12 @@ int fa_ewise(fa_ctx *ctx, fa_tensor a, fa_tensor b, int op, fa_tensor *out) {
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, ra->rows, ra->cols, S_F32, (size_t)n * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   ra = get(ctx, a); rb = get(ctx, b);
   ProfScope ps(ctx, "ewise");
   if (n) FA_LAUNCH(ps, ewise_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, F32(ra), F32(rb), F32(ro), n, ra->cols, bcast, op ? 1 : 0);
   FA_TRY(check_launch(ctx, "ewise"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -591,11 +599,12 @@ int fa_glu(fa_ctx *ctx, fa_tensor x, fa_tensor *out) {
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, C, T, S_F32, (size_t)C * T * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rx = get(ctx, x);
   ProfScope ps(ctx, "glu");
   if ((long)C * T) FA_LAUNCH(ps, glu_kernel, dim3(gs((long)C * T)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), C, T);
   FA_TRY(check_launch(ctx, "glu"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -607,11 +616,12 @@ int fa_transpose(fa_ctx *ctx, fa_tensor x, fa_tensor *out) {
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, Cc, R, S_F32, (size_t)R * Cc * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rx = get(ctx, x);
   ProfScope ps(ctx, "transpose");
   if ((long)R * Cc) FA_LAUNCH(ps, transpose_kernel, dim3(cdiv(Cc, 32), cdiv(R, 32)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), R, Cc);
   FA_TRY(check_launch(ctx, "transpose"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -623,12 +633,13 @@ int fa_slice_cols(fa_ctx *ctx, fa_tensor x, int col0, int width, fa_tensor *out)
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, rx->rows, width, S_F32, (size_t)rx->rows * width * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rx = get(ctx, x);
   const long n = (long)rx->rows * width;
   ProfScope ps(ctx, "sliceCols");
   if (n) FA_LAUNCH(ps, slice_cols_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), rx->rows, rx->cols, col0, width);
   FA_TRY(check_launch(ctx, "sliceCols"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -653,9 +664,10 @@ int fa_slice_rows(fa_ctx *ctx, fa_tensor x, int row0, int count, fa_tensor *out)
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, count, rx->cols, S_F32, (size_t)count * rx->cols * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rx = get(ctx, x);
   if (count) FA_HIP(ctx, hipMemcpyAsync(ro->ptr, F32(rx) + (size_t)row0 * rx->cols, (size_t)count * rx->cols * 4, hipMemcpyDeviceToDevice, ctx->stream));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -685,6 +697,7 @@ int fa_concat_rows(fa_ctx *ctx, const fa_tensor *ts, int n, fa_tensor *out) {
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, rows, cols, S_F32, (size_t)rows * cols * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   size_t off = 0;
   for (int i = 0; i < n; i++) {
     TensorRec *r = get(ctx, ts[i]);
@@ -693,7 +706,7 @@ int fa_concat_rows(fa_ctx *ctx, const fa_tensor *ts, int n, fa_tensor *out) {
     if (nb) FA_HIP(ctx, hipMemcpyAsync((char *)ro->ptr + off, r->ptr, nb, hipMemcpyDeviceToDevice, ctx->stream));
     off += nb;
   }
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -705,12 +718,13 @@ int fa_sub_reshape(fa_ctx *ctx, fa_tensor x, int C, int Tsub, int F, fa_tensor *
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, Tsub, C * F, S_F32, (size_t)Tsub * C * F * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rx = get(ctx, x);
   const long n = (long)Tsub * C * F;
   ProfScope ps(ctx, "subReshape");
   if (n) FA_LAUNCH(ps, sub_reshape_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), C, Tsub, F);
   FA_TRY(check_launch(ctx, "subReshape"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -723,11 +737,12 @@ int fa_row_bias_act(fa_ctx *ctx, fa_tensor x, fa_tensor bias, int act, fa_tensor
   TensorRec *ro;
   const long n = (long)rx->rows * rx->cols;
   FA_TRY(new_tensor(ctx, rx->rows, rx->cols, S_F32, (size_t)n * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rx = get(ctx, x); rb = get(ctx, bias);
   ProfScope ps(ctx, "rowBiasAct");
   if (n) FA_LAUNCH(ps, row_bias_act_kernel, dim3(gs(n)), dim3(256), 0, ctx->stream, F32(rx), F32(rb), F32(ro), rx->rows, rx->cols, act);
   FA_TRY(check_launch(ctx, "rowBiasAct"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -762,12 +777,13 @@ static int conv1d_impl(fa_ctx *ctx, fa_tensor x, fa_tensor w, int cout, int k, f
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, cout, Lout, S_F32, (size_t)cout * Lout * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rx = get(ctx, x); rw = get(ctx, w); rb = bias ? get(ctx, bias) : nullptr;
   ProfScope ps(ctx, "conv1d");
   FA_LAUNCH(ps, conv1d_kernel, dim3(gs((long)cout * Lout)), dim3(256), 0, ctx->stream, F32(rx), F32(rw), CF32(rb), F32(ro), cout, Cin, L, Lout,
                      k, stride, pad_left, dilation, groups, act);
   FA_TRY(check_launch(ctx, "conv1d"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -785,12 +801,13 @@ int fa_conv2d(fa_ctx *ctx, fa_tensor x, fa_tensor w, int cout, int cin, int h, i
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, cout, Ho * Wo, S_F32, (size_t)cout * Ho * Wo * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rx = get(ctx, x); rw = get(ctx, w); rb = bias ? get(ctx, bias) : nullptr;
   ProfScope ps(ctx, "conv2d");
   FA_LAUNCH(ps, conv2d_kernel, dim3(gs((long)cout * Ho * Wo)), dim3(256), 0, ctx->stream, F32(rx), F32(rw), CF32(rb), F32(ro), cout, cin, h, wd,
                      Ho, Wo, kh, kw, sh, sw, pt, pl, groups, act);
   FA_TRY(check_launch(ctx, "conv2d"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -805,12 +822,13 @@ int fa_bmm_qk(fa_ctx *ctx, fa_tensor q, fa_tensor b, fa_tensor qb, int H, int HD
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, W * H * T, Tb, S_F32, (size_t)W * H * T * Tb * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rq = get(ctx, q); rb = get(ctx, b); rqb = qb ? get(ctx, qb) : nullptr;
   ProfScope ps(ctx, "bmmQK");
   FA_LAUNCH(ps, bmm_qk_kernel, dim3(gs((long)W * H * T * Tb)), dim3(256), 0, ctx->stream, F32(rq), F32(rb), CF32(rqb), F32(ro), T, Tb, H, HD, W,
                      b_shared);
   FA_TRY(check_launch(ctx, "bmmQK"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -824,11 +842,12 @@ int fa_bmm_pv(fa_ctx *ctx, fa_tensor p, fa_tensor v, int H, int HD, int W, fa_te
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, W * Tq, H * HD, S_F32, (size_t)W * Tq * H * HD * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rp = get(ctx, p); rv = get(ctx, v);
   ProfScope ps(ctx, "bmmPV");
   FA_LAUNCH(ps, bmm_pv_kernel, dim3(gs((long)W * Tq * H * HD)), dim3(256), 0, ctx->stream, F32(rp), F32(rv), F32(ro), Tq, Tk, H, HD, W);
   FA_TRY(check_launch(ctx, "bmmPV"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -841,11 +860,12 @@ int fa_rel_shift_b(fa_ctx *ctx, fa_tensor x, int H, fa_tensor *out) {
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, H * t, t, S_F32, (size_t)H * t * t * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rx = get(ctx, x);
   ProfScope ps(ctx, "relShiftB");
   if ((long)H * t * t) FA_LAUNCH(ps, relshift_kernel, dim3(gs((long)H * t * t)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), t, H);
   FA_TRY(check_launch(ctx, "relShiftB"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -862,13 +882,14 @@ int fa_rel_shift_stream(fa_ctx *ctx, fa_tensor x, int H, int n, int Lk, int dMax
   TensorRec *ro;
   const long total = (long)H * n * Lk;
   FA_TRY(new_tensor(ctx, H * n, Lk, S_F32, (size_t)total * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rx = get(ctx, x);
   ProfScope ps(ctx, "relShiftStream");
   if (total)
     FA_LAUNCH(ps, relshift_stream_kernel, dim3(gs(total)), dim3(256), 0, ctx->stream, F32(rx), F32(ro), total, n, Lk, rx->cols, dMax, Lc, subT, C,
               left, right);
   FA_TRY(check_launch(ctx, "relShiftStream"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -888,6 +909,7 @@ int fa_attn_fused(fa_ctx *ctx, fa_tensor q, fa_tensor k, fa_tensor v, fa_tensor 
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, rq->rows, H * HD, S_F32, (size_t)rq->rows * H * HD * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rq = get(ctx, q); rk = get(ctx, k); rv = get(ctx, v); rp = get(ctx, pos); ru = get(ctx, pbu); rw = get(ctx, pbv);
   AttnArgs a;
   a.q = rq->ptr; a.k = rk->ptr; a.v = rv->ptr;
@@ -904,7 +926,7 @@ int fa_attn_fused(fa_ctx *ctx, fa_tensor q, fa_tensor k, fa_tensor v, fa_tensor 
     }
     FA_TRY(relpos_attention(ctx, a, 1, 1, T, "attnFused"));
   }
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -916,11 +938,12 @@ int fa_dequant_int8(fa_ctx *ctx, fa_tensor wq, fa_tensor scale, int K, int N, fa
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, K, N, S_F32, (size_t)K * N * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rw = get(ctx, wq); rs = get(ctx, scale);
   ProfScope ps(ctx, "dequantInt8");
   FA_LAUNCH(ps, dequant_i8_kernel, dim3(gs((long)K * N)), dim3(256), 0, ctx->stream, (const int8_t *)rw->ptr, F32(rs), F32(ro), K, N);
   FA_TRY(check_launch(ctx, "dequantInt8"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -933,11 +956,12 @@ int fa_dequant_int4(fa_ctx *ctx, fa_tensor bq, fa_tensor scales_f16, int K, int 
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, K, N, S_F32, (size_t)K * N * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rq = get(ctx, bq); rs = get(ctx, scales_f16);
   ProfScope ps(ctx, "dequantInt4");
   FA_LAUNCH(ps, dequant_i4_kernel, dim3(gs((long)K * N)), dim3(256), 0, ctx->stream, (const uint8_t *)rq->ptr, (const _Float16 *)rs->ptr, F32(ro), K, N);
   FA_TRY(check_launch(ctx, "dequantInt4"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 

@@ -261,12 +261,13 @@ int fa_leaky_relu(fa_ctx *ctx, fa_tensor x, double slope, fa_tensor *out) {
   FA_TRY(need32(ctx, x, &rx, "leakyRelu"));
   fa_tensor o;
   FA_TRY(out32(ctx, rx->rows, rx->cols, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rx = get(ctx, x);
   const long n = (long)rx->rows * rx->cols;
   ProfScope ps(ctx, "leakyRelu");
   if (n) FA_LAUNCH(ps, leaky_relu_kernel, dim3(grid_of(n)), dim3(256), 0, ctx->stream, F32P(rx), F32P(ro), n, slope);
   FA_TRY(check_launch(ctx, "leakyRelu"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -277,12 +278,13 @@ int fa_snake(fa_ctx *ctx, fa_tensor x, fa_tensor alpha, fa_tensor *out) {
   if ((long)ra->rows * ra->cols < rx->rows) return set_err(ctx, FA_E_INVALID, "snake: alpha has %d values, x has %d rows", ra->rows * ra->cols, rx->rows);
   fa_tensor o;
   FA_TRY(out32(ctx, rx->rows, rx->cols, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rx = get(ctx, x); ra = get(ctx, alpha);
   const long n = (long)rx->rows * rx->cols;
   ProfScope ps(ctx, "snake");
   if (n) FA_LAUNCH(ps, snake_kernel, dim3(grid_of(n)), dim3(256), 0, ctx->stream, F32P(rx), F32P(ra), F32P(ro), rx->rows, rx->cols);
   FA_TRY(check_launch(ctx, "snake"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -295,11 +297,12 @@ int fa_adain(fa_ctx *ctx, fa_tensor x, fa_tensor scale, fa_tensor shift, double 
   if (rx->cols <= 0) return set_err(ctx, FA_E_INVALID, "adain: empty rows");
   fa_tensor o;
   FA_TRY(out32(ctx, rx->rows, rx->cols, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rx = get(ctx, x); rs = get(ctx, scale); rh = get(ctx, shift);
   ProfScope ps(ctx, "adain");
   if (rx->rows) FA_LAUNCH(ps, adain_kernel, dim3(rx->rows), dim3(256), 0, ctx->stream, F32P(rx), F32P(rs), F32P(rh), F32P(ro), rx->cols, eps);
   FA_TRY(check_launch(ctx, "adain"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -312,12 +315,13 @@ int fa_im2col(fa_ctx *ctx, fa_tensor x, int k, int stride, int pad, int dilation
   if (Lout <= 0) return set_err(ctx, FA_E_INVALID, "im2col: empty output");
   fa_tensor o;
   FA_TRY(out32(ctx, Cin * k, Lout, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rx = get(ctx, x);
   const long n = (long)Cin * k * Lout;
   ProfScope ps(ctx, "im2col");
   FA_LAUNCH(ps, im2col_kernel, dim3(grid_of(n)), dim3(256), 0, ctx->stream, F32P(rx), F32P(ro), Cin, L, k, Lout, stride, pad, dilation);
   FA_TRY(check_launch(ctx, "im2col"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -336,12 +340,13 @@ int fa_conv_transpose1d(fa_ctx *ctx, fa_tensor x, fa_tensor w, int cout, int k, 
   if (Lout <= 0) return set_err(ctx, FA_E_INVALID, "convTranspose1d: empty output");
   fa_tensor o;
   FA_TRY(out32(ctx, cout, Lout, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rx = get(ctx, x); rw = get(ctx, w); rb = bias ? get(ctx, bias) : nullptr;
   ProfScope ps(ctx, "convTranspose1d");
   FA_LAUNCH(ps, conv_transpose1d_kernel, dim3(grid_of((long)cout * Lout)), dim3(256), 0, ctx->stream, F32P(rx), F32P(rw), CF32P(rb), F32P(ro), Cin, L,
             cout, k, Lout, stride, pad, dilation, groups, act);
   FA_TRY(check_launch(ctx, "convTranspose1d"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -353,6 +358,7 @@ int fa_gather_cols(fa_ctx *ctx, fa_tensor x, const uint32_t *idx, int n_idx, fa_
     if (idx[f] >= (uint32_t)rx->cols) return set_err(ctx, FA_E_INVALID, "gatherCols: index %u at %d outside %d columns", idx[f], f, rx->cols);
   fa_tensor o, ti;
   FA_TRY(out32(ctx, rx->rows, n_idx, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   FA_TRY(new_tensor(ctx, 1, n_idx, S_BYTES, (size_t)n_idx * 4, &ti, &ri));
   FA_HIP(ctx, hipMemcpyAsync(ri->ptr, idx, (size_t)n_idx * 4, hipMemcpyHostToDevice, ctx->stream));
   FA_HIP(ctx, hipStreamSynchronize(ctx->stream));  // the host index array may go away when this call returns
@@ -362,7 +368,7 @@ int fa_gather_cols(fa_ctx *ctx, fa_tensor x, const uint32_t *idx, int n_idx, fa_
   if (n) FA_LAUNCH(ps, gather_cols_kernel, dim3(grid_of(n)), dim3(256), 0, ctx->stream, F32P(rx), (const uint32_t *)ri->ptr, F32P(ro), rx->rows, rx->cols, n_idx);
   FA_TRY(check_launch(ctx, "gatherCols"));
   FA_TRY(fa_free_tensor(ctx, ti));  // pooled storage: later allocations follow on the same stream
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -378,13 +384,14 @@ int fa_lstm(fa_ctx *ctx, fa_tensor x, fa_tensor w, fa_tensor r, fa_tensor b, int
     return set_err(ctx, FA_E_INVALID, "lstm: W/R/B smaller than [2,4H,%d] / [2,4H,H] / [2,8H]", inp);
   fa_tensor o;
   FA_TRY(out32(ctx, seq, 2 * hid, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rx = get(ctx, x); rw = get(ctx, w); rr = get(ctx, r); rb = get(ctx, b);
   const size_t smem = (size_t)4 * hid * 8 + (size_t)2 * hid * 4;
   ProfScope ps(ctx, "lstm");
   if (seq) FA_LAUNCH(ps, lstm_kernel, dim3(2), dim3(std::max(64, (4 * hid + 63) / 64 * 64)), smem, ctx->stream, F32P(rx), F32P(rw), F32P(rr), F32P(rb), F32P(ro),
                      seq, inp, hid);
   FA_TRY(check_launch(ctx, "lstm"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -396,11 +403,12 @@ int fa_jbatch(fa_ctx *ctx, fa_tensor enc, int base, int B, fa_tensor pred, int h
     return set_err(ctx, FA_E_INVALID, "jbatch: rows [%d, %d) x %d outside the inputs", base, base + B, hid);
   fa_tensor o;
   FA_TRY(out32(ctx, B, hid, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   re = get(ctx, enc); rp = get(ctx, pred);
   ProfScope ps(ctx, "jbatch");
   FA_LAUNCH(ps, jbatch_kernel, dim3(grid_of((long)B * hid)), dim3(256), 0, ctx->stream, F32P(re), F32P(rp), F32P(ro), base, B, hid);
   FA_TRY(check_launch(ctx, "jbatch"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -411,11 +419,12 @@ int fa_argmax_rows(fa_ctx *ctx, fa_tensor x, int B, int vocab, int logits, fa_te
     return set_err(ctx, FA_E_INVALID, "argmaxRows: %d rows of %d logits (vocab %d) outside the input", B, logits, vocab);
   fa_tensor o;
   FA_TRY(out32(ctx, B, 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rx = get(ctx, x);
   ProfScope ps(ctx, "argmaxRows");
   FA_LAUNCH(ps, argmax_rows_kernel, dim3(B), dim3(256), 0, ctx->stream, F32P(rx), F32P(ro), vocab, logits);
   FA_TRY(check_launch(ctx, "argmaxRows"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -432,13 +441,14 @@ int fa_joint_argmax(fa_ctx *ctx, fa_tensor enc, int frame, int count, fa_tensor 
     return set_err(ctx, FA_E_INVALID, "jointArgmax: frames [%d, %d), hidden %d, logits %d outside the inputs", frame, frame + count, hidden, logits);
   fa_tensor o;
   FA_TRY(out32(ctx, count, 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   re = get(ctx, enc); rp = get(ctx, pred); rw = get(ctx, outW); rb = get(ctx, outB);
   const size_t smem = (size_t)hidden * 4;
   ProfScope ps(ctx, "jointArgmax");
   FA_LAUNCH(ps, joint_argmax_kernel, dim3(count), dim3(256), smem, ctx->stream, F32P(re), F32P(rp), F32P(rw), F32P(rb), F32P(ro), frame, hidden, vocab,
             logits);
   FA_TRY(check_launch(ctx, "jointArgmax"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 

@@ -86,6 +86,7 @@ int fa_pack_windows(fa_ctx *ctx, fa_tensor feats, const int32_t *starts, const i
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, (int)rows, MB, S_F32, (size_t)rows * MB * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   rf = get(ctx, feats);
   ProfScope ps(ctx, "pack_windows", n <= kMaxWin);
   for (int w0 = 0; w0 < n; w0 += kMaxWin) {
@@ -105,7 +106,7 @@ int fa_pack_windows(fa_ctx *ctx, fa_tensor feats, const int32_t *starts, const i
                        layout == 1 ? mx : 0, (float *)ro->ptr);
     FA_TRY(check_launch(ctx, "pack_windows"));
   }
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 

@@ -259,9 +259,10 @@ extern "C" int fa_gemv_quant(fa_ctx *ctx, fa_tensor a, fa_tensor w, fa_tensor sc
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, M, N, S_F32, (size_t)M * N * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   ra = get(ctx, a); rw = get(ctx, w); rs = get(ctx, scales);
   FA_TRY(gemv_quant_launch(ctx, (const float *)ra->ptr, rw->ptr, rs->ptr, format, M, N, K, (float *)ro->ptr, nullptr, 0, format == 1 ? "gemv_int8" : "gemv_int4"));
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }
 
@@ -288,6 +289,7 @@ extern "C" int fa_gemv_quant_batch(fa_ctx *ctx, int count, const fa_tensor *a, c
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, count * M, N, S_F32, (size_t)count * M * N * 4, &o, &ro));
+  TensorGuard og(ctx, o);  // released unless the op completes
   float *Y = (float *)ro->ptr;
   GemvArgs base{nullptr, M, K, N, nullptr, nullptr, nullptr, 0, nullptr, nullptr, 0};
   const char *label = format == 1 ? "gemv_batch_int8" : "gemv_batch_int4";
@@ -306,6 +308,6 @@ extern "C" int fa_gemv_quant_batch(fa_ctx *ctx, int count, const fa_tensor *a, c
       FA_LAUNCH(ps, gemv_batch_kernel<2>, grid, dim3(64 * kGemvWaves), gemv_lds(K), ctx->stream, base, b);
     FA_TRY(check_launch(ctx, label));
   }
-  *out = o;
+  *out = og.release();
   return FA_OK;
 }

@@ -176,3 +176,34 @@ def test_rel_shift_stream_matches_oracle(ctx, orc):
         opts = dict(H=H, n=n, Lk=Lk, dMax=dMax, Lc=Lc, subT=subT, C=C, left=left, right=right)
         got = dl(ctx, ctx.relShiftStream(ctx.upload(x, H * n, P), opts))
         assert np.array_equal(got, orc.relshift_stream(x, H, n, Lk, dMax, Lc, subT, C, left, right)), opts
+
+
+def test_ops_failing_after_allocation_release_their_output(ctx):
+    """An op that rejects its inputs after allocating its output releases it:
+    repeated failing calls inside an arena draw no new buffers from the device.
+    matmul (f16 activations with f32 weights) and matmulNBits (scales too
+    small) check those inputs only once the output exists."""
+    rng = np.random.default_rng(3)
+    a16 = ctx.allocF16(64, 128)
+    b32 = ctx.upload(rng.standard_normal((128, 64)).astype(np.float32), 128, 64)
+    a32 = ctx.upload(rng.standard_normal((8, 64)).astype(np.float32), 8, 64)
+    N, nblk = 32, 2
+    bq = ctx.uploadBytes(np.zeros(N * nblk * 16, np.uint8))
+    small = ctx.upload(np.ones((1, 4), np.float32), 1, 4)
+    zp = ctx.uploadBytes(np.full(N, 0x88, np.uint8))
+    arena = ctx.pushArena()
+
+    def fail_both():
+        with pytest.raises(Exception, match="f16 B"):
+            ctx.matmul(a16, b32)
+        with pytest.raises(Exception, match="too small"):
+            ctx.matmulNBits(a32, bq, small, zp, N)
+
+    fail_both()
+    ctx.memStatsStart()
+    for _ in range(3):
+        fail_both()
+    assert ctx.memStats()["created"] == 0
+    ctx.popArena(arena)
+    for t in (a16, b32, a32, bq, small, zp):
+        ctx.freeTensor(t)
