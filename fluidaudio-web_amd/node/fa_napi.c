@@ -76,14 +76,21 @@ static napi_value mkbig(napi_env env, uint64_t x) {
   napi_create_bigint_uint64(env, x, &r);
   return r;
 }
+static size_t typed_el(napi_typedarray_type t) {
+  switch (t) {
+    case napi_float32_array: case napi_int32_array: case napi_uint32_array: return 4;
+    case napi_uint16_array: case napi_int16_array: return 2;
+    case napi_float64_array: case napi_bigint64_array: case napi_biguint64_array: return 8;
+    default: return 1;
+  }
+}
 static void *typed(napi_env env, napi_value v, size_t *len_bytes) {
   napi_typedarray_type t;
   size_t len, off;
   void *data;
   napi_value ab;
   if (napi_get_typedarray_info(env, v, &t, &len, &data, &ab, &off) != napi_ok) return NULL;
-  size_t el = (t == napi_float32_array || t == napi_int32_array || t == napi_uint32_array) ? 4 : (t == napi_uint16_array || t == napi_int16_array) ? 2 : (t == napi_float64_array) ? 8 : 1;
-  if (len_bytes) *len_bytes = len * el;
+  if (len_bytes) *len_bytes = len * typed_el(t);
   return data;
 }
 
@@ -96,7 +103,7 @@ static void *typed_as(napi_env env, napi_value v, napi_typedarray_type want, siz
   void *data;
   napi_value ab;
   if (napi_get_typedarray_info(env, v, &t, &len, &data, &ab, &off) != napi_ok || t != want) return NULL;
-  if (len_bytes) *len_bytes = len * (want == napi_float64_array ? 8 : (want == napi_uint8_array || want == napi_int8_array) ? 1 : 4);
+  if (len_bytes) *len_bytes = len * typed_el(t);
   return data;
 }
 
