@@ -680,12 +680,44 @@ __global__ __launch_bounds__(256) void stream_attn_kernel(const _Float16 *__rest
   _Float16 *kc_out = keep > 0 ? slots.kc_out[w] + kvo : nullptr, *vc_out = slots.vc_out[w] + kvo;
   const int i = blockIdx.x * 4 + wave;
   const int Lk = Lc + nq;
-  for (int idx = threadIdx.x; idx < Lk * (HD / 8); idx += 256) {  // all row loads in flight at once
-    const int j = idx >> 4, c8 = (idx & 15) * 8;
-    const _Float16 *vsrc = j < Lc ? vc + (size_t)j * D + h * HD + c8 : u + (size_t)(j - Lc) * ldu + 2 * D + h * HD + c8;
-    const _Float16 *ksrc = j < Lc ? kc + (size_t)j * D + h * HD + c8 : u + (size_t)(j - Lc) * ldu + D + h * HD + c8;
-    *reinterpret_cast<h8 *>(&vs[j][c8]) = *reinterpret_cast<const h8 *>(vsrc);
-    *reinterpret_cast<h8 *>(&ks[j][c8]) = *reinterpret_cast<const h8 *>(ksrc);
+  // this wave's query row and the positional biases, loaded ahead of the staging
+  float qv[2] = {0.f, 0.f}, bu[2] = {0.f, 0.f}, bv[2] = {0.f, 0.f};
+  if (i < nq) {
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      const int d = lane + 64 * e;
+      qv[e] = (float)u[(size_t)i * ldu + h * HD + d];
+      bu[e] = pbu[h * HD + d];
+      bv[e] = pbv[h * HD + d];
+    }
+  }
+  // K / V rows to LDS: kStage 16-byte loads of each per thread are issued
+  // before any of them is stored (one memory round trip per kStage * 256
+  // pieces, not one per 256)
+  constexpr int kStage = 8;
+  const int npc = Lk * (HD / 8);
+  for (int base = threadIdx.x; base < npc; base += 256 * kStage) {
+    h8 kr[kStage], vr[kStage];
+#pragma unroll
+    for (int t = 0; t < kStage; t++) {
+      const int idx = base + 256 * t;
+      if (idx < npc) {
+        const int j = idx >> 4, c8 = (idx & 15) * 8;
+        const _Float16 *vsrc = j < Lc ? vc + (size_t)j * D + h * HD + c8 : u + (size_t)(j - Lc) * ldu + 2 * D + h * HD + c8;
+        const _Float16 *ksrc = j < Lc ? kc + (size_t)j * D + h * HD + c8 : u + (size_t)(j - Lc) * ldu + D + h * HD + c8;
+        vr[t] = *reinterpret_cast<const h8 *>(vsrc);
+        kr[t] = *reinterpret_cast<const h8 *>(ksrc);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < kStage; t++) {
+      const int idx = base + 256 * t;
+      if (idx < npc) {
+        const int j = idx >> 4, c8 = (idx & 15) * 8;
+        *reinterpret_cast<h8 *>(&vs[j][c8]) = vr[t];
+        *reinterpret_cast<h8 *>(&ks[j][c8]) = kr[t];
+      }
+    }
   }
   __syncthreads();
   if (blockIdx.x == 0 && kc_out) {
@@ -701,9 +733,8 @@ __global__ __launch_bounds__(256) void stream_attn_kernel(const _Float16 *__rest
 #pragma unroll
   for (int e = 0; e < 2; e++) {
     const int d = lane + 64 * e;
-    const float q = (float)u[(size_t)i * ldu + h * HD + d];
-    qs[wave][0][d] = q + pbu[h * HD + d];
-    qs[wave][1][d] = q + pbv[h * HD + d];
+    qs[wave][0][d] = qv[e] + bu[e];
+    qs[wave][1][d] = qv[e] + bv[e];
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);
   __builtin_amdgcn_wave_barrier();
