@@ -691,6 +691,19 @@ __global__ __launch_bounds__(256) void stream_attn_kernel(const _Float16 *__rest
       bv[e] = pbv[h * HD + d];
     }
   }
+  // the positional rows of this lane's first two keys, also loaded ahead
+  // (later keys, Lk > 128, load theirs in the score loop)
+  const int cs = chunk * (i / chunk);
+  h8 pf[2][HD / 8];
+#pragma unroll
+  for (int t = 0; t < 2; t++) {
+    const int j = lane + 64 * t, rel = j - Lc;
+    if (i < nq && j < Lk && rel >= cs - left && rel <= cs + chunk - 1 + right) {
+      const _Float16 *pp = P + (size_t)min(max(dMax - (i - rel), 0), Pn - 1) * D + h * HD;
+#pragma unroll
+      for (int d = 0; d < HD / 8; d++) pf[t][d] = *reinterpret_cast<const h8 *>(pp + 8 * d);
+    }
+  }
   // K / V rows to LDS: kStage 16-byte loads of each per thread are issued
   // before any of them is stored (one memory round trip per kStage * 256
   // pieces, not one per 256)
@@ -738,21 +751,35 @@ __global__ __launch_bounds__(256) void stream_attn_kernel(const _Float16 *__rest
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);
   __builtin_amdgcn_wave_barrier();
-  const int cs = chunk * (i / chunk);
   float mx = -INFINITY;
-  for (int j = lane; j < Lk; j += 64) {
+  auto score = [&](int j, const h8 *pv8) {  // pv8: the key's positional row, 8 halves per piece
+    float acc = 0.f;
+#pragma unroll
+    for (int d = 0; d < HD; d += 8) {
+      const h8 kv = *reinterpret_cast<const h8 *>(&ks[j][d]), pv = pv8[d / 8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) acc += qs[wave][0][d + e] * (float)kv[e] + qs[wave][1][d + e] * (float)pv[e];
+    }
+    return acc;
+  };
+#pragma unroll
+  for (int t = 0; t < 2; t++) {
+    const int j = lane + 64 * t, rel = j - Lc;
+    if (j < Lk) {
+      const float sc = rel >= cs - left && rel <= cs + chunk - 1 + right ? score(j, pf[t]) : -INFINITY;
+      ps[wave][j] = sc;
+      mx = fmaxf(mx, sc);
+    }
+  }
+  for (int j = lane + 128; j < Lk; j += 64) {
     const int rel = j - Lc;
     float sc = -INFINITY;
     if (rel >= cs - left && rel <= cs + chunk - 1 + right) {
-      const int pr = min(max(dMax - (i - rel), 0), Pn - 1);
-      const _Float16 *pp = P + (size_t)pr * D + h * HD;
-      float acc = 0.f;
-      for (int d = 0; d < HD; d += 8) {
-        const h8 kv = *reinterpret_cast<const h8 *>(&ks[j][d]), pv = *reinterpret_cast<const h8 *>(pp + d);
+      const _Float16 *pp = P + (size_t)min(max(dMax - (i - rel), 0), Pn - 1) * D + h * HD;
+      h8 pv8[HD / 8];
 #pragma unroll
-        for (int e = 0; e < 8; e++) acc += qs[wave][0][d + e] * (float)kv[e] + qs[wave][1][d + e] * (float)pv[e];
-      }
-      sc = acc;
+      for (int d = 0; d < HD / 8; d++) pv8[d] = *reinterpret_cast<const h8 *>(pp + 8 * d);
+      sc = score(j, pv8);
     }
     ps[wave][j] = sc;
     mx = fmaxf(mx, sc);
