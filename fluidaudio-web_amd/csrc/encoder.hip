@@ -1066,7 +1066,7 @@ void encoder_ws_free(EncWs &w) {
   for (auto &g : w.graphs)
     if (g.exec) (void)hipGraphExecDestroy(g.exec);
   w.graphs.clear();
-  for (void *p : {w.hlo, w.ulo, w.alo, w.g32, w.vt, w.vrow, w.s2, w.s2p, w.s3, w.s3p, w.h, w.u, w.a, w.g, w.melw, w.xw, w.dw32, w.wdq, w.msrc})
+  for (void *p : {w.hlo, w.ulo, w.alo, w.g32, w.vt, w.vrow, w.s2, w.s2p, w.s3, w.s3p, w.h, w.u, w.a, w.g, w.melw, w.xw, w.dw32, w.wdq, w.msrc, w.skp})
     if (p) (void)hipFree(p);
   w = EncWs();
 }
@@ -1212,6 +1212,7 @@ int pass_workspace(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, int layers, bo
   if (any & FA_EXACT_GLU) FA_TRY(grow(e, &e->W().g32, &e->W().cap_g32, (size_t)M * D * 4));
   if (cln) FA_TRY(grow(e, &e->W().dw32, &e->W().cap_dw32, (size_t)M * D * 4));
   if (e->format != FA_W_F16 && M >= kDequantRows) FA_TRY(grow(e, &e->W().wdq, &e->W().cap_wdq, wdq_bytes(e)));
+  if (stream) FA_TRY(grow(e, &e->W().skp, &e->W().cap_skp, skinny_split_bytes(c.D)));
   if (!stream) {
     // transposed V per (window, head), written by the q|k|v GEMM's epilogue
     // (or v_transpose_kernel).  Keys past a window's end are never written:
@@ -1341,6 +1342,10 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
     p.C = Cp; p.Clo = Clo; p.ldc = ldc; p.out_f16 = out_f16; p.act = act;
     p.add = add; p.ldadd = ldc; p.glu = glu;
     p.M = M; p.allow_skinny = sp != nullptr;
+    if (sp) {
+      p.skp = (float *)e->W().skp;
+      p.skp_bytes = e->W().cap_skp;
+    }
     return gemm_mfma(ctx, p, label);
   };
   _Float16 *hlo = (_Float16 *)e->W().hlo, *ulo = (_Float16 *)e->W().ulo, *alo = (_Float16 *)e->W().alo;

@@ -51,6 +51,8 @@ struct EncWs {
   size_t cap_dw32 = 0;
   void *wdq = nullptr;  // quantised formats, batches of >= kDequantRows rows: one layer's linears widened to f16
   size_t cap_wdq = 0;
+  void *skp = nullptr;  // stream passes: the skinny GEMMs' split-K partial tiles
+  size_t cap_skp = 0;
 };
 
 }  // namespace fa

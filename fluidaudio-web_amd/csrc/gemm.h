@@ -9,6 +9,11 @@ namespace fa {
 enum AKind : int { A_F16 = 0, A_F32 = 1 };
 enum BKind : int { B_F16 = 0, B_I8 = 1, B_I4 = 2 };
 
+// split-K factor of the skinny route for N <= 1024, and its workspace for N
+// columns (two 16-row tiles at most: 64 lanes x 16 bytes per tile)
+constexpr int kSkinnySplit = 4;
+inline size_t skinny_split_bytes(int N) { return (size_t)kSkinnySplit * (N / 16) * 2 * 64 * 16; }
+
 struct GemmArgs {
   const void *A = nullptr;  // [M, lda] row-major, f16 or f32
   const void *Alo = nullptr;  // optional f16 plane [M, lda]: A = A + Alo exactly (f16 x f16 route only)
@@ -35,6 +40,12 @@ struct GemmArgs {
   const float *ln_x = nullptr, *ln_g = nullptr, *ln_b = nullptr;
   float ln_eps = 0.f;
   int ln_lo = 0;
+  // skinny route only: workspace for split-K partial tiles (N <= 1024: the K
+  // range is split over kSkinnySplit workgroups per 16 columns, whose partial
+  // tiles a second kernel adds in split order before the epilogue); null: one
+  // workgroup per 16 columns
+  float *skp = nullptr;
+  size_t skp_bytes = 0;
   const float *bias = nullptr;      // [N]
   const float *add = nullptr;       // f32 residual [M, ldadd]; may alias C
   int ldadd = 0;

@@ -726,14 +726,16 @@ static int launch_dma(fa_ctx *ctx, const GemmArgs &p, const char *label) {
 // with its B (16 columns) and A fragments loaded straight from global, G
 // 32-deep steps of loads in flight; the slices' partial tiles are added
 // through LDS in wave order and wave 0 runs the direct epilogue.
-template <int TI, int KS, int EPI, int LO>
+// SPLIT > 1: workgroup (x, y) sums the y-th of SPLIT K ranges and stores its
+// raw tile in p.skp for gemm_skinny_split_sum_kernel (no epilogue here).
+template <int TI, int KS, int EPI, int LO, int SPLIT = 1>
 __global__ __launch_bounds__(64 * KS) void gemm_skinny_kernel(GemmArgs p) {
   constexpr int G = 8;
   __shared__ f4 part[KS > 1 ? KS - 1 : 1][TI][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c16 = lane & 15, g = lane >> 4;
   const int n0 = blockIdx.x * 16;
-  const int ks = p.K / KS, kb = wave * ks, nst = ks / 32;
+  const int ks = p.K / (KS * SPLIT), kb = blockIdx.y * (p.K / SPLIT) + wave * ks, nst = ks / 32;
   const _Float16 *B = reinterpret_cast<const _Float16 *>(p.B) + (size_t)(n0 + c16) * p.K + kb + g * 8;
   const _Float16 *A[TI], *Al[TI];
 #pragma unroll
@@ -779,7 +781,35 @@ __global__ __launch_bounds__(64 * KS) void gemm_skinny_kernel(GemmArgs p) {
 #pragma unroll
       for (int i = 0; i < TI; i++) acc[i][0] += part[w][i][lane];
   }
+  if constexpr (SPLIT > 1) {
+    f4 *dst = reinterpret_cast<f4 *>(p.skp) + (size_t)(blockIdx.y * gridDim.x + blockIdx.x) * TI * 64 + lane;
+#pragma unroll
+    for (int i = 0; i < TI; i++) dst[i * 64] = acc[i][0];
+    return;
+  }
   epilogue_direct<TI, 1, EPI>(p, acc, 0, n0, lane);
+}
+
+// The split-K skinny route's second launch: one wave per 16 columns adds the
+// SPLIT partial tiles in split order, then runs the direct epilogue.
+template <int TI, int SPLIT, int EPI>
+__global__ __launch_bounds__(64) void gemm_skinny_split_sum_kernel(GemmArgs p) {
+  const int lane = threadIdx.x;
+  const f4 *src = reinterpret_cast<const f4 *>(p.skp) + (size_t)blockIdx.x * TI * 64 + lane;
+  const size_t stride = (size_t)gridDim.x * TI * 64;  // one split's tiles
+  f4 part[SPLIT][TI];
+#pragma unroll
+  for (int sp = 0; sp < SPLIT; sp++)
+#pragma unroll
+    for (int i = 0; i < TI; i++) part[sp][i] = src[sp * stride + i * 64];
+  f4 acc[TI][1];
+#pragma unroll
+  for (int i = 0; i < TI; i++) {
+    acc[i][0] = part[0][i];
+#pragma unroll
+    for (int sp = 1; sp < SPLIT; sp++) acc[i][0] += part[sp][i];
+  }
+  epilogue_direct<TI, 1, EPI>(p, acc, 0, blockIdx.x * 16, lane);
 }
 
 // The skinny route with the LayerNorm of its A rows folded in (stream
@@ -894,7 +924,18 @@ template <int EPI>
 static int launch_skinny(fa_ctx *ctx, const GemmArgs &p, const char *label) {
   const int ks = skinny_ks(p.N);
   const int ti = p.M <= 16 ? 1 : 2;
-  ProfScope ps(ctx, label);
+  static const bool split_on = [] {  // FA_SKINNY_SPLIT=0: one workgroup per 16 columns everywhere
+    const char *e = getenv("FA_SKINNY_SPLIT");
+    return !(e && e[0] == '0');
+  }();
+  // N <= 1024 gives one workgroup per 16 columns only N / 16 <= 64 of the
+  // chip's CUs: with two row tiles (17..32 rows, a batched stream pass) its K
+  // range is split over kSkinnySplit workgroups instead.  Up to 16 rows the
+  // second launch costs more than the extra CUs give (a single stream's pass),
+  // and such passes keep the sums of one workgroup per 16 columns.
+  const bool split = split_on && ti == 2 && !p.ln_x && p.skp && p.N <= 1024 && p.K % (32 * ks * kSkinnySplit) == 0 &&
+                     p.skp_bytes >= skinny_split_bytes(p.N);
+  ProfScope ps(ctx, label, !split);
   const dim3 grid(p.N / 16);
   if (p.ln_x) {  // A = LayerNorm(ln_x), built in the kernel
 #define FA_SKL(TI, KS)                                                                                   \
@@ -914,12 +955,20 @@ static int launch_skinny(fa_ctx *ctx, const GemmArgs &p, const char *label) {
 #undef FA_SKL
     return check_launch(ctx, label);
   }
-#define FA_SK(TI, KS)                                                                                \
-  do {                                                                                               \
-    if (p.Alo)                                                                                       \
-      FA_LAUNCH(ps, (gemm_skinny_kernel<TI, KS, EPI, 1>), grid, dim3(64 * KS), 0, ctx->stream, p); \
-    else                                                                                             \
-      FA_LAUNCH(ps, (gemm_skinny_kernel<TI, KS, EPI, 0>), grid, dim3(64 * KS), 0, ctx->stream, p); \
+#define FA_SK(TI, KS)                                                                                                        \
+  do {                                                                                                                       \
+    if (split) {                                                                                                             \
+      const dim3 g2(p.N / 16, kSkinnySplit);                                                                                 \
+      if (p.Alo)                                                                                                             \
+        hipLaunchKernelGGL((gemm_skinny_kernel<TI, KS, EPI, 1, kSkinnySplit>), g2, dim3(64 * KS), 0, ctx->stream, p);       \
+      else                                                                                                                   \
+        hipLaunchKernelGGL((gemm_skinny_kernel<TI, KS, EPI, 0, kSkinnySplit>), g2, dim3(64 * KS), 0, ctx->stream, p);       \
+      hipLaunchKernelGGL((gemm_skinny_split_sum_kernel<TI, kSkinnySplit, EPI>), grid, dim3(64), 0, ctx->stream, p);         \
+    } else if (p.Alo) {                                                                                                      \
+      FA_LAUNCH(ps, (gemm_skinny_kernel<TI, KS, EPI, 1>), grid, dim3(64 * KS), 0, ctx->stream, p);                         \
+    } else {                                                                                                                 \
+      FA_LAUNCH(ps, (gemm_skinny_kernel<TI, KS, EPI, 0>), grid, dim3(64 * KS), 0, ctx->stream, p);                         \
+    }                                                                                                                        \
   } while (0)
   if (ti == 1) {
     if (ks == 4) FA_SK(1, 4);

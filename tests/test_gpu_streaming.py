@@ -196,6 +196,40 @@ def test_streams_pushed_together_equal_streams_pushed_alone(ctx, fa, monkeypatch
     enc.close()
 
 
+def test_sixteen_streams_pushed_together_track_streams_pushed_alone(ctx, fa):
+    """Sixteen aligned streams: every push is one batched pass of 32 rows, whose
+    GEMMs with N <= 1024 split K over four workgroups per 16 columns (a
+    second launch adds the partial tiles), so the sums are ordered unlike the
+    solo passes': each stream stays within the stream-vs-offline bar of its
+    solo frames, and the batched run is deterministic (a second run gives
+    the same bits)."""
+    cfg, man, enc = _model(ctx, fa)
+    mels = [fa.synth.make_features(cfg["melBins"], 304, seed=60 + i)[0] for i in range(16)]
+    alone = [_stream(ctx, fa, enc, m, [16] * 19) for m in mels]
+
+    def together():
+        sts = [fa.createEncodeStream(ctx, enc) for _ in mels]
+        got = [[] for _ in mels]
+        for t in range(0, 304, 16):
+            for i, o in enumerate(fa.encodeStreamsPush(ctx, sts, [m[:, t:t + 16] for m in mels])):
+                if o is not None:
+                    got[i].append(o)
+        for i, st in enumerate(sts):
+            o = fa.encodeStreamFlush(ctx, st)
+            if o is not None:
+                got[i].append(o)
+            fa.disposeEncodeStream(ctx, st)
+        return [np.concatenate(g, 0) for g in got]
+
+    g1, g2 = together(), together()
+    for i, (a, b, c) in enumerate(zip(alone, g1, g2)):
+        assert a.shape == b.shape
+        assert np.array_equal(b, c), f"stream {i}: batched runs differ"
+        d = float(np.abs(b - a).max() / np.abs(a).max())
+        assert d < 2e-3, f"stream {i}: max rel {d:.2e}"
+    enc.close()
+
+
 @pytest.mark.parametrize("exact", [False, True])
 def test_layernorm_folded_into_skinny_gemms_matches_separate_launches(ctx, fa, monkeypatch, exact):
     """Stream passes fold norm_att / norm_conv / norm_ff2 into the skinny GEMMs
