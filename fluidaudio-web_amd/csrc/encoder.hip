@@ -1212,7 +1212,7 @@ int pass_workspace(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, int layers, bo
   if (any & FA_EXACT_GLU) FA_TRY(grow(e, &e->W().g32, &e->W().cap_g32, (size_t)M * D * 4));
   if (cln) FA_TRY(grow(e, &e->W().dw32, &e->W().cap_dw32, (size_t)M * D * 4));
   if (e->format != FA_W_F16 && M >= kDequantRows) FA_TRY(grow(e, &e->W().wdq, &e->W().cap_wdq, wdq_bytes(e)));
-  if (stream) FA_TRY(grow(e, &e->W().skp, &e->W().cap_skp, skinny_split_bytes(c.D)));
+  if (stream) FA_TRY(grow(e, &e->W().skp, &e->W().cap_skp, skinny_split_bytes(std::min(2 * c.D, kSkinnySplitMaxN))));
   if (!stream) {
     // transposed V per (window, head), written by the q|k|v GEMM's epilogue
     // (or v_transpose_kernel).  Keys past a window's end are never written:

@@ -9,9 +9,9 @@ namespace fa {
 enum AKind : int { A_F16 = 0, A_F32 = 1 };
 enum BKind : int { B_F16 = 0, B_I8 = 1, B_I4 = 2 };
 
-// split-K factor of the skinny route for N <= 1024, and its workspace for N
+// split-K factor of the skinny route for N <= kSkinnySplitMaxN, and its workspace for N
 // columns (two 16-row tiles at most: 64 lanes x 16 bytes per tile)
-constexpr int kSkinnySplit = 4;
+constexpr int kSkinnySplit = 4, kSkinnySplitMaxN = 2048;
 inline size_t skinny_split_bytes(int N) { return (size_t)kSkinnySplit * (N / 16) * 2 * 64 * 16; }
 
 struct GemmArgs {
@@ -40,7 +40,7 @@ struct GemmArgs {
   const float *ln_x = nullptr, *ln_g = nullptr, *ln_b = nullptr;
   float ln_eps = 0.f;
   int ln_lo = 0;
-  // skinny route only: workspace for split-K partial tiles (N <= 1024: the K
+  // skinny route only: workspace for split-K partial tiles (N <= 2048: the K
   // range is split over kSkinnySplit workgroups per 16 columns, whose partial
   // tiles a second kernel adds in split order before the epilogue); null: one
   // workgroup per 16 columns

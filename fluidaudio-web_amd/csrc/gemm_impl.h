@@ -928,12 +928,12 @@ static int launch_skinny(fa_ctx *ctx, const GemmArgs &p, const char *label) {
     const char *e = getenv("FA_SKINNY_SPLIT");
     return !(e && e[0] == '0');
   }();
-  // N <= 1024 gives one workgroup per 16 columns only N / 16 <= 64 of the
+  // N <= 2048 gives one workgroup per 16 columns only N / 16 <= 128 of the
   // chip's CUs: with two row tiles (17..32 rows, a batched stream pass) its K
   // range is split over kSkinnySplit workgroups instead.  Up to 16 rows the
   // second launch costs more than the extra CUs give (a single stream's pass),
   // and such passes keep the sums of one workgroup per 16 columns.
-  const bool split = split_on && ti == 2 && !p.ln_x && p.skp && p.N <= 1024 && p.K % (32 * ks * kSkinnySplit) == 0 &&
+  const bool split = split_on && ti == 2 && !p.ln_x && p.skp && p.N <= kSkinnySplitMaxN && p.K % (32 * ks * kSkinnySplit) == 0 &&
                      p.skp_bytes >= skinny_split_bytes(p.N);
   ProfScope ps(ctx, label, !split);
   const dim3 grid(p.N / 16);
