@@ -418,13 +418,16 @@ int fa_encoder_tsub_of(const fa_encoder *enc, int T);
 typedef struct fa_stream fa_stream;
 int fa_stream_create(fa_ctx *ctx, fa_encoder *enc, int lookahead_chunks, int max_chunk, fa_stream **out);
 int fa_stream_push(fa_stream *st, const float *mel, int count, fa_tensor *out);
-/* Push to n distinct streams of one context in one call: stream i gets
- * mels[i] (counts[i] frames) and outs[i] exactly as fa_stream_push would give
- * it.  Each stream's passes run on a HIP stream of its own with a workspace of
- * its own, so the n streams' chunk passes (each a chain of small,
- * latency-bound launches) run concurrently; they start after the work queued
- * on the context stream, and the context stream waits for all of them.  The
- * reference serves one stream per encodeStreamPush
+/* Push to n distinct streams of one encoder in one call: stream i gets
+ * mels[i] (counts[i] frames) and outs[i] as fa_stream_push would give it.
+ * Streams whose next passes have the same shape run as one batched pass (up
+ * to 16 streams, the weights read once for all); other groups run at the same
+ * time on the encoder's stream lanes (HIP streams with workspaces of their
+ * own).  The lanes start after the work queued on the context stream, and the
+ * context stream waits for all of them.  Frames equal solo pushes bit for bit
+ * while a batched pass has at most 16 rows; larger passes sum in another
+ * order, within the encoder's tolerance (deterministic).  On failure every
+ * outs[i] is 0.  The reference serves one stream per encodeStreamPush
  * (streaming-encoder.js:182-297); this is that call for n streams at once. */
 int fa_stream_push_many(int n, fa_stream *const *sts, const float *const *mels, const int *counts, fa_tensor *outs);
 int fa_stream_flush(fa_stream *st, fa_tensor *out);
