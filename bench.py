@@ -304,6 +304,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--windows", type=int, default=16, help="decode workload: windows per decode call (1..64)")
     ap.add_argument("--audio-sec", type=float, default=3600.0, help="e2e workload: seconds of synthetic audio")
+    ap.add_argument("--streams", default="4,8,16,32", help="stream workload: concurrent stream counts timed after the single stream")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); multi-GPU runs are not part of it", file=sys.stderr)
@@ -648,7 +649,7 @@ def bench_stream(args, fa, ctx):
             fa.disposeEncodeStream(ctx, st)
 
     concurrent = {}
-    for n in (4, 8, 16, 32):
+    for n in [int(v) for v in args.streams.split(",") if v.strip()]:
         run_many(n)
         ctx.sync()
         t0 = time.perf_counter()
