@@ -196,13 +196,13 @@ def test_streams_pushed_together_equal_streams_pushed_alone(ctx, fa, monkeypatch
     enc.close()
 
 
-def test_sixteen_streams_pushed_together_track_streams_pushed_alone(ctx, fa):
+def test_sixteen_streams_pushed_together_track_streams_pushed_alone(ctx, fa, monkeypatch):
     """Sixteen aligned streams: every push is one batched pass of 32 rows, whose
-    GEMMs with N <= 1024 split K over four workgroups per 16 columns (a
+    GEMMs with N <= 2048 split K over four workgroups per 16 columns (a
     second launch adds the partial tiles), so the sums are ordered unlike the
     solo passes': each stream stays within the stream-vs-offline bar of its
     solo frames, and the batched run is deterministic (a second run gives
-    the same bits)."""
+    the same bits, and eager passes give the captured passes' bits)."""
     cfg, man, enc = _model(ctx, fa)
     mels = [fa.synth.make_features(cfg["melBins"], 304, seed=60 + i)[0] for i in range(16)]
     alone = [_stream(ctx, fa, enc, m, [16] * 19) for m in mels]
@@ -222,9 +222,12 @@ def test_sixteen_streams_pushed_together_track_streams_pushed_alone(ctx, fa):
         return [np.concatenate(g, 0) for g in got]
 
     g1, g2 = together(), together()
-    for i, (a, b, c) in enumerate(zip(alone, g1, g2)):
+    monkeypatch.setenv("FA_GRAPH", "0")
+    g3 = together()
+    for i, (a, b, c, e) in enumerate(zip(alone, g1, g2, g3)):
         assert a.shape == b.shape
         assert np.array_equal(b, c), f"stream {i}: batched runs differ"
+        assert np.array_equal(b, e), f"stream {i}: eager passes differ from captured ones"
         d = float(np.abs(b - a).max() / np.abs(a).max())
         assert d < 2e-3, f"stream {i}: max rel {d:.2e}"
     enc.close()
