@@ -233,6 +233,35 @@ def test_sixteen_streams_pushed_together_track_streams_pushed_alone(ctx, fa, mon
     enc.close()
 
 
+def test_sixteen_streams_at_full_width_track_streams_pushed_alone(ctx, fa):
+    """The split-K skinny GEMMs at this path's widths (d_model 1024, FF 4096,
+    8 heads; two layers): in 32-row batched passes the out-projection, pw2
+    (K 1024, N 1024), pw1 (N 2048) and FF W2 (K 4096) all split K; every
+    stream stays within the stream-vs-offline bar of its solo frames."""
+    cfg = dict(fa.synth.small_stream_cfg(layers=2), D=1024, DFF=4096, H=8)
+    man = fa.synth.make_weights(cfg, seed=12)
+    enc = fa.FusedEncoder(ctx, man, "f16", max_T=128, cfg=cfg)
+    mels = [fa.synth.make_features(cfg["melBins"], 160, seed=80 + i)[0] for i in range(16)]
+    alone = [_stream(ctx, fa, enc, m, [16] * 10) for m in mels]
+    sts = [fa.createEncodeStream(ctx, enc) for _ in mels]
+    got = [[] for _ in mels]
+    for t in range(0, 160, 16):
+        for i, o in enumerate(fa.encodeStreamsPush(ctx, sts, [m[:, t:t + 16] for m in mels])):
+            if o is not None:
+                got[i].append(o)
+    for i, st in enumerate(sts):
+        o = fa.encodeStreamFlush(ctx, st)
+        if o is not None:
+            got[i].append(o)
+        fa.disposeEncodeStream(ctx, st)
+    for i, (a, g) in enumerate(zip(alone, got)):
+        g = np.concatenate(g, 0)
+        assert g.shape == a.shape
+        d = float(np.abs(g - a).max() / np.abs(a).max())
+        assert d < 2e-3, f"stream {i}: max rel {d:.2e}"
+    enc.close()
+
+
 @pytest.mark.parametrize("exact", [False, True])
 def test_layernorm_folded_into_skinny_gemms_matches_separate_launches(ctx, fa, monkeypatch, exact):
     """Stream passes fold norm_att / norm_conv / norm_ff2 into the skinny GEMMs
