@@ -678,8 +678,15 @@ __global__ __launch_bounds__(256) void stream_attn_kernel(const _Float16 *__rest
   if (out_lo) out_lo += (size_t)w * nq * D;
   const _Float16 *kc = slots.kc_in[w] + kvo, *vc = slots.vc_in[w] + kvo;
   _Float16 *kc_out = keep > 0 ? slots.kc_out[w] + kvo : nullptr, *vc_out = slots.vc_out[w] + kvo;
-  const int i = blockIdx.x * 4 + wave;
   const int Lk = Lc + nq;
+  // A block has four waves.  With more than two queries (nq > 2) each wave
+  // takes one query; otherwise each query's keys are split over two waves
+  // (kh = 2: [jb, je) is this wave's half), whose maxima, sums and P.V
+  // partial rows meet in LDS.  The grid is cdiv(nq, 4) blocks either way.
+  const int kh = nq <= 2 ? 2 : 1;
+  const int i = blockIdx.x * (4 / kh) + wave / kh, half = wave % kh;
+  const int Lh = (Lk + kh - 1) / kh, jb = half * Lh, je = min(Lk, jb + Lh);
+  const bool act = i < nq;
   // this wave's query row and the positional biases, loaded ahead of the staging
   float qv[2] = {0.f, 0.f}, bu[2] = {0.f, 0.f}, bv[2] = {0.f, 0.f};
   if (i < nq) {
@@ -692,13 +699,13 @@ __global__ __launch_bounds__(256) void stream_attn_kernel(const _Float16 *__rest
     }
   }
   // the positional rows of this lane's first two keys, also loaded ahead
-  // (later keys, Lk > 128, load theirs in the score loop)
+  // (later keys, more than 128 in the wave's range, load theirs in the score loop)
   const int cs = chunk * (i / chunk);
   h8 pf[2][HD / 8];
 #pragma unroll
   for (int t = 0; t < 2; t++) {
-    const int j = lane + 64 * t, rel = j - Lc;
-    if (i < nq && j < Lk && rel >= cs - left && rel <= cs + chunk - 1 + right) {
+    const int j = jb + lane + 64 * t, rel = j - Lc;
+    if (act && j < je && rel >= cs - left && rel <= cs + chunk - 1 + right) {
       const _Float16 *pp = P + (size_t)min(max(dMax - (i - rel), 0), Pn - 1) * D + h * HD;
 #pragma unroll
       for (int d = 0; d < HD / 8; d++) pf[t][d] = *reinterpret_cast<const h8 *>(pp + 8 * d);
@@ -742,69 +749,97 @@ __global__ __launch_bounds__(256) void stream_attn_kernel(const _Float16 *__rest
       *reinterpret_cast<h8 *>(vc_out + (size_t)r * D + h * HD + c8) = *reinterpret_cast<const h8 *>(&vs[src][c8]);
     }
   }
-  if (i >= nq) return;
+  __shared__ float xmx[4], xsum[4];
+  __shared__ float opart[4][HD];
+  float mx = -INFINITY, sum = 0.f, o[2] = {0.f, 0.f};
+  if (act) {
 #pragma unroll
-  for (int e = 0; e < 2; e++) {
-    const int d = lane + 64 * e;
-    qs[wave][0][d] = qv[e] + bu[e];
-    qs[wave][1][d] = qv[e] + bv[e];
-  }
-  __builtin_amdgcn_s_waitcnt(0xc07f);
-  __builtin_amdgcn_wave_barrier();
-  float mx = -INFINITY;
-  auto score = [&](int j, const h8 *pv8) {  // pv8: the key's positional row, 8 halves per piece
-    float acc = 0.f;
-#pragma unroll
-    for (int d = 0; d < HD; d += 8) {
-      const h8 kv = *reinterpret_cast<const h8 *>(&ks[j][d]), pv = pv8[d / 8];
-#pragma unroll
-      for (int e = 0; e < 8; e++) acc += qs[wave][0][d + e] * (float)kv[e] + qs[wave][1][d + e] * (float)pv[e];
+    for (int e = 0; e < 2; e++) {
+      const int d = lane + 64 * e;
+      qs[wave][0][d] = qv[e] + bu[e];
+      qs[wave][1][d] = qv[e] + bv[e];
     }
-    return acc;
-  };
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    auto score = [&](int j, const h8 *pv8) {  // pv8: the key's positional row, 8 halves per piece
+      float acc = 0.f;
 #pragma unroll
-  for (int t = 0; t < 2; t++) {
-    const int j = lane + 64 * t, rel = j - Lc;
-    if (j < Lk) {
-      const float sc = rel >= cs - left && rel <= cs + chunk - 1 + right ? score(j, pf[t]) : -INFINITY;
+      for (int d = 0; d < HD; d += 8) {
+        const h8 kv = *reinterpret_cast<const h8 *>(&ks[j][d]), pv = pv8[d / 8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc += qs[wave][0][d + e] * (float)kv[e] + qs[wave][1][d + e] * (float)pv[e];
+      }
+      return acc;
+    };
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+      const int j = jb + lane + 64 * t, rel = j - Lc;
+      if (j < je) {
+        const float sc = rel >= cs - left && rel <= cs + chunk - 1 + right ? score(j, pf[t]) : -INFINITY;
+        ps[wave][j] = sc;
+        mx = fmaxf(mx, sc);
+      }
+    }
+    for (int j = jb + lane + 128; j < je; j += 64) {
+      const int rel = j - Lc;
+      float sc = -INFINITY;
+      if (rel >= cs - left && rel <= cs + chunk - 1 + right) {
+        const _Float16 *pp = P + (size_t)min(max(dMax - (i - rel), 0), Pn - 1) * D + h * HD;
+        h8 pv8[HD / 8];
+#pragma unroll
+        for (int d = 0; d < HD / 8; d++) pv8[d] = *reinterpret_cast<const h8 *>(pp + 8 * d);
+        sc = score(j, pv8);
+      }
       ps[wave][j] = sc;
       mx = fmaxf(mx, sc);
     }
+    mx = wave_max(mx);  // one half may see only masked keys (-inf); the query's max is finite
   }
-  for (int j = lane + 128; j < Lk; j += 64) {
-    const int rel = j - Lc;
-    float sc = -INFINITY;
-    if (rel >= cs - left && rel <= cs + chunk - 1 + right) {
-      const _Float16 *pp = P + (size_t)min(max(dMax - (i - rel), 0), Pn - 1) * D + h * HD;
-      h8 pv8[HD / 8];
-#pragma unroll
-      for (int d = 0; d < HD / 8; d++) pv8[d] = *reinterpret_cast<const h8 *>(pp + 8 * d);
-      sc = score(j, pv8);
+  if (kh == 2) {  // the query's max over both halves
+    if (act && lane == 0) xmx[wave] = mx;
+    __syncthreads();
+    if (act) mx = fmaxf(mx, xmx[wave ^ 1]);
+  }
+  if (act) {
+    for (int j = jb + lane; j < je; j += 64) {
+      const float p = __expf(ps[wave][j] - mx);  // masked keys: exp(-inf) = 0
+      ps[wave][j] = p;
+      sum += p;
     }
-    ps[wave][j] = sc;
-    mx = fmaxf(mx, sc);
+    sum = wave_sum(sum);
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      const int d = lane + 64 * e;
+      float acc = 0.f;
+#pragma unroll 8
+      for (int j = jb; j < je; j++) acc += ps[wave][j] * (float)vs[j][d];  // masked keys carry p = 0
+      o[e] = acc;
+    }
   }
-  mx = wave_max(mx);  // finite: a query always sees its own chunk
-  float sum = 0.f;
-  for (int j = lane; j < Lk; j += 64) {
-    const float p = __expf(ps[wave][j] - mx);  // masked keys: exp(-inf) = 0
-    ps[wave][j] = p;
-    sum += p;
+  if (kh == 2) {  // the second half's sum and P.V row join the first half's
+    if (act && half) {
+      if (lane == 0) xsum[wave] = sum;
+#pragma unroll
+      for (int e = 0; e < 2; e++) opart[wave][lane + 64 * e] = o[e];
+    }
+    __syncthreads();
+    if (!act || half) return;
+    sum += xsum[wave + 1];
+#pragma unroll
+    for (int e = 0; e < 2; e++) o[e] += opart[wave + 1][lane + 64 * e];
+  } else if (!act) {
+    return;
   }
-  sum = wave_sum(sum);
-  __builtin_amdgcn_s_waitcnt(0xc07f);
-  __builtin_amdgcn_wave_barrier();
   const float inv = 1.f / sum;
 #pragma unroll
   for (int e = 0; e < 2; e++) {
     const int d = lane + 64 * e;
-    float o = 0.f;
-#pragma unroll 8
-    for (int j = 0; j < Lk; j++) o += ps[wave][j] * (float)vs[j][d];  // masked keys carry p = 0
-    o *= inv;
-    const _Float16 hi = (_Float16)o;
+    const float v = o[e] * inv;
+    const _Float16 hi = (_Float16)v;
     out[(size_t)i * D + h * HD + d] = hi;
-    if (out_lo) out_lo[(size_t)i * D + h * HD + d] = (_Float16)(o - (float)hi);
+    if (out_lo) out_lo[(size_t)i * D + h * HD + d] = (_Float16)(v - (float)hi);
   }
 }
 
