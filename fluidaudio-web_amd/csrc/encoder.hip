@@ -592,21 +592,36 @@ __global__ __launch_bounds__(256) void dwconv_ln_kernel(const TI *__restrict__ x
   const size_t base = (size_t)st.off[win] * D + c0;
   float r[4] = {0.f, 0.f, 0.f, 0.f};
   if (act) {
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    // every tap's inputs and weights are loaded before the first product
+    // (one memory round trip, not one per tap)
+    float v[KT][4], wk[KT][4];
 #pragma unroll
     for (int k = 0; k < KT; k++) {
+      const float4 w4 = *reinterpret_cast<const float4 *>(wt + k * D + c0);
+      wk[k][0] = w4.x; wk[k][1] = w4.y; wk[k][2] = w4.z; wk[k][3] = w4.w;
       const int ti = t - pad + k;
-      float v[4] = {0.f, 0.f, 0.f, 0.f};
       if (ti >= 0 && ti < T) {
+        if constexpr (sizeof(TI) == 4) {
+          const float4 a = *reinterpret_cast<const float4 *>(x + base + (size_t)ti * D);
+          v[k][0] = a.x; v[k][1] = a.y; v[k][2] = a.z; v[k][3] = a.w;
+        } else {
+          const h4 a = *reinterpret_cast<const h4 *>(x + base + (size_t)ti * D);
 #pragma unroll
-        for (int e = 0; e < 4; e++) v[e] = (float)x[base + (size_t)ti * D + e];
+          for (int e = 0; e < 4; e++) v[k][e] = (float)a[e];
+        }
       } else if (ti < 0 && cache) {
+        const float4 a = *reinterpret_cast<const float4 *>(cache + (size_t)(KT - 1 + ti) * D + c0);
+        v[k][0] = a.x; v[k][1] = a.y; v[k][2] = a.z; v[k][3] = a.w;
+      } else {
 #pragma unroll
-        for (int e = 0; e < 4; e++) v[e] = cache[(size_t)(KT - 1 + ti) * D + c0 + e];
+        for (int e = 0; e < 4; e++) v[k][e] = 0.f;
       }
-#pragma unroll
-      for (int e = 0; e < 4; e++) acc[e] += v[e] * wt[k * D + c0 + e];
     }
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < KT; k++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) acc[e] += v[k][e] * wk[k][e];
 #pragma unroll
     for (int e = 0; e < 4; e++) r[e] = acc[e] + b[c0 + e];
   }
