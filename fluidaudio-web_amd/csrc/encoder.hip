@@ -165,11 +165,14 @@ __global__ __launch_bounds__(256) void sub_c01_kernel(const float *__restrict__ 
       o[e] = fmaxf(acc, 0.f);
     }
   };
+  // output columns [fb, fe): blockIdx.z of gridDim.z column groups (small
+  // grids, a stream pass, spread a row's columns over more waves)
+  const int fper = (F2 + gridDim.z - 1) / gridDim.z, fb = blockIdx.z * fper, fe = min(F2, fb + fper);
   float left[3][CPL];  // c0 column 2*f2-pl of rows 2*t2-pt .. 2*t2-pt+2 (the previous step's right column)
 #pragma unroll
-  for (int a = 0; a < 3; a++) c0(2 * t2 - pt + a, -pl, left[a]);
+  for (int a = 0; a < 3; a++) c0(2 * t2 - pt + a, 2 * fb - pl, left[a]);
   _Float16 *yr = y + (size_t)(s2.off[win] + t2) * F2 * 2 * C + 2 * CPL * lane;
-  for (int f2 = 0; f2 < F2; f2++) {
+  for (int f2 = fb; f2 < fe; f2++) {
     float o[CPL];
 #pragma unroll
     for (int e = 0; e < CPL; e++) o[e] = c1b[e];
@@ -203,7 +206,7 @@ __global__ __launch_bounds__(256) void sub_dw_kernel(const float *__restrict__ x
   constexpr int C = 64 * CPL;
   const int lane = threadIdx.x & 63, win = blockIdx.y;
   const int to = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (vrow && lane == 0 && (to < out.len[win] || to < vpad)) vrow[out.off[win] + to] = to < out.len[win] ? win * vstride + to : -1;
+  if (vrow && lane == 0 && blockIdx.z == 0 && (to < out.len[win] || to < vpad)) vrow[out.off[win] + to] = to < out.len[win] ? win * vstride + to : -1;
   if (to >= out.len[win]) return;
   float wr[9][CPL], br[CPL];
 #pragma unroll
@@ -224,11 +227,13 @@ __global__ __launch_bounds__(256) void sub_dw_kernel(const float *__restrict__ x
       for (int e = 0; e < CPL; e++) v[e] = 0.f;
     }
   };
+  // output columns [fb, fe): blockIdx.z of gridDim.z column groups, as sub_c01_kernel
+  const int fper = (Fout + gridDim.z - 1) / gridDim.z, fb = blockIdx.z * fper, fe = min(Fout, fb + fper);
   float left[3][CPL];  // input column 2*fo-pl of rows 2*to-pt .. 2*to-pt+2
 #pragma unroll
-  for (int a = 0; a < 3; a++) ld(2 * to - pt + a, -pl, left[a]);
+  for (int a = 0; a < 3; a++) ld(2 * to - pt + a, 2 * fb - pl, left[a]);
   _Float16 *yr = y + (size_t)(out.off[win] + to) * Fout * 2 * C + 2 * CPL * lane;
-  for (int fo = 0; fo < Fout; fo++) {
+  for (int fo = fb; fo < fe; fo++) {
     float o[CPL];
 #pragma unroll
     for (int e = 0; e < CPL; e++) o[e] = br[e];
@@ -1280,6 +1285,11 @@ int pass_workspace(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, int layers, bo
 // The whole forward of one pass as a fixed kernel sequence (captured into a
 // hipGraph by the callers when it repeats).  mel: [R0, melBins] time-major
 // rows; x: [M, D] f32, the residual stream and the pass's output.
+// Column groups of the front end's c01 / depthwise launches: a grid of fewer
+// blocks than the chip's 256 CUs (a stream pass: a few rows) spreads each
+// row's frequency columns over 8 groups; larger grids keep one.
+static unsigned front_groups(unsigned blocks) { return blocks < 256 ? 8u : 1u; }
+
 int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp, float *x, int layers, const StreamPass *sp) {
   const fa_encoder_cfg &c = e->cfg;
   const fa_encoder_opts &o = e->opts;
@@ -1292,7 +1302,7 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
   // ── subsampling ──
   {
     ProfScope ps(ctx, "sub_c01");
-    FA_TRY(launch_c01(ctx, ps, dim3(cdiv(mx[2], 4), n), melp, MB, s0, s1, F1, s2, F2, e->c0w, e->c0b, e->c1w, e->c1b, (_Float16 *)e->W().s2, C, e->c01_lds,
+    FA_TRY(launch_c01(ctx, ps, dim3(cdiv(mx[2], 4), n, front_groups(cdiv(mx[2], 4) * n)), melp, MB, s0, s1, F1, s2, F2, e->c0w, e->c0b, e->c1w, e->c1b, (_Float16 *)e->W().s2, C, e->c01_lds,
                       g.pt, o.sub_pad_l, o.sub_pad_r, g.mel_src));
     FA_TRY(check_launch(ctx, "sub_c01"));
   }
@@ -1306,7 +1316,7 @@ int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *melp
   }
   {
     ProfScope ps(ctx, "sub_dw3");
-    FA_TRY(launch_dw(ctx, ps, dim3(cdiv(mx[3], 4), n), (const float *)e->W().s2p, s2, F2, s3, F3, e->c3w, e->c3b, (_Float16 *)e->W().s3, C,
+    FA_TRY(launch_dw(ctx, ps, dim3(cdiv(mx[3], 4), n, front_groups(cdiv(mx[3], 4) * n)), (const float *)e->W().s2p, s2, F2, s3, F3, e->c3w, e->c3b, (_Float16 *)e->W().s3, C,
                      sp ? nullptr : (int *)e->W().vrow, c.H * c.HD * Tp, layout == 1 ? mx[3] : 0, g.pt, o.sub_pad_l));
     FA_TRY(check_launch(ctx, "sub_dw3"));
   }
