@@ -522,13 +522,16 @@ def bench_e2e(args, fa, ctx):
     synthetic speech-like PCM -> log-mel -> 24-layer encoder (f16 weights) ->
     joint projection -> greedy TDT decode -> seam stitching, the reference's
     headline configuration (README.md:10-12: 1 h file, 293x RTFx on
-    Chrome/macOS WebGPU).  One step = one full transcription; value =
-    audio-s / wall-s (RTFx).  Synthetic weights: the tokens are meaningless,
-    every stage does its full work."""
+    Chrome/macOS WebGPU).  One step = one full transcription, pipelined
+    (fa_transcribe_groups: group g+1's mel / encoder / projection on an
+    encoder lane while group g decodes), groups of up to 32 windows; value =
+    audio-s / wall-s (RTFx).  The same transcription stage by stage
+    (pipelined=False) is timed beside it, and one stage-by-stage pass with a
+    synchronisation after each stage gives the stages' own times.  No profile
+    window is open.  Synthetic weights: the tokens are meaningless, every
+    stage does its full work."""
     import importlib
     pl = importlib.import_module(fa.__name__ + ".pipeline")
-    raise SystemExit("bench --workload e2e is switched off: its first run (1 h of audio in 64-window groups) faulted the GPU "
-                     "and the cause has not been found")
     seconds = args.audio_sec
     audio = fa.synth.make_pcm(seconds, seed=1)
     man = fa.synth.make_weights(dict(FULL), seed=1)
@@ -539,29 +542,64 @@ def bench_e2e(args, fa, ctx):
     W, b = fa.synth.make_joint_projection(2)
     projW, projB = ctx.upload(W, W.shape[0], W.shape[1]), ctx.upload(b.reshape(1, -1), 1, b.size)
     log(f"[bench] e2e: {seconds:.0f} s of audio, weights loaded")
-    for _ in range(args.warmup):
+    for _ in range(max(1, args.warmup)):
         r = pl.transcribeWindowed(ctx, enc, dec, projW, projB, audio)
-    ctx.startProfile(400000)
-    r = pl.transcribeWindowed(ctx, enc, dec, projW, projB, audio)
-    prof = ctx.endProfile()
-    stages = {}
-    for p in prof:
-        lab = p["label"]
-        st = "mel" if lab.startswith("mel") else "decode" if lab.startswith("tdt") else "pack" if lab.startswith("pack") else \
-             "projection" if lab.startswith("matmul") else "encoder"
-        stages[st] = stages.get(st, 0.0) + p["ms"]
+        rs = pl.transcribeWindowed(ctx, enc, dec, projW, projB, audio, pipelined=False)
+    assert r["ids"] == rs["ids"], "pipelined and stage-by-stage transcriptions differ"
+    log(f"[bench] e2e warm: {r['stats']}")
     ctx.sync()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         r = pl.transcribeWindowed(ctx, enc, dec, projW, projB, audio)
     wall = (time.perf_counter() - t0) / args.steps
+    t0 = time.perf_counter()
+    for _ in range(max(1, args.steps // 4)):
+        pl.transcribeWindowed(ctx, enc, dec, projW, projB, audio, pipelined=False)
+    wall_serial = (time.perf_counter() - t0) / max(1, args.steps // 4)
+    # the stages' own times: every group's stages one after another, synchronised
+    tsub = importlib.import_module(fa.__name__ + ".encoder").tsub
+    x = np.ascontiguousarray(audio, np.float32)
+    total = len(x)
+    starts = pl.planWindows(total, 240000, 208000)
+    groups = pl.groupWindows(starts, total, 240000, pl.MAX_WINDOWS)
+    pcm = ctx.upload(x.reshape(1, -1), 1, total)
+    stages = {"mel": 0.0, "encoder": 0.0, "projection": 0.0, "decode": 0.0}
+    for grp in groups:
+        st = [starts[i] for i in grp]
+        ln = [min(s_ + 240000, total) - s_ for s_ in st]
+        keep = [j for j, l in enumerate(ln) if l // 160 > 0]
+        if not keep:
+            continue
+        st, ln = [st[j] for j in keep], [ln[j] for j in keep]
+        T = [l // 160 for l in ln]
+        offs = np.concatenate([[0], np.cumsum(T)[:-1]]).astype(np.int32)
+        arena = ctx.pushArena()
+        t = time.perf_counter()
+        feats = ctx.melWindows(pcm, st, ln)
+        ctx.sync()
+        stages["mel"] += time.perf_counter() - t
+        t = time.perf_counter()
+        y = enc.forwardStream(feats, offs, T)
+        ctx.sync()
+        stages["encoder"] += time.perf_counter() - t
+        t = time.perf_counter()
+        proj = ctx.matmul(y, projW, bias=projB)
+        ctx.sync()
+        stages["projection"] += time.perf_counter() - t
+        t = time.perf_counter()
+        dec.decodeBatch(proj, [tsub(v) for v in T])
+        stages["decode"] += time.perf_counter() - t
+        ctx.popArena(arena)
+    ctx.freeTensor(pcm)
     line = {"metric": "end-to-end transcription RTFx (audio-s/wall-s) at 1 GPU", "value": round(seconds / wall, 1), "unit": "audio-s/wall-s",
             "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 2), "higher_is_better": True,
             "scaling": "weak", "vs_baseline": round(seconds / wall / 293.0, 2), "baseline_note": "293x RTFx, 1 h file, Chrome/macOS WebGPU (README.md:10-12); other hardware",
             "dtype": "f16", "data": "synthetic speech-like PCM, random-init encoder/decoder/projection weights",
-            "config": {"workload": f"{seconds:.0f} s PCM, 15 s windows at 13 s hop, groups of up to 64 windows, Parakeet TDT 0.6B shapes (24 layers)",
+            "config": {"workload": f"{seconds:.0f} s PCM, 15 s windows at 13 s hop, groups of up to {pl.MAX_WINDOWS} windows, Parakeet TDT 0.6B shapes "
+                                   "(24 layers), pipelined: group g+1's mel / encoder / projection on an encoder lane while group g decodes",
                        "windows": r["stats"]["windows"], "groups": r["stats"]["groups"], "tokens": r["stats"]["tokens"]},
-            "stages_ms": {k: round(v, 2) for k, v in sorted(stages.items(), key=lambda kv: -kv[1])}}
+            "stage_by_stage": {"ms_per_step": round(wall_serial * 1e3, 2), "value": round(seconds / wall_serial, 1)},
+            "stages_ms": {k: round(v * 1e3, 2) for k, v in stages.items()}}
     if not args.no_cpu:
         # one window through the oracle: mel + preEncode + 1 layer (scaled to 24) + decode of the window's frames
         orc = ge.load_oracle()

@@ -8,7 +8,9 @@ import ctypes as C
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libfa_hip.so")
+# FA_LIB_PATH names another build of the same C ABI (the launch-audit build
+# of tests/audit, which runs the host code against a stand-in runtime)
+LIB_PATH = os.environ.get("FA_LIB_PATH") or os.path.join(HERE, "libfa_hip.so")
 
 FA_OK, FA_E_INVALID, FA_E_STATE, FA_E_DEVICE, FA_E_OOM, FA_E_UNSUPPORTED = range(6)
 ACT = {"none": 0, "gelu": 1, "tanh": 2, "relu": 3, "silu": 4, "gelu_erf": 5}
@@ -117,6 +119,7 @@ SIGNATURES = [
     ("fa_tdt_load", I, [P, C.POINTER(C.POINTER(C.c_float)), C.POINTER(P)]),
     ("fa_tdt_destroy", None, [P]),
     ("fa_tdt_decode", I, [P, T, I32P, I, I, I32P, I32P, I32P]),
+    ("fa_transcribe_groups", I, [P, P, P, T, I, I32P, I32P, I32P, T, T, I, C.c_double, I, I, I32P, I32P, I32P, I32P]),
     ("fa_window_row_map", I, [P, I32P, I, I, I, I32P, C.POINTER(I)]),
     ("fa_encoder_load", I, [P, C.POINTER(EncoderCfg), I, C.POINTER(C.c_char_p), C.POINTER(F32P), C.POINTER(C.c_int64), I, I, C.POINTER(P)]),
     ("fa_encoder_destroy", None, [P]),

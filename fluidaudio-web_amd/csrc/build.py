@@ -16,7 +16,7 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 OUT = os.path.join(PKG, "libfa_hip.so")
-SOURCES = ["runtime.hip", "gemm.hip", "gemm_q8.hip", "gemm_q4.hip", "attention.hip", "ops.hip", "quant.hip", "encoder.hip", "pack.hip", "mel.hip", "tdt.hip", "ops_aux.hip", "stream.hip"]
+SOURCES = ["runtime.hip", "gemm.hip", "gemm_q8.hip", "gemm_q4.hip", "attention.hip", "ops.hip", "quant.hip", "encoder.hip", "pack.hip", "mel.hip", "tdt.hip", "ops_aux.hip", "stream.hip", "transcribe.hip"]
 # per-source flags: the log-mel and TDT-decoder kernels restate the
 # reference's JS / wasm arithmetic, so no multiply-add may be fused there
 EXTRA = {"mel.hip": ["-ffp-contract=off"], "tdt.hip": ["-ffp-contract=off"], "ops_aux.hip": ["-ffp-contract=off"]}

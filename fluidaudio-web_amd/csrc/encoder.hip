@@ -1611,43 +1611,46 @@ __global__ void set_mel_src_kernel(MelSrc v, MelSrc *dst) {
   if (threadIdx.x < kMaxWin) dst->start[threadIdx.x] = v.start[threadIdx.x];
 }
 
-// Shared body of fa_encoder_forward (mel: time-major rows, stream_ttot 0) and
-// fa_encoder_forward_stream (mel: channel-major stream [melBins, stream_ttot],
-// starts: the windows' first columns).
-static int encoder_forward_impl(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t *starts, long stream_ttot, const int32_t *lens, int n,
-                                int layout, int layers_run, fa_tensor *out, const char *who) {
+// The forward over one batch of windows, from raw device pointers.  mel is
+// either time-major rows [R0, melBins] (stream false) or the channel-major
+// feature stream [melBins, mel_cols] whose windows start at columns starts[]
+// (stream true).  xout: the [M, D] f32 result goes there; null: it stays in
+// the workspace's xw (valid until the next forward in this workspace) and
+// *xres names it.
+int fa::encoder_forward_dev(fa_ctx *ctx, fa_encoder *e, const float *mel, int mel_rows, long mel_cols, bool stream, const int32_t *starts,
+                        const int32_t *lens, int n, int layout, int layers_run, float *xout, const float **xres, int *M_out, const char *who) {
   if (!e || e->ctx != ctx) return set_err(ctx, FA_E_INVALID, "%s: encoder belongs to another context", who);
   if (n <= 0) return set_err(ctx, FA_E_INVALID, "%s: no windows", who);
   // At most 32 windows per batch: the largest batch validated on the GPU.  A
   // 64-window batch inside a one-hour windowed transcription once faulted the
   // GPU with no cause shown yet, so larger batches are refused here rather
   // than only by the Python pipeline.
-  constexpr int kMaxEncWin = 32;
+#ifndef FA_ENC_MAX_WINDOWS  // raised only by the launch-audit build (tests/audit), never shipped
+#define FA_ENC_MAX_WINDOWS 32
+#endif
+  constexpr int kMaxEncWin = FA_ENC_MAX_WINDOWS;
   static_assert(kMaxEncWin <= kMaxWin, "window tables");
   if (n > kMaxEncWin) return set_err(ctx, FA_E_UNSUPPORTED, "%s: %d windows in one batch (max %d)", who, n, kMaxEncWin);
   if (layout != 0 && layout != 1) return set_err(ctx, FA_E_INVALID, "%s: layout %d", who, layout);
   const fa_encoder_cfg &c = e->cfg;
   const int D = c.D, MB = c.melBins;
-  TensorRec *rm;
-  FA_TRY(need(ctx, mel, &rm, who));
-  const bool stream = starts != nullptr;
-  if (!stream && (rm->kind != S_F32 || rm->cols != MB)) return set_err(ctx, FA_E_INVALID, "%s: mel must be f32 [rows, %d]", who, MB);
-  if (stream && (rm->kind != S_F32 || rm->rows != MB)) return set_err(ctx, FA_E_INVALID, "%s: features must be f32 [%d, T]", who, MB);
+  if (!stream && mel_cols != MB) return set_err(ctx, FA_E_INVALID, "%s: mel must be f32 [rows, %d]", who, MB);
+  if (stream && mel_rows != MB) return set_err(ctx, FA_E_INVALID, "%s: features must be f32 [%d, T]", who, MB);
   PassGeom g;
   FA_TRY(pass_geometry(ctx, e, lens, n, layout, e->opts.sub_pad_t, e->opts.sub_pad_b, &g));
   MelSrc src{};
   if (stream) {
-    stream_ttot = rm->cols;
-    src.ttot = stream_ttot;
+    src.ttot = mel_cols;
     for (int i = 0; i < n; i++) {
-      if (starts[i] < 0 || (long)starts[i] + lens[i] > stream_ttot)
-        return set_err(ctx, FA_E_INVALID, "%s: window %d [%d, +%d) outside the %ld-frame stream", who, i, starts[i], lens[i], stream_ttot);
+      if (starts[i] < 0 || (long)starts[i] + lens[i] > mel_cols)
+        return set_err(ctx, FA_E_INVALID, "%s: window %d [%d, +%d) outside the %ld-frame stream", who, i, starts[i], lens[i], mel_cols);
       src.start[i] = starts[i];
     }
-  } else if (rm->rows < g.R[0]) {
-    return set_err(ctx, FA_E_INVALID, "%s: mel has %d rows, windows need %d", who, rm->rows, g.R[0]);
+  } else if (mel_rows < g.R[0]) {
+    return set_err(ctx, FA_E_INVALID, "%s: mel has %d rows, windows need %d", who, mel_rows, g.R[0]);
   }
   const int M = g.M;
+  if (M_out) *M_out = M;
   const int layers = layers_run < 0 ? c.layers : std::min(layers_run, c.layers);
   FA_TRY(pass_workspace(ctx, e, g, layers, false));
   const char *ge = getenv("FA_GRAPH");
@@ -1656,27 +1659,19 @@ static int encoder_forward_impl(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const
     FA_TRY(grow(e, &e->W().msrc, &e->W().cap_msrc, sizeof(MelSrc)));
     g.mel_src = (const MelSrc *)e->W().msrc;
   }
-  if (use_graph) {
-    if (!stream) FA_TRY(grow(e, &e->W().melw, &e->W().cap_melw, (size_t)g.R[0] * MB * 4));
-    FA_TRY(grow(e, &e->W().xw, &e->W().cap_xw, (size_t)M * D * 4));
-  }
-  fa_tensor ox;
-  TensorRec *rx;
-  FA_TRY(new_tensor(ctx, M, D, S_F32, (size_t)M * D * 4, &ox, &rx));
-  TensorGuard og(ctx, ox);  // released unless the forward is queued
-  rm = get(ctx, mel);
-  float *const xout = (float *)rx->ptr;
+  if (use_graph && !stream) FA_TRY(grow(e, &e->W().melw, &e->W().cap_melw, (size_t)g.R[0] * MB * 4));
+  if (use_graph || !xout) FA_TRY(grow(e, &e->W().xw, &e->W().cap_xw, (size_t)M * D * 4));
+  float *const x = xout ? xout : (float *)e->W().xw;
+  if (xres) *xres = (const float *)e->W().xw;
   auto set_src = [&]() -> int {
-    src.ptr = (const float *)rm->ptr;
+    src.ptr = mel;
     ProfScope ps(ctx, "enc_src");
     FA_LAUNCH(ps, set_mel_src_kernel, dim3(1), dim3(64), 0, ctx->stream, src, (MelSrc *)e->W().msrc);
     return check_launch(ctx, "enc_src");
   };
   if (!use_graph) {  // profiling (its events are per launch) or FA_GRAPH=0
     if (stream) FA_TRY(set_src());
-    FA_TRY(pass_launch(ctx, e, g, (const float *)rm->ptr, xout, layers, nullptr));
-    *out = og.release();
-    return FA_OK;
+    return pass_launch(ctx, e, g, mel, x, layers, nullptr);
   }
   // The whole forward is a fixed kernel sequence for a given signature: it is
   // captured once into a hipGraph and replayed (one submission instead of
@@ -1690,8 +1685,31 @@ static int encoder_forward_impl(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const
   FA_TRY(encoder_graph_run(
       ctx, e, key,
       [&]() { return pass_launch(ctx, e, g, stream ? nullptr : (const float *)e->W().melw, (float *)e->W().xw, layers, nullptr); },
-      [&]() { return stream ? set_src() : copy_f4(ctx, rm->ptr, e->W().melw, (size_t)g.R[0] * MB * 4, "enc_in"); }));
-  FA_TRY(copy_f4(ctx, e->W().xw, xout, (size_t)M * D * 4, "enc_out"));
+      [&]() { return stream ? set_src() : copy_f4(ctx, mel, e->W().melw, (size_t)g.R[0] * MB * 4, "enc_in"); }));
+  if (xout) FA_TRY(copy_f4(ctx, e->W().xw, xout, (size_t)M * D * 4, "enc_out"));
+  return FA_OK;
+}
+
+// Shared body of fa_encoder_forward (mel: time-major rows) and
+// fa_encoder_forward_stream (mel: channel-major stream [melBins, T],
+// starts: the windows' first columns): the output tensor around
+// encoder_forward_dev.
+static int encoder_forward_impl(fa_ctx *ctx, fa_encoder *e, fa_tensor mel, const int32_t *starts, long, const int32_t *lens, int n,
+                                int layout, int layers_run, fa_tensor *out, const char *who) {
+  if (!e || e->ctx != ctx) return set_err(ctx, FA_E_INVALID, "%s: encoder belongs to another context", who);
+  if (n <= 0) return set_err(ctx, FA_E_INVALID, "%s: no windows", who);
+  TensorRec *rm;
+  FA_TRY(need(ctx, mel, &rm, who));
+  if (rm->kind != S_F32) return set_err(ctx, FA_E_INVALID, "%s: %s must be f32", who, starts ? "features" : "mel");
+  PassGeom g;
+  FA_TRY(pass_geometry(ctx, e, lens, n, layout == 1 ? 1 : 0, e->opts.sub_pad_t, e->opts.sub_pad_b, &g));
+  fa_tensor ox;
+  TensorRec *rx;
+  FA_TRY(new_tensor(ctx, g.M, e->cfg.D, S_F32, (size_t)g.M * e->cfg.D * 4, &ox, &rx));
+  TensorGuard og(ctx, ox);  // released unless the forward is queued
+  rm = get(ctx, mel);
+  FA_TRY(encoder_forward_dev(ctx, e, (const float *)rm->ptr, rm->rows, rm->cols, starts != nullptr, starts, lens, n, layout, layers_run,
+                             (float *)rx->ptr, nullptr, nullptr, who));
   *out = og.release();
   return FA_OK;
 }

@@ -155,6 +155,11 @@ struct StreamPass {
 int pass_geometry(fa_ctx *ctx, const fa_encoder *e, const int32_t *lens, int n, int layout, int pt, int pb, PassGeom *g);
 int pass_workspace(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, int layers, bool stream);
 int pass_launch(fa_ctx *ctx, fa_encoder *e, const PassGeom &g, const float *mel, float *x, int layers, const StreamPass *sp);
+// One batched forward from raw device pointers (encoder.hip): the feature
+// stream [melBins, mel_cols] (stream) or time-major mel rows; the result goes
+// to xout, or stays in the current workspace's xw (xout null, *xres names it).
+int encoder_forward_dev(fa_ctx *ctx, fa_encoder *e, const float *mel, int mel_rows, long mel_cols, bool stream, const int32_t *starts,
+                        const int32_t *lens, int n, int layout, int layers_run, float *xout, const float **xres, int *M_out, const char *who);
 int encoder_grow(fa_encoder *e, void **buf, size_t *cap, size_t need);
 // frees a workspace's buffers and captured forwards (the device must be idle for them)
 void encoder_ws_free(EncWs &w);

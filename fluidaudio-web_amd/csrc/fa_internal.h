@@ -154,6 +154,11 @@ int check_launch(fa_ctx *ctx, const char *what);
 // Looks up the allocation-free mel path's static device array for ctx->device
 // (once per device; mel.hip).  Called by fa_ctx_create with the device current.
 int mel_static_init(fa_ctx *ctx);
+// Log-mel internals shared with the windowed-transcription runner (mel.hip).
+int tdt_decode_dev(fa_tdt *d, const float *fr, long rows, const int32_t *lens, int n, int cap, int32_t *ids, int32_t *frame_idx, int32_t *counts);
+int mel_prepare(fa_ctx *ctx, int n, int n_mels, int normalize);
+int mel_windows_dev(fa_ctx *ctx, const float *pcm, long nsamp, const int32_t *starts, const int32_t *lens, int n, int n_mels, double log_guard,
+                    int normalize, float *y, long *total);
 
 inline unsigned cdiv(long a, long b) { return (unsigned)((a + b - 1) / b); }
 

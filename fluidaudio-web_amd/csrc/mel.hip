@@ -398,6 +398,38 @@ int mel_static_init(fa_ctx *ctx) {
   return FA_OK;
 }
 
+// The constant tables for n_mels bins and the statistics scratch for n
+// windows (growing either waits for the context stream), so that later
+// calls for at most n windows allocate nothing.
+int mel_prepare(fa_ctx *ctx, int n, int n_mels, int normalize) {
+  FA_TRY(ensure_tables(ctx, n_mels));
+  const size_t sbytes = (size_t)std::min(std::max(n, 1), kMaxWin) * n_mels * 2 * sizeof(double);
+  if (normalize && ctx->mel_scratch_bytes < sbytes) {
+    if (ctx->mel_scratch) {
+      FA_HIP(ctx, hipStreamSynchronize(ctx->stream));
+      (void)hipFree(ctx->mel_scratch);
+      ctx->mel_scratch = nullptr;
+      ctx->mel_scratch_bytes = 0;
+    }
+    if (!(ctx->mel_scratch = dev_alloc(ctx, sbytes))) return FA_E_OOM;
+    ctx->mel_scratch_bytes = sbytes;
+  }
+  return FA_OK;
+}
+
+// The log-mel features of n windows of a resident PCM stream into y
+// [n_mels, *total] on the context stream (after mel_prepare for n windows).
+int mel_windows_dev(fa_ctx *ctx, const float *pcm, long nsamp, const int32_t *starts, const int32_t *lens, int n, int n_mels, double log_guard,
+                    int normalize, float *y, long *total) {
+  FA_TRY(mel_check(ctx, nsamp, starts, lens, n, n_mels, log_guard, total));
+  FA_TRY(mel_prepare(ctx, n, n_mels, normalize));
+  if (*total == 0) return FA_OK;
+  const MelTab *tab = (const MelTab *)ctx->mel_tab;
+  const float *fb = (const float *)((const char *)ctx->mel_tab + kTabFb);
+  const int *bounds = (const int *)((const char *)ctx->mel_tab + kTabFb + (size_t)n_mels * kBins * 4);
+  return mel_launch(ctx, pcm, nsamp, starts, lens, n, n_mels, log_guard, normalize, *total, y, tab, fb, bounds, (double *)ctx->mel_scratch);
+}
+
 }  // namespace fa
 
 using namespace fa;
@@ -412,32 +444,13 @@ int fa_mel_windows(fa_ctx *ctx, fa_tensor pcm, const int32_t *starts, const int3
   const long nsamp = (long)rp->rows * rp->cols;
   long total = 0;
   FA_TRY(mel_check(ctx, nsamp, starts, lens, n, n_mels, log_guard, &total));
-  FA_TRY(ensure_tables(ctx, n_mels));
+  FA_TRY(mel_prepare(ctx, n, n_mels, normalize));
   fa_tensor o;
   TensorRec *ro;
   FA_TRY(new_tensor(ctx, n_mels, (int)total, S_F32, (size_t)n_mels * total * 4, &o, &ro));
   TensorGuard og(ctx, o);  // released unless the op completes
   rp = get(ctx, pcm);
-  if (total == 0) {
-    *out = og.release();
-    return FA_OK;
-  }
-  const size_t sbytes = (size_t)std::min(n, kMaxWin) * n_mels * 2 * sizeof(double);
-  if (normalize && ctx->mel_scratch_bytes < sbytes) {
-    if (ctx->mel_scratch) {
-      FA_HIP(ctx, hipStreamSynchronize(ctx->stream));
-      (void)hipFree(ctx->mel_scratch);
-      ctx->mel_scratch = nullptr;
-      ctx->mel_scratch_bytes = 0;
-    }
-    if (!(ctx->mel_scratch = dev_alloc(ctx, sbytes))) return FA_E_OOM;
-    ctx->mel_scratch_bytes = sbytes;
-  }
-  const MelTab *tab = (const MelTab *)ctx->mel_tab;
-  const float *fb = (const float *)((const char *)ctx->mel_tab + kTabFb);
-  const int *bounds = (const int *)((const char *)ctx->mel_tab + kTabFb + (size_t)n_mels * kBins * 4);
-  FA_TRY(mel_launch(ctx, (const float *)rp->ptr, nsamp, starts, lens, n, n_mels, log_guard, normalize, total, (float *)ro->ptr, tab, fb, bounds,
-                    (double *)ctx->mel_scratch));
+  if (total > 0) FA_TRY(mel_windows_dev(ctx, (const float *)rp->ptr, nsamp, starts, lens, n, n_mels, log_guard, normalize, (float *)ro->ptr, &total));
   *out = og.release();
   return FA_OK;
 }

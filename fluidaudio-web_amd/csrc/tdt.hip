@@ -604,6 +604,15 @@ int fa_tdt_decode(fa_tdt *d, fa_tensor frames, const int32_t *lens, int n, int c
   TensorRec *rf;
   FA_TRY(need(ctx, frames, &rf, "tdtDecode"));
   if (rf->kind != S_F32 || rf->cols != TH) return set_err(ctx, FA_E_INVALID, "tdtDecode: frames must be f32 [rows, %d] (pre-projected)", TH);
+  return fa::tdt_decode_dev(d, (const float *)rf->ptr, rf->rows, lens, n, cap, ids, frame_idx, counts);
+}
+
+}  // extern "C"
+
+// The decode of n windows whose projected frames are rows of fr ([rows,
+// 640] f32 on the device), on the context stream; the host waits for it.
+int fa::tdt_decode_dev(fa_tdt *d, const float *fr, long rows, const int32_t *lens, int n, int cap, int32_t *ids, int32_t *frame_idx, int32_t *counts) {
+  fa_ctx *ctx = d->ctx;
   if (n <= 0 || n > kMaxWin) return set_err(ctx, FA_E_INVALID, "tdtDecode: %d windows (1..%d)", n, kMaxWin);
   if (cap <= 0) return set_err(ctx, FA_E_INVALID, "tdtDecode: capacity %d", cap);
   std::vector<TdtWin> win(n);
@@ -615,7 +624,7 @@ int fa_tdt_decode(fa_tdt *d, fa_tensor frames, const int32_t *lens, int n, int c
     off += lens[i];
     tmax = std::max(tmax, lens[i]);
   }
-  if (off > rf->rows) return set_err(ctx, FA_E_INVALID, "tdtDecode: %ld frames in the windows, %d in the tensor", off, rf->rows);
+  if (off > rows) return set_err(ctx, FA_E_INVALID, "tdtDecode: %ld frames in the windows, %ld in the tensor", off, rows);
   // state layout
   size_t o = 0;
   auto take = [&](size_t bytes) {
@@ -651,8 +660,6 @@ int fa_tdt_decode(fa_tdt *d, fa_tensor frames, const int32_t *lens, int n, int c
   st.ids = (int *)(base + o_ids);
   st.frs = (int *)(base + o_frs);
   st.alive = (int *)(base + o_act);
-  rf = get(ctx, frames);
-  const float *fr = (const float *)rf->ptr;
   constexpr int zg = 2;  // emitting windows per LSTM block (measured: 2 < 4 < 8)
   FA_HIP(ctx, hipMemsetAsync(base + o_h, 0, o_pp - o_h, ctx->stream));  // both state slots = 0
   FA_HIP(ctx, hipMemsetAsync(st.alive, 0, 4ul * n, ctx->stream));
@@ -708,4 +715,4 @@ int fa_tdt_decode(fa_tdt *d, fa_tensor frames, const int32_t *lens, int n, int c
   return FA_OK;
 }
 
-}  // extern "C"
+

@@ -6,13 +6,18 @@ featurised, encoded, projected and decoded on the GPU, and the per-window
 tokens are merged by the reference's seam stitcher (stitcher.js:7-41).
 
 The reference overlaps three stages across CPU and GPU (mel and the WASM
-decode on the CPU, the encoder on the GPU).  Here every stage runs on the GPU
-on the context's stream, so the host only plans windows and stitches tokens:
+decode on the CPU, the encoder on the GPU).  Here every stage runs on the GPU,
+so the host only plans windows and stitches tokens:
   PCM (uploaded once) -> fa_mel_windows (all windows of a group)
     -> fa_encoder_forward_stream (ragged batch read in place from the stream)
     -> matmul(projW, projB) -> fa_tdt_decode (all windows in lock-step)
     -> tokens back to the host -> stitch.
-Projected frames never leave the device.  A group holds up to `wb` windows
+Pipelined (the default, like the reference's): the whole group loop is one
+native call, fa_transcribe_groups, which queues group g+1's mel, encoder and
+projection on an encoder lane before group g decodes on the context stream.
+pipelined=False runs the stages one call at a time (the reference's serial
+gate baseline); both give the same tokens.  Projected frames never leave the
+device.  A group holds up to `wb` windows
 (at most 32, the largest encoder batch validated on the GPU; one run with
 64-window groups over an hour of audio faulted the GPU and its cause has not
 been found): the encoder's GEMMs and the decoder's steps both get cheaper per
@@ -68,13 +73,15 @@ def _js_round(x: float) -> int:
 
 
 def transcribeWindowed(ctx, enc, dec, projW, projB, samples, sampleRate: int = 16000, windowSec: float = 15, overlapSec: float = 2,
-                       wb: int = MAX_WINDOWS, keepFrames: bool = False) -> dict:
+                       wb: int = MAX_WINDOWS, keepFrames: bool = False, pipelined: bool = True) -> dict:
     """pipeline.js:31 transcribeWindowed(ctx, enc, dec, mel, projW, projB,
     samples, opts) with the GPU stages: enc a FusedEncoder, dec a TdtDecoder,
     projW / projB device tensors [D, 640] / [1, 640] (the decoder manifest's
     encW / encB).  Returns {"ids", "idTimes", "stats"} like the reference;
     keepFrames=True adds "frames" (each window's projected frames, host copies)
-    for checks."""
+    for checks (stage by stage).  pipelined=True runs the group loop as one
+    native call (fa_transcribe_groups) with group g+1's encoder overlapping
+    group g's decode."""
     if not 1 <= wb <= MAX_WINDOWS:
         raise ValueError(f"wb={wb}: 1..{MAX_WINDOWS} windows per group")
     t_start = time.perf_counter()
@@ -94,6 +101,14 @@ def transcribeWindowed(ctx, enc, dec, projW, projB, samples, sampleRate: int = 1
     from .encoder import tsub
 
     pcm = ctx.upload(x.reshape(1, -1), 1, total)
+    if pipelined and not keepFrames:
+        try:
+            _run_pipelined(ctx, enc, dec, projW, projB, pcm, starts, groups, winSamples, total, stitch, stats)
+        finally:
+            ctx.freeTensor(pcm)
+        stats["tokens"] = len(ids)
+        stats["wallMs"] = (time.perf_counter() - t_start) * 1e3
+        return {"ids": ids, "idTimes": idTimes, "stats": stats}
     try:
         for grp in groups:
             st = [starts[i] for i in grp]
@@ -132,3 +147,41 @@ def transcribeWindowed(ctx, enc, dec, projW, projB, samples, sampleRate: int = 1
     if keepFrames:
         out["frames"] = frames_out
     return out
+
+
+def _run_pipelined(ctx, enc, dec, projW, projB, pcm, starts, groups, winSamples, total, stitch, stats):
+    """The group loop as one fa_transcribe_groups call, then the seam
+    stitcher over the windows in order (zero-length mels are dropped, as the
+    reference's mel scheduler drops them)."""
+    import ctypes as C
+
+    from . import _lib as L
+    from .decoder import MAX_OUT_PER_WINDOW
+
+    win, lns, counts = [], [], []
+    for grp in groups:
+        kept = [(w, min(starts[w] + winSamples, total) - starts[w]) for w in grp]
+        kept = [(w, l) for w, l in kept if l // HOP > 0]
+        if kept:
+            counts.append(len(kept))
+            win += [w for w, _ in kept]
+            lns += [l for _, l in kept]
+    if not win:
+        return
+    nw, cap = len(win), MAX_OUT_PER_WINDOW
+    st = np.asarray([starts[w] for w in win], np.int32)
+    ln = np.asarray(lns, np.int32)
+    cn = np.asarray(counts, np.int32)
+    ids = np.empty((nw, cap), np.int32)
+    frs = np.empty((nw, cap), np.int32)
+    nout = np.empty(nw, np.int32)
+    ts = np.empty(nw, np.int32)
+    I = L.I32P
+    L.check(ctx._p, L.lib().fa_transcribe_groups(ctx._p, enc._p, dec._p, pcm.h, len(cn), cn.ctypes.data_as(I), st.ctypes.data_as(I),
+                                                 ln.ctypes.data_as(I), projW.h, projB.h if projB is not None else 0, int(enc.cfg["melBins"]), C.c_double(2.0 ** -24),
+                                                 1, cap, ids.ctypes.data_as(I), frs.ctypes.data_as(I), nout.ctypes.data_as(I), ts.ctypes.data_as(I)))
+    for i, w in enumerate(win):
+        k = min(int(nout[i]), cap)
+        stitch(w, int(ln[i]), int(ts[i]), ids[i, :k].tolist(), frs[i, :k].tolist())
+    stats["windows"] += nw
+    stats["groups"] += len(cn)

@@ -262,6 +262,25 @@ typedef struct fa_tdt fa_tdt;
 int fa_tdt_load(fa_ctx *ctx, const float *const *w, fa_tdt **out);
 void fa_tdt_destroy(fa_tdt *dec);
 int fa_tdt_decode(fa_tdt *dec, fa_tensor frames, const int32_t *lens, int n, int cap, int32_t *ids, int32_t *frame_idx, int32_t *counts);
+/* Windowed transcription's device stages, pipelined (replaces the group loop
+ * of src/engines/asr-parakeet/pipeline.js:32-143 transcribeWindowed with the
+ * GPU decoder): n_groups groups of windows of one resident f32 PCM tensor,
+ * group g = the next counts[g] (1..32) windows of starts/lens (samples; every
+ * window must hold at least one 160-sample mel hop).  Per group: log-mel
+ * features (fa_mel_windows with n_mels = the encoder's bins, log_guard,
+ * normalize), the encoder forward over the group read in place from them
+ * (fa_encoder_forward_stream, packed layout), the joint projection
+ * x @ projW (+ projB) (f32 [D, 640], [640]; fa_matmul's f32 route), and the
+ * greedy TDT decode (fa_tdt_decode with capacity cap).  Group g+1's mel,
+ * encoder and projection are queued on an encoder lane before group g
+ * decodes on the context stream, so they overlap; the results equal the
+ * stage-by-stage calls bit for bit.  Outputs per window w (in plan order):
+ * ids / frame_idx [w * cap, +cap), n_out[w] (tokens emitted, may exceed cap),
+ * tsub[w] (encoder frames).  Buffers are the call's own (two groups' worth);
+ * the call returns when everything it queued has finished. */
+int fa_transcribe_groups(fa_ctx *ctx, fa_encoder *enc, fa_tdt *dec, fa_tensor pcm, int n_groups, const int32_t *counts, const int32_t *starts,
+                         const int32_t *lens, fa_tensor projW, fa_tensor projB, int n_mels, double log_guard, int normalize, int cap, int32_t *ids,
+                         int32_t *frame_idx, int32_t *n_out, int32_t *tsub);
 
 /* ── log-mel front end (PCM windows -> the feature stream above) ─────────────
  * Replaces ParakeetMel.process (src/engines/asr-parakeet/parakeet-mel.js:14-22)

@@ -1,0 +1,114 @@
+"""Builds the launch-audit library: the product's own objects
+(fluidaudio-web_amd/csrc/_build/*.o, written by build()) linked with the
+host-only HIP stand-in in launch_audit.cpp instead of the HIP runtime, and the
+table of every kernel's argument layout read from the gfx950 code objects
+inside those objects (the AMDGPU metadata note: argument offsets, sizes and
+kinds, maximum workgroup size, static LDS and scratch).
+
+    python tests/audit/build_audit.py [--max-windows N]
+
+--max-windows recompiles encoder.hip with FA_ENC_MAX_WINDOWS=N for the audit
+build only (the shipped library keeps its limit).  Outputs go to
+tests/audit/_build/ (libfa_hip_audit.so, kernargs.txt).
+"""
+from __future__ import annotations
+
+import os
+import struct
+import subprocess
+import sys
+
+import msgpack
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+CSRC = os.path.join(ROOT, "fluidaudio-web_amd", "csrc")
+OUT = os.path.join(HERE, "_build")
+MAGIC = b"__CLANG_OFFLOAD_BUNDLE__"
+
+
+def _code_objects(blob: bytes):
+    """gfx950 code objects of every offload bundle in an object file."""
+    pos = blob.find(MAGIC)
+    while pos >= 0:
+        n = struct.unpack_from("<Q", blob, pos + 24)[0]
+        p = pos + 32
+        for _ in range(n):
+            off, size, tlen = struct.unpack_from("<QQQ", blob, p)
+            triple = blob[p + 24:p + 24 + tlen].decode()
+            p += 24 + tlen
+            if "gfx950" in triple and size:
+                yield blob[pos + off:pos + off + size]
+        pos = blob.find(MAGIC, pos + 1)
+
+
+def _metadata(elf: bytes) -> dict:
+    """The NT_AMDGPU_METADATA note (msgpack) of an ELF64 code object."""
+    shoff = struct.unpack_from("<Q", elf, 0x28)[0]
+    shentsize, shnum = struct.unpack_from("<HH", elf, 0x3A)
+    for i in range(shnum):
+        sh = shoff + i * shentsize
+        stype = struct.unpack_from("<I", elf, sh + 4)[0]
+        if stype != 7:  # SHT_NOTE
+            continue
+        off, size = struct.unpack_from("<QQ", elf, sh + 0x18)
+        p = off
+        while p < off + size:
+            namesz, descsz, ntype = struct.unpack_from("<III", elf, p)
+            name = elf[p + 12:p + 12 + namesz]
+            dpos = p + 12 + ((namesz + 3) & ~3)
+            if ntype == 32 and name.startswith(b"AMDGPU"):
+                return msgpack.unpackb(elf[dpos:dpos + descsz], raw=False, strict_map_key=False)
+            p = dpos + ((descsz + 3) & ~3)
+    return {}
+
+
+def kernarg_table(objs) -> list[str]:
+    lines = {}
+    for o in objs:
+        blob = open(o, "rb").read()
+        for co in _code_objects(blob):
+            for k in _metadata(co).get("amdhsa.kernels", []):
+                args = k.get(".args", [])
+                fields = [k[".name"], str(k.get(".max_flat_workgroup_size", 1024)), str(k.get(".group_segment_fixed_size", 0)),
+                          str(k.get(".private_segment_fixed_size", 0)), str(len(args))]
+                for a in args:
+                    fields += [str(a[".offset"]), str(a[".size"]), a[".value_kind"]]
+                lines[k[".name"]] = " ".join(fields)
+    return list(lines.values())
+
+
+def build(max_windows: int | None = None) -> str:
+    os.makedirs(OUT, exist_ok=True)
+    objs = [os.path.join(CSRC, "_build", f) for f in sorted(os.listdir(os.path.join(CSRC, "_build"))) if f.endswith(".o")]
+    if not objs:
+        raise RuntimeError("no objects in fluidaudio-web_amd/csrc/_build: run __graft_entry__.build() first")
+    if max_windows:
+        spec = __import__("importlib.util").util.spec_from_file_location("fa_build", os.path.join(CSRC, "build.py"))
+        b = __import__("importlib.util").util.module_from_spec(spec)
+        spec.loader.exec_module(b)
+        enc = os.path.join(OUT, f"encoder_w{max_windows}.o")
+        cmd = [b.HIPCC, *b.FLAGS, f"-DFA_ENC_MAX_WINDOWS={max_windows}", "-c", os.path.join(CSRC, "encoder.hip"), "-o", enc]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode:
+            raise RuntimeError(r.stderr)
+        objs = [enc if os.path.basename(o) == "encoder.o" else o for o in objs]
+    fake = os.path.join(OUT, "launch_audit.o")
+    r = subprocess.run(["g++", "-std=c++17", "-O1", "-fPIC", "-I/opt/rocm/include", "-c", os.path.join(HERE, "launch_audit.cpp"), "-o", fake],
+                       capture_output=True, text=True)
+    if r.returncode:
+        raise RuntimeError(r.stderr)
+    tag = f"_w{max_windows}" if max_windows else ""
+    lib = os.path.join(OUT, f"libfa_hip_audit{tag}.so")
+    r = subprocess.run(["g++", "-shared", "-fPIC", "-Wl,-Bsymbolic", "-o", lib, *objs, fake], capture_output=True, text=True)
+    if r.returncode:
+        raise RuntimeError(r.stderr)
+    tab = kernarg_table(objs)
+    with open(os.path.join(OUT, f"kernargs{tag}.txt"), "w") as f:
+        f.write("\n".join(tab) + "\n")
+    return lib
+
+
+if __name__ == "__main__":
+    mw = int(sys.argv[sys.argv.index("--max-windows") + 1]) if "--max-windows" in sys.argv else None
+    print(build(mw))

@@ -1,0 +1,200 @@
+"""Scenarios run against the launch-audit build (build_audit.py), one per
+process:
+
+    FA_LIB_PATH=.../libfa_hip_audit.so FA_AUDIT_KERNARGS=.../kernargs.txt \
+        python tests/audit/plans.py <scenario>
+
+Each prints one JSON line: the stand-in runtime's violations and counters.
+Kernels do not run, so device buffers hold what the host wrote (zeros after
+allocation); only host-side control flow that reads device results (the TDT
+decoder's live-window count) sees those zeros and ends early.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import json
+import os
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, ROOT)
+
+FULL = dict(D=1024, DFF=4096, H=8, HD=128, layers=24, dwK=9, Csub=256, Fsub=16, melBins=128)
+# FA_AUDIT_LAYERS: fewer encoder layers (same shapes per layer, fewer launches) for quicker plans
+if os.environ.get("FA_AUDIT_LAYERS"):
+    FULL["layers"] = int(os.environ["FA_AUDIT_LAYERS"])
+
+
+def report(L, extra=None):
+    buf = C.create_string_buffer(1 << 20)
+    cnt = (C.c_ulonglong * 4)()
+    L.audit_report.restype = C.c_int
+    n = L.audit_report(buf, len(buf), cnt)
+    out = {"violations": [v for v in buf.value.decode().splitlines() if v], "count": n, "launches": cnt[0], "graph_replays": cnt[1],
+           "replayed_launches": cnt[2], "allocations": cnt[3]}
+    out.update(extra or {})
+    print(json.dumps(out), flush=True)
+
+
+class Dim3(C.Structure):
+    _fields_ = [("x", C.c_uint32), ("y", C.c_uint32), ("z", C.c_uint32)]
+
+
+def controls(L):
+    """Negative controls: each misuse below must be reported."""
+    V = C.c_void_p
+    L.hipMalloc.argtypes = [C.POINTER(V), C.c_size_t]
+    L.hipFree.argtypes = [V]
+    L.hipMemcpy.argtypes = [V, V, C.c_size_t, C.c_int]
+    L.hipEventCreate.argtypes = [C.POINTER(V)]
+    L.hipEventDestroy.argtypes = [V]
+    L.hipEventRecord.argtypes = [V, V]
+    L.hipStreamCreateWithFlags.argtypes = [C.POINTER(V), C.c_uint]
+    L.hipStreamBeginCapture.argtypes = [V, C.c_int]
+    L.hipStreamEndCapture.argtypes = [V, C.POINTER(V)]
+    L.hipGraphInstantiateWithFlags.argtypes = [C.POINTER(V), V, C.c_ulonglong]
+    L.hipGraphLaunch.argtypes = [V, V]
+    L.hipLaunchKernel.argtypes = [V, Dim3, Dim3, C.POINTER(V), C.c_size_t, V]
+    got = {}
+
+    def step(name, fn):
+        L.audit_clear()
+        fn()
+        buf = C.create_string_buffer(1 << 16)
+        got[name] = L.audit_report(buf, len(buf), None)
+
+    a, b = V(), V()
+    L.hipMalloc(C.byref(a), 4096)
+    L.hipMalloc(C.byref(b), 4096)
+    host = (C.c_char * 8192)()
+    # copy into a freed block; a copy running past its block's end
+    L.hipFree(b)
+    step("copy_into_freed_block", lambda: L.hipMemcpy(b, host, 16, 1))
+    step("copy_past_block_end", lambda: L.hipMemcpy(a, host, 8192, 1))
+    # an event recorded after destruction
+    ev = V()
+    L.hipEventCreate(C.byref(ev))
+    L.hipEventDestroy(ev)
+    step("event_after_destroy", lambda: L.hipEventRecord(ev, None))
+    # a kernel whose pointer argument lies in a freed block (f32_to_f16_kernel(src, dst, n))
+    kern = C.addressof(C.c_char.in_dll(L, "_ZN2fa17f32_to_f16_kernelEPKfPDF16_l"))
+    n = C.c_long(16)
+    args = (V * 3)(C.cast(C.pointer(b), V), C.cast(C.pointer(a), V), C.cast(C.pointer(n), V))
+    step("kernel_arg_in_freed_block", lambda: L.hipLaunchKernel(kern, Dim3(1, 1, 1), Dim3(64, 1, 1), args, 0, None))
+    # a block size above the kernel's maximum
+    args2 = (V * 3)(C.cast(C.pointer(a), V), C.cast(C.pointer(a), V), C.cast(C.pointer(n), V))
+    step("block_above_max", lambda: L.hipLaunchKernel(kern, Dim3(1, 1, 1), Dim3(2048, 1, 1), args2, 0, None))
+    # a graph whose captured pointer is freed before a replay
+    s, g, x, c = V(), V(), V(), V()
+    L.hipStreamCreateWithFlags(C.byref(s), 0)
+    L.hipMalloc(C.byref(c), 4096)
+    args3 = (V * 3)(C.cast(C.pointer(c), V), C.cast(C.pointer(a), V), C.cast(C.pointer(n), V))
+    L.hipStreamBeginCapture(s, 0)
+    L.hipLaunchKernel(kern, Dim3(1, 1, 1), Dim3(64, 1, 1), args3, 0, s)
+    L.hipStreamEndCapture(s, C.byref(g))
+    L.hipGraphInstantiateWithFlags(C.byref(x), g, 0)
+    step("graph_replay_clean", lambda: L.hipGraphLaunch(x, s))
+    L.hipFree(c)
+    step("graph_replay_after_free", lambda: L.hipGraphLaunch(x, s))
+    L.audit_clear()
+    print(json.dumps({"controls": got}), flush=True)
+
+
+def e2e(L, fa, wb: int, seconds: float, profile: bool, pipelined: bool = True):
+    """pipeline.transcribeWindowed over `seconds` of synthetic PCM in groups of
+    `wb` windows with the full encoder (f16): one pass with captured graphs,
+    then one pass with a profile window of 400,000 launches open."""
+    import importlib
+    pl = importlib.import_module(fa.__name__ + ".pipeline")
+    pl.MAX_WINDOWS = max(pl.MAX_WINDOWS, wb)  # the audit build's encoder takes wb windows
+    ctx = fa.createContext("hip")
+    man = fa.synth.make_weights(dict(FULL), seed=1)
+    enc = fa.FusedEncoder(ctx, man, "f16", max_T=188)
+    del man
+    dec = fa.TdtDecoder(ctx, fa.synth.make_decoder_weights(1))
+    W, b = fa.synth.make_joint_projection(2)
+    projW, projB = ctx.upload(W, W.shape[0], W.shape[1]), ctx.upload(b.reshape(1, -1), 1, b.size)
+    audio = fa.synth.make_pcm(seconds, seed=1)
+    r = pl.transcribeWindowed(ctx, enc, dec, projW, projB, audio, wb=wb, pipelined=pipelined)
+    n_prof = 0
+    if profile:
+        ctx.startProfile(400000)
+        r = pl.transcribeWindowed(ctx, enc, dec, projW, projB, audio, wb=wb, pipelined=pipelined)
+        n_prof = len(ctx.endProfile())
+    stats = r["stats"]
+    enc.close()
+    dec.close()
+    ctx.destroy()
+    report(L, {"windows": stats["windows"], "groups": stats["groups"], "profiled_launches": n_prof})
+
+
+def ragged(L, fa):
+    """the hour's ragged windows in packed batches of up to 32,
+    every batch through fa_encoder_forward_stream_batches (two lanes)."""
+    import numpy as np
+    ctx = fa.createContext("hip")
+    man = fa.synth.make_weights(dict(FULL), seed=1)
+    enc = fa.FusedEncoder(ctx, man, "f16", max_T=375)
+    del man
+    total = 360000
+    starts, lens = fa.windowing.planRaggedWindows(total, 200, 3000, 100, seed=1)
+    batches = [(starts[b], lens[b]) for b in (np.asarray(g) for g in fa.windowing.packBatches(lens, 32))]
+    feats = ctx.upload(np.zeros((128, total), np.float32), 128, total)
+    for _ in range(2):
+        for o in enc.forwardStreamBatches(feats, batches, "packed"):
+            ctx.freeTensor(o)
+    enc.close()
+    ctx.destroy()
+    report(L, {"batches": len(batches)})
+
+
+def stream(L, fa, profile: bool):
+    """The stream workload (EOU config): one stream pushed 160 ms at a time,
+    then 16 streams pushed together, with or without a profile window."""
+    cfg = dict(FULL, subPad={"t": 2, "b": 1, "l": 2, "r": 1}, convCausal=True, attChunk=2, attLeft=70, Fsub=17)
+    ctx = fa.createContext("hip")
+    man = fa.synth.make_weights(cfg, seed=1)
+    enc = fa.FusedEncoder(ctx, man, "f16", max_T=128, cfg=cfg)
+    del man
+    mel = fa.synth.make_features(128, 800, seed=2)[0]
+    if profile:
+        ctx.startProfile(200000)
+    st = fa.createEncodeStream(ctx, enc)
+    for t in range(0, mel.shape[1], 16):
+        fa.encodeStreamPush(ctx, st, mel[:, t:t + 16])
+    fa.encodeStreamFlush(ctx, st)
+    fa.disposeEncodeStream(ctx, st)
+    sts = [fa.createEncodeStream(ctx, enc) for _ in range(16)]
+    for t in range(0, mel.shape[1], 16):
+        fa.encodeStreamsPush(ctx, sts, [mel[:, t:t + 16]] * 16)
+    for s in sts:
+        fa.encodeStreamFlush(ctx, s)
+        fa.disposeEncodeStream(ctx, s)
+    if profile:
+        ctx.endProfile()
+    enc.close()
+    ctx.destroy()
+    report(L)
+
+
+def main():
+    import __graft_entry__ as ge
+    fa = ge.load_package()
+    L = fa._lib.lib()
+    what = sys.argv[1]
+    if what == "controls":
+        controls(L)
+    elif what.startswith("e2e"):
+        # e2e<wb>[s][p] [seconds]: s = stage by stage, p = a profiled pass too
+        wb = int(what[3:].rstrip("ps"))
+        e2e(L, fa, wb, float(sys.argv[2]) if len(sys.argv) > 2 else 3600.0, what.endswith("p"), "s" not in what[3:])
+    elif what == "ragged":
+        ragged(L, fa)
+    elif what in ("stream", "streamp"):
+        stream(L, fa, what == "streamp")
+    else:
+        raise SystemExit(f"unknown scenario {what}")
+
+
+if __name__ == "__main__":
+    main()

@@ -65,3 +65,39 @@ def test_short_empty_and_tail_inputs(ctx, fa, orc, parts):
     tail = fa.synth.make_pcm(416080 / 16000, seed=7)  # windows of 240000, 208080 and 80 samples
     r = pl.transcribeWindowed(ctx, enc, dec, projW, projB, tail)
     assert r["stats"]["windows"] == 2
+
+
+@pytest.mark.parametrize("wb,seconds", [(2, 120.0), (3, 100.0), (32, 470.0)])
+def test_pipelined_equals_stage_by_stage(ctx, fa, parts, wb, seconds):
+    """fa_transcribe_groups (group g+1's mel / encoder / projection on an
+    encoder lane while group g decodes, two groups' buffers reused in turn)
+    gives the tokens and times of the stage-by-stage calls, for odd and even
+    group counts and a full 32-window group."""
+    pl, enc, dec, _, projW, projB = parts
+    audio = fa.synth.make_pcm(seconds, seed=8)
+    a = pl.transcribeWindowed(ctx, enc, dec, projW, projB, audio, wb=wb, pipelined=False)
+    b = pl.transcribeWindowed(ctx, enc, dec, projW, projB, audio, wb=wb, pipelined=True)
+    assert a["stats"]["groups"] == b["stats"]["groups"] >= 2
+    assert a["stats"]["windows"] == b["stats"]["windows"]
+    assert a["ids"] == b["ids"] and a["idTimes"] == b["idTimes"]
+    assert len(a["ids"]) > 10
+
+
+def test_pipelined_rejects_bad_plans(ctx, fa, parts):
+    import ctypes as C
+    from importlib import import_module
+    L = import_module(fa.__name__ + "._lib")
+    pl, enc, dec, _, projW, projB = parts
+    pcm = ctx.upload(np.zeros((1, 16000 * 20), np.float32), 1, 16000 * 20)
+    I = L.I32P
+    out = [np.zeros(64 * 16, np.int32) for _ in range(2)] + [np.zeros(64, np.int32) for _ in range(2)]
+
+    def call(counts, starts, lens):
+        c, s, l = (np.asarray(v, np.int32) for v in (counts, starts, lens))
+        return L.lib().fa_transcribe_groups(ctx._p, enc._p, dec._p, pcm.h, len(c), c.ctypes.data_as(I), s.ctypes.data_as(I), l.ctypes.data_as(I),
+                                            projW.h, projB.h, 128, C.c_double(2.0 ** -24), 1, 16, *[o.ctypes.data_as(I) for o in out])
+    assert call([1], [0], [100]) == L.FA_E_INVALID            # no mel frame
+    assert call([1], [0], [16000 * 21]) == L.FA_E_INVALID     # past the stream
+    assert call([33], [0] * 33, [16000] * 33) == L.FA_E_INVALID  # more than 32 windows in a group
+    assert call([1], [0], [16000]) == L.FA_OK
+    ctx.freeTensor(pcm)
