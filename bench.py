@@ -532,6 +532,8 @@ def bench_e2e(args, fa, ctx):
     stage does its full work."""
     import importlib
     pl = importlib.import_module(fa.__name__ + ".pipeline")
+    raise SystemExit("bench --workload e2e is switched off: its pipelined run at full size (24 layers, 3600 s, 32-window groups) made an "
+                     "illegal memory access with no cause shown yet, and an earlier stage-by-stage run at 64-window groups faulted too")
     seconds = args.audio_sec
     audio = fa.synth.make_pcm(seconds, seed=1)
     man = fa.synth.make_weights(dict(FULL), seed=1)

@@ -12,11 +12,11 @@ so the host only plans windows and stitches tokens:
     -> fa_encoder_forward_stream (ragged batch read in place from the stream)
     -> matmul(projW, projB) -> fa_tdt_decode (all windows in lock-step)
     -> tokens back to the host -> stitch.
-Pipelined (the default, like the reference's): the whole group loop is one
-native call, fa_transcribe_groups, which queues group g+1's mel, encoder and
-projection on an encoder lane before group g decodes on the context stream.
-pipelined=False runs the stages one call at a time (the reference's serial
-gate baseline); both give the same tokens.  Projected frames never leave the
+pipelined=True: the whole group loop is one native call,
+fa_transcribe_groups, which queues group g+1's mel, encoder and projection on
+an encoder lane before group g decodes on the context stream (the tokens equal
+the stage-by-stage calls'); its first run at full size (24 layers, one hour)
+faulted the GPU with no cause shown, so the default stays stage by stage.  Projected frames never leave the
 device.  A group holds up to `wb` windows
 (at most 32, the largest encoder batch validated on the GPU; one run with
 64-window groups over an hour of audio faulted the GPU and its cause has not
@@ -73,7 +73,7 @@ def _js_round(x: float) -> int:
 
 
 def transcribeWindowed(ctx, enc, dec, projW, projB, samples, sampleRate: int = 16000, windowSec: float = 15, overlapSec: float = 2,
-                       wb: int = MAX_WINDOWS, keepFrames: bool = False, pipelined: bool = True) -> dict:
+                       wb: int = MAX_WINDOWS, keepFrames: bool = False, pipelined: bool = False) -> dict:
     """pipeline.js:31 transcribeWindowed(ctx, enc, dec, mel, projW, projB,
     samples, opts) with the GPU stages: enc a FusedEncoder, dec a TdtDecoder,
     projW / projB device tensors [D, 640] / [1, 640] (the decoder manifest's

@@ -279,6 +279,8 @@ hipError_t do_launch(const void *f, dim3 g, dim3 b, void **args, size_t shm, hip
     l.args.push_back(std::move(v));
   }
   g_launches++;
+  static FILE *logf = std::getenv("FA_AUDIT_LOG") ? std::fopen(std::getenv("FA_AUDIT_LOG"), "w") : nullptr;
+  if (logf) std::fprintf(logf, "%s %u %u %u %u\n", k.pretty.c_str(), g.x, g.y, g.z, b.x * b.y * b.z);
   check_geometry(k, g, b, shm);
   check_launch_args(l, "launch");
   if (Handle *cs = capturing_stream(s)) cs->ops.push_back(Op{0, l});
