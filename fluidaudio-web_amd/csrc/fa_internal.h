@@ -154,6 +154,7 @@ int check_launch(fa_ctx *ctx, const char *what);
 // Looks up the allocation-free mel path's static device array for ctx->device
 // (once per device; mel.hip).  Called by fa_ctx_create with the device current.
 int mel_static_init(fa_ctx *ctx);
+void mel_static_release(fa_ctx *ctx);  // fa_ctx_destroy: gives up the static scratch
 // Log-mel internals shared with the windowed-transcription runner (mel.hip).
 int tdt_decode_dev(fa_tdt *d, const float *fr, long rows, const int32_t *lens, int n, int cap, int32_t *ids, int32_t *frame_idx, int32_t *counts);
 int mel_prepare(fa_ctx *ctx, int n, int n_mels, int normalize);

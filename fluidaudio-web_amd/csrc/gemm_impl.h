@@ -924,10 +924,8 @@ template <int EPI>
 static int launch_skinny(fa_ctx *ctx, const GemmArgs &p, const char *label) {
   const int ks = skinny_ks(p.N);
   const int ti = p.M <= 16 ? 1 : 2;
-  static const bool split_on = [] {  // FA_SKINNY_SPLIT=0: one workgroup per 16 columns everywhere
-    const char *e = getenv("FA_SKINNY_SPLIT");
-    return !(e && e[0] == '0');
-  }();
+  const char *se = getenv("FA_SKINNY_SPLIT");  // 0: one workgroup per 16 columns everywhere (read per call)
+  const bool split_on = !(se && se[0] == '0');
   // N <= 2048 gives one workgroup per 16 columns only N / 16 <= 128 of the
   // chip's CUs: with two row tiles (17..32 rows, a batched stream pass) its K
   // range is split over kSkinnySplit workgroups instead.  Up to 16 rows the

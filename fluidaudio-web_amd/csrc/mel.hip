@@ -356,12 +356,16 @@ static_assert(kScratchBytes == 273920, "static scratch size (documented in fa_hi
 static __device__ __align__(256) char scratch[kScratchBytes];
 
 // Per device: the array's device address (from hipGetSymbolAddress with that
-// device current; the array's host-side name is not a device address) and the
-// bin count its tables currently hold.
+// device current; the array's host-side name is not a device address), the
+// bin count its tables currently hold, and the context that uses it: one
+// context per device at a time, so every use is ordered on that context's
+// stream (calls from a second context are refused until the first is
+// destroyed).
 constexpr int kMaxDevices = 64;
 struct StaticScratch {
   char *ptr = nullptr;
   int tab_mels = 0;
+  const fa_ctx *owner = nullptr;
 };
 static StaticScratch g_static[kMaxDevices];
 static std::mutex g_static_mu;
@@ -375,8 +379,8 @@ static int upload_static_tables(fa_ctx *ctx, StaticScratch &ss, int nmels) {
   std::memcpy(host.data(), &t, kTabFb);
   std::memcpy(host.data() + kTabFb, fb.data(), fb.size() * 4);
   std::memcpy(host.data() + kTabFb + fb.size() * 4, bounds.data(), bounds.size() * 4);
-  // earlier calls may still read the tables being replaced
-  FA_HIP(ctx, hipDeviceSynchronize());
+  // earlier calls (all on this context's stream) may still read the tables being replaced
+  FA_HIP(ctx, hipStreamSynchronize(ctx->stream));
   FA_HIP(ctx, hipMemcpy(ss.ptr, host.data(), host.size(), hipMemcpyHostToDevice));
   ss.tab_mels = nmels;
   return FA_OK;
@@ -396,6 +400,13 @@ int mel_static_init(fa_ctx *ctx) {
     FA_TRY(upload_static_tables(ctx, ss, kMaxMels));
   }
   return FA_OK;
+}
+
+// fa_ctx_destroy: the context gives up the static scratch of its device.
+void mel_static_release(fa_ctx *ctx) {
+  if (ctx->device < 0 || ctx->device >= kMaxDevices) return;
+  std::lock_guard<std::mutex> lk(g_static_mu);
+  if (g_static[ctx->device].owner == ctx) g_static[ctx->device].owner = nullptr;
 }
 
 // The constant tables for n_mels bins and the statistics scratch for n
@@ -463,13 +474,15 @@ int fa_mel_windows_static(fa_ctx *ctx, const float *pcm, int64_t nsamp, const in
   long total = 0;
   FA_TRY(mel_check(ctx, (long)nsamp, starts, lens, n, n_mels, log_guard, &total));
   if (total != out_cols) return set_err(ctx, FA_E_INVALID, "melWindowsStatic: the windows give %ld frames, out has %lld columns", total, (long long)out_cols);
-  if (ctx->device < 0 || ctx->device >= kMaxDevices || !g_static[ctx->device].ptr)
-    return set_err(ctx, FA_E_STATE, "melWindowsStatic: static scratch not set up for device %d", ctx->device);
+  if (ctx->device < 0 || ctx->device >= kMaxDevices) return set_err(ctx, FA_E_STATE, "melWindowsStatic: device %d", ctx->device);
+  // held from the owner / table check through the launch
+  std::lock_guard<std::mutex> lk(g_static_mu);
   StaticScratch &ss = g_static[ctx->device];
-  if (ss.tab_mels != n_mels) {  // another bin count: synchronous table upload (not capturable)
-    std::lock_guard<std::mutex> lk(g_static_mu);
-    if (ss.tab_mels != n_mels) FA_TRY(upload_static_tables(ctx, ss, n_mels));
-  }
+  if (!ss.ptr) return set_err(ctx, FA_E_STATE, "melWindowsStatic: static scratch not set up for device %d", ctx->device);
+  if (ss.owner && ss.owner != ctx)
+    return set_err(ctx, FA_E_STATE, "melWindowsStatic: another context on device %d uses the static scratch (one context per device)", ctx->device);
+  ss.owner = ctx;
+  if (ss.tab_mels != n_mels) FA_TRY(upload_static_tables(ctx, ss, n_mels));  // another bin count: synchronous (not capturable)
   if (total == 0) return FA_OK;
   const MelTab *tab = (const MelTab *)ss.ptr;
   const float *fb = (const float *)(ss.ptr + kTabFb);

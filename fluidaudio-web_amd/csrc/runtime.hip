@@ -259,6 +259,7 @@ void fa_ctx_destroy(fa_ctx *ctx) {
   if (!ctx) return;
   (void)hipSetDevice(ctx->device);
   (void)hipStreamSynchronize(ctx->stream);
+  mel_static_release(ctx);
   for (auto &r : ctx->recs) {
     if (!r.live) continue;
     if (!r.view && r.ptr) (void)hipFree(r.ptr);

@@ -55,6 +55,9 @@ struct fa_stream {
   _Float16 *kc[2] = {nullptr, nullptr}, *vc[2] = {nullptr, nullptr};  // [layers][left][D]
   float *cc[2] = {nullptr, nullptr};                                  // [layers][8][D]
   int cur = 0, Lc = 0;
+  // a pass failed after it had started changing this stream's caches: its
+  // state is unknown, so later pushes are refused
+  bool failed = false;
 };
 
 // One lane of stream passes: HIP stream, workspace, the pass's mel rows and
@@ -178,7 +181,13 @@ void advance_fifo(fa_stream *st, int nemit) {
 
 // One pass of n streams with the same plan and the same cached-key count, on
 // lane L: window w = sts[w]; its emitted frames are appended to outs[w].
-int run_group(fa_ctx *ctx, fa_encoder *e, StreamLane *L, fa_stream *const *sts, int n, const PassPlan &pl, std::vector<fa_tensor> *const *outs) {
+// The stream state (cache half, cached-key count, FIFO, emitted frames) moves
+// only once the pass is queued, all of it together: a failure before that
+// (sizes, allocations) leaves every stream as it was, so the same push can be
+// repeated; a failure while the pass is being queued marks the streams failed.
+// advance: drop the FIFO rows the next pass no longer reads (false: a flush).
+int run_group(fa_ctx *ctx, fa_encoder *e, StreamLane *L, fa_stream *const *sts, int n, const PassPlan &pl, std::vector<fa_tensor> *const *outs,
+              bool advance) {
   PassScope scope(ctx, e, L);
   const fa_encoder_cfg &c = e->cfg;
   const int MB = c.melBins, D = c.D, m = pl.m, nComp = pl.nComp, nemit = pl.nemit;
@@ -191,23 +200,62 @@ int run_group(fa_ctx *ctx, fa_encoder *e, StreamLane *L, fa_stream *const *sts, 
   if (g.M != n * nComp) return set_err(ctx, FA_E_STATE, "stream pass: %d mel rows give %d frames, expected %d", m, g.M / n, nComp);
   if (s0->Lc + nComp > 256) return set_err(ctx, FA_E_UNSUPPORTED, "stream pass: %d cached + %d new keys (at most 256)", s0->Lc, nComp);
   FA_TRY(pass_workspace(ctx, e, g, c.layers, true));
-  FA_TRY(lane_grow(ctx, L, (void **)&L->mel_dev, &L->mel_cap, (size_t)n * m * MB * 4));
-  FA_TRY(lane_grow(ctx, L, (void **)&L->x_dev, &L->x_cap, (size_t)n * nComp * D * 4));
+  // the windows' output tensors first: nothing is queued and no state moves
+  // unless all of them exist
+  OutRows orows{};
+  std::vector<fa_tensor> mine;
+  for (int w = 0; w < n; w++) {
+    fa_tensor o;
+    TensorRec *ro;
+    const int st = new_tensor(ctx, nemit, D, S_F32, (size_t)nemit * D * 4, &o, &ro);
+    if (st != FA_OK) {
+      for (fa_tensor t : mine) (void)fa_free_tensor(ctx, t);
+      return st;
+    }
+    orows.dst[w] = (float *)ro->ptr;
+    mine.push_back(o);
+  }
+  auto give_back = [&]() {
+    for (fa_tensor t : mine) (void)fa_free_tensor(ctx, t);
+    return FA_OK;
+  };
+  // from the first queued operation on, a failure leaves the caches unknown
+  auto fail = [&](int st) {
+    for (int w = 0; w < n; w++) sts[w]->failed = true;
+    give_back();
+    return st;
+  };
+  {
+    int st = lane_grow(ctx, L, (void **)&L->mel_dev, &L->mel_cap, (size_t)n * m * MB * 4);
+    if (st == FA_OK) st = lane_grow(ctx, L, (void **)&L->x_dev, &L->x_cap, (size_t)n * nComp * D * 4);
+    if (st != FA_OK) {
+      give_back();
+      return st;
+    }
+  }
   {  // the windows' mel rows, copied from the FIFOs into pinned staging, then to the device
     const int b = L->next_stage;
     L->next_stage ^= 1;
     const size_t bytes = (size_t)n * m * MB * 4;
-    FA_HIP(ctx, hipEventSynchronize(L->staged[b]));  // this buffer's previous copy (two passes back) is done
+    if (hipEventSynchronize(L->staged[b]) != hipSuccess) {  // this buffer's previous copy (two passes back) is done
+      give_back();
+      return set_err(ctx, FA_E_DEVICE, "stream pass: staging wait");
+    }
     if (bytes > L->stage_cap[b]) {
-      if (L->stage[b]) FA_HIP(ctx, hipHostFree(L->stage[b]));
+      if (L->stage[b]) (void)hipHostFree(L->stage[b]);
       L->stage[b] = nullptr;
       L->stage_cap[b] = 0;
-      FA_HIP(ctx, hipHostMalloc((void **)&L->stage[b], bytes, hipHostMallocDefault));
+      if (hipHostMalloc((void **)&L->stage[b], bytes, hipHostMallocDefault) != hipSuccess) {
+        L->stage[b] = nullptr;
+        give_back();
+        return set_err(ctx, FA_E_OOM, "stream pass: pinned staging of %zu bytes", bytes);
+      }
       L->stage_cap[b] = bytes;
     }
     for (int w = 0; w < n; w++) std::memcpy(L->stage[b] + (size_t)w * m * MB, sts[w]->fifo.data(), (size_t)m * MB * 4);
-    FA_HIP(ctx, hipMemcpyAsync(L->mel_dev, L->stage[b], bytes, hipMemcpyHostToDevice, L->hs));
-    FA_HIP(ctx, hipEventRecord(L->staged[b], L->hs));
+    if (hipMemcpyAsync(L->mel_dev, L->stage[b], bytes, hipMemcpyHostToDevice, L->hs) != hipSuccess ||
+        hipEventRecord(L->staged[b], L->hs) != hipSuccess)
+      return fail(set_err(ctx, FA_E_DEVICE, "stream pass: mel upload"));
   }
   KvSlots kv{};
   CcSlots cc{};
@@ -249,19 +297,20 @@ int run_group(fa_ctx *ctx, fa_encoder *e, StreamLane *L, fa_stream *const *sts, 
     for (auto &gr : L->graphs)
       if (gr.key == key) hit = &gr;
     if (!hit) {
-      FA_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+      if (hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal) != hipSuccess)
+        return fail(set_err(ctx, FA_E_DEVICE, "stream pass: graph capture"));
       const int rc = launch();
       hipGraph_t graph = nullptr;
       const hipError_t ce = hipStreamEndCapture(ctx->stream, &graph);
       if (rc != FA_OK) {
         if (graph) (void)hipGraphDestroy(graph);
-        return rc;
+        return fail(rc);
       }
-      if (ce != hipSuccess) return set_err(ctx, FA_E_DEVICE, "stream pass: graph capture: %s", hipGetErrorString(ce));
+      if (ce != hipSuccess) return fail(set_err(ctx, FA_E_DEVICE, "stream pass: graph capture: %s", hipGetErrorString(ce)));
       hipGraphExec_t exec = nullptr;
       const hipError_t ie = hipGraphInstantiateWithFlags(&exec, graph, 0);
       (void)hipGraphDestroy(graph);
-      if (ie != hipSuccess) return set_err(ctx, FA_E_DEVICE, "stream pass: graph instantiate: %s", hipGetErrorString(ie));
+      if (ie != hipSuccess) return fail(set_err(ctx, FA_E_DEVICE, "stream pass: graph instantiate: %s", hipGetErrorString(ie)));
       if (L->graphs.size() >= 16) {  // two per stable set of streams and chunk shape
         size_t lru = 0;
         for (size_t i = 1; i < L->graphs.size(); i++)
@@ -274,29 +323,26 @@ int run_group(fa_ctx *ctx, fa_encoder *e, StreamLane *L, fa_stream *const *sts, 
       hit = &L->graphs.back();
     }
     hit->used = ++L->graph_clock;
-    FA_HIP(ctx, hipGraphLaunch(hit->exec, ctx->stream));
+    if (hipGraphLaunch(hit->exec, ctx->stream) != hipSuccess) return fail(set_err(ctx, FA_E_DEVICE, "stream pass: graph launch"));
   } else {
-    FA_TRY(launch());
-  }
-  // the pass is queued: every window's caches moved to the other buffer half
-  for (int w = 0; w < n; w++) {
-    sts[w]->cur ^= 1;
-    sts[w]->Lc = sp.keep;
-  }
-  OutRows orows{};
-  for (int w = 0; w < n; w++) {
-    fa_tensor o;
-    TensorRec *ro;
-    FA_TRY(new_tensor(ctx, nemit, D, S_F32, (size_t)nemit * D * 4, &o, &ro));
-    orows.dst[w] = (float *)ro->ptr;
-    outs[w]->push_back(o);
+    const int rc = launch();
+    if (rc != FA_OK) return fail(rc);
   }
   {
     ProfScope ps(ctx, "stream_out");
     const long n4 = (long)nemit * (D / 4);
     FA_LAUNCH(ps, stream_out_kernel, dim3((unsigned)std::max<long>(1, std::min<long>(cdiv(n4, 256), 64)), n), dim3(256), 0, ctx->stream,
               (const float4 *)L->x_dev, nComp, nemit, D / 4, orows);
-    FA_TRY(check_launch(ctx, "stream_out"));
+    const int rc = check_launch(ctx, "stream_out");
+    if (rc != FA_OK) return fail(rc);
+  }
+  // the pass is queued: every window's caches moved to the other buffer half,
+  // its FIFO moves past the rows this pass consumed, the frames are its own
+  for (int w = 0; w < n; w++) {
+    sts[w]->cur ^= 1;
+    sts[w]->Lc = sp.keep;
+    if (advance) advance_fifo(sts[w], nemit);
+    outs[w]->push_back(mine[w]);
   }
   return FA_OK;
 }
@@ -372,9 +418,7 @@ int run_rounds(fa_ctx *ctx, fa_encoder *e, std::vector<fa_stream *> &sts, std::v
           g[w] = sts[mem[b0 + w]];
           o[w] = &frames[mem[b0 + w]];
         }
-        rc = run_group(ctx, e, L, g.data(), nb, p, o.data());
-        if (rc == FA_OK && !flush)
-          for (int w = 0; w < nb; w++) advance_fifo(g[w], p.nemit);
+        rc = run_group(ctx, e, L, g.data(), nb, p, o.data(), !flush);
       }
       if (rc != FA_OK) break;
     }
@@ -474,6 +518,7 @@ int fa_stream_push_many(int n, fa_stream *const *sts, const float *const *mels, 
     for (int j = 0; j < i; j++)
       if (sts[j] == st) return set_err(ctx, FA_E_INVALID, "encodeStreamPush: stream %d repeats stream %d in one call", i, j);
     if (st->flushed) return set_err(ctx, FA_E_STATE, "encodeStreamPush: stream already flushed; create a new stream");
+    if (st->failed) return set_err(ctx, FA_E_STATE, "encodeStreamPush: a pass of this stream failed earlier; create a new stream");
     if (counts[i] < 0 || (counts[i] > 0 && !mels[i])) return set_err(ctx, FA_E_INVALID, "encodeStreamPush: %d frames", counts[i]);
   }
   const int MB = e->cfg.melBins;
@@ -487,7 +532,12 @@ int fa_stream_push_many(int n, fa_stream *const *sts, const float *const *mels, 
       for (int ch = 0; ch < MB; ch++) st->fifo[(old + t) * MB + ch] = mels[i][(size_t)ch * count + t];
   }
   std::vector<std::vector<fa_tensor>> frames(n);
+  // the FIFO rows stay appended on failure: a stream whose passes did not
+  // start can be pushed to again; one whose passes ran in this call lost their
+  // frames with the error and is marked failed
   int rc = run_rounds(ctx, e, v, frames, nullptr);
+  std::vector<bool> moved(n);
+  for (int i = 0; i < n; i++) moved[i] = !frames[i].empty();
   for (int i = 0; i < n; i++) {
     if (rc == FA_OK)
       rc = emit(sts[i], frames[i], &outs[i]);
@@ -495,11 +545,13 @@ int fa_stream_push_many(int n, fa_stream *const *sts, const float *const *mels, 
       for (fa_tensor t : frames[i]) (void)fa_free_tensor(ctx, t);
   }
   if (rc != FA_OK)
-    for (int i = 0; i < n; i++)
+    for (int i = 0; i < n; i++) {
+      if (moved[i]) sts[i]->failed = true;
       if (outs[i]) {
         (void)fa_free_tensor(ctx, outs[i]);
         outs[i] = 0;
       }
+    }
   return rc;
 }
 
@@ -508,6 +560,7 @@ int fa_stream_flush(fa_stream *st, fa_tensor *out) {
   fa_ctx *ctx = st->ctx;
   *out = 0;
   if (st->flushed) return set_err(ctx, FA_E_STATE, "encodeStreamFlush: stream already flushed");
+  if (st->failed) return set_err(ctx, FA_E_STATE, "encodeStreamFlush: a pass of this stream failed earlier");
   st->flushed = true;
   const int MB = st->enc->cfg.melBins;
   const int M = (int)(st->fifo.size() / MB);

@@ -570,11 +570,13 @@ static napi_value js_encoder_forward_stream_batches(napi_env env, napi_callback_
   napi_value arr;
   napi_status ok = napi_create_array_with_length(env, (size_t)nb, &arr);
   for (int b = 0; b < nb && ok == napi_ok; b++) ok = napi_set_element(env, arr, (uint32_t)b, mkbig(env, outs[b]));
-  free(outs);
-  if (ok != napi_ok) {
+  if (ok != napi_ok) {  /* no array reaches the caller: every batch's tensor is released here */
+    for (int b = 0; b < nb; b++) (void)fa_free_tensor(c, outs[b]);
+    free(outs);
     napi_throw_error(env, NULL, "encoderForwardStreamBatches: building the result array failed");
     return NULL;
   }
+  free(outs);
   return arr;
 }
 

@@ -312,8 +312,10 @@ int fa_mel_windows(fa_ctx *ctx, fa_tensor pcm, const int32_t *starts, const int3
  * fa_ctx_create.  Limits: n <= 64 windows per call (FA_E_UNSUPPORTED above),
  * n_mels <= 128.  The first call with an n_mels other than 128 on a device
  * uploads that bin count's tables with a synchronous copy (make it outside
- * graph capture).  Every call on a GPU shares the array: calls that overlap
- * on one GPU (two streams, two contexts) race. */
+ * graph capture).  Every call on a GPU shares the array, so it serves one
+ * context per GPU at a time: the first context that calls it owns it until
+ * that context is destroyed, and calls from another context on the same GPU
+ * return FA_E_STATE; the owner's calls are ordered on its stream. */
 int fa_mel_windows_static(fa_ctx *ctx, const float *pcm, int64_t nsamp, const int32_t *starts, const int32_t *lens, int n, int n_mels,
                           double log_guard, int normalize, float *out, int64_t out_cols);
 /* Row -> window index map of a batch (the index map every window-aware kernel
@@ -444,9 +446,17 @@ int fa_stream_push(fa_stream *st, const float *mel, int count, fa_tensor *out);
  * time on the encoder's stream lanes (HIP streams with workspaces of their
  * own).  The lanes start after the work queued on the context stream, and the
  * context stream waits for all of them.  Frames equal solo pushes bit for bit
- * while a batched pass has at most 16 rows; larger passes sum in another
- * order, within the encoder's tolerance (deterministic).  On failure every
- * outs[i] is 0.  The reference serves one stream per encodeStreamPush
+ * while a batched pass has at most 16 rows; from 17 to 32 rows the K range of
+ * the GEMMs is split over workgroups and summed in split order, and beyond 32
+ * rows the tiled GEMMs sum in their order: within the encoder's tolerance and
+ * deterministic for a given grouping, but a stream's bits then depend on
+ * which other streams had a pass ready in the same call.  On failure every
+ * outs[i] is 0 and the pushed frames stay queued in each stream: a failure
+ * before a stream's pass was queued (sizes, allocations) leaves it as it was,
+ * and its next push emits the frames of both pushes; a stream whose pass had
+ * been queued in this call (its caches moved, its frames discarded with the
+ * error) is marked failed, and every later push or flush of it returns
+ * FA_E_STATE.  The reference serves one stream per encodeStreamPush
  * (streaming-encoder.js:182-297); this is that call for n streams at once. */
 int fa_stream_push_many(int n, fa_stream *const *sts, const float *const *mels, const int *counts, fa_tensor *outs);
 int fa_stream_flush(fa_stream *st, fa_tensor *out);

@@ -42,6 +42,9 @@ std::mutex &mu() { static std::mutex *m = new std::mutex(); return *m; }
 std::vector<std::string> &viol() { static auto *v = new std::vector<std::string>(); return *v; }
 #define g_viol viol()
 size_t g_launches = 0, g_replays = 0, g_replayed_launches = 0, g_allocs = 0;
+// failure injection (tests of error paths): the allocation / launch after this
+// many more successful ones fails once (-1: off)
+long g_fail_alloc_after = -1, g_fail_launch_after = -1;
 
 void violation(const std::string &s) {
   if (g_viol.size() < 1000) g_viol.push_back(s);
@@ -264,6 +267,10 @@ hipError_t do_launch(const void *f, dim3 g, dim3 b, void **args, size_t shm, hip
     return hipErrorInvalidDeviceFunction;
   }
   KernelInfo &k = it->second;
+  if (g_fail_launch_after >= 0 && g_fail_launch_after-- == 0) {
+    g_last = hipErrorLaunchFailure;
+    return hipErrorLaunchFailure;
+  }
   if (!k.known) {
     violation(k.pretty + ": no argument layout in the table");
     return hipSuccess;
@@ -382,6 +389,10 @@ hipError_t hipGetSymbolAddress(void **dev, const void *sym) {
 // ── memory ──
 hipError_t hipMalloc(void **p, size_t n) {
   std::lock_guard<std::mutex> lk(g_mu);
+  if (g_fail_alloc_after >= 0 && g_fail_alloc_after-- == 0) {
+    *p = nullptr;
+    return hipErrorOutOfMemory;
+  }
   *p = dev_alloc(n, "hipMalloc");
   return *p ? hipSuccess : hipErrorOutOfMemory;
 }
@@ -566,6 +577,14 @@ int audit_report(char *buf, int cap, unsigned long long *counts) {
     counts[3] = g_allocs;
   }
   return (int)g_viol.size();
+}
+void audit_fail_alloc(long after) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_fail_alloc_after = after;
+}
+void audit_fail_launch(long after) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_fail_launch_after = after;
 }
 void audit_clear(void) {
   std::lock_guard<std::mutex> lk(g_mu);

@@ -177,6 +177,65 @@ def stream(L, fa, profile: bool):
     report(L)
 
 
+def stream_failures(L, fa):
+    """Error paths of stream pushes, with failures injected into the stand-in
+    runtime: an allocation that fails before a pass is queued leaves the
+    stream as it was (the next push emits the frames of both pushes), a
+    launch that fails while a pass is queued marks the stream failed (later
+    pushes are refused with FA_E_STATE)."""
+    cfg = dict(FULL, layers=2, subPad={"t": 2, "b": 1, "l": 2, "r": 1}, convCausal=True, attChunk=2, attLeft=70, Fsub=17)
+    ctx = fa.createContext("hip")
+    man = fa.synth.make_weights(cfg, seed=1)
+    enc = fa.FusedEncoder(ctx, man, "f16", max_T=128, cfg=cfg)
+    mel = fa.synth.make_features(128, 320, seed=2)[0]
+    pieces = [mel[:, t:t + 32] for t in range(0, 320, 32)]
+
+    def frames(o):
+        return 0 if o is None else o.shape[0]
+
+    ref = fa.createEncodeStream(ctx, enc)
+    ref_counts = [frames(fa.encodeStreamPush(ctx, ref, p)) for p in pieces]
+    fa.disposeEncodeStream(ctx, ref)
+    out = {"reference_frames": sum(ref_counts)}
+    # allocation failure on push 3: nothing moves, push 4 catches up
+    st = fa.createEncodeStream(ctx, enc)
+    got, err = [], None
+    for i, p in enumerate(pieces):
+        if i == 3:
+            ctx.trimPool(0)
+            L.audit_fail_alloc(0)
+            try:
+                fa.encodeStreamPush(ctx, st, p)
+            except fa.FaError as e:
+                err = e.code
+            L.audit_fail_alloc(-1)
+            continue
+        got.append(frames(fa.encodeStreamPush(ctx, st, p)))
+    out["alloc_failure_code"] = err
+    out["alloc_failure_frames"] = sum(got)
+    fa.disposeEncodeStream(ctx, st)
+    # launch failure inside a pass: the stream is refused afterwards
+    st = fa.createEncodeStream(ctx, enc)
+    fa.encodeStreamPush(ctx, st, pieces[0])
+    L.audit_fail_launch(5)
+    try:
+        fa.encodeStreamPush(ctx, st, pieces[1])
+        out["launch_failure_code"] = 0
+    except fa.FaError as e:
+        out["launch_failure_code"] = e.code
+    L.audit_fail_launch(-1)
+    try:
+        fa.encodeStreamPush(ctx, st, pieces[2])
+        out["after_failure_code"] = 0
+    except fa.FaError as e:
+        out["after_failure_code"] = e.code
+    fa.disposeEncodeStream(ctx, st)
+    enc.close()
+    ctx.destroy()
+    L.audit_clear()
+    print(json.dumps(out), flush=True)
+
+
 def main():
     import __graft_entry__ as ge
     fa = ge.load_package()
@@ -190,6 +249,8 @@ def main():
         e2e(L, fa, wb, float(sys.argv[2]) if len(sys.argv) > 2 else 3600.0, what.endswith("p"), "s" not in what[3:])
     elif what == "ragged":
         ragged(L, fa)
+    elif what == "stream_failures":
+        stream_failures(L, fa)
     elif what in ("stream", "streamp"):
         stream(L, fa, what == "streamp")
     else:

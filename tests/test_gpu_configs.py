@@ -5,14 +5,16 @@ configs[0]  the FFN linear X[750,1024] @ W[1024,4096] + bias on the f16 route
             the reference's CPU matmul and a float64 product;
 configs[1]  the fused encoder with one layer on 8 x 15 s windows (M = 1504
             frames) against the oracle at full dims;
-configs[2]  one window of the 16-window, 24-layer batch against the oracle's
-            24-layer encode of that window alone;
+configs[2]  all 16 windows of the 24-layer batch against the oracle's
+            24-layer encode of the same windows;
 configs[3]  a full 32-window ragged batch (the first packed batch of the
-            3600 s stream) equal to 32 standalone encodes;
+            3600 s stream) equal to 32 standalone encodes, and the whole hour
+            (8 batches, 233 windows) equal to standalone encodes;
 configs[4]  the 24-layer int8 and int4 encoders on 16 x 15 s against the HIP
             fp32 op path loaded with the same weights quantised and
-            dequantised (the quantiser is pinned bit-exact to the oracle on
-            the CPU, test_oracle.py).
+            dequantised, and window 0 against the oracle's 24-layer encode
+            with those weights (the quantiser is pinned bit-exact to the
+            oracle on the CPU, test_oracle.py).
 North-star bar for the encoder: rel-L2 <= 1e-2 vs the fp32 path and
 frame-wise argmax of R [1024, 64] ~ N(0,1) (seed 2) identical on >= 99.9 %
 of frames.
@@ -87,15 +89,22 @@ def test_config1_one_layer_vs_oracle(ctx, fa, orc):
 
 
 # ── configs[2] ──────────────────────────────────────────────────────────────
-def test_config2_window_vs_oracle_24_layers(ctx, fa, orc, full_weights):
+def test_config2_all_16_windows_vs_oracle_24_layers(ctx, fa, orc, full_weights):
+    """Every window of the 16-window, 24-layer batch against the oracle's
+    24-layer encode of the same 16 windows (the oracle's threads run the
+    windows in parallel)."""
     mels = fa.synth.make_features(128, 1500, seed=12, W=16)
     enc = fa.FusedEncoder(ctx, full_weights, "f16", max_T=188)
     got = enc.encode(mels)
     enc.close()
-    ref = orc.encode_batch(FULL, full_weights, [mels[0]])
-    r, f = rel_l2(got[0], ref), flips(got[0], ref)
-    print(f"configs[2] window 0 of 16, 24 layers: rel-L2 vs oracle {r:.2e}, argmax disagreements {f}/{len(ref)}")
-    assert r <= 1e-2 and f <= 1
+    ref = orc.encode_batch(FULL, full_weights, mels)
+    g = np.concatenate(got)
+    assert g.shape == ref.shape == (16 * 188, 1024)
+    worst = max(rel_l2(g[i * 188:(i + 1) * 188], ref[i * 188:(i + 1) * 188]) for i in range(16))
+    f = flips(g, ref)
+    print(f"configs[2] all 16 windows, 24 layers: rel-L2 vs oracle {rel_l2(g, ref):.2e} (worst window {worst:.2e}), "
+          f"argmax disagreements {f}/{len(ref)}")
+    assert worst <= 1e-2 and f <= 0.001 * len(ref)
 
 
 # ── configs[3] ──────────────────────────────────────────────────────────────
@@ -126,6 +135,39 @@ def test_encoder_refuses_more_than_32_windows(ctx, fa):
         enc.encode(mels)
     assert len(enc.encode(mels[:32])) == 32
     enc.close()
+
+
+def test_config3_hour_all_batches_equal_standalone(ctx, fa, full_weights, monkeypatch):
+    """The whole 3600 s configs[3] plan: its 233 ragged windows in 8 packed
+    batches of <= 32 (two encoder lanes), read in place from one feature
+    stream, equal each window encoded alone (eager, so no graph per length)."""
+    total = 360000
+    starts, lens = fa.windowing.planRaggedWindows(total, 200, 3000, 100, seed=1)
+    batches = [(starts[b], lens[b]) for b in (np.asarray(g) for g in fa.windowing.packBatches(lens, 32))]
+    assert len(batches) == 8 and sum(len(b[0]) for b in batches) == len(lens)
+    feats_h = np.random.default_rng(5).standard_normal((128, total), dtype=np.float32)
+    feats = ctx.upload(feats_h, 128, total)
+    enc = fa.FusedEncoder(ctx, full_weights, "f16", max_T=375)
+    outs = enc.forwardStreamBatches(feats, batches)
+    got = []
+    for o, (st, ln) in zip(outs, batches):
+        h = ctx.download(o).reshape(-1, 1024)
+        ctx.freeTensor(o)
+        off = 0
+        for s_, l_ in zip(st, ln):
+            t = fa.encoder.tsub(int(l_))
+            got.append((int(s_), int(l_), h[off:off + t]))
+            off += t
+    monkeypatch.setenv("FA_GRAPH", "0")
+    worst = 0.0
+    for s_, l_, g in got:
+        alone = enc.encode([feats_h[:, s_:s_ + l_]])[0]
+        assert alone.shape == g.shape
+        worst = max(worst, float(np.abs(g - alone).max()))
+    enc.close()
+    ctx.freeTensor(feats)
+    print(f"configs[3] hour: {len(got)} windows in 8 batches, max |batch - standalone| = {worst:.2e}")
+    assert worst < 1e-4
 
 
 # ── configs[4] ──────────────────────────────────────────────────────────────
@@ -170,6 +212,11 @@ def test_config4_quantized_encoder_vs_fp32_path(ctx, fa, orc, full_weights, fmt)
     print(f"configs[4] {fmt} encoder, 24 layers x 16 x 15 s: rel-L2 vs fp32 path (dequantised weights) {r:.2e}, "
           f"argmax disagreements {f}/{len(got)}")
     assert r <= 1e-2 and f <= 0.001 * len(got)
+    # window 0 against the oracle's own 24-layer encode with the dequantised weights
+    ro = orc.encode_batch(FULL, deq, [mels[0]])
+    r0, f0 = rel_l2(got[:188], ro), flips(got[:188], ro)
+    print(f"configs[4] {fmt} window 0 vs oracle (dequantised weights): rel-L2 {r0:.2e}, argmax disagreements {f0}/188")
+    assert r0 <= 1e-2 and f0 <= 1
 
 
 @pytest.mark.parametrize("fmt", ["int8", "int4"])

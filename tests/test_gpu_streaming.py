@@ -288,3 +288,36 @@ def test_layernorm_folded_into_skinny_gemms_matches_separate_launches(ctx, fa, m
     r = rel_l2(outs[0], outs[1])
     print(f"folded vs separate LayerNorm: rel-L2 {r:.2e}, max |diff| {np.abs(outs[0] - outs[1]).max():.2e}")
     assert r < 2e-5, r
+
+
+def test_split_k_skinny_gemms_match_single_workgroup_route(ctx, fa, monkeypatch):
+    """The split-K skinny route (32-row batched passes, K of every GEMM with
+    N <= 2048 split over four workgroups and summed in split order) against
+    the single-workgroup route at the same rows (FA_SKINNY_SPLIT=0), at this
+    path's widths: the two differ only in the f32 summation order, so the
+    frames agree to rel-L2 1e-5."""
+    cfg = dict(fa.synth.small_stream_cfg(layers=2), D=1024, DFF=4096, H=8)
+    man = fa.synth.make_weights(cfg, seed=13)
+    enc = fa.FusedEncoder(ctx, man, "f16", max_T=128, cfg=cfg)
+    mels = [fa.synth.make_features(cfg["melBins"], 96, seed=120 + i)[0] for i in range(16)]
+
+    def run():
+        sts = [fa.createEncodeStream(ctx, enc) for _ in mels]
+        got = [[] for _ in mels]
+        for t in range(0, 96, 16):
+            for i, o in enumerate(fa.encodeStreamsPush(ctx, sts, [m[:, t:t + 16] for m in mels])):
+                if o is not None:
+                    got[i].append(o)
+        for st in sts:
+            fa.disposeEncodeStream(ctx, st)
+        return [np.concatenate(g, 0) for g in got]
+
+    split = run()
+    monkeypatch.setenv("FA_SKINNY_SPLIT", "0")
+    single = run()
+    monkeypatch.delenv("FA_SKINNY_SPLIT")
+    for i, (a, b) in enumerate(zip(single, split)):
+        assert a.shape == b.shape and a.shape[0] > 0
+        assert rel_l2(b, a) < 1e-5, f"stream {i}: rel-L2 {rel_l2(b, a):.2e}"
+    assert any(not np.array_equal(a, b) for a, b in zip(single, split)), "the split route did not run"
+    enc.close()

@@ -81,3 +81,15 @@ def test_stream_workload(builds, scenario):
     r = run(builds, scenario, layers=4)
     assert r["launches"] > 2000
     assert r["violations"] == []
+
+
+def test_stream_push_failures_leave_consistent_state(builds):
+    """An allocation that fails before a stream pass is queued changes nothing
+    (the next push emits both pushes' frames: the reference total); a launch
+    that fails while a pass is queued marks the stream failed, and the next
+    push is refused with FA_E_STATE."""
+    r = run(builds, "stream_failures")
+    assert r["alloc_failure_code"] == 4  # FA_E_OOM
+    assert r["alloc_failure_frames"] == r["reference_frames"] > 0
+    assert r["launch_failure_code"] == 3  # FA_E_DEVICE
+    assert r["after_failure_code"] == 2  # FA_E_STATE

@@ -232,6 +232,35 @@ def test_int4_format_is_matmulnbits_with_zero_point_8(orc):
     assert np.abs(deq - w).max() <= np.max(sf) / 2 + 1e-7  # rounding error <= s/2
 
 
+def test_matmul_nbits_zero_point_nibbles_known_answer(orc):
+    """Asymmetric MatMulNBits with a different zero point in every block:
+    block b of a row reads the low nibble of zero-point byte b // 2 when b is
+    even and the high nibble when b is odd (lib.rs:185-186).  The expected
+    product is built from the zero points as chosen, not from their packing,
+    so a swapped nibble order, a zero point read from the wrong byte or a
+    flipped (q - zp) sign each fail."""
+    K, N, bs = 96, 2, 32                       # three blocks, two zero-point bytes per row
+    zps = [[3, 11, 5], [14, 0, 9]]             # per row, per block
+    sc = np.array([[0.5, 0.25, 2.0], [1.5, 0.125, 0.75]], np.float32)
+    q = (np.arange(K)[None, :] * np.array([[5], [7]]) + np.array([[1], [4]])) % 16  # 4-bit codes, [N][K]
+    bq = np.zeros((N, 3, 16), np.uint8)
+    for n in range(N):
+        for k in range(K):
+            b, t = divmod(k, bs)
+            bq[n, b, t // 2] |= np.uint8(q[n, k] << (4 * (t & 1)))  # low nibble = even index
+    zp = np.array([[zps[n][0] | (zps[n][1] << 4), zps[n][2]] for n in range(N)], np.uint8)
+    assert zp.tolist() == [[0xB3, 0x05], [0x0E, 0x09]]
+    a = np.zeros((2, K), np.float32)
+    a[0, :] = 1.0                                # row 0: column sums
+    a[1, 5], a[1, 40], a[1, 77] = 1.0, 2.0, -1.0  # row 1: one k in each block
+    w = np.array([[(q[n, k] - zps[n][k // bs]) * sc[n, k // bs] for n in range(N)] for k in range(K)], np.float64)  # [K][N]
+    y = orc.matmul_nbits(a, bq, sc, zp, N)
+    assert np.abs(y - a.astype(np.float64) @ w).max() < 1e-4
+    # row 1, column 0 by hand: k = 5 (block 0), 40 (block 1), 77 (block 2)
+    hand = (q[0, 5] - 3) * 0.5 + 2.0 * (q[0, 40] - 11) * 0.25 - (q[0, 77] - 5) * 2.0
+    assert y[1, 0] == np.float32(hand)
+
+
 def test_library_quantizer_is_bitexact_with_oracle(fa, orc):
     import ctypes as C
 

@@ -86,3 +86,19 @@ def test_mel_windows_static_rejects_sizes(ctx, fa):
     assert _static(fa, ctx, pcm.ptr.value, n, [159000], [1600], 128, 2.0 ** -24, 1, out.ptr.value, 10) == 1  # outside the stream
     out.free()
     pcm.free()
+
+
+def test_mel_windows_static_serves_one_context_per_device(ctx, fa):
+    """A second context on the same GPU is refused (FA_E_STATE) while the
+    first one owns the static array."""
+    nsamp = 16000 * 2
+    pcm_h = np.random.default_rng(3).standard_normal(nsamp).astype(np.float32) * 0.1
+    pcm_d = DevBuf(pcm_h.nbytes).put(pcm_h)
+    out_d = DevBuf(128 * 200 * 4)
+    assert _static(fa, ctx, pcm_d.ptr.value, nsamp, [0], [32000], 128, 2.0 ** -24, 1, out_d.ptr.value, 200) == 0
+    other = fa.createContext("hip")
+    assert _static(fa, other, pcm_d.ptr.value, nsamp, [0], [32000], 128, 2.0 ** -24, 1, out_d.ptr.value, 200) == fa._lib.FA_E_STATE
+    assert b"another context" in fa.lib().fa_last_error(other._p)
+    other.destroy()
+    pcm_d.free()
+    out_d.free()
