@@ -295,7 +295,8 @@ def test_split_k_skinny_gemms_match_single_workgroup_route(ctx, fa, monkeypatch)
     N <= 2048 split over four workgroups and summed in split order) against
     the single-workgroup route at the same rows (FA_SKINNY_SPLIT=0), at this
     path's widths: the two differ only in the f32 summation order, so the
-    frames agree to rel-L2 1e-5."""
+    frames agree to rel-L2 1e-4 (an f32 difference can move an f16 rounding
+    of a later operand by one ulp; the stream-vs-offline bar is 2e-3)."""
     cfg = dict(fa.synth.small_stream_cfg(layers=2), D=1024, DFF=4096, H=8)
     man = fa.synth.make_weights(cfg, seed=13)
     enc = fa.FusedEncoder(ctx, man, "f16", max_T=128, cfg=cfg)
@@ -318,6 +319,6 @@ def test_split_k_skinny_gemms_match_single_workgroup_route(ctx, fa, monkeypatch)
     monkeypatch.delenv("FA_SKINNY_SPLIT")
     for i, (a, b) in enumerate(zip(single, split)):
         assert a.shape == b.shape and a.shape[0] > 0
-        assert rel_l2(b, a) < 1e-5, f"stream {i}: rel-L2 {rel_l2(b, a):.2e}"
+        assert rel_l2(b, a) < 1e-4, f"stream {i}: rel-L2 {rel_l2(b, a):.2e}"
     assert any(not np.array_equal(a, b) for a, b in zip(single, split)), "the split route did not run"
     enc.close()
