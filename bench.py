@@ -300,7 +300,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="encoder", choices=["encoder", "layer", "ragged", "quant", "quant4", "gemv", "copy", "mel", "decode", "e2e", "stream"])
+    ap.add_argument("--workload", default="encoder", choices=["encoder", "layer", "ragged", "quant", "quant4", "gemv", "copy", "mel", "decode", "e2e", "stream", "oppath"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--windows", type=int, default=16, help="decode workload: windows per decode call (1..64)")
     ap.add_argument("--audio-sec", type=float, default=3600.0, help="e2e workload: seconds of synthetic audio")
@@ -327,6 +327,8 @@ def main():
         return bench_e2e(args, fa, ctx)
     if args.workload == "stream":
         return bench_stream(args, fa, ctx)
+    if args.workload == "oppath":
+        return bench_oppath(args, fa, ctx)
     cfg = dict(FULL)
     layout = "packed"
     rng = np.random.default_rng(1)
@@ -622,6 +624,55 @@ def bench_e2e(args, fa, ctx):
                                           f"(preEncode + 1 layer scaled to 24) + decode {t_dec:.2f} s, oracle/fa_oracle.c single thread"}
     dec.close()
     enc.close()
+    print(json.dumps(line), flush=True)
+
+
+def bench_oppath(args, fa, ctx):
+    """configs[2] through the reference's own op sequence (parakeetEncodeBatch,
+    raw-encoder.js:235-386, on the ComputeContext ops: ~700 launches per
+    batch) with f16 weights (uploadF16, the probed uploadTileMajorF16 of a Node
+    host), beside the fused encoder on the same windows: the throughput an
+    unchanged engine gets from this backend.  Timed twice: the multi-op
+    attention chain, and the reference's opt-in attnFused member."""
+    man = fa.synth.make_weights(dict(FULL), seed=1)
+    mels = fa.synth.make_features(FULL["melBins"], 1500, seed=1, W=16)
+    enc = fa.loadParakeetEncoder(ctx, man, weights="f16")
+    del man
+    line_kern = {}
+
+    def run(fused):
+        a = ctx.pushArena()
+        y, _ = fa.parakeetEncodeBatch(ctx, enc, mels, attnFused=fused)
+        ctx.sync()
+        ctx.popArena(a)
+
+    res = {}
+    for fused in (False, True):
+        for _ in range(max(1, args.warmup)):
+            run(fused)
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            run(fused)
+        wall = (time.perf_counter() - t0) / args.steps
+        res["attnFused" if fused else "chain"] = {"ms_per_step": round(wall * 1e3, 2), "value": round(240.0 / wall, 1)}
+        log(f"[bench] op path, attnFused={fused}: {wall * 1e3:.1f} ms per 16 x 15 s")
+    # launches per batch and the op path's busiest kernels, from one profiled batch
+    ctx.startProfile(20000)
+    run(True)
+    prof = ctx.endProfile()
+    for r in prof:
+        k = line_kern.setdefault(r["label"], {"launches": 0, "ms": 0.0})
+        k["launches"] += 1
+        k["ms"] += r["ms"]
+    top = sorted(line_kern.items(), key=lambda kv: -kv[1]["ms"])[:12]
+    best = max(res.values(), key=lambda v: v["value"])
+    line = {"metric": "encoder audio-s/wall-s at 1 GPU (reference op sequence)", "value": best["value"], "unit": "audio-s/wall-s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": best["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f16", "data": "synthetic log-mel ~N(0,1) (seed 1), random-init weights (seed 1)",
+            "config": {"workload": "configs[2] (24 layers, 16 x 15 s) through parakeetEncodeBatch's ComputeContext calls, f16 weights, one "
+                                   "withBatchSync per batch", "launches_per_batch": len(prof)},
+            "variants": res,
+            "kernels_top": {k: {"launches": v["launches"], "ms_per_batch": round(v["ms"], 3)} for k, v in top}}
     print(json.dumps(line), flush=True)
 
 

@@ -140,10 +140,15 @@ def _pre_encode(ctx, enc, mel):
     return ctx.matmul(flat, enc["sub"]["linw"], bias=enc["sub"]["linb"]), Hh
 
 
-def parakeetEncodeBatch(ctx: HipContext, enc: dict, mels: list) -> tuple:
+def parakeetEncodeBatch(ctx: HipContext, enc: dict, mels: list, attnFused: bool = False) -> tuple:
     """raw-encoder.js:235-386, including the streaming models' options
     (chunk-limited attention mask, causal depthwise conv, conv-module
-    LayerNorm).  Returns (frames [W*Tsub, D] tensor, Tsub)."""
+    LayerNorm).  Returns (frames [W*Tsub, D] tensor, Tsub).  As in the
+    reference, the positional projection of a batched (W > 1) Tsub is cached
+    per layer (raw-encoder.js:304-321), and attnFused=True (the reference's
+    opt-in globalThis.__attnFused, raw-encoder.js:334) sends unmasked
+    attention through the context's attnFused member instead of the
+    bmmQK / relShiftB / softmax / bmmPV chain."""
     cfg = enc["cfg"]
     D, H, HD, K = cfg["D"], cfg["H"], cfg["HD"], cfg["dwK"]
     W = len(mels)
@@ -170,14 +175,27 @@ def parakeetEncodeBatch(ctx: HipContext, enc: dict, mels: list) -> tuple:
             q = ctx.matmul(xln, w["q"], bias=w["qb"])
             k = ctx.matmul(xln, w["k"], bias=w["kb"])
             v = ctx.matmul(xln, w["v"], bias=w["vb"])
-            p = ctx.matmul(peT, w["pos"])
-            ac = ctx.bmmQK(q, k, w["pbuAll"], H, HD, W)
-            bd = ctx.relShiftB(ctx.bmmQK(q, p, w["pbvAll"], H, HD, W, True), W * H)
-            sc = ctx.add(ac, bd)
-            if maskT is not None:
-                sc = ctx.add(sc, maskT)
-            probs = ctx.softmax(sc)
-            outc = ctx.bmmPV(probs, v, H, HD, W)
+            if W > 1:
+                cache = enc.setdefault("_posProj", {})
+                key = (id(w), Tsub)
+                p = cache.get(key)
+                if p is None:
+                    p = ctx.matmul(peT, w["pos"])
+                    ctx.pin(p)  # cached across groups: exempt from the arena
+                    cache[key] = p
+            else:
+                p = ctx.matmul(peT, w["pos"])
+            outc = None
+            if maskT is None and attnFused and hasattr(ctx, "attnFused"):
+                outc = ctx.attnFused(q, k, v, p, w["pbuAll"], w["pbvAll"], H, HD, W)
+            if outc is None:
+                ac = ctx.bmmQK(q, k, w["pbuAll"], H, HD, W)
+                bd = ctx.relShiftB(ctx.bmmQK(q, p, w["pbvAll"], H, HD, W, True), W * H)
+                sc = ctx.add(ac, bd)
+                if maskT is not None:
+                    sc = ctx.add(sc, maskT)
+                probs = ctx.softmax(sc)
+                outc = ctx.bmmPV(probs, v, H, HD, W)
             x = ctx.matmul(outc, w["out"], bias=w["outb"], add=x)
             pre1 = ctx.matmul(ln(x, w["lnconv"]), w["pw1T"], bias=w["pw1b"])
             glu = ctx.glu(ctx.transpose(pre1))

@@ -279,3 +279,23 @@ def test_forward_stream_batches_equal_one_batch_at_a_time(ctx, fa, small, monkey
     ctx.popArena(arena)
     ctx.freeTensor(f)
     enc.close()
+
+
+def test_op_path_attn_fused_member_matches_op_chain(ctx, fa):
+    """parakeetEncodeBatch with the reference's opt-in attnFused member
+    (raw-encoder.js:334) against the bmmQK / relShiftB / softmax / bmmPV
+    chain, fp32 weights, two layers, two windows (the positional projection
+    cached per layer across the two calls)."""
+    cfg = dict(D=256, DFF=1024, H=2, HD=128, layers=2, dwK=9, Csub=64, Fsub=16, melBins=128)
+    man = fa.synth.make_weights(cfg, seed=4)
+    enc = fa.loadParakeetEncoder(ctx, man, weights="f32")
+    mels = fa.synth.make_features(128, 400, seed=5, W=2)
+    outs = []
+    for fused in (False, True):
+        a = ctx.pushArena()
+        y, T = fa.parakeetEncodeBatch(ctx, enc, mels, attnFused=fused)
+        outs.append(ctx.download(y).reshape(-1, 256))
+        ctx.popArena(a)
+    d = float(np.linalg.norm(outs[1] - outs[0]) / np.linalg.norm(outs[0]))
+    print(f"op path: attnFused vs op chain rel-L2 {d:.2e}")
+    assert d < 1e-4
