@@ -381,6 +381,15 @@ __device__ __forceinline__ void epilogue_direct(const GemmArgs &p, f4 (&acc)[TI]
           o[2 * e + 1] = (_Float16)(t - (float)hi);
         }
         *reinterpret_cast<h8 *>(reinterpret_cast<_Float16 *>(p.C) + (size_t)row * p.ldc + 2 * col) = o;
+      } else if constexpr (EPI == EPI_GENERIC) {  // the ComputeContext's act-then-add, f32 or f16 out
+        f4 t;
+#pragma unroll
+        for (int e = 0; e < 4; e++) t[e] = act_apply(v[e], p.act);
+        if (p.add) t += *reinterpret_cast<const f4 *>(p.add + (size_t)row * p.ldadd + col);
+        if (p.out_f16)
+          *reinterpret_cast<h4 *>(reinterpret_cast<_Float16 *>(p.C) + (size_t)row * p.ldc + col) = h4{to_f16(t[0]), to_f16(t[1]), to_f16(t[2]), to_f16(t[3])};
+        else
+          *reinterpret_cast<f4 *>(reinterpret_cast<float *>(p.C) + (size_t)row * p.ldc + col) = t;
       } else {
         h4 o, ol;
 #pragma unroll
@@ -1008,6 +1017,8 @@ static int launch_tile(fa_ctx *ctx, const GemmArgs &p, const char *label) {
         default: return set_err(ctx, FA_E_UNSUPPORTED, "%s: lo plane needs N %% 128 == 0, K %% 64 == 0 and 16-byte aligned operands", label);
       }
     }
+  }
+  if constexpr (AK == A_F16 && BKND == B_F16) {  // also the ComputeContext's generic (act-then-add) epilogue
     switch (pick_dma(ctx, p)) {
       case 0: return launch_dma<192, 256, 2, 4, 2, EPI>(ctx, p, label);
       case 1: return launch_dma<192, 128, 4, 2, 3, EPI>(ctx, p, label);

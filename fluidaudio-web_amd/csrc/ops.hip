@@ -170,6 +170,21 @@ __global__ void conv1d_kernel(const float *x, const float *w, const float *bias,
     y[idx] = act_apply(acc, act);
   }
 }
+// f32 -> f16 (round to nearest even), 4 values per thread (n % 4 == 0)
+__global__ void round_f16_kernel(const float *__restrict__ x, _Float16 *__restrict__ y, long n) {
+  for (long i = ((long)blockIdx.x * blockDim.x + threadIdx.x) * 4; i < n; i += (long)gridDim.x * blockDim.x * 4) {
+    const float4 v = *reinterpret_cast<const float4 *>(x + i);
+    *reinterpret_cast<h4 *>(y + i) = h4{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+  }
+}
+// y[r][c] = act(y[r][c] + bias[r]) over rows of `cols` values (bias may be null)
+__global__ void chan_bias_act_kernel(float *__restrict__ y, const float *__restrict__ bias, int cols, long n, int act) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    float v = y[i];
+    if (bias) v += bias[i / cols];
+    y[i] = act_apply(v, act);
+  }
+}
 __global__ void conv2d_kernel(const float *x, const float *w, const float *bias, float *y, int cout, int cin, int H, int Wd, int Ho, int Wo, int kh,
                               int kw, int sh, int sw, int pt, int pl, int groups, int act) {
   const long n = (long)cout * Ho * Wo;
@@ -386,8 +401,24 @@ static int matmul_impl(fa_ctx *ctx, fa_tensor a, fa_tensor b, fa_tensor bias, in
   if (ra->kind == S_F16RM && (rb->kind != S_F16KM || K % 64)) return set_err(ctx, FA_E_UNSUPPORTED, "matmul: f16 A needs an f16 B and K %% 64 == 0");
   if (rb->kind == S_F16KM) {
     if (K % 64 == 0) {
+      // f32 A on the f16 route is rounded to f16 (compute.js:413-416): for
+      // more than a few rows it is rounded once into a scratch tensor, so the
+      // product runs on the direct-to-LDS kernels (same values and K order as
+      // the register-staged kernel, which rounds inside its loads)
+      fa_tensor a16 = 0;
+      TensorRec *r16 = nullptr;
+      if (ra->kind == S_F32 && M >= 256) {
+        FA_TRY(new_tensor(ctx, M, K, S_F16RM, (size_t)M * K * 2, &a16, &r16));
+        ra = get(ctx, a); rb = get(ctx, b); rbias = bias ? get(ctx, bias) : nullptr; radd = add ? get(ctx, add) : nullptr; ro = get(ctx, og.t);
+        ProfScope ps(ctx, "matmul_a16");
+        const long n = (long)M * K;
+        FA_LAUNCH(ps, round_f16_kernel, dim3((unsigned)std::min<long>(cdiv(n / 4, 256), 4096)), dim3(256), 0, ctx->stream, F32(ra),
+                  (_Float16 *)r16->ptr, n);
+        FA_TRY(check_launch(ctx, "matmul_a16"));
+      }
+      TensorGuard g16(ctx, a16);  // pool-ordered: released after the product is queued
       GemmArgs p;
-      p.A = ra->ptr; p.lda = K; p.akind = ra->kind == S_F16RM ? A_F16 : A_F32;
+      p.A = r16 ? r16->ptr : ra->ptr; p.lda = K; p.akind = (r16 || ra->kind == S_F16RM) ? A_F16 : A_F32;
       p.B = rb->ptr; p.bkind = B_F16;
       p.C = ro->ptr; p.ldc = N;
       p.bias = CF32(rbias); p.add = CF32(radd); p.ldadd = N; p.act = act;
@@ -803,6 +834,20 @@ int fa_conv2d(fa_ctx *ctx, fa_tensor x, fa_tensor w, int cout, int cin, int h, i
   FA_TRY(new_tensor(ctx, cout, Ho * Wo, S_F32, (size_t)cout * Ho * Wo * 4, &o, &ro));
   TensorGuard og(ctx, o);  // released unless the op completes
   rx = get(ctx, x); rw = get(ctx, w); rb = bias ? get(ctx, bias) : nullptr;
+  if (kh == 1 && kw == 1 && sh == 1 && sw == 1 && groups == 1 && pt == 0 && pb == 0 && pl == 0 && pr == 0 && cin % 16 == 0 && (Ho * Wo) % 4 == 0) {
+    // a pointwise conv is the product W [cout, cin] x X [cin, H*W] (channel-major
+    // x is row-major X): the f32 GEMM, then the per-channel bias and activation
+    FA_TRY(gemm_f32(ctx, F32(rw), F32(rx), F32(ro), nullptr, nullptr, cout, Ho * Wo, cin, 0, "conv2d_pw"));
+    if (rb || act) {
+      ProfScope ps(ctx, "conv2d_pw_bias");
+      const long n = (long)cout * Ho * Wo;
+      FA_LAUNCH(ps, chan_bias_act_kernel, dim3((unsigned)std::min<long>(cdiv(n, 256), 8192)), dim3(256), 0, ctx->stream, F32(ro), CF32(rb), Ho * Wo,
+                n, act);
+      FA_TRY(check_launch(ctx, "conv2d_pw_bias"));
+    }
+    *out = og.release();
+    return FA_OK;
+  }
   ProfScope ps(ctx, "conv2d");
   FA_LAUNCH(ps, conv2d_kernel, dim3(gs((long)cout * Ho * Wo)), dim3(256), 0, ctx->stream, F32(rx), F32(rw), CF32(rb), F32(ro), cout, cin, h, wd,
                      Ho, Wo, kh, kw, sh, sw, pt, pl, groups, act);
