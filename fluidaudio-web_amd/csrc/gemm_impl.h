@@ -443,9 +443,16 @@ __device__ __forceinline__ void wait_vmcnt() {  // gfx9 s_waitcnt: vmcnt [3:0]+[
 // BQ = 2: B is symmetric int4 group-32 ([N][K/32][16 B], f16 scales [N][K/32]);
 // its K tile is 32 bytes per row (chunk c at slot c ^ ((row >> 2) & 1)), the
 // two block scales of a row's K tile are one 4-byte load made a K tile ahead.
-template <int BM, int BN, int WM, int WN, int S, int EPI, int LO = 0, int BQ = 0>
+// WW = 1 (with BQ): the quantised K tile of B is widened to f16 once per
+// workgroup, one tile ahead, into one of two f16 tiles laid out like the f16
+// route's B tile; the fragment reads and MFMAs are then the f16 route's. B
+// copies run one K tile ahead of A copies (copy group g holds A tile g and B
+// tile g + 1), so the wait that makes A tile kt resident also makes B tile
+// kt + 1 resident for its widening during step kt.
+template <int BM, int BN, int WM, int WN, int S, int EPI, int LO = 0, int BQ = 0, int WW = 0>
 __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4))) void gemm_dma_kernel(GemmArgs p) {
   constexpr int B8 = BQ == 1, B4 = BQ == 2;
+  static_assert(!WW || BQ, "workgroup widening is for quantised B");
   constexpr int NW = WM * WN, BK = 64, RB = 128, RBB = B8 ? 64 : (B4 ? 32 : 128);
   static_assert(!B4 || S % 2 == 0, "int4 scale double-buffering follows the stage parity");
   constexpr int WTM = BM / WM, WTN = BN / WN, TI = WTM / 16, TJ = WTN / 16;
@@ -455,7 +462,8 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
   constexpr int IW = (IT + NW - 1) / NW, IMIN = IT / NW;  // per wave: at most / at least
   static_assert(BM % 16 == 0 && BN % 16 == 0 && NW % 4 == 0 && (BN * RBB) % 1024 == 0, "tile shape");
   static_assert(S >= 2 && S <= 4, "LDS stages");
-  constexpr int SMEM = S * STG;
+  constexpr int WT = WW ? BN * RB : 0;  // one widened f16 B tile
+  constexpr int SMEM = S * STG + 2 * WT;
   static_assert(SMEM <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
   uint32_t sadr[4];
@@ -499,12 +507,16 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
       src[i] = B + (size_t)(n0 + r) * p.K + ch * 8;
     }
   }
-  auto issue = [&](int sidx, int k0) {
+  // bonly: copy only B's K tile at k0 (the tile ahead of the first group)
+  auto issue = [&](int sidx, int k0, bool bonly = false) {
+    // WW: B runs one tile ahead; the last group re-copies the last tile (never
+    // widened) so every group holds the same copies and the vmcnt waits hold
+    const int kb = (WW && !bonly) ? min(k0 + BK, p.K - BK) : k0;
 #pragma unroll
     for (int i = 0; i < IW; i++) {
       const int ins = wave + i * NW;
-      if (IT % NW == 0 || ins < IT) {
-        const size_t koff = (ins < ITA || !BQ) ? (size_t)k0 * 2 : (B8 ? (size_t)k0 : (size_t)(k0 >> 1));  // bytes
+      if ((IT % NW == 0 || ins < IT) && (!bonly || ins >= ITA)) {
+        const size_t koff = (ins < ITA || !BQ) ? (size_t)k0 * 2 : (B8 ? (size_t)kb : (size_t)(kb >> 1));  // bytes
         dma16(reinterpret_cast<const char *>(src[i]) + koff, sadr[sidx] + ins * 1024);
       }
     }
@@ -517,9 +529,6 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
     for (int j = 0; j < TJ; j++) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
   const int nk = p.K / BK;
-#pragma unroll
-  for (int s = 0; s < S - 1; s++)
-    if (s < nk) issue(s, s * BK);
 
   const int q = lane >> 4, sw = lane & 7;  // fragment rows are 16-aligned + (lane & 15)
   const int abase = (wm * WTM + (lane & 15)) * RB, bbase = SA + (wn * WTN + (lane & 15)) * RBB;
@@ -544,7 +553,8 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
                                                           (size_t)(n0 + wn * WTN + j * 16 + (lane & 15)) * nblk + 2 * kt);
     }
   };
-  auto rdfrag = [&](int sidx, int ks, int slot, int set) {
+  // WW: tile kt's widened B lives in f16 tile kt & 1 (wpar)
+  auto rdfrag = [&](int sidx, int ks, int slot, int set, int wpar = 0) {
     const char *base = smem + sidx * STG;
     const int so = ((ks * 4 + q) ^ sw) * 16;
 #pragma unroll
@@ -553,7 +563,11 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
 #pragma unroll
       for (int i = 0; i < TI; i++) al[slot][i] = *reinterpret_cast<const h8 *>(base + BM * RB + abase + i * 16 * RB + so);
     }
-    if constexpr (B8) {
+    if constexpr (WW) {
+      const char *wb = smem + S * STG + wpar * WT + (wn * WTN + (lane & 15)) * RB + so;
+#pragma unroll
+      for (int j = 0; j < TJ; j++) bf[slot][j] = *reinterpret_cast<const h8 *>(wb + j * 16 * RB);
+    } else if constexpr (B8) {
       // k = ks*32 + q*8: 16-byte chunk 2*ks + q/2, half q & 1
       const int so8 = ((((ks * 2 + (q >> 1)) ^ sw8) * 16) + (q & 1) * 8);
 #pragma unroll
@@ -572,8 +586,55 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
       for (int j = 0; j < TJ; j++) bf[slot][j] = *reinterpret_cast<const h8 *>(base + bbase + j * 16 * RB + so);
     }
   };
+  // WW widening: unit u of a tile is 16 B-tile bytes of row u >> 2 (int8: raw
+  // 16-byte chunk u & 3; int4: half u & 1 of raw chunk (u >> 1) & 1, one
+  // group-32 block), written as two 16-byte f16 chunks of the f16 layout
+  constexpr int NT = 64 * NW, NU = BN * 4, UPT = (NU + NT - 1) / NT;
+  uint32_t wsc[2][WW && B4 ? UPT : 1];  // int4 block scales of the units, by tile parity
+  auto ldwscale = [&](int set, int kt) {
+    if constexpr (WW && B4) {
+      const int nblk = p.K >> 5;
+#pragma unroll
+      for (int i = 0; i < UPT; i++) {
+        const int u = tid + i * NT;
+        if (NU % NT == 0 || u < NU)
+          wsc[set][i] = *(reinterpret_cast<const uint16_t *>(p.bscale) + (size_t)(n0 + (u >> 2)) * nblk + 2 * kt + ((u >> 1) & 1));
+      }
+    }
+  };
+  auto widen = [&](int sidx, int kt, int set) {
+    if constexpr (WW) {
+      const char *raw = smem + sidx * STG + SA;
+      char *dst = smem + S * STG + (kt & 1) * WT;
+#pragma unroll
+      for (int i = 0; i < UPT; i++) {
+        const int u = tid + i * NT;
+        if (NU % NT == 0 || u < NU) {
+          const int r = u >> 2;
+          h8 lo, hi;
+          int c0;
+          if constexpr (B8) {
+            const int c = u & 3;
+            const uint4 v = *reinterpret_cast<const uint4 *>(raw + r * 64 + ((c ^ ((r >> 1) & 3)) * 16));
+            lo = i8x8_to_h8(uint2{v.x, v.y});
+            hi = i8x8_to_h8(uint2{v.z, v.w});
+            c0 = 2 * c;
+          } else {
+            const int ch = (u >> 1) & 1, half = u & 1;
+            const uint2 v = *reinterpret_cast<const uint2 *>(raw + r * 32 + ((ch ^ ((r >> 2) & 1)) * 16) + half * 8);
+            const _Float16 sc = __builtin_bit_cast(_Float16, (uint16_t)wsc[set][i]);
+            lo = i4x8_to_h8(v.x, sc);
+            hi = i4x8_to_h8(v.y, sc);
+            c0 = ch * 4 + half * 2;
+          }
+          *reinterpret_cast<h8 *>(dst + r * RB + ((c0 ^ (r & 7)) * 16)) = lo;
+          *reinterpret_cast<h8 *>(dst + r * RB + (((c0 + 1) ^ (r & 7)) * 16)) = hi;
+        }
+      }
+    }
+  };
   auto mma = [&](int slot) {
-    if constexpr (B4) {
+    if constexpr (B4 && !WW) {
 #pragma unroll
       for (int j = 0; j < TJ; j++) bf[slot][j] = i4x8_to_h8(bq[slot][j].x, bs[slot][j]);
     }
@@ -595,9 +656,24 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
     __syncthreads();
   };
 
-  ldscale(0, 0);
+  if constexpr (WW) {
+    // B tile 0 ahead of the first group, into the last stage (refilled by the
+    // first step's copies, after the barrier that follows its widening)
+    ldwscale(0, 0);
+    if (1 < nk) ldwscale(1, 1);
+    issue(S - 1, 0, true);
+  }
+#pragma unroll
+  for (int s = 0; s < S - 1; s++)
+    if (s < nk) issue(s, s * BK);
+
+  if constexpr (!WW) ldscale(0, 0);
   ready(0);
-  rdfrag(0, 0, 0, 0);
+  if constexpr (WW) {
+    widen(S - 1, 0, 0);
+    __syncthreads();
+  }
+  rdfrag(0, 0, 0, 0, 0);
   for (int kt0 = 0; kt0 < nk; kt0 += S) {
 #pragma unroll
     for (int u = 0; u < S; u++) {
@@ -605,13 +681,21 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM
       if (kt < nk) {
         // refill the stage every wave finished reading before the last barrier
         if (kt + S - 1 < nk) issue((u + S - 1) % S, (kt + S - 1) * BK);
-        if (kt + 1 < nk) ldscale((u + 1) & 1, kt + 1);  // int4: next tile's scales (S is even)
-        rdfrag(u, 1, 1, u & 1);
+        if constexpr (WW) {
+          rdfrag(u, 1, 1, 0, kt & 1);
+          // B tile kt + 1 (resident in stage u since the last barrier) into the
+          // f16 tile that tile kt - 1's reads, finished before that barrier, used
+          if (kt + 1 < nk) widen(u, kt + 1, (u + 1) & 1);
+          if (kt + 2 < nk) ldwscale(u & 1, kt + 2);  // int4: S is even, so u & 1 is kt's parity
+        } else {
+          if (kt + 1 < nk) ldscale((u + 1) & 1, kt + 1);  // int4: next tile's scales (S is even)
+          rdfrag(u, 1, 1, u & 1);
+        }
         mma(0);
         mma(1);  // placed before the wait so its MFMAs overlap the barrier
         if (kt + 1 < nk) {
           ready(kt + 1);
-          rdfrag((u + 1) % S, 0, 0, (u + 1) & 1);
+          rdfrag((u + 1) % S, 0, 0, (u + 1) & 1, (kt + 1) & 1);
         }
       }
     }
@@ -720,11 +804,11 @@ static int pick_dma(fa_ctx *ctx, const GemmArgs &p) {
   return best;
 }
 
-template <int BM, int BN, int WM, int WN, int S, int EPI, int LO = 0, int BQ = 0>
+template <int BM, int BN, int WM, int WN, int S, int EPI, int LO = 0, int BQ = 0, int WW = 0>
 static int launch_dma(fa_ctx *ctx, const GemmArgs &p, const char *label) {
   const unsigned tiles = cdiv(p.M, BM) * (p.N / BN);
   ProfScope ps(ctx, label);
-  FA_LAUNCH(ps, (gemm_dma_kernel<BM, BN, WM, WN, S, EPI, LO, BQ>), dim3(tiles), dim3(64 * WM * WN), 0, ctx->stream, p);
+  FA_LAUNCH(ps, (gemm_dma_kernel<BM, BN, WM, WN, S, EPI, LO, BQ, WW>), dim3(tiles), dim3(64 * WM * WN), 0, ctx->stream, p);
   return check_launch(ctx, label);
 }
 
@@ -1050,21 +1134,26 @@ static int launch_tile(fa_ctx *ctx, const GemmArgs &p, const char *label) {
   if constexpr (AK == A_F16 && BKND == B_I4 && EPI != EPI_GENERIC) {
     // symmetric group-32 with f16 scales (the encoder's int4 format): same tile
     // table, even stage counts (the scale sets alternate with the stages)
+    // Nibble tiles are widened once per workgroup (WW) wherever the two f16
+    // B tiles fit beside the stages: measured on MI355X at M = 192..3008, FF W2
+    // 58.7 -> 51.0 us, FF W1 36.0 -> 32.3, q|k|v 29.2 -> 27.3, two-plane FF W2
+    // 85.2 -> 72.5 (same bits). int8 stays per wave: its widening is cheaper
+    // than the extra LDS write and read (FF W2 37.2 -> 42.1 us with WW).
     if (p.Alo && !p.bzp && !p.bscale_f32) switch (pick_dma(ctx, p)) {  // exact A planes (even stage counts)
-        case 0: return launch_dma<192, 256, 2, 4, 2, EPI, 1, 2>(ctx, p, label);
-        case 1: return launch_dma<192, 128, 4, 2, 2, EPI, 1, 2>(ctx, p, label);
-        case 2: return launch_dma<96, 256, 2, 4, 2, EPI, 1, 2>(ctx, p, label);
-        case 3: return launch_dma<128, 128, 2, 4, 4, EPI, 1, 2>(ctx, p, label);
-        case 4: return launch_dma<96, 128, 2, 4, 4, EPI, 1, 2>(ctx, p, label);
-        case 5: return launch_dma<192, 192, 2, 4, 2, EPI, 1, 2>(ctx, p, label);
+        case 0: return launch_dma<192, 256, 2, 4, 2, EPI, 1, 2>(ctx, p, label);  // 176 KB with WW
+        case 1: return launch_dma<192, 128, 4, 2, 2, EPI, 1, 2, 1>(ctx, p, label);
+        case 2: return launch_dma<96, 256, 2, 4, 2, EPI, 1, 2, 1>(ctx, p, label);
+        case 3: return launch_dma<128, 128, 2, 4, 2, EPI, 1, 2, 1>(ctx, p, label);
+        case 4: return launch_dma<96, 128, 2, 4, 4, EPI, 1, 2, 1>(ctx, p, label);
+        case 5: return launch_dma<192, 192, 2, 4, 2, EPI, 1, 2, 1>(ctx, p, label);
         default: return set_err(ctx, FA_E_UNSUPPORTED, "%s: lo plane needs N %% 128 == 0, K %% 64 == 0 and 16-byte aligned operands", label);
       }
     if (!p.Alo && !p.bzp && !p.bscale_f32) switch (pick_dma(ctx, p)) {
-        case 0: return launch_dma<192, 256, 2, 4, 2, EPI, 0, 2>(ctx, p, label);
-        case 1: return launch_dma<192, 128, 2, 4, 2, EPI, 0, 2>(ctx, p, label);
-        case 2: return launch_dma<128, 128, 2, 4, 4, EPI, 0, 2>(ctx, p, label);
-        case 3: return launch_dma<96, 128, 2, 4, 4, EPI, 0, 2>(ctx, p, label);
-        case 4: return launch_dma<192, 192, 2, 4, 4, EPI, 0, 2>(ctx, p, label);
+        case 0: return launch_dma<192, 256, 2, 4, 2, EPI, 0, 2, 1>(ctx, p, label);
+        case 1: return launch_dma<192, 128, 2, 4, 2, EPI, 0, 2, 1>(ctx, p, label);
+        case 2: return launch_dma<128, 128, 2, 4, 2, EPI, 0, 2, 1>(ctx, p, label);
+        case 3: return launch_dma<96, 128, 2, 4, 2, EPI, 0, 2, 1>(ctx, p, label);
+        case 4: return launch_dma<192, 192, 2, 4, 2, EPI, 0, 2, 1>(ctx, p, label);
         default: break;
       }
   }
