@@ -303,7 +303,7 @@ def main():
     ap.add_argument("--workload", default="encoder", choices=["encoder", "layer", "ragged", "quant", "quant4", "gemv", "copy", "mel", "decode", "e2e", "stream", "oppath"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--windows", type=int, default=16, help="decode workload: windows per decode call (1..64)")
-    ap.add_argument("--audio-sec", type=float, default=3600.0, help="e2e workload: seconds of synthetic audio")
+    ap.add_argument("--audio-sec", type=float, default=470.0, help="e2e workload: seconds of synthetic audio (at most 470: longer inputs faulted)")
     ap.add_argument("--streams", default="4,8,16,32", help="stream workload: concurrent stream counts timed after the single stream")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -520,23 +520,23 @@ def bench_decode(args, fa, ctx):
 
 
 def bench_e2e(args, fa, ctx):
-    """Windowed transcription end to end (pipeline.transcribeWindowed): 1 h of
-    synthetic speech-like PCM -> log-mel -> 24-layer encoder (f16 weights) ->
-    joint projection -> greedy TDT decode -> seam stitching, the reference's
-    headline configuration (README.md:10-12: 1 h file, 293x RTFx on
-    Chrome/macOS WebGPU).  One step = one full transcription, pipelined
-    (fa_transcribe_groups: group g+1's mel / encoder / projection on an
-    encoder lane while group g decodes), groups of up to 32 windows; value =
-    audio-s / wall-s (RTFx).  The same transcription stage by stage
-    (pipelined=False) is timed beside it, and one stage-by-stage pass with a
-    synchronisation after each stage gives the stages' own times.  No profile
-    window is open.  Synthetic weights: the tokens are meaningless, every
-    stage does its full work."""
+    """Windowed transcription end to end (pipeline.transcribeWindowed): 470 s
+    of synthetic speech-like PCM (37 windows, 3 groups) -> log-mel -> 24-layer encoder (f16 weights) ->
+    joint projection -> greedy TDT decode -> seam stitching; the reference's
+    headline configuration is a 1 h file (README.md:10-12: 293x RTFx on
+    Chrome/macOS WebGPU), whose transcription faulted here.  One step = one full transcription, stage by stage
+    on the context stream (pipelined=False: the cross-stream pipelined form
+    stays off, its full-size run made an illegal memory access with no cause
+    shown), groups of up to 32 windows; value = audio-s / wall-s (RTFx).  One
+    more pass with a synchronisation after each stage gives the stages' own
+    times.  No profile window is open.  Synthetic weights: the tokens are
+    meaningless, every stage does its full work."""
     import importlib
     pl = importlib.import_module(fa.__name__ + ".pipeline")
-    raise SystemExit("bench --workload e2e is switched off: its pipelined run at full size (24 layers, 3600 s, 32-window groups) made an "
-                     "illegal memory access with no cause shown yet, and an earlier stage-by-stage run at 64-window groups faulted too")
     seconds = args.audio_sec
+    if seconds > 470.0:
+        raise SystemExit("bench --workload e2e runs at most 470 s of audio: every transcription of the hour (64- and 32-window groups, stage "
+                         "by stage and pipelined) made an illegal memory access on the GPU with no cause shown yet; 470 s ran")
     audio = fa.synth.make_pcm(seconds, seed=1)
     man = fa.synth.make_weights(dict(FULL), seed=1)
     enc = fa.FusedEncoder(ctx, man, "f16", max_T=188)
@@ -546,20 +546,16 @@ def bench_e2e(args, fa, ctx):
     W, b = fa.synth.make_joint_projection(2)
     projW, projB = ctx.upload(W, W.shape[0], W.shape[1]), ctx.upload(b.reshape(1, -1), 1, b.size)
     log(f"[bench] e2e: {seconds:.0f} s of audio, weights loaded")
-    for _ in range(max(1, args.warmup)):
-        r = pl.transcribeWindowed(ctx, enc, dec, projW, projB, audio)
-        rs = pl.transcribeWindowed(ctx, enc, dec, projW, projB, audio, pipelined=False)
-    assert r["ids"] == rs["ids"], "pipelined and stage-by-stage transcriptions differ"
+    for i in range(max(1, args.warmup)):
+        log(f"[bench] e2e warmup transcription {i}")
+        r = pl.transcribeWindowed(ctx, enc, dec, projW, projB, audio, pipelined=False)
     log(f"[bench] e2e warm: {r['stats']}")
     ctx.sync()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        r = pl.transcribeWindowed(ctx, enc, dec, projW, projB, audio)
+    for i in range(args.steps):
+        r = pl.transcribeWindowed(ctx, enc, dec, projW, projB, audio, pipelined=False)
+        log(f"[bench] e2e step {i}: {time.perf_counter() - t0:.3f} s")
     wall = (time.perf_counter() - t0) / args.steps
-    t0 = time.perf_counter()
-    for _ in range(max(1, args.steps // 4)):
-        pl.transcribeWindowed(ctx, enc, dec, projW, projB, audio, pipelined=False)
-    wall_serial = (time.perf_counter() - t0) / max(1, args.steps // 4)
     # the stages' own times: every group's stages one after another, synchronised
     tsub = importlib.import_module(fa.__name__ + ".encoder").tsub
     x = np.ascontiguousarray(audio, np.float32)
@@ -600,9 +596,8 @@ def bench_e2e(args, fa, ctx):
             "scaling": "weak", "vs_baseline": round(seconds / wall / 293.0, 2), "baseline_note": "293x RTFx, 1 h file, Chrome/macOS WebGPU (README.md:10-12); other hardware",
             "dtype": "f16", "data": "synthetic speech-like PCM, random-init encoder/decoder/projection weights",
             "config": {"workload": f"{seconds:.0f} s PCM, 15 s windows at 13 s hop, groups of up to {pl.MAX_WINDOWS} windows, Parakeet TDT 0.6B shapes "
-                                   "(24 layers), pipelined: group g+1's mel / encoder / projection on an encoder lane while group g decodes",
+                                   "(24 layers), stage by stage on one stream",
                        "windows": r["stats"]["windows"], "groups": r["stats"]["groups"], "tokens": r["stats"]["tokens"]},
-            "stage_by_stage": {"ms_per_step": round(wall_serial * 1e3, 2), "value": round(seconds / wall_serial, 1)},
             "stages_ms": {k: round(v * 1e3, 2) for k, v in stages.items()}}
     if not args.no_cpu:
         # one window through the oracle: mel + preEncode + 1 layer (scaled to 24) + decode of the window's frames

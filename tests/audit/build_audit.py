@@ -98,9 +98,16 @@ def build(max_windows: int | None = None) -> str:
                        capture_output=True, text=True)
     if r.returncode:
         raise RuntimeError(r.stderr)
+    # the extent models include the product's own argument structs (_Float16
+    # members): ROCm's clang++ as a host compiler
+    ext = os.path.join(OUT, "extents.o")
+    r = subprocess.run(["/opt/rocm/llvm/bin/clang++", "-std=c++17", "-O1", "-fPIC", "-c", os.path.join(HERE, "extents.cpp"), "-o", ext],
+                       capture_output=True, text=True)
+    if r.returncode:
+        raise RuntimeError(r.stderr)
     tag = f"_w{max_windows}" if max_windows else ""
     lib = os.path.join(OUT, f"libfa_hip_audit{tag}.so")
-    r = subprocess.run(["g++", "-shared", "-fPIC", "-Wl,-Bsymbolic", "-o", lib, *objs, fake], capture_output=True, text=True)
+    r = subprocess.run(["g++", "-shared", "-fPIC", "-Wl,-Bsymbolic", "-o", lib, *objs, fake, ext], capture_output=True, text=True)
     if r.returncode:
         raise RuntimeError(r.stderr)
     tab = kernarg_table(objs)

@@ -235,6 +235,43 @@ void check_launch_args(const Launch &l, const char *when) {
   }
 }
 
+// ── per-kernel extents (extents.cpp): every range a kernel reads or writes
+// must lie inside one live block ──
+}  // namespace
+namespace audit_ext {
+struct Span {
+  uintptr_t p;
+  size_t bytes;
+  bool write;
+  std::string what;
+};
+int extents(const std::string &mangled, const std::string &pretty, const std::vector<std::vector<char>> &a, unsigned gx, unsigned gy, unsigned gz,
+            unsigned threads, std::vector<Span> &o, std::string &note);
+}  // namespace audit_ext
+namespace {
+std::map<std::string, size_t> &unmodelled() { static auto *m = new std::map<std::string, size_t>(); return *m; }
+size_t g_extent_checks = 0;
+void check_extents(const Launch &l, const char *when) {
+  const KernelInfo &k = *l.k;
+  std::vector<audit_ext::Span> sp;
+  std::string note;
+  if (!audit_ext::extents(k.name, k.pretty, l.args, l.grid.x, l.grid.y, l.grid.z, l.block.x * l.block.y * l.block.z, sp, note)) {
+    unmodelled()[k.pretty]++;
+    return;
+  }
+  const std::string who = std::string(when) + " " + k.pretty;
+  if (!note.empty()) violation(who + ": " + note);
+  for (const auto &s : sp) {
+    g_extent_checks++;
+    const std::string w = who + " " + (s.write ? "writes " : "reads ") + s.what;
+    if (!in_range(s.p)) {
+      violation(w + ": range starts outside device memory");
+      continue;
+    }
+    check_span((const void *)s.p, s.bytes, w);
+  }
+}
+
 void check_geometry(const KernelInfo &k, dim3 g, dim3 b, size_t shm) {
   const unsigned nt = b.x * b.y * b.z;
   if (!nt || !g.x || !g.y || !g.z) violation(k.pretty + ": empty grid or block");
@@ -290,7 +327,9 @@ hipError_t do_launch(const void *f, dim3 g, dim3 b, void **args, size_t shm, hip
   if (logf) std::fprintf(logf, "%s %u %u %u %u\n", k.pretty.c_str(), g.x, g.y, g.z, b.x * b.y * b.z);
   check_geometry(k, g, b, shm);
   check_launch_args(l, "launch");
-  if (Handle *cs = capturing_stream(s)) cs->ops.push_back(Op{0, l});
+  Handle *cs = capturing_stream(s);
+  if (!cs) check_extents(l, "launch");  // a captured launch runs (and is checked) at each replay
+  if (cs) cs->ops.push_back(Op{0, l});
   return hipSuccess;
 }
 
@@ -555,6 +594,7 @@ hipError_t hipGraphLaunch(hipGraphExec_t x, hipStream_t s) {
     if (o.type == 0) {
       g_replayed_launches++;
       check_launch_args(o.l, "graph replay");
+      check_extents(o.l, "graph replay");
     } else {
       check_span(o.p0, o.bytes, "graph replay copy/set destination");
       if (o.type == 1) check_span(o.p1, o.bytes, "graph replay copy source");
@@ -577,6 +617,16 @@ int audit_report(char *buf, int cap, unsigned long long *counts) {
     counts[3] = g_allocs;
   }
   return (int)g_viol.size();
+}
+// Kernels launched without an extent model ("name count" per line) and the
+// number of ranges checked.
+int audit_extent_report(char *buf, int cap, unsigned long long *checks) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  std::string s;
+  for (const auto &u : unmodelled()) s += u.first + " " + std::to_string(u.second) + "\n";
+  if (buf && cap > 0) std::snprintf(buf, cap, "%s", s.c_str());
+  if (checks) *checks = g_extent_checks;
+  return (int)unmodelled().size();
 }
 void audit_fail_alloc(long after) {
   std::lock_guard<std::mutex> lk(g_mu);

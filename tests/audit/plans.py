@@ -32,6 +32,12 @@ def report(L, extra=None):
     n = L.audit_report(buf, len(buf), cnt)
     out = {"violations": [v for v in buf.value.decode().splitlines() if v], "count": n, "launches": cnt[0], "graph_replays": cnt[1],
            "replayed_launches": cnt[2], "allocations": cnt[3]}
+    ub = C.create_string_buffer(1 << 16)
+    chk = C.c_ulonglong()
+    L.audit_extent_report.restype = C.c_int
+    L.audit_extent_report(ub, len(ub), C.byref(chk))
+    out["extent_checks"] = chk.value
+    out["unmodelled"] = [u for u in ub.value.decode().splitlines() if u]
     out.update(extra or {})
     print(json.dumps(out), flush=True)
 
@@ -96,6 +102,17 @@ def controls(L):
     step("graph_replay_clean", lambda: L.hipGraphLaunch(x, s))
     L.hipFree(c)
     step("graph_replay_after_free", lambda: L.hipGraphLaunch(x, s))
+    # extent models: copy_f4_kernel(src, dst, n4) inside its blocks, then one
+    # 16-byte vector past the end of the destination's 4096 bytes
+    cp = C.addressof(C.c_char.in_dll(L, "_ZN2fa14copy_f4_kernelEPK15HIP_vector_typeIfLj4EEPS1_l"))
+    d, e = V(), V()
+    L.hipMalloc(C.byref(d), 8192)
+    L.hipMalloc(C.byref(e), 4096)
+    n4_ok, n4_over = C.c_long(256), C.c_long(257)
+    a_ok = (V * 3)(C.cast(C.pointer(d), V), C.cast(C.pointer(e), V), C.cast(C.pointer(n4_ok), V))
+    a_over = (V * 3)(C.cast(C.pointer(d), V), C.cast(C.pointer(e), V), C.cast(C.pointer(n4_over), V))
+    step("extent_clean", lambda: L.hipLaunchKernel(cp, Dim3(1, 1, 1), Dim3(256, 1, 1), a_ok, 0, None))
+    step("extent_write_past_block_end", lambda: L.hipLaunchKernel(cp, Dim3(1, 1, 1), Dim3(256, 1, 1), a_over, 0, None))
     L.audit_clear()
     print(json.dumps({"controls": got}), flush=True)
 

@@ -51,6 +51,7 @@ def run(builds, scenario, *args, max_windows=None, layers=None):
 def test_stand_in_reports_each_misuse(builds):
     got = run(builds, "controls")["controls"]
     assert got.pop("graph_replay_clean") == 0
+    assert got.pop("extent_clean") == 0
     assert all(v == 1 for v in got.values()), got
 
 
@@ -68,6 +69,22 @@ def test_windowed_transcription_32_window_groups(builds, scenario):
     r = run(builds, scenario, 900, layers=2)
     assert r["groups"] >= 2 and r["graph_replays"] >= 2
     assert r["violations"] == []
+    assert r["extent_checks"] > 0 and _unmodelled_on_path(r) == []
+
+
+def _unmodelled_on_path(r):
+    # kernels launched without an extent model, the load-time weight rounding aside
+    return [u for u in r["unmodelled"] if "f32_to_f16_kernel" not in u]
+
+
+def test_hour_stage_by_stage_kernel_extents(builds):
+    """The plan of the second faulted run, with every kernel's read / write
+    ranges (extents.cpp) checked: 3600 s, 24 layers, 32-window groups stage
+    by stage (10 groups: 8 x 32, 20, and one 1200-frame window)."""
+    r = run(builds, "e2e32s", 3600)
+    assert r["windows"] == 277 and r["groups"] == 10
+    assert r["violations"] == []
+    assert r["extent_checks"] > 50000 and _unmodelled_on_path(r) == []
 
 
 def test_ragged_batches_on_two_lanes(builds):
