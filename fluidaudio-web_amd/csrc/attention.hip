@@ -219,6 +219,11 @@ __global__ __launch_bounds__(256) void v_transpose_kernel(const _Float16 *__rest
 __device__ __forceinline__ void attn_dma16(const void *g, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_addr) : "memory", "m0");
 }
+// the same copy from a wave-uniform base (SGPRs) plus the lane's 32-bit byte
+// offset: a block's copies then change only the scalar base
+__device__ __forceinline__ void attn_dma16_s(uint32_t voff, const void *sbase, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_addr) : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // Workgroup = QB = 16·NWV queries of one (window, head), one 16-query row
@@ -279,31 +284,61 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu((NWV +
   const uint32_t radr = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)ring);
   const int pbase0 = a.pcenter - (q0 + QB - 1);
 
+  // LDS layouts (64 banks read 16 lanes = 256 bytes at a time): a 256-byte K
+  // or band row r keeps its 16-byte chunk c at slot c ^ (key / band row & 15),
+  // a 64-byte Vt row d its chunk c at slot c ^ ((d >> 2) & 3), so the 16 rows
+  // one read phase touches hit distinct banks.
+  // copy i of this wave: the lane's byte offset from the block's scalar base
+  // (K rows, Vt rows, band rows), the same for every block
+  uint32_t voff[IW0];
+#pragma unroll
+  for (int i = 0; i < IW0; i++) {
+    const int ins = wave + i * NWV;
+    if (ins < 8) {
+      const int r = ins * 4 + (lane >> 4), ch = (lane & 15) ^ ((r >> 1) & 15);
+      voff[i] = (uint32_t)(r * a.ldk + ch * 8) * 2;
+    } else if (ins < 16) {
+      const int r = (ins - 8) * 16 + (lane >> 2), ch = (lane & 3) ^ ((r >> 2) & 3);
+      voff[i] = (uint32_t)(r * Tp + ch * 8) * 2;
+    } else {
+      const int rl = (ins - 16) * 4 + (lane >> 4), ch = (lane & 15) ^ (rl & 15);
+      voff[i] = (uint32_t)(rl * a.ldp + ch * 8) * 2;
+    }
+  }
   auto issue = [&](int sidx, int j0, int rb, auto first) {
     constexpr bool F = decltype(first)::value;
-    constexpr int IT = F ? IT0 : IT1, IW = F ? IW0 : IW1, R0 = F ? 0 : BR - KB;
+    constexpr int IT = F ? IT0 : IT1, IW = F ? IW0 : IW1, R0 = F ? 0 : BR - KB, PN = F ? BR : KB;
     const uint32_t base = sadr0 + (uint32_t)sidx * KVB;
+    // rows past the window (keys) or outside the positional table (band) are
+    // clamped, in the blocks that have them, with per-lane addresses
+    const bool kclamp = j0 + KB > T;
+    const int prow0 = pbase0 + j0 + R0;  // the first band row this issue copies (rb + R0 is a multiple of 16)
+    const bool pclamp = prow0 < 0 || prow0 + PN > a.prows;
 #pragma unroll
     for (int i = 0; i < IW; i++) {
       const int ins = wave + i * NWV;
       if (IT % NWV != 0 && ins >= IT) break;
-      const void *src;
-      uint32_t dst;
       if (ins < 8) {
-        const int r = ins * 4 + (lane >> 4), ch = (lane & 15) ^ ((r >> 1) & 7);
-        src = Kp + (size_t)min(j0 + r, T - 1) * a.ldk + ch * 8;
-        dst = base + ins * 1024;
+        const uint32_t dst = base + ins * 1024;
+        if (!kclamp) {
+          attn_dma16_s(voff[i], Kp + (size_t)j0 * a.ldk, dst);
+        } else {
+          const int r = ins * 4 + (lane >> 4), ch = (lane & 15) ^ ((r >> 1) & 15);
+          attn_dma16(Kp + (size_t)min(j0 + r, T - 1) * a.ldk + ch * 8, dst);
+        }
       } else if (ins < 16) {
-        const int r = (ins - 8) * 16 + (lane >> 2), ch = (lane & 3) ^ ((r >> 1) & 3);
-        src = Vt + (size_t)r * Tp + j0 + ch * 8;
-        dst = base + ins * 1024;
+        attn_dma16_s(voff[i], Vt + j0, base + ins * 1024);
       } else {
-        const int x = rb + R0 + (ins - 16) * 4, sl = (x + (lane >> 4)) & (RS - 1), ch = (lane & 15) ^ (sl & 7);
-        const int pr = min(max(pbase0 + j0 - rb + x + (lane >> 4), 0), a.prows - 1);
-        src = Pp + (size_t)pr * a.ldp + ch * 8;
-        dst = radr + (uint32_t)(x & (RS - 1)) * 256;
+        const int x = rb + R0 + (ins - 16) * 4;
+        const uint32_t dst = radr + (uint32_t)(x & (RS - 1)) * 256;
+        if (!pclamp) {
+          attn_dma16_s(voff[i], Pp + (size_t)prow0 * a.ldp, dst);
+        } else {
+          const int rl = (ins - 16) * 4 + (lane >> 4), ch = (lane & 15) ^ (rl & 15);
+          const int pr = min(max(prow0 + rl, 0), a.prows - 1);
+          attn_dma16(Pp + (size_t)pr * a.ldp + ch * 8, dst);
+        }
       }
-      attn_dma16(src, dst);
     }
   };
 
@@ -368,13 +403,13 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu((NWV +
     for (int kt = 0; kt < 2; kt++) {
       const int r = 2 * c16 + kt;  // MFMA row c16 of key tile kt = key 2 c16 + kt
 #pragma unroll
-      for (int s = 0; s < 4; s++) kf[kt][s] = *reinterpret_cast<const h8 *>(Ks + r * 256 + (((s * 4 + g) ^ ((r >> 1) & 7)) * 16));
+      for (int s = 0; s < 4; s++) kf[kt][s] = *reinterpret_cast<const h8 *>(Ks + r * 256 + (((s * 4 + g) ^ ((r >> 1) & 15)) * 16));
     }
 #pragma unroll
     for (int u = 0; u < 3; u++) {
       const int sl = (rb + lbw + u * 16 + c16) & (RS - 1);
 #pragma unroll
-      for (int s = 0; s < 4; s++) pf[u][s] = *reinterpret_cast<const h8 *>(ring + sl * 256 + (((s * 4 + g) ^ (sl & 7)) * 16));
+      for (int s = 0; s < 4; s++) pf[u][s] = *reinterpret_cast<const h8 *>(ring + sl * 256 + (((s * 4 + g) ^ (sl & 15)) * 16));
     }
     __builtin_amdgcn_sched_barrier(0);
     f4 sc[2], bd[3];
@@ -394,7 +429,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu((NWV +
 #pragma unroll
     for (int t = 0; t < 8; t++) {
       const int d = t * 16 + c16;
-      vf[t] = *reinterpret_cast<const h8 *>(Vs + d * 64 + ((g ^ ((d >> 1) & 3)) * 16));
+      vf[t] = *reinterpret_cast<const h8 *>(Vs + d * 64 + ((g ^ ((d >> 2) & 3)) * 16));
     }
 #pragma unroll
     for (int u = 0; u < 3; u++) *reinterpret_cast<f4 *>(strip + c16 * SW + u * 16 + g * 4) = bd[u];
