@@ -46,6 +46,20 @@ struct TdtStateM {
   float *dv;
   int *di, *ids, *frs, *alive;
 };
+// streaming passes: per-window cache pointers (encoder_impl.h KvSlots /
+// CcSlots) and output rows (stream.hip OutRows), kMaxStreamGroup = 16 windows
+constexpr int kSG = 16;
+struct KvSlotsM {
+  const _Float16 *kc_in[kSG], *vc_in[kSG];
+  _Float16 *kc_out[kSG], *vc_out[kSG];
+};
+struct CcSlotsM {
+  const float *cc_in[kSG];
+  float *cc_out[kSG];
+};
+struct OutRowsM {
+  float *dst[kSG];
+};
 constexpr int kTH = 640, kTV = 8193, kTL = 8198, kTNB = (kTL + 63) / 64, kTLP = kTNB * 64;
 constexpr int kBins = 257, kHop = 160;
 
@@ -353,6 +367,116 @@ int extents(const std::string &mangled, const std::string &pretty, const std::ve
     if ((long)gx * gy * gz < tiles) note = "GEMM: grid below its tiles";
     if (dma && (p.N % BN || p.K % 64)) note = "GEMM: N or K not a whole number of tiles";
     gemm_spans(p, (int)epi, o, note);
+    return 1;
+  }
+  if (has("gemm_skinny_kernel") || has("gemm_skinny_split_sum_kernel") || has("gemm_skinny_ln_kernel")) {
+    if (!size_is(a, 0, sizeof(GemmArgs))) return 0;
+    const GemmArgs p = arg<GemmArgs>(a, 0);
+    const std::vector<long> ta = targs(pretty);
+    // gemm_skinny_kernel<TI, KS, EPI, LO, SPLIT>, gemm_skinny_split_sum_kernel<TI, SPLIT, EPI>, gemm_skinny_ln_kernel<TI, KS, EPI, LO>
+    if (ta.size() < 3) return 0;
+    const bool sum = has("gemm_skinny_split_sum_kernel"), ln = has("gemm_skinny_ln_kernel");
+    const long TI = ta[0], epi = ta[2], split = sum ? ta[1] : (!ln && ta.size() >= 5 ? ta[4] : 1);
+    if (16 * TI < p.M) note = "skinny GEMM: row tiles below M";
+    if ((long)gx * 16 != p.N) note = "skinny GEMM: grid.x * 16 != N";
+    if (ln) {
+      if (p.M > 32) note = "skinny LayerNorm GEMM: more rows than its statistics slots";
+      rng(o, p.ln_x, 0, (long)p.M * p.K, 4, false, "LayerNorm rows");
+      rd(o, p.ln_g, (size_t)p.K * 4, "LayerNorm gamma");
+      rd(o, p.ln_b, (size_t)p.K * 4, "LayerNorm beta");
+    }
+    const size_t tiles = (size_t)split * gx * TI * 64 * 16;  // bytes of the split partial tiles
+    if (sum || split > 1) {
+      if (tiles > p.skp_bytes) note = "skinny split: partial tiles past the workspace";
+      if (sum) rd(o, p.skp, tiles, "split partials");
+      else wr(o, p.skp, tiles, "split partials");
+    }
+    if (sum) {  // the epilogue only
+      GemmArgs q = p;
+      q.A = q.Alo = nullptr;
+      q.B = nullptr;
+      gemm_spans(q, (int)epi, o, note);
+    } else if (split > 1) {  // operands only, no epilogue
+      GemmArgs q = p;
+      q.C = q.Clo = nullptr;
+      q.add = nullptr;
+      q.bias = nullptr;
+      q.colscale = nullptr;
+      gemm_spans(q, (int)epi, o, note);
+    } else {
+      gemm_spans(p, (int)epi, o, note);
+    }
+    return 1;
+  }
+  if (has("stream_attn_kernel")) {
+    if (!size_is(a, 2, sizeof(KvSlotsM))) return 0;
+    const _Float16 *u = arg<const _Float16 *>(a, 0);
+    const int ldu = arg<int>(a, 1), Lc = arg<int>(a, 4), nq = arg<int>(a, 5), D = arg<int>(a, 6), Pn = arg<int>(a, 8), nemit = arg<int>(a, 17),
+              keep = arg<int>(a, 18);
+    const KvSlotsM kv = arg<KvSlotsM>(a, 2);
+    const size_t kvo = arg<size_t>(a, 3);
+    const int H = (int)gy, n = (int)gz;
+    if (Lc + nq > 256) note = "stream attention: more keys than its 256 LDS rows";
+    if (H * 128 != D) note = "stream attention: heads x 128 != D";
+    if (n > kSG) note = "stream attention: more windows than cache slots";
+    if ((long)gx * 4 < nq) note = "stream attention: grid.x below the queries";
+    rng(o, arg<const void *>(a, 7), 0, (long)Pn * D, 2, false, "positional rows");
+    rd(o, arg<const void *>(a, 10), (size_t)D * 4, "pos bias u");
+    rd(o, arg<const void *>(a, 11), (size_t)D * 4, "pos bias v");
+    for (int w = 0; w < std::min(n, kSG); w++) {
+      rng(o, u, (long)w * nq * ldu, (long)w * nq * ldu + (long)(nq - 1) * ldu + 3 * D, 2, false, "q|k|v rows");
+      rng(o, kv.kc_in[w], kvo, kvo + (size_t)Lc * D, 2, false, "cached keys");
+      rng(o, kv.vc_in[w], kvo, kvo + (size_t)Lc * D, 2, false, "cached values");
+      if (keep > 0 && kv.kc_out[w]) {
+        if (Lc + nemit - keep < 0 || Lc + nemit > Lc + nq) note = "stream attention: kept rows outside the keys";
+        rng(o, kv.kc_out[w], kvo, kvo + (size_t)keep * D, 2, true, "next keys");
+        rng(o, kv.vc_out[w], kvo, kvo + (size_t)keep * D, 2, true, "next values");
+      }
+      rng(o, arg<const void *>(a, 15), (long)w * nq * D, (long)(w + 1) * nq * D, 2, true, "attention out");
+      rng(o, arg<const void *>(a, 16), (long)w * nq * D, (long)(w + 1) * nq * D, 2, true, "attention out lo");
+    }
+    return 1;
+  }
+  if (has("dwconv_ln_kernel")) {
+    if (!size_is(a, 1, sizeof(CcSlotsM)) || !size_is(a, 4, sizeof(WinTable))) return 0;
+    const size_t xe = has("dwconv_ln_kernelIfE") ? 4 : 2;
+    const CcSlotsM cc = arg<CcSlotsM>(a, 1);
+    const int use = arg<int>(a, 2), D = arg<int>(a, 10), nemit = arg<int>(a, 13);
+    const size_t cco = arg<size_t>(a, 3);
+    const WinTable st = arg<WinTable>(a, 4);
+    rd(o, arg<const void *>(a, 6), (size_t)9 * D * 4, "dw taps");
+    for (int i = 7; i <= 9; i++) rd(o, arg<const void *>(a, i), (size_t)D * 4, "dw bias / LayerNorm");
+    const int nw = (int)gy;
+    if (nw > st.n) note = "dwconv_ln: grid covers more windows than the table";
+    if ((int)threads * 4 < D) note = "dwconv_ln: block below D / 4 threads";
+    for (int w = 0; w < std::min(nw, st.n); w++) {
+      rng(o, arg<const void *>(a, 0), (long)st.off[w] * D, (long)(st.off[w] + st.len[w]) * D, xe, false, "dw in");
+      rng(o, arg<const void *>(a, 11), (long)st.off[w] * D, (long)(st.off[w] + st.len[w]) * D, 2, true, "dw out");
+      rng(o, arg<const void *>(a, 12), (long)st.off[w] * D, (long)(st.off[w] + st.len[w]) * D, 2, true, "dw out lo");
+      if ((int)gx < st.len[w]) note = "dwconv_ln: grid.x below a window's frames";
+      if (use && w < kSG) {
+        rng(o, cc.cc_in[w], cco, cco + (size_t)8 * D, 4, false, "conv cache");
+        rng(o, cc.cc_out[w], cco, cco + (size_t)8 * D, 4, true, "next conv cache");
+        if (nemit > st.len[w]) note = "dwconv_ln: emitted rows past the window";
+      }
+    }
+    return 1;
+  }
+  if (has("stream_out_kernel")) {
+    if (!size_is(a, 4, sizeof(OutRowsM))) return 0;
+    const int nq = arg<int>(a, 1), nemit = arg<int>(a, 2), D4 = arg<int>(a, 3);
+    const OutRowsM r = arg<OutRowsM>(a, 4);
+    for (int w = 0; w < std::min<int>((int)gy, kSG); w++) {
+      rng(o, arg<const void *>(a, 0), (long)w * nq * D4, (long)w * nq * D4 + (long)nemit * D4, 16, false, "pass rows");
+      rng(o, r.dst[w], 0, (long)nemit * D4, 16, true, "stream output");
+    }
+    if (nemit > nq) note = "stream_out: more emitted rows than the pass has";
+    return 1;
+  }
+  if (has("f32_to_f16_kernel")) {
+    const long n = arg<long>(a, 2);
+    rng(o, arg<const void *>(a, 0), 0, n, 4, false, "f32 in");
+    rng(o, arg<const void *>(a, 1), 0, n, 2, true, "f16 out");
     return 1;
   }
   if (has("gemm_f32_kernel")) {

@@ -52,7 +52,7 @@ def test_stand_in_reports_each_misuse(builds):
     got = run(builds, "controls")["controls"]
     assert got.pop("graph_replay_clean") == 0
     assert got.pop("extent_clean") == 0
-    assert all(v == 1 for v in got.values()), got
+    assert all(v >= 1 for v in got.values()), got  # a kernel's misuse can also show in its extents
 
 
 def test_hour_in_64_window_groups_with_profile_window(builds):
@@ -73,8 +73,8 @@ def test_windowed_transcription_32_window_groups(builds, scenario):
 
 
 def _unmodelled_on_path(r):
-    # kernels launched without an extent model, the load-time weight rounding aside
-    return [u for u in r["unmodelled"] if "f32_to_f16_kernel" not in u]
+    # kernels launched without an extent model
+    return list(r["unmodelled"])
 
 
 def test_hour_stage_by_stage_kernel_extents(builds):
@@ -91,6 +91,7 @@ def test_ragged_batches_on_two_lanes(builds):
     r = run(builds, "ragged", layers=2)
     assert r["batches"] == 8 and r["graph_replays"] >= 8
     assert r["violations"] == []
+    assert r["extent_checks"] > 0 and _unmodelled_on_path(r) == []
 
 
 @pytest.mark.parametrize("scenario", ["stream", "streamp"])
@@ -98,6 +99,7 @@ def test_stream_workload(builds, scenario):
     r = run(builds, scenario, layers=4)
     assert r["launches"] > 2000
     assert r["violations"] == []
+    assert r["extent_checks"] > 10000 and _unmodelled_on_path(r) == []
 
 
 def test_stream_push_failures_leave_consistent_state(builds):
