@@ -33,6 +33,11 @@ from .windowing import groupWindows, planWindows
 
 HOP = 160  # mel hop in samples
 MAX_WINDOWS = 32  # windows per encoder / decoder batch (largest validated encoder batch)
+# The longest input a windowed transcription has run on the GPU.  Every
+# transcription of one hour (64- and 32-window groups, stage by stage and
+# pipelined) made an illegal memory access on the GPU with no cause shown, so
+# longer inputs are refused unless the caller opts in (untested=True).
+MAX_TESTED_SECONDS = 470.0
 
 
 def createStitcher(hop: int, sampleRate: int, overlapSamples: int):
@@ -73,7 +78,7 @@ def _js_round(x: float) -> int:
 
 
 def transcribeWindowed(ctx, enc, dec, projW, projB, samples, sampleRate: int = 16000, windowSec: float = 15, overlapSec: float = 2,
-                       wb: int = MAX_WINDOWS, keepFrames: bool = False, pipelined: bool = False) -> dict:
+                       wb: int = MAX_WINDOWS, keepFrames: bool = False, pipelined: bool = False, untested: bool = False) -> dict:
     """pipeline.js:31 transcribeWindowed(ctx, enc, dec, mel, projW, projB,
     samples, opts) with the GPU stages: enc a FusedEncoder, dec a TdtDecoder,
     projW / projB device tensors [D, 640] / [1, 640] (the decoder manifest's
@@ -81,12 +86,16 @@ def transcribeWindowed(ctx, enc, dec, projW, projB, samples, sampleRate: int = 1
     keepFrames=True adds "frames" (each window's projected frames, host copies)
     for checks (stage by stage).  pipelined=True runs the group loop as one
     native call (fa_transcribe_groups) with group g+1's encoder overlapping
-    group g's decode."""
+    group g's decode.  Inputs longer than MAX_TESTED_SECONDS are refused unless
+    untested=True."""
     if not 1 <= wb <= MAX_WINDOWS:
         raise ValueError(f"wb={wb}: 1..{MAX_WINDOWS} windows per group")
     t_start = time.perf_counter()
     x = np.ascontiguousarray(samples, np.float32).reshape(-1)
     total = len(x)
+    if not untested and total > MAX_TESTED_SECONDS * sampleRate:
+        raise ValueError(f"{total / sampleRate:.1f} s of audio: transcriptions longer than {MAX_TESTED_SECONDS:.0f} s have faulted the GPU "
+                         "with no cause shown (untested=True runs them anyway)")
     winSamples = int(round(windowSec * sampleRate))
     overlapSamples = int(round(overlapSec * sampleRate))
     hop = winSamples - overlapSamples

@@ -132,11 +132,11 @@ def e2e(L, fa, wb: int, seconds: float, profile: bool, pipelined: bool = True):
     W, b = fa.synth.make_joint_projection(2)
     projW, projB = ctx.upload(W, W.shape[0], W.shape[1]), ctx.upload(b.reshape(1, -1), 1, b.size)
     audio = fa.synth.make_pcm(seconds, seed=1)
-    r = pl.transcribeWindowed(ctx, enc, dec, projW, projB, audio, wb=wb, pipelined=pipelined)
+    r = pl.transcribeWindowed(ctx, enc, dec, projW, projB, audio, wb=wb, pipelined=pipelined, untested=True)
     n_prof = 0
     if profile:
         ctx.startProfile(400000)
-        r = pl.transcribeWindowed(ctx, enc, dec, projW, projB, audio, wb=wb, pipelined=pipelined)
+        r = pl.transcribeWindowed(ctx, enc, dec, projW, projB, audio, wb=wb, pipelined=pipelined, untested=True)
         n_prof = len(ctx.endProfile())
     stats = r["stats"]
     enc.close()

@@ -51,3 +51,12 @@ def test_overlap_estimate_rounds_half_up(pl):
     # Tenc * overlap / sliceLen = 5 * 1 / 2 = 2.5 -> Math.round 3: frames 0..2 skipped
     stitch(1, 2, 5, [7, 8, 9, 10], [0, 1, 2, 3])
     assert ids == [1, 10]
+
+
+def test_longer_than_tested_transcription_is_refused(pl):
+    """Inputs past the longest transcription that has run on the GPU are refused
+    before any device work (no context is touched), unless the caller opts in."""
+    import numpy as np
+    audio = np.zeros(int((pl.MAX_TESTED_SECONDS + 1) * 16000), np.float32)
+    with pytest.raises(ValueError, match="faulted the GPU"):
+        pl.transcribeWindowed(None, None, None, None, None, audio)
