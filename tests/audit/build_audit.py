@@ -5,11 +5,13 @@ table of every kernel's argument layout read from the gfx950 code objects
 inside those objects (the AMDGPU metadata note: argument offsets, sizes and
 kinds, maximum workgroup size, static LDS and scratch).
 
-    python tests/audit/build_audit.py [--max-windows N]
+    python tests/audit/build_audit.py [--max-windows N] [--asan]
 
 --max-windows recompiles encoder.hip with FA_ENC_MAX_WINDOWS=N for the audit
-build only (the shipped library keeps its limit).  Outputs go to
-tests/audit/_build/ (libfa_hip_audit.so, kernargs.txt).
+build only (the shipped library keeps its limit).  --asan compiles every
+library source again with host-side AddressSanitizer and UBSan
+(libfa_hip_audit_asan.so; the Python process preloads asan_runtime()).
+Outputs go to tests/audit/_build/ (libfa_hip_audit.so, kernargs.txt).
 """
 from __future__ import annotations
 
@@ -78,8 +80,59 @@ def kernarg_table(objs) -> list[str]:
     return list(lines.values())
 
 
-def build(max_windows: int | None = None) -> str:
+# host-side sanitizers (the device code is compiled as for the library)
+SAN = ["-fsanitize=address", "-fsanitize=undefined", "-fno-omit-frame-pointer"]
+CLANGXX = "/opt/rocm/llvm/bin/clang++"
+
+
+def asan_runtime() -> str:
+    """The clang AddressSanitizer runtime to preload into the Python process
+    that loads the sanitized audit library."""
+    r = subprocess.run([CLANGXX, "-print-file-name=libclang_rt.asan-x86_64.so"], capture_output=True, text=True)
+    return r.stdout.strip()
+
+
+def _asan_objects() -> list[str]:
+    """Every library source compiled again with host-side ASan + UBSan
+    (`-Xarch_host` before each flag: the gfx950 code is unchanged)."""
+    from concurrent.futures import ThreadPoolExecutor
+    spec = __import__("importlib.util").util.spec_from_file_location("fa_build", os.path.join(CSRC, "build.py"))
+    b = __import__("importlib.util").util.module_from_spec(spec)
+    spec.loader.exec_module(b)
+    out = os.path.join(OUT, "asan")
+    os.makedirs(out, exist_ok=True)
+    host = [x for f in SAN for x in ("-Xarch_host", f)]
+
+    def one(src):
+        obj = os.path.join(out, src.replace(".hip", ".o"))
+        r = subprocess.run([b.HIPCC, *b.FLAGS, *b.EXTRA.get(src, []), *host, "-c", os.path.join(CSRC, src), "-o", obj], capture_output=True, text=True)
+        if r.returncode:
+            raise RuntimeError(r.stderr[-3000:])
+        return obj
+
+    with ThreadPoolExecutor(max_workers=8) as ex:
+        return list(ex.map(one, b.SOURCES))
+
+
+def build(max_windows: int | None = None, asan: bool = False) -> str:
     os.makedirs(OUT, exist_ok=True)
+    if asan:
+        objs = _asan_objects()
+        parts = []
+        for src in ("launch_audit.cpp", "extents.cpp"):
+            o = os.path.join(OUT, "asan", src.replace(".cpp", ".o"))
+            r = subprocess.run([CLANGXX, "-std=c++17", "-O1", "-fPIC", *SAN, "-I/opt/rocm/include", "-c", os.path.join(HERE, src), "-o", o],
+                               capture_output=True, text=True)
+            if r.returncode:
+                raise RuntimeError(r.stderr)
+            parts.append(o)
+        lib = os.path.join(OUT, "libfa_hip_audit_asan.so")
+        r = subprocess.run([CLANGXX, "-shared", "-fPIC", "-shared-libsan", *SAN, "-Wl,-Bsymbolic", "-o", lib, *objs, *parts], capture_output=True, text=True)
+        if r.returncode:
+            raise RuntimeError(r.stderr)
+        with open(os.path.join(OUT, "kernargs_asan.txt"), "w") as f:
+            f.write("\n".join(kernarg_table(objs)) + "\n")
+        return lib
     objs = [os.path.join(CSRC, "_build", f) for f in sorted(os.listdir(os.path.join(CSRC, "_build"))) if f.endswith(".o")]
     if not objs:
         raise RuntimeError("no objects in fluidaudio-web_amd/csrc/_build: run __graft_entry__.build() first")
@@ -118,4 +171,4 @@ def build(max_windows: int | None = None) -> str:
 
 if __name__ == "__main__":
     mw = int(sys.argv[sys.argv.index("--max-windows") + 1]) if "--max-windows" in sys.argv else None
-    print(build(mw))
+    print(build(mw, asan="--asan" in sys.argv))
