@@ -253,6 +253,132 @@ def stream_failures(L, fa):
     print(json.dumps(out), flush=True)
 
 
+def abi(L, fa):
+    """The library's host-side semantics and error paths through its Python
+    bindings, with no GPU (results read back are whatever the stand-in holds:
+    only control flow, bookkeeping and validation are checked): arenas and
+    pool reuse, pin, staged reads, batch nesting, shape errors, encoder /
+    decoder / log-mel / transcription argument checks, the allocation-free
+    entry point's size limits and its one-context-per-device rule."""
+    import ctypes as C
+    import importlib
+    import numpy as np
+    pl = importlib.import_module(fa.__name__ + ".pipeline")
+    ctx = fa.createContext("hip")
+    got = {}
+
+    def check(name, fn):
+        try:
+            fn()
+            got[name] = "ok"
+        except Exception as e:  # noqa: BLE001 (reported per check)
+            got[name] = f"{type(e).__name__}: {e}"
+
+    def raises(fn, match=""):
+        try:
+            fn()
+        except (fa.FaError, ValueError) as e:
+            if match and match not in str(e):
+                raise AssertionError(f"error without {match!r}: {e}")
+            return
+        raise AssertionError("no error")
+
+    def arenas():
+        x = ctx.upload(np.ones((64, 64), np.float32), 64, 64)
+        ctx.memStatsStart()
+        t = None
+        for _ in range(3):
+            a = ctx.pushArena()
+            t = ctx.transpose(ctx.scale(x, 2.0))
+            ctx.popArena(a)
+        st = ctx.memStats()
+        assert st["reused"] >= 4 and st["created"] <= 2, st
+        raises(lambda: ctx.download(t), "stale")
+
+    def pin():
+        x = ctx.upload(np.ones((4, 4), np.float32), 4, 4)
+        outer = ctx.pushArena()
+        inner = ctx.pushArena()
+        y = ctx.scale(x, 3.0)
+        z = ctx.scale(x, 5.0)
+        ctx.pin(y, True)
+        ctx.popArena(inner)
+        ctx.download(y)
+        raises(lambda: ctx.download(z))
+        ctx.popArena(outer)
+        raises(lambda: ctx.download(y))
+
+    def staged():
+        x = ctx.upload(np.arange(6, dtype=np.float32), 2, 3)
+        s = ctx.stageDownload(ctx.scale(x, 2.0))
+        s.read()
+        raises(s.read, "single-use")
+        ctx.beginBatch()
+        raises(ctx.beginBatch, "already open")
+        ctx.endBatch()
+        raises(ctx.endBatch)
+
+    def shapes():
+        a = ctx.upload(np.zeros((3, 5), np.float32), 3, 5)
+        b = ctx.upload(np.zeros((4, 2), np.float32), 4, 2)
+        raises(lambda: ctx.matmul(a, b), "matmul")
+        raises(lambda: ctx.relShiftB(a, 2))
+
+    def encoder():
+        cfg = dict(D=256, DFF=1024, H=2, HD=128, layers=1, dwK=9, Csub=64, Fsub=16, melBins=128)
+        enc = fa.FusedEncoder(ctx, fa.synth.make_weights(cfg, seed=1), "f16", max_T=32)
+        mel = ctx.upload(np.zeros((1000, 128), np.float32), 1000, 128)
+        raises(lambda: enc.forward(mel, [999]), "max_T")
+        raises(lambda: enc.forward(mel, [200, 200, 200, 200, 201]), "rows")
+        raises(lambda: enc.forward(mel, [10] * 65), "windows")
+        enc.close()
+
+    def decoder():
+        d = fa.TdtDecoder(ctx, fa.synth.make_decoder_weights(1))
+        raises(lambda: d.decodeBatch(ctx.upload(np.zeros((10, 100), np.float32), 10, 100), [10]))  # not 640 wide
+        raises(lambda: d.decodeBatch(ctx.upload(np.zeros((10, 640), np.float32), 10, 640), [11]))  # more frames than rows
+        raises(lambda: d.decodeBatch(ctx.upload(np.zeros((10, 640), np.float32), 10, 640), [-1]))  # negative length
+        d.close()
+
+    def mel():
+        pcm = ctx.upload(np.zeros((1, 1000), np.float32), 1, 1000)
+        raises(lambda: ctx.melWindows(pcm, [0], [2000]))
+        raises(lambda: ctx.melWindows(pcm, [0], [1000], nMels=129))
+        raises(lambda: ctx.melWindows(pcm, [-1], [10]))
+
+    def transcription():
+        raises(lambda: pl.transcribeWindowed(None, None, None, None, None, np.zeros(16000, np.float32), wb=0), "wb")
+        raises(lambda: pl.transcribeWindowed(None, None, None, None, None, np.zeros(int(471 * 16000), np.float32)), "faulted the GPU")
+
+    def mel_static():
+        L.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+        pcm, out = C.c_void_p(), C.c_void_p()
+        n = 16000 * 10
+        L.hipMalloc(C.byref(pcm), n * 4)
+        L.hipMalloc(C.byref(out), 128 * 200 * 4)
+
+        def call(c, starts, lens, n_mels, cols):
+            st = np.ascontiguousarray(starts, np.int32)
+            ln = np.ascontiguousarray(lens, np.int32)
+            return fa.lib().fa_mel_windows_static(c._p, pcm, n, st.ctypes.data_as(C.POINTER(C.c_int32)), ln.ctypes.data_as(C.POINTER(C.c_int32)),
+                                                  len(st), n_mels, 2.0 ** -24, 1, out, cols)
+        assert call(ctx, [0] * 65, [160] * 65, 128, 65) == fa._lib.FA_E_UNSUPPORTED  # > 64 windows
+        assert call(ctx, [0], [1600], 129, 10) == fa._lib.FA_E_INVALID  # > 128 bins
+        assert call(ctx, [0], [1600], 128, 11) == fa._lib.FA_E_INVALID  # wrong output size
+        assert call(ctx, [159000], [1600], 128, 10) == fa._lib.FA_E_INVALID  # outside the stream
+        assert call(ctx, [0], [32000], 128, 200) == 0
+        other = fa.createContext("hip")
+        assert call(other, [0], [32000], 128, 200) == fa._lib.FA_E_STATE  # the array serves one context per device
+        assert b"another context" in fa.lib().fa_last_error(other._p)
+        other.destroy()
+
+    for name, fn in [("arenas", arenas), ("pin", pin), ("staged", staged), ("shapes", shapes), ("encoder", encoder), ("decoder", decoder),
+                     ("mel", mel), ("transcription", transcription), ("mel_static", mel_static)]:
+        check(name, fn)
+    ctx.destroy()
+    report(L, {"checks": got})
+
+
 def main():
     import __graft_entry__ as ge
     fa = ge.load_package()
@@ -266,6 +392,8 @@ def main():
         e2e(L, fa, wb, float(sys.argv[2]) if len(sys.argv) > 2 else 3600.0, what.endswith("p"), "s" not in what[3:])
     elif what == "ragged":
         ragged(L, fa)
+    elif what == "abi":
+        abi(L, fa)
     elif what == "stream_failures":
         stream_failures(L, fa)
     elif what in ("stream", "streamp"):

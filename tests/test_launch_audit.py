@@ -12,9 +12,13 @@ profile window open (the run that faulted the GPU; the audit build lifts the
 encoder's 32-window limit for it), the same hour in 32-window groups
 pipelined and stage by stage, configs[3]'s ragged batches on two lanes, and
 the stream workload with and without a profile window (the workload whose
-rocprofv3 trace crashed in the host).  In-kernel index ranges are not
-modelled: a kernel that indexes past its buffer from valid arguments is not
-caught here."""
+rocprofv3 trace crashed in the host).  Each path kernel also has an extent
+model (tests/audit/extents.cpp): from its arguments and grid it derives the
+byte span every pointer argument is read or written over and checks that span
+against the block, so a launch whose index ranges run past a buffer is caught
+as well.  The "abi" scenario runs the bindings' host semantics and argument
+validation (arenas, pin, staged reads, batches, shape and size errors, the
+allocation-free log-mel entry point's limits) against the same stand-in."""
 import json
 import os
 import subprocess
@@ -112,3 +116,14 @@ def test_stream_push_failures_leave_consistent_state(builds):
     assert r["alloc_failure_frames"] == r["reference_frames"] > 0
     assert r["launch_failure_code"] == 3  # FA_E_DEVICE
     assert r["after_failure_code"] == 2  # FA_E_STATE
+
+
+def test_host_semantics_and_argument_checks(builds):
+    """Arena reuse and stale handles, pin, single-use staged reads, batch
+    nesting, shape errors, encoder / decoder / log-mel / transcription
+    argument checks and the allocation-free log-mel entry point's limits and
+    one-context-per-device rule, with no GPU; the calls that pass validation
+    launch inside their blocks."""
+    r = run(builds, "abi")
+    assert r["checks"] == {k: "ok" for k in ("arenas", "pin", "staged", "shapes", "encoder", "decoder", "mel", "transcription", "mel_static")}
+    assert r["violations"] == [] and r["launches"] > 0
