@@ -16,7 +16,16 @@
 //     hardware limits;
 //   * streams, events, graphs and graph executables are checked for use after
 //     destruction, events for elapsed-time queries before being recorded, and
-//     graph launches for executables destroyed or never instantiated.
+//     graph launches for executables destroyed or never instantiated;
+//   * ordering between streams: every stream, event and the host thread keep
+//     a vector clock (stream order, event record / wait, stream / event /
+//     device synchronisation, synchronous copies on the null stream, hipFree
+//     as a device synchronisation), and every byte range a kernel (from its
+//     extent model), copy or fill touches is checked against the earlier
+//     accesses to the same block: a write and another access to overlapping
+//     bytes from two streams with no happens-before path between them is a
+//     race.  All library streams are non-blocking, so the null stream is
+//     ordered with none of them.
 // Violations are collected and read back with audit_report().  The contents
 // of device memory are whatever the host wrote (kernels never run), so a
 // readback sees zeros or uploaded data.
@@ -24,6 +33,7 @@
 #include <hip/hip_runtime_api.h>
 #include <sys/mman.h>
 #include <cxxabi.h>
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -160,8 +170,12 @@ struct Op {  // a captured operation
   const void *p0 = nullptr, *p1 = nullptr;
   size_t bytes = 0;
 };
+using VClock = std::vector<uint64_t>;
 struct Handle {
   int kind;
+  int sid = 0;  // streams: index of the stream's clock (0 = the null stream)
+  bool blocking = false;  // streams created without hipStreamNonBlocking
+  VClock vc;    // events: the recording stream's clock at the record
   bool live = true;
   bool recorded = false;   // events
   bool capturing = false;  // streams
@@ -169,9 +183,16 @@ struct Handle {
 };
 std::vector<Handle *> &handles() { static auto *v = new std::vector<Handle *>(); return *v; }
 #define g_handles handles()
+std::vector<VClock> &stream_clocks() { static auto *v = new std::vector<VClock>(1); return *v; }  // [sid]
+std::vector<char> &stream_blocking() { static auto *v = new std::vector<char>(1, 0); return *v; }  // [sid]
 Handle *new_handle(int kind) {
   Handle *h = new Handle();
   h->kind = kind;
+  if (kind == K_STREAM) {
+    h->sid = (int)stream_clocks().size();
+    stream_clocks().emplace_back();
+    stream_blocking().push_back(0);
+  }
   g_handles.push_back(h);
   return h;
 }
@@ -235,6 +256,73 @@ void check_launch_args(const Launch &l, const char *when) {
   }
 }
 
+// ── ordering between streams: vector clocks and per-block access lists ──
+VClock g_host;  // what the host thread has waited for
+void vc_join(VClock &a, const VClock &b) {
+  if (a.size() < b.size()) a.resize(b.size(), 0);
+  for (size_t i = 0; i < b.size(); i++)
+    if (b[i] > a[i]) a[i] = b[i];
+}
+bool vc_covers(const VClock &v, int sid, uint64_t clk) { return (size_t)sid < v.size() && v[sid] >= clk; }
+int stream_sid(hipStream_t s) { return s ? ((Handle *)s)->sid : 0; }
+// One operation queued on a stream: it follows everything the host has waited
+// for and everything earlier on its stream; the null stream and the blocking
+// streams also wait for each other's earlier work.  Returns the stream's clock.
+VClock &begin_op(int sid) {
+  VClock &v = stream_clocks()[sid];
+  vc_join(v, g_host);
+  if (sid == 0) {
+    for (size_t i = 1; i < stream_clocks().size(); i++)
+      if (stream_blocking()[i]) vc_join(v, stream_clocks()[i]);
+  } else if (stream_blocking()[sid]) {
+    vc_join(v, stream_clocks()[0]);
+  }
+  if (v.size() <= (size_t)sid) v.resize(sid + 1, 0);
+  v[sid]++;
+  return v;
+}
+struct Acc {
+  uintptr_t lo, hi;
+  bool write;
+  int sid;
+  uint64_t clk;
+  std::string who;
+};
+std::map<uintptr_t, std::vector<Acc>> &accesses() { static auto *m = new std::map<uintptr_t, std::vector<Acc>>(); return *m; }  // block start -> list
+size_t g_race_checks = 0;
+std::map<std::string, size_t> &races() { static auto *m = new std::map<std::string, size_t>(); return *m; }
+void access(int sid, uintptr_t p, size_t n, bool write, const std::string &who) {
+  if (!n || !in_range(p)) return;
+  const auto *b = block_of(p);
+  if (!b || !b->second.live) return;  // reported by the range checks
+  const uintptr_t lo = p, hi = std::min<uintptr_t>(p + n, b->first + b->second.size);
+  const VClock &v = stream_clocks()[sid];
+  const uint64_t clk = v[sid];
+  std::vector<Acc> &list = accesses()[b->first];
+  g_race_checks++;
+  size_t keep = 0;
+  for (size_t i = 0; i < list.size(); i++) {
+    Acc &e = list[i];
+    const bool ordered = vc_covers(v, e.sid, e.clk);
+    if (e.lo < hi && lo < e.hi && (e.write || write) && !ordered) {
+      const std::string key = who + (write ? " writes" : " reads") + " / " + e.who + (e.write ? " writes" : " reads");
+      if (races()[key]++ == 0)
+        violation("race: " + who + (write ? " writes " : " reads ") + std::to_string(hi - lo) + " bytes of a block (" + b->second.what +
+                  ") on stream " + std::to_string(sid) + " with no ordering after " + e.who + (e.write ? " (write)" : " (read)") + " on stream " +
+                  std::to_string(e.sid));
+    }
+    // an access the host has waited for precedes every later operation; one
+    // covered by this access and ordered before it is shadowed by it
+    const bool drop = vc_covers(g_host, e.sid, e.clk) || (lo <= e.lo && e.hi <= hi && ordered && (write || !e.write));
+    if (!drop) list[keep++] = std::move(e);
+  }
+  list.resize(keep);
+  list.push_back(Acc{lo, hi, write, sid, clk, who});
+}
+void host_join_all() {
+  for (const VClock &v : stream_clocks()) vc_join(g_host, v);
+}
+
 // ── per-kernel extents (extents.cpp): every range a kernel reads or writes
 // must lie inside one live block ──
 }  // namespace
@@ -251,7 +339,7 @@ int extents(const std::string &mangled, const std::string &pretty, const std::ve
 namespace {
 std::map<std::string, size_t> &unmodelled() { static auto *m = new std::map<std::string, size_t>(); return *m; }
 size_t g_extent_checks = 0;
-void check_extents(const Launch &l, const char *when) {
+void check_extents(const Launch &l, const char *when, int sid) {
   const KernelInfo &k = *l.k;
   std::vector<audit_ext::Span> sp;
   std::string note;
@@ -269,6 +357,7 @@ void check_extents(const Launch &l, const char *when) {
       continue;
     }
     check_span((const void *)s.p, s.bytes, w);
+    access(sid, s.p, s.bytes, s.write, k.pretty + " (" + s.what + ")");
   }
 }
 
@@ -328,7 +417,11 @@ hipError_t do_launch(const void *f, dim3 g, dim3 b, void **args, size_t shm, hip
   check_geometry(k, g, b, shm);
   check_launch_args(l, "launch");
   Handle *cs = capturing_stream(s);
-  if (!cs) check_extents(l, "launch");  // a captured launch runs (and is checked) at each replay
+  if (!cs) {  // a captured launch runs (and is checked) at each replay
+    const int sid = stream_sid(s);
+    begin_op(sid);
+    check_extents(l, "launch", sid);
+  }
   if (cs) cs->ops.push_back(Op{0, l});
   return hipSuccess;
 }
@@ -381,8 +474,14 @@ hipError_t hipExtLaunchKernel(const void *f, dim3 g, dim3 b, void **args, size_t
       return hipErrorInvalidHandle;
     if (e0) ((Handle *)e0)->recorded = true;
     if (e1) ((Handle *)e1)->recorded = true;
+    if (e0 && check_handle(s, K_STREAM, "hipExtLaunchKernel", true) && !capturing_stream(s)) ((Handle *)e0)->vc = begin_op(stream_sid(s));
   }
-  return do_launch(f, g, b, args, shm, s);
+  const hipError_t r = do_launch(f, g, b, args, shm, s);
+  if (e1) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (check_handle(s, K_STREAM, "hipExtLaunchKernel", true) && !capturing_stream(s)) ((Handle *)e1)->vc = stream_clocks()[stream_sid(s)];
+  }
+  return r;
 }
 hipError_t hipFuncSetAttribute(const void *, hipFuncAttribute, int) { return hipSuccess; }
 hipError_t hipGetLastError(void) {
@@ -413,7 +512,11 @@ hipError_t hipGetDevicePropertiesR0600(hipDeviceProp_tR0600 *p, int d) {
   p->minor = 5;
   return hipSuccess;
 }
-hipError_t hipDeviceSynchronize(void) { return hipSuccess; }
+hipError_t hipDeviceSynchronize(void) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  host_join_all();
+  return hipSuccess;
+}
 hipError_t hipGetSymbolAddress(void **dev, const void *sym) {
   std::lock_guard<std::mutex> lk(g_mu);
   auto it = g_vars.find(sym);
@@ -448,6 +551,8 @@ hipError_t hipFree(void *p) {
     return hipErrorInvalidValue;
   }
   it->second.live = false;
+  host_join_all();  // hipFree waits for the device
+  accesses().erase(it->first);
   madvise(p, it->second.size, MADV_DONTNEED);  // hand the pages back; the addresses stay reserved
   return hipSuccess;
 }
@@ -459,11 +564,18 @@ hipError_t hipHostFree(void *p) {
   std::free(p);
   return hipSuccess;
 }
-static hipError_t copy(void *dst, const void *src, size_t n, hipStream_t s, const char *api) {
+static hipError_t copy(void *dst, const void *src, size_t n, hipStream_t s, const char *api, bool sync) {
   std::lock_guard<std::mutex> lk(g_mu);
   if (!check_handle(s, K_STREAM, api, true)) return hipErrorInvalidHandle;
   check_span(dst, n, std::string(api) + " destination");
   check_span(src, n, std::string(api) + " source");
+  if (!capturing_stream(s)) {
+    const int sid = stream_sid(s);
+    begin_op(sid);
+    access(sid, (uintptr_t)src, n, false, std::string(api) + " source");
+    access(sid, (uintptr_t)dst, n, true, std::string(api) + " destination");
+    if (sync) vc_join(g_host, stream_clocks()[sid]);  // returns when the copy is done
+  }
   if (Handle *cs = capturing_stream(s)) {
     Op o;
     o.type = 1;
@@ -475,12 +587,17 @@ static hipError_t copy(void *dst, const void *src, size_t n, hipStream_t s, cons
   if (n) std::memmove(dst, src, n);
   return hipSuccess;
 }
-hipError_t hipMemcpy(void *dst, const void *src, size_t n, hipMemcpyKind) { return copy(dst, src, n, nullptr, "hipMemcpy"); }
-hipError_t hipMemcpyAsync(void *dst, const void *src, size_t n, hipMemcpyKind, hipStream_t s) { return copy(dst, src, n, s, "hipMemcpyAsync"); }
+hipError_t hipMemcpy(void *dst, const void *src, size_t n, hipMemcpyKind) { return copy(dst, src, n, nullptr, "hipMemcpy", true); }
+hipError_t hipMemcpyAsync(void *dst, const void *src, size_t n, hipMemcpyKind, hipStream_t s) { return copy(dst, src, n, s, "hipMemcpyAsync", false); }
 hipError_t hipMemsetAsync(void *dst, int v, size_t n, hipStream_t s) {
   std::lock_guard<std::mutex> lk(g_mu);
   if (!check_handle(s, K_STREAM, "hipMemsetAsync", true)) return hipErrorInvalidHandle;
   check_span(dst, n, "hipMemsetAsync");
+  if (!capturing_stream(s)) {
+    const int sid = stream_sid(s);
+    begin_op(sid);
+    access(sid, (uintptr_t)dst, n, true, "hipMemsetAsync");
+  }
   if (Handle *cs = capturing_stream(s)) {
     violation("hipMemsetAsync recorded into a captured graph");
     Op o;
@@ -494,9 +611,12 @@ hipError_t hipMemsetAsync(void *dst, int v, size_t n, hipStream_t s) {
 }
 
 // ── streams and events ──
-hipError_t hipStreamCreateWithFlags(hipStream_t *s, unsigned int) {
+hipError_t hipStreamCreateWithFlags(hipStream_t *s, unsigned int flags) {
   std::lock_guard<std::mutex> lk(g_mu);
-  *s = (hipStream_t)new_handle(K_STREAM);
+  Handle *h = new_handle(K_STREAM);
+  h->blocking = !(flags & hipStreamNonBlocking);
+  stream_blocking()[h->sid] = h->blocking;
+  *s = (hipStream_t)h;
   return hipSuccess;
 }
 hipError_t hipStreamDestroy(hipStream_t s) {
@@ -507,11 +627,15 @@ hipError_t hipStreamDestroy(hipStream_t s) {
 }
 hipError_t hipStreamSynchronize(hipStream_t s) {
   std::lock_guard<std::mutex> lk(g_mu);
-  return check_handle(s, K_STREAM, "hipStreamSynchronize", true) ? hipSuccess : hipErrorInvalidHandle;
+  if (!check_handle(s, K_STREAM, "hipStreamSynchronize", true)) return hipErrorInvalidHandle;
+  vc_join(g_host, stream_clocks()[stream_sid(s)]);
+  return hipSuccess;
 }
 hipError_t hipStreamWaitEvent(hipStream_t s, hipEvent_t e, unsigned int) {
   std::lock_guard<std::mutex> lk(g_mu);
   if (!check_handle(s, K_STREAM, "hipStreamWaitEvent", true) || !check_handle(e, K_EVENT, "hipStreamWaitEvent", false)) return hipErrorInvalidHandle;
+  if (capturing_stream(s)) violation("hipStreamWaitEvent on a capturing stream (not modelled)");
+  else vc_join(stream_clocks()[stream_sid(s)], ((Handle *)e)->vc);
   return hipSuccess;
 }
 hipError_t hipEventCreate(hipEvent_t *e) {
@@ -530,11 +654,19 @@ hipError_t hipEventRecord(hipEvent_t e, hipStream_t s) {
   std::lock_guard<std::mutex> lk(g_mu);
   if (!check_handle(e, K_EVENT, "hipEventRecord", false) || !check_handle(s, K_STREAM, "hipEventRecord", true)) return hipErrorInvalidHandle;
   ((Handle *)e)->recorded = true;
+  if (capturing_stream(s)) violation("hipEventRecord on a capturing stream (not modelled)");
+  else {
+    VClock &v = stream_clocks()[stream_sid(s)];
+    vc_join(v, g_host);
+    ((Handle *)e)->vc = v;
+  }
   return hipSuccess;
 }
 hipError_t hipEventSynchronize(hipEvent_t e) {
   std::lock_guard<std::mutex> lk(g_mu);
-  return check_handle(e, K_EVENT, "hipEventSynchronize", false) ? hipSuccess : hipErrorInvalidHandle;
+  if (!check_handle(e, K_EVENT, "hipEventSynchronize", false)) return hipErrorInvalidHandle;
+  vc_join(g_host, ((Handle *)e)->vc);
+  return hipSuccess;
 }
 hipError_t hipEventElapsedTime(float *ms, hipEvent_t a, hipEvent_t b) {
   std::lock_guard<std::mutex> lk(g_mu);
@@ -590,14 +722,19 @@ hipError_t hipGraphLaunch(hipGraphExec_t x, hipStream_t s) {
   std::lock_guard<std::mutex> lk(g_mu);
   if (!check_handle(x, K_EXEC, "hipGraphLaunch", false) || !check_handle(s, K_STREAM, "hipGraphLaunch", true)) return hipErrorInvalidHandle;
   g_replays++;
-  for (const Op &o : ((Handle *)x)->ops) {
+  if (capturing_stream(s)) violation("hipGraphLaunch into a capturing stream");
+  const int sid = stream_sid(s);
+  for (const Op &o : ((Handle *)x)->ops) {  // nodes captured from one stream run in order
+    begin_op(sid);
     if (o.type == 0) {
       g_replayed_launches++;
       check_launch_args(o.l, "graph replay");
-      check_extents(o.l, "graph replay");
+      check_extents(o.l, "graph replay", sid);
     } else {
       check_span(o.p0, o.bytes, "graph replay copy/set destination");
       if (o.type == 1) check_span(o.p1, o.bytes, "graph replay copy source");
+      if (o.type == 1) access(sid, (uintptr_t)o.p1, o.bytes, false, "graph replay copy source");
+      access(sid, (uintptr_t)o.p0, o.bytes, true, "graph replay copy/set destination");
     }
   }
   return hipSuccess;
@@ -628,6 +765,16 @@ int audit_extent_report(char *buf, int cap, unsigned long long *checks) {
   if (checks) *checks = g_extent_checks;
   return (int)unmodelled().size();
 }
+// Accesses checked for ordering, and the races found ("access / earlier
+// access count" per line).
+int audit_race_report(char *buf, int cap, unsigned long long *checks) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  std::string s;
+  for (const auto &r : races()) s += r.first + " " + std::to_string(r.second) + "\n";
+  if (buf && cap > 0) std::snprintf(buf, cap, "%s", s.c_str());
+  if (checks) *checks = g_race_checks;
+  return (int)races().size();
+}
 void audit_fail_alloc(long after) {
   std::lock_guard<std::mutex> lk(g_mu);
   g_fail_alloc_after = after;
@@ -639,6 +786,7 @@ void audit_fail_launch(long after) {
 void audit_clear(void) {
   std::lock_guard<std::mutex> lk(g_mu);
   g_viol.clear();
+  races().clear();
 }
 
 }  // extern "C"

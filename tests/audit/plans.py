@@ -38,6 +38,11 @@ def report(L, extra=None):
     L.audit_extent_report(ub, len(ub), C.byref(chk))
     out["extent_checks"] = chk.value
     out["unmodelled"] = [u for u in ub.value.decode().splitlines() if u]
+    rb = C.create_string_buffer(1 << 16)
+    L.audit_race_report.restype = C.c_int
+    L.audit_race_report(rb, len(rb), C.byref(chk))
+    out["order_checks"] = chk.value
+    out["races"] = [r for r in rb.value.decode().splitlines() if r]
     out.update(extra or {})
     print(json.dumps(out), flush=True)
 
@@ -113,6 +118,43 @@ def controls(L):
     a_over = (V * 3)(C.cast(C.pointer(d), V), C.cast(C.pointer(e), V), C.cast(C.pointer(n4_over), V))
     step("extent_clean", lambda: L.hipLaunchKernel(cp, Dim3(1, 1, 1), Dim3(256, 1, 1), a_ok, 0, None))
     step("extent_write_past_block_end", lambda: L.hipLaunchKernel(cp, Dim3(1, 1, 1), Dim3(256, 1, 1), a_over, 0, None))
+    # ordering: two non-blocking streams write the same block, first with an
+    # event between them (ordered), then without; a synchronous copy on the
+    # null stream into a block a queued kernel writes; the same after a
+    # stream synchronisation
+    L.hipStreamWaitEvent.argtypes = [V, V, C.c_uint]
+    L.hipStreamSynchronize.argtypes = [V]
+    s1, s2, ev2 = V(), V(), V()
+    L.hipStreamCreateWithFlags(C.byref(s1), 1)
+    L.hipStreamCreateWithFlags(C.byref(s2), 1)
+    L.hipEventCreate(C.byref(ev2))
+
+    def ordered():
+        L.hipLaunchKernel(cp, Dim3(1, 1, 1), Dim3(256, 1, 1), a_ok, 0, s1)
+        L.hipEventRecord(ev2, s1)
+        L.hipStreamWaitEvent(s2, ev2, 0)
+        L.hipLaunchKernel(cp, Dim3(1, 1, 1), Dim3(256, 1, 1), a_ok, 0, s2)
+
+    def unordered():
+        L.hipLaunchKernel(cp, Dim3(1, 1, 1), Dim3(256, 1, 1), a_ok, 0, s1)
+        L.hipLaunchKernel(cp, Dim3(1, 1, 1), Dim3(256, 1, 1), a_ok, 0, s2)
+
+    def null_copy(sync):
+        def f():
+            L.hipLaunchKernel(cp, Dim3(1, 1, 1), Dim3(256, 1, 1), a_ok, 0, s1)
+            if sync:
+                L.hipStreamSynchronize(s1)
+            L.hipMemcpy(e, host, 64, 1)
+        return f
+
+    L.hipStreamSynchronize(None)
+    step("streams_ordered_by_event", ordered)
+    L.hipStreamSynchronize(s2)
+    step("streams_unordered_write_write", unordered)
+    L.hipStreamSynchronize(s2)
+    L.hipStreamSynchronize(s1)
+    step("null_stream_copy_after_sync", null_copy(True))
+    step("null_stream_copy_over_queued_kernel", null_copy(False))
     L.audit_clear()
     print(json.dumps({"controls": got}), flush=True)
 

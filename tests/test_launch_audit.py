@@ -16,7 +16,10 @@ rocprofv3 trace crashed in the host).  Each path kernel also has an extent
 model (tests/audit/extents.cpp): from its arguments and grid it derives the
 byte span every pointer argument is read or written over and checks that span
 against the block, so a launch whose index ranges run past a buffer is caught
-as well.  The "abi" scenario runs the bindings' host semantics and argument
+as well.  Those ranges also feed a happens-before check across streams
+(vector clocks over stream order, events, synchronisations and hipFree): a
+write and another access to overlapping bytes from two streams with no
+ordering between them is reported as a race.  The "abi" scenario runs the bindings' host semantics and argument
 validation (arenas, pin, staged reads, batches, shape and size errors, the
 allocation-free log-mel entry point's limits) against the same stand-in."""
 import json
@@ -56,6 +59,8 @@ def test_stand_in_reports_each_misuse(builds):
     got = run(builds, "controls")["controls"]
     assert got.pop("graph_replay_clean") == 0
     assert got.pop("extent_clean") == 0
+    assert got.pop("streams_ordered_by_event") == 0
+    assert got.pop("null_stream_copy_after_sync") == 0
     assert all(v >= 1 for v in got.values()), got  # a kernel's misuse can also show in its extents
 
 
@@ -89,6 +94,19 @@ def test_hour_stage_by_stage_kernel_extents(builds):
     assert r["windows"] == 277 and r["groups"] == 10
     assert r["violations"] == []
     assert r["extent_checks"] > 50000 and _unmodelled_on_path(r) == []
+    assert r["races"] == [] and r["order_checks"] > 50000
+
+
+def test_hour_pipelined_stream_ordering(builds):
+    """The plan of the pipelined hour that faulted: 3600 s, 24 layers,
+    32-window groups with group g + 1's log-mel, encoder and projection on an
+    encoder lane while group g decodes on the context stream.  Every range
+    each kernel, copy and fill touches is ordered against the other streams'
+    earlier accesses to the same bytes: no race."""
+    r = run(builds, "e2e32", 3600)
+    assert r["windows"] == 277 and r["launches"] > 2000
+    assert r["violations"] == [] and _unmodelled_on_path(r) == []
+    assert r["races"] == [] and r["order_checks"] > 50000
 
 
 def test_ragged_batches_on_two_lanes(builds):
@@ -96,6 +114,7 @@ def test_ragged_batches_on_two_lanes(builds):
     assert r["batches"] == 8 and r["graph_replays"] >= 8
     assert r["violations"] == []
     assert r["extent_checks"] > 0 and _unmodelled_on_path(r) == []
+    assert r["races"] == [] and r["order_checks"] > 10000
 
 
 @pytest.mark.parametrize("scenario", ["stream", "streamp"])
@@ -104,6 +123,7 @@ def test_stream_workload(builds, scenario):
     assert r["launches"] > 2000
     assert r["violations"] == []
     assert r["extent_checks"] > 10000 and _unmodelled_on_path(r) == []
+    assert r["races"] == [] and r["order_checks"] > 10000
 
 
 def test_stream_push_failures_leave_consistent_state(builds):
