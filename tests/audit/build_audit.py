@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import os
 import struct
+import shutil
 import subprocess
 import sys
 
@@ -167,6 +168,29 @@ def build(max_windows: int | None = None, asan: bool = False) -> str:
     with open(os.path.join(OUT, f"kernargs{tag}.txt"), "w") as f:
         f.write("\n".join(tab) + "\n")
     return lib
+
+
+NODE_INC = "/usr/include/node"
+NODE_SRC = os.path.join(os.path.dirname(CSRC), "node")
+
+
+def build_node(lib: str) -> str | None:
+    """The N-API addon (node/fa_napi.c) linked against the audit library
+    `lib` instead of libfa_hip.so, beside copies of the package's JS host
+    files (they load fa_hip.node from their own folder), in
+    tests/audit/_build/node.  None when Node's headers are absent."""
+    if not os.path.exists(os.path.join(NODE_INC, "node_api.h")):
+        return None
+    out = os.path.join(OUT, "node")
+    os.makedirs(out, exist_ok=True)
+    addon = os.path.join(out, "fa_hip.node")
+    r = subprocess.run(["gcc", "-O1", "-g", "-Wall", "-shared", "-fPIC", f"-I{NODE_INC}", os.path.join(NODE_SRC, "fa_napi.c"), "-o", addon,
+                        f"-L{os.path.dirname(lib)}", f"-l:{os.path.basename(lib)}", f"-Wl,-rpath,{os.path.dirname(lib)}"], capture_output=True, text=True)
+    if r.returncode:
+        raise RuntimeError(r.stderr)
+    for js in ("hip-context.js", "conformance.js", "selftest.js"):
+        shutil.copyfile(os.path.join(NODE_SRC, js), os.path.join(out, js))
+    return out
 
 
 if __name__ == "__main__":

@@ -790,3 +790,23 @@ void audit_clear(void) {
 }
 
 }  // extern "C"
+
+namespace {
+// Hosts that cannot call audit_report (the N-API addon under Node): with
+// FA_AUDIT_REPORT set, the counts, the violations, the kernels without an
+// extent model and the races are written to that file at process exit, one
+// "key value" line each for the counts.
+struct ExitReport {
+  ~ExitReport() {
+    const char *path = std::getenv("FA_AUDIT_REPORT");
+    if (!path) return;
+    std::lock_guard<std::mutex> lk(g_mu);
+    std::ofstream f(path);
+    f << "launches " << g_launches << "\nreplays " << g_replays << "\nallocations " << g_allocs << "\nextent_checks " << g_extent_checks
+      << "\norder_checks " << g_race_checks << "\n";
+    for (const std::string &v : g_viol) f << "violation " << v << "\n";
+    for (const auto &u : unmodelled()) f << "unmodelled " << u.first << "\n";
+    for (const auto &r : races()) f << "race " << r.first << "\n";
+  }
+} g_exit_report;
+}  // namespace

@@ -21,7 +21,9 @@ as well.  Those ranges also feed a happens-before check across streams
 write and another access to overlapping bytes from two streams with no
 ordering between them is reported as a race.  The "abi" scenario runs the bindings' host semantics and argument
 validation (arenas, pin, staged reads, batches, shape and size errors, the
-allocation-free log-mel entry point's limits) against the same stand-in."""
+allocation-free log-mel entry point's limits) against the same stand-in,
+and the N-API addon is built against it too, so the Node host's conformance
+cases and self-test run through the addon on the CPU."""
 import json
 import os
 import subprocess
@@ -147,3 +149,44 @@ def test_host_semantics_and_argument_checks(builds):
     r = run(builds, "abi")
     assert r["checks"] == {k: "ok" for k in ("arenas", "pin", "staged", "shapes", "encoder", "decoder", "mel", "transcription", "mel_static")}
     assert r["violations"] == [] and r["launches"] > 0
+
+
+def _node_report(builds, script, tmp_path):
+    import shutil
+    import build_audit
+    if shutil.which("node") is None:
+        pytest.skip("node not installed")
+    ndir = build_audit.build_node(builds[None])
+    if ndir is None:
+        pytest.skip("Node headers not installed")
+    rep = tmp_path / f"{script}.txt"
+    env = dict(os.environ, FA_AUDIT_KERNARGS=os.path.join(AUD, "_build", "kernargs.txt"), FA_AUDIT_REPORT=str(rep))
+    r = subprocess.run(["node", os.path.join(ndir, f"{script}.js"), str(tmp_path / "dump.json")], env=env, capture_output=True, text=True, timeout=300)
+    lines = rep.read_text().splitlines()
+    counts = {k: int(v) for k, v in (ln.split(" ", 1) for ln in lines if ln.split(" ", 1)[0] in ("launches", "replays", "extent_checks", "order_checks"))}
+    bad = [ln for ln in lines if ln.startswith(("violation", "race"))]
+    return r, counts, bad
+
+
+def test_node_addon_conformance_cases(builds, tmp_path):
+    """The N-API addon (node/fa_napi.c) and HipContext (hip-context.js) run
+    every required ComputeContext method's conformance case against the
+    stand-in runtime: the addon's argument marshalling, tensor handles and
+    error paths make no launch, copy or handle error and no unordered access
+    (the numbers are not checked: kernels do not run)."""
+    r, counts, bad = _node_report(builds, "conformance", tmp_path)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    assert "58 cases cover every required method" in r.stdout
+    assert counts["launches"] > 50 and bad == []
+
+
+def test_node_addon_selftest_runs_to_the_end(builds, tmp_path):
+    """The Node self-test (fused encoder, log-mel windows, TDT decode through
+    the addon) runs to its last case against the stand-in (exit 1 = only
+    numeric checks failed, as kernels do not run; 2 would be an exception),
+    with graph replays and no violation."""
+    r, counts, bad = _node_report(builds, "selftest", tmp_path)
+    assert r.returncode in (0, 1), r.stdout[-2000:] + r.stderr[-2000:]
+    assert "tdtDecode known answer" in r.stdout
+    assert counts["launches"] > 200 and counts["replays"] > 0 and counts["extent_checks"] > 1000 and bad == []
+
