@@ -166,6 +166,340 @@ static void gemm_spans(const fa::GemmArgs &p, int epi, std::vector<Span> &o, std
 
 // Returns 1 and fills `o` when the kernel has a model; 0 otherwise.
 // `note` receives a geometry complaint (a grid that does not cover the work).
+// ── ComputeContext op kernels (ops.hip, ops_aux.hip, quant.hip fallbacks,
+// gemm.hip's any-shape GEMM): grid-stride loops over their outputs, inputs
+// indexed as each kernel does ──
+struct GemvArgsM {
+  const float *A;
+  int M, K, N;
+  const void *W, *scales;
+  const uint8_t *zp;
+  int zpb;
+  float *Y;
+  const float *bias;
+  int act;
+};
+struct GemvItemM {
+  const float *A;
+  const void *W, *scales;
+  float *Y;
+};
+constexpr int kGemvItems = 48, kGemvWavesM = 8;
+
+// quantised weights of one product ([N] rows of K, fmt 1 int8 + f32 column
+// scales, 2 int4 group-32 + f16 scales, 3 int4 + f32 scales + zero points)
+static void gemv_spans(const GemvArgsM &p, int fmt, std::vector<Span> &o) {
+  const long nblk = (p.K + 31) / 32;
+  rng(o, p.A, 0, (long)p.M * p.K, 4, false, "gemv A");
+  if (fmt == 1) {
+    rng(o, p.W, 0, (long)p.N * p.K, 1, false, "gemv W int8");
+    rng(o, p.scales, 0, p.N, 4, false, "gemv scales");
+  } else {
+    rng(o, p.W, 0, (long)p.N * nblk * 16, 1, false, "gemv W int4");
+    rng(o, p.scales, 0, (long)p.N * nblk, fmt == 2 ? 2 : 4, false, "gemv scales");
+    if (fmt == 3) rng(o, p.zp, 0, (long)(p.N - 1) * p.zpb + (nblk - 1) / 2 + 1, 1, false, "gemv zero points");
+  }
+  rng(o, p.Y, 0, (long)p.M * p.N, 4, true, "gemv Y");
+  rng(o, p.bias, 0, p.N, 4, false, "gemv bias");
+}
+
+static int op_extents(const std::string &mangled, const std::vector<std::vector<char>> &a, unsigned gx, unsigned gy, unsigned gz, unsigned threads,
+                      std::vector<Span> &o, std::string &note) {
+  (void)gz;
+  // the identifier as mangled (its length, then the name), so "transpose_kernel"
+  // does not match "v_transpose_kernel"
+  auto has = [&](const char *s) { return mangled.find(std::to_string(std::strlen(s)) + s) != std::string::npos; };
+  auto P = [&](size_t i) { return arg<const void *>(a, i); };
+  auto I = [&](size_t i) { return (long)arg<int>(a, i); };
+  if (has("layernorm_kernel")) {
+    const long rows = I(4), cols = I(5), ldx = I(6), ldy = I(7);
+    const size_t ye = mangled.find("layernorm_kernelIfE") != std::string::npos ? 4 : 2;
+    if (rows > 0) {
+      rng(o, P(0), 0, (rows - 1) * ldx + cols, 4, false, "layernorm x");
+      rng(o, P(3), 0, (rows - 1) * ldy + cols, ye, true, "layernorm y");
+    }
+    rng(o, P(1), 0, cols, 4, false, "gamma");
+    rng(o, P(2), 0, cols, 4, false, "beta");
+    if ((long)gx * 4 < rows) note = "layernorm: grid below its rows";
+    return 1;
+  }
+  if (has("softmax_kernel")) {
+    const long rows = I(2), cols = I(3);
+    rng(o, P(0), 0, rows * cols, 4, false, "softmax x");
+    rng(o, P(1), 0, rows * cols, 4, true, "softmax y");
+    if ((long)gx * 4 < rows) note = "softmax: grid below its rows";
+    return 1;
+  }
+  if (has("ewise_kernel")) {
+    const long n = arg<long>(a, 3), cols = I(4);
+    const int bcast = arg<int>(a, 5);
+    rng(o, P(0), 0, n, 4, false, "ewise a");
+    rng(o, P(1), 0, bcast ? std::min(n, cols) : n, 4, false, "ewise b");
+    rng(o, P(2), 0, n, 4, true, "ewise c");
+    return 1;
+  }
+  if (has("unary_kernel") || has("leaky_relu_kernel")) {
+    const long n = arg<long>(a, 2);
+    rng(o, P(0), 0, n, 4, false, "unary x");
+    rng(o, P(1), 0, n, 4, true, "unary y");
+    return 1;
+  }
+  if (has("glu_kernel")) {
+    const long C = I(2), T = I(3);
+    rng(o, P(0), 0, 2 * C * T, 4, false, "glu x");
+    rng(o, P(1), 0, C * T, 4, true, "glu y");
+    return 1;
+  }
+  if (has("transpose_kernel")) {
+    const long R = I(2), C = I(3);
+    rng(o, P(0), 0, R * C, 4, false, "transpose x");
+    rng(o, P(1), 0, R * C, 4, true, "transpose y");
+    if ((long)gx * 32 < C || (long)gy * 32 < R) note = "transpose: grid below the matrix";
+    return 1;
+  }
+  if (has("slice_cols_kernel") || has("set_cols_kernel")) {
+    const bool set = has("set_cols_kernel");
+    const long rows = I(2), C = I(3), c0 = I(4), W = I(5);
+    if (rows > 0 && W > 0) {
+      rng(o, P(set ? 0 : 1), 0, rows * W, 4, !set, set ? "setCols src" : "sliceCols y");
+      rng(o, P(set ? 1 : 0), c0, (rows - 1) * C + c0 + W, 4, set, set ? "setCols dst" : "sliceCols x");
+    }
+    if (c0 < 0 || c0 + W > C) note = "slice/set cols: columns outside the row";
+    return 1;
+  }
+  if (has("sub_reshape_kernel")) {
+    const long n = I(2) * I(3) * I(4);
+    rng(o, P(0), 0, n, 4, false, "subReshape x");
+    rng(o, P(1), 0, n, 4, true, "subReshape y");
+    return 1;
+  }
+  if (has("row_bias_act_kernel")) {
+    const long rows = I(3), cols = I(4);
+    rng(o, P(0), 0, rows * cols, 4, false, "rowBiasAct x");
+    rng(o, P(1), 0, rows, 4, false, "rowBiasAct bias");
+    rng(o, P(2), 0, rows * cols, 4, true, "rowBiasAct y");
+    return 1;
+  }
+  if (has("chan_bias_act_kernel")) {
+    const long cols = I(2), n = arg<long>(a, 3);
+    rng(o, P(0), 0, n, 4, true, "chanBiasAct y");
+    if (cols > 0) rng(o, P(1), 0, (n + cols - 1) / cols, 4, false, "chanBiasAct bias");
+    return 1;
+  }
+  if (has("round_f16_kernel")) {
+    const long n = arg<long>(a, 2);
+    rng(o, P(0), 0, n, 4, false, "round x");
+    rng(o, P(1), 0, n, 2, true, "round y");
+    if (n % 4) note = "round_f16: n not a multiple of 4";
+    return 1;
+  }
+  if (has("conv1d_kernel")) {
+    const long cout = I(4), cin = I(5), L = I(6), Lout = I(7), K = I(8), groups = I(12);
+    if (groups <= 0 || cin % groups || cout % groups) note = "conv1d: groups";
+    rng(o, P(0), 0, cin * L, 4, false, "conv1d x");
+    rng(o, P(1), 0, cout * (groups > 0 ? cin / groups : 0) * K, 4, false, "conv1d w");
+    rng(o, P(2), 0, cout, 4, false, "conv1d bias");
+    rng(o, P(3), 0, cout * Lout, 4, true, "conv1d y");
+    return 1;
+  }
+  if (has("conv2d_kernel")) {
+    const long cout = I(4), cin = I(5), H = I(6), Wd = I(7), Ho = I(8), Wo = I(9), kh = I(10), kw = I(11), groups = I(16);
+    if (groups <= 0 || cin % groups || cout % groups) note = "conv2d: groups";
+    rng(o, P(0), 0, cin * H * Wd, 4, false, "conv2d x");
+    rng(o, P(1), 0, cout * (groups > 0 ? cin / groups : 0) * kh * kw, 4, false, "conv2d w");
+    rng(o, P(2), 0, cout, 4, false, "conv2d bias");
+    rng(o, P(3), 0, cout * Ho * Wo, 4, true, "conv2d y");
+    return 1;
+  }
+  if (has("conv_transpose1d_kernel")) {
+    const long Cin = I(4), L = I(5), Cout = I(6), k = I(7), Lout = I(8), groups = I(12);
+    if (groups <= 0 || Cin % groups || Cout % groups) note = "convTranspose1d: groups";
+    rng(o, P(0), 0, Cin * L, 4, false, "convT x");
+    rng(o, P(1), 0, Cin * (groups > 0 ? Cout / groups : 0) * k, 4, false, "convT w");
+    rng(o, P(2), 0, Cout, 4, false, "convT bias");
+    rng(o, P(3), 0, Cout * Lout, 4, true, "convT y");
+    return 1;
+  }
+  if (has("im2col_kernel")) {
+    const long Cin = I(2), L = I(3), k = I(4), Lout = I(5);
+    rng(o, P(0), 0, Cin * L, 4, false, "im2col x");
+    rng(o, P(1), 0, Cin * k * Lout, 4, true, "im2col y");
+    return 1;
+  }
+  if (has("bmm_qk_kernel")) {
+    const long T = I(4), Tb = I(5), H = I(6), HD = I(7), W = I(8), shared = I(9);
+    rng(o, P(0), 0, W * T * H * HD, 4, false, "bmmQK q");
+    rng(o, P(1), 0, (shared ? Tb : W * Tb) * H * HD, 4, false, "bmmQK b");
+    rng(o, P(2), 0, H * HD, 4, false, "bmmQK q bias");
+    rng(o, P(3), 0, W * H * T * Tb, 4, true, "bmmQK out");
+    return 1;
+  }
+  if (has("bmm_pv_kernel")) {
+    const long Tq = I(3), Tk = I(4), H = I(5), HD = I(6), W = I(7);
+    rng(o, P(0), 0, W * H * Tq * Tk, 4, false, "bmmPV p");
+    rng(o, P(1), 0, W * Tk * H * HD, 4, false, "bmmPV v");
+    rng(o, P(2), 0, W * Tq * H * HD, 4, true, "bmmPV out");
+    return 1;
+  }
+  if (has("relshift_stream_kernel")) {
+    const long total = arg<long>(a, 2), Lk = I(4), Pw = I(5);
+    rng(o, P(1), 0, total, 4, true, "relShiftStream y");
+    if (Lk > 0 && total > 0) rng(o, P(0), 0, ((total - 1) / Lk + 1) * Pw, 4, false, "relShiftStream x");
+    return 1;
+  }
+  if (has("relshift_kernel")) {
+    const long t = I(2), H = I(3);
+    rng(o, P(1), 0, H * t * t, 4, true, "relShift y");
+    if (t > 0 && H > 0) {
+      // x[(h t + f / 2t) p + (f mod 2t) - 1] grows with f over the columns it
+      // reads (f mod 2t != 0): the largest is at the last such f
+      const long p = 2 * t - 1, twoT = 2 * t;
+      long f = t + (t - 1) * p + (t - 1);
+      if (f % twoT == 0) f--;
+      rng(o, P(0), 0, ((H - 1) * t + f / twoT) * p + (f % twoT - 1) + 1, 4, false, "relShift x");
+    }
+    return 1;
+  }
+  if (has("repack_i8_kernel")) {
+    const long K = I(2), N = I(3);
+    rng(o, P(0), 0, K * N, 1, false, "repack src");
+    rng(o, P(1), 0, K * N, 1, true, "repack dst");
+    if ((long)gx * 64 < N || (long)gy * 64 < K) note = "repack_i8: grid below the matrix";
+    return 1;
+  }
+  if (has("dequant_i8_kernel")) {
+    const long K = I(3), N = I(4);
+    rng(o, P(0), 0, K * N, 1, false, "dequant q");
+    rng(o, P(1), 0, N, 4, false, "dequant scales");
+    rng(o, P(2), 0, K * N, 4, true, "dequant w");
+    return 1;
+  }
+  if (has("dequant_i4_kernel")) {
+    const long K = I(3), N = I(4), nblk = (K + 31) / 32;
+    rng(o, P(0), 0, N * nblk * 16, 1, false, "dequant q4");
+    rng(o, P(1), 0, N * nblk, 2, false, "dequant scales");
+    rng(o, P(2), 0, K * N, 4, true, "dequant w");
+    return 1;
+  }
+  if (has("f16_to_f32_rows_kernel")) {
+    const long n = I(2) * I(3);
+    rng(o, P(0), 0, n, 2, false, "f16 src");
+    rng(o, P(1), 0, n, 4, true, "f32 dst");
+    return 1;
+  }
+  if (has("nbits_dequant_f32_kernel")) {
+    const long zpb = I(3), K = I(4), N = I(5), nblk = (K + 31) / 32;
+    rng(o, P(0), 0, N * nblk * 16, 1, false, "nbits q");
+    rng(o, P(1), 0, N * nblk, 4, false, "nbits scales");
+    if (N > 0) rng(o, P(2), 0, (N - 1) * zpb + (nblk - 1) / 2 + 1, 1, false, "nbits zero points");
+    rng(o, P(6), 0, K * N, 4, true, "nbits w");
+    return 1;
+  }
+  if (has("snake_kernel")) {
+    const long C = I(3), L = I(4);
+    rng(o, P(0), 0, C * L, 4, false, "snake x");
+    rng(o, P(1), 0, C, 4, false, "snake alpha");
+    rng(o, P(2), 0, C * L, 4, true, "snake y");
+    return 1;
+  }
+  if (has("adain_kernel")) {
+    const long L = I(4), rows = gx;
+    rng(o, P(0), 0, rows * L, 4, false, "adain x");
+    rng(o, P(1), 0, rows, 4, false, "adain scale");
+    rng(o, P(2), 0, rows, 4, false, "adain shift");
+    rng(o, P(3), 0, rows * L, 4, true, "adain y");
+    return 1;
+  }
+  if (has("gather_cols_kernel")) {
+    const uint32_t *idx = arg<const uint32_t *>(a, 1);
+    const long C = I(3), T = I(4), outCols = I(5);
+    rng(o, idx, 0, outCols, 4, false, "gather indices");
+    rng(o, P(2), 0, C * outCols, 4, true, "gather y");
+    long mx = -1;  // the indices as uploaded (the host writes them)
+    for (long f = 0; f < outCols && idx; f++) mx = std::max<long>(mx, idx[f]);
+    if (mx >= T) note = "gatherCols: an index outside the row";
+    if (C > 0 && mx >= 0) rng(o, P(0), 0, (C - 1) * T + mx + 1, 4, false, "gather x");
+    return 1;
+  }
+  if (has("lstm_kernel")) {
+    const long seq = I(5), inp = I(6), hid = I(7), dirs = gx;
+    rng(o, P(0), 0, seq * inp, 4, false, "lstm x");
+    rng(o, P(1), 0, dirs * 4 * hid * inp, 4, false, "lstm w");
+    rng(o, P(2), 0, dirs * 4 * hid * hid, 4, false, "lstm r");
+    rng(o, P(3), 0, dirs * 8 * hid, 4, false, "lstm b");
+    rng(o, P(4), 0, seq * 2 * hid, 4, true, "lstm out");
+    if (dirs > 2 || (long)threads < 4 * hid) note = "lstm: block below its gate rows or more than 2 directions";
+    return 1;
+  }
+  if (has("jbatch_kernel")) {
+    const long base = I(3), B = I(4), hid = I(5);
+    rng(o, P(0), base * hid, (base + B) * hid, 4, false, "jbatch enc");
+    rng(o, P(1), 0, hid, 4, false, "jbatch pred");
+    rng(o, P(2), 0, B * hid, 4, true, "jbatch y");
+    return 1;
+  }
+  if (has("argmax_rows_kernel")) {
+    const long logits = I(3), rows = gx;
+    rng(o, P(0), 0, rows * logits, 4, false, "argmax x");
+    rng(o, P(1), 0, rows * 4, 4, true, "argmax res");
+    return 1;
+  }
+  if (has("joint_argmax_kernel")) {
+    const long frame = I(5), hidden = I(6), logits = I(8), rows = gx;
+    rng(o, P(0), frame * hidden, (frame + rows) * hidden, 4, false, "jointArgmax enc");
+    rng(o, P(1), 0, hidden, 4, false, "jointArgmax pred");
+    rng(o, P(2), 0, hidden * logits, 4, false, "jointArgmax outW");
+    rng(o, P(3), 0, logits, 4, false, "jointArgmax outB");
+    rng(o, P(4), 0, rows * 4, 4, true, "jointArgmax res");
+    return 1;
+  }
+  if (has("gemm_naive_kernel")) {
+    const int bk = arg<int>(a, 2);
+    const long M = I(6), N = I(7), K = I(8);
+    rng(o, P(0), 0, M * K, 4, false, "naive A");
+    rng(o, P(1), 0, K * N, bk ? 2 : 4, false, "naive B");
+    rng(o, P(3), 0, M * N, 4, true, "naive C");
+    rng(o, P(4), 0, N, 4, false, "naive bias");
+    rng(o, P(5), 0, M * N, 4, false, "naive add");
+    if ((long)gx * threads < M * N) note = "gemm_naive: grid below its outputs";
+    return 1;
+  }
+  if (has("gemv_naive_kernel") || has("gemv_mfma_kernel")) {
+    if (!size_is(a, 0, sizeof(GemvArgsM))) {
+      note = "GemvArgs layout differs from its mirror";
+      return 0;
+    }
+    const GemvArgsM p = arg<GemvArgsM>(a, 0);
+    const bool naive = has("gemv_naive_kernel");
+    const int fmt = naive ? arg<int>(a, 1) : (mangled.find("gemv_mfma_kernelILi1E") != std::string::npos ? 1 : 2);
+    gemv_spans(p, fmt, o);
+    if (naive && (long)gx * threads < (long)p.M * p.N) note = "gemv_naive: grid below its outputs";
+    if (!naive && (p.M > 16 || (long)gx * 16 < p.N || p.K % 128)) note = "gemv_mfma: more than 16 rows, grid below N, or K not a multiple of 128";
+    return 1;
+  }
+  if (has("gemv_batch_kernel")) {
+    if (!size_is(a, 0, sizeof(GemvArgsM)) || !size_is(a, 1, sizeof(GemvItemM) * kGemvItems)) {
+      note = "GemvArgs / GemvBatch layout differs from its mirror";
+      return 0;
+    }
+    const GemvArgsM base = arg<GemvArgsM>(a, 0);
+    std::vector<GemvItemM> it(kGemvItems);
+    std::memcpy(it.data(), a[1].data(), sizeof(GemvItemM) * kGemvItems);
+    const int fmt = mangled.find("gemv_batch_kernelILi1E") != std::string::npos ? 1 : 2;
+    for (unsigned y = 0; y < gy && y < (unsigned)kGemvItems; y++) {
+      GemvArgsM p = base;
+      p.A = it[y].A;
+      p.W = it[y].W;
+      p.scales = it[y].scales;
+      p.Y = it[y].Y;
+      gemv_spans(p, fmt, o);
+    }
+    if (gy > (unsigned)kGemvItems || base.M > 16 || (long)gx * 16 * kGemvWavesM < base.N) note = "gemv_batch: items, rows or grid out of range";
+    return 1;
+  }
+  return 0;
+}
+
 int extents(const std::string &mangled, const std::string &pretty, const std::vector<std::vector<char>> &a, unsigned gx, unsigned gy, unsigned gz,
             unsigned threads, std::vector<Span> &o, std::string &note) {
   using namespace fa;
@@ -462,6 +796,144 @@ int extents(const std::string &mangled, const std::string &pretty, const std::ve
     }
     return 1;
   }
+  if (has("dwconv_gen_kernel")) {
+    if (!size_is(a, 1, sizeof(CcSlotsM)) || !size_is(a, 4, sizeof(WinTable))) return 0;
+    const size_t xe = has("dwconv_gen_kernelIfE") ? 4 : 2;
+    const CcSlotsM cc = arg<CcSlotsM>(a, 1);
+    const int use = arg<int>(a, 2), D = arg<int>(a, 8);
+    const size_t cco = arg<size_t>(a, 3);
+    const WinTable st = arg<WinTable>(a, 4);
+    const void *y32 = arg<const void *>(a, 11);
+    rd(o, arg<const void *>(a, 6), (size_t)9 * D * 4, "dw taps");
+    rd(o, arg<const void *>(a, 7), (size_t)D * 4, "dw bias");
+    const int nw = (int)gy;
+    if (nw > st.n) note = "dwconv_gen: grid covers more windows than the table";
+    if ((long)gz * 64 * 4 < D || D % 4) note = "dwconv_gen: grid.z below D / 4 lanes, or D not a multiple of 4";
+    for (int w = 0; w < std::min(nw, st.n); w++) {
+      const long lo = (long)st.off[w] * D, hi = (long)(st.off[w] + st.len[w]) * D;
+      rng(o, arg<const void *>(a, 0), lo, hi, xe, false, "dw in");
+      if (y32) {
+        rng(o, y32, lo, hi, 4, true, "dw out f32");
+      } else {
+        rng(o, arg<const void *>(a, 9), lo, hi, 2, true, "dw out");
+        rng(o, arg<const void *>(a, 10), lo, hi, 2, true, "dw out lo");
+      }
+      if ((int)gx < st.len[w]) note = "dwconv_gen: grid.x below a window's frames";
+      if (use && w < kSG) rng(o, cc.cc_in[w], cco, cco + (size_t)8 * D, 4, false, "conv cache");
+    }
+    return 1;
+  }
+  if (has("stream_conv_cache_kernel")) {
+    if (!size_is(a, 0, sizeof(CcSlotsM))) return 0;
+    const size_t xe = has("stream_conv_cache_kernelIfE") ? 4 : 2;
+    const CcSlotsM cc = arg<CcSlotsM>(a, 0);
+    const size_t cco = arg<size_t>(a, 1);
+    const long D = arg<int>(a, 3), nemit = arg<int>(a, 4), nq = arg<int>(a, 5);
+    if (gx != 8) note = "stream_conv_cache: grid.x is not the cache's 8 rows";
+    for (unsigned w = 0; w < gy && w < (unsigned)kSG; w++) {
+      rng(o, cc.cc_out[w], cco, cco + 8 * D, 4, true, "next conv cache");
+      if (nemit < 8) rng(o, cc.cc_in[w], cco + nemit * D, cco + 8 * D, 4, false, "conv cache");
+      if (nemit > 0) rng(o, arg<const void *>(a, 2), ((long)w * nq + std::max(0L, nemit - 8)) * D, ((long)w * nq + nemit) * D, xe, false, "GLU rows");
+      if (nemit > nq) note = "stream_conv_cache: emitted rows past the pass";
+    }
+    if (gy > (unsigned)kSG) note = "stream_conv_cache: more windows than cache slots";
+    return 1;
+  }
+  if (has("zero_pad_rows_kernel")) {
+    if (!size_is(a, 2, sizeof(WinTable))) return 0;
+    float *x = arg<float *>(a, 0);
+    const long D = arg<int>(a, 1), Tpad = arg<int>(a, 3);
+    const WinTable st = arg<WinTable>(a, 2);
+    if ((int)gy > st.n) note = "zero_pad_rows: grid covers more windows than the table";
+    for (int w = 0; w < std::min((int)gy, st.n); w++) {
+      const long end = std::min<long>(Tpad, gx);
+      if (end > st.len[w]) rng(o, x, (st.off[w] + (long)st.len[w]) * D, (st.off[w] + end) * D, 4, true, "pad rows");
+    }
+    return 1;
+  }
+  if (has("v_transpose_kernel")) {
+    if (!size_is(a, 2, sizeof(WinTable))) return 0;
+    const long ldv = arg<int>(a, 1), H = arg<int>(a, 3), Tp = arg<int>(a, 4), HD = 128;
+    const WinTable win = arg<WinTable>(a, 2);
+    if ((long)gx * 64 < Tp || (long)gy != H) note = "v_transpose: grid below the keys or heads";
+    if ((int)gz > win.n) note = "v_transpose: grid covers more windows than the table";
+    for (int w = 0; w < std::min((int)gz, win.n); w++) {
+      if (win.len[w] > Tp) note = "v_transpose: a window longer than Tp";
+      if (win.len[w] > 0) rng(o, arg<const void *>(a, 0), win.off[w] * ldv, (win.off[w] + (long)win.len[w] - 1) * ldv + H * HD, 2, false, "v rows");
+      rng(o, arg<const void *>(a, 5), (long)w * H * HD * Tp, (long)(w + 1) * H * HD * Tp, 2, true, "vt");
+    }
+    return 1;
+  }
+  if (has("relpos_attn_kernel")) {
+    if (!size_is(a, 0, sizeof(AttnArgs))) return 0;
+    const AttnArgs t = arg<AttnArgs>(a, 0);
+    const size_t e = mangled.find("relpos_attn_kernelIffE") != std::string::npos ? 4 : 2;
+    const long HW = (long)t.H * t.HD;
+    rd(o, t.pbu, HW * 4, "pos bias u");
+    rd(o, t.pbv, HW * 4, "pos bias v");
+    rng(o, t.pos, 0, (long)(t.prows - 1) * t.ldp + HW, e, false, "pos table");
+    const int nw = (int)gz;
+    if (nw > t.win.n) note = "attention: grid covers more windows than the table";
+    for (int w = 0; w < std::min(nw, t.win.n); w++) {
+      const long off = t.win.off[w], T = t.win.len[w];
+      if (T <= 0) continue;
+      rng(o, t.q, off * t.ldq, (off + T - 1) * t.ldq + HW, e, false, "q");
+      rng(o, t.k, off * t.ldk, (off + T - 1) * t.ldk + HW, e, false, "k");
+      rng(o, t.v, off * t.ldv, (off + T - 1) * t.ldv + HW, e, false, "v");
+      rng(o, t.out, off * t.ldo, (off + T - 1) * t.ldo + HW, e, true, "attention out");
+      rng(o, t.out_lo, off * t.ldo, (off + T - 1) * t.ldo + HW, 2, true, "attention out lo");
+      if ((long)gx * 64 < T) note = "attention: grid.x below a window's queries";
+      if (T - 1 > t.pcenter || t.pcenter + T - 1 >= t.prows) note = "attention: window longer than the positional table";
+    }
+    return 1;
+  }
+  if (has("pack_windows_kernel")) {
+    if (!size_is(a, 3, sizeof(WinTable))) return 0;
+    const long Ttot = arg<long>(a, 1), MB = arg<int>(a, 2), Tpad = arg<int>(a, 5);
+    const WinTable dst = arg<WinTable>(a, 3), src = arg<WinTable>(a, 4);
+    if ((long)gy * 64 < MB || (int)gz > dst.n) note = "pack_windows: grid below the channels or above the windows";
+    for (int w = 0; w < std::min((int)gz, dst.n); w++) {
+      const long len = dst.len[w], rows = Tpad > 0 ? Tpad : len, start = src.off[w];
+      if ((long)gx * 64 < rows) note = "pack_windows: grid.x below a window's rows";
+      const long tin = std::min(len, Ttot - start);  // frames read: t < len and start + t < Ttot
+      if (tin > 0 && MB > 0) rng(o, arg<const void *>(a, 0), start, (MB - 1) * Ttot + start + tin, 4, false, "feature stream");
+      if (rows > 0 && MB > 0) rng(o, arg<const void *>(a, 6), dst.off[w] * MB, (dst.off[w] + rows) * MB, 4, true, "packed rows");
+    }
+    return 1;
+  }
+  if (has("row_map_kernel")) {
+    const long rows = arg<int>(a, 1);
+    rng(o, arg<const void *>(a, 2), 0, rows, 4, true, "row map");
+    if ((long)gx * threads < rows) note = "row_map: grid below its rows";
+    return 1;
+  }
+  if (has("wdq_kernel")) {
+    struct WdqListM {
+      const uint8_t *w[8];
+      const _Float16 *s[8];
+      _Float16 *out[8];
+      long chunks[8];
+      int n, i4;
+    };
+    if (!size_is(a, 0, sizeof(WdqListM))) {
+      note = "WdqList layout differs from its mirror";
+      return 0;
+    }
+    const WdqListM L = arg<WdqListM>(a, 0);
+    if ((int)gy > L.n || L.n > 8) note = "wdq: grid covers more items than the list";
+    for (int i = 0; i < std::min<int>((int)gy, 8); i++) {
+      const long n8 = L.chunks[i];
+      if ((long)gx * 256 * 4 < n8) note = "wdq: grid below an item's chunks";
+      if (L.i4) {
+        rng(o, L.w[i], 0, n8, 4, false, "int4 words");
+        rng(o, L.s[i], 0, (n8 + 3) / 4, 2, false, "int4 scales");
+      } else {
+        rng(o, L.w[i], 0, n8, 8, false, "int8 bytes");
+      }
+      rng(o, L.out[i], 0, n8, 16, true, "widened f16");
+    }
+    return 1;
+  }
   if (has("stream_out_kernel")) {
     if (!size_is(a, 4, sizeof(OutRowsM))) return 0;
     const int nq = arg<int>(a, 1), nemit = arg<int>(a, 2), D4 = arg<int>(a, 3);
@@ -498,20 +970,23 @@ int extents(const std::string &mangled, const std::string &pretty, const std::ve
     rng(o, arg<const void *>(a, 1), 0, n4, 16, true, "copy dst");
     return 1;
   }
-  // ── TDT decoder: window state as uploaded by the host (t = 0, T = lens) ──
-  auto tdt_state = [&](size_t i, int n) {
+  // ── TDT decoder: window state as uploaded by the host (t = 0, T = lens);
+  // `w` names the fields the kernel writes (the others are read) ──
+  enum { W_WIN = 1, W_HC = 2, W_PPJ = 4, W_Z = 8, W_P = 16, W_ALIVE = 32 };
+  auto tdt_state = [&](size_t i, int n, int w) {
     const TdtStateM s = arg<TdtStateM>(a, i);
-    rd(o, s.win, (size_t)n * sizeof(TdtWinM), "tdt windows");
-    rd(o, s.h, (size_t)n * 4 * kTH * 4, "tdt h");
-    rd(o, s.c, (size_t)n * 4 * kTH * 4, "tdt c");
-    rd(o, s.pp, (size_t)n * kTH * 4, "tdt pp");
-    rd(o, s.j, (size_t)n * kTH * 4, "tdt j");
-    rd(o, s.z, (size_t)n * 32 * kTH * 4, "tdt z");
-    rd(o, s.pv, (size_t)n * kTNB * 4, "tdt pv");
-    rd(o, s.pi, (size_t)n * kTNB * 4, "tdt pi");
-    rd(o, s.dv, (size_t)n * 4, "tdt dv");
-    rd(o, s.di, (size_t)n * 4, "tdt di");
-    rd(o, s.alive, (size_t)n * 4, "tdt alive");
+    auto f = [&](const void *p, size_t bytes, int bit, const char *what) { (w & bit ? wr : rd)(o, p, bytes, what); };
+    f(s.win, (size_t)n * sizeof(TdtWinM), W_WIN, "tdt windows");
+    f(s.h, (size_t)n * 4 * kTH * 4, W_HC, "tdt h");
+    f(s.c, (size_t)n * 4 * kTH * 4, W_HC, "tdt c");
+    f(s.pp, (size_t)n * kTH * 4, W_PPJ, "tdt pp");
+    f(s.j, (size_t)n * kTH * 4, W_PPJ, "tdt j");
+    f(s.z, (size_t)n * 32 * kTH * 4, W_Z, "tdt z");
+    f(s.pv, (size_t)n * kTNB * 4, W_P, "tdt pv");
+    f(s.pi, (size_t)n * kTNB * 4, W_P, "tdt pi");
+    f(s.dv, (size_t)n * 4, W_P, "tdt dv");
+    f(s.di, (size_t)n * 4, W_P, "tdt di");
+    f(s.alive, (size_t)n * 4, W_ALIVE, "tdt alive");
     return s;
   };
   if (has("tdt_joint_kernel")) {
@@ -522,13 +997,13 @@ int extents(const std::string &mangled, const std::string &pretty, const std::ve
     rd(o, arg<const void *>(a, 4), (size_t)n * kTH * 4, "joint x");
     if (ldw < (int)gx * 64) note = "tdt_joint: slabs past the padded row";
     if (n > 64 || (long)gy * 8 < n) note = "tdt_joint: windows not covered";
-    tdt_state(5, n);
+    tdt_state(5, n, W_P);
     return 1;
   }
   if (has("tdt_update_kernel")) {
     if (!size_is(a, 0, sizeof(TdtStateM))) return 0;
     const int cap = arg<int>(a, 1), n = (int)gx;
-    const TdtStateM s = tdt_state(0, n);
+    const TdtStateM s = tdt_state(0, n, W_WIN | W_ALIVE);
     wr(o, s.ids, (size_t)n * cap * 4, "tdt ids");
     wr(o, s.frs, (size_t)n * cap * 4, "tdt frames");
     return 1;
@@ -538,7 +1013,7 @@ int extents(const std::string &mangled, const std::string &pretty, const std::ve
     const int n = arg<int>(a, 5);
     rd(o, arg<const void *>(a, 0), (size_t)4 * kTH * kTH * 4, "lstm W");
     rd(o, arg<const void *>(a, 1), (size_t)4 * kTH * kTH * 4, "lstm R");
-    const TdtStateM s = tdt_state(4, n);
+    const TdtStateM s = tdt_state(4, n, W_Z);
     const float *embed = arg<const float *>(a, 2);
     for (int w = 0; w < n && s.win; w++) {
       const int last = s.win[w].last;
@@ -552,7 +1027,7 @@ int extents(const std::string &mangled, const std::string &pretty, const std::ve
     if (!size_is(a, 2, sizeof(TdtStateM))) return 0;
     const int n = (int)gy;
     rd(o, arg<const void *>(a, 0), (size_t)8 * kTH * 4, "lstm bias");
-    tdt_state(2, n);
+    tdt_state(2, n, W_HC);
     return 1;
   }
   if (has("tdt_proj_kernel")) {
@@ -561,14 +1036,14 @@ int extents(const std::string &mangled, const std::string &pretty, const std::ve
     rd(o, arg<const void *>(a, 0), (size_t)kTH * kTH * 4, "pred W");
     rd(o, arg<const void *>(a, 1), (size_t)kTH * 4, "pred bias");
     rd(o, arg<const void *>(a, 2), (size_t)n * 4 * kTH * 4, "pred h");
-    const TdtStateM s = tdt_state(4, n);
+    const TdtStateM s = tdt_state(4, n, W_PPJ);
     const float *fr = arg<const float *>(a, 3);
     for (int w = 0; w < n && s.win; w++)
       if (s.win[w].T > 0) rng(o, fr, (long)s.win[w].off * kTH, (long)(s.win[w].off + s.win[w].T) * kTH, 4, false, "frames");
     if (gx * 64 != kTH) note = "tdt_proj: grid.x";
     return 1;
   }
-  return 0;
+  return op_extents(mangled, a, gx, gy, gz, threads, o, note);
 }
 
 }  // namespace audit_ext

@@ -207,6 +207,50 @@ def ragged(L, fa):
     report(L, {"batches": len(batches)})
 
 
+def quant(L, fa):
+    """the quantised encoder (int8, int4) on both of its routes:
+    4 windows of 15 s (752 rows: each layer's weights widened once by
+    wdq_kernel, then the f16 GEMMs) and 2 windows of 8 s (200 rows: the
+    dequantisation inside the GEMM)."""
+    ctx = fa.createContext("hip")
+    man = fa.synth.make_weights(dict(FULL), seed=1)
+    for fmt in ("int8", "int4"):
+        enc = fa.FusedEncoder(ctx, man, fmt, max_T=188)
+        for T, W in ((1500, 4), (800, 2)):
+            enc.encode(fa.synth.make_features(128, T, seed=3, W=W))
+        enc.close()
+    ctx.destroy()
+    report(L, {"formats": 2})
+
+
+def oppath(L, fa):
+    """The reference's op sequence (parakeetEncodeBatch over ComputeContext
+    ops) with f16 and f32 weights, with and without the attnFused member, on
+    2 windows; then the fused encoder's packed and padded forwards from
+    packWindows."""
+    import numpy as np
+    ctx = fa.createContext("hip")
+    man = fa.synth.make_weights(dict(FULL), seed=1)
+    mels = fa.synth.make_features(128, 400, seed=5, W=2)
+    for weights in ("f16", "f32"):
+        enc = fa.loadParakeetEncoder(ctx, man, weights=weights)
+        for fused in (False, True):
+            a = ctx.pushArena()
+            fa.parakeetEncodeBatch(ctx, enc, mels, attnFused=fused)
+            ctx.popArena(a)
+    fe = fa.FusedEncoder(ctx, man, "f16", max_T=188)
+    stream_ = np.concatenate(mels, axis=1)
+    feats = ctx.upload(stream_, 128, stream_.shape[1])
+    for layout in ("packed", "padded"):
+        a = ctx.pushArena()
+        packed = ctx.packWindows(feats, [0, 400], [400, 400], layout)
+        fe.forward(packed, [400, 400], layout)
+        ctx.popArena(a)
+    fe.close()
+    ctx.destroy()
+    report(L, {"routes": 5})
+
+
 def stream(L, fa, profile: bool):
     """The stream workload (EOU config): one stream pushed 160 ms at a time,
     then 16 streams pushed together, with or without a profile window."""
@@ -434,6 +478,10 @@ def main():
         e2e(L, fa, wb, float(sys.argv[2]) if len(sys.argv) > 2 else 3600.0, what.endswith("p"), "s" not in what[3:])
     elif what == "ragged":
         ragged(L, fa)
+    elif what == "quant":
+        quant(L, fa)
+    elif what == "oppath":
+        oppath(L, fa)
     elif what == "abi":
         abi(L, fa)
     elif what == "stream_failures":

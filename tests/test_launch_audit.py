@@ -119,6 +119,26 @@ def test_ragged_batches_on_two_lanes(builds):
     assert r["races"] == [] and r["order_checks"] > 10000
 
 
+def test_quantized_encoder_routes(builds):
+    """configs[4]'s int8 and int4 encoder on both routes (weights widened once
+    per layer for 752 rows; dequantisation inside the GEMM for 200 rows):
+    every kernel modelled, inside its blocks, no unordered access."""
+    r = run(builds, "quant", layers=2)
+    assert r["launches"] > 100
+    assert r["violations"] == [] and _unmodelled_on_path(r) == [] and r["races"] == []
+    assert r["extent_checks"] > 500
+
+
+def test_reference_op_sequence_and_packed_forwards(builds):
+    """parakeetEncodeBatch's ComputeContext ops (f16 and f32 weights, with and
+    without attnFused) and the fused encoder's packed / padded forwards from
+    packWindows: every kernel modelled, inside its blocks."""
+    r = run(builds, "oppath", layers=2)
+    assert r["launches"] > 300
+    assert r["violations"] == [] and _unmodelled_on_path(r) == [] and r["races"] == []
+    assert r["extent_checks"] > 1000
+
+
 @pytest.mark.parametrize("scenario", ["stream", "streamp"])
 def test_stream_workload(builds, scenario):
     r = run(builds, scenario, layers=4)
@@ -177,7 +197,8 @@ def test_node_addon_conformance_cases(builds, tmp_path):
     r, counts, bad = _node_report(builds, "conformance", tmp_path)
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
     assert "58 cases cover every required method" in r.stdout
-    assert counts["launches"] > 50 and bad == []
+    assert counts["launches"] > 50 and counts["extent_checks"] > 100 and bad == []
+    assert not any(ln.startswith("unmodelled") for ln in (tmp_path / "conformance.txt").read_text().splitlines())
 
 
 def test_node_addon_selftest_runs_to_the_end(builds, tmp_path):
