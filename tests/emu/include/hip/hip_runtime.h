@@ -1,0 +1,218 @@
+// CPU execution of the library's kernel sources (test infrastructure).
+//
+// This header stands in for <hip/hip_runtime.h> when a .hip source is
+// compiled as host C++ (tests/emu/build_emu.py): kernels become ordinary
+// functions, and a launch runs every workgroup on the CPU, one workgroup at a
+// time, each thread a fiber (emu_rt.cpp).  __syncthreads and the wave
+// operations the kernels use (ballot, shfl_xor, readfirstlane) block their
+// fiber until the threads (or the wave's lanes) that take part have arrived.
+// __shared__ arrays become static storage: one workgroup runs at a time, so
+// they are the workgroup's LDS.  Device memory is host memory from malloc,
+// sized as asked, so AddressSanitizer sees every out-of-bounds access a
+// kernel makes.  The HIP API calls are synchronous.
+#pragma once
+#include <cmath>
+#include <cstddef>
+#include <cstdint>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <type_traits>
+#include <utility>
+
+// ── qualifiers ──
+#define __global__
+#define __device__
+#define __host__
+#define __shared__ static
+#define __constant__ static
+#define __forceinline__ inline __attribute__((always_inline))
+#define __launch_bounds__(...)
+
+struct dim3 {
+  unsigned x = 1, y = 1, z = 1;
+  constexpr dim3(unsigned a = 1, unsigned b = 1, unsigned c = 1) : x(a), y(b), z(c) {}
+};
+
+// ── vector types (HIP's layouts: 8- and 16-byte aligned structs) ──
+struct alignas(8) float2 {
+  float x, y;
+};
+struct alignas(16) float4 {
+  float x, y, z, w;
+};
+struct alignas(8) uint2 {
+  unsigned x, y;
+};
+struct alignas(16) uint4 {
+  unsigned x, y, z, w;
+};
+struct alignas(8) int2 {
+  int x, y;
+};
+struct alignas(16) int4 {
+  int x, y, z, w;
+};
+inline float4 make_float4(float x, float y, float z, float w) { return float4{x, y, z, w}; }
+inline float2 make_float2(float x, float y) { return float2{x, y}; }
+
+// ── runtime types ──
+typedef enum hipError_t {
+  hipSuccess = 0,
+  hipErrorInvalidValue = 1,
+  hipErrorOutOfMemory = 2,
+  hipErrorInvalidDevice = 101,
+  hipErrorInvalidHandle = 400,
+  hipErrorNotReady = 600,
+  hipErrorLaunchFailure = 719,
+} hipError_t;
+typedef enum hipMemcpyKind {
+  hipMemcpyHostToHost = 0,
+  hipMemcpyHostToDevice = 1,
+  hipMemcpyDeviceToHost = 2,
+  hipMemcpyDeviceToDevice = 3,
+  hipMemcpyDefault = 4,
+} hipMemcpyKind;
+struct ihipStream_t;
+struct ihipEvent_t;
+typedef ihipStream_t *hipStream_t;
+typedef ihipEvent_t *hipEvent_t;
+#define hipStreamNonBlocking 0x01
+#define hipEventDisableTiming 0x02
+#define hipHostMallocDefault 0x0
+struct hipDeviceProp_t {
+  char name[256];
+  char gcnArchName[256];
+  int multiProcessorCount;
+  size_t totalGlobalMem;
+  int warpSize;
+  int maxThreadsPerBlock;
+  size_t sharedMemPerBlock;
+};
+
+hipError_t hipGetDeviceCount(int *n);
+hipError_t hipSetDevice(int d);
+hipError_t hipGetDeviceProperties(hipDeviceProp_t *p, int d);
+hipError_t hipDeviceSynchronize(void);
+hipError_t hipMalloc(void **p, size_t n);
+hipError_t hipFree(void *p);
+hipError_t hipHostMalloc(void **p, size_t n, unsigned int flags);
+hipError_t hipHostFree(void *p);
+hipError_t hipMemcpy(void *dst, const void *src, size_t n, hipMemcpyKind k);
+hipError_t hipMemcpyAsync(void *dst, const void *src, size_t n, hipMemcpyKind k, hipStream_t s);
+hipError_t hipMemsetAsync(void *dst, int v, size_t n, hipStream_t s);
+hipError_t hipStreamCreateWithFlags(hipStream_t *s, unsigned int flags);
+hipError_t hipStreamDestroy(hipStream_t s);
+hipError_t hipStreamSynchronize(hipStream_t s);
+hipError_t hipStreamWaitEvent(hipStream_t s, hipEvent_t e, unsigned int flags);
+hipError_t hipEventCreate(hipEvent_t *e);
+hipError_t hipEventCreateWithFlags(hipEvent_t *e, unsigned flags);
+hipError_t hipEventDestroy(hipEvent_t e);
+hipError_t hipEventRecord(hipEvent_t e, hipStream_t s);
+hipError_t hipEventSynchronize(hipEvent_t e);
+hipError_t hipEventElapsedTime(float *ms, hipEvent_t a, hipEvent_t b);
+hipError_t hipGetLastError(void);
+const char *hipGetErrorString(hipError_t e);
+
+// ── execution of a launch (emu_rt.cpp) ──
+namespace emu {
+struct Thread {
+  dim3 tid;
+  int lane, wave;
+};
+extern dim3 g_block_idx, g_block_dim, g_grid_dim;
+Thread &self();
+void run_grid(dim3 grid, dim3 block, const std::function<void()> &body);
+void barrier();
+uint64_t wave_exchange_u64(uint64_t v, int src_lane_xor, bool ballot);
+void check_uniform(uint64_t v, const char *what);
+void dma16(const void *g, uint32_t lds_addr);
+uint32_t lds_base_hi();
+void report(const char *what);
+
+template <class... P, class... A>
+void launch(void (*k)(P...), dim3 g, dim3 b, size_t shm, A &&...a) {
+  (void)shm;
+  // arguments are copied once, as a kernel's by-value parameters are
+  std::tuple<std::decay_t<P>...> args(std::forward<A>(a)...);
+  run_grid(g, b, [&]() { std::apply([&](auto &...x) { k(x...); }, args); });
+}
+}  // namespace emu
+
+#define hipLaunchKernelGGL(k, g, b, shm, s, ...) ::emu::launch(k, dim3(g), dim3(b), (size_t)(shm), ##__VA_ARGS__)
+
+// ── built-in variables ──
+#define threadIdx (::emu::self().tid)
+#define blockIdx (::emu::g_block_idx)
+#define blockDim (::emu::g_block_dim)
+#define gridDim (::emu::g_grid_dim)
+
+// ── device functions ──
+inline void __syncthreads() { ::emu::barrier(); }
+inline unsigned long long __ballot(int pred) { return ::emu::wave_exchange_u64(pred ? 1 : 0, 0, true); }
+inline int __popcll(unsigned long long v) { return __builtin_popcountll(v); }
+inline int __shfl_xor(int v, int m) { return (int)(uint32_t)::emu::wave_exchange_u64((uint32_t)v, m, false); }
+inline unsigned __shfl_xor(unsigned v, int m) { return (unsigned)::emu::wave_exchange_u64(v, m, false); }
+inline float __shfl_xor(float v, int m) {
+  uint32_t u;
+  std::memcpy(&u, &v, 4);
+  u = (uint32_t)::emu::wave_exchange_u64(u, m, false);
+  std::memcpy(&v, &u, 4);
+  return v;
+}
+inline double __shfl_xor(double v, int m) {
+  uint64_t u;
+  std::memcpy(&u, &v, 8);
+  u = ::emu::wave_exchange_u64(u, m, false);
+  std::memcpy(&v, &u, 8);
+  return v;
+}
+inline float __uint_as_float(unsigned u) {
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+inline unsigned __float_as_uint(float f) {
+  unsigned u;
+  std::memcpy(&u, &f, 4);
+  return u;
+}
+template <class T>
+inline T emu_readfirstlane(T v) {  // the kernels apply it to values every lane holds alike: checked
+  ::emu::check_uniform((uint64_t)v, "readfirstlane of a value that differs between lanes");
+  return v;
+}
+#define __builtin_amdgcn_readfirstlane(x) emu_readfirstlane(x)
+#define __builtin_amdgcn_s_waitcnt(x) ((void)(x))
+// raw buffer loads: reads past the resource's size return 0 (the hardware's
+// range check), reported as a finding
+struct emu_rsrc {
+  const char *base;
+  int bytes;
+};
+#define __amdgpu_buffer_rsrc_t emu_rsrc
+inline emu_rsrc emu_make_rsrc(void *p, int stride, int bytes, int flags) {
+  (void)stride;
+  (void)flags;
+  return emu_rsrc{(const char *)p, bytes};
+}
+#define __builtin_amdgcn_make_buffer_rsrc(p, s, n, f) emu_make_rsrc((p), (s), (n), (f))
+inline uint32_t emu_buffer_load_b32(emu_rsrc r, int voff, int soff, int aux) {
+  (void)aux;
+  const long o = (long)voff + soff;
+  if (o < 0 || o + 4 > r.bytes) {
+    ::emu::report("raw buffer load outside its resource (returns 0 on the GPU)");
+    return 0;
+  }
+  uint32_t v;
+  std::memcpy(&v, r.base + o, 4);
+  return v;
+}
+#define __builtin_amdgcn_raw_buffer_load_b32(r, v, s, a) emu_buffer_load_b32((r), (v), (s), (a))
+
+inline int min(int a, int b) { return a < b ? a : b; }
+inline int max(int a, int b) { return a > b ? a : b; }
+inline long min(long a, long b) { return a < b ? a : b; }
+inline long max(long a, long b) { return a > b ? a : b; }
+inline unsigned min(unsigned a, unsigned b) { return a < b ? a : b; }
+inline unsigned max(unsigned a, unsigned b) { return a > b ? a : b; }
