@@ -1,9 +1,9 @@
-"""Build the CPU execution of the decoder's kernel sources (test
-infrastructure): fluidaudio-web_amd/csrc/runtime.hip and tdt.hip compiled as
+"""Build the CPU execution of the decoder and log-mel kernel sources (test
+infrastructure): fluidaudio-web_amd/csrc/runtime.hip, tdt.hip and mel.hip compiled as
 host C++ against the HIP stand-in in tests/emu/include (kernels run as fibers,
 emu_rt.cpp), with AddressSanitizer and UBSan, into
 tests/emu/_build/libfa_emu.so.  The library's C ABI entry points that these
-two sources do not define are stubs returning FA_E_UNSUPPORTED, so the
+sources do not define are stubs returning FA_E_UNSUPPORTED, so the
 package's Python bindings load it through FA_LIB_PATH.
 
 The sources are used as they are, with one rewrite: the inline-asm
@@ -56,7 +56,8 @@ def _entry_points() -> list[str]:
 def build(tdt_src: str | None = None, tag: str = "") -> str:
     os.makedirs(OUT, exist_ok=True)
     objs = []
-    srcs = [("runtime.hip", os.path.join(CSRC, "runtime.hip")), ("tdt.hip", tdt_src or os.path.join(CSRC, "tdt.hip"))]
+    srcs = [("runtime.hip", os.path.join(CSRC, "runtime.hip")), ("tdt.hip", tdt_src or os.path.join(CSRC, "tdt.hip")),
+            ("mel.hip", os.path.join(CSRC, "mel.hip"))]
     for name, path in srcs:
         cpp = os.path.join(OUT, name.replace(".hip", f"{tag}.cpp"))
         with open(cpp, "w") as f:
@@ -81,12 +82,12 @@ def build(tdt_src: str | None = None, tag: str = "") -> str:
         undefined |= {ln.split()[-1] for ln in nm.splitlines() if ln.strip()}
     stubs = os.path.join(OUT, f"stubs{tag}.c")
     with open(stubs, "w") as f:
-        f.write("/* entry points outside runtime.hip and tdt.hip: FA_E_UNSUPPORTED */\n")
+        f.write("/* entry points outside the compiled sources: FA_E_UNSUPPORTED */\n")
         for n in _entry_points():
             if n not in defined:
                 f.write(f"int {n}(void) {{ return 5; }}\n")
-        # internal functions of the other sources that runtime.hip calls (the
-        # log-mel scratch set-up and release): no-ops returning 0
+        # internal functions of the other sources that these call: no-ops
+        # returning 0
         for i, n in enumerate(sorted(x for x in undefined - defined if x.startswith("_ZN2fa"))):
             f.write(f'int emu_stub_{i}(void) __asm__("{n}");\nint emu_stub_{i}(void) {{ return 0; }}\n')
     so = stubs.replace(".c", ".o")

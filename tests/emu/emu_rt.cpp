@@ -33,6 +33,7 @@
 #ifdef EMU_ASAN
 extern "C" void __sanitizer_start_switch_fiber(void **fake_stack_save, const void *bottom, size_t size);
 extern "C" void __sanitizer_finish_switch_fiber(void *fake_stack_save, const void **bottom_old, size_t *size_old);
+extern "C" void __asan_unpoison_memory_region(void const volatile *addr, size_t size);
 #endif
 
 // x86-64 context switch: saves the callee-saved registers on the current
@@ -135,6 +136,11 @@ void start(Fiber &f) {
       std::abort();
     }
   }
+#ifdef EMU_ASAN
+  // a finished fiber's last switch never returns, so the redzones of that
+  // frame are still marked in the shadow of its stack: clear them for reuse
+  __asan_unpoison_memory_region(f.stack, kStack);
+#endif
   // initial frame: six callee-saved registers, then the return address
   // (trampoline); the top is 16-byte aligned, so trampoline starts with the
   // stack alignment of a called function
@@ -381,6 +387,10 @@ hipError_t hipEventElapsedTime(float *ms, hipEvent_t a, hipEvent_t b) {
   if (!a->recorded || !b->recorded) return hipErrorNotReady;
   *ms = std::chrono::duration<float, std::milli>(b->t - a->t).count();
   return hipSuccess;
+}
+hipError_t hipGetSymbolAddress(void **dev, const void *sym) {  // a __device__ array is host static data here
+  *dev = const_cast<void *>(sym);
+  return sym ? hipSuccess : hipErrorInvalidValue;
 }
 hipError_t hipGetLastError(void) {
   hipError_t e = g_last;

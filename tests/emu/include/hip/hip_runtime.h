@@ -28,6 +28,8 @@
 #define __constant__ static
 #define __forceinline__ inline __attribute__((always_inline))
 #define __launch_bounds__(...)
+#define __align__(n) __attribute__((aligned(n)))
+#define HIP_SYMBOL(x) ((const void *)&(x))
 
 struct dim3 {
   unsigned x = 1, y = 1, z = 1;
@@ -90,6 +92,7 @@ struct hipDeviceProp_t {
   size_t sharedMemPerBlock;
 };
 
+extern "C" {
 hipError_t hipGetDeviceCount(int *n);
 hipError_t hipSetDevice(int d);
 hipError_t hipGetDeviceProperties(hipDeviceProp_t *p, int d);
@@ -111,8 +114,10 @@ hipError_t hipEventDestroy(hipEvent_t e);
 hipError_t hipEventRecord(hipEvent_t e, hipStream_t s);
 hipError_t hipEventSynchronize(hipEvent_t e);
 hipError_t hipEventElapsedTime(float *ms, hipEvent_t a, hipEvent_t b);
+hipError_t hipGetSymbolAddress(void **dev, const void *sym);
 hipError_t hipGetLastError(void);
 const char *hipGetErrorString(hipError_t e);
+}  // extern "C"
 
 // ── execution of a launch (emu_rt.cpp) ──
 namespace emu {

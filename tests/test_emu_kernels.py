@@ -1,12 +1,16 @@
-"""The decoder's kernel sources executed on the CPU (tests/emu): runtime.hip and
-tdt.hip compiled as host C++ against a HIP stand-in whose launches run every
-workgroup's threads as fibers (barriers and wave operations wait for the
+"""The decoder's and the log-mel front end's kernel sources executed on the CPU
+(tests/emu): runtime.hip, tdt.hip and mel.hip compiled as host C++ against a
+HIP stand-in whose launches run every workgroup's threads as fibers (barriers and wave operations wait for the
 threads that take part), device memory malloc'd at its exact size, the whole
 build under AddressSanitizer and UBSan.  The package's own TdtDecoder drives it
 through FA_LIB_PATH, and each window's token ids and frame indices must equal
 the CPU oracle's (the GPU tests' bar), with no sanitizer report and no finding
 of the stand-in (buffer loads past their resource, readfirstlane of values
-that differ between lanes).
+that differ between lanes).  The log-mel features are held to the GPU
+tests' bar: raw log-mel >= 99.9 % bit-identical and within 1 ulp of the
+oracle (its libm may round a log differently in the last bit), normalised
+features within 1e-5, and the allocation-free entry point bit-identical to
+the allocating one.
 
 The same run covers the removed two-windows-per-wave joint kernel, which made
 an illegal memory access on the GPU at 40 windows: executed from source at 40
@@ -43,9 +47,9 @@ def emu():
     return {"shipped": build_emu.build(), "two_windows": build_emu.build(variant, "_alt"), "rt": rt}
 
 
-def run(emu, lib, case):
+def run(emu, lib, case, script="run_tdt.py"):
     env = dict(os.environ, FA_LIB_PATH=emu[lib], LD_PRELOAD=emu["rt"], ASAN_OPTIONS="detect_leaks=0:detect_stack_use_after_return=0")
-    r = subprocess.run([sys.executable, os.path.join(EMU, "run_tdt.py"), case], env=env, capture_output=True, text=True, timeout=600)
+    r = subprocess.run([sys.executable, os.path.join(EMU, script), case], env=env, capture_output=True, text=True, timeout=600)
     assert r.returncode == 0, r.stderr[-4000:]
     assert "ERROR: AddressSanitizer" not in r.stderr and "runtime error" not in r.stderr, r.stderr[-4000:]
     return json.loads(r.stdout.strip().splitlines()[-1])
@@ -61,3 +65,16 @@ def test_decoder_kernel_sources_match_the_oracle_on_the_cpu(emu, case):
 def test_two_windows_per_wave_joint_stays_in_bounds_at_40_windows(emu):
     r = run(emu, "two_windows", "ragged40")
     assert r["windows"] == 40 and all(r["equal"]) and r["findings"] == [], r
+
+
+@pytest.mark.parametrize("case", ["signals", "stream"])
+def test_log_mel_kernel_sources_match_the_oracle_on_the_cpu(emu, case):
+    r = run(emu, "shipped", case, "run_mel.py")
+    assert r["findings"] == [], r
+    assert r["raw_same_frac"] >= 0.999 and r["raw_max_ulp"] <= 1 and r["feat_max_abs"] <= 1e-5, r
+
+
+def test_allocation_free_log_mel_equals_the_allocating_entry_on_the_cpu(emu):
+    r = run(emu, "shipped", "static", "run_mel.py")
+    assert r["checks"] == 4 and r["bit_identical"] and r["findings"] == [], r
+
