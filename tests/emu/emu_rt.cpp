@@ -68,7 +68,7 @@ dim3 g_block_idx, g_block_dim, g_grid_dim;
 
 namespace {
 enum State { READY, AT_BARRIER, AT_WAVE, DONE };
-enum WaveOp { W_BALLOT, W_SHFL, W_UNIFORM };
+enum WaveOp { W_BALLOT, W_SHFL, W_UNIFORM, W_READLANE, W_DPP, W_SYNC, W_MFMA };
 constexpr size_t kStack = 128 * 1024;
 
 struct Fiber {
@@ -80,6 +80,8 @@ struct Fiber {
   uint64_t val = 0, res = 0;
   int arg = 0;
   const char *what = nullptr;
+  float a[8], b[8];  // MFMA operands
+  float c[4], d[4];
 };
 
 std::vector<Fiber> g_f;
@@ -174,10 +176,46 @@ bool release_waves(int nthreads) {
     if (op == W_BALLOT)
       for (int i = l0; i < l1; i++)
         if (g_f[i].st == AT_WAVE && g_f[i].val) bits |= 1ull << (i - l0);
+    if (op == W_MFMA) {  // D = C + A B: A[m][k] from lane m + 16 (k / kb), B[k][n] from lane n + 16 (k / kb)
+      for (int i = l0; i < l1; i++)
+        if (g_f[i].st != AT_WAVE) report("MFMA with lanes of the wave absent");
+      for (int i = l0; i < l1; i++) {
+        Fiber &f = g_f[i];
+        if (f.st != AT_WAVE) continue;
+        const int li = i - l0, n = li & 15, kb = f.arg;
+        for (int r = 0; r < 4; r++) {
+          const int m = 4 * (li >> 4) + r;
+          float acc = 0.f;
+          for (int k = 0; k < 4 * kb; k++) {
+            const int la = l0 + m + 16 * (k / kb), lb = l0 + n + 16 * (k / kb);
+            if (la < l1 && lb < l1) acc += g_f[la].a[k % kb] * g_f[lb].b[k % kb];
+          }
+          f.d[r] = f.c[r] + acc;
+        }
+      }
+      for (int i = l0; i < l1; i++)
+        if (g_f[i].st == AT_WAVE) g_f[i].st = READY;
+      any = true;
+      continue;
+    }
     for (int i = l0; i < l1; i++) {
       Fiber &f = g_f[i];
       if (f.st != AT_WAVE) continue;
-      if (op == W_BALLOT) {
+      if (op == W_SYNC) {
+        f.res = 0;
+      } else if (op == W_READLANE) {
+        const int j = l0 + (f.arg & 63);
+        f.res = (j < l1 && g_f[j].st == AT_WAVE) ? g_f[j].val : f.val;
+      } else if (op == W_DPP) {
+        const int li = i - l0, c = f.arg;
+        int src = -1;
+        if (c >= 0 && c <= 0xff) src = (li & ~3) | ((c >> (2 * (li & 3))) & 3);  // quad_perm
+        else if (c == 0x140) src = (li & ~15) | (15 - (li & 15));              // row_mirror
+        else if (c == 0x141) src = (li & ~7) | (7 - (li & 7));                 // row_half_mirror
+        else report("DPP control the CPU build does not know");
+        const int j = l0 + src;
+        f.res = (src >= 0 && j < l1 && g_f[j].st == AT_WAVE) ? g_f[j].val : 0;
+      } else if (op == W_BALLOT) {
         f.res = bits;
       } else if (op == W_SHFL) {
         const int j = l0 + ((i - l0) ^ f.arg);
@@ -272,6 +310,37 @@ uint64_t wave_exchange_u64(uint64_t v, int arg, bool ballot) {
   return g_f[g_cur].res;
 }
 
+static uint64_t collective(WaveOp op, uint64_t v, int arg) {
+  Fiber &f = g_f[g_cur];
+  f.st = AT_WAVE;
+  f.op = op;
+  f.val = v;
+  f.arg = arg;
+  to_sched();
+  return g_f[g_cur].res;
+}
+uint64_t wave_readlane(uint64_t v, int lane) { return collective(W_READLANE, v, lane); }
+uint32_t wave_dpp(uint32_t v, int ctrl) { return (uint32_t)collective(W_DPP, v, ctrl); }
+void wave_sync() { (void)collective(W_SYNC, 0, 0); }
+void wave_mfma_16x16(const float *a, const float *b, int kb, const float *c4, float *d4) {
+  Fiber &f = g_f[g_cur];
+  std::memcpy(f.a, a, 4 * kb);
+  std::memcpy(f.b, b, 4 * kb);
+  std::memcpy(f.c, c4, 16);
+  (void)collective(W_MFMA, 0, kb);
+  std::memcpy(d4, g_f[g_cur].d, 16);
+}
+
+// dynamic LDS (extern __shared__): one buffer per launch, of the launch's size
+static void *g_dyn = nullptr;
+void set_dyn_lds(size_t bytes) {
+  std::free(g_dyn);
+  const size_t n = (bytes + 15) & ~(size_t)15;
+  g_dyn = std::aligned_alloc(16, n ? n : 16);
+  std::memset(g_dyn, 0xff, n ? n : 16);
+}
+void *dyn_lds() { return g_dyn; }
+
 void check_uniform(uint64_t v, const char *what) {
   Fiber &f = g_f[g_cur];
   f.st = AT_WAVE;
@@ -306,7 +375,19 @@ void report(const char *what) {
 // ── synchronous HIP API on host memory ──
 struct ihipStream_t {
   int flags;
+  bool capturing = false;
+  std::vector<std::function<void()>> ops;
 };
+struct ihipGraph_t {
+  std::vector<std::function<void()>> ops;
+};
+struct ihipGraphExec_t {
+  std::vector<std::function<void()>> ops;
+};
+namespace emu {
+bool capturing(hipStream_t s) { return s && s->capturing; }
+void record(hipStream_t s, std::function<void()> op) { s->ops.push_back(std::move(op)); }
+}  // namespace emu
 struct ihipEvent_t {
   std::chrono::steady_clock::time_point t;
   bool recorded = false;
@@ -353,9 +434,51 @@ hipError_t hipMemcpy(void *dst, const void *src, size_t n, hipMemcpyKind) {
   if (n) std::memmove(dst, src, n);
   return hipSuccess;
 }
-hipError_t hipMemcpyAsync(void *dst, const void *src, size_t n, hipMemcpyKind k, hipStream_t) { return hipMemcpy(dst, src, n, k); }
-hipError_t hipMemsetAsync(void *dst, int v, size_t n, hipStream_t) {
+hipError_t hipMemcpyAsync(void *dst, const void *src, size_t n, hipMemcpyKind k, hipStream_t s) {
+  if (emu::capturing(s)) {
+    emu::record(s, [=]() { (void)hipMemcpy(dst, src, n, k); });
+    return hipSuccess;
+  }
+  return hipMemcpy(dst, src, n, k);
+}
+hipError_t hipMemsetAsync(void *dst, int v, size_t n, hipStream_t s) {
+  if (emu::capturing(s)) {
+    emu::report("hipMemsetAsync recorded into a captured graph");
+    emu::record(s, [=]() { std::memset(dst, v, n); });
+    return hipSuccess;
+  }
   if (n) std::memset(dst, v, n);
+  return hipSuccess;
+}
+hipError_t hipFuncSetAttribute(const void *, hipFuncAttribute, int) { return hipSuccess; }
+hipError_t hipStreamBeginCapture(hipStream_t s, hipStreamCaptureMode) {
+  if (!s || s->capturing) return hipErrorInvalidValue;
+  s->capturing = true;
+  s->ops.clear();
+  return hipSuccess;
+}
+hipError_t hipStreamEndCapture(hipStream_t s, hipGraph_t *g) {
+  if (!s || !s->capturing) return hipErrorInvalidValue;
+  s->capturing = false;
+  *g = new ihipGraph_t{std::move(s->ops)};
+  s->ops.clear();
+  return hipSuccess;
+}
+hipError_t hipGraphInstantiateWithFlags(hipGraphExec_t *x, hipGraph_t g, unsigned long long) {
+  *x = new ihipGraphExec_t{g->ops};
+  return hipSuccess;
+}
+hipError_t hipGraphLaunch(hipGraphExec_t x, hipStream_t s) {
+  if (emu::capturing(s)) return hipErrorInvalidValue;
+  for (auto &op : x->ops) op();
+  return hipSuccess;
+}
+hipError_t hipGraphDestroy(hipGraph_t g) {
+  delete g;
+  return hipSuccess;
+}
+hipError_t hipGraphExecDestroy(hipGraphExec_t x) {
+  delete x;
   return hipSuccess;
 }
 hipError_t hipStreamCreateWithFlags(hipStream_t *s, unsigned int flags) {
@@ -377,7 +500,8 @@ hipError_t hipEventDestroy(hipEvent_t e) {
   delete e;
   return hipSuccess;
 }
-hipError_t hipEventRecord(hipEvent_t e, hipStream_t) {
+hipError_t hipEventRecord(hipEvent_t e, hipStream_t s) {
+  if (emu::capturing(s)) return hipSuccess;
   e->t = std::chrono::steady_clock::now();
   e->recorded = true;
   return hipSuccess;

@@ -5,6 +5,6 @@
 #define hipExtLaunchKernelGGL(k, g, b, shm, s, e0, e1, flags, ...)        \
   do {                                                                    \
     if (e0) (void)hipEventRecord((e0), (s));                              \
-    ::emu::launch(k, dim3(g), dim3(b), (size_t)(shm), ##__VA_ARGS__);     \
+    ::emu::launch((s), k, dim3(g), dim3(b), (size_t)(shm), ##__VA_ARGS__); \
     if (e1) (void)hipEventRecord((e1), (s));                              \
   } while (0)

@@ -77,8 +77,20 @@ typedef enum hipMemcpyKind {
 } hipMemcpyKind;
 struct ihipStream_t;
 struct ihipEvent_t;
+struct ihipGraph_t;
+struct ihipGraphExec_t;
 typedef ihipStream_t *hipStream_t;
 typedef ihipEvent_t *hipEvent_t;
+typedef ihipGraph_t *hipGraph_t;
+typedef ihipGraphExec_t *hipGraphExec_t;
+typedef enum hipStreamCaptureMode {
+  hipStreamCaptureModeGlobal = 0,
+  hipStreamCaptureModeThreadLocal = 1,
+  hipStreamCaptureModeRelaxed = 2,
+} hipStreamCaptureMode;
+typedef enum hipFuncAttribute {
+  hipFuncAttributeMaxDynamicSharedMemorySize = 8,
+} hipFuncAttribute;
 #define hipStreamNonBlocking 0x01
 #define hipEventDisableTiming 0x02
 #define hipHostMallocDefault 0x0
@@ -115,6 +127,13 @@ hipError_t hipEventRecord(hipEvent_t e, hipStream_t s);
 hipError_t hipEventSynchronize(hipEvent_t e);
 hipError_t hipEventElapsedTime(float *ms, hipEvent_t a, hipEvent_t b);
 hipError_t hipGetSymbolAddress(void **dev, const void *sym);
+hipError_t hipFuncSetAttribute(const void *f, hipFuncAttribute a, int v);
+hipError_t hipStreamBeginCapture(hipStream_t s, hipStreamCaptureMode m);
+hipError_t hipStreamEndCapture(hipStream_t s, hipGraph_t *g);
+hipError_t hipGraphInstantiateWithFlags(hipGraphExec_t *x, hipGraph_t g, unsigned long long flags);
+hipError_t hipGraphLaunch(hipGraphExec_t x, hipStream_t s);
+hipError_t hipGraphDestroy(hipGraph_t g);
+hipError_t hipGraphExecDestroy(hipGraphExec_t x);
 hipError_t hipGetLastError(void);
 const char *hipGetErrorString(hipError_t e);
 }  // extern "C"
@@ -130,21 +149,39 @@ Thread &self();
 void run_grid(dim3 grid, dim3 block, const std::function<void()> &body);
 void barrier();
 uint64_t wave_exchange_u64(uint64_t v, int src_lane_xor, bool ballot);
+uint64_t wave_readlane(uint64_t v, int lane);
+uint32_t wave_dpp(uint32_t v, int ctrl);
+void wave_sync();
+// 16x16 MFMA with kb values of A and B per lane (K = 4 kb): lane l holds
+// A[l % 16][kb (l / 16) + j] and B[kb (l / 16) + j][l % 16], and receives
+// D[4 (l / 16) + r][l % 16]
+void wave_mfma_16x16(const float *a, const float *b, int kb, const float *c4, float *d4);
+void *dyn_lds();
 void check_uniform(uint64_t v, const char *what);
 void dma16(const void *g, uint32_t lds_addr);
 uint32_t lds_base_hi();
 void report(const char *what);
 
-template <class... P, class... A>
-void launch(void (*k)(P...), dim3 g, dim3 b, size_t shm, A &&...a) {
-  (void)shm;
-  // arguments are copied once, as a kernel's by-value parameters are
-  std::tuple<std::decay_t<P>...> args(std::forward<A>(a)...);
-  run_grid(g, b, [&]() { std::apply([&](auto &...x) { k(x...); }, args); });
+void set_dyn_lds(size_t bytes);
+// a stream under capture records its operations (replayed by hipGraphLaunch)
+bool capturing(hipStream_t s);
+void record(hipStream_t s, std::function<void()> op);
+template <class K, class... A>
+void launch(hipStream_t s, K k, dim3 g, dim3 b, size_t shm, A &&...a) {
+  // arguments are copied when the launch is made, as a kernel's by-value
+  // parameters are (a captured launch replays these copies)
+  std::function<void()> op = [k, g, b, shm, args = std::tuple<std::decay_t<A>...>(std::forward<A>(a)...)]() mutable {
+    set_dyn_lds(shm);
+    run_grid(g, b, [&]() { std::apply([&](auto &...x) { k(x...); }, args); });
+  };
+  if (capturing(s))
+    record(s, std::move(op));
+  else
+    op();
 }
 }  // namespace emu
 
-#define hipLaunchKernelGGL(k, g, b, shm, s, ...) ::emu::launch(k, dim3(g), dim3(b), (size_t)(shm), ##__VA_ARGS__)
+#define hipLaunchKernelGGL(k, g, b, shm, s, ...) ::emu::launch((s), k, dim3(g), dim3(b), (size_t)(shm), ##__VA_ARGS__)
 
 // ── built-in variables ──
 #define threadIdx (::emu::self().tid)
@@ -214,6 +251,72 @@ inline uint32_t emu_buffer_load_b32(emu_rsrc r, int voff, int soff, int aux) {
   return v;
 }
 #define __builtin_amdgcn_raw_buffer_load_b32(r, v, s, a) emu_buffer_load_b32((r), (v), (s), (a))
+
+// cross-lane: readlane, DPP lane swaps (quad_perm, row_mirror,
+// row_half_mirror), wave barriers, and the 16x16x32 f16 MFMA (operands
+// exchanged across the wave, products summed in k order in f32, as one
+// instruction on the device; the device's internal summation may round
+// differently)
+template <class T>
+inline T emu_readlane(T v, int lane) {
+  return (T)::emu::wave_readlane((uint64_t)(uint32_t)v, lane);
+}
+#define __builtin_amdgcn_readlane(v, l) emu_readlane((v), (l))
+inline int emu_update_dpp(int old, int src, int ctrl, int row_mask, int bank_mask, bool bound_ctrl) {
+  (void)old;
+  (void)row_mask;
+  (void)bank_mask;
+  (void)bound_ctrl;
+  return (int)::emu::wave_dpp((uint32_t)src, ctrl);
+}
+#define __builtin_amdgcn_update_dpp(o, s, c, rm, bm, bc) emu_update_dpp((o), (s), (c), (rm), (bm), (bc))
+#define __builtin_amdgcn_wave_barrier() ::emu::wave_sync()
+#define __builtin_amdgcn_sched_barrier(x) ((void)(x))
+#define __builtin_amdgcn_ballot_w64(p) __ballot(p)
+#define __builtin_amdgcn_exp2f(x) exp2f(x)
+// v_perm_b32: byte i of the result is byte sel_i of {src0 : src1} (src1 the
+// low bytes); selectors 0x0c / >= 0x0d give 0x00 / 0xff
+inline uint32_t emu_perm(uint32_t s0, uint32_t s1, uint32_t sel) {
+  const uint64_t both = ((uint64_t)s0 << 32) | s1;
+  uint32_t r = 0;
+  for (int i = 0; i < 4; i++) {
+    const uint32_t b = (sel >> (8 * i)) & 0xff;
+    uint32_t v;
+    if (b < 8) v = (uint32_t)(both >> (8 * b)) & 0xff;
+    else if (b == 0x0c) v = 0x00;
+    else v = 0xff;
+    r |= v << (8 * i);
+  }
+  return r;
+}
+#define __builtin_amdgcn_perm(a, b, s) emu_perm((a), (b), (s))
+typedef _Float16 emu_h8 __attribute__((ext_vector_type(8)));
+typedef float emu_f4 __attribute__((ext_vector_type(4)));
+inline emu_f4 emu_mfma_16x16x32_f16(emu_h8 a, emu_h8 b, emu_f4 c, int cbsz, int abid, int blgp) {
+  (void)cbsz;
+  (void)abid;
+  (void)blgp;
+  float af[8], bf[8], cin[4] = {c[0], c[1], c[2], c[3]}, d[4];
+  for (int j = 0; j < 8; j++) {
+    af[j] = (float)a[j];
+    bf[j] = (float)b[j];
+  }
+  ::emu::wave_mfma_16x16(af, bf, 8, cin, d);
+  return emu_f4{d[0], d[1], d[2], d[3]};
+}
+#define __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, x, y, z) emu_mfma_16x16x32_f16((a), (b), (c), (x), (y), (z))
+inline emu_f4 emu_mfma_16x16x4_f32(float a, float b, emu_f4 c, int cbsz, int abid, int blgp) {
+  (void)cbsz;
+  (void)abid;
+  (void)blgp;
+  float cin[4] = {c[0], c[1], c[2], c[3]}, d[4];
+  ::emu::wave_mfma_16x16(&a, &b, 1, cin, d);
+  return emu_f4{d[0], d[1], d[2], d[3]};
+}
+#define __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, x, y, z) emu_mfma_16x16x4_f32((a), (b), (c), (x), (y), (z))
+inline float __expf(float x) { return expf(x); }
+inline float __fdividef(float a, float b) { return a / b; }
+inline float rsqrtf(float x) { return 1.0f / sqrtf(x); }
 
 inline int min(int a, int b) { return a < b ? a : b; }
 inline int max(int a, int b) { return a > b ? a : b; }

@@ -44,7 +44,8 @@ def emu():
     variant = os.path.join(build_emu.OUT, "tdt_joint_two_windows.hip")
     with open(variant, "w") as f:
         f.write(joint_two_windows.variant_source())
-    return {"shipped": build_emu.build(), "two_windows": build_emu.build(variant, "_alt"), "rt": rt}
+    srcs = ["runtime.hip", "tdt.hip", "mel.hip"]
+    return {"shipped": build_emu.build(tag="_dec", sources=srcs), "two_windows": build_emu.build(variant, "_alt", srcs), "rt": rt}
 
 
 def run(emu, lib, case, script="run_tdt.py"):
