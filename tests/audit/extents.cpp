@@ -70,6 +70,9 @@ struct VrowShadow {
   long entries = 0;
 };
 static VrowShadow g_vrow;
+// a dry call (whether a kernel has a model, asked while a graph is being
+// captured) computes the ranges but executes nothing
+bool g_dry = false;
 
 template <typename T>
 static T arg(const std::vector<std::vector<char>> &a, size_t i) {
@@ -548,7 +551,7 @@ int extents(const std::string &mangled, const std::string &pretty, const std::ve
     const MelSrcM v = arg<MelSrcM>(a, 0);
     MelSrcM *d = arg<MelSrcM *>(a, 1);
     wr(o, d, sizeof(MelSrcM), "MelSrc");
-    if (d) std::memcpy(d, &v, sizeof v);  // executed: the front end indexes through it
+    if (d && !g_dry) std::memcpy(d, &v, sizeof v);  // executed: the front end indexes through it
     return 1;
   }
   if (has("sub_c01_kernel")) {
@@ -606,7 +609,7 @@ int extents(const std::string &mangled, const std::string &pretty, const std::ve
         vmax = std::max<long>(vmax, (long)out.off[w] + nv);
       }
     }
-    if (vrow) {  // executed: the q|k|v epilogue scatters V through it
+    if (vrow && !g_dry) {  // executed: the q|k|v epilogue scatters V through it
       g_vrow.base = (uintptr_t)vrow;
       g_vrow.entries = vmax;
       for (int w = 0; w < std::min(nw, out.n); w++) {

@@ -242,12 +242,18 @@ void check_span(const void *p, size_t n, const std::string &who) {
   if (v + n > b->first + b->second.size) violation(who + ": span of " + std::to_string(n) + " bytes runs past the end of its block");
 }
 
-void check_launch_args(const Launch &l, const char *when) {
+// Pointer arguments must point into live blocks.  By-value aggregates are
+// scanned word by word only for kernels without an extent model: a struct's
+// padding is not initialised, so a word that joins an int field to padding
+// holding half of an old pointer can read as an address; a kernel with a
+// model has the fields it uses checked by the model instead.
+void check_launch_args(const Launch &l, const char *when, bool scan_aggregates) {
   const KernelInfo &k = *l.k;
   const std::string who = std::string(when) + " " + k.pretty;
   for (size_t i = 0; i < l.args.size(); i++) {
     const std::vector<char> &a = l.args[i];
     const Arg &m = k.args[i];
+    if (!m.pointer && !scan_aggregates && a.size() > 8) continue;
     for (size_t o = 0; o + 8 <= a.size(); o += 8) {
       uint64_t v;
       std::memcpy(&v, a.data() + o, 8);
@@ -335,17 +341,19 @@ struct Span {
 };
 int extents(const std::string &mangled, const std::string &pretty, const std::vector<std::vector<char>> &a, unsigned gx, unsigned gy, unsigned gz,
             unsigned threads, std::vector<Span> &o, std::string &note);
+extern bool g_dry;
 }  // namespace audit_ext
 namespace {
 std::map<std::string, size_t> &unmodelled() { static auto *m = new std::map<std::string, size_t>(); return *m; }
 size_t g_extent_checks = 0;
-void check_extents(const Launch &l, const char *when, int sid) {
+// returns whether the kernel has an extent model
+bool check_extents(const Launch &l, const char *when, int sid) {
   const KernelInfo &k = *l.k;
   std::vector<audit_ext::Span> sp;
   std::string note;
   if (!audit_ext::extents(k.name, k.pretty, l.args, l.grid.x, l.grid.y, l.grid.z, l.block.x * l.block.y * l.block.z, sp, note)) {
     unmodelled()[k.pretty]++;
-    return;
+    return false;
   }
   const std::string who = std::string(when) + " " + k.pretty;
   if (!note.empty()) violation(who + ": " + note);
@@ -359,6 +367,7 @@ void check_extents(const Launch &l, const char *when, int sid) {
     check_span((const void *)s.p, s.bytes, w);
     access(sid, s.p, s.bytes, s.write, k.pretty + " (" + s.what + ")");
   }
+  return true;
 }
 
 void check_geometry(const KernelInfo &k, dim3 g, dim3 b, size_t shm) {
@@ -415,12 +424,18 @@ hipError_t do_launch(const void *f, dim3 g, dim3 b, void **args, size_t shm, hip
   static FILE *logf = std::getenv("FA_AUDIT_LOG") ? std::fopen(std::getenv("FA_AUDIT_LOG"), "w") : nullptr;
   if (logf) std::fprintf(logf, "%s %u %u %u %u\n", k.pretty.c_str(), g.x, g.y, g.z, b.x * b.y * b.z);
   check_geometry(k, g, b, shm);
-  check_launch_args(l, "launch");
   Handle *cs = capturing_stream(s);
   if (!cs) {  // a captured launch runs (and is checked) at each replay
     const int sid = stream_sid(s);
     begin_op(sid);
-    check_extents(l, "launch", sid);
+    check_launch_args(l, "launch", !check_extents(l, "launch", sid));
+  } else {  // captured: checked at each replay; here only the pointer arguments
+    std::vector<audit_ext::Span> sp;
+    std::string note;
+    audit_ext::g_dry = true;
+    const bool has_model = audit_ext::extents(k.name, k.pretty, l.args, g.x, g.y, g.z, b.x * b.y * b.z, sp, note) != 0;
+    audit_ext::g_dry = false;
+    check_launch_args(l, "launch", !has_model);
   }
   if (cs) cs->ops.push_back(Op{0, l});
   return hipSuccess;
@@ -728,8 +743,7 @@ hipError_t hipGraphLaunch(hipGraphExec_t x, hipStream_t s) {
     begin_op(sid);
     if (o.type == 0) {
       g_replayed_launches++;
-      check_launch_args(o.l, "graph replay");
-      check_extents(o.l, "graph replay", sid);
+      check_launch_args(o.l, "graph replay", !check_extents(o.l, "graph replay", sid));
     } else {
       check_span(o.p0, o.bytes, "graph replay copy/set destination");
       if (o.type == 1) check_span(o.p1, o.bytes, "graph replay copy source");
