@@ -102,12 +102,9 @@ __global__ __launch_bounds__(256) void sub_c01_kernel(const float *__restrict__ 
   const int rblk = 16 * blockIdx.x - 3 * pt;
   // the window's first mel frame: time-major row (element ti * MB + fi) or
   // channel-major stream column (element fi * ttot + ti)
-  long ttot = 0;
-  const float *m = mel + (size_t)s0.off[win] * MB;
-  if (src) {
-    ttot = src->ttot;
-    m = src->ptr + src->start[win];
-  }
+  // (mel is null when the descriptor is given: no offset is applied to it then)
+  const long ttot = src ? src->ttot : 0;
+  const float *m = src ? src->ptr + src->start[win] : mel + (size_t)s0.off[win] * MB;
   const int T0 = s0.len[win], T1 = s1.len[win];
   if constexpr (LM) {  // slot [r][j] holds frame rblk + r, bin j - pl; zero outside the window
     for (int idx = threadIdx.x; idx < kRows * kC01MelStride; idx += 256) {
